@@ -1,0 +1,194 @@
+"""Benchmark of the super-gemma quantized compute core on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Prints ONE JSON line (rank 0).  A "step" is one pass of the hot path over one
+batch of synthetic input, already resident in HBM:
+
+  gemv    BASELINE config 1: Q4_0 GEMV K=5376, N=21504 (decode), rotating over
+          8 weight copies (520 MB > the 256 MB MALL) so every launch streams
+          its weights from HBM.
+  mmq     BASELINE config 2: Q4_0×Q8 int8-MFMA GEMM M=512, K=5376, N=21504.
+  splitk  BASELINE config 3: down-proj M=2048, K=21504, N=5376, split-K 4.
+
+The timed region is bracketed by torch.cuda.synchronize() and measured with
+HIP events on the stream the kernels run on.  The cpu_baseline leg times the
+CPU restatement of the reference's Q4_0 matmul (oracle/, reference.rs:402-444)
+on a bounded sample on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "super-gemma_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, TOP/s
+METRIC = "decode tok/s (31B Q4_0 shape, bs=1) + Q4_0 GEMV GB/s vs HBM peak"
+
+
+def q4_bytes(n, k):
+    return n * (k // 32) * 18
+
+
+class Gemv:
+    name = "gemv_q4_0 K=5376 N=21504 (BASELINE config 1), 8 rotating weight copies"
+    kernel = "gemv_q4_0_kernel"
+
+    def __init__(self, ctx, torch):
+        self.ctx, self.torch = ctx, torch
+        self.k, self.n = 5376, 21504
+        self.copies = 8
+        nbytes = q4_bytes(self.n, self.k)
+        self.w = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(self.copies)]
+        for i, w in enumerate(self.w):
+            ctx.fill_q4_0_random(w, nbytes // 18, seed=100 + i, sigma=0.02)
+        self.x = torch.empty(self.k, dtype=torch.float32, device="cuda")
+        ctx.fill_normal(self.x, seed=7)
+        self.y = torch.empty(self.n, dtype=torch.float32, device="cuda")
+        # algorithmic bytes per launch: W + x (fp32) + y (fp32)
+        self.bytes = nbytes + self.k * 4 + self.n * 4
+
+    def step(self, i):
+        self.ctx.gemv_q4_0(self.w[i % self.copies], self.x, self.y, self.n, self.k)
+
+    def result(self, ms_per_step):
+        gbs = self.bytes / (ms_per_step * 1e-3) / 1e9
+        return {
+            "value": gbs, "unit": "GB/s", "dtype": "q4_0 weights, fp32 x/y (int8 dot4 on 3-limb x)",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "config": {"workload": self.name, "m": 1, "k": self.k, "n": self.n,
+                       "bytes_per_launch": self.bytes},
+        }
+
+
+class Mmq:
+    kernel = "mmq_kernel"
+
+    def __init__(self, ctx, torch, m=512, k=5376, n=21504, split=1, label="BASELINE config 2"):
+        self.ctx, self.torch = ctx, torch
+        self.m, self.k, self.n, self.split = m, k, n, split
+        self.name = f"gemm_q4_0_q8 int8 MFMA M={m} K={k} N={n} split_k={split} ({label})"
+        self.w = torch.empty(q4_bytes(n, k), dtype=torch.uint8, device="cuda")
+        ctx.fill_q4_0_random(self.w, n * k // 32, seed=21, sigma=0.02)
+        x = torch.empty(m * k, dtype=torch.float32, device="cuda")
+        ctx.fill_normal(x, seed=22)
+        if split > 1:  # config 3: GeGLU-like activations gelu(N(0,1))*N(0,1)
+            u = torch.empty_like(x)
+            ctx.fill_normal(u, seed=23)
+            x = (torch.nn.functional.gelu(x, approximate="tanh") * u).contiguous()
+        self.xs = torch.empty(m * k // 32, dtype=torch.int16, device="cuda")
+        self.xq = torch.empty(m * k, dtype=torch.int8, device="cuda")
+        ctx.quant_q8_0(x, self.xs, self.xq)
+        del x
+        self.y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+        self.part = (torch.empty(split * m * n, dtype=torch.float32, device="cuda")
+                     if split > 1 else None)
+        self.ops = 2.0 * m * n * k
+
+    def step(self, i):
+        self.ctx.gemm_q4_0_q8(self.w, self.xq, self.xs, self.y, self.m, self.n, self.k,
+                              self.split, self.part)
+
+    def result(self, ms_per_step):
+        tops = self.ops / (ms_per_step * 1e-3) / 1e12
+        return {
+            "value": tops, "unit": "TOP/s", "dtype": "int8 x q4_0 -> i32 MFMA, fp32 rescale",
+            "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": tops / INT8_PEAK_TOPS, "traffic": None},
+            "config": {"workload": self.name, "m": self.m, "k": self.k, "n": self.n,
+                       "split_k": self.split, "ops_per_launch": self.ops},
+        }
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    """Time the CPU restatement of CpuModel::matmul (dequant_row + 8-lane f64
+    dot, row-parallel) on BASELINE config 1, full size, on the host cores."""
+    import numpy as np
+    from oracle import oracle
+
+    k, n = 5376, 21504
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rng = oracle.Rng(0xBA5E)
+    w = rng.random_q4_0(n * k // 32)
+    x = rng.f32_vec(k)
+    oracle.matmul_q4_0(w, x, 1, n, k, threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matmul_q4_0(w, x, 1, n, k, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= 400:
+            break
+    gbs = q4_bytes(n, k) * reps / el / 1e9
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config 1 GEMV (K=5376, N=21504) full size, {reps} reps in {el:.1f} s, "
+                      f"C restatement of reference.rs:402-444 on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="gemv", choices=["gemv", "mmq", "splitk"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build runs on one GPU only "
+              "(no collectives, no multi-GPU path); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import sgq
+
+    ctx = sgq.GpuContext(0)
+    if args.workload == "gemv":
+        wl = Gemv(ctx, torch)
+    elif args.workload == "mmq":
+        wl = Mmq(ctx, torch)
+    else:
+        wl = Mmq(ctx, torch, m=2048, k=21504, n=5376, split=4, label="BASELINE config 3")
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        wl.step(i)
+    torch.cuda.synchronize()
+    ctx.timer_start()
+    for i in range(args.steps):
+        wl.step(i)
+    ms_total = ctx.timer_stop()
+    torch.cuda.synchronize()
+    ms = ms_total / args.steps
+    res = wl.result(ms)
+    out = {
+        "metric": METRIC,
+        "value": res["value"],
+        "unit": res["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": res["dtype"],
+        "data": "synthetic (device-generated, seeded)",
+        "config": res["config"],
+        "roofline": res["roofline"],
+        "kernel": wl.kernel,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,159 @@
+/*
+ * sgq.h — C ABI of libsgq, the MI355X (gfx950) quantized compute core that
+ * replaces super-gemma's sg-gpu kernel-dispatch surface.
+ *
+ * Two layers, both plain C (no torch or HIP types in any signature):
+ *
+ *  1. The dispatch surface, mirroring sg-gpu's public API
+ *     (crates/sg-gpu/src/lib.rs:20-44): a context, device buffers, kernel
+ *     lookup by variant NAME, a dispatch of (kernel, bindings, push constants,
+ *     groups), re-submittable recorded graphs and a per-step state buffer.
+ *     Variant names, binding order, push-constant layout and group counts are
+ *     the reference's (crates/sg-gpu/build.rs VARIANTS), so a forward graph
+ *     that records `load_kernel(name)` + `dispatch(...)` drives this library
+ *     unchanged.  Activation buffers hold fp32 where the reference held f16;
+ *     Q4_0 weights and Q8_0 pages are byte-identical formats.
+ *
+ *  2. Typed entry points (sgq_gemv_q4_0, sgq_gemm_q4_0_q8, ...) that compute
+ *     their own launch geometry; the name dispatch routes to the same code.
+ *
+ * Pointers passed as buffers are device pointers (from sgq_buf_alloc or any
+ * HIP allocation on the context's device).  All work is enqueued on the
+ * context's stream (sgq_ctx_set_stream) in call order, which gives the
+ * compute→compute ordering the reference gets from its per-dispatch barrier.
+ * A context is used by one host thread at a time.
+ */
+#ifndef SGQ_H
+#define SGQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes mirror sg_gpu::GpuError (crates/sg-gpu/src/lib.rs:31-44);
+ * SGQ_ERR_HIP takes the place of the Vulkan error. */
+typedef enum {
+    SGQ_OK = 0,
+    SGQ_ERR_LIBRARY = 1,        /* GpuError::Library */
+    SGQ_ERR_HIP = 2,            /* GpuError::Vk */
+    SGQ_ERR_NO_DEVICE = 3,      /* GpuError::NoDevice: callers skip, not fail */
+    SGQ_ERR_UNKNOWN_KERNEL = 4, /* GpuError::UnknownKernel */
+    SGQ_ERR_PIPELINE = 5,       /* GpuError::Pipeline */
+    SGQ_ERR_VALIDATION = 6      /* GpuError::Validation: bad shapes/bindings */
+} sgq_status;
+
+typedef struct sgq_ctx sgq_ctx;
+typedef struct sgq_kernel sgq_kernel;
+typedef struct sgq_graph sgq_graph;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *sgq_last_error(void);
+/* Library version string. */
+const char *sgq_version(void);
+
+/* ---- context: GpuContext::new (crates/sg-gpu/src/context.rs:103-236) ---- */
+int sgq_ctx_create(int device, sgq_ctx **out);
+int sgq_ctx_destroy(sgq_ctx *ctx);
+/* Use an existing hipStream_t (passed as void*); NULL = the null stream. */
+int sgq_ctx_set_stream(sgq_ctx *ctx, void *hip_stream);
+/* submit_blocking's wait half (crates/sg-gpu/src/graph.rs:640). */
+int sgq_sync(sgq_ctx *ctx);
+
+/* ---- buffers: crates/sg-gpu/src/buffer.rs:233-300 ------------------------ */
+int sgq_buf_alloc(sgq_ctx *ctx, uint64_t bytes, void **dev_ptr);
+int sgq_buf_free(sgq_ctx *ctx, void *dev_ptr);
+int sgq_buf_upload(sgq_ctx *ctx, void *dst_dev, const void *src_host, uint64_t bytes);
+int sgq_buf_download(sgq_ctx *ctx, void *dst_host, const void *src_dev, uint64_t bytes);
+int sgq_buf_fill_zero(sgq_ctx *ctx, void *dev_ptr, uint64_t bytes);
+
+/* ---- kernel registry: KernelBlob (crates/sg-gpu/src/kernel.rs:18-34) and
+ *      GpuContext::load_kernel (kernel.rs:79-163) ------------------------- */
+typedef struct {
+    uint32_t workgroup[3]; /* the reference's workgroup size (for its group math) */
+    uint32_t bindings;     /* storage-buffer bindings 0..bindings-1 */
+    uint32_t push_bytes;   /* push-constant bytes (0 = none) */
+    uint32_t subgroup_size;
+} sgq_kernel_info;
+
+int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
+                      sgq_kernel_info *info);
+/* Number of registered variant names / the i-th one (for enumeration). */
+uint32_t sgq_kernel_count(void);
+const char *sgq_kernel_name(uint32_t i);
+
+/* BufferBinding{binding, buffer, offset, range} (graph.rs:199-225).
+ * range == 0 means "to the end of the allocation is unknown": callers pass the
+ * byte length actually bound, as Vulkan's arrayLength() semantics need it. */
+typedef struct {
+    uint32_t binding;
+    uint32_t _pad;
+    void *ptr;
+    uint64_t offset;
+    uint64_t range;
+} sgq_binding;
+
+/* GraphRecorder::dispatch (crates/sg-gpu/src/graph.rs:225-324): groups are the
+ * reference's group counts for this variant. */
+int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bindings,
+                 uint32_t n_bindings, const void *push, uint32_t push_bytes,
+                 const uint32_t groups[3]);
+
+/* ---- recorded graphs: CommandGraph / GraphRecorder / submit (graph.rs:
+ *      523-660), backed by hipGraph capture of the context's stream ------- */
+int sgq_graph_begin(sgq_ctx *ctx);
+int sgq_graph_end(sgq_ctx *ctx, sgq_graph **out);
+int sgq_graph_submit(sgq_ctx *ctx, sgq_graph *graph);
+int sgq_graph_destroy(sgq_graph *graph);
+
+/* StepState::write_to (crates/sg-gpu/src/graph.rs:33-61): the 4-word step
+ * buffer [pos, kv_len_sliding, kv_len_global, q0], written on the stream. */
+int sgq_step_write(sgq_ctx *ctx, void *step_dev, uint32_t pos, uint32_t kv_len_sliding,
+                   uint32_t kv_len_global, uint32_t q0);
+
+/* ---- timers: GpuTimer (graph.rs:404-460) over hipEvents ----------------- */
+int sgq_timer_start(sgq_ctx *ctx);
+/* Milliseconds since sgq_timer_start, after waiting for the stream. */
+int sgq_timer_stop(sgq_ctx *ctx, float *ms);
+
+/* ---- typed entry points -------------------------------------------------- */
+
+/* Decode GEMV y[n] = W[n×k]·x[k]; W is Q4_0 row-major (k/32 blocks of 18 B
+ * per row), x and y fp32.  Replaces gemv_q4_0_k{K} / gemv_q4_0_generic
+ * (crates/sg-gpu/shaders/gemv_q4_0.wgsl:52-112).  k % 64 == 0, k <= 65536. */
+int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_t n,
+                  uint32_t k);
+
+/* Q8_0 quantization of n fp32 values (n % 32 == 0) into f16 scales [n/32] and
+ * int8 quants [n]: kv_quant_q8 (crates/sg-gpu/shaders/kv_quant_q8.wgsl:30-57),
+ * d = amax*(1/127), q = round_ties_even(x/d) with an IEEE reciprocal. */
+int sgq_quant_q8_0(sgq_ctx *ctx, const float *x, uint16_t *scales, int8_t *quants,
+                   uint64_t n);
+
+/* Q8_0 → fp32 (x = f32(d)*q): kv_dequant_q8 with fp32 output. */
+int sgq_dequant_q8_0(sgq_ctx *ctx, const uint16_t *scales, const int8_t *quants, float *out,
+                     uint64_t n);
+
+/* Prefill int8 MMQ Y[m×n] = Xq[m×k]·W[n×k]^T with per-32-block rescale
+ * (d_a[m,b]*d_w[n,b]) in fp32: gemm_q4_0_i8_* (crates/sg-gpu/shaders/
+ * gemm_q4_0_i8.wgsl:153-393, gemm_q4_0_i8_bb_pfd.wgsl).  split_k in
+ * {1,2,4,8}: for split_k > 1, `partials` must hold split_k*m*n floats and the
+ * slices are summed in fixed order s = 0..split_k-1.  k % 32 == 0. */
+int sgq_gemm_q4_0_q8(sgq_ctx *ctx, const void *w, const int8_t *xq, const uint16_t *xs,
+                     float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
+                     float *partials);
+
+/* ---- synthetic inputs (not on the hot path; for benches and tests) ------ */
+/* Q4_0 blocks with d = f16(|N(0, sigma)|) and uniform nibble bytes, from a
+ * counter-based generator keyed by (seed, block index). */
+int sgq_fill_q4_0_random(sgq_ctx *ctx, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
+/* fp32 N(mean, sigma) from a counter-based generator keyed by (seed, index). */
+int sgq_fill_normal(sgq_ctx *ctx, float *x, uint64_t n, uint64_t seed, float mean,
+                    float sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SGQ_H */

@@ -1,0 +1,520 @@
+// libsgq C ABI: context, buffers, the variant registry with name dispatch,
+// recorded graphs, step buffer, timers and the typed entry points.
+//
+// The name registry is the drop-in half of the boundary: it accepts the
+// variant names of crates/sg-gpu/build.rs VARIANTS (plus the same families
+// at the BASELINE geometry, e.g. head_dim 128), with their binding order,
+// push-constant layout and group-count convention, and routes each dispatch
+// to the typed launcher that computes its own HIP grid.
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "sgq_internal.h"
+
+struct sgq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool capturing = false;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+
+struct sgq_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace sgq {
+
+static thread_local char g_err[1024] = "";
+
+int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int check_hip(hipError_t e, const char *what) {
+    return fail(SGQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+const DeviceInfo &device_info() {
+    static DeviceInfo info[16];
+    static bool done[16] = {};
+    static std::mutex mu;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= 16) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!done[dev]) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) == hipSuccess) info[dev].cus = p.multiProcessorCount;
+        done[dev] = true;
+    }
+    return info[dev];
+}
+
+hipStream_t ctx_stream(const sgq_ctx *ctx) { return ctx ? ctx->stream : nullptr; }
+
+}  // namespace sgq
+
+using namespace sgq;
+
+// ---------------------------------------------------------------------------
+// Kernel registry
+// ---------------------------------------------------------------------------
+
+enum class Kind {
+    Gemv,          // gemv_q4_0_k{K} / gemv_q4_0_generic
+    QuantQ8,       // kv_quant_q8
+    DequantQ8,     // kv_dequant_q8
+    AppendQ8,      // kv_append_global_q8 (linear) / kv_append_sliding_q8 (ring)
+    GemmI8,        // gemm_q4_0_i8_*_k{K}_n{N}: groups [M/64, N/16]
+    GemmI8Down,    // gemm_q4_0_i8_bb_pfd{1,2,4}: K=21504, N=5376, groups [M/64, 336]
+    GemmI8Split,   // gemm_q4_0_i8_splitk{S}_k{K}_n{N} (no reference counterpart)
+};
+
+struct sgq_kernel {
+    std::string name;
+    Kind kind;
+    sgq_kernel_info info;
+    uint32_t k = 0, n = 0;  // baked dims (0 = from push/bindings)
+    uint32_t param = 0;     // split factor, ring length, ...
+};
+
+namespace {
+
+// Every name a caller may look up; the numbers in the pattern names are
+// parsed from the actual name at lookup (e.g. gemv_q4_0_k5376).
+const char *const kNames[] = {
+    "gemv_q4_0_k5376",  "gemv_q4_0_k8192",  "gemv_q4_0_k16384", "gemv_q4_0_k21504",
+    "gemv_q4_0_k4096",  "gemv_q4_0_generic", "kv_quant_q8",     "kv_dequant_q8",
+    "kv_append_global_q8",
+    "gemm_q4_0_i8_swz_m4n1_k5376_n21504",   "gemm_q4_0_i8_swz_m4n1_k21504_n5376",
+    "gemm_q4_0_i8_swz_m4n1_k5376_n8192",    "gemm_q4_0_i8_swz_m4n1_k5376_n16384",
+    "gemm_q4_0_i8_swz_m4n1_k5376_n4096",    "gemm_q4_0_i8_swz_m4n1_k5376_n2048",
+    "gemm_q4_0_i8_swz_m4n1_k8192_n5376",    "gemm_q4_0_i8_swz_m4n1_k16384_n5376",
+    "gemm_q4_0_i8_swz_m4n1_k4096_n5376",    "gemm_q4_0_i8_bb_pfd4",
+    "gemm_q4_0_i8_splitk4_k21504_n5376",
+};
+
+bool parse_u32_after(const std::string &s, const std::string &key, uint32_t *out) {
+    size_t p = s.rfind(key);
+    if (p == std::string::npos) return false;
+    p += key.size();
+    if (p >= s.size() || s[p] < '0' || s[p] > '9') return false;
+    uint64_t v = 0;
+    while (p < s.size() && s[p] >= '0' && s[p] <= '9') v = v * 10 + (uint64_t)(s[p++] - '0');
+    if (v > 0xffffffffu) return false;
+    *out = (uint32_t)v;
+    return true;
+}
+
+bool starts_with(const std::string &s, const char *p) { return s.rfind(p, 0) == 0; }
+
+// Build the registry entry for `name`, or return false if it is unknown.
+bool resolve(const std::string &name, sgq_kernel *k) {
+    k->name = name;
+    k->info = {{64, 1, 1}, 0, 0, 0};
+    if (starts_with(name, "gemv_q4_0_")) {
+        k->kind = Kind::Gemv;
+        k->info.bindings = 3;
+        if (name == "gemv_q4_0_generic") {
+            k->info.push_bytes = 4;
+            return true;
+        }
+        if (!parse_u32_after(name, "_k", &k->k)) return false;
+        return name == "gemv_q4_0_k" + std::to_string(k->k) && k->k % 64 == 0 && k->k > 0;
+    }
+    if (name == "kv_quant_q8") {
+        k->kind = Kind::QuantQ8;
+        k->info.bindings = 3;
+        return true;
+    }
+    if (name == "kv_dequant_q8") {
+        k->kind = Kind::DequantQ8;
+        k->info.bindings = 3;
+        return true;
+    }
+    if (name == "kv_append_global_q8") {
+        k->kind = Kind::AppendQ8;
+        k->info.bindings = 4;
+        k->param = 0;
+        return true;
+    }
+    if (starts_with(name, "gemm_q4_0_i8_bb_pfd")) {
+        k->kind = Kind::GemmI8Down;
+        k->info.bindings = 4;
+        k->k = 21504;
+        k->n = 5376;
+        return name == "gemm_q4_0_i8_bb_pfd1" || name == "gemm_q4_0_i8_bb_pfd2" ||
+               name == "gemm_q4_0_i8_bb_pfd4";
+    }
+    if (starts_with(name, "gemm_q4_0_i8_splitk")) {
+        k->kind = Kind::GemmI8Split;
+        k->info.bindings = 5;
+        if (!parse_u32_after(name, "splitk", &k->param)) return false;
+        if (!parse_u32_after(name, "_k", &k->k) || !parse_u32_after(name, "_n", &k->n))
+            return false;
+        return (k->param == 1 || k->param == 2 || k->param == 4 || k->param == 8) &&
+               k->k % 64 == 0 && k->n > 0;
+    }
+    if (starts_with(name, "gemm_q4_0_i8_")) {
+        k->kind = Kind::GemmI8;
+        k->info.bindings = 4;
+        if (!parse_u32_after(name, "_k", &k->k) || !parse_u32_after(name, "_n", &k->n))
+            return false;
+        return k->k % 64 == 0 && k->n > 0;
+    }
+    return false;
+}
+
+struct Registry {
+    std::mutex mu;
+    std::vector<sgq_kernel *> loaded;
+    ~Registry() {
+        for (auto *k : loaded) delete k;
+    }
+};
+Registry &registry() {
+    static Registry r;
+    return r;
+}
+
+// Binding table lookup with range check.
+struct Binds {
+    const sgq_binding *b[8] = {};
+    int get(uint32_t i, void **p, uint64_t *range) const {
+        if (i >= 8 || !b[i]) return fail(SGQ_ERR_VALIDATION, "binding %u missing", i);
+        *p = static_cast<uint8_t *>(b[i]->ptr) + b[i]->offset;
+        *range = b[i]->range;
+        return SGQ_OK;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+const char *sgq_last_error(void) { return g_err; }
+const char *sgq_version(void) { return "sgq 0.1 (gfx950)"; }
+
+int sgq_ctx_create(int device, sgq_ctx **out) {
+    if (!out) return fail(SGQ_ERR_VALIDATION, "out is NULL");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(SGQ_ERR_NO_DEVICE, "no HIP device");
+    if (device < 0 || device >= count) return fail(SGQ_ERR_NO_DEVICE, "device %d absent", device);
+    SGQ_HIP(hipSetDevice(device));
+    hipDeviceProp_t p;
+    SGQ_HIP(hipGetDeviceProperties(&p, device));
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(SGQ_ERR_NO_DEVICE, "device %d is %s, libsgq is built for gfx950", device,
+                    p.gcnArchName);
+    auto *c = new sgq_ctx;
+    c->device = device;
+    if (hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess) {
+        delete c;
+        return fail(SGQ_ERR_HIP, "hipEventCreate failed");
+    }
+    *out = c;
+    return SGQ_OK;
+}
+
+int sgq_ctx_destroy(sgq_ctx *ctx) {
+    if (!ctx) return SGQ_OK;
+    if (ctx->t0) (void)hipEventDestroy(ctx->t0);
+    if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+    delete ctx;
+    return SGQ_OK;
+}
+
+int sgq_ctx_set_stream(sgq_ctx *ctx, void *hip_stream) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
+    return SGQ_OK;
+}
+
+int sgq_sync(sgq_ctx *ctx) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    SGQ_HIP(hipStreamSynchronize(ctx->stream));
+    return SGQ_OK;
+}
+
+int sgq_buf_alloc(sgq_ctx *ctx, uint64_t bytes, void **dev_ptr) {
+    if (!ctx || !dev_ptr) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_HIP(hipSetDevice(ctx->device));
+    SGQ_HIP(hipMalloc(dev_ptr, bytes ? bytes : 256));
+    return SGQ_OK;
+}
+
+int sgq_buf_free(sgq_ctx *ctx, void *dev_ptr) {
+    (void)ctx;
+    if (dev_ptr) SGQ_HIP(hipFree(dev_ptr));
+    return SGQ_OK;
+}
+
+int sgq_buf_upload(sgq_ctx *ctx, void *dst_dev, const void *src_host, uint64_t bytes) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    SGQ_HIP(hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    SGQ_HIP(hipStreamSynchronize(ctx->stream));
+    return SGQ_OK;
+}
+
+int sgq_buf_download(sgq_ctx *ctx, void *dst_host, const void *src_dev, uint64_t bytes) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    SGQ_HIP(hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    SGQ_HIP(hipStreamSynchronize(ctx->stream));
+    return SGQ_OK;
+}
+
+int sgq_buf_fill_zero(sgq_ctx *ctx, void *dev_ptr, uint64_t bytes) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    SGQ_HIP(hipMemsetAsync(dev_ptr, 0, bytes, ctx->stream));
+    return SGQ_OK;
+}
+
+uint32_t sgq_kernel_count(void) { return (uint32_t)(sizeof kNames / sizeof kNames[0]); }
+
+const char *sgq_kernel_name(uint32_t i) {
+    return i < sgq_kernel_count() ? kNames[i] : nullptr;
+}
+
+int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
+                      sgq_kernel_info *info) {
+    (void)ctx;
+    if (!name || !out) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    auto *k = new sgq_kernel;
+    if (!resolve(name, k)) {
+        delete k;
+        return fail(SGQ_ERR_UNKNOWN_KERNEL, "unknown kernel variant '%s'", name);
+    }
+    {
+        Registry &r = registry();
+        std::lock_guard<std::mutex> lock(r.mu);
+        r.loaded.push_back(k);
+    }
+    *out = k;
+    if (info) *info = k->info;
+    return SGQ_OK;
+}
+
+int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bindings,
+                 uint32_t n_bindings, const void *push, uint32_t push_bytes,
+                 const uint32_t groups[3]) {
+    if (!ctx || !kernel || !groups) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    if (push_bytes != kernel->info.push_bytes)
+        return fail(SGQ_ERR_VALIDATION, "%s: push constants are %u bytes, got %u",
+                    kernel->name.c_str(), kernel->info.push_bytes, push_bytes);
+    if (push_bytes && !push) return fail(SGQ_ERR_VALIDATION, "push is NULL");
+    Binds B;
+    for (uint32_t i = 0; i < n_bindings; i++) {
+        if (bindings[i].binding >= 8 || bindings[i].binding >= kernel->info.bindings)
+            return fail(SGQ_ERR_VALIDATION, "%s: binding %u out of range",
+                        kernel->name.c_str(), bindings[i].binding);
+        B.b[bindings[i].binding] = &bindings[i];
+    }
+    hipStream_t st = ctx->stream;
+    void *p0, *p1, *p2, *p3, *p4;
+    uint64_t r0, r1, r2, r3, r4;
+    int rc;
+    switch (kernel->kind) {
+        case Kind::Gemv: {
+            // bindings: 0 weights, 1 x, 2 y; groups [N, 1, 1] (one WG per row)
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            uint32_t k = kernel->k;
+            if (!k) std::memcpy(&k, push, 4);
+            const uint32_t n = groups[0];
+            if (r0 && r0 < (uint64_t)n * (k / 32) * 18)
+                return fail(SGQ_ERR_VALIDATION, "%s: weights binding too small", kernel->name.c_str());
+            if (r1 && r1 < (uint64_t)k * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: x binding too small", kernel->name.c_str());
+            if (r2 && r2 < (uint64_t)n * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: y binding too small", kernel->name.c_str());
+            return launch_gemv_q4_0(st, p0, static_cast<const float *>(p1), static_cast<float *>(p2),
+                                    n, k);
+        }
+        case Kind::QuantQ8: {
+            // bindings: 0 src fp32, 1 scales f16, 2 quants; blocks = arrayLength(src)/32
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            if (!r0) return fail(SGQ_ERR_VALIDATION, "kv_quant_q8: src range required");
+            const uint64_t n = r0 / 4 / 32 * 32;
+            return launch_quant_q8_0(st, static_cast<const float *>(p0), static_cast<uint16_t *>(p1),
+                                     static_cast<int8_t *>(p2), n);
+        }
+        case Kind::DequantQ8: {
+            // bindings: 0 scales, 1 quants, 2 out fp32; elements = arrayLength(quants)
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            if (!r1) return fail(SGQ_ERR_VALIDATION, "kv_dequant_q8: quants range required");
+            return launch_dequant_q8_0(st, static_cast<const uint16_t *>(p0),
+                                       static_cast<const int8_t *>(p1), static_cast<float *>(p2),
+                                       r1 / 32 * 32);
+        }
+        case Kind::AppendQ8: {
+            // bindings: 0 src fp32 [n_tokens × row], 1 scales, 2 quants, 3 step;
+            // groups cover n_tokens × row/32 blocks; row length is the group
+            // count's y extent when given, else the kv row of the BASELINE
+            // geometry (16 kv heads × 128).
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)) ||
+                (rc = B.get(3, &p3, &r3)))
+                return rc;
+            const uint32_t row = groups[1] > 1 ? groups[1] * 32 : 2048;
+            if (!r0) return fail(SGQ_ERR_VALIDATION, "kv_append: src range required");
+            const uint32_t ntok = (uint32_t)(r0 / 4 / row);
+            return launch_kv_append_q8(st, static_cast<const float *>(p0),
+                                       static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2),
+                                       static_cast<const uint32_t *>(p3), ntok, row, kernel->param);
+        }
+        case Kind::GemmI8:
+        case Kind::GemmI8Down:
+        case Kind::GemmI8Split: {
+            // bindings: 0 weights, 1 xq, 2 x_scales, 3 y (+4 partials for split-K);
+            // groups [M/64, N/16] (swizzled, M_TILES=4) — M from groups.
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)) ||
+                (rc = B.get(3, &p3, &r3)))
+                return rc;
+            const uint32_t m = groups[0] * 64;
+            const uint32_t n = kernel->n, k = kernel->k;
+            if (kernel->kind == Kind::GemmI8Down && groups[1] != n / 16)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups.y must be %u", kernel->name.c_str(), n / 16);
+            if (r1 && r1 < (uint64_t)m * k)
+                return fail(SGQ_ERR_VALIDATION, "%s: x binding too small for M=%u", kernel->name.c_str(), m);
+            if (r3 && r3 < (uint64_t)m * n * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: y binding too small", kernel->name.c_str());
+            uint32_t split = 1;
+            float *partials = nullptr;
+            if (kernel->kind == Kind::GemmI8Split) {
+                split = kernel->param;
+                if (split > 1) {
+                    if ((rc = B.get(4, &p4, &r4))) return rc;
+                    partials = static_cast<float *>(p4);
+                }
+            }
+            return launch_gemm_q4_0_q8(st, p0, static_cast<const int8_t *>(p1),
+                                       static_cast<const uint16_t *>(p2), static_cast<float *>(p3),
+                                       m, n, k, split, partials);
+        }
+    }
+    return fail(SGQ_ERR_LIBRARY, "unhandled kernel kind");
+}
+
+int sgq_graph_begin(sgq_ctx *ctx) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    if (!ctx->stream) SGQ_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    SGQ_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return SGQ_OK;
+}
+
+int sgq_graph_end(sgq_ctx *ctx, sgq_graph **out) {
+    if (!ctx || !out) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    if (!ctx->capturing) return fail(SGQ_ERR_VALIDATION, "no capture in progress");
+    auto *g = new sgq_graph;
+    ctx->capturing = false;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+    if (e != hipSuccess) {
+        delete g;
+        return check_hip(e, "hipStreamEndCapture");
+    }
+    e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g->graph);
+        delete g;
+        return check_hip(e, "hipGraphInstantiate");
+    }
+    *out = g;
+    return SGQ_OK;
+}
+
+int sgq_graph_submit(sgq_ctx *ctx, sgq_graph *graph) {
+    if (!ctx || !graph) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_HIP(hipGraphLaunch(graph->exec, ctx->stream));
+    return SGQ_OK;
+}
+
+int sgq_graph_destroy(sgq_graph *graph) {
+    if (!graph) return SGQ_OK;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+    return SGQ_OK;
+}
+
+}  // extern "C"
+
+namespace {
+__global__ void step_write_kernel(uint32_t *step, uint32_t a, uint32_t b, uint32_t c,
+                                  uint32_t d) {
+    const uint32_t t = threadIdx.x;
+    if (t < 4) step[t] = t == 0 ? a : t == 1 ? b : t == 2 ? c : d;
+}
+}  // namespace
+
+extern "C" {
+
+int sgq_step_write(sgq_ctx *ctx, void *step_dev, uint32_t pos, uint32_t kv_len_sliding,
+                   uint32_t kv_len_global, uint32_t q0) {
+    if (!ctx || !step_dev) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    hipLaunchKernelGGL(step_write_kernel, dim3(1), dim3(64), 0, ctx->stream,
+                       static_cast<uint32_t *>(step_dev), pos, kv_len_sliding, kv_len_global, q0);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int sgq_timer_start(sgq_ctx *ctx) {
+    if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    SGQ_HIP(hipEventRecord(ctx->t0, ctx->stream));
+    return SGQ_OK;
+}
+
+int sgq_timer_stop(sgq_ctx *ctx, float *ms) {
+    if (!ctx || !ms) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_HIP(hipEventRecord(ctx->t1, ctx->stream));
+    SGQ_HIP(hipEventSynchronize(ctx->t1));
+    SGQ_HIP(hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+    return SGQ_OK;
+}
+
+int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_t n,
+                  uint32_t k) {
+    if (!ctx || !w || !x || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_gemv_q4_0(ctx->stream, w, x, y, n, k);
+}
+
+int sgq_quant_q8_0(sgq_ctx *ctx, const float *x, uint16_t *scales, int8_t *quants, uint64_t n) {
+    if (!ctx || (n && (!x || !scales || !quants))) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_quant_q8_0(ctx->stream, x, scales, quants, n);
+}
+
+int sgq_dequant_q8_0(sgq_ctx *ctx, const uint16_t *scales, const int8_t *quants, float *out,
+                     uint64_t n) {
+    if (!ctx || (n && (!out || !scales || !quants))) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_dequant_q8_0(ctx->stream, scales, quants, out, n);
+}
+
+int sgq_gemm_q4_0_q8(sgq_ctx *ctx, const void *w, const int8_t *xq, const uint16_t *xs, float *y,
+                     uint32_t m, uint32_t n, uint32_t k, uint32_t split_k, float *partials) {
+    if (!ctx || !w || !xq || !xs || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_gemm_q4_0_q8(ctx->stream, w, xq, xs, y, m, n, k, split_k, partials);
+}
+
+int sgq_fill_q4_0_random(sgq_ctx *ctx, void *w, uint64_t n_blocks, uint64_t seed, float sigma) {
+    if (!ctx || (n_blocks && !w)) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_fill_q4_0(ctx->stream, w, n_blocks, seed, sigma);
+}
+
+int sgq_fill_normal(sgq_ctx *ctx, float *x, uint64_t n, uint64_t seed, float mean, float sigma) {
+    if (!ctx || (n && !x)) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_fill_normal(ctx->stream, x, n, seed, mean, sigma);
+}
+
+}  // extern "C"

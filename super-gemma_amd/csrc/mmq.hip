@@ -1,0 +1,297 @@
+// Prefill int8 MMQ GEMM for gfx950: Y[m×n] = Xq[m×k] · W[n×k]^T with the
+// per-32-block rescale of the reference's gemm_q4_0_i8 family
+// (crates/sg-gpu/shaders/gemm_q4_0_i8.wgsl:153-393; FFN-down variant
+// gemm_q4_0_i8_bb_pfd.wgsl): for every block b,
+//     Y[m,n] += (d_a[m,b] * d_w[n,b]) * f32( sum_j xq[m,32b+j] * (wq[n,32b+j]-8) )
+// where the i32 block dot is exact and the scale product of two f16 values
+// is exact in f32.
+//
+// Design:
+//  * One v_mfma_i32_32x32x32_i8 is exactly one Q4_0 block (K = 32) of a
+//    32×32 output tile: lane (r, h) = (lane%32, lane/32) feeds 16 K-bytes
+//    [16h, 16h+16) of row/column r.  For the weights that half is the low
+//    (h = 0) or high (h = 1) nibbles of the block's 16 qs bytes, so the
+//    logical K order of q4_0.rs:31-42 falls out with no shuffle.
+//  * Workgroup = 4 waves (2×2), tile 128×128, each wave 64×64 = 2×2 MFMA
+//    tiles.  A K-stage is 4 blocks (128 K): activations (int8) and weights
+//    (unpacked once per workgroup to int8 q-8 by the loading thread) go to
+//    LDS, rows padded to 144 B so the 16-byte fragment reads of 8 lanes hit
+//    32 distinct banks.  Double-buffered: stage s+1's global loads are in
+//    flight while stage s computes; one barrier per stage.
+//  * Rescale on the VALU: per output element and block, one cvt, one
+//    multiply (d_a·d_w), one FMA.  That — not the MFMA — bounds the kernel.
+//  * Tile order is XCD-aware: consecutive workgroup ids land on different
+//    XCDs (each with its own L2), so ids are remapped so that every XCD
+//    walks a contiguous range of N-tiles with all their M-tiles, and a
+//    weight strip is fetched from HBM once per XCD.
+//  * Split-K (slices of the block range, factor 1/2/4/8) writes fp32
+//    partial tiles; a second kernel sums them in fixed order s = 0..S-1.
+#include "sgq_internal.h"
+
+namespace sgq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 128, KB = 4;   // tile rows, cols, blocks per stage
+constexpr int ROWB = KB * 32 + 16;          // padded LDS row bytes (144)
+constexpr int kMWG = 256;
+
+struct Stage {
+    int8_t a[BM * ROWB];      // activations, [row][k]
+    int8_t b[BN * ROWB];      // weights (q-8), [col][k]
+    float da[KB][BM];         // activation scales, [block][row]
+    float dw[KB][BN];         // weight scales, [block][col]
+};
+
+__device__ __forceinline__ uint32_t unpack_lo(uint32_t q) {
+    return ((q & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;  // nibble-8 as int8
+}
+__device__ __forceinline__ uint32_t unpack_hi(uint32_t q) {
+    return (((q >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+}
+
+struct Prefetch {
+    uint4 a[4];        // 64 activation bytes: row = tid/2, k-half = tid%2
+    uint32_t w[9];     // two Q4_0 blocks (36 bytes): col = tid/2, blocks 2*(tid%2)+{0,1}
+    uint16_t da[4];    // threads < 128: 4 block scales of row tid
+};
+
+__device__ __forceinline__ void load_stage(Prefetch &pf, const int8_t *__restrict__ xq,
+                                           const uint16_t *__restrict__ xs,
+                                           const uint8_t *__restrict__ W, int m, int n, int k,
+                                           int nb, int m0, int n0, int b0, int b_end) {
+    const int t = threadIdx.x;
+    {   // activations: 64 contiguous bytes
+        const int row = t >> 1, half = t & 1;
+        const int gm = m0 + row;
+        const int kb = b0 * 32 + half * 64;  // first K index of this thread's 64 bytes
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int kk = kb + i * 16;
+            if (gm < m && kk < b_end * 32)
+                pf.a[i] = *reinterpret_cast<const uint4 *>(xq + (size_t)gm * k + kk);
+            else
+                pf.a[i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+    {   // weights: two blocks, 36 bytes, 4-aligned (b0 and the pair index are even)
+        const int col = t >> 1, pair = t & 1;
+        const int gn = n0 + col;
+        const int b = b0 + 2 * pair;
+        if (gn < n && b < b_end) {
+            const uint32_t *src =
+                reinterpret_cast<const uint32_t *>(W + ((size_t)gn * nb + b) * 18);
+            const bool two = b + 1 < b_end;
+#pragma unroll
+            for (int j = 0; j < 9; j++)
+                pf.w[j] = (j < 5 || two) ? __builtin_nontemporal_load(src + j) : 0u;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 9; j++) pf.w[j] = 0u;
+        }
+    }
+    if (t < BM) {
+        const int gm = m0 + t;
+#pragma unroll
+        for (int i = 0; i < KB; i++) {
+            const int b = b0 + i;
+            pf.da[i] = (gm < m && b < b_end) ? xs[(size_t)gm * nb + b] : (uint16_t)0;
+        }
+    }
+}
+
+__device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
+    const int t = threadIdx.x;
+    {
+        const int row = t >> 1, half = t & 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *reinterpret_cast<uint4 *>(&S.a[row * ROWB + half * 64 + i * 16]) = pf.a[i];
+    }
+    {
+        const int col = t >> 1, pair = t & 1;
+        // Block A: d in low half of w0, qs bytes = w0.hi .. w4.lo
+        uint32_t qa[4], qb[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            qa[j] = __builtin_amdgcn_alignbyte(pf.w[j + 1], pf.w[j], 2);
+            qb[j] = pf.w[5 + j];
+        }
+        int8_t *dst = &S.b[col * ROWB + pair * 64];
+        uint4 lo, hi;
+        lo = make_uint4(unpack_lo(qa[0]), unpack_lo(qa[1]), unpack_lo(qa[2]), unpack_lo(qa[3]));
+        hi = make_uint4(unpack_hi(qa[0]), unpack_hi(qa[1]), unpack_hi(qa[2]), unpack_hi(qa[3]));
+        *reinterpret_cast<uint4 *>(dst) = lo;
+        *reinterpret_cast<uint4 *>(dst + 16) = hi;
+        lo = make_uint4(unpack_lo(qb[0]), unpack_lo(qb[1]), unpack_lo(qb[2]), unpack_lo(qb[3]));
+        hi = make_uint4(unpack_hi(qb[0]), unpack_hi(qb[1]), unpack_hi(qb[2]), unpack_hi(qb[3]));
+        *reinterpret_cast<uint4 *>(dst + 32) = lo;
+        *reinterpret_cast<uint4 *>(dst + 48) = hi;
+        S.dw[2 * pair][col] = f16_bits_to_f32(pf.w[0] & 0xffffu);
+        S.dw[2 * pair + 1][col] = f16_bits_to_f32(pf.w[4] >> 16);
+    }
+    if (t < BM) {
+#pragma unroll
+        for (int i = 0; i < KB; i++) S.da[i][t] = f16_bits_to_f32(pf.da[i]);
+    }
+}
+
+__global__ __launch_bounds__(kMWG, 2) void mmq_kernel(const uint8_t *__restrict__ W,
+                                                      const int8_t *__restrict__ xq,
+                                                      const uint16_t *__restrict__ xs,
+                                                      float *__restrict__ out, int m, int n,
+                                                      int k, int mt, int nt, int split) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    Stage *stages = reinterpret_cast<Stage *>(smem);
+
+    // XCD-aware tile order (see header).
+    const int tiles = mt * nt;
+    int id = blockIdx.x;
+    const int xcds = 8;
+    if (tiles % xcds == 0) id = (id % xcds) * (tiles / xcds) + id / xcds;
+    const int tn = id / mt, tm = id % mt;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int nb = k / 32;
+    const int z = blockIdx.y;
+    const int b_beg = (int)((long)nb * z / split) & ~(KB - 1);
+    const int b_end = z + 1 == split ? nb : ((int)((long)nb * (z + 1) / split) & ~(KB - 1));
+    const int n_stages = (b_end - b_beg + KB - 1) / KB;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r = lane & 31, h = lane >> 5;
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[a][b][i] = 0.f;
+
+    Prefetch pf;
+    if (n_stages > 0) {
+        load_stage(pf, xq, xs, W, m, n, k, nb, m0, n0, b_beg, b_end);
+        store_stage(pf, stages[0]);
+    }
+    __syncthreads();
+
+    for (int s = 0; s < n_stages; s++) {
+        const bool more = s + 1 < n_stages;
+        if (more) load_stage(pf, xq, xs, W, m, n, k, nb, m0, n0, b_beg + (s + 1) * KB, b_end);
+        const Stage &S = stages[s & 1];
+#pragma unroll 1  // keeps the 4 live MFMA results + 64 accumulators within 256 VGPRs
+        for (int blk = 0; blk < KB; blk++) {
+            v4i af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                af[i] = *reinterpret_cast<const v4i *>(
+                    &S.a[(wm * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
+                bf[i] = *reinterpret_cast<const v4i *>(
+                    &S.b[(wn * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
+            }
+            float dwv[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) dwv[j] = S.dw[blk][wn * 64 + j * 32 + r];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                // rows of this lane: 8*(q/4) + 4*h + q%4, q = 0..15
+                float dav[16];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 t4 = *reinterpret_cast<const float4 *>(
+                        &S.da[blk][wm * 64 + i * 32 + 8 * g + 4 * h]);
+                    dav[4 * g] = t4.x;
+                    dav[4 * g + 1] = t4.y;
+                    dav[4 * g + 2] = t4.z;
+                    dav[4 * g + 3] = t4.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    v16i zero = {};
+                    v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 16; q++)
+                        acc[i][j][q] = __builtin_fmaf(dav[q] * dwv[j], (float)d[q], acc[i][j][q]);
+                }
+            }
+        }
+        if (more) store_stage(pf, stages[(s + 1) & 1]);
+        __syncthreads();
+    }
+
+    float *dst = out + (size_t)z * m * n;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + wn * 64 + j * 32 + r;
+            if (col >= n) continue;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int row = m0 + wm * 64 + i * 32 + 8 * (q / 4) + 4 * h + (q % 4);
+                if (row < m) dst[(size_t)row * n + col] = acc[i][j][q];
+            }
+        }
+}
+
+__global__ void splitk_reduce_kernel(const float4 *__restrict__ part, float4 *__restrict__ y,
+                                     uint64_t n4, int split) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float4 a = part[i];
+        for (int s = 1; s < split; s++) {
+            const float4 b = part[(uint64_t)s * n4 + i];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        y[i] = a;
+    }
+}
+
+}  // namespace
+
+int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
+                        float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
+                        float *partials) {
+    SGQ_CHECK(k % 64 == 0 && k > 0, "gemm_q4_0_q8: k=%u must be a positive multiple of 64", k);
+    SGQ_CHECK(m > 0 && n > 0, "gemm_q4_0_q8: empty shape");
+    SGQ_CHECK(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8,
+              "gemm_q4_0_q8: split_k=%u not in {1,2,4,8}", split_k);
+    SGQ_CHECK(split_k == 1 || partials != nullptr, "gemm_q4_0_q8: split_k>1 needs partials");
+    SGQ_CHECK(k % 16 == 0 && ((uintptr_t)xq & 15) == 0, "gemm_q4_0_q8: xq must be 16-byte aligned");
+    SGQ_CHECK(((uintptr_t)w & 3) == 0, "gemm_q4_0_q8: weights must be 4-byte aligned");
+    SGQ_CHECK((uint64_t)m * n < (1ull << 31) * 4, "gemm_q4_0_q8: output too large");
+    SGQ_CHECK(split_k == 1 || (m * (uint64_t)n) % 4 == 0, "gemm_q4_0_q8: m*n must be a multiple of 4 for split-K");
+    static bool attr = false;
+    const size_t lds = 2 * sizeof(Stage);
+    if (!attr) {
+        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr = true;
+    }
+    const int mt = (int)((m + BM - 1) / BM), nt = (int)((n + BN - 1) / BN);
+    float *dst = split_k == 1 ? y : partials;
+    hipLaunchKernelGGL(mmq_kernel, dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+                       static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k, mt,
+                       nt, (int)split_k);
+    SGQ_HIP(hipGetLastError());
+    if (split_k > 1) {
+        const uint64_t n4 = (uint64_t)m * n / 4;
+        uint64_t g = (n4 + 255) / 256;
+        if (g > (uint64_t)device_info().cus * 8) g = (uint64_t)device_info().cus * 8;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)g), dim3(256), 0, st,
+                           reinterpret_cast<const float4 *>(partials),
+                           reinterpret_cast<float4 *>(y), n4, (int)split_k);
+        SGQ_HIP(hipGetLastError());
+    }
+    return SGQ_OK;
+}
+
+}  // namespace sgq

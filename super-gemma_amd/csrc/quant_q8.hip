@@ -1,0 +1,153 @@
+// Q8_0 quantization / dequantization / KV append for gfx950.
+//
+// Semantics: kv_quant_q8 (crates/sg-gpu/shaders/kv_quant_q8.wgsl:30-57) and
+// kv_append_global_q8 (kv_append_global_q8.wgsl:29-60): per 32-element
+// block, amax in f32, d = amax * (1/127) (a multiply, so the f16 scale is
+// bit-exact), id = d > 0 ? 1/d : 0 from the unrounded d, scale = f16(d)
+// round-to-nearest-even, q = round_ties_even(x * id) as int8.  Unlike the
+// reference GPU (a 2.5-ulp reciprocal), 1/d here is the IEEE-correct
+// division hipcc emits by default, so the quants match the CPU oracle
+// bit for bit as well, not just within ±1.
+//
+// Layout: structure of arrays (the reference's page format): scales f16
+// [n/32], quants int8 [n] (4 per 32-bit word, element order).
+//
+// HBM-bound streaming op.  Eight lanes share a block, each holding one
+// float4: a wave reads 1 KB contiguous per load and writes 256 B of quants
+// per store (one dword per lane); amax is a 3-step butterfly inside each
+// 8-lane group.
+#include "sgq_internal.h"
+
+namespace sgq {
+namespace {
+
+constexpr int kQWG = 256;
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int pack_q(float a, float b, float c, float d, float id) {
+    int qa = (int)__builtin_rintf(a * id);
+    int qb = (int)__builtin_rintf(b * id);
+    int qc = (int)__builtin_rintf(c * id);
+    int qd = (int)__builtin_rintf(d * id);
+    return (qa & 0xff) | ((qb & 0xff) << 8) | ((qc & 0xff) << 16) | ((qd & 0xff) << 24);
+}
+
+// Quantize the float4 this lane holds; lanes 8g..8g+7 form block g.
+__device__ __forceinline__ void quant_lane(float4 v, int sub, uint16_t *scale_out,
+                                           int *quant_out) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, kWave));
+    const float d = amax * (1.0f / 127.0f);
+    const float id = d > 0.f ? 1.0f / d : 0.f;
+    *quant_out = pack_q(v.x, v.y, v.z, v.w, id);
+    if (sub == 0) *scale_out = f32_to_f16_bits(d);
+}
+
+__global__ __launch_bounds__(kQWG) void quant_q8_0_kernel(const float4 *__restrict__ x,
+                                                          uint16_t *__restrict__ scales,
+                                                          int *__restrict__ quants,
+                                                          uint64_t n4) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kQWG + threadIdx.x; i < n4;
+         i += (uint64_t)gridDim.x * kQWG) {
+        const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(x) + i);
+        float4 v = make_float4(t.x, t.y, t.z, t.w);
+        int q;
+        quant_lane(v, (int)(i & 7), &scales[i >> 3], &q);
+        quants[i] = q;
+    }
+}
+
+__global__ __launch_bounds__(kQWG) void dequant_q8_0_kernel(const uint16_t *__restrict__ scales,
+                                                            const int *__restrict__ quants,
+                                                            float4 *__restrict__ out,
+                                                            uint64_t n4) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kQWG + threadIdx.x; i < n4;
+         i += (uint64_t)gridDim.x * kQWG) {
+        const float d = f16_bits_to_f32(scales[i >> 3]);
+        const int q = quants[i];
+        float4 v;
+        v.x = d * (float)(int8_t)(q & 0xff);
+        v.y = d * (float)(int8_t)((q >> 8) & 0xff);
+        v.z = d * (float)(int8_t)((q >> 16) & 0xff);
+        v.w = d * (float)(int8_t)((q >> 24) & 0xff);
+        out[i] = v;
+    }
+}
+
+// kv_append_*_q8: token t of `src` ([n_tokens × row_len] fp32) is quantized
+// into slot (step[0] + t), or (step[0] + t) % ring when ring > 0.
+__global__ __launch_bounds__(kQWG) void kv_append_q8_kernel(const float4 *__restrict__ src,
+                                                            uint16_t *__restrict__ scales,
+                                                            int *__restrict__ quants,
+                                                            const uint32_t *__restrict__ step,
+                                                            uint64_t n4, uint32_t row4,
+                                                            uint32_t ring) {
+    const uint32_t pos = step[0];
+    for (uint64_t i = (uint64_t)blockIdx.x * kQWG + threadIdx.x; i < n4;
+         i += (uint64_t)gridDim.x * kQWG) {
+        const uint64_t t = i / row4;
+        const uint64_t c = i - t * row4;
+        uint64_t slot = pos + t;
+        if (ring) slot %= ring;
+        const uint64_t o = slot * row4 + c;
+        float4 v = src[i];
+        int q;
+        quant_lane(v, (int)(i & 7), &scales[o >> 3], &q);
+        quants[o] = q;
+    }
+}
+
+int grid_for(uint64_t n4) {
+    uint64_t g = (n4 + kQWG - 1) / kQWG;
+    const uint64_t cap = (uint64_t)device_info().cus * 8;
+    return (int)(g < cap ? (g ? g : 1) : cap);
+}
+
+}  // namespace
+
+int launch_quant_q8_0(hipStream_t st, const float *x, uint16_t *scales, int8_t *quants,
+                      uint64_t n) {
+    SGQ_CHECK(n % 32 == 0, "quant_q8_0: n=%llu must be a multiple of 32", (unsigned long long)n);
+    SGQ_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)quants & 3) == 0 &&
+                  ((uintptr_t)scales & 1) == 0,
+              "quant_q8_0: misaligned buffers");
+    if (n == 0) return SGQ_OK;
+    const uint64_t n4 = n / 4;
+    hipLaunchKernelGGL(quant_q8_0_kernel, dim3(grid_for(n4)), dim3(kQWG), 0, st,
+                       reinterpret_cast<const float4 *>(x), scales, reinterpret_cast<int *>(quants),
+                       n4);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_dequant_q8_0(hipStream_t st, const uint16_t *scales, const int8_t *quants, float *out,
+                        uint64_t n) {
+    SGQ_CHECK(n % 32 == 0, "dequant_q8_0: n must be a multiple of 32");
+    SGQ_CHECK(((uintptr_t)out & 15) == 0 && ((uintptr_t)quants & 3) == 0,
+              "dequant_q8_0: misaligned buffers");
+    if (n == 0) return SGQ_OK;
+    const uint64_t n4 = n / 4;
+    hipLaunchKernelGGL(dequant_q8_0_kernel, dim3(grid_for(n4)), dim3(kQWG), 0, st, scales,
+                       reinterpret_cast<const int *>(quants), reinterpret_cast<float4 *>(out), n4);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_kv_append_q8(hipStream_t st, const float *src, uint16_t *scales, int8_t *quants,
+                        const uint32_t *step, uint32_t n_tokens, uint32_t row_len,
+                        uint32_t ring) {
+    SGQ_CHECK(row_len % 32 == 0 && row_len > 0, "kv_append_q8: row_len must be a multiple of 32");
+    SGQ_CHECK(((uintptr_t)src & 15) == 0 && ((uintptr_t)quants & 3) == 0,
+              "kv_append_q8: misaligned buffers");
+    if (n_tokens == 0) return SGQ_OK;
+    const uint64_t n4 = (uint64_t)n_tokens * row_len / 4;
+    hipLaunchKernelGGL(kv_append_q8_kernel, dim3(grid_for(n4)), dim3(kQWG), 0, st,
+                       reinterpret_cast<const float4 *>(src), scales,
+                       reinterpret_cast<int *>(quants), step, n4, row_len / 4, ring);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+}  // namespace sgq

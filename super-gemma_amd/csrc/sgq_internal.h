@@ -1,0 +1,68 @@
+// Internal declarations shared by the libsgq translation units.
+// gfx950 (CDNA4) only: wave64, MFMA, v_dot4_i32_i8.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/sgq.h"
+
+namespace sgq {
+
+constexpr int kWave = 64;
+
+// Status plumbing: every entry point returns an sgq_status and leaves a
+// human-readable message in a thread-local buffer (sgq_last_error()).
+int fail(int status, const char *fmt, ...);
+int check_hip(hipError_t e, const char *what);
+#define SGQ_HIP(expr)                                            \
+    do {                                                         \
+        hipError_t _e = (expr);                                  \
+        if (_e != hipSuccess) return ::sgq::check_hip(_e, #expr); \
+    } while (0)
+#define SGQ_CHECK(cond, ...)                                          \
+    do {                                                              \
+        if (!(cond)) return ::sgq::fail(SGQ_ERR_VALIDATION, __VA_ARGS__); \
+    } while (0)
+
+// Launch-time device facts, cached per device ordinal.
+struct DeviceInfo {
+    int cus = 256;
+    int xcds = 8;
+};
+const DeviceInfo &device_info();
+
+hipStream_t ctx_stream(const sgq_ctx *ctx);
+
+// ---- kernel launchers (one per hot-path kernel family) ------------------
+int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
+                     uint32_t k);
+int launch_quant_q8_0(hipStream_t st, const float *x, uint16_t *scales, int8_t *quants,
+                      uint64_t n_elems);
+int launch_dequant_q8_0(hipStream_t st, const uint16_t *scales, const int8_t *quants, float *out,
+                        uint64_t n_elems);
+int launch_kv_append_q8(hipStream_t st, const float *src, uint16_t *scales, int8_t *quants,
+                        const uint32_t *step, uint32_t n_tokens, uint32_t row_len,
+                        uint32_t ring);
+int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
+                        float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
+                        float *partials);
+int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
+int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
+                       float sigma);
+
+}  // namespace sgq
+
+// ---- small device helpers -------------------------------------------------
+namespace sgq {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    // v_cvt_f16_f32 rounds to nearest even in the default FP mode.
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+}  // namespace sgq

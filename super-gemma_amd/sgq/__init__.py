@@ -1,0 +1,342 @@
+"""sgq — Python host mirror of super-gemma's sg-gpu dispatch surface over libsgq.
+
+The reference host API (crates/sg-gpu/src/lib.rs:20-44) is::
+
+    ctx = GpuContext::new()?;                    // NoDevice → tests skip
+    let k = ctx.load_kernel("gemv_q4_0_k5376")?; // UnknownKernel on a bad name
+    ctx.dispatch_blocking(&k, vec![BufferBinding::buffer(0, w), ...], push, groups)?;
+
+This module exposes the same calls (``GpuContext``, ``load_kernel``,
+``dispatch``, ``dispatch_blocking``, ``BufferBinding``, ``StepState``,
+``GraphRecorder``) with torch device tensors as buffers, plus the typed entry
+points of include/sgq.h.  Everything goes through the C ABI of
+``libsgq.so`` via ctypes; there is no Python or CPU fallback: if the library
+or a gfx950 device is missing, calls raise.
+
+torch is imported first so that libsgq binds to the HIP runtime torch
+already loaded (one runtime per process).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsgq.so")
+
+SGQ_OK = 0
+ERRORS = {
+    1: "Library",
+    2: "Hip",
+    3: "NoDevice",
+    4: "UnknownKernel",
+    5: "Pipeline",
+    6: "Validation",
+}
+
+
+class GpuError(RuntimeError):
+    """Mirrors sg_gpu::GpuError (crates/sg-gpu/src/lib.rs:31-44)."""
+
+    def __init__(self, code: int, msg: str):
+        self.code = code
+        self.kind = ERRORS.get(code, f"code{code}")
+        super().__init__(f"{self.kind}: {msg}")
+
+
+class NoDevice(GpuError):
+    pass
+
+
+class UnknownKernel(GpuError):
+    pass
+
+
+class ValidationError(GpuError):
+    pass
+
+
+_lib = None
+
+
+class _Info(C.Structure):
+    _fields_ = [("workgroup", C.c_uint32 * 3), ("bindings", C.c_uint32),
+                ("push_bytes", C.c_uint32), ("subgroup_size", C.c_uint32)]
+
+
+class _Binding(C.Structure):
+    _fields_ = [("binding", C.c_uint32), ("_pad", C.c_uint32), ("ptr", C.c_void_p),
+                ("offset", C.c_uint64), ("range", C.c_uint64)]
+
+
+# Exported symbols and their ctypes signatures (checked against include/sgq.h
+# by tests/test_abi.py).
+P, U32, U64, I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
+SIGNATURES = {
+    "sgq_last_error": (C.c_char_p, []),
+    "sgq_version": (C.c_char_p, []),
+    "sgq_ctx_create": (I, [I, C.POINTER(P)]),
+    "sgq_ctx_destroy": (I, [P]),
+    "sgq_ctx_set_stream": (I, [P, P]),
+    "sgq_sync": (I, [P]),
+    "sgq_buf_alloc": (I, [P, U64, C.POINTER(P)]),
+    "sgq_buf_free": (I, [P, P]),
+    "sgq_buf_upload": (I, [P, P, P, U64]),
+    "sgq_buf_download": (I, [P, P, P, U64]),
+    "sgq_buf_fill_zero": (I, [P, P, U64]),
+    "sgq_kernel_lookup": (I, [P, C.c_char_p, C.POINTER(P), C.POINTER(_Info)]),
+    "sgq_kernel_count": (U32, []),
+    "sgq_kernel_name": (C.c_char_p, [U32]),
+    "sgq_dispatch": (I, [P, P, C.POINTER(_Binding), U32, P, U32, C.POINTER(U32)]),
+    "sgq_graph_begin": (I, [P]),
+    "sgq_graph_end": (I, [P, C.POINTER(P)]),
+    "sgq_graph_submit": (I, [P, P]),
+    "sgq_graph_destroy": (I, [P]),
+    "sgq_step_write": (I, [P, P, U32, U32, U32, U32]),
+    "sgq_timer_start": (I, [P]),
+    "sgq_timer_stop": (I, [P, C.POINTER(C.c_float)]),
+    "sgq_gemv_q4_0": (I, [P, P, P, P, U32, U32]),
+    "sgq_quant_q8_0": (I, [P, P, P, P, U64]),
+    "sgq_dequant_q8_0": (I, [P, P, P, P, U64]),
+    "sgq_gemm_q4_0_q8": (I, [P, P, P, P, P, U32, U32, U32, U32, P]),
+    "sgq_fill_q4_0_random": (I, [P, P, U64, U64, C.c_float]),
+    "sgq_fill_normal": (I, [P, P, U64, U64, C.c_float, C.c_float]),
+}
+
+
+def lib():
+    """Load libsgq.so (built by super-gemma_amd/build.py); raises if absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GpuError(1, f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int):
+    if rc != SGQ_OK:
+        msg = lib().sgq_last_error().decode(errors="replace")
+        cls = {3: NoDevice, 4: UnknownKernel, 6: ValidationError}.get(rc, GpuError)
+        raise cls(rc, msg)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValidationError(6, "buffers must be device tensors")
+    if not t.is_contiguous():
+        raise ValidationError(6, "buffers must be contiguous")
+    return C.c_void_p(t.data_ptr())
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+@dataclass
+class Kernel:
+    """A looked-up variant: KernelBlob's name/workgroup/bindings/push_bytes."""
+    name: str
+    handle: C.c_void_p
+    workgroup: tuple
+    bindings: int
+    push_bytes: int
+
+    def groups_for(self, n: int):
+        """Kernel::groups_for (crates/sg-gpu/src/kernel.rs:56-58)."""
+        return [(n + self.workgroup[0] - 1) // self.workgroup[0], 1, 1]
+
+
+@dataclass
+class BufferBinding:
+    """BufferBinding{binding, buffer, offset, range} over a torch tensor."""
+    binding: int
+    buffer: torch.Tensor
+    offset: int = 0
+    range: Optional[int] = None
+
+    @staticmethod
+    def buffer(binding: int, t: torch.Tensor) -> "BufferBinding":
+        return BufferBinding(binding, t)
+
+
+@dataclass
+class StepState:
+    """StepState (crates/sg-gpu/src/graph.rs:33-61)."""
+    pos: int = 0
+    kv_len_sliding: int = 0
+    kv_len_global: int = 0
+    q0: int = 0
+
+
+class GpuContext:
+    """GpuContext over one gfx950 device; work goes on torch's current stream."""
+
+    def __init__(self, device: int = 0):
+        if not torch.cuda.is_available():
+            raise NoDevice(3, "no HIP device visible to torch")
+        h = C.c_void_p()
+        _check(lib().sgq_ctx_create(device, C.byref(h)))
+        self._h = h
+        self.device = device
+        self.set_stream(torch.cuda.current_stream(device))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and _lib is not None:
+            _lib.sgq_ctx_destroy(h)
+            self._h = None
+
+    @property
+    def handle(self):
+        return self._h
+
+    def set_stream(self, stream: torch.cuda.Stream):
+        _check(lib().sgq_ctx_set_stream(self._h, C.c_void_p(stream.cuda_stream)))
+
+    def synchronize(self):
+        _check(lib().sgq_sync(self._h))
+
+    # -- kernel registry / dispatch (the reference's name-based surface) --
+    def load_kernel(self, name: str) -> Kernel:
+        h = C.c_void_p()
+        info = _Info()
+        _check(lib().sgq_kernel_lookup(self._h, name.encode(), C.byref(h), C.byref(info)))
+        return Kernel(name, h, tuple(info.workgroup), info.bindings, info.push_bytes)
+
+    def dispatch(self, kernel: Kernel, bindings: Sequence[BufferBinding], push: Optional[bytes],
+                 groups: Sequence[int]):
+        arr = (_Binding * max(1, len(bindings)))()
+        keep = []
+        for i, b in enumerate(bindings):
+            nbytes = _nbytes(b.buffer)
+            rng = b.range if b.range is not None else nbytes - b.offset
+            if b.offset + rng > nbytes:
+                raise ValidationError(6, f"binding {b.binding}: range past the end of the buffer")
+            arr[i] = _Binding(b.binding, 0, _ptr(b.buffer), b.offset, rng)
+            keep.append(b.buffer)
+        pb = push or b""
+        pbuf = C.create_string_buffer(pb, len(pb)) if pb else None
+        g = (C.c_uint32 * 3)(*[int(v) for v in groups])
+        _check(lib().sgq_dispatch(self._h, kernel.handle, arr, len(bindings),
+                                  C.cast(pbuf, C.c_void_p) if pbuf else None, len(pb), g))
+
+    def dispatch_blocking(self, kernel, bindings, push, groups):
+        """crates/sg-gpu/src/exec.rs:9-23: record one dispatch, submit, wait."""
+        self.dispatch(kernel, bindings, push, groups)
+        self.synchronize()
+
+    def step_write(self, step_buf: torch.Tensor, s: StepState):
+        _check(lib().sgq_step_write(self._h, _ptr(step_buf), s.pos, s.kv_len_sliding,
+                                    s.kv_len_global, s.q0))
+
+    # -- typed entry points -------------------------------------------------
+    def gemv_q4_0(self, w: torch.Tensor, x: torch.Tensor, y: torch.Tensor, n: int, k: int):
+        _need(w, torch.uint8, n * (k // 32) * 18, "w")
+        _need(x, torch.float32, k, "x")
+        _need(y, torch.float32, n, "y")
+        _check(lib().sgq_gemv_q4_0(self._h, _ptr(w), _ptr(x), _ptr(y), n, k))
+
+    def quant_q8_0(self, x: torch.Tensor, scales: torch.Tensor, quants: torch.Tensor):
+        n = x.numel()
+        _need(x, torch.float32, n, "x")
+        _need(scales, (torch.uint16, torch.int16, torch.float16), n // 32, "scales")
+        _need(quants, torch.int8, n, "quants")
+        _check(lib().sgq_quant_q8_0(self._h, _ptr(x), _ptr(scales), _ptr(quants), n))
+
+    def dequant_q8_0(self, scales, quants, out):
+        n = quants.numel()
+        _need(out, torch.float32, n, "out")
+        _need(scales, (torch.uint16, torch.int16, torch.float16), n // 32, "scales")
+        _check(lib().sgq_dequant_q8_0(self._h, _ptr(scales), _ptr(quants), _ptr(out), n))
+
+    def gemm_q4_0_q8(self, w, xq, xs, y, m, n, k, split_k=1, partials=None):
+        _need(w, torch.uint8, n * (k // 32) * 18, "w")
+        _need(xq, torch.int8, m * k, "xq")
+        _need(xs, (torch.uint16, torch.int16, torch.float16), m * (k // 32), "xs")
+        _need(y, torch.float32, m * n, "y")
+        if split_k > 1:
+            _need(partials, torch.float32, split_k * m * n, "partials")
+        _check(lib().sgq_gemm_q4_0_q8(self._h, _ptr(w), _ptr(xq), _ptr(xs), _ptr(y), m, n, k,
+                                      split_k, _ptr(partials)))
+
+    def fill_q4_0_random(self, w: torch.Tensor, n_blocks: int, seed: int, sigma: float = 0.02):
+        _need(w, torch.uint8, n_blocks * 18, "w")
+        _check(lib().sgq_fill_q4_0_random(self._h, _ptr(w), n_blocks, seed, sigma))
+
+    def fill_normal(self, x: torch.Tensor, seed: int, mean: float = 0.0, sigma: float = 1.0):
+        _need(x, torch.float32, x.numel(), "x")
+        _check(lib().sgq_fill_normal(self._h, _ptr(x), x.numel(), seed, mean, sigma))
+
+    # -- timing -------------------------------------------------------------
+    def timer_start(self):
+        _check(lib().sgq_timer_start(self._h))
+
+    def timer_stop(self) -> float:
+        ms = C.c_float()
+        _check(lib().sgq_timer_stop(self._h, C.byref(ms)))
+        return ms.value
+
+
+class Graph:
+    """A recorded, re-submittable command graph (CommandGraph)."""
+
+    def __init__(self, ctx: GpuContext, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def submit(self):
+        _check(lib().sgq_graph_submit(self.ctx.handle, self.handle))
+
+    def __del__(self):
+        if getattr(self, "handle", None) is not None and _lib is not None:
+            _lib.sgq_graph_destroy(self.handle)
+            self.handle = None
+
+
+class GraphRecorder:
+    """Context manager capturing every dispatch on ctx's stream into a Graph.
+
+    The context's stream must not be the null stream while recording; use a
+    side torch stream (``with torch.cuda.stream(s): ctx.set_stream(s)``).
+    """
+
+    def __init__(self, ctx: GpuContext):
+        self.ctx = ctx
+        self.graph: Optional[Graph] = None
+
+    def __enter__(self):
+        _check(lib().sgq_graph_begin(self.ctx.handle))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = C.c_void_p()
+        rc = lib().sgq_graph_end(self.ctx.handle, C.byref(h))
+        if exc_type is None:
+            _check(rc)
+            self.graph = Graph(self.ctx, h)
+        return False
+
+
+def _need(t, dtypes, numel, name):
+    if t is None:
+        raise ValidationError(6, f"{name} is required")
+    if not isinstance(dtypes, tuple):
+        dtypes = (dtypes,)
+    if t.dtype not in dtypes:
+        raise ValidationError(6, f"{name}: dtype {t.dtype} not in {dtypes}")
+    if t.numel() < numel:
+        raise ValidationError(6, f"{name}: {t.numel()} elements < required {numel}")
+    if not t.is_contiguous():
+        raise ValidationError(6, f"{name}: must be contiguous")

@@ -1,0 +1,75 @@
+"""CPU checks of the C ABI: libsgq.so loads, exports exactly what
+include/sgq.h declares, and the host-side validation paths fail loudly.
+No compute runs here (no GPU in this container)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sgq.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sgq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import sgq
+
+    assert os.path.exists(sgq.LIB_PATH), "libsgq.so not built"
+    L = C.CDLL(sgq.LIB_PATH)
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, f"declared but not exported: {missing}"
+    # the Python mirror binds every declared symbol with a signature
+    assert set(syms) == set(sgq.SIGNATURES), set(syms) ^ set(sgq.SIGNATURES)
+
+
+def test_exports_are_c_abi_and_gfx950_only():
+    import sgq
+
+    out = subprocess.run(["nm", "-D", "--defined-only", sgq.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert all(s in exported for s in declared_symbols())
+    # code objects: gfx950 only
+    blob = open(sgq.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in blob
+
+
+def test_registry_names_resolve_without_device():
+    import sgq
+
+    L = sgq.lib()
+    names = [L.sgq_kernel_name(i).decode() for i in range(L.sgq_kernel_count())]
+    assert "gemv_q4_0_k5376" in names and "kv_quant_q8" in names
+    assert "gemm_q4_0_i8_swz_m4n1_k5376_n21504" in names and "gemm_q4_0_i8_bb_pfd4" in names
+    for n in names:
+        h = C.c_void_p()
+        info = sgq._Info()
+        rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
+        assert rc == 0, (n, L.sgq_last_error())
+        assert info.bindings >= 3
+    rc = L.sgq_kernel_lookup(None, b"gemv_q6_k_logits_nonexistent", C.byref(h), C.byref(info))
+    assert rc == 4 and b"unknown kernel" in L.sgq_last_error()
+
+
+def test_ctx_create_without_device_reports_no_device():
+    import torch
+    import sgq
+
+    if torch.cuda.is_available():
+        pytest.skip("device present")
+    h = C.c_void_p()
+    rc = sgq.lib().sgq_ctx_create(0, C.byref(h))
+    assert rc == 3  # NoDevice: callers skip, as GpuContext::new's error does
+    with pytest.raises(sgq.NoDevice):
+        sgq.GpuContext(0)

@@ -1,0 +1,147 @@
+"""GPU parity: Q4_0 GEMV (libsgq) vs the f64 CPU oracle.
+
+Template: crates/sg-gpu/tests/parity_gemv.rs (seeded xorshift64* inputs,
+random_q4_0 weights, f64 reference over sampled rows, bit-determinism).
+Tolerance: fp32 output within 1e-3 relative (BASELINE) — asserted as
+|err| <= 1e-3*|want| + 1e-4*rms(want) per element, and the normwise error
+max|err|/max|want| <= 2e-6 (the kernel's x limbs are fp32-grade).
+"""
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close, dev, empty, host, rel_err, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+# (K, N): BASELINE config 1, the decoder's matmul sites at the BASELINE shape,
+# and the reference's Gemma shapes (parity_gemv.rs:72-82).
+SHAPES = [
+    (5376, 21504),   # config 1 / FFN gate, up
+    (5376, 4096),    # q proj
+    (5376, 2048),    # k / v proj
+    (4096, 5376),    # o proj
+    (21504, 5376),   # down proj
+    (5376, 8192),    # reference sliding q
+    (8192, 5376),    # reference sliding o
+    (16384, 5376),   # reference global o
+]
+
+
+def _inputs(oracle, seed, n, k):
+    rng = oracle.Rng(seed)
+    w = rng.random_q4_0(n * k // 32)
+    x = oracle.through_f16(rng.f32_vec(k))
+    return w, x
+
+
+def _check(oracle, w, x, y, n, k):
+    rows = sample_rows(n)
+    want = oracle.gemv_rows(w, x, k, rows)
+    got = y[rows]
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert_close(got, want, 1e-3, 1e-4 * rms, f"gemv k={k} n={n}")
+    assert rel_err(got, want) <= 2e-6, rel_err(got, want)
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_gemv_matches_oracle(ctx, oracle, k, n):
+    print(f"gemv parity k={k} n={n}", flush=True)
+    w, x = _inputs(oracle, 0x6E44 + k + n, n, k)
+    tw, tx, ty = dev(w), dev(x), empty(n, torch.float32)
+    ctx.gemv_q4_0(tw, tx, ty, n, k)
+    torch.cuda.synchronize()
+    _check(oracle, w, x, host(ty), n, k)
+
+
+@pytest.mark.parametrize("k,n", [(64, 1), (128, 37), (192, 5), (320, 333), (1536, 63),
+                                 (6144, 130), (6208, 9), (12352, 17), (24640, 3), (65536, 11)])
+def test_gemv_ragged_shapes(ctx, oracle, k, n):
+    """Edge shapes: one row, row counts not a multiple of the per-wave tile,
+    K at each slice/blocks-per-lane boundary, the 65536 maximum."""
+    print(f"gemv ragged k={k} n={n}", flush=True)
+    w, x = _inputs(oracle, 0xAB + k * 7 + n, n, k)
+    ty = empty(n, torch.float32)
+    ctx.gemv_q4_0(dev(w), dev(x), ty, n, k)
+    torch.cuda.synchronize()
+    got = host(ty)
+    want = oracle.gemv_rows(w, x, k, np.arange(n))
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert_close(got, want, 1e-3, 1e-4 * rms, f"gemv k={k} n={n}")
+
+
+def test_gemv_baseline_distribution_full_rows(ctx, oracle):
+    """BASELINE config 1 (K=5376, N=21504) on its own synthetic distribution
+    (d = f16(|N(0,0.02)|), uniform nibbles, x ~ N(0,1)) generated on the
+    device, checked on EVERY row against the oracle."""
+    k, n = 5376, 21504
+    tw = empty(n * k // 32 * 18, torch.uint8)
+    tx = empty(k, torch.float32)
+    ctx.fill_q4_0_random(tw, n * k // 32, seed=1234, sigma=0.02)
+    ctx.fill_normal(tx, seed=99)
+    ty = empty(n, torch.float32)
+    ctx.gemv_q4_0(tw, tx, ty, n, k)
+    torch.cuda.synchronize()
+    w, x, y = host(tw), host(tx), host(ty)
+    d = w.reshape(-1, 18)[:, :2].copy().view(np.float16).astype(np.float32)
+    assert (d >= 0).all() and 0.01 < float(d.mean()) < 0.03  # |N(0, 0.02)| has mean 0.016
+    assert abs(float(x.mean())) < 0.05 and 0.9 < float(x.std()) < 1.1
+    want = oracle.gemv_rows(w, x, k, np.arange(n))
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert_close(y, want, 1e-3, 1e-4 * rms, "gemv config 1")
+    assert rel_err(y, want) <= 2e-6
+
+
+def test_gemv_is_bit_deterministic(ctx, oracle):
+    """parity_gemv.rs:181-219: two runs, identical bits."""
+    k, n = 21504, 5376
+    w, x = _inputs(oracle, 0xD0, n, k)
+    tw, tx = dev(w), dev(x)
+    a, b = empty(n, torch.float32), empty(n, torch.float32)
+    ctx.gemv_q4_0(tw, tx, a, n, k)
+    ctx.gemv_q4_0(tw, tx, b, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_gemv_name_dispatch_matches_typed(ctx, oracle):
+    """The reference surface: load_kernel(variant) + dispatch(bindings 0..2,
+    groups [N,1,1]) gives the typed entry point's bits; the generic variant
+    takes K as a 4-byte push constant."""
+    import sgq
+
+    k, n = 5376, 4096
+    w, x = _inputs(oracle, 0x6E45, n, k)
+    tw, tx = dev(w), dev(x)
+    ref = empty(n, torch.float32)
+    ctx.gemv_q4_0(tw, tx, ref, n, k)
+    kern = ctx.load_kernel("gemv_q4_0_k5376")
+    assert kern.bindings == 3 and kern.push_bytes == 0 and kern.workgroup[0] == 64
+    y1 = empty(n, torch.float32)
+    ctx.dispatch_blocking(kern, [sgq.BufferBinding.buffer(0, tw), sgq.BufferBinding.buffer(1, tx),
+                                 sgq.BufferBinding.buffer(2, y1)], None, [n, 1, 1])
+    gen = ctx.load_kernel("gemv_q4_0_generic")
+    y2 = empty(n, torch.float32)
+    ctx.dispatch_blocking(gen, [sgq.BufferBinding.buffer(0, tw), sgq.BufferBinding.buffer(1, tx),
+                                sgq.BufferBinding.buffer(2, y2)], struct.pack("<I", k), [n, 1, 1])
+    torch.cuda.synchronize()
+    assert torch.equal(ref, y1) and torch.equal(ref, y2)
+    with pytest.raises(sgq.UnknownKernel):
+        ctx.load_kernel("gemv_q4_0_k5377")
+    with pytest.raises(sgq.ValidationError):  # binding too small for N rows
+        ctx.dispatch(kern, [sgq.BufferBinding.buffer(0, tw), sgq.BufferBinding.buffer(1, tx),
+                            sgq.BufferBinding.buffer(2, y1)], None, [2 * n, 1, 1])
+
+
+def test_gemv_rejects_bad_shapes(ctx):
+    import sgq
+
+    w = empty(18 * 4, torch.uint8)
+    x = empty(128, torch.float32)
+    y = empty(2, torch.float32)
+    with pytest.raises(sgq.ValidationError):
+        ctx.gemv_q4_0(w, x, y, 1, 96)  # K not a multiple of 64
+    with pytest.raises(sgq.ValidationError):
+        ctx.gemv_q4_0(w, x, y, 2, 128)  # W too small for N=2
