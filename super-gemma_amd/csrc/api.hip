@@ -19,6 +19,7 @@
 struct sgq_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    void *workspace = nullptr;  // per-context scratch (GEMV x limb table)
     bool capturing = false;
     hipEvent_t t0 = nullptr, t1 = nullptr;
 };
@@ -61,6 +62,7 @@ const DeviceInfo &device_info() {
 }
 
 hipStream_t ctx_stream(const sgq_ctx *ctx) { return ctx ? ctx->stream : nullptr; }
+void *ctx_workspace(const sgq_ctx *ctx) { return ctx ? ctx->workspace : nullptr; }
 
 }  // namespace sgq
 
@@ -219,9 +221,11 @@ int sgq_ctx_create(int device, sgq_ctx **out) {
                     p.gcnArchName);
     auto *c = new sgq_ctx;
     c->device = device;
-    if (hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess) {
-        delete c;
-        return fail(SGQ_ERR_HIP, "hipEventCreate failed");
+    if (hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess ||
+        hipMalloc(&c->workspace, kGemvWorkspace) != hipSuccess) {
+        sgq_ctx_destroy(c);
+        return fail(SGQ_ERR_HIP, "context resources (events / %zu-byte workspace) failed",
+                    kGemvWorkspace);
     }
     *out = c;
     return SGQ_OK;
@@ -231,6 +235,7 @@ int sgq_ctx_destroy(sgq_ctx *ctx) {
     if (!ctx) return SGQ_OK;
     if (ctx->t0) (void)hipEventDestroy(ctx->t0);
     if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+    if (ctx->workspace) (void)hipFree(ctx->workspace);
     delete ctx;
     return SGQ_OK;
 }
@@ -339,7 +344,7 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             if (r2 && r2 < (uint64_t)n * 4)
                 return fail(SGQ_ERR_VALIDATION, "%s: y binding too small", kernel->name.c_str());
             return launch_gemv_q4_0(st, p0, static_cast<const float *>(p1), static_cast<float *>(p2),
-                                    n, k);
+                                    n, k, ctx->workspace);
         }
         case Kind::QuantQ8: {
             // bindings: 0 src fp32, 1 scales f16, 2 quants; blocks = arrayLength(src)/32
@@ -487,7 +492,7 @@ int sgq_timer_stop(sgq_ctx *ctx, float *ms) {
 int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_t n,
                   uint32_t k) {
     if (!ctx || !w || !x || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
-    return launch_gemv_q4_0(ctx->stream, w, x, y, n, k);
+    return launch_gemv_q4_0(ctx->stream, w, x, y, n, k, ctx->workspace);
 }
 
 int sgq_quant_q8_0(sgq_ctx *ctx, const float *x, uint16_t *scales, int8_t *quants, uint64_t n) {

