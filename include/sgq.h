@@ -145,6 +145,20 @@ int sgq_gemm_q4_0_q8(sgq_ctx *ctx, const void *w, const int8_t *xq, const uint16
                      float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
                      float *partials);
 
+/* Split-K decode attention over a Q8_0 KV cache: attn_decode_global_q8k /
+ * attn_decode_sliding + attn_reduce (crates/sg-gpu/shaders/
+ * attn_decode_global_q8k.wgsl:41-112, attn_reduce.wgsl:24-57), with V in
+ * Q8_0 as well.  q [n_q_heads × head_dim] fp32; cache quants
+ * [slot × n_kv_heads × head_dim] int8 and scales [slot × n_kv_heads ×
+ * head_dim/32] f16 for K and V; slots 0..kv_len-1 are attended in physical
+ * order (a linear cache or a full/partial ring); out [n_q_heads × head_dim].
+ * Query head h reads kv head h / (n_q_heads / n_kv_heads).  The n_splits
+ * chunks are merged in split order inside the same launch.  head_dim 128. */
+int sgq_attn_decode_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
+                       const uint16_t *k_scales, const int8_t *v_quants, const uint16_t *v_scales,
+                       uint32_t kv_len, uint32_t n_q_heads, uint32_t n_kv_heads,
+                       uint32_t head_dim, uint32_t n_splits, float scale, float *out);
+
 /* ---- synthetic inputs (not on the hot path; for benches and tests) ------ */
 /* Q4_0 blocks with d = f16(|N(0, sigma)|) and uniform nibble bytes, from a
  * counter-based generator keyed by (seed, block index). */

@@ -222,10 +222,11 @@ int sgq_ctx_create(int device, sgq_ctx **out) {
     auto *c = new sgq_ctx;
     c->device = device;
     if (hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess ||
-        hipMalloc(&c->workspace, kGemvWorkspace) != hipSuccess) {
+        hipMalloc(&c->workspace, kWorkspaceBytes) != hipSuccess ||
+        hipMemset(c->workspace, 0, kWorkspaceBytes) != hipSuccess) {
         sgq_ctx_destroy(c);
         return fail(SGQ_ERR_HIP, "context resources (events / %zu-byte workspace) failed",
-                    kGemvWorkspace);
+                    kWorkspaceBytes);
     }
     *out = c;
     return SGQ_OK;
@@ -510,6 +511,17 @@ int sgq_gemm_q4_0_q8(sgq_ctx *ctx, const void *w, const int8_t *xq, const uint16
                      uint32_t m, uint32_t n, uint32_t k, uint32_t split_k, float *partials) {
     if (!ctx || !w || !xq || !xs || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     return launch_gemm_q4_0_q8(ctx->stream, w, xq, xs, y, m, n, k, split_k, partials);
+}
+
+int sgq_attn_decode_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
+                       const uint16_t *k_scales, const int8_t *v_quants, const uint16_t *v_scales,
+                       uint32_t kv_len, uint32_t n_q_heads, uint32_t n_kv_heads,
+                       uint32_t head_dim, uint32_t n_splits, float scale, float *out) {
+    if (!ctx || !q || !k_quants || !k_scales || !v_quants || !v_scales || !out)
+        return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_attn_decode_q8(ctx->stream, q, k_quants, k_scales, v_quants, v_scales, nullptr, 0,
+                                 kv_len, (int)n_q_heads, (int)n_kv_heads, (int)head_dim,
+                                 (int)n_splits, scale, out, ctx->workspace, kWorkspaceBytes);
 }
 
 int sgq_fill_q4_0_random(sgq_ctx *ctx, void *w, uint64_t n_blocks, uint64_t seed, float sigma) {

@@ -1,0 +1,265 @@
+// Q8_0-KV attention for gfx950: split-K decode.
+//
+// Semantics: attn_decode_global_q8k / attn_decode_sliding + attn_reduce
+// (crates/sg-gpu/shaders/attn_decode_global_q8k.wgsl:41-112,
+// attn_reduce.wgsl:24-57): for each query head h (GQA: kv head h/QPK),
+// s_t = scale · q_h·k_t over the valid cache slots t < kv_len (physical
+// order), softmax, out_h = Σ p_t v_t.  K and V are Q8_0 pages in the
+// structure-of-arrays format (int8 quants [slot × n_kv × hd], f16 scales
+// [slot × n_kv × hd/32], 32-blocks along head_dim), dequantized on the fly
+// as f16(d)·q — the reference keeps V in f16; here both K and V are Q8_0.
+//
+// Design (HBM-bound: 2·(hd + hd/16) bytes per slot and kv head against
+// ~QPK·4·hd flops):
+//  * Grid [n_kv, n_splits]: each workgroup streams one kv head's slots of one
+//    contiguous chunk, 256 slots at a time: thread i scores slot i for all
+//    QPK query heads (K row = 128 B = one cache line; q from LDS,
+//    broadcast), the sub-chunk's scores go through an online softmax
+//    (m, l, rescaled acc), and PV runs with thread (head, 4-dim word, slot
+//    group) so that a wave reads whole V rows.
+//  * Splits are merged without a second launch: each workgroup writes its
+//    (acc, m, l) partial, and the last workgroup of a kv head to finish
+//    (device-scope atomic on a per-head counter, which it resets) merges
+//    the partials in split order 0..S-1 — the same fixed order as
+//    attn_reduce.wgsl:40-52, so results do not depend on which workgroup
+//    merged.  Empty splits carry (m = -3e38, l = 0, acc = 0).
+#include "sgq_internal.h"
+
+namespace sgq {
+namespace {
+
+constexpr int kHD = 128;
+constexpr int kAWG = 256;
+constexpr int kSub = 256;             // slots scored per pass
+constexpr float kNegBig = -3.0e38f;
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < kAWG / kWave; w++) r += red[w];
+    return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < kAWG / kWave; w++) r = fmaxf(r, red[w]);
+    return r;
+}
+
+// Dequantized dot of a 128-wide K row (int8 + 4 f16 scales) with q (LDS).
+__device__ __forceinline__ float k_row_dot(const int4 (&kr)[8], const float (&ksc)[4],
+                                           const float *qs) {
+    float s = 0.f;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        float part = 0.f;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int4 v = kr[2 * b + c];
+            const int w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(qs + 32 * b + 16 * c + 4 * e);
+                part = __builtin_fmaf(q4.x, (float)(int8_t)(w[e] & 0xff), part);
+                part = __builtin_fmaf(q4.y, (float)(int8_t)((w[e] >> 8) & 0xff), part);
+                part = __builtin_fmaf(q4.z, (float)(int8_t)((w[e] >> 16) & 0xff), part);
+                part = __builtin_fmaf(q4.w, (float)(int8_t)((w[e] >> 24) & 0xff), part);
+            }
+        }
+        s = __builtin_fmaf(ksc[b], part, s);
+    }
+    return s;
+}
+
+template <int QPK>
+__global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
+    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
+    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
+    const uint32_t *__restrict__ step, int step_word, uint32_t kv_len_direct, int n_kv,
+    int n_splits, float scale, float *__restrict__ part, unsigned *__restrict__ counters,
+    float *__restrict__ out) {
+    constexpr int G = kAWG / (QPK * (kHD / 4));  // slot groups in the PV phase
+    static_assert(G >= 1, "QPK too large for one workgroup");
+    __shared__ __align__(16) float q_s[QPK][kHD];
+    __shared__ float s_s[QPK][kSub];     // scores, then probabilities
+    __shared__ float vs_s[kSub][kHD / 32];  // V scales of the sub-chunk
+    __shared__ float red[kAWG / kWave];
+    __shared__ float acc_s[G][QPK][kHD];
+    __shared__ int last_s;
+
+    const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+    const uint32_t kv_len = step ? step[step_word] : kv_len_direct;
+    const uint32_t chunk = (kv_len + n_splits - 1) / n_splits;
+    const uint32_t t_begin = min((uint32_t)split * chunk, kv_len);
+    const uint32_t t_end = min(t_begin + chunk, kv_len);
+
+    for (int i = tid; i < QPK * kHD; i += kAWG)
+        q_s[i / kHD][i % kHD] = q[(size_t)(kvh * QPK) * kHD + i];
+
+    // PV thread role: head ph, 4-dim word pw, slot group pg
+    const int ph = tid / (kHD / 4) % QPK, pw = tid % (kHD / 4), pg = tid / (QPK * kHD / 4);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float m_run[QPK], l_run[QPK];
+#pragma unroll
+    for (int h = 0; h < QPK; h++) {
+        m_run[h] = kNegBig;
+        l_run[h] = 0.f;
+    }
+    __syncthreads();
+
+    for (uint32_t base = t_begin; base < t_end; base += kSub) {
+        const int n_here = (int)min((uint32_t)kSub, t_end - base);
+        // ---- scores: thread tid scores slot base + tid for every head
+        {
+            const int t = tid;
+            float sc[QPK];
+            if (t < n_here) {
+                const size_t row = (size_t)(base + t) * n_kv + kvh;
+                const int4 *kp = reinterpret_cast<const int4 *>(kq + row * kHD);
+                int4 kr[8];
+#pragma unroll
+                for (int c = 0; c < 8; c++) kr[c] = kp[c];
+                const uint2 kss = *reinterpret_cast<const uint2 *>(ks + row * (kHD / 32));
+                const uint2 vss = *reinterpret_cast<const uint2 *>(vs + row * (kHD / 32));
+                const float ksc[4] = {f16_bits_to_f32(kss.x & 0xffff), f16_bits_to_f32(kss.x >> 16),
+                                      f16_bits_to_f32(kss.y & 0xffff), f16_bits_to_f32(kss.y >> 16)};
+                vs_s[t][0] = f16_bits_to_f32(vss.x & 0xffff);
+                vs_s[t][1] = f16_bits_to_f32(vss.x >> 16);
+                vs_s[t][2] = f16_bits_to_f32(vss.y & 0xffff);
+                vs_s[t][3] = f16_bits_to_f32(vss.y >> 16);
+#pragma unroll
+                for (int h = 0; h < QPK; h++) sc[h] = k_row_dot(kr, ksc, q_s[h]) * scale;
+            } else {
+#pragma unroll
+                for (int h = 0; h < QPK; h++) sc[h] = kNegBig;
+            }
+            // ---- online softmax over this sub-chunk, per head
+#pragma unroll
+            for (int h = 0; h < QPK; h++) {
+                const float mx = block_max(sc[h], red);
+                const float m_new = fmaxf(m_run[h], mx);
+                const float p = t < n_here ? __expf(sc[h] - m_new) : 0.f;
+                s_s[h][t] = p;
+                const float corr = __expf(m_run[h] - m_new);
+                m_run[h] = m_new;
+                if (h == ph) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[e] *= corr;
+                }
+                l_run[h] = l_run[h] * corr + block_sum(p, red);  // fixed-order tree sum
+            }
+        }
+        __syncthreads();
+        // ---- PV: thread (ph, pw, pg) accumulates slots pg, pg+G, ...
+        for (int i = pg; i < n_here; i += G) {
+            const size_t row = (size_t)(base + i) * n_kv + kvh;
+            const int v4 = *reinterpret_cast<const int *>(vq + row * kHD + 4 * pw);
+            const float pp = s_s[ph][i] * vs_s[i][pw / 8];
+            acc[0] = __builtin_fmaf(pp, (float)(int8_t)(v4 & 0xff), acc[0]);
+            acc[1] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 8) & 0xff), acc[1]);
+            acc[2] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 16) & 0xff), acc[2]);
+            acc[3] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 24) & 0xff), acc[3]);
+        }
+        __syncthreads();  // s_s / vs_s reused by the next sub-chunk
+    }
+
+    // ---- combine the G slot groups (fixed order) and write the partial
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc_s[pg][ph][4 * pw + e] = acc[e];
+    __syncthreads();
+    const int stride = kHD + 2;
+    for (int i = tid; i < QPK * kHD; i += kAWG) {
+        const int h = i / kHD, d = i % kHD;
+        float a = 0.f;
+        for (int g = 0; g < G; g++) a += acc_s[g][h][d];
+        part[((size_t)(kvh * QPK + h) * n_splits + split) * stride + d] = a;
+    }
+    if (tid < QPK) {
+        const size_t rowp = ((size_t)(kvh * QPK + tid) * n_splits + split) * stride;
+        part[rowp + kHD] = m_run[tid];
+        part[rowp + kHD + 1] = l_run[tid];
+    }
+
+    // ---- last workgroup of this kv head merges all splits
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = atomicAdd(&counters[kvh], 1u);
+        last_s = prev == (unsigned)(n_splits - 1);
+        if (last_s) counters[kvh] = 0u;  // self-reset for the next launch
+    }
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();
+    for (int i = tid; i < QPK * kHD; i += kAWG) {
+        const int h = i / kHD, d = i % kHD;
+        const float *ph_part = part + (size_t)(kvh * QPK + h) * n_splits * stride;
+        float m = kNegBig, l = 0.f, a = 0.f;
+        for (int s = 0; s < n_splits; s++) {
+            const float *r = ph_part + (size_t)s * stride;
+            const float ms = __builtin_nontemporal_load(r + kHD);
+            const float ls = __builtin_nontemporal_load(r + kHD + 1);
+            const float as = __builtin_nontemporal_load(r + d);
+            const float mn = fmaxf(m, ms);
+            const float ca = __expf(m - mn), cb = __expf(ms - mn);
+            a = a * ca + as * cb;
+            l = l * ca + ls * cb;
+            m = mn;
+        }
+        out[(size_t)(kvh * QPK + h) * kHD + d] = a / l;
+    }
+}
+
+}  // namespace
+
+int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
+                          const int8_t *vq, const uint16_t *vs, const uint32_t *step,
+                          int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
+                          int n_splits, float scale, float *out, void *workspace,
+                          size_t workspace_bytes) {
+    SGQ_CHECK(head_dim == kHD, "attn_decode_q8: head_dim %d unsupported (128)", head_dim);
+    SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_decode_q8: n_q %% n_kv != 0");
+    SGQ_CHECK(n_splits >= 1 && n_splits <= 1024, "attn_decode_q8: n_splits %d out of range", n_splits);
+    SGQ_CHECK(step != nullptr || kv_len > 0, "attn_decode_q8: kv_len must be > 0");
+    SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0 && ((uintptr_t)ks & 7) == 0 &&
+                  ((uintptr_t)vs & 7) == 0,
+              "attn_decode_q8: misaligned cache");
+    SGQ_CHECK(n_kv <= kAttnMaxKv, "attn_decode_q8: n_kv %d > %d", n_kv, kAttnMaxKv);
+    const size_t part_bytes = (size_t)n_q * n_splits * (kHD + 2) * 4;
+    SGQ_CHECK(kAttnPartOff + part_bytes <= workspace_bytes,
+              "attn_decode_q8: workspace too small (%zu < %zu)", workspace_bytes,
+              kAttnPartOff + part_bytes);
+    // Counters sit at a fixed offset, zeroed when the workspace is created
+    // and reset by the merging workgroup; partials follow.
+    unsigned *counters =
+        reinterpret_cast<unsigned *>(static_cast<uint8_t *>(workspace) + kAttnCounterOff);
+    float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + kAttnPartOff);
+    const int qpk = n_q / n_kv;
+    dim3 grid(n_kv, n_splits);
+#define SGQ_ATTN(Q)                                                                               \
+    case Q:                                                                                       \
+        hipLaunchKernelGGL(attn_decode_q8_kernel<Q>, grid, dim3(kAWG), 0, st, q, kq, ks, vq, vs,  \
+                           step, step_word, kv_len, n_kv, n_splits, scale, part, counters, out); \
+        break;
+    switch (qpk) {
+        SGQ_ATTN(1)
+        SGQ_ATTN(2)
+        default:
+            return fail(SGQ_ERR_VALIDATION, "attn_decode_q8: %d q heads per kv head unsupported",
+                        qpk);
+    }
+#undef SGQ_ATTN
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+}  // namespace sgq

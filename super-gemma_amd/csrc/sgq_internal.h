@@ -40,6 +40,14 @@ void *ctx_workspace(const sgq_ctx *ctx);
 // workspace: >= kGemvWorkspace bytes of device memory (x limb table), or
 // nullptr to force the register path.
 constexpr size_t kGemvWorkspace = 2048 * 96;
+// Context workspace layout (device memory, per context):
+//   [0, kGemvWorkspace)                GEMV x limb table
+//   [kAttnCounterOff, +4 KB)           attention split counters (zero at rest)
+//   [kAttnPartOff, kWorkspaceBytes)    attention split partials
+constexpr int kAttnMaxKv = 1024;
+constexpr size_t kAttnCounterOff = 256 * 1024;
+constexpr size_t kAttnPartOff = kAttnCounterOff + 4096;
+constexpr size_t kWorkspaceBytes = 16u << 20;
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
                      uint32_t k, void *workspace);
 int launch_quant_q8_0(hipStream_t st, const float *x, uint16_t *scales, int8_t *quants,
@@ -52,6 +60,11 @@ int launch_kv_append_q8(hipStream_t st, const float *src, uint16_t *scales, int8
 int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
                         float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
                         float *partials);
+int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
+                          const int8_t *vq, const uint16_t *vs, const uint32_t *step,
+                          int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
+                          int n_splits, float scale, float *out, void *workspace,
+                          size_t workspace_bytes);
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);

@@ -103,6 +103,7 @@ SIGNATURES = {
     "sgq_quant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_dequant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_gemm_q4_0_q8": (I, [P, P, P, P, P, U32, U32, U32, U32, P]),
+    "sgq_attn_decode_q8": (I, [P, P, P, P, P, P, U32, U32, U32, U32, U32, C.c_float, P]),
     "sgq_fill_q4_0_random": (I, [P, P, U64, U64, C.c_float]),
     "sgq_fill_normal": (I, [P, P, U64, U64, C.c_float, C.c_float]),
 }
@@ -270,6 +271,20 @@ class GpuContext:
             _need(partials, torch.float32, split_k * m * n, "partials")
         _check(lib().sgq_gemm_q4_0_q8(self._h, _ptr(w), _ptr(xq), _ptr(xs), _ptr(y), m, n, k,
                                       split_k, _ptr(partials)))
+
+    def attn_decode_q8(self, q, kq, ks, vq, vs, kv_len, n_q, n_kv, out, n_splits=16,
+                       scale=None, head_dim=128):
+        """Split-K decode attention over a Q8_0 K/V cache (fp32 q/out)."""
+        _need(q, torch.float32, n_q * head_dim, "q")
+        _need(out, torch.float32, n_q * head_dim, "out")
+        _need(kq, torch.int8, kv_len * n_kv * head_dim, "k_quants")
+        _need(vq, torch.int8, kv_len * n_kv * head_dim, "v_quants")
+        _need(ks, (torch.uint16, torch.int16, torch.float16), kv_len * n_kv * head_dim // 32, "k_scales")
+        _need(vs, (torch.uint16, torch.int16, torch.float16), kv_len * n_kv * head_dim // 32, "v_scales")
+        if scale is None:
+            scale = 1.0 / head_dim ** 0.5
+        _check(lib().sgq_attn_decode_q8(self._h, _ptr(q), _ptr(kq), _ptr(ks), _ptr(vq), _ptr(vs),
+                                        kv_len, n_q, n_kv, head_dim, n_splits, scale, _ptr(out)))
 
     def fill_q4_0_random(self, w: torch.Tensor, n_blocks: int, seed: int, sigma: float = 0.02):
         _need(w, torch.uint8, n_blocks * 18, "w")
