@@ -5,6 +5,9 @@
 Prints ONE JSON line (rank 0).  A "step" is one pass of the hot path over one
 batch of synthetic input, already resident in HBM:
 
+  decode  BASELINE config 5 (default): one bs=1 decode step of the 62-layer
+          random-init decoder at an 8K context (synthetic Q8_0 K/V pages for
+          positions 0..8191), replayed as one hipGraph; value = tok/s.
   gemv    BASELINE config 1: Q4_0 GEMV K=5376, N=21504 (decode), rotating over
           8 weight copies (520 MB > the 256 MB MALL) so every launch streams
           its weights from HBM.
@@ -109,6 +112,91 @@ class Mmq:
         }
 
 
+class Decode:
+    """one bs=1 decode step of the full 62-layer random-init
+    decoder at an 8K-token context, replayed as one hipGraph per step."""
+    kernel = "gemv_q4_0_ring_kernel"
+
+    def __init__(self, ctx, torch, context=8192):
+        import sgq
+
+        self.ctx, self.torch, self.sgq = ctx, torch, sgq
+        self.stream = torch.cuda.Stream()
+        ctx.set_stream(self.stream)
+        self.cfg = sgq.default_model_config(max_ctx=16384)
+        self.model = sgq.Model(ctx, self.cfg)
+        self.context = context
+        self.model.fill_cache(context)
+        self.logits = torch.empty(self.cfg.vocab, dtype=torch.float32, device="cuda")
+        c = self.cfg
+        H, F, QD, KD = c.hidden, c.ffn, c.n_q_heads * 128, c.n_kv_heads * 128
+        n_glob = sum(1 for l in range(c.n_layers) if l % c.global_every == c.global_every - 1)
+        n_slide = c.n_layers - n_glob
+        per_layer = q4_bytes(QD, H) + q4_bytes(KD, H) + q4_bytes(H, QD) + 2 * q4_bytes(F, H) \
+            + q4_bytes(H, F)
+        self.weight_bytes = c.n_layers * per_layer + n_slide * q4_bytes(KD, H) \
+            + (0 if c.global_k_eq_v else n_glob * q4_bytes(KD, H)) + q4_bytes(c.vocab, H)
+        kv_row = KD * (1 + 2 / 32) * 2  # K and V quants + f16 scales per position
+        ctx_pos = context + 1
+        self.kv_bytes = int(kv_row * (n_slide * min(ctx_pos, c.sliding_window) + n_glob * ctx_pos))
+        self.bytes = self.weight_bytes + self.kv_bytes
+        self.rng = __import__("random").Random(5)
+
+    def step(self, i):
+        self.model.decode(self.rng.randrange(self.cfg.vocab), self.logits, graph=True)
+
+    def kernel_roofline(self, steps=124):
+        """The dominant kernel: the Q4_0 GEMV on the model's own ffn_gate
+        matrices (K=5376, N=21504), rotating over all layers so every launch
+        streams from HBM; HIP events on the context's stream around `steps`
+        launches (each launch = the x-limb pass + the streamed GEMV)."""
+        import ctypes as C
+
+        lib = self.sgq.lib()
+        c = self.cfg
+        x = self.torch.empty(c.hidden, dtype=self.torch.float32, device="cuda")
+        self.ctx.fill_normal(x, seed=3)
+        y = self.torch.empty(c.ffn, dtype=self.torch.float32, device="cuda")
+        ptrs = [self.model.tensor_ptr("ffn_gate", l)[0] for l in range(c.n_layers)]
+
+        def run(n):
+            for j in range(n):
+                rc = lib.sgq_gemv_q4_0(self.ctx.handle, C.c_void_p(ptrs[j % len(ptrs)]),
+                                       C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr()),
+                                       c.ffn, c.hidden)
+                assert rc == 0
+        run(len(ptrs))
+        self.ctx.synchronize()
+        self.ctx.timer_start()
+        run(steps)
+        ms = self.ctx.timer_stop() / steps
+        nbytes = q4_bytes(c.ffn, c.hidden) + c.hidden * 4 + c.ffn * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "gemv_q4_0 (ffn_gate)",
+                "bytes_per_launch": nbytes, "us_per_launch": ms * 1e3}
+
+    def result(self, ms_per_step):
+        tok_s = 1000.0 / ms_per_step
+        step_gbs = self.bytes / (ms_per_step * 1e-3) / 1e9
+        c = self.cfg
+        return {
+            "value": tok_s, "unit": "tok/s",
+            "dtype": "q4_0 weights, q8_0 kv, fp32 activations",
+            "roofline": self.kernel_roofline(),
+            "step_roofline": {"bound": "hbm", "achieved": step_gbs, "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS,
+                              "bytes_per_step": self.bytes},
+            "config": {"workload": "decode step, bs=1, 8K context (BASELINE config 5), "
+                                   "62-layer random-init decoder, hipGraph per step",
+                       "n_layers": c.n_layers, "hidden": c.hidden, "ffn": c.ffn,
+                       "n_q_heads": c.n_q_heads, "n_kv_heads": c.n_kv_heads, "head_dim": 128,
+                       "vocab": c.vocab, "sliding_window": c.sliding_window,
+                       "global_every": c.global_every, "context": self.context,
+                       "weight_bytes": self.weight_bytes, "kv_bytes_read": self.kv_bytes},
+        }
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """Time the CPU restatement of CpuModel::matmul (dequant_row + 8-lane f64
     dot, row-parallel) on BASELINE config 1, full size, on the host cores."""
@@ -137,9 +225,9 @@ def cpu_baseline(budget_s: float = 12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gemv", choices=["gemv", "mmq", "splitk"])
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mmq", "splitk"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -151,7 +239,13 @@ def main():
     import sgq
 
     ctx = sgq.GpuContext(0)
-    if args.workload == "gemv":
+    if args.steps is None:
+        args.steps = 100 if args.workload == "decode" else 200
+    if args.warmup is None:
+        args.warmup = 10 if args.workload == "decode" else 20
+    if args.workload == "decode":
+        wl = Decode(ctx, torch)
+    elif args.workload == "gemv":
         wl = Gemv(ctx, torch)
     elif args.workload == "mmq":
         wl = Mmq(ctx, torch)
@@ -166,6 +260,7 @@ def main():
         wl.step(i)
     ms_total = ctx.timer_stop()
     torch.cuda.synchronize()
+    ctx.synchronize()
     ms = ms_total / args.steps
     res = wl.result(ms)
     out = {
@@ -183,6 +278,7 @@ def main():
         "data": "synthetic (device-generated, seeded)",
         "config": res["config"],
         "roofline": res["roofline"],
+        **({"step_roofline": res["step_roofline"]} if "step_roofline" in res else {}),
         "kernel": wl.kernel,
     }
     if not args.no_cpu_baseline:

@@ -159,6 +159,58 @@ int sgq_attn_decode_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
                        uint32_t kv_len, uint32_t n_q_heads, uint32_t n_kv_heads,
                        uint32_t head_dim, uint32_t n_splits, float scale, float *out);
 
+/* ---- decode-step driver ------------------------------------------------- */
+/* A random-init decoder of the reference's model family (the CPU forward pass
+ * crates/sg-model/src/reference.rs:157-316 and the GPU graph
+ * crates/sg-model/src/graph.rs:478-756): Q4_0 linears, weighted q/k norms,
+ * weightless v norm, NEOX RoPE (sliding theta / global theta with the first
+ * global_rope_frac of pairs rotating), Q8_0 K and V pages (a ring of
+ * sliding_window slots on sliding layers, max_ctx slots on global ones),
+ * GeGLU FFN, post-norms, per-layer output scale, tied Q4_0 LM head with
+ * softcap.  Layer l is global iff l % global_every == global_every - 1.
+ * Weights: Q4_0 d = f16(|N(0, weight_sigma)|) with uniform nibbles, norm
+ * weights N(1, 0.1), layer output scales N(0.9, 0.05), all keyed by seed. */
+typedef struct sgq_model sgq_model;
+typedef struct {
+    uint32_t n_layers, hidden, ffn, n_q_heads, n_kv_heads, head_dim, vocab;
+    uint32_t sliding_window, global_every, max_ctx;
+    float rope_theta_sliding, rope_theta_global, global_rope_frac;
+    float eps, attn_scale, final_softcap, weight_sigma;
+    uint32_t global_k_eq_v; /* 1: global layers take V from the K projection */
+    uint32_t _pad;
+    uint64_t seed;
+} sgq_model_config;
+
+/* The benchmark shape: 62 layers, hidden 5376, ffn 21504, 32 q / 16 kv heads
+ * of 128, vocab 262144, window 1024, every 6th layer global, 16K context. */
+void sgq_model_default_config(sgq_model_config *cfg);
+/* Allocates and fills every weight and cache on the context's device. */
+int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out);
+int sgq_model_destroy(sgq_model *model);
+/* Forget the cached context (position back to 0). */
+int sgq_model_reset(sgq_model *model);
+uint32_t sgq_model_position(const sgq_model *model);
+/* One decode step at the current position: appends token's K/V, writes the
+ * softcapped logits [vocab] fp32 to the device buffer `logits`, advances the
+ * position.  Enqueued on the context's stream (no host wait).  The _graph
+ * form records the step into a hipGraph on first use (per logits buffer) and
+ * replays it; the per-token inputs travel through a device step buffer. */
+int sgq_model_decode(sgq_model *model, uint32_t token, float *logits);
+int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
+/* Synthetic context: fills the K/V pages of positions 0..n_tokens-1 (the
+ * last sliding_window of them on ring layers) with Q8_0 of N(0,1) values and
+ * sets the position to n_tokens, so a decode step can be measured at a long
+ * context without decoding up to it.  Blocks the host until done. */
+int sgq_model_fill_cache(sgq_model *model, uint32_t n_tokens, uint64_t seed);
+/* Device pointer and byte size of a named tensor: layer -1 for
+ * token_embd / output_norm / x (the residual stream); per layer the GGUF
+ * names attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down,
+ * attn_norm, attn_q_norm, attn_k_norm, post_attention_norm, ffn_norm,
+ * post_ffw_norm, layer_output_scale and the cache pages k_quants, k_scales,
+ * v_quants, v_scales. */
+int sgq_model_tensor(const sgq_model *model, int layer, const char *name, void **ptr,
+                     uint64_t *bytes);
+
 /* ---- synthetic inputs (not on the hot path; for benches and tests) ------ */
 /* Q4_0 blocks with d = f16(|N(0, sigma)|) and uniform nibble bytes, from a
  * counter-based generator keyed by (seed, block index). */

@@ -1,0 +1,122 @@
+"""CPU decoder forward pass of the reference model family, over the oracle's
+C primitives.
+
+TEST INFRASTRUCTURE ONLY: the checker for libsgq's decode-step driver
+(sgq_model_*), imported by tests/ and ``__graft_entry__.smoke()``.  Never part
+of the product path.
+
+Follows crates/sg-model/src/reference.rs:157-316 (ReferenceModel::forward):
+  x = dequant(E[token]) * embed_scale            (reference.rs:163-172)
+  per layer (reference.rs:184-303):
+    xn = rmsnorm(x, attn_norm)
+    q = rope(rmsnorm_h(Wq xn, q_norm)); k = rope(rmsnorm_h(Wk xn, k_norm))
+    v = rmsnorm_h(Wv xn) weightless; global layers take v from Wk xn
+        (attention_k_eq_v, reference.rs:214-222)
+    a = attention over the window (sliding) or all keys (global),
+        scale attn_scale                         (reference.rs:483-531)
+    x += rmsnorm(Wo a, post_attention_norm)
+    x += rmsnorm(Wd (gelu_tanh(Wg fn) * Wu fn), post_ffw_norm),
+        fn = rmsnorm(x, ffn_norm)
+    x *= layer_output_scale
+  logits = cap * tanh((E rmsnorm(x, output_norm)) / cap)  (reference.rs:307-316)
+One deviation, on purpose, to match the GPU graph instead of the f32 CPU
+cache: K and V are stored as Q8_0 pages (kv_quant_q8, crates/sg-gpu/shaders/
+kv_quant_q8.wgsl:30-57, recorded by crates/sg-model/src/graph.rs:560-600), so
+the oracle round-trips each K/V row through Q8_0 before caching it.
+RoPE: NEOX, angles in f64 via cos_sin_table (crates/sg-model/src/rope.rs:
+27-48); global layers use divisor factors [1]*live + [1e30]*rest, which is
+how partial_rotary_factor materializes (rope.rs:13-16).
+Linear layers use the f64 Q4_0 GEMV (gemv_rows); everything is fp32 between
+ops, as in the reference.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import oracle as O
+
+
+class OracleDecoder:
+    """``weights``: dict of host arrays keyed like sgq_model_tensor
+    ((name, layer) -> array; Q4_0 tensors as uint8 bytes, the rest float32).
+    ``cfg``: dict with the sgq_model_config fields."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.c = cfg
+        self.w = weights
+        L = cfg["n_layers"]
+        self.k_cache = [[] for _ in range(L)]
+        self.v_cache = [[] for _ in range(L)]
+        self.pos = 0
+        hd = cfg["head_dim"]
+        live = int(round(cfg["global_rope_frac"] * hd / 2))
+        self.global_factors = np.array([1.0] * live + [1e30] * (hd // 2 - live), np.float32)
+
+    def is_global(self, layer: int) -> bool:
+        ge = self.c["global_every"]
+        return layer % ge == ge - 1
+
+    def _lin(self, name, layer, x, n_out):
+        k = x.size
+        return O.gemv_rows(self.w[(name, layer)], x, k, np.arange(n_out))
+
+    def _q8_round_trip(self, row):
+        s, q = O.quant_q8_0(row)
+        return O.dequant_q8_0(s, q)
+
+    def decode(self, token: int) -> np.ndarray:
+        c, w = self.c, self.w
+        H, F, hd = c["hidden"], c["ffn"], c["head_dim"]
+        nq, nkv = c["n_q_heads"], c["n_kv_heads"]
+        eps = c["eps"]
+        emb = w[("token_embd", -1)]
+        row = O.q4_0_dequant(emb[token * (H // 32) * 18:(token + 1) * (H // 32) * 18], 1, H)[0]
+        x = (row * np.float32(math.sqrt(H))).astype(np.float32)
+        pos = self.pos
+        for l in range(c["n_layers"]):
+            glob = self.is_global(l)
+            xn = O.rmsnorm(x, w[("attn_norm", l)], H, eps)
+            q = self._lin("attn_q", l, xn, nq * hd)
+            k_proj = self._lin("attn_k", l, xn, nkv * hd)
+            if glob and c["global_k_eq_v"]:
+                v = k_proj.copy()
+            else:
+                v = self._lin("attn_v", l, xn, nkv * hd)
+            if glob:
+                cs = O.cos_sin_table([pos], hd, c["rope_theta_global"], self.global_factors)
+            else:
+                cs = O.cos_sin_table([pos], hd, c["rope_theta_sliding"])
+            q = O.rmsnorm(q, w[("attn_q_norm", l)], hd, eps)
+            q = O.rope(q, hd, hd, nq, cs)
+            k = O.rmsnorm(k_proj, w[("attn_k_norm", l)], hd, eps)
+            k = O.rope(k, hd, hd, nkv, cs)
+            v = O.rmsnorm(v, None, hd, eps)
+            self.k_cache[l].append(self._q8_round_trip(k))
+            self.v_cache[l].append(self._q8_round_trip(v))
+            ck = np.concatenate(self.k_cache[l])
+            cv = np.concatenate(self.v_cache[l])
+            window = None if glob else c["sliding_window"]
+            a = O.attention(q, ck, cv, 1, pos, nq, nkv, hd, window, c["attn_scale"]).reshape(-1)
+            o = self._lin("attn_output", l, a, H)
+            o = O.rmsnorm(o, w[("post_attention_norm", l)], H, eps)
+            x = (x + o).astype(np.float32)
+            fn = O.rmsnorm(x, w[("ffn_norm", l)], H, eps)
+            g = self._lin("ffn_gate", l, fn, F)
+            u = self._lin("ffn_up", l, fn, F)
+            h = O.geglu(g, u)
+            f = self._lin("ffn_down", l, h, H)
+            f = O.rmsnorm(f, w[("post_ffw_norm", l)], H, eps)
+            x = (x + f).astype(np.float32)
+            x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
+        self.pos += 1
+        xf = O.rmsnorm(x, w[("output_norm", -1)], H, eps)
+        logits = O.gemv_rows(emb, xf, H, np.arange(c["vocab"]))
+        cap = np.float64(c["final_softcap"])
+        return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
+
+
+LAYER_TENSORS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",
+                 "attn_norm", "attn_q_norm", "attn_k_norm", "post_attention_norm", "ffn_norm",
+                 "post_ffw_norm", "layer_output_scale")

@@ -21,20 +21,12 @@
 //    (even blocks start 4-aligned, odd blocks 2 bytes past); v_perm_b32
 //    realigns the 16 nibble bytes with a per-lane selector.
 //  * Row sums: butterfly over the wave (fixed order: deterministic).
-#include "sgq_internal.h"
+#include "limbs.h"
 
 namespace sgq {
 namespace {
 
 constexpr int kWG = 256;  // 4 waves
-constexpr int kLimbs = 5;
-
-template <int NBL>
-struct XLimbs {
-    int q[NBL][kLimbs][4];  // i4 × 8 per word, in the nibble order of a qs word
-    float d[NBL];           // (amax/7) / 14^4: scale of the Horner-combined sum
-};
-
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -45,49 +37,6 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Word w of a limb holds, nibble by nibble, the limb values of weights
 // 4w, 16+4w, 4w+1, 17+4w, 4w+2, 18+4w, 4w+3, 19+4w: the order in which qs
 // byte 4w..4w+3's low/high nibbles appear in a 32-bit qs word.
-template <int NBL>
-__device__ __forceinline__ void quantize_values(const float (&v)[32], XLimbs<NBL> &L, int i) {
-    float amax = 0.f;
-#pragma unroll
-    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
-    const float d = amax * (1.0f / 7.0f);
-    const float id = d > 0.f ? 1.0f / d : 0.f;
-    L.d[i] = d * (1.0f / 38416.0f);  // 14^4
-    uint32_t word[kLimbs][4] = {};
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-        float r = v[j] * id;
-        const int w = (j & 15) >> 2;
-        const int shift = 4 * (2 * (j & 3) + (j >> 4));
-#pragma unroll
-        for (int l = 0; l < kLimbs; l++) {
-            const float c = __builtin_rintf(r);
-            r = (r - c) * 14.f;
-            word[l][w] |= ((uint32_t)(int)c & 0xFu) << shift;
-        }
-    }
-#pragma unroll
-    for (int l = 0; l < kLimbs; l++)
-#pragma unroll
-        for (int w = 0; w < 4; w++) L.q[i][l][w] = (int)word[l][w];
-}
-
-template <int NBL>
-__device__ __forceinline__ void quantize_block(const float *__restrict__ xb, XLimbs<NBL> &L,
-                                               int i) {
-    float v[32];
-    const float4 *x4 = reinterpret_cast<const float4 *>(xb);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        float4 t = x4[j];
-        v[4 * j] = t.x;
-        v[4 * j + 1] = t.y;
-        v[4 * j + 2] = t.z;
-        v[4 * j + 3] = t.w;
-    }
-    quantize_values(v, L, i);
-}
-
 // One block's contribution d_w * sum_j (q_j - 8) * x_j from its 5 raw words.
 template <int NBL>
 __device__ __forceinline__ float block_dot(const uint32_t (&w)[5], uint32_t sel, uint32_t dshift,
@@ -113,24 +62,6 @@ __device__ __forceinline__ float block_dot(const uint32_t (&w)[5], uint32_t sel,
     const float c = __builtin_fmaf((float)c_hi, 196.0f, (float)c_lo);
     const float dw = f16_bits_to_f32((w[0] >> dshift) & 0xffffu);
     return dw * (L.d[i] * c);
-}
-
-// Per-block x limbs as stored in the table the streamed kernel reads (96 B).
-struct BlockLimbs {
-    int q[kLimbs][4];
-    float d;
-    int pad[3];
-};
-
-__device__ __forceinline__ void quantize_to_table(const float *__restrict__ xb, BlockLimbs &t) {
-    XLimbs<1> L;
-    quantize_block(xb, L, 0);
-#pragma unroll
-    for (int l = 0; l < kLimbs; l++)
-#pragma unroll
-        for (int w = 0; w < 4; w++) t.q[l][w] = L.q[0][l][w];
-    t.d = L.d[0];
-    t.pad[0] = t.pad[1] = t.pad[2] = 0;
 }
 
 template <int R, int NBL>
@@ -309,12 +240,25 @@ __device__ __forceinline__ float lds_read_f32(const uint8_t *p) {
     return v;
 }
 
+// Row r of the concatenated targets -> (matrix, local row).
+__device__ __forceinline__ int target_of(const GemvTargets &tg, int row, int *local) {
+    int j = 0;
+#pragma unroll
+    for (int q = 0; q < kGemvMaxTargets - 1; q++)
+        if (q < tg.count - 1 && row >= tg.end[q]) j = q + 1;
+    *local = row - (j ? tg.end[j - 1] : 0);
+    return j;
+}
+
 // DMA one row slice (<= 3072 B) into a ring slot; past-the-end rows are
 // clamped to row 0 so every call issues exactly kRLoads loads.
-__device__ __forceinline__ void issue_slice(const uint8_t *__restrict__ W, uint8_t *slot, int row,
-                                            int n, size_t row_bytes, int slice_off,
-                                            int slice_bytes, int lane) {
-    const uint8_t *src = W + (size_t)(row < n ? row : 0) * row_bytes + slice_off;
+__device__ __forceinline__ void issue_slice(const GemvTargets &tg, uint8_t *slot, int row, int n,
+                                            size_t row_bytes, int slice_off, int slice_bytes,
+                                            int lane) {
+    int local;
+    const int j = target_of(tg, row < n ? row : 0, &local);
+    const uint8_t *src =
+        static_cast<const uint8_t *>(tg.w[j]) + (size_t)local * row_bytes + slice_off;
 #pragma unroll
     for (int i = 0; i < kRLoads; i++) {
         int off = (i * kWave + lane) * 16;
@@ -332,11 +276,19 @@ __global__ __launch_bounds__(256) void gemv_prep_x_kernel(const float *__restric
     quantize_to_table(x + (size_t)b * 32, xl[b]);
 }
 
+__device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float v) {
+    int local;
+    const int j = target_of(tg, row, &local);
+    if (tg.softcap > 0.f) v = tg.softcap * tanhf(v / tg.softcap);
+    tg.y[j][local] = v;
+}
+
+// Rows of up to kGemvMaxTargets matrices sharing x (e.g. Q/K/V, gate/up) are
+// one concatenated row space: one launch, one x table.
 template <int NBL>
-__global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(const uint8_t *__restrict__ W,
+__global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
                                                               const BlockLimbs *__restrict__ xl,
-                                                              float *__restrict__ y, int n, int nb,
-                                                              int S, int slice) {
+                                                              int n, int nb, int S, int slice) {
     extern __shared__ __align__(16) uint8_t gemv_smem[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -375,7 +327,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(const uint8_t *__r
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 #pragma unroll
     for (int j = 0; j < kRStages - 1; j++)
-        issue_slice(W, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, slice_bytes, lane);
+        issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, slice_bytes, lane);
 
     // lb even: qs = bytes 2..17 of the window, d = low half of word 0;
     // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
@@ -384,7 +336,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(const uint8_t *__r
     const int rows_rounds = (n - blockIdx.x * P + G - 1) / G;  // same for every wave of the group
     for (int it = 0; it < rows_rounds; it++) {
         const int row = r0 + it * G;
-        issue_slice(W, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
+        issue_slice(tg, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
                     row + (kRStages - 1) * G, n, row_bytes, slice_off, slice_bytes, lane);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * (kRStages - 1)));
         const uint8_t *st = ring + (it % kRStages) * kRSlot;
@@ -398,14 +350,14 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(const uint8_t *__r
         }
         a = wave_sum(a);
         if (S == 1) {
-            if (lane == 0 && row < n) y[row] = a;
+            if (lane == 0 && row < n) store_row(tg, row, a);
         } else {
             if (lane == 0) lds_write_f32(red + wave * 4, a);
             __builtin_amdgcn_s_barrier();
             if (s == 0 && lane == 0 && row < n) {
                 float v = 0.f;
                 for (int q = 0; q < S; q++) v += lds_read_f32(red + (rw * S + q) * 4);
-                y[row] = v;
+                store_row(tg, row, v);
             }
             __builtin_amdgcn_s_barrier();
         }
@@ -414,20 +366,26 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(const uint8_t *__r
 }
 
 template <int NBL>
-int launch_ring(hipStream_t st, const void *w, const BlockLimbs *xl, float *y, int n, int nb,
-                int S, int slice) {
+int ring_attr() {
     static bool attr = false;
     if (!attr) {
         SGQ_HIP(hipFuncSetAttribute((const void *)gemv_q4_0_ring_kernel<NBL>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, kRLds));
         attr = true;
     }
+    return SGQ_OK;
+}
+
+template <int NBL>
+int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n, int nb, int S,
+                int slice) {
+    if (int rc = ring_attr<NBL>()) return rc;
     const int P = (kRWG / kWave) / S;
     int grid = device_info().cus * 2;  // two 72 KB workgroups per CU
     const int max_grid = (n + P - 1) / P;
     if (grid > max_grid) grid = max_grid;
-    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL>), dim3(grid), dim3(kRWG), kRLds, st,
-                       static_cast<const uint8_t *>(w), xl, y, n, nb, S, slice);
+    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL>), dim3(grid), dim3(kRWG), kRLds, st, tg, xl,
+                       n, nb, S, slice);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }
@@ -455,6 +413,59 @@ int launch(hipStream_t st, const void *w, const float *x, float *y, int n, int n
 
 }  // namespace
 
+// Streamed path geometry for K (x limbs in a table): S K-slices of `slice`
+// blocks, or false when K is outside it (K % 256 != 0 or a slice > 3 KB).
+static bool ring_geometry(int nb, int *S_out, int *slice_out) {
+    if (nb % 8 != 0) return false;
+    int S = 1;
+    while (S < 4 && (nb + S - 1) / S > kRSlot / 18) S *= 2;
+    int slice = (nb + S - 1) / S;
+    slice = (slice + 7) & ~7;  // 144-byte multiple: 16-byte aligned slice starts
+    if (slice * 18 > kRSlot || slice > 3 * kWave) return false;
+    *S_out = S;
+    *slice_out = slice;
+    return true;
+}
+
+static int launch_ring_any(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n,
+                           int nb, int S, int slice) {
+    const int nbl = (slice + kWave - 1) / kWave;
+    if (nbl == 1) return launch_ring<1>(st, tg, xl, n, nb, S, slice);
+    if (nbl == 2) return launch_ring<2>(st, tg, xl, n, nb, S, slice);
+    return launch_ring<3>(st, tg, xl, n, nb, S, slice);
+}
+
+int gemv_prepare() {
+    int rc = ring_attr<1>();
+    if (!rc) rc = ring_attr<2>();
+    if (!rc) rc = ring_attr<3>();
+    return rc;
+}
+
+int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k) {
+    SGQ_CHECK(k % 32 == 0 && k > 0, "quant_limbs: k=%u must be a multiple of 32", k);
+    SGQ_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)xl & 15) == 0, "quant_limbs: misaligned");
+    const int nb = (int)(k / 32);
+    hipLaunchKernelGGL(gemv_prep_x_kernel, dim3((nb + 255) / 256), dim3(256), 0, st, x,
+                       static_cast<BlockLimbs *>(xl), nb);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k) {
+    SGQ_CHECK(tg.count >= 1 && tg.count <= kGemvMaxTargets, "gemv: %d targets", tg.count);
+    SGQ_CHECK(k % 256 == 0 && k > 0 && k <= 65536, "gemv (limbs): k=%u must be a multiple of 256", k);
+    for (int j = 0; j < tg.count; j++) {
+        SGQ_CHECK(((uintptr_t)tg.w[j] & 15) == 0, "gemv (limbs): weights must be 16-byte aligned");
+        SGQ_CHECK(tg.end[j] > (j ? tg.end[j - 1] : 0), "gemv (limbs): empty target %d", j);
+    }
+    int S, slice;
+    const int nb = (int)(k / 32);
+    SGQ_CHECK(ring_geometry(nb, &S, &slice), "gemv (limbs): k=%u outside the streamed geometry", k);
+    return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1], nb,
+                           S, slice);
+}
+
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
                      uint32_t k, void *workspace) {
     SGQ_CHECK(k % 64 == 0 && k > 0, "gemv_q4_0: k=%u must be a positive multiple of 64", k);
@@ -465,26 +476,22 @@ int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, ui
     const int nb = (int)(k / 32);
     // Streamed path: 16-byte aligned rows (K % 256 == 0), x limbs prepared
     // once into the workspace, row slices of <= 170 blocks.
-    if (k % 256 == 0 && ((uintptr_t)w & 15) == 0 && workspace != nullptr) {
-        int S = 1;
-        while (S < 4 && (nb + S - 1) / S > kRSlot / 18) S *= 2;
-        int slice = (nb + S - 1) / S;
-        slice = (slice + 7) & ~7;  // 144-byte multiple: 16-byte aligned slice starts
-        if (slice * 18 <= kRSlot && slice <= 3 * kWave) {
-            BlockLimbs *xl = static_cast<BlockLimbs *>(workspace);
-            hipLaunchKernelGGL(gemv_prep_x_kernel, dim3((nb + 255) / 256), dim3(256), 0, st, x, xl,
-                               nb);
-            SGQ_HIP(hipGetLastError());
-            const int nbl = (slice + kWave - 1) / kWave;
-            if (nbl == 1) return launch_ring<1>(st, w, xl, y, (int)n, nb, S, slice);
-            if (nbl == 2) return launch_ring<2>(st, w, xl, y, (int)n, nb, S, slice);
-            return launch_ring<3>(st, w, xl, y, (int)n, nb, S, slice);
-        }
+    int S, slice;
+    if (((uintptr_t)w & 15) == 0 && workspace != nullptr && ring_geometry(nb, &S, &slice)) {
+        int rc = launch_quant_limbs(st, x, workspace, k);
+        if (rc) return rc;
+        GemvTargets tg{};
+        tg.w[0] = w;
+        tg.y[0] = y;
+        tg.end[0] = (int)n;
+        tg.count = 1;
+        return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(workspace), (int)n, nb, S,
+                               slice);
     }
     // Register path (any K % 64 == 0): each wave quantizes its own blocks.
-    int S = 1;
+    S = 1;
     while (S < 4 && (nb + S - 1) / S > 3 * kWave) S *= 2;
-    int slice = (nb + S - 1) / S;
+    slice = (nb + S - 1) / S;
     slice += slice & 1;  // even: lane parity == block parity
     const int nbl = (slice + kWave - 1) / kWave;
     switch (nbl) {

@@ -1,0 +1,571 @@
+// Decode-step driver: the caller side of the hot path at the BASELINE shape
+// (a random-init Gemma-4-style decoder, Q4_0 linears, Q8_0 KV cache).
+//
+// Semantics follow the reference's CPU model forward pass
+// (crates/sg-model/src/reference.rs:157-316) and its GPU graph
+// (crates/sg-model/src/graph.rs:478-756, record_layer / record_logits):
+//   x = embed(token)·√hidden
+//   per layer: xn = rmsnorm(x, attn_norm); q,k,v = Wq/Wk/Wv·xn;
+//     q = rope(rmsnorm(q_h, q_norm)); k = rope(rmsnorm(k_h, k_norm));
+//     v = rmsnorm(v_h) (weightless); append Q8_0(k), Q8_0(v) at the slot;
+//     a = softmax(scale·q·kᵀ)·v over the window (sliding) or all (global);
+//     x += rmsnorm(Wo·a, post_attention_norm);
+//     f = Wd·(gelu_tanh(Wg·fn)·Wu·fn) with fn = rmsnorm(x, ffn_norm);
+//     x = (x + rmsnorm(f, post_ffw_norm))·layer_output_scale
+//   logits = softcap·tanh((E·rmsnorm(x, output_norm))/softcap), E tied.
+// Shape deviations from the real checkpoint follow the benchmark's decoder:
+// every layer has 32 q / 16 kv heads of dim 128, K and V pages are both
+// Q8_0, and the tied head is Q4_0.  Global layers take V from the K
+// projection (attention_k_eq_v, reference.rs:214-222) unless
+// global_k_eq_v is 0.
+//
+// Every per-token input lives on the device (token, position and the two
+// kv lengths in a step buffer; RoPE angles are computed on the device in
+// f64 from the position), so one decode step can be captured into a hipGraph
+// once and replayed — the reference records its graph once and rewrites the
+// step buffer (graph.rs:462-476, 1485-1529).
+//
+// Kernels per layer: norm/embed row kernel -> QKV GEMV (one launch, three
+// matrices) -> q/k/v post (norms, RoPE, Q8 append) -> split-K attention ->
+// limb quant -> O GEMV -> post-attention row kernel -> gate/up GEMV (one
+// launch) -> GeGLU+limbs -> down GEMV -> post-FFN row kernel (fused with the
+// next layer's input norm).  Row kernels write the next GEMV's x limb table.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "limbs.h"
+
+struct sgq_model;
+
+namespace sgq {
+namespace {
+
+constexpr int kRowWG = 1024;
+constexpr int kHeadDim = 128;
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k = 0.7978845608028654f;
+    return 0.5f * x * (1.f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+// Sum over the workgroup in a fixed tree order (deterministic).
+template <int WG>
+__device__ __forceinline__ float wg_sum(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int w = 0; w < WG / kWave; w++) r += red[w];
+    return r;
+}
+
+// buf[0..n) <- buf * rsqrt(mean(buf²) + eps) * w  (w == nullptr: weightless)
+__device__ __forceinline__ void rmsnorm_lds(float *buf, int n, const float *__restrict__ w,
+                                            float eps, float *red) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kRowWG) ss += buf[i] * buf[i];
+    ss = wg_sum<kRowWG>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kRowWG) buf[i] = buf[i] * inv * (w ? w[i] : 1.f);
+    __syncthreads();
+}
+
+// limbs of buf[0..n) (n % 32 == 0), one thread per 32-block
+__device__ __forceinline__ void limbs_lds(const float *buf, int n, BlockLimbs *__restrict__ xl) {
+    for (int b = threadIdx.x; b < n / 32; b += kRowWG) {
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) v[j] = buf[b * 32 + j];
+        BlockLimbs t;
+        limbs_from_values(v, t);
+        xl[b] = t;
+    }
+}
+
+// x = dequant(E[token])·scale; xl = limbs(rmsnorm(x, w))
+__global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__restrict__ E,
+                                                             const uint32_t *__restrict__ step,
+                                                             int hidden, float scale,
+                                                             const float *__restrict__ w, float eps,
+                                                             float *__restrict__ x,
+                                                             BlockLimbs *__restrict__ xl) {
+    extern __shared__ float row[];
+    __shared__ float red[kRowWG / kWave];
+    const uint32_t token = step[4];
+    const uint8_t *er = E + (size_t)token * (hidden / 32) * 18;
+    for (int i = threadIdx.x; i < hidden; i += kRowWG) {
+        const uint8_t *blk = er + (i / 32) * 18;
+        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+        const int j = i % 32;
+        const int q = j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4);
+        const float v = d * (float)(q - 8) * scale;
+        x[i] = v;
+        row[i] = v;
+    }
+    __syncthreads();
+    rmsnorm_lds(row, hidden, w, eps, red);
+    limbs_lds(row, hidden, xl);
+}
+
+// x += rmsnorm(o, w_post); xl = limbs(rmsnorm(x, w_next))   (post-attention)
+// x = (x + rmsnorm(o, w_post))·scale; xl = limbs(rmsnorm(x, w_next)) (post-FFN)
+__global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
+    const float *__restrict__ o, const float *__restrict__ w_post, float *__restrict__ x,
+    const float *__restrict__ scale_ptr, const float *__restrict__ w_next, int hidden, float eps,
+    BlockLimbs *__restrict__ xl) {
+    extern __shared__ float row[];
+    __shared__ float red[kRowWG / kWave];
+    for (int i = threadIdx.x; i < hidden; i += kRowWG) row[i] = o[i];
+    __syncthreads();
+    rmsnorm_lds(row, hidden, w_post, eps, red);
+    const float s = scale_ptr ? *scale_ptr : 1.f;
+    for (int i = threadIdx.x; i < hidden; i += kRowWG) {
+        const float v = (x[i] + row[i]) * s;
+        x[i] = v;
+        row[i] = v;
+    }
+    __syncthreads();
+    rmsnorm_lds(row, hidden, w_next, eps, red);
+    limbs_lds(row, hidden, xl);
+}
+
+// h = gelu_tanh(g)·u, then its limb table; one thread per 32-block.
+__global__ __launch_bounds__(256) void geglu_limbs_kernel(const float *__restrict__ g,
+                                                          const float *__restrict__ u, int n,
+                                                          BlockLimbs *__restrict__ xl) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= n / 32) return;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = gelu_tanh(g[b * 32 + j]) * u[b * 32 + j];
+    BlockLimbs t;
+    limbs_from_values(v, t);
+    xl[b] = t;
+}
+
+// Per-head post-projection: q heads -> rmsnorm(q_norm) + RoPE -> q_out;
+// k heads -> rmsnorm(k_norm) + RoPE -> Q8_0 into the cache slot;
+// v heads -> weightless rmsnorm -> Q8_0 into the cache slot.
+// Grid: n_q + 2·n_kv workgroups of 128 threads (one element each).
+__global__ __launch_bounds__(kHeadDim) void qkv_post_kernel(
+    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
+    const float *__restrict__ v_raw, const float *__restrict__ wq_norm,
+    const float *__restrict__ wk_norm, const uint32_t *__restrict__ step, int n_q, int n_kv,
+    float theta, int live_pairs, int ring, float eps, float *__restrict__ q_out,
+    int8_t *__restrict__ kq, uint16_t *__restrict__ ks, int8_t *__restrict__ vq,
+    uint16_t *__restrict__ vs) {
+    __shared__ float row[kHeadDim];
+    __shared__ float red[kHeadDim / kWave];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const uint32_t pos = step[0];
+    int kind;  // 0 q, 1 k, 2 v
+    int head;
+    if (h < n_q) {
+        kind = 0;
+        head = h;
+    } else if (h < n_q + n_kv) {
+        kind = 1;
+        head = h - n_q;
+    } else {
+        kind = 2;
+        head = h - n_q - n_kv;
+    }
+    const float *src = kind == 0 ? q_raw : kind == 1 ? k_raw : v_raw;
+    float v = src[head * kHeadDim + t];
+    // rmsnorm over the head (f32 sum of squares, fixed tree)
+    float ss = v * v;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1];
+    const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + eps);
+    const float wn = kind == 0 ? wq_norm[t] : kind == 1 ? wk_norm[t] : 1.f;
+    v = v * inv * wn;
+    row[t] = v;
+    __syncthreads();
+    if (kind < 2) {  // NEOX RoPE: pair i couples (i, i + 64); live pairs rotate
+        const int half = kHeadDim / 2;
+        const int i = t % half;
+        if (i < live_pairs) {
+            const double freq = pow((double)theta, -2.0 * (double)i / (double)kHeadDim);
+            const double ang = (double)pos * freq;
+            const float c = (float)cos(ang), sn = (float)sin(ang);
+            const float a = row[i], b = row[i + half];
+            v = t < half ? a * c - b * sn : b * c + a * sn;
+        }
+    }
+    if (kind == 0) {
+        q_out[head * kHeadDim + t] = v;
+        return;
+    }
+    // Q8_0 per 32 elements along head_dim (kv_quant_q8.wgsl:41-56 semantics)
+    float amax = fabsf(v);
+    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
+    const float d = amax * (1.0f / 127.0f);
+    const float id = d > 0.f ? 1.0f / d : 0.f;
+    const int qv = (int)__builtin_rintf(v * id);
+    const uint32_t slot = ring ? pos % (uint32_t)ring : pos;
+    const size_t e = ((size_t)slot * n_kv + head) * kHeadDim + t;
+    int8_t *dq = kind == 1 ? kq : vq;
+    uint16_t *ds = kind == 1 ? ks : vs;
+    dq[e] = (int8_t)qv;
+    if ((t & 31) == 0) ds[e / 32] = f32_to_f16_bits(d);
+}
+
+// step words [pos, kv_len_sliding, kv_len_global, q0, token]
+__global__ void model_step_kernel(uint32_t *step, uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                  uint32_t e) {
+    const uint32_t t = threadIdx.x;
+    if (t < 5) step[t] = t == 0 ? a : t == 1 ? b : t == 2 ? c : t == 3 ? d : e;
+}
+
+}  // namespace
+}  // namespace sgq
+
+using namespace sgq;
+
+struct LayerW {
+    void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr,
+         *wu = nullptr, *wd = nullptr;  // Q4_0 (wv null: V from the K projection)
+    float *attn_norm, *q_norm, *k_norm, *post_attn_norm, *ffn_norm, *post_ffw_norm;
+    float *out_scale;  // 1 float
+    bool global;
+    int8_t *kq, *vq;
+    uint16_t *ks, *vs;
+    uint32_t slots;
+};
+
+struct sgq_model {
+    sgq_ctx *ctx;
+    sgq_model_config cfg;
+    std::vector<LayerW> layers;
+    void *embd = nullptr;
+    float *out_norm = nullptr;
+    std::vector<void *> allocs;
+    // activations
+    float *x, *q_raw, *k_raw, *v_raw, *q, *attn, *o, *g, *u, *f;
+    void *xl;  // limb table (largest K)
+    uint32_t *step;
+    uint32_t pos = 0;
+    sgq_graph *graph = nullptr;
+    float *graph_logits = nullptr;
+};
+
+namespace {
+
+int alloc(sgq_model *m, size_t bytes, void **p) {
+    SGQ_HIP(hipMalloc(p, bytes ? bytes : 256));
+    m->allocs.push_back(*p);
+    return SGQ_OK;
+}
+
+uint64_t mix(uint64_t a, uint64_t b) { return (a + 0x9E3779B97F4A7C15ull) * 0xBF58476D1CE4E5B9ull ^ b; }
+
+int q4_tensor(sgq_model *m, size_t rows, size_t cols, uint64_t seed, void **p) {
+    int rc = alloc(m, rows * (cols / 32) * 18, p);
+    if (rc) return rc;
+    return launch_fill_q4_0(ctx_stream(m->ctx), *p, rows * (cols / 32), seed, m->cfg.weight_sigma);
+}
+
+int f32_tensor(sgq_model *m, size_t n, uint64_t seed, float mean, float sigma, float **p) {
+    int rc = alloc(m, n * 4, reinterpret_cast<void **>(p));
+    if (rc) return rc;
+    return launch_fill_normal(ctx_stream(m->ctx), *p, n, seed, mean, sigma);
+}
+
+int record_step(sgq_model *m, float *logits) {
+    const sgq_model_config &c = m->cfg;
+    hipStream_t st = ctx_stream(m->ctx);
+    const int H = (int)c.hidden, F = (int)c.ffn, QD = (int)(c.n_q_heads * kHeadDim),
+              KD = (int)(c.n_kv_heads * kHeadDim);
+    BlockLimbs *xl = static_cast<BlockLimbs *>(m->xl);
+    const size_t row_lds = (size_t)H * 4;
+    int rc;
+    hipLaunchKernelGGL(embed_norm_kernel, dim3(1), dim3(kRowWG), row_lds, st,
+                       static_cast<const uint8_t *>(m->embd), m->step, H, sqrtf((float)H),
+                       m->layers[0].attn_norm, c.eps, m->x, xl);
+    SGQ_HIP(hipGetLastError());
+    for (size_t li = 0; li < m->layers.size(); li++) {
+        const LayerW &L = m->layers[li];
+        GemvTargets qkv{};
+        qkv.w[0] = L.wq, qkv.w[1] = L.wk, qkv.w[2] = L.wv;
+        qkv.y[0] = m->q_raw, qkv.y[1] = m->k_raw, qkv.y[2] = m->v_raw;
+        qkv.end[0] = QD, qkv.end[1] = QD + KD, qkv.end[2] = QD + 2 * KD;
+        qkv.count = L.wv ? 3 : 2;
+        const float *v_src = L.wv ? m->v_raw : m->k_raw;
+        if ((rc = launch_gemv_limbs(st, qkv, xl, H))) return rc;
+        const float theta = L.global ? c.rope_theta_global : c.rope_theta_sliding;
+        const int live = L.global ? (int)lroundf(c.global_rope_frac * kHeadDim / 2) : kHeadDim / 2;
+        hipLaunchKernelGGL(qkv_post_kernel, dim3(c.n_q_heads + 2 * c.n_kv_heads), dim3(kHeadDim), 0,
+                           st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm, m->step,
+                           (int)c.n_q_heads, (int)c.n_kv_heads, theta, live,
+                           L.global ? 0 : (int)c.sliding_window, c.eps, m->q, L.kq, L.ks, L.vq,
+                           L.vs);
+        SGQ_HIP(hipGetLastError());
+        const int n_splits = L.global ? 32 : 16;
+        if ((rc = launch_attn_decode_q8(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step, L.global ? 2 : 1,
+                                        0, (int)c.n_q_heads, (int)c.n_kv_heads, kHeadDim, n_splits,
+                                        c.attn_scale, m->attn, ctx_workspace(m->ctx),
+                                        kWorkspaceBytes)))
+            return rc;
+        if ((rc = launch_quant_limbs(st, m->attn, xl, QD))) return rc;
+        GemvTargets ot{};
+        ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
+        if ((rc = launch_gemv_limbs(st, ot, xl, QD))) return rc;
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), row_lds, st, m->o,
+                           L.post_attn_norm, m->x, (const float *)nullptr, L.ffn_norm, H, c.eps, xl);
+        SGQ_HIP(hipGetLastError());
+        GemvTargets gu{};
+        gu.w[0] = L.wg, gu.w[1] = L.wu, gu.y[0] = m->g, gu.y[1] = m->u;
+        gu.end[0] = F, gu.end[1] = 2 * F, gu.count = 2;
+        if ((rc = launch_gemv_limbs(st, gu, xl, H))) return rc;
+        hipLaunchKernelGGL(geglu_limbs_kernel, dim3((F / 32 + 255) / 256), dim3(256), 0, st, m->g,
+                           m->u, F, xl);
+        SGQ_HIP(hipGetLastError());
+        GemvTargets dt{};
+        dt.w[0] = L.wd, dt.y[0] = m->f, dt.end[0] = H, dt.count = 1;
+        if ((rc = launch_gemv_limbs(st, dt, xl, F))) return rc;
+        const float *w_next =
+            li + 1 < m->layers.size() ? m->layers[li + 1].attn_norm : m->out_norm;
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), row_lds, st, m->f,
+                           L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
+        SGQ_HIP(hipGetLastError());
+    }
+    GemvTargets head{};
+    head.w[0] = m->embd, head.y[0] = logits, head.end[0] = (int)c.vocab, head.count = 1;
+    head.softcap = c.final_softcap;
+    return launch_gemv_limbs(st, head, xl, H);
+}
+
+}  // namespace
+
+extern "C" {
+
+void sgq_model_default_config(sgq_model_config *c) {
+    std::memset(c, 0, sizeof *c);
+    c->n_layers = 62;
+    c->hidden = 5376;
+    c->ffn = 21504;
+    c->n_q_heads = 32;
+    c->n_kv_heads = 16;
+    c->head_dim = 128;
+    c->vocab = 262144;
+    c->sliding_window = 1024;
+    c->global_every = 6;
+    c->max_ctx = 16384;
+    c->rope_theta_sliding = 10000.f;
+    c->rope_theta_global = 1000000.f;
+    c->global_rope_frac = 0.25f;
+    c->eps = 1e-6f;
+    c->attn_scale = 1.0f;
+    c->final_softcap = 30.f;
+    c->weight_sigma = 0.02f;
+    c->seed = 0x5EED;
+    c->global_k_eq_v = 1;
+}
+
+int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out) {
+    if (!ctx || !cfg || !out) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    const sgq_model_config &c = *cfg;
+    SGQ_CHECK(c.head_dim == kHeadDim, "model: head_dim must be 128");
+    SGQ_CHECK(c.hidden % 256 == 0 && c.ffn % 256 == 0 && (c.n_q_heads * kHeadDim) % 256 == 0,
+              "model: hidden, ffn and q_dim must be multiples of 256");
+    SGQ_CHECK(c.n_kv_heads > 0 && c.n_q_heads % c.n_kv_heads == 0 &&
+                  c.n_q_heads / c.n_kv_heads <= 2,
+              "model: 1 or 2 q heads per kv head");
+    SGQ_CHECK(c.hidden <= 32768, "model: hidden too large for a row kernel");
+    SGQ_CHECK(c.ffn <= 65536 && c.n_q_heads * kHeadDim <= 65536, "model: GEMV K above 65536");
+    SGQ_CHECK(c.n_layers >= 1 && c.vocab >= 1 && c.max_ctx >= 1 && c.sliding_window >= 1,
+              "model: empty dimension");
+    SGQ_CHECK(c.global_every >= 1, "model: global_every must be >= 1");
+    SGQ_CHECK(c.global_rope_frac >= 0.f && c.global_rope_frac <= 1.f, "model: global_rope_frac");
+    if (int rc0 = gemv_prepare()) return rc0;
+    (void)device_info();
+    auto *m = new sgq_model;
+    m->ctx = ctx;
+    m->cfg = c;
+    const size_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim,
+                 KD = c.n_kv_heads * kHeadDim;
+    int rc = SGQ_OK;
+    auto fail_out = [&](int r) {
+        sgq_model_destroy(m);
+        return r;
+    };
+    uint64_t s = c.seed;
+    if ((rc = q4_tensor(m, c.vocab, H, mix(s, 1), &m->embd))) return fail_out(rc);
+    if ((rc = f32_tensor(m, H, mix(s, 2), 1.0f, 0.1f, &m->out_norm))) return fail_out(rc);
+    m->layers.resize(c.n_layers);
+    for (uint32_t li = 0; li < c.n_layers; li++) {
+        LayerW &L = m->layers[li];
+        const uint64_t ls = mix(s, 1000 + li);
+        L.global = (li % c.global_every) == c.global_every - 1;
+        if ((rc = q4_tensor(m, QD, H, mix(ls, 1), &L.wq)) || (rc = q4_tensor(m, KD, H, mix(ls, 2), &L.wk)) ||
+            (!(L.global && c.global_k_eq_v) && (rc = q4_tensor(m, KD, H, mix(ls, 3), &L.wv))) ||
+            (rc = q4_tensor(m, H, QD, mix(ls, 4), &L.wo)) ||
+            (rc = q4_tensor(m, F, H, mix(ls, 5), &L.wg)) || (rc = q4_tensor(m, F, H, mix(ls, 6), &L.wu)) ||
+            (rc = q4_tensor(m, H, F, mix(ls, 7), &L.wd)) ||
+            (rc = f32_tensor(m, H, mix(ls, 8), 1.f, 0.1f, &L.attn_norm)) ||
+            (rc = f32_tensor(m, kHeadDim, mix(ls, 9), 1.f, 0.1f, &L.q_norm)) ||
+            (rc = f32_tensor(m, kHeadDim, mix(ls, 10), 1.f, 0.1f, &L.k_norm)) ||
+            (rc = f32_tensor(m, H, mix(ls, 11), 1.f, 0.1f, &L.post_attn_norm)) ||
+            (rc = f32_tensor(m, H, mix(ls, 12), 1.f, 0.1f, &L.ffn_norm)) ||
+            (rc = f32_tensor(m, H, mix(ls, 13), 1.f, 0.1f, &L.post_ffw_norm)) ||
+            (rc = f32_tensor(m, 1, mix(ls, 14), 0.9f, 0.05f, &L.out_scale)))
+            return fail_out(rc);
+        L.slots = L.global ? c.max_ctx : std::min(c.sliding_window, c.max_ctx);
+        const size_t kvn = (size_t)L.slots * KD;
+        if ((rc = alloc(m, kvn, reinterpret_cast<void **>(&L.kq))) ||
+            (rc = alloc(m, kvn, reinterpret_cast<void **>(&L.vq))) ||
+            (rc = alloc(m, kvn / 32 * 2, reinterpret_cast<void **>(&L.ks))) ||
+            (rc = alloc(m, kvn / 32 * 2, reinterpret_cast<void **>(&L.vs))))
+            return fail_out(rc);
+    }
+    float **acts[] = {&m->x, &m->q_raw, &m->k_raw, &m->v_raw, &m->q, &m->attn, &m->o, &m->g, &m->u, &m->f};
+    const size_t act_n[] = {H, QD, KD, KD, QD, QD, H, F, F, H};
+    for (int i = 0; i < 10; i++)
+        if ((rc = alloc(m, act_n[i] * 4, reinterpret_cast<void **>(acts[i])))) return fail_out(rc);
+    if ((rc = alloc(m, std::max(H, F) / 32 * sizeof(BlockLimbs), &m->xl))) return fail_out(rc);
+    if ((rc = alloc(m, 64, reinterpret_cast<void **>(&m->step)))) return fail_out(rc);
+    if (hipStreamSynchronize(ctx_stream(ctx)) != hipSuccess) return fail_out(fail(SGQ_ERR_HIP, "init sync"));
+    *out = m;
+    return SGQ_OK;
+}
+
+int sgq_model_destroy(sgq_model *m) {
+    if (!m) return SGQ_OK;
+    if (m->graph) sgq_graph_destroy(m->graph);
+    (void)hipDeviceSynchronize();
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+    return SGQ_OK;
+}
+
+int sgq_model_reset(sgq_model *m) {
+    if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
+    m->pos = 0;
+    return SGQ_OK;
+}
+
+uint32_t sgq_model_position(const sgq_model *m) { return m ? m->pos : 0; }
+
+static int write_step(sgq_model *m, uint32_t token) {
+    const sgq_model_config &c = m->cfg;
+    SGQ_CHECK(token < c.vocab, "model: token %u >= vocab %u", token, c.vocab);
+    SGQ_CHECK(m->pos < c.max_ctx, "model: context full (%u)", c.max_ctx);
+    const uint32_t kv_sl = std::min(m->pos + 1, std::min(c.sliding_window, c.max_ctx));
+    hipLaunchKernelGGL(model_step_kernel, dim3(1), dim3(64), 0, ctx_stream(m->ctx), m->step,
+                       m->pos, kv_sl, m->pos + 1, m->pos, token);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int sgq_model_decode(sgq_model *m, uint32_t token, float *logits) {
+    if (!m || !logits) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    int rc = write_step(m, token);
+    if (rc) return rc;
+    if ((rc = record_step(m, logits))) return rc;
+    m->pos++;
+    return SGQ_OK;
+}
+
+int sgq_model_decode_graph(sgq_model *m, uint32_t token, float *logits) {
+    if (!m || !logits) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_CHECK(ctx_stream(m->ctx) != nullptr,
+              "model: graph decode needs a non-null stream (sgq_ctx_set_stream)");
+    int rc = write_step(m, token);
+    if (rc) return rc;
+    if (!m->graph || m->graph_logits != logits) {
+        if (m->graph) {
+            sgq_graph_destroy(m->graph);
+            m->graph = nullptr;
+        }
+        if ((rc = sgq_graph_begin(m->ctx))) return rc;
+        rc = record_step(m, logits);
+        sgq_graph *g = nullptr;
+        const int rc2 = sgq_graph_end(m->ctx, &g);
+        if (rc) {
+            if (g) sgq_graph_destroy(g);
+            return rc;
+        }
+        if (rc2) return rc2;
+        m->graph = g;
+        m->graph_logits = logits;
+    }
+    if ((rc = sgq_graph_submit(m->ctx, m->graph))) return rc;
+    m->pos++;
+    return SGQ_OK;
+}
+
+int sgq_model_fill_cache(sgq_model *m, uint32_t n_tokens, uint64_t seed) {
+    if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
+    const sgq_model_config &c = m->cfg;
+    SGQ_CHECK(n_tokens <= c.max_ctx, "model: fill_cache %u > max_ctx %u", n_tokens, c.max_ctx);
+    const size_t KD = (size_t)c.n_kv_heads * kHeadDim;
+    hipStream_t st = ctx_stream(m->ctx);
+    size_t most = 0;
+    for (const LayerW &L : m->layers) most = std::max(most, (size_t)std::min(n_tokens, L.slots));
+    float *tmp = nullptr;
+    if (most) SGQ_HIP(hipMalloc(&tmp, most * KD * 4));
+    int rc = SGQ_OK;
+    for (size_t li = 0; li < m->layers.size() && !rc; li++) {
+        const LayerW &L = m->layers[li];
+        const size_t rows = std::min(n_tokens, L.slots);
+        if (!rows) continue;
+        for (int kv = 0; kv < 2 && !rc; kv++) {
+            rc = launch_fill_normal(st, tmp, rows * KD, mix(seed, li * 2 + kv), 0.f, 1.f);
+            if (!rc)
+                rc = launch_quant_q8_0(st, tmp, kv ? L.vs : L.ks, kv ? L.vq : L.kq, rows * KD);
+        }
+    }
+    if (tmp) {
+        const hipError_t e = hipStreamSynchronize(st);
+        (void)hipFree(tmp);
+        if (!rc && e != hipSuccess) rc = check_hip(e, "fill_cache sync");
+    }
+    if (!rc) m->pos = n_tokens;
+    return rc;
+}
+
+int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr,
+                     uint64_t *bytes) {
+    if (!m || !name || !ptr || !bytes) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    const sgq_model_config &c = m->cfg;
+    const size_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim;
+    auto q4 = [](size_t r, size_t k) { return (uint64_t)(r * (k / 32) * 18); };
+    std::string n(name);
+    if (layer < 0) {
+        if (n == "token_embd") { *ptr = m->embd; *bytes = q4(c.vocab, H); return SGQ_OK; }
+        if (n == "output_norm") { *ptr = m->out_norm; *bytes = H * 4; return SGQ_OK; }
+        if (n == "x") { *ptr = m->x; *bytes = H * 4; return SGQ_OK; }
+        return fail(SGQ_ERR_VALIDATION, "model: no global tensor '%s'", name);
+    }
+    SGQ_CHECK(layer < (int)m->layers.size(), "model: layer %d out of range", layer);
+    const LayerW &L = m->layers[layer];
+    struct E { const char *n; void *p; uint64_t b; };
+    const uint64_t kvn = (uint64_t)L.slots * KD;
+    const E table[] = {
+        {"attn_q", L.wq, q4(QD, H)}, {"attn_k", L.wk, q4(KD, H)}, {"attn_v", L.wv, q4(KD, H)},
+        {"attn_output", L.wo, q4(H, QD)}, {"ffn_gate", L.wg, q4(F, H)}, {"ffn_up", L.wu, q4(F, H)},
+        {"ffn_down", L.wd, q4(H, F)}, {"attn_norm", L.attn_norm, H * 4},
+        {"attn_q_norm", L.q_norm, kHeadDim * 4}, {"attn_k_norm", L.k_norm, kHeadDim * 4},
+        {"post_attention_norm", L.post_attn_norm, H * 4}, {"ffn_norm", L.ffn_norm, H * 4},
+        {"post_ffw_norm", L.post_ffw_norm, H * 4}, {"layer_output_scale", L.out_scale, 4},
+        {"k_quants", L.kq, kvn}, {"v_quants", L.vq, kvn}, {"k_scales", L.ks, kvn / 16},
+        {"v_scales", L.vs, kvn / 16},
+    };
+    for (const E &e : table)
+        if (n == e.n && e.p) {
+            *ptr = e.p;
+            *bytes = e.b;
+            return SGQ_OK;
+        }
+    return fail(SGQ_ERR_VALIDATION, "model: no layer tensor '%s'", name);
+}
+
+}  // extern "C"

@@ -50,6 +50,21 @@ constexpr size_t kAttnPartOff = kAttnCounterOff + 4096;
 constexpr size_t kWorkspaceBytes = 16u << 20;
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
                      uint32_t k, void *workspace);
+// Up to kGemvMaxTargets Q4_0 matrices with the same K whose rows form one
+// concatenated row space (rows [end[j-1], end[j]) belong to matrix j), read
+// against one x limb table.  softcap > 0 applies cap*tanh(v/cap) on output.
+constexpr int kGemvMaxTargets = 4;
+struct GemvTargets {
+    const void *w[kGemvMaxTargets];
+    float *y[kGemvMaxTargets];
+    int end[kGemvMaxTargets];
+    int count;
+    float softcap;
+};
+// Sets the streamed kernels' launch attributes (call before graph capture).
+int gemv_prepare();
+int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k);
+int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k);
 int launch_quant_q8_0(hipStream_t st, const float *x, uint16_t *scales, int8_t *quants,
                       uint64_t n_elems);
 int launch_dequant_q8_0(hipStream_t st, const uint16_t *scales, const int8_t *quants, float *out,

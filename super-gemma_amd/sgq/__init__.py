@@ -73,6 +73,19 @@ class _Binding(C.Structure):
                 ("offset", C.c_uint64), ("range", C.c_uint64)]
 
 
+class ModelConfig(C.Structure):
+    """sgq_model_config (include/sgq.h)."""
+    _fields_ = [(n, C.c_uint32) for n in (
+        "n_layers", "hidden", "ffn", "n_q_heads", "n_kv_heads", "head_dim", "vocab",
+        "sliding_window", "global_every", "max_ctx")] + [(n, C.c_float) for n in (
+        "rope_theta_sliding", "rope_theta_global", "global_rope_frac", "eps", "attn_scale",
+        "final_softcap", "weight_sigma")] + [("global_k_eq_v", C.c_uint32), ("_pad", C.c_uint32),
+                                             ("seed", C.c_uint64)]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_ if n != "_pad"}
+
+
 # Exported symbols and their ctypes signatures (checked against include/sgq.h
 # by tests/test_abi.py).
 P, U32, U64, I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
@@ -104,6 +117,15 @@ SIGNATURES = {
     "sgq_dequant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_gemm_q4_0_q8": (I, [P, P, P, P, P, U32, U32, U32, U32, P]),
     "sgq_attn_decode_q8": (I, [P, P, P, P, P, P, U32, U32, U32, U32, U32, C.c_float, P]),
+    "sgq_model_default_config": (None, [C.POINTER(ModelConfig)]),
+    "sgq_model_create": (I, [P, C.POINTER(ModelConfig), C.POINTER(P)]),
+    "sgq_model_destroy": (I, [P]),
+    "sgq_model_reset": (I, [P]),
+    "sgq_model_position": (U32, [P]),
+    "sgq_model_decode": (I, [P, U32, P]),
+    "sgq_model_decode_graph": (I, [P, U32, P]),
+    "sgq_model_fill_cache": (I, [P, U32, U64]),
+    "sgq_model_tensor": (I, [P, I, C.c_char_p, C.POINTER(P), C.POINTER(U64)]),
     "sgq_fill_q4_0_random": (I, [P, P, U64, U64, C.c_float]),
     "sgq_fill_normal": (I, [P, P, U64, U64, C.c_float, C.c_float]),
 }
@@ -203,8 +225,10 @@ class GpuContext:
     def handle(self):
         return self._h
 
-    def set_stream(self, stream: torch.cuda.Stream):
-        _check(lib().sgq_ctx_set_stream(self._h, C.c_void_p(stream.cuda_stream)))
+    def set_stream(self, stream: Optional[torch.cuda.Stream]):
+        """Enqueue on a torch stream from now on (None: the null stream)."""
+        h = None if stream is None else stream.cuda_stream
+        _check(lib().sgq_ctx_set_stream(self._h, C.c_void_p(h)))
 
     def synchronize(self):
         _check(lib().sgq_sync(self._h))
@@ -342,6 +366,71 @@ class GraphRecorder:
             _check(rc)
             self.graph = Graph(self.ctx, h)
         return False
+
+
+def default_model_config(**overrides) -> ModelConfig:
+    """The benchmark decoder shape (sgq_model_default_config), with overrides."""
+    cfg = ModelConfig()
+    lib().sgq_model_default_config(C.byref(cfg))
+    for k, v in overrides.items():
+        if not hasattr(cfg, k):
+            raise ValidationError(6, f"unknown model config field {k}")
+        setattr(cfg, k, v)
+    return cfg
+
+
+class Model:
+    """The decode-step driver (sgq_model_*): a random-init decoder resident on
+    the context's device.  ``decode(token, logits)`` runs one step at the
+    current position and advances it; ``graph=True`` replays a recorded
+    hipGraph of the step (the context needs a non-null stream)."""
+
+    def __init__(self, ctx: GpuContext, cfg: Optional[ModelConfig] = None):
+        self.ctx = ctx
+        self.cfg = cfg if cfg is not None else default_model_config()
+        h = C.c_void_p()
+        _check(lib().sgq_model_create(ctx.handle, C.byref(self.cfg), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and _lib is not None:
+            _lib.sgq_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def position(self) -> int:
+        return int(lib().sgq_model_position(self._h))
+
+    def reset(self):
+        _check(lib().sgq_model_reset(self._h))
+
+    def decode(self, token: int, logits: torch.Tensor, graph: bool = False):
+        _need(logits, torch.float32, self.cfg.vocab, "logits")
+        fn = lib().sgq_model_decode_graph if graph else lib().sgq_model_decode
+        _check(fn(self._h, int(token), _ptr(logits)))
+
+    def fill_cache(self, n_tokens: int, seed: int = 0xCAC4E):
+        """Synthetic Q8_0 K/V for positions [0, n_tokens); position = n_tokens."""
+        _check(lib().sgq_model_fill_cache(self._h, n_tokens, seed))
+
+    def tensor_ptr(self, name: str, layer: int = -1):
+        p, b = C.c_void_p(), C.c_uint64()
+        _check(lib().sgq_model_tensor(self._h, layer, name.encode(), C.byref(p), C.byref(b)))
+        return p.value, b.value
+
+    def read_tensor(self, name: str, layer: int = -1, dtype=None):
+        """Host copy (numpy) of a named device tensor."""
+        import numpy as np
+        p, b = self.tensor_ptr(name, layer)
+        out = np.empty(b, np.uint8)
+        _check(lib().sgq_buf_download(self.ctx.handle, out.ctypes.data, p, b))
+        if dtype is None:
+            dtype = np.uint8 if name.startswith(("attn_", "ffn_", "token_embd")) and \
+                not name.endswith("norm") else np.float32
+        return out.view(dtype)
 
 
 def _need(t, dtypes, numel, name):

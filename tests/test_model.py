@@ -1,0 +1,157 @@
+"""GPU parity: the decode-step driver (sgq_model_*) vs the CPU oracle decoder.
+
+Template: the reference's GPU-vs-CPU model checks (crates/sg-model/tests/
+gpu_forward.rs: logits of the GPU graph vs ReferenceModel::forward with a
+max-abs / top-1 agreement).  The oracle reads the very weights the library
+generated (sgq_model_tensor) and runs reference.rs:157-316 in f64/f32 with
+Q8_0 K/V pages.
+
+Tolerance on logits, per step: |err| <= 2e-3*|want| + 2e-3*max|want|
+elementwise, and the same argmax (top-1) at every step.  The GPU differs from
+the oracle by the GEMV's x limbs (|err| <= 1.9e-6*amax per block), f32 vs f64
+accumulation, and an occasional Q8_0 rounding flip of a K/V element.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(model, cfg):
+    from oracle.model import LAYER_TENSORS
+
+    w = {("token_embd", -1): model.read_tensor("token_embd"),
+         ("output_norm", -1): model.read_tensor("output_norm")}
+    for l in range(cfg["n_layers"]):
+        for name in LAYER_TENSORS:
+            try:
+                w[(name, l)] = model.read_tensor(name, l)
+            except Exception:
+                if name != "attn_v":
+                    raise
+    return w
+
+
+def _check_logits(got, want, step):
+    top = float(np.abs(want).max())
+    assert_close(got, want, 2e-3, 2e-3 * top, f"logits step {step}")
+    assert int(np.argmax(got)) == int(np.argmax(want)), f"top-1 differs at step {step}"
+
+
+def _small_cfg(sgq, **kw):
+    base = dict(n_layers=4, hidden=512, ffn=1024, n_q_heads=4, n_kv_heads=2, vocab=2048,
+                sliding_window=4, global_every=2, max_ctx=16, seed=0x1234)
+    base.update(kw)
+    return sgq.default_model_config(**base)
+
+
+@pytest.mark.parametrize("k_eq_v", [1, 0])
+def test_model_small_decode_matches_oracle(ctx, oracle, k_eq_v):
+    """4 layers (2 sliding with a 4-slot ring, 2 global), 10 steps: the ring
+    wraps twice, global layers grow linearly."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print(f"model small k_eq_v={k_eq_v}", flush=True)
+    cfg = _small_cfg(sgq, global_k_eq_v=k_eq_v)
+    model = sgq.Model(ctx, cfg)
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    logits = empty(cfg.vocab, torch.float32)
+    tokens = [1, 2047, 5, 5, 100, 0, 1999, 42, 7, 3]
+    for i, t in enumerate(tokens):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    assert model.position == len(tokens)
+    model.close()
+
+
+def test_model_graph_replays_match_eager(ctx):
+    """hipGraph decode == eager decode, bit for bit, on every replay, with the
+    program's own eager work and synchronizations between replays."""
+    import sgq
+
+    print("model graph vs eager", flush=True)
+    cfg = _small_cfg(sgq, seed=0x777)
+    eager = sgq.Model(ctx, cfg)
+    graphed = sgq.Model(ctx, cfg)
+    s = torch.cuda.Stream()
+    a = empty(cfg.vocab, torch.float32)
+    b = empty(cfg.vocab, torch.float32)
+    ctx.set_stream(s)
+    try:
+        for i, t in enumerate([3, 9, 27, 81, 243, 729, 11, 13]):
+            eager.decode(t, a)
+            graphed.decode(t, b, graph=True)
+            ctx.synchronize()
+            scratch = torch.randn(4096, device="cuda").sum()  # unrelated eager work
+            torch.cuda.synchronize()
+            ga, gb = host(a), host(b)
+            assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), f"replay {i}"
+            assert np.isfinite(ga).all() and float(scratch) == float(scratch)
+    finally:
+        ctx.set_stream(None)
+    eager.close()
+    graphed.close()
+
+
+def test_model_reset_reproduces(ctx):
+    import sgq
+
+    cfg = _small_cfg(sgq, seed=0x99)
+    m = sgq.Model(ctx, cfg)
+    out = empty(cfg.vocab, torch.float32)
+    first = []
+    for t in (4, 8, 15):
+        m.decode(t, out)
+        torch.cuda.synchronize()
+        first.append(host(out).copy())
+    m.reset()
+    assert m.position == 0
+    for i, t in enumerate((4, 8, 15)):
+        m.decode(t, out)
+        torch.cuda.synchronize()
+        assert np.array_equal(first[i].view(np.uint32), host(out).view(np.uint32))
+    m.close()
+
+
+def test_model_full_width_two_layers_matches_oracle(ctx, oracle):
+    """The benchmark widths (hidden 5376, ffn 21504, 32 q / 16 kv heads,
+    vocab 262144) at 2 layers (one sliding, one global): 3 steps."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print("model full width 2 layers", flush=True)
+    cfg = sgq.default_model_config(n_layers=2, global_every=2, max_ctx=64, seed=0xF00D)
+    model = sgq.Model(ctx, cfg)
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([2, 262143, 31337]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
+
+
+def test_model_rejects_bad_inputs(ctx):
+    import sgq
+
+    cfg = _small_cfg(sgq, max_ctx=2)
+    m = sgq.Model(ctx, cfg)
+    out = empty(cfg.vocab, torch.float32)
+    with pytest.raises(sgq.GpuError):
+        m.decode(cfg.vocab, out)  # token out of range
+    m.decode(1, out)
+    m.decode(1, out)
+    with pytest.raises(sgq.GpuError):
+        m.decode(1, out)  # context full
+    m.close()
+    with pytest.raises(sgq.GpuError):
+        sgq.Model(ctx, sgq.default_model_config(head_dim=64))
+    with pytest.raises(sgq.GpuError):
+        sgq.Model(ctx, sgq.default_model_config(n_q_heads=48))  # 3 q heads per kv head
