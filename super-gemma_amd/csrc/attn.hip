@@ -23,7 +23,7 @@
 //    the partials in split order 0..S-1 — the same fixed order as
 //    attn_reduce.wgsl:40-52, so results do not depend on which workgroup
 //    merged.  Empty splits carry (m = -3e38, l = 0, acc = 0).
-#include "sgq_internal.h"
+#include "limbs.h"
 
 namespace sgq {
 namespace {
@@ -32,28 +32,6 @@ constexpr int kHD = 128;
 constexpr int kAWG = 256;
 constexpr int kSub = 256;             // slots scored per pass
 constexpr float kNegBig = -3.0e38f;
-
-__device__ __forceinline__ float block_sum(float v, float *red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < kAWG / kWave; w++) r += red[w];
-    return r;
-}
-
-__device__ __forceinline__ float block_max(float v, float *red) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < kAWG / kWave; w++) r = fmaxf(r, red[w]);
-    return r;
-}
 
 // Dequantized dot of a 128-wide K row (int8 + 4 f16 scales) with q (LDS).
 __device__ __forceinline__ float k_row_dot(const int4 (&kr)[8], const float (&ksc)[4],
@@ -86,17 +64,21 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
     const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
     const uint32_t *__restrict__ step, int step_word, uint32_t kv_len_direct, int n_kv,
     int n_splits, float scale, float *__restrict__ part, unsigned *__restrict__ counters,
-    float *__restrict__ out) {
+    float *__restrict__ out, BlockLimbs *__restrict__ limbs_out) {
     constexpr int G = kAWG / (QPK * (kHD / 4));  // slot groups in the PV phase
     static_assert(G >= 1, "QPK too large for one workgroup");
+    constexpr int kVRow = kHD / 4 + 4;           // V row in LDS, ints (padded)
     __shared__ __align__(16) float q_s[QPK][kHD];
-    __shared__ float s_s[QPK][kSub];     // scores, then probabilities
-    __shared__ float vs_s[kSub][kHD / 32];  // V scales of the sub-chunk
-    __shared__ float red[kAWG / kWave];
+    __shared__ float s_s[QPK][kSub];             // probabilities of the sub-chunk
+    __shared__ float vs_s[kSub][kHD / 32];       // V scales of the sub-chunk
+    __shared__ __align__(16) int v_s[kSub][kVRow];  // V quants of the sub-chunk
+    __shared__ float red[QPK][kAWG / kWave];
     __shared__ float acc_s[G][QPK][kHD];
+    __shared__ float wgt_s[2][QPK][64];          // merge: split weights, batch of 64
     __shared__ int last_s;
 
     const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const uint32_t kv_len = step ? step[step_word] : kv_len_direct;
     const uint32_t chunk = (kv_len + n_splits - 1) / n_splits;
     const uint32_t t_begin = min((uint32_t)split * chunk, kv_len);
@@ -114,62 +96,93 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
         m_run[h] = kNegBig;
         l_run[h] = 0.f;
     }
-    __syncthreads();
 
     for (uint32_t base = t_begin; base < t_end; base += kSub) {
         const int n_here = (int)min((uint32_t)kSub, t_end - base);
-        // ---- scores: thread tid scores slot base + tid for every head
-        {
-            const int t = tid;
-            float sc[QPK];
-            if (t < n_here) {
-                const size_t row = (size_t)(base + t) * n_kv + kvh;
-                const int4 *kp = reinterpret_cast<const int4 *>(kq + row * kHD);
-                int4 kr[8];
+        const int t = tid;
+        // ---- one slot per thread: K row, V row and both scale words issued
+        // together (one memory round trip for the whole sub-chunk)
+        int4 kr[8], vr[8];
+        uint2 kss = {0u, 0u}, vss = {0u, 0u};
+        if (t < n_here) {
+            const size_t row = (size_t)(base + t) * n_kv + kvh;
+            const int4 *kp = reinterpret_cast<const int4 *>(kq + row * kHD);
+            const int4 *vp = reinterpret_cast<const int4 *>(vq + row * kHD);
 #pragma unroll
-                for (int c = 0; c < 8; c++) kr[c] = kp[c];
-                const uint2 kss = *reinterpret_cast<const uint2 *>(ks + row * (kHD / 32));
-                const uint2 vss = *reinterpret_cast<const uint2 *>(vs + row * (kHD / 32));
-                const float ksc[4] = {f16_bits_to_f32(kss.x & 0xffff), f16_bits_to_f32(kss.x >> 16),
-                                      f16_bits_to_f32(kss.y & 0xffff), f16_bits_to_f32(kss.y >> 16)};
-                vs_s[t][0] = f16_bits_to_f32(vss.x & 0xffff);
-                vs_s[t][1] = f16_bits_to_f32(vss.x >> 16);
-                vs_s[t][2] = f16_bits_to_f32(vss.y & 0xffff);
-                vs_s[t][3] = f16_bits_to_f32(vss.y >> 16);
+            for (int c = 0; c < 8; c++) kr[c] = kp[c];
 #pragma unroll
-                for (int h = 0; h < QPK; h++) sc[h] = k_row_dot(kr, ksc, q_s[h]) * scale;
-            } else {
+            for (int c = 0; c < 8; c++) vr[c] = vp[c];
+            kss = *reinterpret_cast<const uint2 *>(ks + row * (kHD / 32));
+            vss = *reinterpret_cast<const uint2 *>(vs + row * (kHD / 32));
+        }
+        __syncthreads();  // q_s ready; previous sub-chunk's LDS reads done
+        float sc[QPK];
+        if (t < n_here) {
 #pragma unroll
-                for (int h = 0; h < QPK; h++) sc[h] = kNegBig;
-            }
-            // ---- online softmax over this sub-chunk, per head
+            for (int c = 0; c < 8; c++) *reinterpret_cast<int4 *>(&v_s[t][4 * c]) = vr[c];
+            vs_s[t][0] = f16_bits_to_f32(vss.x & 0xffff);
+            vs_s[t][1] = f16_bits_to_f32(vss.x >> 16);
+            vs_s[t][2] = f16_bits_to_f32(vss.y & 0xffff);
+            vs_s[t][3] = f16_bits_to_f32(vss.y >> 16);
+            const float ksc[4] = {f16_bits_to_f32(kss.x & 0xffff), f16_bits_to_f32(kss.x >> 16),
+                                  f16_bits_to_f32(kss.y & 0xffff), f16_bits_to_f32(kss.y >> 16)};
 #pragma unroll
-            for (int h = 0; h < QPK; h++) {
-                const float mx = block_max(sc[h], red);
-                const float m_new = fmaxf(m_run[h], mx);
-                const float p = t < n_here ? __expf(sc[h] - m_new) : 0.f;
-                s_s[h][t] = p;
-                const float corr = __expf(m_run[h] - m_new);
-                m_run[h] = m_new;
-                if (h == ph) {
+            for (int h = 0; h < QPK; h++) sc[h] = k_row_dot(kr, ksc, q_s[h]) * scale;
+        } else {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[e] *= corr;
-                }
-                l_run[h] = l_run[h] * corr + block_sum(p, red);  // fixed-order tree sum
-            }
+            for (int h = 0; h < QPK; h++) sc[h] = kNegBig;
+        }
+        // ---- online softmax over this sub-chunk: one max and one sum
+        // round per sub-chunk for all heads (fixed-order trees)
+        float mx[QPK];
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            float v = sc[h];
+            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+            if (lane == 0) red[h][wave] = v;
         }
         __syncthreads();
-        // ---- PV: thread (ph, pw, pg) accumulates slots pg, pg+G, ...
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            float r = red[h][0];
+            for (int w = 1; w < kAWG / kWave; w++) r = fmaxf(r, red[h][w]);
+            mx[h] = r;
+        }
+        float p[QPK], corr[QPK];
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            const float m_new = fmaxf(m_run[h], mx[h]);
+            p[h] = t < n_here ? __expf(sc[h] - m_new) : 0.f;
+            s_s[h][t] = p[h];
+            corr[h] = __expf(m_run[h] - m_new);
+            m_run[h] = m_new;
+        }
+        __syncthreads();  // red (max) consumed; s_s, v_s, vs_s written
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            float v = p[h];
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+            if (lane == 0) red[h][wave] = v;
+        }
+        const float cph = QPK == 1 ? corr[0] : (ph == 0 ? corr[0] : corr[QPK - 1]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[e] *= cph;
+        // ---- PV from LDS: thread (ph, pw, pg) takes slots pg, pg+G, ...
         for (int i = pg; i < n_here; i += G) {
-            const size_t row = (size_t)(base + i) * n_kv + kvh;
-            const int v4 = *reinterpret_cast<const int *>(vq + row * kHD + 4 * pw);
+            const int v4 = v_s[i][pw];
             const float pp = s_s[ph][i] * vs_s[i][pw / 8];
             acc[0] = __builtin_fmaf(pp, (float)(int8_t)(v4 & 0xff), acc[0]);
             acc[1] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 8) & 0xff), acc[1]);
             acc[2] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 16) & 0xff), acc[2]);
             acc[3] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 24) & 0xff), acc[3]);
         }
-        __syncthreads();  // s_s / vs_s reused by the next sub-chunk
+        __syncthreads();  // red (sum) written
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            float r = red[h][0];
+            for (int w = 1; w < kAWG / kWave; w++) r += red[h][w];
+            l_run[h] = l_run[h] * corr[h] + r;
+        }
     }
 
     // ---- combine the G slot groups (fixed order) and write the partial
@@ -200,22 +213,67 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
     __syncthreads();
     if (!last_s) return;
     __threadfence();
-    for (int i = tid; i < QPK * kHD; i += kAWG) {
-        const int h = i / kHD, d = i % kHD;
-        const float *ph_part = part + (size_t)(kvh * QPK + h) * n_splits * stride;
-        float m = kNegBig, l = 0.f, a = 0.f;
-        for (int s = 0; s < n_splits; s++) {
-            const float *r = ph_part + (size_t)s * stride;
-            const float ms = __builtin_nontemporal_load(r + kHD);
-            const float ls = __builtin_nontemporal_load(r + kHD + 1);
-            const float as = __builtin_nontemporal_load(r + d);
-            const float mn = fmaxf(m, ms);
-            const float ca = __expf(m - mn), cb = __expf(ms - mn);
-            a = a * ca + as * cb;
-            l = l * ca + ls * cb;
-            m = mn;
+    // out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s, sums in
+    // split order 0..S-1 (fixed, so the result does not depend on which
+    // workgroup merges).  Wave h computes M for head h.
+    float M[QPK];
+    if (wave < QPK) {
+        const float *ph_part = part + (size_t)(kvh * QPK + wave) * n_splits * stride;
+        float v = kNegBig;
+        for (int s2 = lane; s2 < n_splits; s2 += kWave)
+            v = fmaxf(v, __builtin_nontemporal_load(ph_part + (size_t)s2 * stride + kHD));
+        for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+        if (lane == 0) red[wave][0] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < QPK; h++) M[h] = red[h][0];
+    const int h = tid / kHD % QPK, d = tid % kHD;
+    const bool active = tid < QPK * kHD;
+    const float *ph_part = part + (size_t)(kvh * QPK + h) * n_splits * stride;
+    float a = 0.f, l = 0.f;
+    for (int s0 = 0; s0 < n_splits; s0 += 64) {
+        const int nb = min(64, n_splits - s0);
+        // weights e^(m_s - M) and l_s for this batch, one lane per split
+        if (wave < QPK && lane < nb) {
+            const float *r = part + ((size_t)(kvh * QPK + wave) * n_splits + s0 + lane) * stride;
+            wgt_s[0][wave][lane] = __expf(__builtin_nontemporal_load(r + kHD) - M[wave]);
+            wgt_s[1][wave][lane] = __builtin_nontemporal_load(r + kHD + 1);
         }
-        out[(size_t)(kvh * QPK + h) * kHD + d] = a / l;
+        __syncthreads();
+        if (active) {
+            int j = 0;
+            for (; j + 8 <= nb; j += 8) {
+                float as[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    as[u] = __builtin_nontemporal_load(ph_part + (size_t)(s0 + j + u) * stride + d);
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    a = __builtin_fmaf(as[u], wgt_s[0][h][j + u], a);
+                    l = __builtin_fmaf(wgt_s[1][h][j + u], wgt_s[0][h][j + u], l);
+                }
+            }
+            for (; j < nb; j++) {
+                const float as = __builtin_nontemporal_load(ph_part + (size_t)(s0 + j) * stride + d);
+                a = __builtin_fmaf(as, wgt_s[0][h][j], a);
+                l = __builtin_fmaf(wgt_s[1][h][j], wgt_s[0][h][j], l);
+            }
+        }
+        __syncthreads();
+    }
+    if (active) {
+        const float r = a / l;
+        out[(size_t)(kvh * QPK + h) * kHD + d] = r;
+        acc_s[0][h][d] = r;
+    }
+    if (limbs_out == nullptr) return;
+    // x limbs of this kv head's QPK output rows for the next GEMV (8 lanes
+    // per 32-block; the rows are contiguous in the output vector)
+    __syncthreads();
+    if (tid < QPK * kHD / 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(&acc_s[0][0][4 * tid]);
+        limbs_block8(v, tid & 7, &limbs_out[(kvh * QPK * kHD) / 32 + (tid >> 3)]);
     }
 }
 
@@ -225,7 +283,7 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
                           const int8_t *vq, const uint16_t *vs, const uint32_t *step,
                           int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
                           int n_splits, float scale, float *out, void *workspace,
-                          size_t workspace_bytes) {
+                          size_t workspace_bytes, void *limbs_out) {
     SGQ_CHECK(head_dim == kHD, "attn_decode_q8: head_dim %d unsupported (128)", head_dim);
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_decode_q8: n_q %% n_kv != 0");
     SGQ_CHECK(n_splits >= 1 && n_splits <= 1024, "attn_decode_q8: n_splits %d out of range", n_splits);
@@ -248,7 +306,8 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
 #define SGQ_ATTN(Q)                                                                               \
     case Q:                                                                                       \
         hipLaunchKernelGGL(attn_decode_q8_kernel<Q>, grid, dim3(kAWG), 0, st, q, kq, ks, vq, vs,  \
-                           step, step_word, kv_len, n_kv, n_splits, scale, part, counters, out); \
+                           step, step_word, kv_len, n_kv, n_splits, scale, part, counters, out,    \
+                           static_cast<BlockLimbs *>(limbs_out));                                 \
         break;
     switch (qpk) {
         SGQ_ATTN(1)

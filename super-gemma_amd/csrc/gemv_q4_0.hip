@@ -8,13 +8,13 @@
 //  * VALU, not the MFMA, is the scarce unit next to an 8 TB/s weight stream:
 //    at ~1 wave-instruction per 4 cycles per SIMD, an fp32 FMA form (nibble
 //    split, int->f32, FMA: ~2.4 ops/weight) takes as long as the stream.
-//    So x is split once per 32-block into five signed 4-bit limbs,
-//    x ≈ (amax/7)·(l1 + l2/14 + l3/14² + l4/14³ + l5/14⁴), l ∈ [-7, 7]
-//    (|error| ≤ amax·1.9e-6), and the inner loop is v_dot8_i32_i4 on the
+//    So x is split once per 32-block into four signed 4-bit limbs,
+//    x ≈ (amax/7)·(l1 + l2/14 + l3/14² + l4/14³), l ∈ [-7, 7]
+//    (|error| ≤ amax·2.6e-5), and the inner loop is v_dot8_i32_i4 on the
 //    weight nibbles themselves: qs ^ 0x88888888 turns every nibble q into
 //    the signed 4-bit value q-8, so one XOR per 8 weights is the whole
-//    unpack.  Per block: 4 perm + 4 xor + 20 dot8 + 3 Horner steps in two
-//    exact integer accumulators + 2 cvt + 1 fma + 2 mul.
+//    unpack.  Per block: 4 perm + 4 xor + 16 dot8 + 3 Horner steps in one
+//    exact integer accumulator (|c| <= 1792·2955 < 2^23) + cvt + 2 mul.
 //  * x limbs live in registers for the whole kernel: lane l of a wave always
 //    owns blocks l, l+64, l+128 of its K-slice.
 //  * Each lane reads its block as 20 bytes from a 4-byte-aligned address
@@ -44,22 +44,17 @@ __device__ __forceinline__ float block_dot(const uint32_t (&w)[5], uint32_t sel,
     int t[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) t[j] = (int)(__builtin_amdgcn_perm(w[j + 1], w[j], sel) ^ 0x88888888u);
-    // limbs 1-3 Horner-combined in c_hi (|c_hi| <= 1792·211, 24-bit safe),
-    // limbs 4-5 in c_lo; joined in f32: c_hi·196 + c_lo.
-    int c_hi = 0, c_lo = 0;
+    // Horner over the limbs in one exact integer accumulator: each limb's
+    // partial is <= 32·8·7 = 1792 in magnitude, so |c| <= 1792·2955 < 2^23
+    // and the 24-bit multiply is exact.
+    int ci = 0;
 #pragma unroll
-    for (int l = 0; l < 3; l++) {
-        if (l) c_hi = __mul24(c_hi, 14);
+    for (int l = 0; l < kLimbs; l++) {
+        if (l) ci = __mul24(ci, 14);
 #pragma unroll
-        for (int j = 0; j < 4; j++) c_hi = __builtin_amdgcn_sdot8(t[j], L.q[i][l][j], c_hi, false);
+        for (int j = 0; j < 4; j++) ci = __builtin_amdgcn_sdot8(t[j], L.q[i][l][j], ci, false);
     }
-#pragma unroll
-    for (int l = 3; l < kLimbs; l++) {
-        if (l > 3) c_lo = __mul24(c_lo, 14);
-#pragma unroll
-        for (int j = 0; j < 4; j++) c_lo = __builtin_amdgcn_sdot8(t[j], L.q[i][l][j], c_lo, false);
-    }
-    const float c = __builtin_fmaf((float)c_hi, 196.0f, (float)c_lo);
+    const float c = (float)ci;
     const float dw = f16_bits_to_f32((w[0] >> dshift) & 0xffffu);
     return dw * (L.d[i] * c);
 }
@@ -202,7 +197,7 @@ constexpr int kRWG = 256;                       // 4 waves
 constexpr int kRStages = 6;                     // ring slots per wave
 constexpr int kRLoads = 3;                      // 3 × 1 KB DMA per slot
 constexpr int kRSlot = kRLoads * kWave * 16;    // 3072 B: row slice <= 170 blocks
-constexpr int kRLds = (kRWG / kWave) * kRStages * kRSlot + 64;  // 72 KB + reduction
+constexpr int kRLds = (kRWG / kWave) * kRStages * kRSlot + 64;  // 72 KB + 2×4 partials
 
 // s_waitcnt immediate for gfx9: wait until at most `n` vector-memory ops are
 // outstanding (vmcnt bits [3:0] and [15:14]); expcnt/lgkmcnt left at "any".
@@ -210,25 +205,67 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
 
-// Reads a block's 20-byte window from a ring slot.  Written as asm so the
-// compiler's waitcnt pass, which cannot tell these reads from slots still
-// being filled by LDS DMA, does not force vmcnt(0) (a full drain of the
-// ring) in front of them; the explicit vmcnt wait already orders them.
-// Outputs are early-clobber: the address register must survive until the
-// last read has issued.
-__device__ __forceinline__ void lds_read_block(const uint8_t *p, uint32_t (&w)[5]) {
-    const uint32_t a = (uint32_t)(uintptr_t)p;
+// Reads the NBL 20-byte block windows of a lane from a ring slot, all
+// issued before one wait.  Written as asm so the compiler's waitcnt pass,
+// which cannot tell these reads from slots still being filled by LDS DMA,
+// does not force vmcnt(0) (a full drain of the ring) in front of them; the
+// explicit vmcnt wait already orders them.  Outputs are early-clobber: the
+// address registers must survive until the last read has issued.
+#define SGQ_RD5(o, a)                                       \
+    "ds_read_b32 %" #o "0, %" #a "\n"                      \
+    "ds_read_b32 %" #o "1, %" #a " offset:4\n"             \
+    "ds_read_b32 %" #o "2, %" #a " offset:8\n"             \
+    "ds_read_b32 %" #o "3, %" #a " offset:12\n"            \
+    "ds_read_b32 %" #o "4, %" #a " offset:16\n"
+template <int NBL>
+__device__ __forceinline__ void lds_read_blocks(const uint8_t *st, const int (&boff)[NBL],
+                                                uint32_t (&w)[NBL][5]);
+template <>
+__device__ __forceinline__ void lds_read_blocks<1>(const uint8_t *st, const int (&boff)[1],
+                                                   uint32_t (&w)[1][5]) {
+    const uint32_t a0 = (uint32_t)(uintptr_t)(st + boff[0]);
     asm volatile(
-        "ds_read_b32 %0, %5\n"
-        "ds_read_b32 %1, %5 offset:4\n"
-        "ds_read_b32 %2, %5 offset:8\n"
-        "ds_read_b32 %3, %5 offset:12\n"
-        "ds_read_b32 %4, %5 offset:16\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4])
-        : "v"(a)
+        "ds_read_b32 %0, %5\n ds_read_b32 %1, %5 offset:4\n ds_read_b32 %2, %5 offset:8\n"
+        "ds_read_b32 %3, %5 offset:12\n ds_read_b32 %4, %5 offset:16\n s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0][0]), "=&v"(w[0][1]), "=&v"(w[0][2]), "=&v"(w[0][3]), "=&v"(w[0][4])
+        : "v"(a0)
         : "memory");
 }
+template <>
+__device__ __forceinline__ void lds_read_blocks<2>(const uint8_t *st, const int (&boff)[2],
+                                                   uint32_t (&w)[2][5]) {
+    const uint32_t a0 = (uint32_t)(uintptr_t)(st + boff[0]);
+    const uint32_t a1 = (uint32_t)(uintptr_t)(st + boff[1]);
+    asm volatile(
+        "ds_read_b32 %0, %10\n ds_read_b32 %1, %10 offset:4\n ds_read_b32 %2, %10 offset:8\n"
+        "ds_read_b32 %3, %10 offset:12\n ds_read_b32 %4, %10 offset:16\n"
+        "ds_read_b32 %5, %11\n ds_read_b32 %6, %11 offset:4\n ds_read_b32 %7, %11 offset:8\n"
+        "ds_read_b32 %8, %11 offset:12\n ds_read_b32 %9, %11 offset:16\n s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0][0]), "=&v"(w[0][1]), "=&v"(w[0][2]), "=&v"(w[0][3]), "=&v"(w[0][4]),
+          "=&v"(w[1][0]), "=&v"(w[1][1]), "=&v"(w[1][2]), "=&v"(w[1][3]), "=&v"(w[1][4])
+        : "v"(a0), "v"(a1)
+        : "memory");
+}
+template <>
+__device__ __forceinline__ void lds_read_blocks<3>(const uint8_t *st, const int (&boff)[3],
+                                                   uint32_t (&w)[3][5]) {
+    const uint32_t a0 = (uint32_t)(uintptr_t)(st + boff[0]);
+    const uint32_t a1 = (uint32_t)(uintptr_t)(st + boff[1]);
+    const uint32_t a2 = (uint32_t)(uintptr_t)(st + boff[2]);
+    asm volatile(
+        "ds_read_b32 %0, %15\n ds_read_b32 %1, %15 offset:4\n ds_read_b32 %2, %15 offset:8\n"
+        "ds_read_b32 %3, %15 offset:12\n ds_read_b32 %4, %15 offset:16\n"
+        "ds_read_b32 %5, %16\n ds_read_b32 %6, %16 offset:4\n ds_read_b32 %7, %16 offset:8\n"
+        "ds_read_b32 %8, %16 offset:12\n ds_read_b32 %9, %16 offset:16\n"
+        "ds_read_b32 %10, %17\n ds_read_b32 %11, %17 offset:4\n ds_read_b32 %12, %17 offset:8\n"
+        "ds_read_b32 %13, %17 offset:12\n ds_read_b32 %14, %17 offset:16\n s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0][0]), "=&v"(w[0][1]), "=&v"(w[0][2]), "=&v"(w[0][3]), "=&v"(w[0][4]),
+          "=&v"(w[1][0]), "=&v"(w[1][1]), "=&v"(w[1][2]), "=&v"(w[1][3]), "=&v"(w[1][4]),
+          "=&v"(w[2][0]), "=&v"(w[2][1]), "=&v"(w[2][2]), "=&v"(w[2][3]), "=&v"(w[2][4])
+        : "v"(a0), "v"(a1), "v"(a2)
+        : "memory");
+}
+#undef SGQ_RD5
 __device__ __forceinline__ void lds_write_f32(uint8_t *p, float v) {
     const uint32_t a = (uint32_t)(uintptr_t)p;
     asm volatile("ds_write_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : : "v"(a), "v"(v) : "memory");
@@ -238,6 +275,25 @@ __device__ __forceinline__ float lds_read_f32(const uint8_t *p) {
     float v;
     asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
     return v;
+}
+
+// Sum over the wave in a fixed order with DPP: row_shr 1/2/4/8 leave each
+// 16-lane row's sum in its lane 15, row_bcast 15/31 carry them up, lane 63
+// ends with the total (deterministic).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf,
+                                              false);
+    return v + __builtin_bit_cast(float, t);
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_add<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_add<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15
+    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Row r of the concatenated targets -> (matrix, local row).
@@ -250,30 +306,31 @@ __device__ __forceinline__ int target_of(const GemvTargets &tg, int row, int *lo
     return j;
 }
 
-// DMA one row slice (<= 3072 B) into a ring slot; past-the-end rows are
-// clamped to row 0 so every call issues exactly kRLoads loads.
+// DMA one row slice (<= 3072 B) into a ring slot.  `row` is wave-uniform
+// (scalar); past-the-end rows are clamped to row 0 so every call issues
+// exactly kRLoads loads.  doff: the lane's precomputed byte offsets within
+// the slice (clamped to 0 past its end).
 __device__ __forceinline__ void issue_slice(const GemvTargets &tg, uint8_t *slot, int row, int n,
-                                            size_t row_bytes, int slice_off, int slice_bytes,
-                                            int lane) {
+                                            size_t row_bytes, int slice_off,
+                                            const int (&doff)[kRLoads]) {
     int local;
     const int j = target_of(tg, row < n ? row : 0, &local);
     const uint8_t *src =
         static_cast<const uint8_t *>(tg.w[j]) + (size_t)local * row_bytes + slice_off;
 #pragma unroll
-    for (int i = 0; i < kRLoads; i++) {
-        int off = (i * kWave + lane) * 16;
-        if (off + 16 > slice_bytes) off = 0;
-        __builtin_amdgcn_global_load_lds((gvoid_t *)(src + off), (lvoid_t *)(slot + i * kWave * 16),
-                                         16, 0, 0);
-    }
+    for (int i = 0; i < kRLoads; i++)
+        __builtin_amdgcn_global_load_lds((gvoid_t *)(src + doff[i]),
+                                         (lvoid_t *)(slot + i * kWave * 16), 16, 0, 0);
 }
 
 // x (fp32, nb blocks of 32) -> limb table, one thread per block.
+// x limbs: 8 lanes per 32-block, one float4 each (limbs_block8).
 __global__ __launch_bounds__(256) void gemv_prep_x_kernel(const float *__restrict__ x,
                                                           BlockLimbs *__restrict__ xl, int nb) {
-    const int b = blockIdx.x * 256 + threadIdx.x;
-    if (b >= nb) return;
-    quantize_to_table(x + (size_t)b * 32, xl[b]);
+    const int i = blockIdx.x * 256 + threadIdx.x;  // float4 index
+    if (i >= nb * 8) return;                         // whole 8-lane groups exit together
+    const float4 v = reinterpret_cast<const float4 *>(x)[i];
+    limbs_block8(v, i & 7, &xl[i >> 3]);
 }
 
 __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float v) {
@@ -284,19 +341,23 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
 }
 
 // Rows of up to kGemvMaxTargets matrices sharing x (e.g. Q/K/V, gate/up) are
-// one concatenated row space: one launch, one x table.
+// one concatenated row space: one launch, one x table.  Everything that
+// depends only on the wave (its K-slice, its rows, the DMA sources) is
+// computed in scalar registers; the VALU does the block dots and the DPP
+// reduction.  Lanes past the slice's last block read a genuine block of the
+// slot (block 0 or 1, so its scale is a finite f16) against zero limbs.
 template <int NBL>
 __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
                                                               const BlockLimbs *__restrict__ xl,
                                                               int n, int nb, int S, int slice) {
     extern __shared__ __align__(16) uint8_t gemv_smem[];
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int s = wave % S;              // K-slice of this wave
     const int rw = wave / S;             // row within the workgroup's row group
     const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
     uint8_t *ring = gemv_smem + wave * (kRStages * kRSlot);
-    uint8_t *red = gemv_smem + (kRWG / kWave) * kRStages * kRSlot;
+    uint8_t *red = gemv_smem + (kRWG / kWave) * kRStages * kRSlot;  // [2][4] floats
     const size_t row_bytes = (size_t)nb * 18;
     const int b0 = s * slice;
     const int slice_blocks = min(slice, nb - b0);
@@ -305,16 +366,21 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const int G = gridDim.x * P;         // rows advanced per iteration by the grid
     const int r0 = blockIdx.x * P + rw;
 
+    int doff[kRLoads];
+#pragma unroll
+    for (int i = 0; i < kRLoads; i++) {
+        const int off = (i * kWave + lane) * 16;
+        doff[i] = off + 16 > slice_bytes ? 0 : off;
+    }
     // limbs for this lane's blocks, straight from the (L2-resident) table
     XLimbs<NBL> L;
     int boff[NBL];
-    bool valid[NBL];
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int lb = lane + kWave * i;
-        valid[i] = lb < slice_blocks;
-        boff[i] = valid[i] ? lb * 18 - (lane & 1) * 2 : 0;
-        BlockLimbs t = valid[i] ? xl[b0 + lb] : BlockLimbs{};
+        const bool valid = lb < slice_blocks;
+        boff[i] = valid ? lb * 18 - (lane & 1) * 2 : (lane & 1) * 16;
+        BlockLimbs t = valid ? xl[b0 + lb] : BlockLimbs{};
 #pragma unroll
         for (int l = 0; l < kLimbs; l++)
 #pragma unroll
@@ -327,7 +393,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 #pragma unroll
     for (int j = 0; j < kRStages - 1; j++)
-        issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, slice_bytes, lane);
+        issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
 
     // lb even: qs = bytes 2..17 of the window, d = low half of word 0;
     // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
@@ -337,29 +403,28 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     for (int it = 0; it < rows_rounds; it++) {
         const int row = r0 + it * G;
         issue_slice(tg, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
-                    row + (kRStages - 1) * G, n, row_bytes, slice_off, slice_bytes, lane);
+                    row + (kRStages - 1) * G, n, row_bytes, slice_off, doff);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * (kRStages - 1)));
-        const uint8_t *st = ring + (it % kRStages) * kRSlot;
+        uint32_t wv[NBL][5];
+        lds_read_blocks<NBL>(ring + (it % kRStages) * kRSlot, boff, wv);
         float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            if (!valid[i]) continue;
-            uint32_t wv[5];
-            lds_read_block(st + boff[i], wv);
-            a += block_dot(wv, sel, dshift, L, i);
-        }
-        a = wave_sum(a);
+        for (int i = 0; i < NBL; i++) a += block_dot(wv[i], sel, dshift, L, i);
+        a = wave_sum_dpp(a);
         if (S == 1) {
             if (lane == 0 && row < n) store_row(tg, row, a);
         } else {
-            if (lane == 0) lds_write_f32(red + wave * 4, a);
+            // one barrier per row: partials alternate between two slots, and
+            // a slot is rewritten only after the next row's barrier, which
+            // the reading wave reaches after its reads
+            uint8_t *rb = red + (it & 1) * 16;
+            if (lane == 0) lds_write_f32(rb + wave * 4, a);
             __builtin_amdgcn_s_barrier();
             if (s == 0 && lane == 0 && row < n) {
                 float v = 0.f;
-                for (int q = 0; q < S; q++) v += lds_read_f32(red + (rw * S + q) * 4);
+                for (int q = 0; q < S; q++) v += lds_read_f32(rb + (rw * S + q) * 4);
                 store_row(tg, row, v);
             }
-            __builtin_amdgcn_s_barrier();
         }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain the clamped tail loads
@@ -446,7 +511,7 @@ int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k) {
     SGQ_CHECK(k % 32 == 0 && k > 0, "quant_limbs: k=%u must be a multiple of 32", k);
     SGQ_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)xl & 15) == 0, "quant_limbs: misaligned");
     const int nb = (int)(k / 32);
-    hipLaunchKernelGGL(gemv_prep_x_kernel, dim3((nb + 255) / 256), dim3(256), 0, st, x,
+    hipLaunchKernelGGL(gemv_prep_x_kernel, dim3((nb * 8 + 255) / 256), dim3(256), 0, st, x,
                        static_cast<BlockLimbs *>(xl), nb);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;

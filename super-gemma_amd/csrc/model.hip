@@ -51,42 +51,26 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.f + tanhf(k * (x + 0.044715f * x * x * x)));
 }
 
-// Sum over the workgroup in a fixed tree order (deterministic).
-template <int WG>
+// Sum over the workgroup in a fixed tree order (deterministic).  `red` holds
+// one float per wave; the caller separates reuses with a barrier.
 __device__ __forceinline__ float wg_sum(float v, float *red) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
     if (lane == 0) red[wave] = v;
     __syncthreads();
     float r = 0.f;
-    for (int w = 0; w < WG / kWave; w++) r += red[w];
+    for (int w = 0; w < kRowWG / kWave; w++) r += red[w];
     return r;
 }
 
-// buf[0..n) <- buf * rsqrt(mean(buf²) + eps) * w  (w == nullptr: weightless)
-__device__ __forceinline__ void rmsnorm_lds(float *buf, int n, const float *__restrict__ w,
-                                            float eps, float *red) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kRowWG) ss += buf[i] * buf[i];
-    ss = wg_sum<kRowWG>(ss, red);
-    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += kRowWG) buf[i] = buf[i] * inv * (w ? w[i] : 1.f);
-    __syncthreads();
+__device__ __forceinline__ float sumsq4(float4 a) {
+    return a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
 }
 
-// limbs of buf[0..n) (n % 32 == 0), one thread per 32-block
-__device__ __forceinline__ void limbs_lds(const float *buf, int n, BlockLimbs *__restrict__ xl) {
-    for (int b = threadIdx.x; b < n / 32; b += kRowWG) {
-        float v[32];
-#pragma unroll
-        for (int j = 0; j < 32; j++) v[j] = buf[b * 32 + j];
-        BlockLimbs t;
-        limbs_from_values(v, t);
-        xl[b] = t;
-    }
-}
+// Row kernels: one workgroup of kRowWG threads, thread t owns the float4s
+// t, t + kRowWG, ... (at most kRowV of them) in registers; the limb table of
+// the result is written by 8-lane groups (float4 index i -> block i/8).
+constexpr int kRowV = 4;  // hidden <= 4 * 4 * kRowWG = 16384
 
 // x = dequant(E[token])·scale; xl = limbs(rmsnorm(x, w))
 __global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__restrict__ E,
@@ -95,58 +79,105 @@ __global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__res
                                                              const float *__restrict__ w, float eps,
                                                              float *__restrict__ x,
                                                              BlockLimbs *__restrict__ xl) {
-    extern __shared__ float row[];
     __shared__ float red[kRowWG / kWave];
-    const uint32_t token = step[4];
-    const uint8_t *er = E + (size_t)token * (hidden / 32) * 18;
-    for (int i = threadIdx.x; i < hidden; i += kRowWG) {
-        const uint8_t *blk = er + (i / 32) * 18;
-        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
-        const int j = i % 32;
-        const int q = j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4);
-        const float v = d * (float)(q - 8) * scale;
-        x[i] = v;
-        row[i] = v;
+    const int n4 = hidden / 4, t = threadIdx.x;
+    const uint8_t *er = E + (size_t)step[4] * (hidden / 32) * 18;
+    float4 v[kRowV];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            const uint8_t *blk = er + (i >> 3) * 18;
+            const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+            const int j0 = 4 * (i & 7);
+            const int sh = j0 < 16 ? 0 : 4;
+            const uint8_t *qs = blk + 2 + (j0 & 15);
+            float e[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) e[u] = d * (float)(((qs[u] >> sh) & 15) - 8) * scale;
+            v[k] = make_float4(e[0], e[1], e[2], e[3]);
+            reinterpret_cast<float4 *>(x)[i] = v[k];
+            ss += sumsq4(v[k]);
+        }
     }
-    __syncthreads();
-    rmsnorm_lds(row, hidden, w, eps, red);
-    limbs_lds(row, hidden, xl);
+    ss = wg_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            const float4 wv = reinterpret_cast<const float4 *>(w)[i];
+            const float4 y = make_float4(v[k].x * inv * wv.x, v[k].y * inv * wv.y,
+                                         v[k].z * inv * wv.z, v[k].w * inv * wv.w);
+            limbs_block8(y, i & 7, &xl[i >> 3]);
+        }
+    }
 }
 
-// x += rmsnorm(o, w_post); xl = limbs(rmsnorm(x, w_next))   (post-attention)
-// x = (x + rmsnorm(o, w_post))·scale; xl = limbs(rmsnorm(x, w_next)) (post-FFN)
+// post-attention: x += rmsnorm(o, w_post);            xl = limbs(rmsnorm(x, w_next))
+// post-FFN:       x = (x + rmsnorm(o, w_post))·scale;  xl = limbs(rmsnorm(x, w_next))
 __global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
     const float *__restrict__ o, const float *__restrict__ w_post, float *__restrict__ x,
     const float *__restrict__ scale_ptr, const float *__restrict__ w_next, int hidden, float eps,
     BlockLimbs *__restrict__ xl) {
-    extern __shared__ float row[];
-    __shared__ float red[kRowWG / kWave];
-    for (int i = threadIdx.x; i < hidden; i += kRowWG) row[i] = o[i];
-    __syncthreads();
-    rmsnorm_lds(row, hidden, w_post, eps, red);
-    const float s = scale_ptr ? *scale_ptr : 1.f;
-    for (int i = threadIdx.x; i < hidden; i += kRowWG) {
-        const float v = (x[i] + row[i]) * s;
-        x[i] = v;
-        row[i] = v;
+    __shared__ float red[2][kRowWG / kWave];
+    const int n4 = hidden / 4, t = threadIdx.x;
+    float4 ov[kRowV], xv[kRowV];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            ov[k] = reinterpret_cast<const float4 *>(o)[i];
+            xv[k] = reinterpret_cast<const float4 *>(x)[i];
+            ss += sumsq4(ov[k]);
+        }
     }
-    __syncthreads();
-    rmsnorm_lds(row, hidden, w_next, eps, red);
-    limbs_lds(row, hidden, xl);
+    const float s = scale_ptr ? *scale_ptr : 1.f;
+    ss = wg_sum(ss, red[0]);
+    const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+    float ss2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            const float4 wp = reinterpret_cast<const float4 *>(w_post)[i];
+            float4 r;
+            r.x = (xv[k].x + ov[k].x * inv * wp.x) * s;
+            r.y = (xv[k].y + ov[k].y * inv * wp.y) * s;
+            r.z = (xv[k].z + ov[k].z * inv * wp.z) * s;
+            r.w = (xv[k].w + ov[k].w * inv * wp.w) * s;
+            xv[k] = r;
+            reinterpret_cast<float4 *>(x)[i] = r;
+            ss2 += sumsq4(r);
+        }
+    }
+    ss2 = wg_sum(ss2, red[1]);
+    const float inv2 = 1.0f / sqrtf(ss2 / (float)hidden + eps);
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            const float4 wv = reinterpret_cast<const float4 *>(w_next)[i];
+            const float4 y = make_float4(xv[k].x * inv2 * wv.x, xv[k].y * inv2 * wv.y,
+                                         xv[k].z * inv2 * wv.z, xv[k].w * inv2 * wv.w);
+            limbs_block8(y, i & 7, &xl[i >> 3]);
+        }
+    }
 }
 
-// h = gelu_tanh(g)·u, then its limb table; one thread per 32-block.
+// h = gelu_tanh(g)·u, then its limb table; one float4 per thread.
 __global__ __launch_bounds__(256) void geglu_limbs_kernel(const float *__restrict__ g,
                                                           const float *__restrict__ u, int n,
                                                           BlockLimbs *__restrict__ xl) {
-    const int b = blockIdx.x * 256 + threadIdx.x;
-    if (b >= n / 32) return;
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 32; j++) v[j] = gelu_tanh(g[b * 32 + j]) * u[b * 32 + j];
-    BlockLimbs t;
-    limbs_from_values(v, t);
-    xl[b] = t;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n / 4) return;  // n % 32 == 0: whole 8-lane groups exit together
+    const float4 gv = reinterpret_cast<const float4 *>(g)[i];
+    const float4 uv = reinterpret_cast<const float4 *>(u)[i];
+    const float4 h = make_float4(gelu_tanh(gv.x) * uv.x, gelu_tanh(gv.y) * uv.y,
+                                 gelu_tanh(gv.z) * uv.z, gelu_tanh(gv.w) * uv.w);
+    limbs_block8(h, i & 7, &xl[i >> 3]);
 }
 
 // Per-head post-projection: q heads -> rmsnorm(q_norm) + RoPE -> q_out;
@@ -285,9 +316,8 @@ int record_step(sgq_model *m, float *logits) {
     const int H = (int)c.hidden, F = (int)c.ffn, QD = (int)(c.n_q_heads * kHeadDim),
               KD = (int)(c.n_kv_heads * kHeadDim);
     BlockLimbs *xl = static_cast<BlockLimbs *>(m->xl);
-    const size_t row_lds = (size_t)H * 4;
     int rc;
-    hipLaunchKernelGGL(embed_norm_kernel, dim3(1), dim3(kRowWG), row_lds, st,
+    hipLaunchKernelGGL(embed_norm_kernel, dim3(1), dim3(kRowWG), 0, st,
                        static_cast<const uint8_t *>(m->embd), m->step, H, sqrtf((float)H),
                        m->layers[0].attn_norm, c.eps, m->x, xl);
     SGQ_HIP(hipGetLastError());
@@ -308,24 +338,24 @@ int record_step(sgq_model *m, float *logits) {
                            L.global ? 0 : (int)c.sliding_window, c.eps, m->q, L.kq, L.ks, L.vq,
                            L.vs);
         SGQ_HIP(hipGetLastError());
-        const int n_splits = L.global ? 32 : 16;
+        // about 256 slots per workgroup at a full cache
+        const int n_splits = L.global ? (int)std::min(64u, std::max(8u, L.slots / 256)) : 8;
         if ((rc = launch_attn_decode_q8(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step, L.global ? 2 : 1,
                                         0, (int)c.n_q_heads, (int)c.n_kv_heads, kHeadDim, n_splits,
                                         c.attn_scale, m->attn, ctx_workspace(m->ctx),
-                                        kWorkspaceBytes)))
+                                        kWorkspaceBytes, xl)))
             return rc;
-        if ((rc = launch_quant_limbs(st, m->attn, xl, QD))) return rc;
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
         if ((rc = launch_gemv_limbs(st, ot, xl, QD))) return rc;
-        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), row_lds, st, m->o,
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->o,
                            L.post_attn_norm, m->x, (const float *)nullptr, L.ffn_norm, H, c.eps, xl);
         SGQ_HIP(hipGetLastError());
         GemvTargets gu{};
         gu.w[0] = L.wg, gu.w[1] = L.wu, gu.y[0] = m->g, gu.y[1] = m->u;
         gu.end[0] = F, gu.end[1] = 2 * F, gu.count = 2;
         if ((rc = launch_gemv_limbs(st, gu, xl, H))) return rc;
-        hipLaunchKernelGGL(geglu_limbs_kernel, dim3((F / 32 + 255) / 256), dim3(256), 0, st, m->g,
+        hipLaunchKernelGGL(geglu_limbs_kernel, dim3((F / 4 + 255) / 256), dim3(256), 0, st, m->g,
                            m->u, F, xl);
         SGQ_HIP(hipGetLastError());
         GemvTargets dt{};
@@ -333,7 +363,7 @@ int record_step(sgq_model *m, float *logits) {
         if ((rc = launch_gemv_limbs(st, dt, xl, F))) return rc;
         const float *w_next =
             li + 1 < m->layers.size() ? m->layers[li + 1].attn_norm : m->out_norm;
-        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), row_lds, st, m->f,
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->f,
                            L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
         SGQ_HIP(hipGetLastError());
     }
@@ -379,7 +409,7 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
     SGQ_CHECK(c.n_kv_heads > 0 && c.n_q_heads % c.n_kv_heads == 0 &&
                   c.n_q_heads / c.n_kv_heads <= 2,
               "model: 1 or 2 q heads per kv head");
-    SGQ_CHECK(c.hidden <= 32768, "model: hidden too large for a row kernel");
+    SGQ_CHECK(c.hidden <= 16384, "model: hidden above 16384 (row kernels)");
     SGQ_CHECK(c.ffn <= 65536 && c.n_q_heads * kHeadDim <= 65536, "model: GEMV K above 65536");
     SGQ_CHECK(c.n_layers >= 1 && c.vocab >= 1 && c.max_ctx >= 1 && c.sliding_window >= 1,
               "model: empty dimension");

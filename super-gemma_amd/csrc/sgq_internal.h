@@ -79,7 +79,7 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
                           const int8_t *vq, const uint16_t *vs, const uint32_t *step,
                           int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
                           int n_splits, float scale, float *out, void *workspace,
-                          size_t workspace_bytes);
+                          size_t workspace_bytes, void *limbs_out = nullptr);
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);

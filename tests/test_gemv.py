@@ -3,9 +3,11 @@
 Template: crates/sg-gpu/tests/parity_gemv.rs (seeded xorshift64* inputs,
 random_q4_0 weights, f64 reference over sampled rows, bit-determinism).
 Tolerance: fp32 output within 1e-3 relative (BASELINE) — asserted as
-|err| <= 1e-3*|want| + 1e-4*rms(want) per element, and the normwise error
-max|err|/max|want| <= 5e-6 (x enters the kernel as five 4-bit limbs,
-per-element error <= 1.9e-6 of the block's max |x|).
+|err| <= 1e-3*|want| + 3e-4*rms(want) per element, and the normwise error
+max|err|/max|want| <= 1e-4.  x enters the kernel as four 4-bit limbs
+(per-element error <= 2.6e-5 of its block's max |x|), so an output's error
+is ~3e-5*rms(want) (1 sigma): four times below what the reference's own f16
+activation buffers cost its GEMV (2^-12 relative rounding per element).
 """
 import struct
 
@@ -43,8 +45,8 @@ def _check(oracle, w, x, y, n, k):
     want = oracle.gemv_rows(w, x, k, rows)
     got = y[rows]
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
-    assert_close(got, want, 1e-3, 1e-4 * rms, f"gemv k={k} n={n}")
-    assert rel_err(got, want) <= 5e-6, rel_err(got, want)
+    assert_close(got, want, 1e-3, 3e-4 * rms, f"gemv k={k} n={n}")
+    assert rel_err(got, want) <= 1e-4, rel_err(got, want)
 
 
 @pytest.mark.parametrize("k,n", SHAPES)
@@ -70,7 +72,7 @@ def test_gemv_ragged_shapes(ctx, oracle, k, n):
     got = host(ty)
     want = oracle.gemv_rows(w, x, k, np.arange(n))
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
-    assert_close(got, want, 1e-3, 1e-4 * rms, f"gemv k={k} n={n}")
+    assert_close(got, want, 1e-3, 3e-4 * rms, f"gemv k={k} n={n}")
 
 
 def test_gemv_baseline_distribution_full_rows(ctx, oracle):
@@ -91,8 +93,8 @@ def test_gemv_baseline_distribution_full_rows(ctx, oracle):
     assert abs(float(x.mean())) < 0.05 and 0.9 < float(x.std()) < 1.1
     want = oracle.gemv_rows(w, x, k, np.arange(n))
     rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
-    assert_close(y, want, 1e-3, 1e-4 * rms, "gemv config 1")
-    assert rel_err(y, want) <= 5e-6
+    assert_close(y, want, 1e-3, 3e-4 * rms, "gemv config 1")
+    assert rel_err(y, want) <= 1e-4
 
 
 def test_gemv_is_bit_deterministic(ctx, oracle):
