@@ -17,12 +17,14 @@
 //    broadcast), the sub-chunk's scores go through an online softmax
 //    (m, l, rescaled acc), and PV runs with thread (head, 4-dim word, slot
 //    group) so that a wave reads whole V rows.
-//  * Splits are merged without a second launch: each workgroup writes its
-//    (acc, m, l) partial, and the last workgroup of a kv head to finish
-//    (device-scope atomic on a per-head counter, which it resets) merges
-//    the partials in split order 0..S-1 — the same fixed order as
-//    attn_reduce.wgsl:40-52, so results do not depend on which workgroup
-//    merged.  Empty splits carry (m = -3e38, l = 0, acc = 0).
+//  * Each workgroup writes its (acc, m, l) partial; a small merge kernel
+//    (one workgroup per kv head) combines them in split order 0..S-1, the
+//    fixed order of attn_reduce.wgsl:40-52.  A second launch is cheaper
+//    than merging in the same launch: that needs a device-scope release
+//    fence per workgroup, which on a multi-XCD part writes back L2.
+//    Empty splits carry (m = -3e38, l = 0, acc = 0).
+//  * K row, V row and both scale words of a slot are issued together, so a
+//    sub-chunk costs one memory round trip; V is staged in LDS for PV.
 #include "limbs.h"
 
 namespace sgq {
@@ -63,8 +65,7 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
     const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
     const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
     const uint32_t *__restrict__ step, int step_word, uint32_t kv_len_direct, int n_kv,
-    int n_splits, float scale, float *__restrict__ part, unsigned *__restrict__ counters,
-    float *__restrict__ out, BlockLimbs *__restrict__ limbs_out) {
+    int n_splits, float scale, float *__restrict__ part) {
     constexpr int G = kAWG / (QPK * (kHD / 4));  // slot groups in the PV phase
     static_assert(G >= 1, "QPK too large for one workgroup");
     constexpr int kVRow = kHD / 4 + 4;           // V row in LDS, ints (padded)
@@ -74,8 +75,6 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
     __shared__ __align__(16) int v_s[kSub][kVRow];  // V quants of the sub-chunk
     __shared__ float red[QPK][kAWG / kWave];
     __shared__ float acc_s[G][QPK][kHD];
-    __shared__ float wgt_s[2][QPK][64];          // merge: split weights, batch of 64
-    __shared__ int last_s;
 
     const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -198,81 +197,73 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
     }
     if (tid < QPK) {
         const size_t rowp = ((size_t)(kvh * QPK + tid) * n_splits + split) * stride;
-        part[rowp + kHD] = m_run[tid];
-        part[rowp + kHD + 1] = l_run[tid];
+        float mv = m_run[0], lv = l_run[0];
+#pragma unroll
+        for (int h = 1; h < QPK; h++)
+            if (tid == h) mv = m_run[h], lv = l_run[h];
+        part[rowp + kHD] = mv;
+        part[rowp + kHD + 1] = lv;
     }
 
-    // ---- last workgroup of this kv head merges all splits
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&counters[kvh], 1u);
-        last_s = prev == (unsigned)(n_splits - 1);
-        if (last_s) counters[kvh] = 0u;  // self-reset for the next launch
-    }
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
-    // out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s, sums in
-    // split order 0..S-1 (fixed, so the result does not depend on which
-    // workgroup merges).  Wave h computes M for head h.
-    float M[QPK];
-    if (wave < QPK) {
-        const float *ph_part = part + (size_t)(kvh * QPK + wave) * n_splits * stride;
-        float v = kNegBig;
-        for (int s2 = lane; s2 < n_splits; s2 += kWave)
-            v = fmaxf(v, __builtin_nontemporal_load(ph_part + (size_t)s2 * stride + kHD));
-        for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-        if (lane == 0) red[wave][0] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < QPK; h++) M[h] = red[h][0];
-    const int h = tid / kHD % QPK, d = tid % kHD;
-    const bool active = tid < QPK * kHD;
+}
+
+// Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
+// out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s, both sums in
+// split order 0..S-1.  One workgroup per kv head, thread (h, d); the
+// kernel boundary after the split kernel makes the partials visible (no
+// device-scope fences or atomics).  Optionally writes the x limbs of the
+// output rows for the next GEMV (8 lanes per 32-block).
+template <int QPK>
+__global__ __launch_bounds__(QPK * kHD) void attn_merge_kernel(const float *__restrict__ part,
+                                                               int n_splits,
+                                                               float *__restrict__ out,
+                                                               BlockLimbs *__restrict__ limbs_out) {
+    __shared__ __align__(16) float o_s[QPK * kHD];
+    const int kvh = blockIdx.x, tid = threadIdx.x;
+    const int h = tid / kHD, d = tid % kHD;
+    const int stride = kHD + 2;
     const float *ph_part = part + (size_t)(kvh * QPK + h) * n_splits * stride;
+    float M = kNegBig;
+    int s0 = 0;
+    for (; s0 + 8 <= n_splits; s0 += 8) {
+        float mv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) mv[u] = ph_part[(size_t)(s0 + u) * stride + kHD];
+#pragma unroll
+        for (int u = 0; u < 8; u++) M = fmaxf(M, mv[u]);
+    }
+    for (; s0 < n_splits; s0++) M = fmaxf(M, ph_part[(size_t)s0 * stride + kHD]);
     float a = 0.f, l = 0.f;
-    for (int s0 = 0; s0 < n_splits; s0 += 64) {
-        const int nb = min(64, n_splits - s0);
-        // weights e^(m_s - M) and l_s for this batch, one lane per split
-        if (wave < QPK && lane < nb) {
-            const float *r = part + ((size_t)(kvh * QPK + wave) * n_splits + s0 + lane) * stride;
-            wgt_s[0][wave][lane] = __expf(__builtin_nontemporal_load(r + kHD) - M[wave]);
-            wgt_s[1][wave][lane] = __builtin_nontemporal_load(r + kHD + 1);
-        }
-        __syncthreads();
-        if (active) {
-            int j = 0;
-            for (; j + 8 <= nb; j += 8) {
-                float as[8];
+    s0 = 0;
+    for (; s0 + 8 <= n_splits; s0 += 8) {
+        float mv[8], lv[8], av[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++)
-                    as[u] = __builtin_nontemporal_load(ph_part + (size_t)(s0 + j + u) * stride + d);
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    a = __builtin_fmaf(as[u], wgt_s[0][h][j + u], a);
-                    l = __builtin_fmaf(wgt_s[1][h][j + u], wgt_s[0][h][j + u], l);
-                }
-            }
-            for (; j < nb; j++) {
-                const float as = __builtin_nontemporal_load(ph_part + (size_t)(s0 + j) * stride + d);
-                a = __builtin_fmaf(as, wgt_s[0][h][j], a);
-                l = __builtin_fmaf(wgt_s[1][h][j], wgt_s[0][h][j], l);
-            }
+        for (int u = 0; u < 8; u++) {
+            const float *r = ph_part + (size_t)(s0 + u) * stride;
+            mv[u] = r[kHD];
+            lv[u] = r[kHD + 1];
+            av[u] = r[d];
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float w = __expf(mv[u] - M);
+            a = __builtin_fmaf(av[u], w, a);
+            l = __builtin_fmaf(lv[u], w, l);
+        }
     }
-    if (active) {
-        const float r = a / l;
-        out[(size_t)(kvh * QPK + h) * kHD + d] = r;
-        acc_s[0][h][d] = r;
+    for (; s0 < n_splits; s0++) {
+        const float *r = ph_part + (size_t)s0 * stride;
+        const float w = __expf(r[kHD] - M);
+        a = __builtin_fmaf(r[d], w, a);
+        l = __builtin_fmaf(r[kHD + 1], w, l);
     }
+    const float res = a / l;
+    out[(size_t)(kvh * QPK + h) * kHD + d] = res;
     if (limbs_out == nullptr) return;
-    // x limbs of this kv head's QPK output rows for the next GEMV (8 lanes
-    // per 32-block; the rows are contiguous in the output vector)
+    o_s[tid] = res;
     __syncthreads();
     if (tid < QPK * kHD / 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(&acc_s[0][0][4 * tid]);
+        const float4 v = *reinterpret_cast<const float4 *>(&o_s[4 * tid]);
         limbs_block8(v, tid & 7, &limbs_out[(kvh * QPK * kHD) / 32 + (tid >> 3)]);
     }
 }
@@ -296,18 +287,16 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     SGQ_CHECK(kAttnPartOff + part_bytes <= workspace_bytes,
               "attn_decode_q8: workspace too small (%zu < %zu)", workspace_bytes,
               kAttnPartOff + part_bytes);
-    // Counters sit at a fixed offset, zeroed when the workspace is created
-    // and reset by the merging workgroup; partials follow.
-    unsigned *counters =
-        reinterpret_cast<unsigned *>(static_cast<uint8_t *>(workspace) + kAttnCounterOff);
     float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + kAttnPartOff);
     const int qpk = n_q / n_kv;
     dim3 grid(n_kv, n_splits);
 #define SGQ_ATTN(Q)                                                                               \
     case Q:                                                                                       \
         hipLaunchKernelGGL(attn_decode_q8_kernel<Q>, grid, dim3(kAWG), 0, st, q, kq, ks, vq, vs,  \
-                           step, step_word, kv_len, n_kv, n_splits, scale, part, counters, out,    \
-                           static_cast<BlockLimbs *>(limbs_out));                                 \
+                           step, step_word, kv_len, n_kv, n_splits, scale, part);                 \
+        SGQ_HIP(hipGetLastError());                                                               \
+        hipLaunchKernelGGL(attn_merge_kernel<Q>, dim3(n_kv), dim3(Q * kHD), 0, st, part,          \
+                           n_splits, out, static_cast<BlockLimbs *>(limbs_out));                  \
         break;
     switch (qpk) {
         SGQ_ATTN(1)

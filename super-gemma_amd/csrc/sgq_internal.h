@@ -42,7 +42,6 @@ void *ctx_workspace(const sgq_ctx *ctx);
 constexpr size_t kGemvWorkspace = 2048 * 96;
 // Context workspace layout (device memory, per context):
 //   [0, kGemvWorkspace)                GEMV x limb table
-//   [kAttnCounterOff, +4 KB)           attention split counters (zero at rest)
 //   [kAttnPartOff, kWorkspaceBytes)    attention split partials
 constexpr int kAttnMaxKv = 1024;
 constexpr size_t kAttnCounterOff = 256 * 1024;

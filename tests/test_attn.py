@@ -100,9 +100,9 @@ def test_attn_decode_uniform_keys_kat(ctx, oracle):
     assert np.allclose(got, want, rtol=1e-5)
 
 
-def test_attn_decode_bit_deterministic_and_counter_reset(ctx, oracle):
-    """Same split count twice -> identical bits (parity_attn.rs:1102-1206); the
-    second launch also proves the merge counters reset themselves."""
+def test_attn_decode_bit_deterministic(ctx, oracle):
+    """Same split count twice -> identical bits (parity_attn.rs:1102-1206);
+    another split count agrees to rounding."""
     n_q, n_kv, kv_len = 32, 16, 2000
     rng = oracle.Rng(0xA7C)
     kq, ks, vq, vs, kd, vd = _cache(oracle, rng, kv_len, n_kv)
