@@ -372,6 +372,15 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         const int off = (i * kWave + lane) * 16;
         doff[i] = off + 16 > slice_bytes ? 0 : off;
     }
+    // Ring prologue first, then the limbs: the compiler cannot order LDS DMA
+    // against ordinary loads and waits for everything (vmcnt(0)) before the
+    // first limb is used, so issuing the DMA first makes that one wait cover
+    // both round trips at once.  The empty asm keeps the limb loads after
+    // the DMA.
+#pragma unroll
+    for (int j = 0; j < kRStages - 1; j++)
+        issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
+    asm volatile("" ::: "memory");
     // limbs for this lane's blocks, straight from the (L2-resident) table
     XLimbs<NBL> L;
     int boff[NBL];
@@ -387,13 +396,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             for (int w = 0; w < 4; w++) L.q[i][l][w] = t.q[l][w];
         L.d[i] = t.d;
     }
-    // Land the limbs before the ring starts: the compiler does not count LDS
-    // DMA in order with ordinary loads and would otherwise drain the whole
-    // prologue (vmcnt(0)) at the first use of a limb register.
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-#pragma unroll
-    for (int j = 0; j < kRStages - 1; j++)
-        issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
 
     // lb even: qs = bytes 2..17 of the window, d = low half of word 0;
     // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
@@ -413,6 +416,8 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         a = wave_sum_dpp(a);
         if (S == 1) {
             if (lane == 0 && row < n) store_row(tg, row, a);
+        } else if (tg.split_out) {
+            if (lane == 0 && row < n) tg.y[0][(size_t)s * n + row] = a;
         } else {
             // one barrier per row: partials alternate between two slots, and
             // a slot is rewritten only after the next row's barrier, which
@@ -517,6 +522,12 @@ int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k) {
     return SGQ_OK;
 }
 
+int gemv_slices(uint32_t k) {
+    int S, slice;
+    if (k % 256 != 0 || k == 0 || k > 65536 || !ring_geometry((int)(k / 32), &S, &slice)) return 0;
+    return S;
+}
+
 int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k) {
     SGQ_CHECK(tg.count >= 1 && tg.count <= kGemvMaxTargets, "gemv: %d targets", tg.count);
     SGQ_CHECK(k % 256 == 0 && k > 0 && k <= 65536, "gemv (limbs): k=%u must be a multiple of 256", k);
@@ -527,6 +538,8 @@ int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     int S, slice;
     const int nb = (int)(k / 32);
     SGQ_CHECK(ring_geometry(nb, &S, &slice), "gemv (limbs): k=%u outside the streamed geometry", k);
+    SGQ_CHECK(!tg.split_out || (tg.count == 1 && tg.softcap == 0.f),
+              "gemv (limbs): split output needs one target and no softcap");
     return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1], nb,
                            S, slice);
 }

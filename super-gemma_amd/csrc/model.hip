@@ -117,10 +117,11 @@ __global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__res
 
 // post-attention: x += rmsnorm(o, w_post);            xl = limbs(rmsnorm(x, w_next))
 // post-FFN:       x = (x + rmsnorm(o, w_post))·scale;  xl = limbs(rmsnorm(x, w_next))
+// o arrives as n_parts K-slice partials (o = Σ_s o[s·hidden + i], s in order).
 __global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
-    const float *__restrict__ o, const float *__restrict__ w_post, float *__restrict__ x,
-    const float *__restrict__ scale_ptr, const float *__restrict__ w_next, int hidden, float eps,
-    BlockLimbs *__restrict__ xl) {
+    const float *__restrict__ o, int n_parts, const float *__restrict__ w_post,
+    float *__restrict__ x, const float *__restrict__ scale_ptr,
+    const float *__restrict__ w_next, int hidden, float eps, BlockLimbs *__restrict__ xl) {
     __shared__ float red[2][kRowWG / kWave];
     const int n4 = hidden / 4, t = threadIdx.x;
     float4 ov[kRowV], xv[kRowV];
@@ -129,7 +130,12 @@ __global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
     for (int k = 0; k < kRowV; k++) {
         const int i = t + k * kRowWG;
         if (i < n4) {
-            ov[k] = reinterpret_cast<const float4 *>(o)[i];
+            float4 a = reinterpret_cast<const float4 *>(o)[i];
+            for (int p = 1; p < n_parts; p++) {
+                const float4 b = reinterpret_cast<const float4 *>(o + (size_t)p * hidden)[i];
+                a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+            }
+            ov[k] = a;
             xv[k] = reinterpret_cast<const float4 *>(x)[i];
             ss += sumsq4(ov[k]);
         }
@@ -348,7 +354,7 @@ int record_step(sgq_model *m, float *logits) {
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
         if ((rc = launch_gemv_limbs(st, ot, xl, QD))) return rc;
-        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->o,
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->o, 1,
                            L.post_attn_norm, m->x, (const float *)nullptr, L.ffn_norm, H, c.eps, xl);
         SGQ_HIP(hipGetLastError());
         GemvTargets gu{};
@@ -360,10 +366,12 @@ int record_step(sgq_model *m, float *logits) {
         SGQ_HIP(hipGetLastError());
         GemvTargets dt{};
         dt.w[0] = L.wd, dt.y[0] = m->f, dt.end[0] = H, dt.count = 1;
+        dt.split_out = gemv_slices(F) > 1;
+        const int f_parts = dt.split_out ? gemv_slices(F) : 1;
         if ((rc = launch_gemv_limbs(st, dt, xl, F))) return rc;
         const float *w_next =
             li + 1 < m->layers.size() ? m->layers[li + 1].attn_norm : m->out_norm;
-        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->f,
+        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->f, f_parts,
                            L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
         SGQ_HIP(hipGetLastError());
     }
@@ -457,7 +465,7 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
             return fail_out(rc);
     }
     float **acts[] = {&m->x, &m->q_raw, &m->k_raw, &m->v_raw, &m->q, &m->attn, &m->o, &m->g, &m->u, &m->f};
-    const size_t act_n[] = {H, QD, KD, KD, QD, QD, H, F, F, H};
+    const size_t act_n[] = {H, QD, KD, KD, QD, QD, H, F, F, 4 * H};  // f: up to 4 K-slices
     for (int i = 0; i < 10; i++)
         if ((rc = alloc(m, act_n[i] * 4, reinterpret_cast<void **>(acts[i])))) return fail_out(rc);
     if ((rc = alloc(m, std::max(H, F) / 32 * sizeof(BlockLimbs), &m->xl))) return fail_out(rc);

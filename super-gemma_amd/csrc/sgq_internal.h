@@ -59,7 +59,14 @@ struct GemvTargets {
     int end[kGemvMaxTargets];
     int count;
     float softcap;
+    // split_out != 0 (single target, K above one slice): each K-slice s
+    // writes its partial row sums to y[0] + s*n instead of meeting at a
+    // workgroup barrier; the consumer adds the slices in order s = 0..S-1.
+    int split_out;
 };
+// Number of K-slices the streamed GEMV uses for K (1, 2 or 4); 0 if K is
+// outside the streamed geometry.
+int gemv_slices(uint32_t k);
 // Sets the streamed kernels' launch attributes (call before graph capture).
 int gemv_prepare();
 int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k);
