@@ -54,6 +54,21 @@ class OracleDecoder:
         live = int(round(cfg["global_rope_frac"] * hd / 2))
         self.global_factors = np.array([1.0] * live + [1e30] * (hd // 2 - live), np.float32)
 
+    def preload_cache(self, pages: dict, n_tokens: int):
+        """Start from a filled context: ``pages[(layer, "k"|"v")]`` = (scales,
+        quants) of the device cache pages.  Global layers hold position p at
+        slot p; ring layers at slot p % slots (positions older than the ring
+        are never attended)."""
+        c = self.c
+        hd, nkv = c["head_dim"], c["n_kv_heads"]
+        for l in range(c["n_layers"]):
+            for kind, cache in (("k", self.k_cache), ("v", self.v_cache)):
+                sc, q = pages[(l, kind)]
+                rows = O.dequant_q8_0(sc, q).reshape(-1, nkv * hd)
+                slots = rows.shape[0]
+                cache[l] = [rows[p % slots].copy() for p in range(n_tokens)]
+        self.pos = n_tokens
+
     def is_global(self, layer: int) -> bool:
         ge = self.c["global_every"]
         return layer % ge == ge - 1

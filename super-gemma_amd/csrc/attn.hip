@@ -31,50 +31,88 @@ namespace sgq {
 namespace {
 
 constexpr int kHD = 128;
-constexpr int kAWG = 256;
-constexpr int kSub = 256;             // slots scored per pass
+constexpr int kAWG = 256;             // split kernel workgroup (= slots per pass)
 constexpr float kNegBig = -3.0e38f;
 
-// Dequantized dot of a 128-wide K row (int8 + 4 f16 scales) with q (LDS).
-__device__ __forceinline__ float k_row_dot(const int4 (&kr)[8], const float (&ksc)[4],
-                                           const float *qs) {
-    float s = 0.f;
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-        float part = 0.f;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int4 v = kr[2 * b + c];
-            const int w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float4 q4 = *reinterpret_cast<const float4 *>(qs + 32 * b + 16 * c + 4 * e);
-                part = __builtin_fmaf(q4.x, (float)(int8_t)(w[e] & 0xff), part);
-                part = __builtin_fmaf(q4.y, (float)(int8_t)((w[e] >> 8) & 0xff), part);
-                part = __builtin_fmaf(q4.z, (float)(int8_t)((w[e] >> 16) & 0xff), part);
-                part = __builtin_fmaf(q4.w, (float)(int8_t)((w[e] >> 24) & 0xff), part);
-            }
-        }
-        s = __builtin_fmaf(ksc[b], part, s);
-    }
-    return s;
+// Native 4 × i32 vector: HIP's int4 is a struct, and copying one into LDS
+// becomes a memcpy out of a stack array (scratch) instead of registers.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr size_t attn_lds_bytes(int qpk, int wg) {
+    return (size_t)wg * kHD + (size_t)qpk * wg * 4 + (size_t)wg * 8;
 }
 
+// Inputs of the fused post-projection (attn_decode_q8_kernel<*, true>).
+struct AttnPost {
+    const float *q_raw, *k_raw, *v_src;  // projections of this token
+    const float *wq, *wk;                // q_norm / k_norm weights [head_dim]
+    const float *rope_cs;                // (cos, sin) × head_dim/2 for this position
+    float eps;
+    int ring;                            // slots of a ring cache, 0 = linear
+    int8_t *kq_w, *vq_w;                 // the cache pages, written by split 0
+    uint16_t *ks_w, *vs_w;
+};
+
+// Dequantized dots of a 128-wide K row (int8 + 4 f16 scales) with the QPK
+// query heads of a kv head (LDS): one pass over the row, every converted
+// K word used for all heads at once (the converted floats die at once).
 template <int QPK>
-__global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
+__device__ __forceinline__ void k_row_dots(const i32x4 (&kr)[8], uint2 kss, const float *q0,
+                                           float scale, float (&sc)[QPK]) {
+    const float ksc[4] = {f16_bits_to_f32(kss.x & 0xffff), f16_bits_to_f32(kss.x >> 16),
+                          f16_bits_to_f32(kss.y & 0xffff), f16_bits_to_f32(kss.y >> 16)};
+    float s[QPK];
+#pragma unroll
+    for (int h = 0; h < QPK; h++) s[h] = 0.f;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        float part[QPK];
+#pragma unroll
+        for (int h = 0; h < QPK; h++) part[h] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int w = kr[2 * b + c][e];
+                const float k0 = (float)(int8_t)(w & 0xff), k1 = (float)(int8_t)((w >> 8) & 0xff);
+                const float k2 = (float)(int8_t)((w >> 16) & 0xff), k3 = (float)(int8_t)(w >> 24);
+#pragma unroll
+                for (int h = 0; h < QPK; h++) {
+                    const float4 q4 =
+                        *reinterpret_cast<const float4 *>(q0 + h * kHD + 32 * b + 16 * c + 4 * e);
+                    part[h] = __builtin_fmaf(q4.x, k0, part[h]);
+                    part[h] = __builtin_fmaf(q4.y, k1, part[h]);
+                    part[h] = __builtin_fmaf(q4.z, k2, part[h]);
+                    part[h] = __builtin_fmaf(q4.w, k3, part[h]);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < QPK; h++) s[h] = __builtin_fmaf(ksc[b], part[h], s[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < QPK; h++) sc[h] = s[h] * scale;
+}
+
+template <int QPK, bool FUSED, int WG>
+__global__ __launch_bounds__(WG) void attn_decode_q8_kernel(
     const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
     const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
     const uint32_t *__restrict__ step, int step_word, uint32_t kv_len_direct, int n_kv,
-    int n_splits, float scale, float *__restrict__ part) {
-    constexpr int G = kAWG / (QPK * (kHD / 4));  // slot groups in the PV phase
+    int n_splits, float scale, float *__restrict__ part, AttnPost post) {
+    constexpr int G = WG / (QPK * (kHD / 4));  // slot groups in the PV phase
     static_assert(G >= 1, "QPK too large for one workgroup");
-    constexpr int kVRow = kHD / 4 + 4;           // V row in LDS, ints (padded)
+    // Dynamic LDS (attn_lds_bytes): V quants of the sub-chunk, one 128-B row
+    // per slot with its eight 16-B chunks XOR-swizzled by slot (conflict-
+    // free row writes and PV reads); probabilities; V scales (f16 × 4).
+    // After the last PV the V area holds the per-group accumulators.
+    extern __shared__ __align__(16) uint8_t attn_smem[];
+    int *v_s = reinterpret_cast<int *>(attn_smem);
+    float *s_s = reinterpret_cast<float *>(attn_smem + WG * kHD);
+    uint2 *vsc_s = reinterpret_cast<uint2 *>(attn_smem + WG * kHD + QPK * WG * 4);
+    float *acc_s = reinterpret_cast<float *>(attn_smem);  // [G][QPK][kHD]
     __shared__ __align__(16) float q_s[QPK][kHD];
-    __shared__ float s_s[QPK][kSub];             // probabilities of the sub-chunk
-    __shared__ float vs_s[kSub][kHD / 32];       // V scales of the sub-chunk
-    __shared__ __align__(16) int v_s[kSub][kVRow];  // V quants of the sub-chunk
-    __shared__ float red[QPK][kAWG / kWave];
-    __shared__ float acc_s[G][QPK][kHD];
+    __shared__ float red[QPK][WG / kWave];
 
     const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -83,8 +121,84 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
     const uint32_t t_begin = min((uint32_t)split * chunk, kv_len);
     const uint32_t t_end = min(t_begin + chunk, kv_len);
 
-    for (int i = tid; i < QPK * kHD; i += kAWG)
-        q_s[i / kHD][i % kHD] = q[(size_t)(kvh * QPK) * kHD + i];
+    // ---- one slot per thread: K row, V row and both scale words issued
+    // together (one memory round trip per sub-chunk); the first sub-chunk is
+    // issued before the post-projection, later ones while PV runs.
+    i32x4 kr[8], vr[8];
+    uint2 kss = {0u, 0u}, vss = {0u, 0u};
+#define SGQ_LOAD_SUB(BASE)                                                          \
+    if ((uint32_t)tid < min((uint32_t)WG, t_end - (BASE))) {                        \
+        const size_t row = (size_t)((BASE) + tid) * n_kv + kvh;                     \
+        const i32x4 *kp = reinterpret_cast<const i32x4 *>(kq + row * kHD);          \
+        const i32x4 *vp = reinterpret_cast<const i32x4 *>(vq + row * kHD);          \
+        _Pragma("unroll") for (int c = 0; c < 8; c++) kr[c] = kp[c];                \
+        _Pragma("unroll") for (int c = 0; c < 8; c++) vr[c] = vp[c];                \
+        kss = *reinterpret_cast<const uint2 *>(ks + row * (kHD / 32));              \
+        vss = *reinterpret_cast<const uint2 *>(vs + row * (kHD / 32));              \
+    }
+    if (t_begin < t_end) {
+        SGQ_LOAD_SUB(t_begin)
+    }
+    uint32_t fresh_slot = 0xffffffffu;
+    __shared__ __align__(16) int fk_s[kHD / 4], fv_s[kHD / 4];  // new K/V row quants
+    __shared__ __align__(8) uint16_t fks_s[kHD / 32], fvs_s[kHD / 32];
+    if (FUSED) {
+        static_assert(2 * kHD <= WG && QPK * kHD <= 2 * kHD, "post layout");
+        __shared__ float pq_s[QPK * kHD], pkv_s[2 * kHD], pred[2][2 * kHD / kWave];
+        const uint32_t pos = step[0];
+        fresh_slot = post.ring ? pos % (uint32_t)post.ring : pos;
+        // threads 0..255: q head g / k (g = 0) or v (g = 1) element d
+        const bool pt = tid < 2 * kHD;
+        const int g = pt ? tid / kHD : 0, d = tid % kHD;
+        float qv = tid < QPK * kHD ? post.q_raw[(size_t)kvh * QPK * kHD + tid] : 0.f;
+        float kvv = !pt ? 0.f
+                  : g == 0 ? post.k_raw[(size_t)kvh * kHD + d] : post.v_src[(size_t)kvh * kHD + d];
+        float a = qv * qv, b = kvv * kvv;
+        for (int o = 32; o > 0; o >>= 1) {
+            a += __shfl_xor(a, o, kWave);
+            b += __shfl_xor(b, o, kWave);
+        }
+        if (lane == 0 && pt) pred[0][wave] = a, pred[1][wave] = b;
+        __syncthreads();
+        const float sq = pred[0][2 * g] + pred[0][2 * g + 1];
+        const float skv = pred[1][2 * g] + pred[1][2 * g + 1];
+        qv = qv * (1.0f / sqrtf(sq / (float)kHD + post.eps)) * post.wq[d];
+        kvv = kvv * (1.0f / sqrtf(skv / (float)kHD + post.eps)) * (g == 0 ? post.wk[d] : 1.f);
+        if (tid < QPK * kHD) pq_s[tid] = qv;
+        if (pt) pkv_s[tid] = kvv;
+        __syncthreads();
+        {  // NEOX RoPE: pair i couples dims (i, i + 64)
+            const int i = d % (kHD / 2), hb = tid - d;  // head base
+            const float c = post.rope_cs[2 * i], sn = post.rope_cs[2 * i + 1];
+            if (tid < QPK * kHD) {
+                const float x0 = pq_s[hb + i], x1 = pq_s[hb + i + kHD / 2];
+                q_s[g][d] = d < kHD / 2 ? x0 * c - x1 * sn : x1 * c + x0 * sn;
+            }
+            if (pt && g == 0) {
+                const float x0 = pkv_s[i], x1 = pkv_s[i + kHD / 2];
+                kvv = d < kHD / 2 ? x0 * c - x1 * sn : x1 * c + x0 * sn;
+            }
+        }
+        // Q8_0 of the new row (kv_quant_q8.wgsl:41-56): 32-lane groups
+        float amax = fabsf(kvv);
+        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
+        const float dq = amax * (1.0f / 127.0f);
+        const float id = dq > 0.f ? 1.0f / dq : 0.f;
+        const int8_t qi = (int8_t)(int)__builtin_rintf(kvv * id);
+        const uint16_t sc = f32_to_f16_bits(dq);
+        if (pt) {
+            reinterpret_cast<int8_t *>(g == 0 ? fk_s : fv_s)[d] = qi;
+            if ((d & 31) == 0) (g == 0 ? fks_s : fvs_s)[d / 32] = sc;
+        }
+        if (pt && split == 0) {
+            const size_t e = ((size_t)fresh_slot * n_kv + kvh) * kHD + d;
+            (g == 0 ? post.kq_w : post.vq_w)[e] = qi;
+            if ((d & 31) == 0) (g == 0 ? post.ks_w : post.vs_w)[e / 32] = sc;
+        }
+    } else {
+        for (int i = tid; i < QPK * kHD; i += WG)
+            q_s[i / kHD][i % kHD] = q[(size_t)(kvh * QPK) * kHD + i];
+    }
 
     // PV thread role: head ph, 4-dim word pw, slot group pg
     const int ph = tid / (kHD / 4) % QPK, pw = tid % (kHD / 4), pg = tid / (QPK * kHD / 4);
@@ -96,40 +210,47 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
         l_run[h] = 0.f;
     }
 
-    for (uint32_t base = t_begin; base < t_end; base += kSub) {
-        const int n_here = (int)min((uint32_t)kSub, t_end - base);
+    for (uint32_t base = t_begin; base < t_end; base += WG) {
+        const int n_here = (int)min((uint32_t)WG, t_end - base);
         const int t = tid;
-        // ---- one slot per thread: K row, V row and both scale words issued
-        // together (one memory round trip for the whole sub-chunk)
-        int4 kr[8], vr[8];
-        uint2 kss = {0u, 0u}, vss = {0u, 0u};
-        if (t < n_here) {
-            const size_t row = (size_t)(base + t) * n_kv + kvh;
-            const int4 *kp = reinterpret_cast<const int4 *>(kq + row * kHD);
-            const int4 *vp = reinterpret_cast<const int4 *>(vq + row * kHD);
-#pragma unroll
-            for (int c = 0; c < 8; c++) kr[c] = kp[c];
-#pragma unroll
-            for (int c = 0; c < 8; c++) vr[c] = vp[c];
-            kss = *reinterpret_cast<const uint2 *>(ks + row * (kHD / 32));
-            vss = *reinterpret_cast<const uint2 *>(vs + row * (kHD / 32));
-        }
-        __syncthreads();  // q_s ready; previous sub-chunk's LDS reads done
+        __syncthreads();  // q_s (and the new row) ready; previous sub-chunk's LDS reads done
         float sc[QPK];
+        // q is re-read from LDS for every pass (an opaque zero offset keeps
+        // the compiler from hoisting 32·QPK float4 out of the loop into
+        // registers, which a 1024-thread workgroup cannot afford)
+        int zoff;
+        asm volatile("s_mov_b32 %0, 0" : "=s"(zoff));
+        if (FUSED) {  // the new row replaces what the cache load returned for it
+            const bool fresh = t < n_here && base + t == fresh_slot;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const i32x4 fk = reinterpret_cast<const i32x4 *>(fk_s + zoff)[c];
+                const i32x4 fv = reinterpret_cast<const i32x4 *>(fv_s + zoff)[c];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    kr[c][e] = fresh ? fk[e] : kr[c][e];
+                    vr[c][e] = fresh ? fv[e] : vr[c][e];
+                }
+            }
+            const uint2 fks = *reinterpret_cast<const uint2 *>(fks_s + zoff);
+            const uint2 fvs = *reinterpret_cast<const uint2 *>(fvs_s + zoff);
+            kss.x = fresh ? fks.x : kss.x;
+            kss.y = fresh ? fks.y : kss.y;
+            vss.x = fresh ? fvs.x : vss.x;
+            vss.y = fresh ? fvs.y : vss.y;
+        }
         if (t < n_here) {
 #pragma unroll
-            for (int c = 0; c < 8; c++) *reinterpret_cast<int4 *>(&v_s[t][4 * c]) = vr[c];
-            vs_s[t][0] = f16_bits_to_f32(vss.x & 0xffff);
-            vs_s[t][1] = f16_bits_to_f32(vss.x >> 16);
-            vs_s[t][2] = f16_bits_to_f32(vss.y & 0xffff);
-            vs_s[t][3] = f16_bits_to_f32(vss.y >> 16);
-            const float ksc[4] = {f16_bits_to_f32(kss.x & 0xffff), f16_bits_to_f32(kss.x >> 16),
-                                  f16_bits_to_f32(kss.y & 0xffff), f16_bits_to_f32(kss.y >> 16)};
-#pragma unroll
-            for (int h = 0; h < QPK; h++) sc[h] = k_row_dot(kr, ksc, q_s[h]) * scale;
+            for (int c = 0; c < 8; c++)
+                *reinterpret_cast<i32x4 *>(&v_s[t * 32 + 4 * (c ^ (t & 7))]) = vr[c];
+            vsc_s[t] = vss;
+            k_row_dots<QPK>(kr, kss, &q_s[0][0] + zoff, scale, sc);
         } else {
 #pragma unroll
             for (int h = 0; h < QPK; h++) sc[h] = kNegBig;
+        }
+        if (base + WG < t_end) {  // lands while this one finishes
+            SGQ_LOAD_SUB(base + WG)
         }
         // ---- online softmax over this sub-chunk: one max and one sum
         // round per sub-chunk for all heads (fixed-order trees)
@@ -144,7 +265,7 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
 #pragma unroll
         for (int h = 0; h < QPK; h++) {
             float r = red[h][0];
-            for (int w = 1; w < kAWG / kWave; w++) r = fmaxf(r, red[h][w]);
+            for (int w = 1; w < WG / kWave; w++) r = fmaxf(r, red[h][w]);
             mx[h] = r;
         }
         float p[QPK], corr[QPK];
@@ -152,7 +273,7 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
         for (int h = 0; h < QPK; h++) {
             const float m_new = fmaxf(m_run[h], mx[h]);
             p[h] = t < n_here ? __expf(sc[h] - m_new) : 0.f;
-            s_s[h][t] = p[h];
+            s_s[h * WG + t] = p[h];
             corr[h] = __expf(m_run[h] - m_new);
             m_run[h] = m_new;
         }
@@ -167,9 +288,12 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[e] *= cph;
         // ---- PV from LDS: thread (ph, pw, pg) takes slots pg, pg+G, ...
+        const int pb = pw / 8;  // this thread's 32-block of head_dim
         for (int i = pg; i < n_here; i += G) {
-            const int v4 = v_s[i][pw];
-            const float pp = s_s[ph][i] * vs_s[i][pw / 8];
+            const int v4 = v_s[i * 32 + 4 * ((pw >> 2) ^ (i & 7)) + (pw & 3)];
+            const uint2 sv = vsc_s[i];
+            const uint32_t sw = pb < 2 ? sv.x : sv.y;
+            const float pp = s_s[ph * WG + i] * f16_bits_to_f32((sw >> ((pb & 1) * 16)) & 0xffffu);
             acc[0] = __builtin_fmaf(pp, (float)(int8_t)(v4 & 0xff), acc[0]);
             acc[1] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 8) & 0xff), acc[1]);
             acc[2] = __builtin_fmaf(pp, (float)(int8_t)((v4 >> 16) & 0xff), acc[2]);
@@ -179,20 +303,21 @@ __global__ __launch_bounds__(kAWG) void attn_decode_q8_kernel(
 #pragma unroll
         for (int h = 0; h < QPK; h++) {
             float r = red[h][0];
-            for (int w = 1; w < kAWG / kWave; w++) r += red[h][w];
+            for (int w = 1; w < WG / kWave; w++) r += red[h][w];
             l_run[h] = l_run[h] * corr[h] + r;
         }
     }
 
     // ---- combine the G slot groups (fixed order) and write the partial
+    __syncthreads();  // v_s (now acc_s) free
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc_s[pg][ph][4 * pw + e] = acc[e];
+    for (int e = 0; e < 4; e++) acc_s[(pg * QPK + ph) * kHD + 4 * pw + e] = acc[e];
     __syncthreads();
     const int stride = kHD + 2;
-    for (int i = tid; i < QPK * kHD; i += kAWG) {
-        const int h = i / kHD, d = i % kHD;
+    if (tid < QPK * kHD) {
+        const int h = tid / kHD, d = tid % kHD;
         float a = 0.f;
-        for (int g = 0; g < G; g++) a += acc_s[g][h][d];
+        for (int g = 0; g < G; g++) a += acc_s[(g * QPK + h) * kHD + d];
         part[((size_t)(kvh * QPK + h) * n_splits + split) * stride + d] = a;
     }
     if (tid < QPK) {
@@ -292,8 +417,9 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     dim3 grid(n_kv, n_splits);
 #define SGQ_ATTN(Q)                                                                               \
     case Q:                                                                                       \
-        hipLaunchKernelGGL(attn_decode_q8_kernel<Q>, grid, dim3(kAWG), 0, st, q, kq, ks, vq, vs,  \
-                           step, step_word, kv_len, n_kv, n_splits, scale, part);                 \
+        hipLaunchKernelGGL((attn_decode_q8_kernel<Q, false, kAWG>), grid, dim3(kAWG),             \
+                           attn_lds_bytes(Q, kAWG), st, q, kq, ks, vq, vs, step, step_word,       \
+                           kv_len, n_kv, n_splits, scale, part, AttnPost{});                      \
         SGQ_HIP(hipGetLastError());                                                               \
         hipLaunchKernelGGL(attn_merge_kernel<Q>, dim3(n_kv), dim3(Q * kHD), 0, st, part,          \
                            n_splits, out, static_cast<BlockLimbs *>(limbs_out));                  \
@@ -304,6 +430,48 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
         default:
             return fail(SGQ_ERR_VALIDATION, "attn_decode_q8: %d q heads per kv head unsupported",
                         qpk);
+    }
+#undef SGQ_ATTN
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int attn_prepare() { return SGQ_OK; }  // all variants fit the default LDS limit
+
+int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_raw,
+                             const float *v_src, const float *wq_norm, const float *wk_norm,
+                             const float *rope_cs, float eps, const uint32_t *step, int step_word,
+                             uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
+                             int n_q, int n_kv, int n_splits, float scale, float *out,
+                             void *workspace, size_t workspace_bytes, void *limbs_out) {
+    SGQ_CHECK(step != nullptr, "attn (fused): needs the step buffer");
+    SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn (fused): n_q %% n_kv != 0");
+    SGQ_CHECK(n_splits >= 1 && n_splits <= 1024, "attn (fused): n_splits %d", n_splits);
+    SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 && ((uintptr_t)ks & 7) == 0 &&
+                  ((uintptr_t)vs & 7) == 0,
+              "attn (fused): misaligned cache");
+    const size_t part_bytes = (size_t)n_q * n_splits * (kHD + 2) * 4;
+    SGQ_CHECK(kAttnPartOff + part_bytes <= workspace_bytes, "attn (fused): workspace too small");
+    float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + kAttnPartOff);
+    const AttnPost post{q_raw, k_raw, v_src, wq_norm, wk_norm, rope_cs, eps, (int)ring,
+                        kq, vq, ks, vs};
+    if (int rc = attn_prepare()) return rc;
+    dim3 grid(n_kv, n_splits);
+#define SGQ_ATTN(Q)                                                                               \
+    case Q:                                                                                       \
+        hipLaunchKernelGGL((attn_decode_q8_kernel<Q, true, kAWG>), grid, dim3(kAWG),              \
+                           attn_lds_bytes(Q, kAWG), st, nullptr, kq, ks, vq, vs, step, step_word, \
+                           0u, n_kv, n_splits, scale, part, post);                                \
+        SGQ_HIP(hipGetLastError());                                                               \
+        hipLaunchKernelGGL(attn_merge_kernel<Q>, dim3(n_kv), dim3(Q * kHD), 0, st, part,          \
+                           n_splits, out, static_cast<BlockLimbs *>(limbs_out));                  \
+        break;
+    switch (n_q / n_kv) {
+        SGQ_ATTN(1)
+        SGQ_ATTN(2)
+        default:
+            return fail(SGQ_ERR_VALIDATION, "attn (fused): %d q heads per kv head unsupported",
+                        n_q / n_kv);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());

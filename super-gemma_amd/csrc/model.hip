@@ -186,80 +186,25 @@ __global__ __launch_bounds__(256) void geglu_limbs_kernel(const float *__restric
     limbs_block8(h, i & 7, &xl[i >> 3]);
 }
 
-// Per-head post-projection: q heads -> rmsnorm(q_norm) + RoPE -> q_out;
-// k heads -> rmsnorm(k_norm) + RoPE -> Q8_0 into the cache slot;
-// v heads -> weightless rmsnorm -> Q8_0 into the cache slot.
-// Grid: n_q + 2·n_kv workgroups of 128 threads (one element each).
-__global__ __launch_bounds__(kHeadDim) void qkv_post_kernel(
-    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
-    const float *__restrict__ v_raw, const float *__restrict__ wq_norm,
-    const float *__restrict__ wk_norm, const uint32_t *__restrict__ step, int n_q, int n_kv,
-    float theta, int live_pairs, int ring, float eps, float *__restrict__ q_out,
-    int8_t *__restrict__ kq, uint16_t *__restrict__ ks, int8_t *__restrict__ vq,
-    uint16_t *__restrict__ vs) {
-    __shared__ float row[kHeadDim];
-    __shared__ float red[kHeadDim / kWave];
-    const int h = blockIdx.x, t = threadIdx.x;
-    const uint32_t pos = step[0];
-    int kind;  // 0 q, 1 k, 2 v
-    int head;
-    if (h < n_q) {
-        kind = 0;
-        head = h;
-    } else if (h < n_q + n_kv) {
-        kind = 1;
-        head = h - n_q;
-    } else {
-        kind = 2;
-        head = h - n_q - n_kv;
-    }
-    const float *src = kind == 0 ? q_raw : kind == 1 ? k_raw : v_raw;
-    float v = src[head * kHeadDim + t];
-    // rmsnorm over the head (f32 sum of squares, fixed tree)
-    float ss = v * v;
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
-    if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    ss = red[0] + red[1];
-    const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + eps);
-    const float wn = kind == 0 ? wq_norm[t] : kind == 1 ? wk_norm[t] : 1.f;
-    v = v * inv * wn;
-    row[t] = v;
-    __syncthreads();
-    if (kind < 2) {  // NEOX RoPE: pair i couples (i, i + 64); live pairs rotate
-        const int half = kHeadDim / 2;
-        const int i = t % half;
-        if (i < live_pairs) {
-            const double freq = pow((double)theta, -2.0 * (double)i / (double)kHeadDim);
-            const double ang = (double)pos * freq;
-            const float c = (float)cos(ang), sn = (float)sin(ang);
-            const float a = row[i], b = row[i + half];
-            v = t < half ? a * c - b * sn : b * c + a * sn;
-        }
-    }
-    if (kind == 0) {
-        q_out[head * kHeadDim + t] = v;
-        return;
-    }
-    // Q8_0 per 32 elements along head_dim (kv_quant_q8.wgsl:41-56 semantics)
-    float amax = fabsf(v);
-    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
-    const float d = amax * (1.0f / 127.0f);
-    const float id = d > 0.f ? 1.0f / d : 0.f;
-    const int qv = (int)__builtin_rintf(v * id);
-    const uint32_t slot = ring ? pos % (uint32_t)ring : pos;
-    const size_t e = ((size_t)slot * n_kv + head) * kHeadDim + t;
-    int8_t *dq = kind == 1 ? kq : vq;
-    uint16_t *ds = kind == 1 ? ks : vs;
-    dq[e] = (int8_t)qv;
-    if ((t & 31) == 0) ds[e / 32] = f32_to_f16_bits(d);
-}
-
-// step words [pos, kv_len_sliding, kv_len_global, q0, token]
+// step words [pos, kv_len_sliding, kv_len_global, q0, token], and the RoPE
+// (cos, sin) tables of position `a` for both layer kinds, angles in f64
+// (crates/sg-model/src/rope.rs:27-48): pair i of 64 turns by
+// pos·theta^(-2i/128)/factor_i; global layers use the divisor factors
+// [1 × live, 1e30 × rest] (rope.rs:13-16), so pairs past `live` barely move.
 __global__ void model_step_kernel(uint32_t *step, uint32_t a, uint32_t b, uint32_t c, uint32_t d,
-                                  uint32_t e) {
+                                  uint32_t e, float *rope_cs, float theta_s, float theta_g,
+                                  int live_g) {
     const uint32_t t = threadIdx.x;
     if (t < 5) step[t] = t == 0 ? a : t == 1 ? b : t == 2 ? c : t == 3 ? d : e;
+    if (t < kHeadDim) {
+        const int kind = t / (kHeadDim / 2), i = t % (kHeadDim / 2);
+        const double theta = kind ? (double)theta_g : (double)theta_s;
+        const double factor = kind && i >= live_g ? 1e30 : 1.0;
+        const double freq = pow(theta, -2.0 * (double)i / (double)kHeadDim);
+        const double ang = (double)a * freq / factor;
+        rope_cs[t * 2] = (float)cos(ang);
+        rope_cs[t * 2 + 1] = (float)sin(ang);
+    }
 }
 
 }  // namespace
@@ -289,6 +234,7 @@ struct sgq_model {
     float *x, *q_raw, *k_raw, *v_raw, *q, *attn, *o, *g, *u, *f;
     void *xl;  // limb table (largest K)
     uint32_t *step;
+    float *rope_cs;  // [2 kinds][head_dim/2][cos, sin] of the current position
     uint32_t pos = 0;
     sgq_graph *graph = nullptr;
     float *graph_logits = nullptr;
@@ -336,20 +282,15 @@ int record_step(sgq_model *m, float *logits) {
         qkv.count = L.wv ? 3 : 2;
         const float *v_src = L.wv ? m->v_raw : m->k_raw;
         if ((rc = launch_gemv_limbs(st, qkv, xl, H))) return rc;
-        const float theta = L.global ? c.rope_theta_global : c.rope_theta_sliding;
-        const int live = L.global ? (int)lroundf(c.global_rope_frac * kHeadDim / 2) : kHeadDim / 2;
-        hipLaunchKernelGGL(qkv_post_kernel, dim3(c.n_q_heads + 2 * c.n_kv_heads), dim3(kHeadDim), 0,
-                           st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm, m->step,
-                           (int)c.n_q_heads, (int)c.n_kv_heads, theta, live,
-                           L.global ? 0 : (int)c.sliding_window, c.eps, m->q, L.kq, L.ks, L.vq,
-                           L.vs);
-        SGQ_HIP(hipGetLastError());
-        // about 256 slots per workgroup at a full cache
-        const int n_splits = L.global ? (int)std::min(64u, std::max(8u, L.slots / 256)) : 8;
-        if ((rc = launch_attn_decode_q8(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step, L.global ? 2 : 1,
-                                        0, (int)c.n_q_heads, (int)c.n_kv_heads, kHeadDim, n_splits,
-                                        c.attn_scale, m->attn, ctx_workspace(m->ctx),
-                                        kWorkspaceBytes, xl)))
+        // splits: 16 for a 1024-slot ring (64 slots per workgroup), about 512
+        // slots per workgroup for a linear cache (measured best)
+        const int n_splits = L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 16;
+        if ((rc = launch_attn_decode_fused(
+                 st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
+                 m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
+                 L.global ? 0u : L.slots, L.kq, L.ks, L.vq, L.vs, (int)c.n_q_heads,
+                 (int)c.n_kv_heads, n_splits, c.attn_scale, m->attn, ctx_workspace(m->ctx),
+                 kWorkspaceBytes, xl)))
             return rc;
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
@@ -424,6 +365,7 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
     SGQ_CHECK(c.global_every >= 1, "model: global_every must be >= 1");
     SGQ_CHECK(c.global_rope_frac >= 0.f && c.global_rope_frac <= 1.f, "model: global_rope_frac");
     if (int rc0 = gemv_prepare()) return rc0;
+    if (int rc0 = attn_prepare()) return rc0;
     (void)device_info();
     auto *m = new sgq_model;
     m->ctx = ctx;
@@ -470,6 +412,8 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
         if ((rc = alloc(m, act_n[i] * 4, reinterpret_cast<void **>(acts[i])))) return fail_out(rc);
     if ((rc = alloc(m, std::max(H, F) / 32 * sizeof(BlockLimbs), &m->xl))) return fail_out(rc);
     if ((rc = alloc(m, 64, reinterpret_cast<void **>(&m->step)))) return fail_out(rc);
+    if ((rc = alloc(m, 2 * kHeadDim * 4, reinterpret_cast<void **>(&m->rope_cs))))
+        return fail_out(rc);
     if (hipStreamSynchronize(ctx_stream(ctx)) != hipSuccess) return fail_out(fail(SGQ_ERR_HIP, "init sync"));
     *out = m;
     return SGQ_OK;
@@ -497,8 +441,10 @@ static int write_step(sgq_model *m, uint32_t token) {
     SGQ_CHECK(token < c.vocab, "model: token %u >= vocab %u", token, c.vocab);
     SGQ_CHECK(m->pos < c.max_ctx, "model: context full (%u)", c.max_ctx);
     const uint32_t kv_sl = std::min(m->pos + 1, std::min(c.sliding_window, c.max_ctx));
-    hipLaunchKernelGGL(model_step_kernel, dim3(1), dim3(64), 0, ctx_stream(m->ctx), m->step,
-                       m->pos, kv_sl, m->pos + 1, m->pos, token);
+    hipLaunchKernelGGL(model_step_kernel, dim3(1), dim3(kHeadDim), 0, ctx_stream(m->ctx), m->step,
+                       m->pos, kv_sl, m->pos + 1, m->pos, token, m->rope_cs,
+                       c.rope_theta_sliding, c.rope_theta_global,
+                       (int)lroundf(c.global_rope_frac * kHeadDim / 2));
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }

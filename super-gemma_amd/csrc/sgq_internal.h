@@ -86,6 +86,18 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
                           int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
                           int n_splits, float scale, float *out, void *workspace,
                           size_t workspace_bytes, void *limbs_out = nullptr);
+// Sets the attention kernels' launch attributes (call before graph capture).
+int attn_prepare();
+// Decode attention with the step's q/k/v post-projection fused in: q, k
+// and v_src are the raw projections (v_src may alias k_raw), rope_cs the
+// (cos, sin) table of the current position; appends the new K/V rows at the
+// current slot (pos % ring, or pos when ring == 0).  head_dim 128.
+int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_raw,
+                             const float *v_src, const float *wq_norm, const float *wk_norm,
+                             const float *rope_cs, float eps, const uint32_t *step, int step_word,
+                             uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
+                             int n_q, int n_kv, int n_splits, float scale, float *out,
+                             void *workspace, size_t workspace_bytes, void *limbs_out);
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);

@@ -138,6 +138,34 @@ def test_model_full_width_two_layers_matches_oracle(ctx, oracle):
     model.close()
 
 
+def test_model_long_context_matches_oracle(ctx, oracle):
+    """A 1024-slot sliding ring that is full and wraps (positions 1030..1033,
+    one 1024-slot attention pass per kv head) and global layers over ~1030
+    positions: synthetic K/V pages (sgq_model_fill_cache) read back into the
+    oracle's cache."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print("model long context", flush=True)
+    cfg = _small_cfg(sgq, sliding_window=1024, max_ctx=1100, seed=0x10C)
+    model = sgq.Model(ctx, cfg)
+    model.fill_cache(1030)
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    pages = {}
+    for l in range(cfg.n_layers):
+        for kind in ("k", "v"):
+            pages[(l, kind)] = (model.read_tensor(f"{kind}_scales", l, np.uint16),
+                                model.read_tensor(f"{kind}_quants", l, np.int8))
+    ref.preload_cache(pages, 1030)
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([11, 1500, 2, 77]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
+
+
 def test_model_rejects_bad_inputs(ctx):
     import sgq
 
