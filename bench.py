@@ -43,7 +43,7 @@ def q4_bytes(n, k):
 
 class Gemv:
     name = "gemv_q4_0 K=5376 N=21504 (BASELINE config 1), 8 rotating weight copies"
-    kernel = "gemv_q4_0_kernel"
+    kernel = "gemv_q4_0_ring_kernel"
 
     def __init__(self, ctx, torch):
         self.ctx, self.torch = ctx, torch
@@ -65,9 +65,10 @@ class Gemv:
     def result(self, ms_per_step):
         gbs = self.bytes / (ms_per_step * 1e-3) / 1e9
         return {
-            "value": gbs, "unit": "GB/s", "dtype": "q4_0 weights, fp32 x/y (int8 dot4 on 3-limb x)",
-            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "value": gbs, "unit": "GB/s",
+            "dtype": "q4_0 weights, fp32 x/y (i4 dot8 on 4-limb x)",
+            "roofline": ring_roofline(self.ctx, self.torch, [w.data_ptr() for w in self.w],
+                                      self.k, self.n),
             "config": {"workload": self.name, "m": 1, "k": self.k, "n": self.n,
                        "bytes_per_launch": self.bytes},
         }
@@ -145,36 +146,10 @@ class Decode:
     def step(self, i):
         self.model.decode(self.rng.randrange(self.cfg.vocab), self.logits, graph=True)
 
-    def kernel_roofline(self, steps=124):
-        """The dominant kernel: the Q4_0 GEMV on the model's own ffn_gate
-        matrices (K=5376, N=21504), rotating over all layers so every launch
-        streams from HBM; HIP events on the context's stream around `steps`
-        launches (each launch = the x-limb pass + the streamed GEMV)."""
-        import ctypes as C
-
-        lib = self.sgq.lib()
-        c = self.cfg
-        x = self.torch.empty(c.hidden, dtype=self.torch.float32, device="cuda")
-        self.ctx.fill_normal(x, seed=3)
-        y = self.torch.empty(c.ffn, dtype=self.torch.float32, device="cuda")
-        ptrs = [self.model.tensor_ptr("ffn_gate", l)[0] for l in range(c.n_layers)]
-
-        def run(n):
-            for j in range(n):
-                rc = lib.sgq_gemv_q4_0(self.ctx.handle, C.c_void_p(ptrs[j % len(ptrs)]),
-                                       C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr()),
-                                       c.ffn, c.hidden)
-                assert rc == 0
-        run(len(ptrs))
-        self.ctx.synchronize()
-        self.ctx.timer_start()
-        run(steps)
-        ms = self.ctx.timer_stop() / steps
-        nbytes = q4_bytes(c.ffn, c.hidden) + c.hidden * 4 + c.ffn * 4
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "gemv_q4_0 (ffn_gate)",
-                "bytes_per_launch": nbytes, "us_per_launch": ms * 1e3}
+    def kernel_roofline(self):
+        return ring_roofline(self.ctx, self.torch,
+                             [self.model.tensor_ptr("ffn_gate", l)[0]
+                              for l in range(self.cfg.n_layers)], 5376, 21504)
 
     def result(self, ms_per_step):
         tok_s = 1000.0 / ms_per_step
@@ -195,6 +170,57 @@ class Decode:
                        "global_every": c.global_every, "context": self.context,
                        "weight_bytes": self.weight_bytes, "kv_bytes_read": self.kv_bytes},
         }
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_ring_k5376_n21504_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the streamed GEMV at K=5376, N=21504, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy
+    kernel of known size); None when that profile is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            return json.load(f)["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
+    """The dominant kernel, gemv_q4_0_ring_kernel, alone at K x N: x limbs
+    made once, then `steps` single-matrix launches rotating over w_ptrs (so
+    each launch streams its weights from HBM), HIP events on the context's
+    stream around them.  Algorithmic bytes per launch: W (18 B per 32
+    weights) + the x limb table (80 B per 32 values) + y (fp32)."""
+    import ctypes as C
+    import sgq
+
+    lib = sgq.lib()
+    x = torch.empty(k, dtype=torch.float32, device="cuda")
+    ctx.fill_normal(x, seed=3)
+    xl = torch.empty(k // 32 * ctx.X_LIMBS_BYTES_PER_BLOCK, dtype=torch.uint8, device="cuda")
+    ctx.x_limbs(x, xl, k)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    yp = (C.c_void_p * 1)(y.data_ptr())
+    rows = (C.c_uint32 * 1)(n)
+
+    def run(m):
+        for j in range(m):
+            wp = (C.c_void_p * 1)(w_ptrs[j % len(w_ptrs)])
+            rc = lib.sgq_gemv_q4_0_limbs(ctx.handle, 1, wp, yp, rows, C.c_void_p(xl.data_ptr()),
+                                         k, 0.0)
+            assert rc == 0, sgq.lib().sgq_last_error()
+    run(len(w_ptrs))
+    ctx.synchronize()
+    ctx.timer_start()
+    run(steps)
+    ms = ctx.timer_stop() / steps
+    nbytes = q4_bytes(n, k) + (k // 32) * 80 + n * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic(),
+            "kernel": f"gemv_q4_0_ring_kernel K={k} N={n}", "bytes_per_launch": nbytes,
+            "us_per_launch": ms * 1e3, "launches": steps}
 
 
 def cpu_baseline(budget_s: float = 12.0):

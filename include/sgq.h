@@ -122,9 +122,27 @@ int sgq_timer_stop(sgq_ctx *ctx, float *ms);
 
 /* Decode GEMV y[n] = W[n×k]·x[k]; W is Q4_0 row-major (k/32 blocks of 18 B
  * per row), x and y fp32.  Replaces gemv_q4_0_k{K} / gemv_q4_0_generic
- * (crates/sg-gpu/shaders/gemv_q4_0.wgsl:52-112).  k % 64 == 0, k <= 65536. */
+ * (crates/sg-gpu/shaders/gemv_q4_0.wgsl:52-112).  k % 64 == 0, k <= 65536.
+ * x enters the integer dot as four signed 4-bit limbs per value (error
+ * <= 2.6e-5 of its 32-block's max |x|, below an f16 rounding of x). */
 int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_t n,
                   uint32_t k);
+
+/* The decode GEMV in its two halves, as the decode graph runs them: x is
+ * split once into its limb table (sgq_x_limbs: k/32 entries of
+ * SGQ_X_LIMBS_BYTES_PER_BLOCK bytes, 16-byte aligned), then one launch
+ * streams up to 4 Q4_0 matrices that share x (the reference's per-matrix
+ * gemv_q4_0 dispatches of one x, e.g. Q/K/V or gate/up, graph.rs:478-560),
+ * writing rows[j] outputs to y[j]; softcap > 0 applies cap·tanh(v/cap) to
+ * every output (the LM head, graph.rs:740-756).  k % 256 == 0,
+ * 256 <= k <= 65536 (up to 4 K-slices of <= 170 blocks); weights 16-byte
+ * aligned.  No counterpart for the limb table in the reference: it is this
+ * GEMV's activation format (four signed 4-bit limbs per value, see
+ * sgq_gemv_q4_0 for the error bound). */
+#define SGQ_X_LIMBS_BYTES_PER_BLOCK 80
+int sgq_x_limbs(sgq_ctx *ctx, const float *x, void *x_limbs, uint32_t k);
+int sgq_gemv_q4_0_limbs(sgq_ctx *ctx, uint32_t n_targets, const void *const *w, float *const *y,
+                        const uint32_t *rows, const void *x_limbs, uint32_t k, float softcap);
 
 /* Q8_0 quantization of n fp32 values (n % 32 == 0) into f16 scales [n/32] and
  * int8 quants [n]: kv_quant_q8 (crates/sg-gpu/shaders/kv_quant_q8.wgsl:30-57),

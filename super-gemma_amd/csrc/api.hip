@@ -496,6 +496,33 @@ int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_
     return launch_gemv_q4_0(ctx->stream, w, x, y, n, k, ctx->workspace);
 }
 
+int sgq_x_limbs(sgq_ctx *ctx, const float *x, void *x_limbs, uint32_t k) {
+    if (!ctx || !x || !x_limbs) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_quant_limbs(ctx->stream, x, x_limbs, k);
+}
+
+int sgq_gemv_q4_0_limbs(sgq_ctx *ctx, uint32_t n_targets, const void *const *w, float *const *y,
+                        const uint32_t *rows, const void *x_limbs, uint32_t k, float softcap) {
+    if (!ctx || !w || !y || !rows || !x_limbs) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_CHECK(n_targets >= 1 && n_targets <= (uint32_t)kGemvMaxTargets,
+              "gemv_q4_0_limbs: %u targets (1..%d)", n_targets, kGemvMaxTargets);
+    SGQ_CHECK(softcap >= 0.f, "gemv_q4_0_limbs: negative softcap");
+    GemvTargets tg{};
+    uint64_t end = 0;
+    for (uint32_t j = 0; j < n_targets; j++) {
+        if (!w[j] || !y[j]) return fail(SGQ_ERR_VALIDATION, "NULL target %u", j);
+        SGQ_CHECK(rows[j] > 0, "gemv_q4_0_limbs: target %u has no rows", j);
+        end += rows[j];
+        SGQ_CHECK(end < (1u << 31), "gemv_q4_0_limbs: too many rows");
+        tg.w[j] = w[j];
+        tg.y[j] = y[j];
+        tg.end[j] = (int)end;
+    }
+    tg.count = (int)n_targets;
+    tg.softcap = softcap;
+    return launch_gemv_limbs(ctx->stream, tg, x_limbs, k);
+}
+
 int sgq_quant_q8_0(sgq_ctx *ctx, const float *x, uint16_t *scales, int8_t *quants, uint64_t n) {
     if (!ctx || (n && (!x || !scales || !quants))) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     return launch_quant_q8_0(ctx->stream, x, scales, quants, n);

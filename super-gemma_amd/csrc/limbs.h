@@ -27,6 +27,8 @@ struct BlockLimbs {
     int pad[3];
 };
 
+static_assert(sizeof(BlockLimbs) == SGQ_X_LIMBS_BYTES_PER_BLOCK, "limb table layout (sgq.h)");
+
 template <int NBL>
 __device__ __forceinline__ void quantize_values(const float (&v)[32], XLimbs<NBL> &L, int i) {
     float amax = 0.f;

@@ -113,6 +113,9 @@ SIGNATURES = {
     "sgq_timer_start": (I, [P]),
     "sgq_timer_stop": (I, [P, C.POINTER(C.c_float)]),
     "sgq_gemv_q4_0": (I, [P, P, P, P, U32, U32]),
+    "sgq_x_limbs": (I, [P, P, P, U32]),
+    "sgq_gemv_q4_0_limbs": (I, [P, U32, C.POINTER(P), C.POINTER(P), C.POINTER(U32), P, U32,
+                                C.c_float]),
     "sgq_quant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_dequant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_gemm_q4_0_q8": (I, [P, P, P, P, P, U32, U32, U32, U32, P]),
@@ -272,6 +275,28 @@ class GpuContext:
         _need(x, torch.float32, k, "x")
         _need(y, torch.float32, n, "y")
         _check(lib().sgq_gemv_q4_0(self._h, _ptr(w), _ptr(x), _ptr(y), n, k))
+
+    X_LIMBS_BYTES_PER_BLOCK = 80
+
+    def x_limbs(self, x: torch.Tensor, xl: torch.Tensor, k: int):
+        """x [k] fp32 -> its limb table (k/32 × 80 bytes, uint8 tensor)."""
+        _need(x, torch.float32, k, "x")
+        _need(xl, torch.uint8, k // 32 * self.X_LIMBS_BYTES_PER_BLOCK, "x_limbs")
+        _check(lib().sgq_x_limbs(self._h, _ptr(x), _ptr(xl), k))
+
+    def gemv_q4_0_limbs(self, ws, ys, rows, xl: torch.Tensor, k: int, softcap: float = 0.0):
+        """One launch over up to 4 matrices sharing x: ys[j][:rows[j]] = ws[j]·x."""
+        n = len(ws)
+        if not (len(ys) == len(rows) == n):
+            raise ValidationError(6, "ws, ys and rows differ in length")
+        for w, y, r in zip(ws, ys, rows):
+            _need(w, torch.uint8, r * (k // 32) * 18, "w")
+            _need(y, torch.float32, r, "y")
+        _need(xl, torch.uint8, k // 32 * self.X_LIMBS_BYTES_PER_BLOCK, "x_limbs")
+        wp = (P * n)(*[_ptr(w) for w in ws])
+        yp = (P * n)(*[_ptr(y) for y in ys])
+        rp = (U32 * n)(*rows)
+        _check(lib().sgq_gemv_q4_0_limbs(self._h, n, wp, yp, rp, _ptr(xl), k, softcap))
 
     def quant_q8_0(self, x: torch.Tensor, scales: torch.Tensor, quants: torch.Tensor):
         n = x.numel()

@@ -148,3 +148,57 @@ def test_gemv_rejects_bad_shapes(ctx):
         ctx.gemv_q4_0(w, x, y, 1, 96)  # K not a multiple of 64
     with pytest.raises(sgq.ValidationError):
         ctx.gemv_q4_0(w, x, y, 2, 128)  # W too small for N=2
+
+
+@pytest.mark.parametrize("k,rows", [(5376, (4096, 2048, 2048)), (5376, (21504, 21504)),
+                                    (21504, (5376,)), (4096, (5376,)), (256, (3, 130, 7, 64))])
+def test_gemv_limbs_multi_target_matches_oracle(ctx, oracle, k, rows):
+    """sgq_x_limbs + one sgq_gemv_q4_0_limbs launch over several matrices
+    sharing x (Q/K/V, gate/up at the decode shapes; ragged row counts)."""
+    print(f"gemv limbs k={k} rows={rows}", flush=True)
+    rng = oracle.Rng(0x1B5 + k + sum(rows))
+    ws = [rng.random_q4_0(r * k // 32) for r in rows]
+    x = oracle.through_f16(rng.f32_vec(k))
+    xl = empty(k // 32 * ctx.X_LIMBS_BYTES_PER_BLOCK, torch.uint8)
+    ctx.x_limbs(dev(x), xl, k)
+    ys = [empty(r, torch.float32) for r in rows]
+    ctx.gemv_q4_0_limbs([dev(w) for w in ws], ys, list(rows), xl, k)
+    torch.cuda.synchronize()
+    for w, y, r in zip(ws, ys, rows):
+        _check(oracle, w, x, host(y), r, k)
+
+
+def test_gemv_limbs_softcap_and_same_bits_as_plain(ctx, oracle):
+    """softcap applies cap*tanh(v/cap) (the tied LM head, graph.rs:740-756);
+    without it the limbs entry gives the very bits of sgq_gemv_q4_0."""
+    k, n, cap = 5376, 4096, 0.5
+    rng = oracle.Rng(0x50F7)
+    w = rng.random_q4_0(n * k // 32)
+    x = oracle.through_f16(rng.f32_vec(k))
+    tw, tx = dev(w), dev(x)
+    xl = empty(k // 32 * ctx.X_LIMBS_BYTES_PER_BLOCK, torch.uint8)
+    ctx.x_limbs(tx, xl, k)
+    plain, lim, capped = (empty(n, torch.float32) for _ in range(3))
+    ctx.gemv_q4_0(tw, tx, plain, n, k)
+    ctx.gemv_q4_0_limbs([tw], [lim], [n], xl, k)
+    ctx.gemv_q4_0_limbs([tw], [capped], [n], xl, k, softcap=cap)
+    torch.cuda.synchronize()
+    p, l, c = host(plain), host(lim), host(capped)
+    assert np.array_equal(p.view(np.uint32), l.view(np.uint32))
+    want = cap * np.tanh(p.astype(np.float64) / cap)
+    assert np.abs(c - want).max() <= 1e-6 * cap
+    assert np.abs(c).max() <= cap
+
+
+def test_gemv_limbs_rejects_bad_shapes(ctx):
+    import sgq
+
+    xl = empty(64 * 80, torch.uint8)
+    w = empty(64 * 18 * 8, torch.uint8)
+    y = empty(64, torch.float32)
+    with pytest.raises(sgq.ValidationError):
+        ctx.gemv_q4_0_limbs([w], [y], [8], xl, 96)    # k % 256 != 0
+    with pytest.raises(sgq.ValidationError):
+        ctx.gemv_q4_0_limbs([w] * 5, [y] * 5, [1] * 5, xl, 256)  # > 4 targets
+    with pytest.raises(sgq.ValidationError):
+        ctx.x_limbs(empty(100, torch.float32), xl, 100)  # k % 32 != 0
