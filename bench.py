@@ -13,6 +13,10 @@ batch of synthetic input, already resident in HBM:
           its weights from HBM.
   mmq     BASELINE config 2: Q4_0×Q8 int8-MFMA GEMM M=512, K=5376, N=21504.
   splitk  BASELINE config 3: down-proj M=2048, K=21504, N=5376, split-K 4.
+  attn_prefill, attn_prefill_sliding
+          BASELINE config 4 prefill: 4096 queries, causal / sliding-1024.
+  attn_decode_4k, attn_decode_32k, attn_decode_128k
+          BASELINE config 4 decode over a 4K / 32K / 128K Q8_0 context.
 
 The timed region is bracketed by torch.cuda.synchronize() and measured with
 HIP events on the stream the kernels run on.  The cpu_baseline leg times the
@@ -110,6 +114,96 @@ class Mmq:
                          "unit": "TOP/s", "frac": tops / INT8_PEAK_TOPS, "traffic": None},
             "config": {"workload": self.name, "m": self.m, "k": self.k, "n": self.n,
                        "split_k": self.split, "ops_per_launch": self.ops},
+        }
+
+
+F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+class AttnPrefill:
+    """BASELINE config 4 prefill: 4096 queries, 32 q / 16 kv heads, hd 128,
+    causal (window 0) or sliding-1024, over a Q8_0 cache of N(0,1) K/V."""
+    kernel = "attn_prefill_kernel"
+
+    def __init__(self, ctx, torch, window=0, n_tok=4096):
+        self.ctx, self.torch, self.window, self.n_tok = ctx, torch, window, n_tok
+        n_q, n_kv, hd = 32, 16, 128
+        self.n_q, self.n_kv = n_q, n_kv
+        kv = torch.empty(n_tok * n_kv * hd, dtype=torch.float32, device="cuda")
+        self.kq = torch.empty(kv.numel(), dtype=torch.int8, device="cuda")
+        self.vq = torch.empty(kv.numel(), dtype=torch.int8, device="cuda")
+        self.ks = torch.empty(kv.numel() // 32, dtype=torch.int16, device="cuda")
+        self.vs = torch.empty(kv.numel() // 32, dtype=torch.int16, device="cuda")
+        ctx.fill_normal(kv, seed=41)
+        ctx.quant_q8_0(kv, self.ks, self.kq)
+        ctx.fill_normal(kv, seed=42)
+        ctx.quant_q8_0(kv, self.vs, self.vq)
+        self.q = torch.empty(n_tok * n_q * hd, dtype=torch.float32, device="cuda")
+        ctx.fill_normal(self.q, seed=43)
+        self.out = torch.empty_like(self.q)
+        pairs = sum(min(i + 1, window) if window else i + 1 for i in range(n_tok))
+        self.flops = 4.0 * hd * n_q * pairs  # QK^T and PV, 2 flops per MAC
+        self.name = (f"attn_prefill_q8 {n_tok} queries, 32q/16kv, hd 128, "
+                     f"{'sliding-%d' % window if window else 'causal'} (BASELINE config 4)")
+
+    def step(self, i):
+        self.ctx.attn_prefill_q8(self.q, self.kq, self.ks, self.vq, self.vs, self.n_tok, 0,
+                                 self.n_q, self.n_kv, self.out, window=self.window)
+
+    def result(self, ms_per_step):
+        tf = self.flops / (ms_per_step * 1e-3) / 1e12
+        return {
+            "value": tf, "unit": "TFLOP/s", "dtype": "f16 MFMA (K/V dequantized from Q8_0), fp32 acc",
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tf / F16_PEAK_TFLOPS, "traffic": None},
+            "config": {"workload": self.name, "flops_per_launch": self.flops},
+        }
+
+
+class AttnDecode:
+    """BASELINE config 4 decode: bs 1, 32 q / 16 kv heads, hd 128, Q8_0 K/V
+    over a context of `ctx_len` (4K/32K/128K), split over the sequence."""
+    kernel = "attn_decode_q8_kernel"
+
+    def __init__(self, ctx, torch, ctx_len=32768):
+        self.ctx, self.torch, self.ctx_len = ctx, torch, ctx_len
+        n_q, n_kv, hd = 32, 16, 128
+        self.n_q, self.n_kv = n_q, n_kv
+        # rotate copies so the KV pages stream from HBM (>= 512 MB in total)
+        self.copies = max(1, (512 << 20) // (ctx_len * 4352))
+        kv = torch.empty(ctx_len * n_kv * hd, dtype=torch.float32, device="cuda")
+        self.pages = []
+        for c in range(self.copies):
+            kq = torch.empty(kv.numel(), dtype=torch.int8, device="cuda")
+            vq = torch.empty(kv.numel(), dtype=torch.int8, device="cuda")
+            ks = torch.empty(kv.numel() // 32, dtype=torch.int16, device="cuda")
+            vs = torch.empty(kv.numel() // 32, dtype=torch.int16, device="cuda")
+            ctx.fill_normal(kv, seed=50 + 2 * c)
+            ctx.quant_q8_0(kv, ks, kq)
+            ctx.fill_normal(kv, seed=51 + 2 * c)
+            ctx.quant_q8_0(kv, vs, vq)
+            self.pages.append((kq, ks, vq, vs))
+        del kv
+        self.q = torch.empty(n_q * hd, dtype=torch.float32, device="cuda")
+        ctx.fill_normal(self.q, seed=52)
+        self.out = torch.empty_like(self.q)
+        self.splits = min(1024, max(16, ctx_len // 512))
+        self.bytes = ctx_len * n_kv * (2 * hd + 2 * (hd // 32) * 2) + 2 * n_q * hd * 4
+
+    def step(self, i):
+        kq, ks, vq, vs = self.pages[i % self.copies]
+        self.ctx.attn_decode_q8(self.q, kq, ks, vq, vs, self.ctx_len, self.n_q, self.n_kv,
+                                self.out, n_splits=self.splits, scale=1.0)
+
+    def result(self, ms_per_step):
+        gbs = self.bytes / (ms_per_step * 1e-3) / 1e9
+        return {
+            "value": gbs, "unit": "GB/s", "dtype": "q8_0 K/V, fp32 q/out",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "config": {"workload": f"attn_decode_q8 ctx {self.ctx_len}, 32q/16kv, hd 128, "
+                                   f"{self.splits} splits, {self.copies} rotating caches "
+                                   "(BASELINE config 4)", "bytes_per_launch": self.bytes},
         }
 
 
@@ -253,7 +347,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "mmq", "splitk"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "gemv", "mmq", "splitk", "attn_prefill",
+                             "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
+                             "attn_decode_128k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -275,6 +372,12 @@ def main():
         wl = Gemv(ctx, torch)
     elif args.workload == "mmq":
         wl = Mmq(ctx, torch)
+    elif args.workload == "attn_prefill":
+        wl = AttnPrefill(ctx, torch)
+    elif args.workload == "attn_prefill_sliding":
+        wl = AttnPrefill(ctx, torch, window=1024)
+    elif args.workload.startswith("attn_decode_"):
+        wl = AttnDecode(ctx, torch, {"4k": 4096, "32k": 32768, "128k": 131072}[args.workload[12:]])
     else:
         wl = Mmq(ctx, torch, m=2048, k=21504, n=5376, split=4, label="BASELINE config 3")
     torch.cuda.synchronize()

@@ -177,6 +177,20 @@ int sgq_attn_decode_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
                        uint32_t kv_len, uint32_t n_q_heads, uint32_t n_kv_heads,
                        uint32_t head_dim, uint32_t n_splits, float scale, float *out);
 
+/* Prefill flash attention over a Q8_0 KV cache (attn_prefill_global_flash_*
+ * and attn_prefill_sliding_ring, crates/sg-gpu/shaders/
+ * attn_prefill_global_flash_sp_q8.wgsl:65-183): q [n_tokens × n_q_heads ×
+ * head_dim] fp32 for positions q0..q0+n_tokens-1; the cache is linear
+ * (slot = position) and must hold positions 0..q0+n_tokens-1 (the chunk's
+ * own K/V included).  Query at position p attends keys k <= p, and with
+ * window > 0 only k > p - window.  K/V are dequantized to f16 and P is
+ * rounded to f16 as in the reference; accumulation fp32.  head_dim 128;
+ * out [n_tokens × n_q_heads × head_dim] fp32. */
+int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
+                        const uint16_t *k_scales, const int8_t *v_quants, const uint16_t *v_scales,
+                        uint32_t n_tokens, uint32_t q0, uint32_t n_q_heads, uint32_t n_kv_heads,
+                        uint32_t head_dim, uint32_t window, float scale, float *out);
+
 /* ---- decode-step driver ------------------------------------------------- */
 /* A random-init decoder of the reference's model family (the CPU forward pass
  * crates/sg-model/src/reference.rs:157-316 and the GPU graph

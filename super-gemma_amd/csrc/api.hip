@@ -523,6 +523,19 @@ int sgq_gemv_q4_0_limbs(sgq_ctx *ctx, uint32_t n_targets, const void *const *w, 
     return launch_gemv_limbs(ctx->stream, tg, x_limbs, k);
 }
 
+int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
+                        const uint16_t *k_scales, const int8_t *v_quants, const uint16_t *v_scales,
+                        uint32_t n_tokens, uint32_t q0, uint32_t n_q_heads, uint32_t n_kv_heads,
+                        uint32_t head_dim, uint32_t window, float scale, float *out) {
+    if (!ctx || !q || !k_quants || !k_scales || !v_quants || !v_scales || !out)
+        return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_CHECK(n_tokens < (1u << 30) && q0 < (1u << 30) && window < (1u << 30),
+              "attn_prefill_q8: size out of range");
+    return launch_attn_prefill_q8(ctx->stream, q, k_quants, k_scales, v_quants, v_scales, out,
+                                  (int)n_tokens, (int)q0, (int)n_q_heads, (int)n_kv_heads,
+                                  (int)head_dim, (int)window, scale);
+}
+
 int sgq_quant_q8_0(sgq_ctx *ctx, const float *x, uint16_t *scales, int8_t *quants, uint64_t n) {
     if (!ctx || (n && (!x || !scales || !quants))) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     return launch_quant_q8_0(ctx->stream, x, scales, quants, n);

@@ -1,0 +1,209 @@
+// Prefill flash attention over a Q8_0 KV cache for gfx950 (causal, optional
+// sliding window).
+//
+// Semantics: attn_prefill_global_flash_* / attn_prefill_sliding_ring
+// (crates/sg-gpu/shaders/attn_prefill_global_flash_sp_q8.wgsl:65-183,
+// attn_prefill_sliding_ring.wgsl:53-152): query i of the chunk sits at
+// position q0+i and attends keys p with p <= q0+i and, with a window W,
+// p > q0+i-W; out = softmax(scale · q·kᵀ)·v per query head, GQA head h
+// reading kv head h/(n_q/n_kv).  K and V come from the Q8_0 pages
+// (int8 [slot × n_kv × 128] + f16 scales per 32) of a linear cache
+// (slot = position) and are dequantized to f16 as in the reference's
+// _sp_q8 variant; P is rounded to f16 for PV, as in the reference.
+//
+// Design (MFMA-bound: 4·hd flops per query-key pair against 2·hd·1 B of
+// K/V per key per query tile):
+//  * Workgroup = 4 waves = 128 queries of one query head; tiles of 64 keys.
+//    K and V of a tile are dequantized once into LDS (K as [key][dim],
+//    V transposed as [dim][key], rows padded) and used by all 128 queries.
+//  * Each wave computes Sᵀ = K·Qᵀ for its 32 queries with
+//    v_mfma_f32_32x32x16_f16 (8 per 32 keys): in that layout lane l owns
+//    query column l%32, so the online softmax needs one cross-half shuffle,
+//    and the probabilities are already in the B-operand layout of
+//    Oᵀ = Vᵀ·Pᵀ (4 dim blocks × 2 key chunks of 16 per 32 keys) — no LDS
+//    round trip for P.  Oᵀ stays in registers (4 × 16 fp32 per lane).
+//  * Causal: tiles run heaviest-first (last query tile first).
+#include "sgq_internal.h"
+
+namespace sgq {
+namespace {
+
+constexpr int kHD = 128;
+constexpr int kQT = 128;           // queries per workgroup (4 waves × 32)
+constexpr int kKT = 64;            // keys per tile
+constexpr int kKRow = kHD + 8;     // K tile row in LDS (f16), padded
+constexpr int kVRow = kKT + 8;     // Vᵀ tile row in LDS (f16), padded
+constexpr float kNegBig = -3.0e38f;
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void attn_prefill_kernel(
+    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
+    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs, float *__restrict__ out,
+    int n_tok, int q0, int n_q, int n_kv, int window, float scale, int qtiles) {
+    __shared__ __align__(16) _Float16 k_s[kKT][kKRow];
+    __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
+
+    const int tile = qtiles - 1 - (int)blockIdx.x;  // heaviest (latest) query tile first
+    const int qh = blockIdx.y, kvh = qh / (n_q / n_kv);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    // this lane's query (column l32 of the wave's 32) and its Qᵀ operand:
+    // dims 16c + 8hh .. +7 for c = 0..7, as f16
+    const int my_q = tile * kQT + wave * 32 + l32;
+    const bool q_valid = my_q < n_tok;
+    const int qp = q0 + my_q;  // its position
+    h8 qb[8];
+    {
+        const float *qr = q + ((size_t)(q_valid ? my_q : 0) * n_q + qh) * kHD + 8 * hh;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 a = *reinterpret_cast<const float4 *>(qr + 16 * c);
+            const float4 b = *reinterpret_cast<const float4 *>(qr + 16 * c + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] : 0.f);
+        }
+    }
+    f32x16 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[d][i] = 0.f;
+    float m_run = kNegBig, l_run = 0.f;
+
+    const int qpos_lo = q0 + tile * kQT;
+    const int qpos_hi = q0 + min((tile + 1) * kQT, n_tok) - 1;
+    const int k_lo = window > 0 ? max(0, qpos_lo + 1 - window) : 0;
+    const int k_hi = qpos_hi;
+
+    for (int kb = k_lo; kb <= k_hi; kb += kKT) {
+        __syncthreads();  // the previous tile's LDS reads are done
+        {   // dequantize K and V of keys kb..kb+63: thread -> (key t/4, 32-block t%4)
+            const int kk = tid >> 2, blk = tid & 3;
+            const int key = kb + kk;
+            _Float16 kv[32], vv[32];
+            if (key <= k_hi) {
+                const size_t row = (size_t)key * n_kv + kvh;
+                const i32x4 *kp = reinterpret_cast<const i32x4 *>(kq + row * kHD + 32 * blk);
+                const i32x4 *vp = reinterpret_cast<const i32x4 *>(vq + row * kHD + 32 * blk);
+                const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+                const float sk = f16_bits_to_f32(ks[row * (kHD / 32) + blk]);
+                const float sv = f16_bits_to_f32(vs[row * (kHD / 32) + blk]);
+                const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                for (int w = 0; w < 8; w++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        kv[4 * w + b] = (_Float16)(sk * (float)(int8_t)((kw[w] >> (8 * b)) & 0xff));
+                        vv[4 * w + b] = (_Float16)(sv * (float)(int8_t)((vw[w] >> (8 * b)) & 0xff));
+                    }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 32; j++) kv[j] = vv[j] = (_Float16)0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                h8 t;
+#pragma unroll
+                for (int e = 0; e < 8; e++) t[e] = kv[8 * j + e];
+                *reinterpret_cast<h8 *>(&k_s[kk][32 * blk + 8 * j]) = t;
+            }
+#pragma unroll
+            for (int j = 0; j < 32; j++) vt_s[32 * blk + j][kk] = vv[j];
+        }
+        __syncthreads();
+
+        // Sᵀ = K·Qᵀ for the tile's two 32-key halves
+        f32x16 s[2];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) s[t2][i] = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const h8 a = *reinterpret_cast<const h8 *>(&k_s[32 * t2 + l32][16 * c + 8 * hh]);
+                s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], s[t2], 0, 0, 0);
+            }
+        }
+        // mask, scale and the online softmax for this lane's query
+        float mx = m_run;
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = kb + 32 * t2 + 8 * (i / 4) + 4 * hh + (i % 4);
+                const bool ok = q_valid && key <= qp && (window <= 0 || key > qp - window);
+                const float v = ok ? s[t2][i] * scale : kNegBig;
+                s[t2][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float corr = __expf(m_run - mx);
+        float rs = 0.f;
+        h8 pb[2][2];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float v = s[t2][i];
+                const float p = v > kNegBig ? __expf(v - mx) : 0.f;
+                rs += p;
+                pb[t2][i / 8][i % 8] = (_Float16)p;
+            }
+        rs += __shfl_xor(rs, 32, kWave);
+        l_run = l_run * corr + rs;
+        m_run = mx;
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[d][i] *= corr;
+        // Oᵀ += Vᵀ·Pᵀ: key chunk (t2, half) = keys 32t2 + 16half + {4hh..+3, 8+4hh..+3}
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const _Float16 *vr = &vt_s[32 * d + l32][32 * t2 + 16 * half + 4 * hh];
+                    const h4 lo = *reinterpret_cast<const h4 *>(vr);
+                    const h4 hi = *reinterpret_cast<const h4 *>(vr + 8);
+                    const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t2][half], o[d], 0, 0, 0);
+                }
+    }
+
+    if (!q_valid) return;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    float *orow = out + ((size_t)my_q * n_q + qh) * kHD;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) orow[32 * d + 8 * (i / 4) + 4 * hh + (i % 4)] = o[d][i] * inv;
+}
+
+}  // namespace
+
+int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
+                           const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
+                           int n_q, int n_kv, int head_dim, int window, float scale) {
+    SGQ_CHECK(head_dim == kHD, "attn_prefill_q8: head_dim %d unsupported (128)", head_dim);
+    SGQ_CHECK(n_tok > 0 && q0 >= 0, "attn_prefill_q8: n_tok %d, q0 %d", n_tok, q0);
+    SGQ_CHECK(n_kv > 0 && n_q > 0 && n_q % n_kv == 0, "attn_prefill_q8: n_q %% n_kv != 0");
+    SGQ_CHECK(window >= 0, "attn_prefill_q8: negative window");
+    SGQ_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 &&
+                  ((uintptr_t)ks & 1) == 0 && ((uintptr_t)vs & 1) == 0,
+              "attn_prefill_q8: misaligned operand");
+    const int qtiles = (n_tok + kQT - 1) / kQT;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(qtiles, n_q), dim3(256), 0, st, q, kq, ks, vq, vs,
+                       out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+}  // namespace sgq

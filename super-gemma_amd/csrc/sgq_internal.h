@@ -98,6 +98,9 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                              uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
                              int n_q, int n_kv, int n_splits, float scale, float *out,
                              void *workspace, size_t workspace_bytes, void *limbs_out);
+int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
+                           const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
+                           int n_q, int n_kv, int head_dim, int window, float scale);
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);

@@ -116,6 +116,7 @@ SIGNATURES = {
     "sgq_x_limbs": (I, [P, P, P, U32]),
     "sgq_gemv_q4_0_limbs": (I, [P, U32, C.POINTER(P), C.POINTER(P), C.POINTER(U32), P, U32,
                                 C.c_float]),
+    "sgq_attn_prefill_q8": (I, [P, P, P, P, P, P, U32, U32, U32, U32, U32, U32, C.c_float, P]),
     "sgq_quant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_dequant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_gemm_q4_0_q8": (I, [P, P, P, P, P, U32, U32, U32, U32, P]),
@@ -334,6 +335,22 @@ class GpuContext:
             scale = 1.0 / head_dim ** 0.5
         _check(lib().sgq_attn_decode_q8(self._h, _ptr(q), _ptr(kq), _ptr(ks), _ptr(vq), _ptr(vs),
                                         kv_len, n_q, n_kv, head_dim, n_splits, scale, _ptr(out)))
+
+    def attn_prefill_q8(self, q, kq, ks, vq, vs, n_tok, q0, n_q, n_kv, out, window=0,
+                        scale=None, head_dim=128):
+        """Prefill attention for positions q0..q0+n_tok-1 over a linear Q8_0
+        cache holding positions 0..q0+n_tok-1."""
+        n_slots = q0 + n_tok
+        _need(q, torch.float32, n_tok * n_q * head_dim, "q")
+        _need(out, torch.float32, n_tok * n_q * head_dim, "out")
+        _need(kq, torch.int8, n_slots * n_kv * head_dim, "k_quants")
+        _need(vq, torch.int8, n_slots * n_kv * head_dim, "v_quants")
+        _need(ks, (torch.uint16, torch.int16, torch.float16), n_slots * n_kv * head_dim // 32, "k_scales")
+        _need(vs, (torch.uint16, torch.int16, torch.float16), n_slots * n_kv * head_dim // 32, "v_scales")
+        if scale is None:
+            scale = 1.0 / head_dim ** 0.5
+        _check(lib().sgq_attn_prefill_q8(self._h, _ptr(q), _ptr(kq), _ptr(ks), _ptr(vq), _ptr(vs),
+                                         n_tok, q0, n_q, n_kv, head_dim, window, scale, _ptr(out)))
 
     def fill_q4_0_random(self, w: torch.Tensor, n_blocks: int, seed: int, sigma: float = 0.02):
         _need(w, torch.uint8, n_blocks * 18, "w")
