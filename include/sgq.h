@@ -191,6 +191,25 @@ int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
                         uint32_t n_tokens, uint32_t q0, uint32_t n_q_heads, uint32_t n_kv_heads,
                         uint32_t head_dim, uint32_t window, float scale, float *out);
 
+/* Row and elementwise operators (fp32 activations; f32 math as in the
+ * reference shaders).  Name dispatch: rmsnorm_{ROW}[_plus1] (bindings x, w,
+ * y; groups [rows]), rope_{sliding,global}_{q,k} and the head_dim-128 forms
+ * rope_hd128_{sliding,global}_{q,k} (bindings xs, cos_sin), geglu (gate,
+ * up, y), add_scaled (a, b, y; push f32 scale). */
+/* rmsnorm.wgsl:24-61: y = x·rsqrt(mean(x²)+eps)·w per row of row_len
+ * (w + 1 when plus_one; w NULL = weightless). */
+int sgq_rmsnorm(sgq_ctx *ctx, const float *x, const float *w, float *y, uint32_t rows,
+                uint32_t row_len, int plus_one, float eps);
+/* rope.wgsl:35-52, in place: rows [n_tokens × n_heads × head_dim]; pair i
+ * couples dims (i, i+head_dim/2), the first rot_dims/2 pairs rotate by
+ * cos_sin[token × rot_dims/2] (cos, sin) (crates/sg-model/src/rope.rs). */
+int sgq_rope(sgq_ctx *ctx, float *x, const float *cos_sin, uint64_t n_tokens, uint32_t n_heads,
+             uint32_t head_dim, uint32_t rot_dims);
+/* geglu.wgsl:14-24: y = gelu_tanh(gate)·up. */
+int sgq_geglu(sgq_ctx *ctx, const float *gate, const float *up, float *y, uint64_t n);
+/* add_scaled.wgsl:21-27: y = (a + b)·s. */
+int sgq_add_scaled(sgq_ctx *ctx, const float *a, const float *b, float *y, uint64_t n, float s);
+
 /* ---- decode-step driver ------------------------------------------------- */
 /* A random-init decoder of the reference's model family (the CPU forward pass
  * crates/sg-model/src/reference.rs:157-316 and the GPU graph

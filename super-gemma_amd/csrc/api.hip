@@ -80,6 +80,10 @@ enum class Kind {
     GemmI8,        // gemm_q4_0_i8_*_k{K}_n{N}: groups [M/64, N/16]
     GemmI8Down,    // gemm_q4_0_i8_bb_pfd{1,2,4}: K=21504, N=5376, groups [M/64, 336]
     GemmI8Split,   // gemm_q4_0_i8_splitk{S}_k{K}_n{N} (no reference counterpart)
+    RmsNorm,       // rmsnorm_{ROW}[_plus1]: groups [rows]
+    Rope,          // rope_{sliding,global}_{q,k} (+ head_dim-128 forms)
+    Geglu,         // geglu
+    AddScaled,     // add_scaled (push: f32 scale)
 };
 
 struct sgq_kernel {
@@ -104,6 +108,27 @@ const char *const kNames[] = {
     "gemm_q4_0_i8_swz_m4n1_k8192_n5376",    "gemm_q4_0_i8_swz_m4n1_k16384_n5376",
     "gemm_q4_0_i8_swz_m4n1_k4096_n5376",    "gemm_q4_0_i8_bb_pfd4",
     "gemm_q4_0_i8_splitk4_k21504_n5376",
+    "rmsnorm_5376", "rmsnorm_5376_plus1", "rmsnorm_512", "rmsnorm_512_plus1",
+    "rmsnorm_256",  "rmsnorm_256_plus1",  "rmsnorm_128", "rmsnorm_128_plus1",
+    "rope_sliding_q", "rope_sliding_k", "rope_global_q", "rope_global_k",
+    "rope_hd128_sliding_q", "rope_hd128_sliding_k", "rope_hd128_global_q", "rope_hd128_global_k",
+    "geglu", "add_scaled",
+};
+
+// RoPE variants: (name, head_dim, rot_dims, n_heads).  The first four are
+// the reference's (crates/sg-gpu/build.rs:126-164: the real checkpoint's
+// head_dim 256 sliding / 512 global with partial rotation 0.25); the
+// hd128 forms, which have no counterpart in the reference, are the
+// benchmark decoder's (32 q / 16 kv heads of 128).
+struct RopeVariant {
+    const char *name;
+    uint32_t head_dim, rot_dims, n_heads;
+};
+const RopeVariant kRope[] = {
+    {"rope_sliding_q", 256, 256, 32}, {"rope_sliding_k", 256, 256, 16},
+    {"rope_global_q", 512, 128, 32},  {"rope_global_k", 512, 128, 4},
+    {"rope_hd128_sliding_q", 128, 128, 32}, {"rope_hd128_sliding_k", 128, 128, 16},
+    {"rope_hd128_global_q", 128, 32, 32},   {"rope_hd128_global_k", 128, 32, 16},
 };
 
 bool parse_u32_after(const std::string &s, const std::string &key, uint32_t *out) {
@@ -166,6 +191,33 @@ bool resolve(const std::string &name, sgq_kernel *k) {
             return false;
         return (k->param == 1 || k->param == 2 || k->param == 4 || k->param == 8) &&
                k->k % 64 == 0 && k->n > 0;
+    }
+    if (starts_with(name, "rmsnorm_")) {
+        k->kind = Kind::RmsNorm;
+        k->info = {{256, 1, 1}, 3, 0, 0};
+        if (!parse_u32_after(name, "rmsnorm_", &k->k) || k->k == 0) return false;
+        const std::string base = "rmsnorm_" + std::to_string(k->k);
+        k->param = name == base + "_plus1";
+        return name == base || k->param;
+    }
+    for (const RopeVariant &v : kRope)
+        if (name == v.name) {
+            k->kind = Kind::Rope;
+            k->info = {{256, 1, 1}, 2, 0, 0};
+            k->k = v.head_dim;
+            k->n = v.n_heads;
+            k->param = v.rot_dims;
+            return true;
+        }
+    if (name == "geglu") {
+        k->kind = Kind::Geglu;
+        k->info = {{256, 1, 1}, 3, 0, 0};
+        return true;
+    }
+    if (name == "add_scaled") {
+        k->kind = Kind::AddScaled;
+        k->info = {{256, 1, 1}, 3, 4, 0};
+        return true;
     }
     if (starts_with(name, "gemm_q4_0_i8_")) {
         k->kind = Kind::GemmI8;
@@ -346,6 +398,46 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                 return fail(SGQ_ERR_VALIDATION, "%s: y binding too small", kernel->name.c_str());
             return launch_gemv_q4_0(st, p0, static_cast<const float *>(p1), static_cast<float *>(p2),
                                     n, k, ctx->workspace);
+        }
+        case Kind::RmsNorm: {
+            // bindings: 0 x, 1 w, 2 y; one workgroup per row (groups[0] rows)
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            const uint64_t need = (uint64_t)groups[0] * kernel->k * 4;
+            if ((r0 && r0 < need) || (r2 && r2 < need) || (r1 && r1 < (uint64_t)kernel->k * 4))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            return launch_rmsnorm(st, static_cast<const float *>(p0), static_cast<const float *>(p1),
+                                  static_cast<float *>(p2), groups[0], kernel->k, (int)kernel->param,
+                                  1e-6f);
+        }
+        case Kind::Rope: {
+            // bindings: 0 xs (in place) [token × n_heads × head_dim], 1 cos_sin
+            // [token × rot/2] (cos, sin); pairs = arrayLength(xs)/head_dim·rot/2
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1))) return rc;
+            if (!r0) return fail(SGQ_ERR_VALIDATION, "%s: xs range required", kernel->name.c_str());
+            const uint64_t rows = r0 / 4 / kernel->k;
+            const uint64_t tokens = (rows + kernel->n - 1) / kernel->n;
+            if (r1 && r1 < tokens * (kernel->param / 2) * 8)
+                return fail(SGQ_ERR_VALIDATION, "%s: cos_sin binding too small", kernel->name.c_str());
+            return launch_rope(st, static_cast<float *>(p0), static_cast<const float *>(p1), rows,
+                               kernel->k, kernel->param, kernel->n);
+        }
+        case Kind::Geglu:
+        case Kind::AddScaled: {
+            // bindings: 0 a (gate), 1 b (up), 2 y; elements = arrayLength(y)
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            if (!r2) return fail(SGQ_ERR_VALIDATION, "%s: y range required", kernel->name.c_str());
+            const uint64_t n = r2 / 4;
+            if ((r0 && r0 < n * 4) || (r1 && r1 < n * 4))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            if (kernel->kind == Kind::Geglu)
+                return launch_geglu(st, static_cast<const float *>(p0), static_cast<const float *>(p1),
+                                    static_cast<float *>(p2), n);
+            float sc;
+            std::memcpy(&sc, push, 4);
+            return launch_add_scaled(st, static_cast<const float *>(p0),
+                                     static_cast<const float *>(p1), static_cast<float *>(p2), n, sc);
         }
         case Kind::QuantQ8: {
             // bindings: 0 src fp32, 1 scales f16, 2 quants; blocks = arrayLength(src)/32
@@ -534,6 +626,28 @@ int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
     return launch_attn_prefill_q8(ctx->stream, q, k_quants, k_scales, v_quants, v_scales, out,
                                   (int)n_tokens, (int)q0, (int)n_q_heads, (int)n_kv_heads,
                                   (int)head_dim, (int)window, scale);
+}
+
+int sgq_rmsnorm(sgq_ctx *ctx, const float *x, const float *w, float *y, uint32_t rows,
+                uint32_t row_len, int plus_one, float eps) {
+    if (!ctx || !x || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_rmsnorm(ctx->stream, x, w, y, rows, row_len, plus_one, eps);
+}
+
+int sgq_rope(sgq_ctx *ctx, float *x, const float *cos_sin, uint64_t n_tokens, uint32_t n_heads,
+             uint32_t head_dim, uint32_t rot_dims) {
+    if (!ctx || !x || !cos_sin) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_rope(ctx->stream, x, cos_sin, n_tokens * n_heads, head_dim, rot_dims, n_heads);
+}
+
+int sgq_geglu(sgq_ctx *ctx, const float *gate, const float *up, float *y, uint64_t n) {
+    if (!ctx || !gate || !up || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_geglu(ctx->stream, gate, up, y, n);
+}
+
+int sgq_add_scaled(sgq_ctx *ctx, const float *a, const float *b, float *y, uint64_t n, float s) {
+    if (!ctx || !a || !b || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_add_scaled(ctx->stream, a, b, y, n, s);
 }
 
 int sgq_quant_q8_0(sgq_ctx *ctx, const float *x, uint16_t *scales, int8_t *quants, uint64_t n) {

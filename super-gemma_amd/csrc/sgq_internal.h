@@ -101,6 +101,13 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
 int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
                            const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
                            int n_q, int n_kv, int head_dim, int window, float scale);
+int launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *y, uint32_t rows,
+                   uint32_t row_len, int plus_one, float eps);
+int launch_rope(hipStream_t st, float *xs, const float *cos_sin, uint64_t rows, uint32_t head_dim,
+                uint32_t rot_dims, uint32_t n_heads);
+int launch_geglu(hipStream_t st, const float *g, const float *u, float *y, uint64_t n);
+int launch_add_scaled(hipStream_t st, const float *a, const float *b, float *y, uint64_t n,
+                      float s);
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);

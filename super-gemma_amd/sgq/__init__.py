@@ -117,6 +117,10 @@ SIGNATURES = {
     "sgq_gemv_q4_0_limbs": (I, [P, U32, C.POINTER(P), C.POINTER(P), C.POINTER(U32), P, U32,
                                 C.c_float]),
     "sgq_attn_prefill_q8": (I, [P, P, P, P, P, P, U32, U32, U32, U32, U32, U32, C.c_float, P]),
+    "sgq_rmsnorm": (I, [P, P, P, P, U32, U32, I, C.c_float]),
+    "sgq_rope": (I, [P, P, P, U64, U32, U32, U32]),
+    "sgq_geglu": (I, [P, P, P, P, U64]),
+    "sgq_add_scaled": (I, [P, P, P, P, U64, C.c_float]),
     "sgq_quant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_dequant_q8_0": (I, [P, P, P, P, U64]),
     "sgq_gemm_q4_0_q8": (I, [P, P, P, P, P, U32, U32, U32, U32, P]),
@@ -351,6 +355,32 @@ class GpuContext:
             scale = 1.0 / head_dim ** 0.5
         _check(lib().sgq_attn_prefill_q8(self._h, _ptr(q), _ptr(kq), _ptr(ks), _ptr(vq), _ptr(vs),
                                          n_tok, q0, n_q, n_kv, head_dim, window, scale, _ptr(out)))
+
+    def rmsnorm(self, x, w, y, rows, row_len, plus_one=False, eps=1e-6):
+        _need(x, torch.float32, rows * row_len, "x")
+        _need(y, torch.float32, rows * row_len, "y")
+        if w is not None:
+            _need(w, torch.float32, row_len, "w")
+        _check(lib().sgq_rmsnorm(self._h, _ptr(x), _ptr(w), _ptr(y), rows, row_len,
+                                 int(plus_one), eps))
+
+    def rope(self, x, cos_sin, n_tokens, n_heads, head_dim, rot_dims):
+        _need(x, torch.float32, n_tokens * n_heads * head_dim, "x")
+        _need(cos_sin, torch.float32, n_tokens * rot_dims, "cos_sin")
+        _check(lib().sgq_rope(self._h, _ptr(x), _ptr(cos_sin), n_tokens, n_heads, head_dim,
+                              rot_dims))
+
+    def geglu(self, g, u, y):
+        n = y.numel()
+        _need(g, torch.float32, n, "gate")
+        _need(u, torch.float32, n, "up")
+        _check(lib().sgq_geglu(self._h, _ptr(g), _ptr(u), _ptr(y), n))
+
+    def add_scaled(self, a, b, y, s):
+        n = y.numel()
+        _need(a, torch.float32, n, "a")
+        _need(b, torch.float32, n, "b")
+        _check(lib().sgq_add_scaled(self._h, _ptr(a), _ptr(b), _ptr(y), n, s))
 
     def fill_q4_0_random(self, w: torch.Tensor, n_blocks: int, seed: int, sigma: float = 0.02):
         _need(w, torch.uint8, n_blocks * 18, "w")

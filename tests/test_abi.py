@@ -57,7 +57,15 @@ def test_registry_names_resolve_without_device():
         info = sgq._Info()
         rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
         assert rc == 0, (n, L.sgq_last_error())
-        assert info.bindings >= 3
+        assert info.bindings >= 2
+    # binding / push layouts of the reference's variants (crates/sg-gpu/build.rs:64-190)
+    want = {"rmsnorm_5376": (3, 0, 256), "rmsnorm_256_plus1": (3, 0, 256),
+            "rope_sliding_q": (2, 0, 256), "rope_global_k": (2, 0, 256),
+            "geglu": (3, 0, 256), "add_scaled": (3, 4, 256)}
+    for n, (nb, pb, wg) in want.items():
+        info = sgq._Info()
+        assert L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info)) == 0
+        assert (info.bindings, info.push_bytes, info.workgroup[0]) == (nb, pb, wg), n
     rc = L.sgq_kernel_lookup(None, b"gemv_q6_k_logits_nonexistent", C.byref(h), C.byref(info))
     assert rc == 4 and b"unknown kernel" in L.sgq_last_error()
 
