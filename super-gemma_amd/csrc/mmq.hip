@@ -18,8 +18,13 @@
 //    LDS, rows padded to 144 B so the 16-byte fragment reads of 8 lanes hit
 //    32 distinct banks.  Double-buffered: stage s+1's global loads are in
 //    flight while stage s computes; one barrier per stage.
-//  * Rescale on the VALU: per output element and block, one cvt, one
-//    multiply (d_a·d_w), one FMA.  That — not the MFMA — bounds the kernel.
+//  * Rescale: the scale products d_a·d_w of a 32×32 tile come from the
+//    matrix cores too — one v_mfma_f32_32x32x16_f16 whose only non-zero K
+//    term is (d_a[row], d_w[col]) gives the exact outer product (f16·f16 is
+//    exact in f32) in the accumulator layout of the int8 MFMA.  The VALU is
+//    left with one cvt and one FMA per output element and block, and that —
+//    not the MFMA — still bounds the kernel (a wave64 VALU op costs 4
+//    cycles against 32 for an MFMA covering 1024 elements).
 //  * Tile order is XCD-aware: consecutive workgroup ids land on different
 //    XCDs (each with its own L2), so ids are remapped so that every XCD
 //    walks a contiguous range of N-tiles with all their M-tiles, and a
@@ -33,6 +38,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, KB = 4;   // tile rows, cols, blocks per stage
 constexpr int ROWB = KB * 32 + 16;          // padded LDS row bytes (144)
@@ -41,8 +48,8 @@ constexpr int kMWG = 256;
 struct Stage {
     int8_t a[BM * ROWB];      // activations, [row][k]
     int8_t b[BN * ROWB];      // weights (q-8), [col][k]
-    float da[KB][BM];         // activation scales, [block][row]
-    float dw[KB][BN];         // weight scales, [block][col]
+    uint16_t da[KB][BM];      // activation scales (f16 bits), [block][row]
+    uint16_t dw[KB][BN];      // weight scales (f16 bits), [block][col]
 };
 
 __device__ __forceinline__ uint32_t unpack_lo(uint32_t q) {
@@ -129,12 +136,12 @@ __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
         hi = make_uint4(unpack_hi(qb[0]), unpack_hi(qb[1]), unpack_hi(qb[2]), unpack_hi(qb[3]));
         *reinterpret_cast<uint4 *>(dst + 32) = lo;
         *reinterpret_cast<uint4 *>(dst + 48) = hi;
-        S.dw[2 * pair][col] = f16_bits_to_f32(pf.w[0] & 0xffffu);
-        S.dw[2 * pair + 1][col] = f16_bits_to_f32(pf.w[4] >> 16);
+        S.dw[2 * pair][col] = (uint16_t)(pf.w[0] & 0xffffu);
+        S.dw[2 * pair + 1][col] = (uint16_t)(pf.w[4] >> 16);
     }
     if (t < BM) {
 #pragma unroll
-        for (int i = 0; i < KB; i++) S.da[i][t] = f16_bits_to_f32(pf.da[i]);
+        for (int i = 0; i < KB; i++) S.da[i][t] = pf.da[i];
     }
 }
 
@@ -173,16 +180,20 @@ __global__ __launch_bounds__(kMWG, 2) void mmq_kernel(const uint8_t *__restrict_
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[a][b][i] = 0.f;
 
-    Prefetch pf;
+    // register prefetch two stages ahead: while stage s computes, stage s+1
+    // waits in registers for its LDS slot and stage s+2 is in flight; the
+    // loop is unrolled by two so both prefetch sets stay in registers
+    Prefetch pf0, pf1;
     if (n_stages > 0) {
-        load_stage(pf, xq, xs, W, m, n, k, nb, m0, n0, b_beg, b_end);
-        store_stage(pf, stages[0]);
+        load_stage(pf0, xq, xs, W, m, n, k, nb, m0, n0, b_beg, b_end);
+        store_stage(pf0, stages[0]);
     }
+    if (n_stages > 1) load_stage(pf1, xq, xs, W, m, n, k, nb, m0, n0, b_beg + KB, b_end);
     __syncthreads();
 
-    for (int s = 0; s < n_stages; s++) {
-        const bool more = s + 1 < n_stages;
-        if (more) load_stage(pf, xq, xs, W, m, n, k, nb, m0, n0, b_beg + (s + 1) * KB, b_end);
+    auto step = [&](int s, Prefetch &pl, Prefetch &ps) {
+        if (s + 2 < n_stages)
+            load_stage(pl, xq, xs, W, m, n, k, nb, m0, n0, b_beg + (s + 2) * KB, b_end);
         const Stage &S = stages[s & 1];
 #pragma unroll 1  // keeps the 4 live MFMA results + 64 accumulators within 256 VGPRs
         for (int blk = 0; blk < KB; blk++) {
@@ -194,34 +205,37 @@ __global__ __launch_bounds__(kMWG, 2) void mmq_kernel(const uint8_t *__restrict_
                 bf[i] = *reinterpret_cast<const v4i *>(
                     &S.b[(wn * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
             }
-            float dwv[2];
-#pragma unroll
-            for (int j = 0; j < 2; j++) dwv[j] = S.dw[blk][wn * 64 + j * 32 + r];
+            // scale operands: lane (r, h = 0) holds K term 0 = d of its row
+            // (A) / column (B); every other K term is zero
+            h8 as[2], bs[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                // rows of this lane: 8*(q/4) + 4*h + q%4, q = 0..15
-                float dav[16];
+                const uint16_t da = h == 0 ? S.da[blk][wm * 64 + i * 32 + r] : (uint16_t)0;
+                const uint16_t dw = h == 0 ? S.dw[blk][wn * 64 + i * 32 + r] : (uint16_t)0;
+                as[i] = h8{};
+                bs[i] = h8{};
+                as[i][0] = __builtin_bit_cast(_Float16, da);
+                bs[i][0] = __builtin_bit_cast(_Float16, dw);
+            }
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 t4 = *reinterpret_cast<const float4 *>(
-                        &S.da[blk][wm * 64 + i * 32 + 8 * g + 4 * h]);
-                    dav[4 * g] = t4.x;
-                    dav[4 * g + 1] = t4.y;
-                    dav[4 * g + 2] = t4.z;
-                    dav[4 * g + 3] = t4.w;
-                }
+            for (int i = 0; i < 2; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
-                    v16i zero = {};
-                    v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
+                    const v16i zero = {};
+                    const f32x16 fzero = {};
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
+                    const f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as[i], bs[j], fzero, 0, 0, 0);
 #pragma unroll
                     for (int q = 0; q < 16; q++)
-                        acc[i][j][q] = __builtin_fmaf(dav[q] * dwv[j], (float)d[q], acc[i][j][q]);
+                        acc[i][j][q] = __builtin_fmaf((float)d[q], sc[q], acc[i][j][q]);
                 }
-            }
         }
-        if (more) store_stage(pf, stages[(s + 1) & 1]);
+        if (s + 1 < n_stages) store_stage(ps, stages[(s + 1) & 1]);
         __syncthreads();
+    };
+    for (int s = 0; s < n_stages; s += 2) {
+        step(s, pf0, pf1);
+        if (s + 1 < n_stages) step(s + 1, pf1, pf0);
     }
 
     float *dst = out + (size_t)z * m * n;
