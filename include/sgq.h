@@ -228,12 +228,13 @@ typedef struct {
     float rope_theta_sliding, rope_theta_global, global_rope_frac;
     float eps, attn_scale, final_softcap, weight_sigma;
     uint32_t global_k_eq_v; /* 1: global layers take V from the K projection */
-    uint32_t _pad;
+    uint32_t prefill_chunk; /* tokens per prefill chunk (its buffers are sized by it) */
     uint64_t seed;
 } sgq_model_config;
 
 /* The benchmark shape: 62 layers, hidden 5376, ffn 21504, 32 q / 16 kv heads
- * of 128, vocab 262144, window 1024, every 6th layer global, 16K context. */
+ * of 128, vocab 262144, window 1024, every 6th layer global, 16K context,
+ * 4096-token prefill chunks. */
 void sgq_model_default_config(sgq_model_config *cfg);
 /* Allocates and fills every weight and cache on the context's device. */
 int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out);
@@ -248,6 +249,15 @@ uint32_t sgq_model_position(const sgq_model *model);
  * replays it; the per-token inputs travel through a device step buffer. */
 int sgq_model_decode(sgq_model *model, uint32_t token, float *logits);
 int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
+/* Prefill (GpuModel::prefill, crates/sg-model/src/graph.rs:1451-1482): runs
+ * the host tokens[0..n) at positions pos..pos+n-1 in chunks of
+ * prefill_chunk, appends their K/V, advances the position, and writes the
+ * last token's softcapped logits to the device buffer `logits` (NULL: none).
+ * Linear layers are int8 MMQs over Q8_0 activations (the reference's
+ * prefill path), attention is the flash kernel of sgq_attn_prefill_q8 with
+ * keys before the chunk from the cache (ring or linear).  Returns after the
+ * last chunk is enqueued. */
+int sgq_model_prefill(sgq_model *model, const uint32_t *tokens, uint32_t n_tokens, float *logits);
 /* Synthetic context: fills the K/V pages of positions 0..n_tokens-1 (the
  * last sliding_window of them on ring layers) with Q8_0 of N(0,1) values and
  * sets the position to n_tokens, so a decode step can be measured at a long

@@ -132,6 +132,68 @@ class OracleDecoder:
         return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
 
 
+class OraclePrefill(OracleDecoder):
+    """Prefill of a token chunk (crates/sg-model/src/graph.rs:1451-1482 with
+    the MMQ record_prefill_layer path): every linear layer sees its input
+    round-tripped through Q8_0 (kv_quant_q8 semantics, per row, 32-blocks),
+    as the reference quantizes activations before its int8 MMQs; attention
+    is causal (window on sliding layers) over the cached positions plus the
+    chunk.  Decoding after it continues with the inherited decode()."""
+
+    def _q8rt(self, x2d):
+        s, q = O.quant_q8_0(np.ascontiguousarray(x2d, np.float32).reshape(-1))
+        return O.dequant_q8_0(s, q).reshape(x2d.shape)
+
+    def _mm(self, name, layer, x2d, n_out):
+        M, K = x2d.shape
+        return O.matmul_q4_0(self.w[(name, layer)], x2d, M, n_out, K, threads=8)
+
+    def prefill(self, tokens) -> np.ndarray:
+        c, w = self.c, self.w
+        H, F, hd = c["hidden"], c["ffn"], c["head_dim"]
+        nq, nkv = c["n_q_heads"], c["n_kv_heads"]
+        eps = c["eps"]
+        M = len(tokens)
+        q0 = self.pos
+        emb = w[("token_embd", -1)]
+        rb = (H // 32) * 18
+        x = np.stack([O.q4_0_dequant(emb[t * rb:(t + 1) * rb], 1, H)[0] for t in tokens])
+        x = (x * np.float32(math.sqrt(H))).astype(np.float32)
+        pos = np.arange(q0, q0 + M, dtype=np.uint32)
+        cs_sl = O.cos_sin_table(pos, hd, c["rope_theta_sliding"])
+        cs_gl = O.cos_sin_table(pos, hd, c["rope_theta_global"], self.global_factors)
+        for l in range(c["n_layers"]):
+            glob = self.is_global(l)
+            xn = self._q8rt(O.rmsnorm(x, w[("attn_norm", l)], H, eps))
+            q = self._mm("attn_q", l, xn, nq * hd)
+            k_proj = self._mm("attn_k", l, xn, nkv * hd)
+            v = k_proj.copy() if glob and c["global_k_eq_v"] else self._mm("attn_v", l, xn, nkv * hd)
+            cs = cs_gl if glob else cs_sl
+            q = O.rope(O.rmsnorm(q, w[("attn_q_norm", l)], hd, eps), hd, hd, nq, cs)
+            k = O.rope(O.rmsnorm(k_proj, w[("attn_k_norm", l)], hd, eps), hd, hd, nkv, cs)
+            v = O.rmsnorm(v, None, hd, eps)
+            for i in range(M):
+                self.k_cache[l].append(self._q8_round_trip(k[i]))
+                self.v_cache[l].append(self._q8_round_trip(v[i]))
+            ck = np.concatenate(self.k_cache[l])
+            cv = np.concatenate(self.v_cache[l])
+            window = None if glob else c["sliding_window"]
+            a = O.attention(q, ck, cv, M, q0, nq, nkv, hd, window, c["attn_scale"])
+            o = self._mm("attn_output", l, self._q8rt(a.reshape(M, nq * hd)), H)
+            x = (x + O.rmsnorm(o, w[("post_attention_norm", l)], H, eps)).astype(np.float32)
+            fn = self._q8rt(O.rmsnorm(x, w[("ffn_norm", l)], H, eps))
+            g = self._mm("ffn_gate", l, fn, F)
+            u = self._mm("ffn_up", l, fn, F)
+            f = self._mm("ffn_down", l, self._q8rt(O.geglu(g, u)), H)
+            x = (x + O.rmsnorm(f, w[("post_ffw_norm", l)], H, eps)).astype(np.float32)
+            x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
+        self.pos += M
+        xf = O.rmsnorm(x[-1], w[("output_norm", -1)], H, eps)
+        logits = O.gemv_rows(emb, xf, H, np.arange(c["vocab"]))
+        cap = np.float64(c["final_softcap"])
+        return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
+
+
 LAYER_TENSORS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",
                  "attn_norm", "attn_q_norm", "attn_k_norm", "post_attention_norm", "ffn_norm",
                  "post_ffw_norm", "layer_output_scale")

@@ -37,6 +37,7 @@
 #include <vector>
 
 #include "limbs.h"
+#include "q8.h"
 
 struct sgq_model;
 
@@ -207,6 +208,203 @@ __global__ void model_step_kernel(uint32_t *step, uint32_t a, uint32_t b, uint32
     }
 }
 
+// ---- prefill row kernels (one chunk of M tokens) ------------------------
+
+// RoPE tables of positions q0..q0+M-1 for both layer kinds, f64 angles as
+// in model_step_kernel; layout [kind][token][pair][cos, sin].
+__global__ void pf_rope_table_kernel(float *__restrict__ cs, int q0, int M, float theta_s,
+                                     float theta_g, int live_g) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    const int half = kHeadDim / 2;
+    if (t >= 2 * M * half) return;
+    const int kind = t / (M * half), r = t % (M * half);
+    const int tok = r / half, i = r % half;
+    const double theta = kind ? (double)theta_g : (double)theta_s;
+    const double factor = kind && i >= live_g ? 1e30 : 1.0;
+    const double ang = (double)(q0 + tok) * pow(theta, -2.0 * (double)i / (double)kHeadDim) / factor;
+    cs[2 * t] = (float)cos(ang);
+    cs[2 * t + 1] = (float)sin(ang);
+}
+
+constexpr int kPfWG = 256;
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return r;
+}
+
+// x[row] = dequant(E[token])·scale; Q8_0 of rmsnorm(x[row], w).  One
+// workgroup per row; thread t owns float4s t, t+256, ... (8-lane groups =
+// one Q8 block, as n4 % 8 == 0).
+__global__ __launch_bounds__(kPfWG) void pf_embed_norm_q8_kernel(
+    const uint8_t *__restrict__ E, const uint32_t *__restrict__ tokens, int H, float scale,
+    const float *__restrict__ w, float eps, float *__restrict__ x, int8_t *__restrict__ xq,
+    uint16_t *__restrict__ xs) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, t = threadIdx.x, n4 = H / 4;
+    const uint8_t *er = E + (size_t)tokens[row] * (H / 32) * 18;
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * H);
+    float ss = 0.f;
+    for (int i = t; i < n4; i += kPfWG) {
+        const uint8_t *blk = er + (i >> 3) * 18;
+        const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+        const int j0 = 4 * (i & 7);
+        const int sh = j0 < 16 ? 0 : 4;
+        const uint8_t *qs = blk + 2 + (j0 & 15);
+        float e[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) e[u] = d * (float)(((qs[u] >> sh) & 15) - 8) * scale;
+        const float4 v = make_float4(e[0], e[1], e[2], e[3]);
+        xr[i] = v;
+        ss += e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
+    }
+    const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+    int *qr = reinterpret_cast<int *>(xq + (size_t)row * H);
+    for (int i = t; i < n4; i += kPfWG) {
+        const float4 v = xr[i], wv = reinterpret_cast<const float4 *>(w)[i];
+        const float4 y = make_float4(v.x * inv * wv.x, v.y * inv * wv.y, v.z * inv * wv.z,
+                                     v.w * inv * wv.w);
+        int q;
+        quant_lane(y, i & 7, &xs[(size_t)row * (H / 32) + (i >> 3)], &q);
+        qr[i] = q;
+    }
+}
+
+// post-attention: x += rmsnorm(o, w_post);            Q8_0 of rmsnorm(x, w_next)
+// post-FFN:       x = (x + rmsnorm(o, w_post))·scale;  Q8_0 of rmsnorm(x, w_next)
+__global__ __launch_bounds__(kPfWG) void pf_residual_norm_q8_kernel(
+    const float *__restrict__ o, const float *__restrict__ w_post, float *__restrict__ x,
+    const float *__restrict__ scale_ptr, const float *__restrict__ w_next, int H, float eps,
+    int8_t *__restrict__ xq, uint16_t *__restrict__ xs) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, t = threadIdx.x, n4 = H / 4;
+    const float4 *orow = reinterpret_cast<const float4 *>(o + (size_t)row * H);
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * H);
+    float ss = 0.f;
+    for (int i = t; i < n4; i += kPfWG) {
+        const float4 v = orow[i];
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+    const float s = scale_ptr ? *scale_ptr : 1.f;
+    float ss2 = 0.f;
+    for (int i = t; i < n4; i += kPfWG) {
+        const float4 v = orow[i], xv = xr[i], wp = reinterpret_cast<const float4 *>(w_post)[i];
+        float4 r;
+        r.x = (xv.x + v.x * inv * wp.x) * s;
+        r.y = (xv.y + v.y * inv * wp.y) * s;
+        r.z = (xv.z + v.z * inv * wp.z) * s;
+        r.w = (xv.w + v.w * inv * wp.w) * s;
+        xr[i] = r;
+        ss2 += r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w;
+    }
+    const float inv2 = 1.0f / sqrtf(block_sum256(ss2, red) / (float)H + eps);
+    int *qr = reinterpret_cast<int *>(xq + (size_t)row * H);
+    for (int i = t; i < n4; i += kPfWG) {
+        const float4 v = xr[i], wv = reinterpret_cast<const float4 *>(w_next)[i];
+        const float4 y = make_float4(v.x * inv2 * wv.x, v.y * inv2 * wv.y, v.z * inv2 * wv.z,
+                                     v.w * inv2 * wv.w);
+        int q;
+        quant_lane(y, i & 7, &xs[(size_t)row * (H / 32) + (i >> 3)], &q);
+        qr[i] = q;
+    }
+}
+
+// h = gelu_tanh(g)·u as Q8_0, one float4 per thread.
+__global__ __launch_bounds__(256) void pf_geglu_q8_kernel(const float4 *__restrict__ g,
+                                                          const float4 *__restrict__ u,
+                                                          uint64_t n4, int *__restrict__ hq,
+                                                          uint16_t *__restrict__ hs) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;  // n4 % 8 == 0: whole 8-lane groups exit together
+    const float4 a = g[i], b = u[i];
+    const float4 h = make_float4(gelu_tanh(a.x) * b.x, gelu_tanh(a.y) * b.y, gelu_tanh(a.z) * b.z,
+                                 gelu_tanh(a.w) * b.w);
+    int q;
+    quant_lane(h, (int)(i & 7), &hs[i >> 3], &q);
+    hq[i] = q;
+}
+
+// Per (token, head): q -> rmsnorm(q_norm) + RoPE (fp32 out); k -> rmsnorm
+// (k_norm) + RoPE -> Q8_0 into the chunk's K pages; v -> weightless rmsnorm
+// -> Q8_0 into the chunk's V pages.  Grid [M, n_q + 2 n_kv], 128 threads.
+__global__ __launch_bounds__(kHeadDim) void pf_qkv_post_kernel(
+    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
+    const float *__restrict__ v_src, const float *__restrict__ wq_norm,
+    const float *__restrict__ wk_norm, const float *__restrict__ cs, int n_q, int n_kv,
+    float eps, float *__restrict__ q_out, int8_t *__restrict__ ckq, uint16_t *__restrict__ cks,
+    int8_t *__restrict__ cvq, uint16_t *__restrict__ cvs) {
+    __shared__ float row[kHeadDim];
+    __shared__ float red[2];
+    const int tok = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    const int QD = n_q * kHeadDim, KD = n_kv * kHeadDim;
+    int kind, head;  // 0 q, 1 k, 2 v
+    if (h < n_q) {
+        kind = 0, head = h;
+    } else if (h < n_q + n_kv) {
+        kind = 1, head = h - n_q;
+    } else {
+        kind = 2, head = h - n_q - n_kv;
+    }
+    const float *src = kind == 0 ? q_raw + (size_t)tok * QD : (kind == 1 ? k_raw : v_src) + (size_t)tok * KD;
+    float v = src[head * kHeadDim + t];
+    float ss = v * v;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((red[0] + red[1]) / (float)kHeadDim + eps);
+    v = v * inv * (kind == 0 ? wq_norm[t] : kind == 1 ? wk_norm[t] : 1.f);
+    row[t] = v;
+    __syncthreads();
+    if (kind < 2) {
+        const int i = t % (kHeadDim / 2);
+        const float c = cs[((size_t)tok * (kHeadDim / 2) + i) * 2];
+        const float sn = cs[((size_t)tok * (kHeadDim / 2) + i) * 2 + 1];
+        const float a = row[i], b = row[i + kHeadDim / 2];
+        v = t < kHeadDim / 2 ? a * c - b * sn : b * c + a * sn;
+    }
+    if (kind == 0) {
+        q_out[(size_t)tok * QD + head * kHeadDim + t] = v;
+        return;
+    }
+    float amax = fabsf(v);
+    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
+    const float d = amax * (1.0f / 127.0f);
+    const float id = d > 0.f ? 1.0f / d : 0.f;
+    const size_t e = ((size_t)tok * n_kv + head) * kHeadDim + t;
+    (kind == 1 ? ckq : cvq)[e] = (int8_t)(int)__builtin_rintf(v * id);
+    if ((t & 31) == 0) (kind == 1 ? cks : cvs)[e / 32] = f32_to_f16_bits(d);
+}
+
+// Append the chunk's K/V pages (rows i = position - q0) to a cache: slot
+// q0+i, or (q0+i) mod ring — then only the last `ring` rows, so no two
+// threads write one slot.  Thread = one 16-byte quant chunk of a row (and one
+// scale where the row has one).
+__global__ void pf_kv_append_kernel(const int8_t *__restrict__ ckq, const uint16_t *__restrict__ cks,
+                                    const int8_t *__restrict__ cvq, const uint16_t *__restrict__ cvs,
+                                    int8_t *__restrict__ kq, uint16_t *__restrict__ ks,
+                                    int8_t *__restrict__ vq, uint16_t *__restrict__ vs, int M,
+                                    int q0, int ring, int KD) {
+    const int per_row = KD / 16;
+    const int i0 = ring && M > ring ? M - ring : 0;
+    const long g = (long)blockIdx.x * 256 + threadIdx.x;
+    if (g >= (long)(M - i0) * per_row) return;
+    const int i = i0 + (int)(g / per_row), c = (int)(g % per_row);
+    const int pos = q0 + i;
+    const size_t slot = ring ? (size_t)(pos % ring) : (size_t)pos;
+    typedef int i4v __attribute__((ext_vector_type(4)));
+    reinterpret_cast<i4v *>(kq + slot * KD)[c] = reinterpret_cast<const i4v *>(ckq + (size_t)i * KD)[c];
+    reinterpret_cast<i4v *>(vq + slot * KD)[c] = reinterpret_cast<const i4v *>(cvq + (size_t)i * KD)[c];
+    if (c < KD / 32) {
+        ks[slot * (KD / 32) + c] = cks[(size_t)i * (KD / 32) + c];
+        vs[slot * (KD / 32) + c] = cvs[(size_t)i * (KD / 32) + c];
+    }
+}
+
 }  // namespace
 }  // namespace sgq
 
@@ -238,6 +436,15 @@ struct sgq_model {
     uint32_t pos = 0;
     sgq_graph *graph = nullptr;
     float *graph_logits = nullptr;
+    // prefill chunk buffers (allocated at the first prefill, `chunk` rows)
+    struct {
+        uint32_t chunk = 0;
+        uint32_t *tok;
+        float *rope;                      // [2 kinds][chunk][64][cos, sin]
+        float *x, *q_raw, *k_raw, *v_raw, *q, *attn, *o, *g, *u, *f, *part, *head_in;
+        int8_t *xq, *aq, *hq, *ckq, *cvq;  // Q8_0 quants
+        uint16_t *xs, *as, *hs, *cks, *cvs;  // and their f16 scales
+    } pf;
 };
 
 namespace {
@@ -347,6 +554,7 @@ void sgq_model_default_config(sgq_model_config *c) {
     c->weight_sigma = 0.02f;
     c->seed = 0x5EED;
     c->global_k_eq_v = 1;
+    c->prefill_chunk = 4096;
 }
 
 int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out) {
@@ -364,6 +572,8 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
               "model: empty dimension");
     SGQ_CHECK(c.global_every >= 1, "model: global_every must be >= 1");
     SGQ_CHECK(c.global_rope_frac >= 0.f && c.global_rope_frac <= 1.f, "model: global_rope_frac");
+    SGQ_CHECK(c.prefill_chunk >= 1 && c.prefill_chunk <= 65536, "model: prefill_chunk %u",
+              c.prefill_chunk);
     if (int rc0 = gemv_prepare()) return rc0;
     if (int rc0 = attn_prepare()) return rc0;
     (void)device_info();
@@ -514,6 +724,151 @@ int sgq_model_fill_cache(sgq_model *m, uint32_t n_tokens, uint64_t seed) {
     }
     if (!rc) m->pos = n_tokens;
     return rc;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Split-K factor for an MMQ of m×n×k: enough (tile, split) work items to fill
+// the chip's workgroup slots, at least 16 blocks of K per split.
+uint32_t mmq_split(uint32_t m, uint32_t n, uint32_t k) {
+    const uint64_t tiles = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
+    uint32_t split = 1;
+    while (split < 8 && tiles * split * 2 <= 1024 && (k / 32) / (split * 2) >= 16) split *= 2;
+    return split;
+}
+constexpr size_t kPfPartialFloats = 1024ull * 128 * 128;  // >= split·m·n for every choice above
+
+int pf_alloc(sgq_model *m) {
+    const sgq_model_config &c = m->cfg;
+    const size_t C = c.prefill_chunk, H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim,
+                 KD = c.n_kv_heads * kHeadDim;
+    auto &p = m->pf;
+    void **f32s[] = {(void **)&p.x, (void **)&p.q_raw, (void **)&p.k_raw, (void **)&p.v_raw,
+                     (void **)&p.q, (void **)&p.attn, (void **)&p.o, (void **)&p.g,
+                     (void **)&p.u, (void **)&p.f, (void **)&p.part, (void **)&p.head_in,
+                     (void **)&p.rope};
+    const size_t f32n[] = {C * H, C * QD, C * KD, C * KD, C * QD, C * QD, C * H, C * F, C * F,
+                           C * H, kPfPartialFloats, H, 2 * C * kHeadDim};
+    int rc;
+    for (int i = 0; i < 13; i++)
+        if ((rc = alloc(m, f32n[i] * 4, f32s[i]))) return rc;
+    void **q8s[] = {(void **)&p.xq, (void **)&p.aq, (void **)&p.hq, (void **)&p.ckq, (void **)&p.cvq};
+    void **scs[] = {(void **)&p.xs, (void **)&p.as, (void **)&p.hs, (void **)&p.cks, (void **)&p.cvs};
+    const size_t q8n[] = {C * H, C * QD, C * F, C * KD, C * KD};
+    for (int i = 0; i < 5; i++)
+        if ((rc = alloc(m, q8n[i], q8s[i])) || (rc = alloc(m, q8n[i] / 32 * 2, scs[i]))) return rc;
+    if ((rc = alloc(m, C * 4, (void **)&p.tok))) return rc;
+    p.chunk = (uint32_t)C;
+    return SGQ_OK;
+}
+
+int mmq(sgq_model *m, hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
+        float *y, uint32_t M, uint32_t n, uint32_t k) {
+    const uint32_t split = mmq_split(M, n, k);
+    return launch_gemm_q4_0_q8(st, w, xq, xs, y, M, n, k, split, split > 1 ? m->pf.part : nullptr);
+}
+
+// One chunk of M tokens at positions q0..q0+M-1 (tokens already on the device).
+int pf_chunk(sgq_model *m, uint32_t M, uint32_t q0) {
+    const sgq_model_config &c = m->cfg;
+    hipStream_t st = ctx_stream(m->ctx);
+    auto &p = m->pf;
+    const uint32_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim;
+    int rc;
+    const int live = (int)lroundf(c.global_rope_frac * kHeadDim / 2);
+    hipLaunchKernelGGL(pf_rope_table_kernel, dim3((2 * M * (kHeadDim / 2) + 255) / 256), dim3(256),
+                       0, st, p.rope, (int)q0, (int)M, c.rope_theta_sliding, c.rope_theta_global,
+                       live);
+    hipLaunchKernelGGL(pf_embed_norm_q8_kernel, dim3(M), dim3(kPfWG), 0, st,
+                       static_cast<const uint8_t *>(m->embd), p.tok, (int)H, sqrtf((float)H),
+                       m->layers[0].attn_norm, c.eps, p.x, p.xq, p.xs);
+    SGQ_HIP(hipGetLastError());
+    for (size_t li = 0; li < m->layers.size(); li++) {
+        const LayerW &L = m->layers[li];
+        if ((rc = mmq(m, st, L.wq, p.xq, p.xs, p.q_raw, M, QD, H)) ||
+            (rc = mmq(m, st, L.wk, p.xq, p.xs, p.k_raw, M, KD, H)))
+            return rc;
+        if (L.wv && (rc = mmq(m, st, L.wv, p.xq, p.xs, p.v_raw, M, KD, H))) return rc;
+        const float *rope = p.rope + (L.global ? (size_t)M * kHeadDim : 0);
+        hipLaunchKernelGGL(pf_qkv_post_kernel, dim3(M, c.n_q_heads + 2 * c.n_kv_heads),
+                           dim3(kHeadDim), 0, st, p.q_raw, p.k_raw, L.wv ? p.v_raw : p.k_raw,
+                           L.q_norm, L.k_norm, rope, (int)c.n_q_heads, (int)c.n_kv_heads, c.eps,
+                           p.q, p.ckq, p.cks, p.cvq, p.cvs);
+        SGQ_HIP(hipGetLastError());
+        const int ring = L.global ? 0 : (int)L.slots;
+        const int window = L.global ? 0 : (int)std::min(c.sliding_window, L.slots);
+        if ((rc = launch_attn_prefill_q8(st, p.q, L.kq, L.ks, L.vq, L.vs, p.attn, (int)M, (int)q0,
+                                         (int)c.n_q_heads, (int)c.n_kv_heads, kHeadDim, window,
+                                         c.attn_scale, ring, p.ckq, p.cks, p.cvq, p.cvs)))
+            return rc;
+        {
+            const int i0 = ring && (int)M > ring ? (int)M - ring : 0;
+            const long threads = (long)(M - i0) * (KD / 16);
+            hipLaunchKernelGGL(pf_kv_append_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                               0, st, p.ckq, p.cks, p.cvq, p.cvs, L.kq, L.ks, L.vq, L.vs, (int)M,
+                               (int)q0, ring, (int)KD);
+            SGQ_HIP(hipGetLastError());
+        }
+        if ((rc = launch_quant_q8_0(st, p.attn, p.as, p.aq, (uint64_t)M * QD))) return rc;
+        if ((rc = mmq(m, st, L.wo, p.aq, p.as, p.o, M, H, QD))) return rc;
+        hipLaunchKernelGGL(pf_residual_norm_q8_kernel, dim3(M), dim3(kPfWG), 0, st, p.o,
+                           L.post_attn_norm, p.x, (const float *)nullptr, L.ffn_norm, (int)H,
+                           c.eps, p.xq, p.xs);
+        SGQ_HIP(hipGetLastError());
+        if ((rc = mmq(m, st, L.wg, p.xq, p.xs, p.g, M, F, H)) ||
+            (rc = mmq(m, st, L.wu, p.xq, p.xs, p.u, M, F, H)))
+            return rc;
+        const uint64_t n4 = (uint64_t)M * F / 4;
+        hipLaunchKernelGGL(pf_geglu_q8_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                           reinterpret_cast<const float4 *>(p.g), reinterpret_cast<const float4 *>(p.u),
+                           n4, reinterpret_cast<int *>(p.hq), p.hs);
+        SGQ_HIP(hipGetLastError());
+        if ((rc = mmq(m, st, L.wd, p.hq, p.hs, p.f, M, H, F))) return rc;
+        const float *w_next = li + 1 < m->layers.size() ? m->layers[li + 1].attn_norm : m->out_norm;
+        hipLaunchKernelGGL(pf_residual_norm_q8_kernel, dim3(M), dim3(kPfWG), 0, st, p.f,
+                           L.post_ffw_norm, p.x, L.out_scale, w_next, (int)H, c.eps, p.xq, p.xs);
+        SGQ_HIP(hipGetLastError());
+    }
+    return SGQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sgq_model_prefill(sgq_model *m, const uint32_t *tokens, uint32_t n_tokens, float *logits) {
+    if (!m || !tokens) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    const sgq_model_config &c = m->cfg;
+    SGQ_CHECK(n_tokens >= 1, "model: empty prompt");
+    SGQ_CHECK((uint64_t)m->pos + n_tokens <= c.max_ctx, "model: prompt of %u at position %u exceeds max_ctx %u",
+              n_tokens, m->pos, c.max_ctx);
+    for (uint32_t i = 0; i < n_tokens; i++)
+        SGQ_CHECK(tokens[i] < c.vocab, "model: token %u at %u >= vocab %u", tokens[i], i, c.vocab);
+    int rc;
+    if (!m->pf.chunk && (rc = pf_alloc(m))) return rc;
+    hipStream_t st = ctx_stream(m->ctx);
+    uint32_t M = 0;
+    for (uint32_t c0 = 0; c0 < n_tokens; c0 += M) {
+        M = std::min(m->pf.chunk, n_tokens - c0);
+        SGQ_HIP(hipMemcpyAsync(m->pf.tok, tokens + c0, (size_t)M * 4, hipMemcpyHostToDevice, st));
+        SGQ_HIP(hipStreamSynchronize(st));  // the host array may go away
+        if ((rc = pf_chunk(m, M, m->pos))) return rc;
+        m->pos += M;
+    }
+    if (logits) {  // the last token's logits: output norm, limbs, tied head with softcap
+        const uint32_t H = c.hidden;
+        if ((rc = launch_rmsnorm(st, m->pf.x + (size_t)(M - 1) * H, m->out_norm, m->pf.head_in, 1, H, 0,
+                                 c.eps)) ||
+            (rc = launch_quant_limbs(st, m->pf.head_in, m->xl, H)))
+            return rc;
+        GemvTargets head{};
+        head.w[0] = m->embd, head.y[0] = logits, head.end[0] = (int)c.vocab, head.count = 1;
+        head.softcap = c.final_softcap;
+        if ((rc = launch_gemv_limbs(st, head, m->xl, H))) return rc;
+    }
+    return SGQ_OK;
 }
 
 int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr,

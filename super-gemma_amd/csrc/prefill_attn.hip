@@ -6,9 +6,12 @@
 // attn_prefill_sliding_ring.wgsl:53-152): query i of the chunk sits at
 // position q0+i and attends keys p with p <= q0+i and, with a window W,
 // p > q0+i-W; out = softmax(scale · q·kᵀ)·v per query head, GQA head h
-// reading kv head h/(n_q/n_kv).  K and V come from the Q8_0 pages
-// (int8 [slot × n_kv × 128] + f16 scales per 32) of a linear cache
-// (slot = position) and are dequantized to f16 as in the reference's
+// reading kv head h/(n_q/n_kv).  K and V come from Q8_0 pages (int8
+// [row × n_kv × 128] + f16 scales per 32) in two ranges, as in
+// attn_prefill_sliding_ring.wgsl: keys before q0 from the cache (slot =
+// position, or position mod ring for a sliding ring), keys from q0 on from
+// the chunk's own pages (row = position - q0) when those are given, else
+// from the cache too.  They are dequantized to f16 as in the reference's
 // _sp_q8 variant; P is rounded to f16 for PV, as in the reference.
 //
 // Design (MFMA-bound: 4·hd flops per query-key pair against 2·hd·1 B of
@@ -40,10 +43,17 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+struct KvSource {
+    const int8_t *kq, *vq;      // cache pages
+    const uint16_t *ks, *vs;
+    int ring;                   // ring slots (0: linear cache)
+    const int8_t *ckq, *cvq;    // the chunk's pages (rows = position - q0), or null
+    const uint16_t *cks, *cvs;
+};
+
 __global__ __launch_bounds__(256) void attn_prefill_kernel(
-    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
-    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs, float *__restrict__ out,
-    int n_tok, int q0, int n_q, int n_kv, int window, float scale, int qtiles) {
+    const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
+    int n_q, int n_kv, int window, float scale, int qtiles) {
     __shared__ __align__(16) _Float16 k_s[kKT][kKRow];
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
 
@@ -88,12 +98,18 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
             const int key = kb + kk;
             _Float16 kv[32], vv[32];
             if (key <= k_hi) {
-                const size_t row = (size_t)key * n_kv + kvh;
-                const i32x4 *kp = reinterpret_cast<const i32x4 *>(kq + row * kHD + 32 * blk);
-                const i32x4 *vp = reinterpret_cast<const i32x4 *>(vq + row * kHD + 32 * blk);
+                const bool fresh = src.ckq != nullptr && key >= q0;
+                const int slot = fresh ? key - q0 : src.ring ? key % src.ring : key;
+                const size_t row = (size_t)slot * n_kv + kvh;
+                const int8_t *kqb = fresh ? src.ckq : src.kq;
+                const int8_t *vqb = fresh ? src.cvq : src.vq;
+                const uint16_t *ksb = fresh ? src.cks : src.ks;
+                const uint16_t *vsb = fresh ? src.cvs : src.vs;
+                const i32x4 *kp = reinterpret_cast<const i32x4 *>(kqb + row * kHD + 32 * blk);
+                const i32x4 *vp = reinterpret_cast<const i32x4 *>(vqb + row * kHD + 32 * blk);
                 const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
-                const float sk = f16_bits_to_f32(ks[row * (kHD / 32) + blk]);
-                const float sv = f16_bits_to_f32(vs[row * (kHD / 32) + blk]);
+                const float sk = f16_bits_to_f32(ksb[row * (kHD / 32) + blk]);
+                const float sv = f16_bits_to_f32(vsb[row * (kHD / 32) + blk]);
                 const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
                 const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
@@ -191,17 +207,26 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 
 int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
                            const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
-                           int n_q, int n_kv, int head_dim, int window, float scale) {
+                           int n_q, int n_kv, int head_dim, int window, float scale, int ring,
+                           const int8_t *ckq, const uint16_t *cks, const int8_t *cvq,
+                           const uint16_t *cvs) {
     SGQ_CHECK(head_dim == kHD, "attn_prefill_q8: head_dim %d unsupported (128)", head_dim);
     SGQ_CHECK(n_tok > 0 && q0 >= 0, "attn_prefill_q8: n_tok %d, q0 %d", n_tok, q0);
     SGQ_CHECK(n_kv > 0 && n_q > 0 && n_q % n_kv == 0, "attn_prefill_q8: n_q %% n_kv != 0");
-    SGQ_CHECK(window >= 0, "attn_prefill_q8: negative window");
+    SGQ_CHECK(window >= 0 && ring >= 0, "attn_prefill_q8: negative window or ring");
+    SGQ_CHECK(ckq == nullptr || (cks && cvq && cvs && ((uintptr_t)ckq & 15) == 0 &&
+                                 ((uintptr_t)cvq & 15) == 0),
+              "attn_prefill_q8: incomplete or misaligned chunk pages");
+    SGQ_CHECK(ring == 0 || ckq != nullptr, "attn_prefill_q8: a ring cache needs the chunk's pages");
+    SGQ_CHECK(ring == 0 || window <= ring, "attn_prefill_q8: window %d exceeds the ring (%d)",
+              window, ring);
     SGQ_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 &&
                   ((uintptr_t)ks & 1) == 0 && ((uintptr_t)vs & 1) == 0,
               "attn_prefill_q8: misaligned operand");
     const int qtiles = (n_tok + kQT - 1) / kQT;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(qtiles, n_q), dim3(256), 0, st, q, kq, ks, vq, vs,
-                       out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
+    const KvSource src{kq, vq, ks, vs, ring, ckq, cvq, cks, cvs};
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(qtiles, n_q), dim3(256), 0, st, q, src, out,
+                       n_tok, q0, n_q, n_kv, window, scale, qtiles);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }

@@ -16,34 +16,13 @@
 // float4: a wave reads 1 KB contiguous per load and writes 256 B of quants
 // per store (one dword per lane); amax is a 3-step butterfly inside each
 // 8-lane group.
-#include "sgq_internal.h"
+#include "q8.h"
 
 namespace sgq {
 namespace {
 
 constexpr int kQWG = 256;
 typedef float f4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ int pack_q(float a, float b, float c, float d, float id) {
-    int qa = (int)__builtin_rintf(a * id);
-    int qb = (int)__builtin_rintf(b * id);
-    int qc = (int)__builtin_rintf(c * id);
-    int qd = (int)__builtin_rintf(d * id);
-    return (qa & 0xff) | ((qb & 0xff) << 8) | ((qc & 0xff) << 16) | ((qd & 0xff) << 24);
-}
-
-// Quantize the float4 this lane holds; lanes 8g..8g+7 form block g.
-__device__ __forceinline__ void quant_lane(float4 v, int sub, uint16_t *scale_out,
-                                           int *quant_out) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, kWave));
-    const float d = amax * (1.0f / 127.0f);
-    const float id = d > 0.f ? 1.0f / d : 0.f;
-    *quant_out = pack_q(v.x, v.y, v.z, v.w, id);
-    if (sub == 0) *scale_out = f32_to_f16_bits(d);
-}
 
 __global__ __launch_bounds__(kQWG) void quant_q8_0_kernel(const float4 *__restrict__ x,
                                                           uint16_t *__restrict__ scales,

@@ -98,9 +98,13 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                              uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
                              int n_q, int n_kv, int n_splits, float scale, float *out,
                              void *workspace, size_t workspace_bytes, void *limbs_out);
+// Keys before q0 come from the cache (ring: slot = pos % ring), keys from q0
+// on from the chunk's pages ckq.. (row = pos - q0) when given, else the cache.
 int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
                            const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
-                           int n_q, int n_kv, int head_dim, int window, float scale);
+                           int n_q, int n_kv, int head_dim, int window, float scale, int ring = 0,
+                           const int8_t *ckq = nullptr, const uint16_t *cks = nullptr,
+                           const int8_t *cvq = nullptr, const uint16_t *cvs = nullptr);
 int launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *y, uint32_t rows,
                    uint32_t row_len, int plus_one, float eps);
 int launch_rope(hipStream_t st, float *xs, const float *cos_sin, uint64_t rows, uint32_t head_dim,

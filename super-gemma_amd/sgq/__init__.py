@@ -79,11 +79,11 @@ class ModelConfig(C.Structure):
         "n_layers", "hidden", "ffn", "n_q_heads", "n_kv_heads", "head_dim", "vocab",
         "sliding_window", "global_every", "max_ctx")] + [(n, C.c_float) for n in (
         "rope_theta_sliding", "rope_theta_global", "global_rope_frac", "eps", "attn_scale",
-        "final_softcap", "weight_sigma")] + [("global_k_eq_v", C.c_uint32), ("_pad", C.c_uint32),
-                                             ("seed", C.c_uint64)]
+        "final_softcap", "weight_sigma")] + [("global_k_eq_v", C.c_uint32),
+                                             ("prefill_chunk", C.c_uint32), ("seed", C.c_uint64)]
 
     def as_dict(self):
-        return {n: getattr(self, n) for n, _ in self._fields_ if n != "_pad"}
+        return {n: getattr(self, n) for n, _ in self._fields_}
 
 
 # Exported symbols and their ctypes signatures (checked against include/sgq.h
@@ -133,6 +133,7 @@ SIGNATURES = {
     "sgq_model_decode": (I, [P, U32, P]),
     "sgq_model_decode_graph": (I, [P, U32, P]),
     "sgq_model_fill_cache": (I, [P, U32, U64]),
+    "sgq_model_prefill": (I, [P, C.POINTER(U32), U32, P]),
     "sgq_model_tensor": (I, [P, I, C.c_char_p, C.POINTER(P), C.POINTER(U64)]),
     "sgq_fill_q4_0_random": (I, [P, P, U64, U64, C.c_float]),
     "sgq_fill_normal": (I, [P, P, U64, U64, C.c_float, C.c_float]),
@@ -483,6 +484,16 @@ class Model:
         _need(logits, torch.float32, self.cfg.vocab, "logits")
         fn = lib().sgq_model_decode_graph if graph else lib().sgq_model_decode
         _check(fn(self._h, int(token), _ptr(logits)))
+
+    def prefill(self, tokens, logits: Optional[torch.Tensor] = None):
+        """Run a prompt (host token ids) through the model at the current
+        position; logits of its last token into `logits` when given."""
+        import numpy as np
+        toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+        if logits is not None:
+            _need(logits, torch.float32, self.cfg.vocab, "logits")
+        _check(lib().sgq_model_prefill(self._h, toks.ctypes.data_as(C.POINTER(U32)), toks.size,
+                                       _ptr(logits)))
 
     def fill_cache(self, n_tokens: int, seed: int = 0xCAC4E):
         """Synthetic Q8_0 K/V for positions [0, n_tokens); position = n_tokens."""

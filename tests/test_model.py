@@ -7,9 +7,11 @@ generated (sgq_model_tensor) and runs reference.rs:157-316 in f64/f32 with
 Q8_0 K/V pages.
 
 Tolerance on logits, per step: |err| <= 2e-3*|want| + 2e-3*max|want|
-elementwise, and the same argmax (top-1) at every step.  The GPU differs from
-the oracle by the GEMV's x limbs (|err| <= 1.9e-6*amax per block), f32 vs f64
-accumulation, and an occasional Q8_0 rounding flip of a K/V element.
+elementwise, and top-1 agreement up to ties within that tolerance (the GPU's
+argmax scores within 2e-3*max|want| of the oracle's best).  The GPU differs from
+the oracle by the GEMV's x limbs (|err| <= 2.6e-5*amax per block), f32 vs f64
+accumulation, and an occasional Q8_0 rounding flip of a K/V element or, in
+prefill, of an activation.
 """
 import numpy as np
 import pytest
@@ -38,7 +40,10 @@ def _weights(model, cfg):
 def _check_logits(got, want, step):
     top = float(np.abs(want).max())
     assert_close(got, want, 2e-3, 2e-3 * top, f"logits step {step}")
-    assert int(np.argmax(got)) == int(np.argmax(want)), f"top-1 differs at step {step}"
+    # top-1 agreement up to ties within the tolerance: the GPU's choice scores
+    # within 2e-3·max|want| of the oracle's best in the oracle's own logits
+    g, w_ = int(np.argmax(got)), int(np.argmax(want))
+    assert want[g] >= want[w_] - 2e-3 * top, f"top-1 differs at step {step}: {g} vs {w_}"
 
 
 def _small_cfg(sgq, **kw):
@@ -166,6 +171,58 @@ def test_model_long_context_matches_oracle(ctx, oracle):
     model.close()
 
 
+@pytest.mark.parametrize("chunk,n_tok", [(64, 37), (16, 37), (4, 10)])
+def test_model_prefill_matches_oracle_then_decodes(ctx, oracle, chunk, n_tok):
+    """Prefill in chunks (keys before a chunk come from the 4-slot sliding
+    ring or the linear global cache, the chunk's own from its pages), last-
+    token logits vs the oracle's prefill (Q8_0 activations into every linear
+    layer, as the reference's MMQ path), then 3 decode steps from the caches
+    the prefill filled."""
+    import sgq
+    from oracle.model import OraclePrefill
+
+    print(f"model prefill chunk={chunk} n_tok={n_tok}", flush=True)
+    cfg = _small_cfg(sgq, max_ctx=64, prefill_chunk=chunk, seed=0x9F + chunk)
+    model = sgq.Model(ctx, cfg)
+    d = cfg.as_dict()
+    ref = OraclePrefill(d, _weights(model, d))
+    rng = np.random.default_rng(chunk + n_tok)
+    toks = rng.integers(0, cfg.vocab, n_tok)
+    logits = empty(cfg.vocab, torch.float32)
+    model.prefill(toks, logits)
+    torch.cuda.synchronize()
+    assert model.position == n_tok
+    # prefill chunks in the oracle mirror the driver's chunking
+    want = None
+    for c0 in range(0, n_tok, chunk):
+        want = ref.prefill(toks[c0:c0 + chunk])
+    _check_logits(host(logits), want, "prefill")
+    for i, t in enumerate([5, 900, 33]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), f"after prefill {i}")
+    model.close()
+
+
+def test_model_prefill_full_width(ctx, oracle):
+    """The benchmark widths at 2 layers, a 300-token prompt in one chunk."""
+    import sgq
+    from oracle.model import OraclePrefill
+
+    print("model prefill full width", flush=True)
+    cfg = sgq.default_model_config(n_layers=2, global_every=2, max_ctx=512, prefill_chunk=512,
+                                   seed=0xBEE)
+    model = sgq.Model(ctx, cfg)
+    d = cfg.as_dict()
+    ref = OraclePrefill(d, _weights(model, d))
+    toks = np.random.default_rng(7).integers(0, cfg.vocab, 300)
+    logits = empty(cfg.vocab, torch.float32)
+    model.prefill(toks, logits)
+    torch.cuda.synchronize()
+    _check_logits(host(logits), ref.prefill(toks), "prefill full width")
+    model.close()
+
+
 def test_model_rejects_bad_inputs(ctx):
     import sgq
 
@@ -183,3 +240,9 @@ def test_model_rejects_bad_inputs(ctx):
         sgq.Model(ctx, sgq.default_model_config(head_dim=64))
     with pytest.raises(sgq.GpuError):
         sgq.Model(ctx, sgq.default_model_config(n_q_heads=48))  # 3 q heads per kv head
+    m = sgq.Model(ctx, _small_cfg(sgq, max_ctx=8))
+    with pytest.raises(sgq.GpuError):
+        m.prefill(np.arange(9))  # longer than max_ctx
+    with pytest.raises(sgq.GpuError):
+        m.prefill([cfg.vocab])  # token out of range
+    m.close()
