@@ -5,6 +5,8 @@
 Prints ONE JSON line (rank 0).  A "step" is one pass of the hot path over one
 batch of synthetic input, already resident in HBM:
 
+  prefill BASELINE config 5's prefill: a 4096-token prompt from position 0;
+          value = prompt tok/s.
   decode  BASELINE config 5 (default): one bs=1 decode step of the 62-layer
           random-init decoder at an 8K context (synthetic Q8_0 K/V pages for
           positions 0..8191), replayed as one hipGraph; value = tok/s.
@@ -207,6 +209,52 @@ class AttnDecode:
         }
 
 
+class Prefill:
+    """BASELINE config 5 prefill: a 4096-token prompt of seeded random ids
+    through the 62-layer random-init decoder from position 0 (one chunk),
+    last-token logits.  value = prompt tokens per second."""
+    kernel = "mmq_kernel"
+
+    def __init__(self, ctx, torch, n_tok=4096):
+        import numpy as np
+        import sgq
+
+        self.ctx, self.torch, self.n_tok = ctx, torch, n_tok
+        self.stream = torch.cuda.Stream()
+        ctx.set_stream(self.stream)
+        self.cfg = sgq.default_model_config(max_ctx=n_tok, prefill_chunk=n_tok)
+        self.model = sgq.Model(ctx, self.cfg)
+        self.tokens = np.random.default_rng(11).integers(0, self.cfg.vocab, n_tok).astype(np.uint32)
+        self.logits = torch.empty(self.cfg.vocab, dtype=torch.float32, device="cuda")
+        c = self.cfg
+        H, F, QD, KD = c.hidden, c.ffn, c.n_q_heads * 128, c.n_kv_heads * 128
+        n_glob = sum(1 for l in range(c.n_layers) if l % c.global_every == c.global_every - 1)
+        per_layer = 2 * n_tok * H * (QD + KD + F + F) + 2 * n_tok * QD * H + 2 * n_tok * F * H
+        self.mmq_ops = c.n_layers * per_layer + (c.n_layers - n_glob) * 2 * n_tok * H * KD
+        attn = lambda w: 4.0 * 128 * c.n_q_heads * sum(min(i + 1, w) if w else i + 1
+                                                     for i in range(n_tok))
+        self.attn_flops = (c.n_layers - n_glob) * attn(c.sliding_window) + n_glob * attn(0)
+
+    def step(self, i):
+        self.model.reset()
+        self.model.prefill(self.tokens, self.logits)
+
+    def result(self, ms_per_step):
+        tops = (self.mmq_ops + self.attn_flops) / (ms_per_step * 1e-3) / 1e12
+        c = self.cfg
+        return {
+            "value": self.n_tok / (ms_per_step * 1e-3), "unit": "tok/s (prefill)",
+            "dtype": "q4_0 weights x q8_0 activations (int8 MFMA), f16 attention",
+            "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": tops / INT8_PEAK_TOPS, "traffic": None,
+                         "note": "whole prefill: MMQ int8 ops + attention flops per second"},
+            "config": {"workload": f"prefill {self.n_tok} tokens from position 0, 62-layer "
+                                   "random-init decoder (BASELINE config 5)",
+                       "n_layers": c.n_layers, "hidden": c.hidden, "ffn": c.ffn,
+                       "mmq_ops": self.mmq_ops, "attn_flops": self.attn_flops},
+        }
+
+
 class Decode:
     """one bs=1 decode step of the full 62-layer random-init
     decoder at an 8K-token context, replayed as one hipGraph per step."""
@@ -348,7 +396,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv", "mmq", "splitk", "attn_prefill",
+                    choices=["decode", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -363,11 +411,13 @@ def main():
 
     ctx = sgq.GpuContext(0)
     if args.steps is None:
-        args.steps = 100 if args.workload == "decode" else 200
+        args.steps = {"decode": 100, "prefill": 5}.get(args.workload, 200)
     if args.warmup is None:
-        args.warmup = 10 if args.workload == "decode" else 20
+        args.warmup = {"decode": 10, "prefill": 1}.get(args.workload, 20)
     if args.workload == "decode":
         wl = Decode(ctx, torch)
+    elif args.workload == "prefill":
+        wl = Prefill(ctx, torch)
     elif args.workload == "gemv":
         wl = Gemv(ctx, torch)
     elif args.workload == "mmq":
