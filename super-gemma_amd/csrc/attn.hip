@@ -348,39 +348,33 @@ __global__ __launch_bounds__(QPK * kHD) void attn_merge_kernel(const float *__re
     const int h = tid / kHD, d = tid % kHD;
     const int stride = kHD + 2;
     const float *ph_part = part + (size_t)(kvh * QPK + h) * n_splits * stride;
-    float M = kNegBig;
-    int s0 = 0;
-    for (; s0 + 8 <= n_splits; s0 += 8) {
-        float mv[8];
+    // one pass: (m, l, a) of up to 64 splits loaded together, then combined
+    // in split order; more splits go through the same loop in batches with
+    // a running max (rescaling the partial sums when it grows)
+    float M = kNegBig, a = 0.f, l = 0.f;
+    for (int s0 = 0; s0 < n_splits; s0 += 16) {
+        float mv[16], lv[16], av[16];
+        const int nb = min(16, n_splits - s0);
 #pragma unroll
-        for (int u = 0; u < 8; u++) mv[u] = ph_part[(size_t)(s0 + u) * stride + kHD];
-#pragma unroll
-        for (int u = 0; u < 8; u++) M = fmaxf(M, mv[u]);
-    }
-    for (; s0 < n_splits; s0++) M = fmaxf(M, ph_part[(size_t)s0 * stride + kHD]);
-    float a = 0.f, l = 0.f;
-    s0 = 0;
-    for (; s0 + 8 <= n_splits; s0 += 8) {
-        float mv[8], lv[8], av[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float *r = ph_part + (size_t)(s0 + u) * stride;
-            mv[u] = r[kHD];
-            lv[u] = r[kHD + 1];
-            av[u] = r[d];
+        for (int u = 0; u < 16; u++) {
+            const float *r = ph_part + (size_t)(s0 + min(u, nb - 1)) * stride;
+            mv[u] = u < nb ? r[kHD] : kNegBig;
+            lv[u] = u < nb ? r[kHD + 1] : 0.f;
+            av[u] = u < nb ? r[d] : 0.f;
         }
+        float Mn = M;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float w = __expf(mv[u] - M);
+        for (int u = 0; u < 16; u++) Mn = fmaxf(Mn, mv[u]);
+        const float corr = __expf(M - Mn);
+        a *= corr;
+        l *= corr;
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const float w = __expf(mv[u] - Mn);
             a = __builtin_fmaf(av[u], w, a);
             l = __builtin_fmaf(lv[u], w, l);
         }
-    }
-    for (; s0 < n_splits; s0++) {
-        const float *r = ph_part + (size_t)s0 * stride;
-        const float w = __expf(r[kHD] - M);
-        a = __builtin_fmaf(r[d], w, a);
-        l = __builtin_fmaf(r[kHD + 1], w, l);
+        M = Mn;
     }
     const float res = a / l;
     out[(size_t)(kvh * QPK + h) * kHD + d] = res;

@@ -377,9 +377,13 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // first limb is used, so issuing the DMA first makes that one wait cover
     // both round trips at once.  The empty asm keeps the limb loads after
     // the DMA.
+    // rounds of rows this workgroup owns (the same for all its waves); only
+    // real rounds are fetched, so no wave waits on loads it never uses
+    const int rows_rounds = (n - blockIdx.x * P + G - 1) / G;
 #pragma unroll
     for (int j = 0; j < kRStages - 1; j++)
-        issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
+        if (j < rows_rounds)
+            issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
     asm volatile("" ::: "memory");
     // limbs for this lane's blocks, straight from the (L2-resident) table
     XLimbs<NBL> L;
@@ -402,12 +406,21 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
     const uint32_t sel = (lane & 1) ? 0x07060504u : 0x05040302u;
     const uint32_t dshift = (lane & 1) ? 16u : 0u;
-    const int rows_rounds = (n - blockIdx.x * P + G - 1) / G;  // same for every wave of the group
     for (int it = 0; it < rows_rounds; it++) {
         const int row = r0 + it * G;
-        issue_slice(tg, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
-                    row + (kRStages - 1) * G, n, row_bytes, slice_off, doff);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * (kRStages - 1)));
+        if (it + kRStages - 1 < rows_rounds)
+            issue_slice(tg, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
+                        row + (kRStages - 1) * G, n, row_bytes, slice_off, doff);
+        // wait for round `it`: the slices issued after it may stay in flight
+        static_assert(kRStages == 6, "the wait switch below covers 0..5 rounds ahead");
+        switch (min(kRStages - 1, rows_rounds - 1 - it)) {
+            case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 5)); break;
+            case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 4)); break;
+            case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 3)); break;
+            case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 2)); break;
+            case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 1)); break;
+            default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+        }
         uint32_t wv[NBL][5];
         lds_read_blocks<NBL>(ring + (it % kRStages) * kRSlot, boff, wv);
         float a = 0.f;
@@ -432,7 +445,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             }
         }
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // drain the clamped tail loads
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // nothing should be left; LDS is released at exit
 }
 
 template <int NBL>

@@ -119,29 +119,42 @@ __global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__res
 // post-attention: x += rmsnorm(o, w_post);            xl = limbs(rmsnorm(x, w_next))
 // post-FFN:       x = (x + rmsnorm(o, w_post))·scale;  xl = limbs(rmsnorm(x, w_next))
 // o arrives as n_parts K-slice partials (o = Σ_s o[s·hidden + i], s in order).
+// Every input is loaded up front (one memory round trip); NP = K-slice
+// partials of o, added in order.
+template <int NP>
 __global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
-    const float *__restrict__ o, int n_parts, const float *__restrict__ w_post,
-    float *__restrict__ x, const float *__restrict__ scale_ptr,
-    const float *__restrict__ w_next, int hidden, float eps, BlockLimbs *__restrict__ xl) {
+    const float *__restrict__ o, const float *__restrict__ w_post, float *__restrict__ x,
+    const float *__restrict__ scale_ptr, const float *__restrict__ w_next, int hidden, float eps,
+    BlockLimbs *__restrict__ xl) {
     __shared__ float red[2][kRowWG / kWave];
     const int n4 = hidden / 4, t = threadIdx.x;
-    float4 ov[kRowV], xv[kRowV];
+    float4 ov[kRowV][NP], xv[kRowV], wp[kRowV], wn[kRowV];
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+#pragma unroll
+            for (int p = 0; p < NP; p++)
+                ov[k][p] = reinterpret_cast<const float4 *>(o + (size_t)p * hidden)[i];
+            xv[k] = reinterpret_cast<const float4 *>(x)[i];
+            wp[k] = reinterpret_cast<const float4 *>(w_post)[i];
+            wn[k] = reinterpret_cast<const float4 *>(w_next)[i];
+        }
+    }
+    const float s = scale_ptr ? *scale_ptr : 1.f;
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < kRowV; k++) {
         const int i = t + k * kRowWG;
         if (i < n4) {
-            float4 a = reinterpret_cast<const float4 *>(o)[i];
-            for (int p = 1; p < n_parts; p++) {
-                const float4 b = reinterpret_cast<const float4 *>(o + (size_t)p * hidden)[i];
-                a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
-            }
-            ov[k] = a;
-            xv[k] = reinterpret_cast<const float4 *>(x)[i];
-            ss += sumsq4(ov[k]);
+            float4 a = ov[k][0];
+#pragma unroll
+            for (int p = 1; p < NP; p++)
+                a.x += ov[k][p].x, a.y += ov[k][p].y, a.z += ov[k][p].z, a.w += ov[k][p].w;
+            ov[k][0] = a;
+            ss += sumsq4(a);
         }
     }
-    const float s = scale_ptr ? *scale_ptr : 1.f;
     ss = wg_sum(ss, red[0]);
     const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
     float ss2 = 0.f;
@@ -149,12 +162,12 @@ __global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
     for (int k = 0; k < kRowV; k++) {
         const int i = t + k * kRowWG;
         if (i < n4) {
-            const float4 wp = reinterpret_cast<const float4 *>(w_post)[i];
+            const float4 a = ov[k][0];
             float4 r;
-            r.x = (xv[k].x + ov[k].x * inv * wp.x) * s;
-            r.y = (xv[k].y + ov[k].y * inv * wp.y) * s;
-            r.z = (xv[k].z + ov[k].z * inv * wp.z) * s;
-            r.w = (xv[k].w + ov[k].w * inv * wp.w) * s;
+            r.x = (xv[k].x + a.x * inv * wp[k].x) * s;
+            r.y = (xv[k].y + a.y * inv * wp[k].y) * s;
+            r.z = (xv[k].z + a.z * inv * wp[k].z) * s;
+            r.w = (xv[k].w + a.w * inv * wp[k].w) * s;
             xv[k] = r;
             reinterpret_cast<float4 *>(x)[i] = r;
             ss2 += sumsq4(r);
@@ -166,9 +179,8 @@ __global__ __launch_bounds__(kRowWG) void residual_norm_kernel(
     for (int k = 0; k < kRowV; k++) {
         const int i = t + k * kRowWG;
         if (i < n4) {
-            const float4 wv = reinterpret_cast<const float4 *>(w_next)[i];
-            const float4 y = make_float4(xv[k].x * inv2 * wv.x, xv[k].y * inv2 * wv.y,
-                                         xv[k].z * inv2 * wv.z, xv[k].w * inv2 * wv.w);
+            const float4 y = make_float4(xv[k].x * inv2 * wn[k].x, xv[k].y * inv2 * wn[k].y,
+                                         xv[k].z * inv2 * wn[k].z, xv[k].w * inv2 * wn[k].w);
             limbs_block8(y, i & 7, &xl[i >> 3]);
         }
     }
@@ -502,7 +514,7 @@ int record_step(sgq_model *m, float *logits) {
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
         if ((rc = launch_gemv_limbs(st, ot, xl, QD))) return rc;
-        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->o, 1,
+        hipLaunchKernelGGL(residual_norm_kernel<1>, dim3(1), dim3(kRowWG), 0, st, m->o,
                            L.post_attn_norm, m->x, (const float *)nullptr, L.ffn_norm, H, c.eps, xl);
         SGQ_HIP(hipGetLastError());
         GemvTargets gu{};
@@ -519,8 +531,15 @@ int record_step(sgq_model *m, float *logits) {
         if ((rc = launch_gemv_limbs(st, dt, xl, F))) return rc;
         const float *w_next =
             li + 1 < m->layers.size() ? m->layers[li + 1].attn_norm : m->out_norm;
-        hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kRowWG), 0, st, m->f, f_parts,
-                           L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
+        if (f_parts == 4)
+            hipLaunchKernelGGL(residual_norm_kernel<4>, dim3(1), dim3(kRowWG), 0, st, m->f,
+                               L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
+        else if (f_parts == 2)
+            hipLaunchKernelGGL(residual_norm_kernel<2>, dim3(1), dim3(kRowWG), 0, st, m->f,
+                               L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
+        else
+            hipLaunchKernelGGL(residual_norm_kernel<1>, dim3(1), dim3(kRowWG), 0, st, m->f,
+                               L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
         SGQ_HIP(hipGetLastError());
     }
     GemvTargets head{};
