@@ -272,6 +272,40 @@ int sgq_model_fill_cache(sgq_model *model, uint32_t n_tokens, uint64_t seed);
 int sgq_model_tensor(const sgq_model *model, int layer, const char *name, void **ptr,
                      uint64_t *bytes);
 
+/* ---- GGUF (crates/sg-gguf/src/parse.rs:112-210): v3 files, read-only
+ * mapped; tensors of type F32 (0), F16 (1), Q4_0 (2), Q8_0 (8), Q6_K (14);
+ * dims in ggml order (dims[0] contiguous); `data` points into the mapping
+ * and lives until sgq_gguf_close.  Malformed files fail with
+ * SGQ_ERR_VALIDATION and a message naming what is wrong. */
+typedef struct sgq_gguf sgq_gguf;
+typedef struct {
+    const char *name;
+    uint32_t type;
+    uint32_t n_dims;
+    uint64_t dims[4];
+    uint64_t offset; /* within the data section */
+    uint64_t bytes;
+    const void *data;
+} sgq_gguf_tensor;
+int sgq_gguf_open(const char *path, sgq_gguf **out);
+int sgq_gguf_close(sgq_gguf *gguf);
+uint64_t sgq_gguf_tensor_count(const sgq_gguf *gguf);
+int sgq_gguf_tensor_at(const sgq_gguf *gguf, uint64_t i, sgq_gguf_tensor *out);
+int sgq_gguf_tensor_find(const sgq_gguf *gguf, const char *name, sgq_gguf_tensor *out);
+/* Metadata: any integer type (and bool) / f32-f64 / string. */
+int sgq_gguf_meta_int(const sgq_gguf *gguf, const char *key, int64_t *out);
+int sgq_gguf_meta_float(const sgq_gguf *gguf, const char *key, double *out);
+int sgq_gguf_meta_string(const sgq_gguf *gguf, const char *key, const char **out);
+/* Upload a GGUF's weights into a model (weights.rs / desc.rs expected_tensors:
+ * token_embd, output_norm and per layer blk.N.{attn_q, attn_k, attn_v (not on
+ * K=V global layers), attn_output, attn_q_norm, attn_k_norm, attn_norm,
+ * post_attention_norm, ffn_norm, post_ffw_norm, ffn_gate, ffn_up, ffn_down,
+ * layer_output_scale}.weight).  Every tensor's type and shape is checked
+ * against the model's config before anything is written; matrices and the
+ * tied embedding must be Q4_0, norms F32.  An optional rope_freqs.weight must
+ * match global_rope_frac. */
+int sgq_model_load_gguf(sgq_model *model, const sgq_gguf *gguf);
+
 /* ---- synthetic inputs (not on the hot path; for benches and tests) ------ */
 /* Q4_0 blocks with d = f16(|N(0, sigma)|) and uniform nibble bytes, from a
  * counter-based generator keyed by (seed, block index). */

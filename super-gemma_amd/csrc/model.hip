@@ -890,6 +890,76 @@ int sgq_model_prefill(sgq_model *m, const uint32_t *tokens, uint32_t n_tokens, f
     return SGQ_OK;
 }
 
+int sgq_model_load_gguf(sgq_model *m, const sgq_gguf *g) {
+    if (!m || !g) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    const sgq_model_config &c = m->cfg;
+    const uint64_t H = c.hidden, F = c.ffn, QD = (uint64_t)c.n_q_heads * kHeadDim,
+                   KD = (uint64_t)c.n_kv_heads * kHeadDim;
+    struct Want {
+        std::string name;
+        const char *model_name;
+        int layer;
+        uint32_t type;  // 0 F32, 2 Q4_0
+        uint64_t d0, d1;
+        bool optional;
+    };
+    std::vector<Want> want = {{"token_embd.weight", "token_embd", -1, 2, H, c.vocab, false},
+                              {"output_norm.weight", "output_norm", -1, 0, H, 1, false}};
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        const bool kv_shared = m->layers[l].wv == nullptr;
+        want.push_back({b + "attn_q.weight", "attn_q", (int)l, 2, H, QD, false});
+        want.push_back({b + "attn_k.weight", "attn_k", (int)l, 2, H, KD, false});
+        if (!kv_shared) want.push_back({b + "attn_v.weight", "attn_v", (int)l, 2, H, KD, false});
+        want.push_back({b + "attn_output.weight", "attn_output", (int)l, 2, QD, H, false});
+        want.push_back({b + "attn_q_norm.weight", "attn_q_norm", (int)l, 0, kHeadDim, 1, false});
+        want.push_back({b + "attn_k_norm.weight", "attn_k_norm", (int)l, 0, kHeadDim, 1, false});
+        want.push_back({b + "attn_norm.weight", "attn_norm", (int)l, 0, H, 1, false});
+        want.push_back({b + "post_attention_norm.weight", "post_attention_norm", (int)l, 0, H, 1, false});
+        want.push_back({b + "ffn_norm.weight", "ffn_norm", (int)l, 0, H, 1, false});
+        want.push_back({b + "post_ffw_norm.weight", "post_ffw_norm", (int)l, 0, H, 1, false});
+        want.push_back({b + "ffn_gate.weight", "ffn_gate", (int)l, 2, H, F, false});
+        want.push_back({b + "ffn_up.weight", "ffn_up", (int)l, 2, H, F, false});
+        want.push_back({b + "ffn_down.weight", "ffn_down", (int)l, 2, F, H, false});
+        want.push_back({b + "layer_output_scale.weight", "layer_output_scale", (int)l, 0, 1, 1, false});
+    }
+    // Check everything before writing anything.
+    std::vector<sgq_gguf_tensor> found(want.size());
+    for (size_t i = 0; i < want.size(); i++) {
+        const Want &w = want[i];
+        if (int rc = sgq_gguf_tensor_find(g, w.name.c_str(), &found[i])) return rc;
+        const sgq_gguf_tensor &t = found[i];
+        const uint64_t t1 = t.n_dims >= 2 ? t.dims[1] : 1;
+        if (t.type != w.type || t.dims[0] != w.d0 || t1 != w.d1 || t.n_dims > 2)
+            return fail(SGQ_ERR_VALIDATION,
+                        "gguf: tensor '%s' is type %u [%llu, %llu]; the model needs type %u [%llu, %llu]",
+                        w.name.c_str(), t.type, (unsigned long long)t.dims[0], (unsigned long long)t1,
+                        w.type, (unsigned long long)w.d0, (unsigned long long)w.d1);
+    }
+    sgq_gguf_tensor rf;
+    if (sgq_gguf_tensor_find(g, "rope_freqs.weight", &rf) == SGQ_OK) {
+        // divisor factors of the global layers' partial rotation (rope.rs:13-16)
+        const int live = (int)lroundf(c.global_rope_frac * kHeadDim / 2);
+        SGQ_CHECK(rf.type == 0 && rf.dims[0] == kHeadDim / 2 && rf.n_dims == 1,
+                  "gguf: rope_freqs.weight must be F32 [%d]", kHeadDim / 2);
+        const float *f = static_cast<const float *>(rf.data);
+        for (int i = 0; i < kHeadDim / 2; i++)
+            SGQ_CHECK(i < live ? f[i] == 1.0f : f[i] >= 1e20f,
+                      "gguf: rope_freqs.weight[%d] = %g does not match global_rope_frac", i, f[i]);
+    }
+    hipStream_t st = ctx_stream(m->ctx);
+    for (size_t i = 0; i < want.size(); i++) {
+        void *dst;
+        uint64_t bytes;
+        if (int rc = sgq_model_tensor(m, want[i].layer, want[i].model_name, &dst, &bytes)) return rc;
+        SGQ_CHECK(bytes == found[i].bytes, "gguf: tensor '%s' is %llu bytes, the model's %llu",
+                  want[i].name.c_str(), (unsigned long long)found[i].bytes, (unsigned long long)bytes);
+        SGQ_HIP(hipMemcpyAsync(dst, found[i].data, bytes, hipMemcpyHostToDevice, st));
+    }
+    SGQ_HIP(hipStreamSynchronize(st));
+    return SGQ_OK;
+}
+
 int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr,
                      uint64_t *bytes) {
     if (!m || !name || !ptr || !bytes) return fail(SGQ_ERR_VALIDATION, "NULL argument");

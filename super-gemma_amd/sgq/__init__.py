@@ -86,6 +86,12 @@ class ModelConfig(C.Structure):
         return {n: getattr(self, n) for n, _ in self._fields_}
 
 
+class _GgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32),
+                ("dims", C.c_uint64 * 4), ("offset", C.c_uint64), ("bytes", C.c_uint64),
+                ("data", C.c_void_p)]
+
+
 # Exported symbols and their ctypes signatures (checked against include/sgq.h
 # by tests/test_abi.py).
 P, U32, U64, I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int
@@ -135,6 +141,15 @@ SIGNATURES = {
     "sgq_model_fill_cache": (I, [P, U32, U64]),
     "sgq_model_prefill": (I, [P, C.POINTER(U32), U32, P]),
     "sgq_model_tensor": (I, [P, I, C.c_char_p, C.POINTER(P), C.POINTER(U64)]),
+    "sgq_gguf_open": (I, [C.c_char_p, C.POINTER(P)]),
+    "sgq_gguf_close": (I, [P]),
+    "sgq_gguf_tensor_count": (U64, [P]),
+    "sgq_gguf_tensor_at": (I, [P, U64, C.POINTER(_GgufTensor)]),
+    "sgq_gguf_tensor_find": (I, [P, C.c_char_p, C.POINTER(_GgufTensor)]),
+    "sgq_gguf_meta_int": (I, [P, C.c_char_p, C.POINTER(C.c_int64)]),
+    "sgq_gguf_meta_float": (I, [P, C.c_char_p, C.POINTER(C.c_double)]),
+    "sgq_gguf_meta_string": (I, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "sgq_model_load_gguf": (I, [P, P]),
     "sgq_fill_q4_0_random": (I, [P, P, U64, U64, C.c_float]),
     "sgq_fill_normal": (I, [P, P, U64, U64, C.c_float, C.c_float]),
 }
@@ -441,6 +456,70 @@ class GraphRecorder:
         return False
 
 
+@dataclass
+class GgufTensor:
+    name: str
+    type: int
+    dims: tuple
+    offset: int
+    nbytes: int
+    data_ptr: int
+
+
+class Gguf:
+    """A GGUF v3 file (sgq_gguf_*, crates/sg-gguf/src/parse.rs): tensor table,
+    metadata, zero-copy tensor bytes.  No GPU needed."""
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        _check(lib().sgq_gguf_open(os.fsencode(path), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and _lib is not None:
+            _lib.sgq_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @staticmethod
+    def _wrap(t: _GgufTensor) -> GgufTensor:
+        return GgufTensor(t.name.decode(), t.type, tuple(t.dims[:t.n_dims]), t.offset, t.bytes,
+                          t.data)
+
+    def tensors(self):
+        out = []
+        for i in range(lib().sgq_gguf_tensor_count(self._h)):
+            t = _GgufTensor()
+            _check(lib().sgq_gguf_tensor_at(self._h, i, C.byref(t)))
+            out.append(self._wrap(t))
+        return out
+
+    def find(self, name: str) -> GgufTensor:
+        t = _GgufTensor()
+        _check(lib().sgq_gguf_tensor_find(self._h, name.encode(), C.byref(t)))
+        return self._wrap(t)
+
+    def data(self, t: GgufTensor) -> bytes:
+        return C.string_at(t.data_ptr, t.nbytes)
+
+    def meta_int(self, key: str) -> int:
+        v = C.c_int64()
+        _check(lib().sgq_gguf_meta_int(self._h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_float(self, key: str) -> float:
+        v = C.c_double()
+        _check(lib().sgq_gguf_meta_float(self._h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_string(self, key: str) -> str:
+        v = C.c_char_p()
+        _check(lib().sgq_gguf_meta_string(self._h, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+
 def default_model_config(**overrides) -> ModelConfig:
     """The benchmark decoder shape (sgq_model_default_config), with overrides."""
     cfg = ModelConfig()
@@ -494,6 +573,10 @@ class Model:
             _need(logits, torch.float32, self.cfg.vocab, "logits")
         _check(lib().sgq_model_prefill(self._h, toks.ctypes.data_as(C.POINTER(U32)), toks.size,
                                        _ptr(logits)))
+
+    def load_gguf(self, gguf: "Gguf"):
+        """Upload a GGUF's weights (sgq_model_load_gguf)."""
+        _check(lib().sgq_model_load_gguf(self._h, gguf._h))
 
     def fill_cache(self, n_tokens: int, seed: int = 0xCAC4E):
         """Synthetic Q8_0 K/V for positions [0, n_tokens); position = n_tokens."""

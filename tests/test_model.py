@@ -223,6 +223,88 @@ def test_model_prefill_full_width(ctx, oracle):
     model.close()
 
 
+def _write_model_gguf(path, cfg, oracle, seed, rope_ok=True):
+    """A GGUF holding every tensor of `cfg` (random Q4_0 matrices, N(1, .1)
+    norms) as the reference's exporter names them (desc.rs:150-193)."""
+    import struct
+
+    from _gguf import write_gguf
+
+    rng = oracle.Rng(seed)
+    H, F, hd = cfg.hidden, cfg.ffn, 128
+    QD, KD = cfg.n_q_heads * hd, cfg.n_kv_heads * hd
+
+    def q4(k, n):
+        return rng.random_q4_0(n * k // 32).tobytes()
+
+    def f32(n, mean=1.0):
+        return (np.float32(mean) + np.float32(0.1) * rng.f32_vec(n)).astype(np.float32).tobytes()
+
+    t = [("token_embd.weight", [H, cfg.vocab], "Q4_0", q4(H, cfg.vocab)),
+         ("output_norm.weight", [H], "F32", f32(H))]
+    live = int(round(cfg.global_rope_frac * hd / 2))
+    rf = [1.0] * live + [1e30] * (hd // 2 - live)
+    if not rope_ok:
+        rf[0] = 2.0
+    t.append(("rope_freqs.weight", [hd // 2], "F32", np.array(rf, np.float32).tobytes()))
+    for l in range(cfg.n_layers):
+        glob = l % cfg.global_every == cfg.global_every - 1
+        b = f"blk.{l}."
+        t += [(b + "attn_q.weight", [H, QD], "Q4_0", q4(H, QD)),
+              (b + "attn_k.weight", [H, KD], "Q4_0", q4(H, KD))]
+        if not (glob and cfg.global_k_eq_v):
+            t.append((b + "attn_v.weight", [H, KD], "Q4_0", q4(H, KD)))
+        t += [(b + "attn_output.weight", [QD, H], "Q4_0", q4(QD, H)),
+              (b + "attn_q_norm.weight", [hd], "F32", f32(hd)),
+              (b + "attn_k_norm.weight", [hd], "F32", f32(hd)),
+              (b + "attn_norm.weight", [H], "F32", f32(H)),
+              (b + "post_attention_norm.weight", [H], "F32", f32(H)),
+              (b + "ffn_norm.weight", [H], "F32", f32(H)),
+              (b + "post_ffw_norm.weight", [H], "F32", f32(H)),
+              (b + "ffn_gate.weight", [H, F], "Q4_0", q4(H, F)),
+              (b + "ffn_up.weight", [H, F], "Q4_0", q4(H, F)),
+              (b + "ffn_down.weight", [F, H], "Q4_0", q4(F, H)),
+              (b + "layer_output_scale.weight", [1], "F32", struct.pack("<f", 0.9))]
+    write_gguf(path, [("general.architecture", "str", "gemma4")], t)
+    return {name: blob for name, _, _, blob in t}
+
+
+def test_model_loads_gguf_weights(ctx, oracle, tmp_path):
+    """sgq_model_load_gguf puts every tensor in place byte for byte, and the
+    model then decodes the file's weights (vs the oracle on the same bytes);
+    a shape mismatch or a wrong rope_freqs is refused before any write."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print("model gguf load", flush=True)
+    cfg = _small_cfg(sgq, seed=0x6A)
+    path = tmp_path / "small.gguf"
+    blobs = _write_model_gguf(path, cfg, oracle, 0x66)
+    model = sgq.Model(ctx, cfg)
+    g = sgq.Gguf(str(path))
+    model.load_gguf(g)
+    assert model.read_tensor("token_embd").tobytes() == blobs["token_embd.weight"]
+    assert model.read_tensor("ffn_down", 3).tobytes() == blobs["blk.3.ffn_down.weight"]
+    assert model.read_tensor("attn_q_norm", 1).tobytes() == blobs["blk.1.attn_q_norm.weight"]
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([3, 1000, 17]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), f"gguf {i}")
+    # a file for another shape, or with the wrong rope factors, is refused
+    other = _small_cfg(sgq, hidden=768, seed=0x6A)
+    with pytest.raises(sgq.ValidationError):
+        sgq.Model(ctx, other).load_gguf(g)
+    bad = tmp_path / "bad_rope.gguf"
+    _write_model_gguf(bad, cfg, oracle, 0x66, rope_ok=False)
+    with pytest.raises(sgq.ValidationError):
+        model.load_gguf(sgq.Gguf(str(bad)))
+    g.close()
+    model.close()
+
+
 def test_model_rejects_bad_inputs(ctx):
     import sgq
 
