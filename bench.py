@@ -260,7 +260,7 @@ class Decode:
     decoder at an 8K-token context, replayed as one hipGraph per step."""
     kernel = "gemv_q4_0_ring_kernel"
 
-    def __init__(self, ctx, torch, context=8192):
+    def __init__(self, ctx, torch, context=8192, mode="kernels"):
         import sgq
 
         self.ctx, self.torch, self.sgq = ctx, torch, sgq
@@ -268,6 +268,8 @@ class Decode:
         ctx.set_stream(self.stream)
         self.cfg = sgq.default_model_config(max_ctx=16384)
         self.model = sgq.Model(ctx, self.cfg)
+        self.mode = mode
+        self.model.decode_mode = 1 if mode == "persistent" else 0
         self.context = context
         self.model.fill_cache(context)
         self.logits = torch.empty(self.cfg.vocab, dtype=torch.float32, device="cuda")
@@ -395,6 +397,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--decode-mode", default="kernels", choices=["persistent", "kernels"],
+                    help="decode workload: one persistent launch per step, or one kernel "
+                         "per operator replayed as a hipGraph")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
@@ -415,7 +420,7 @@ def main():
     if args.warmup is None:
         args.warmup = {"decode": 10, "prefill": 1}.get(args.workload, 20)
     if args.workload == "decode":
-        wl = Decode(ctx, torch)
+        wl = Decode(ctx, torch, mode=args.decode_mode)
     elif args.workload == "prefill":
         wl = Prefill(ctx, torch)
     elif args.workload == "gemv":

@@ -249,6 +249,18 @@ uint32_t sgq_model_position(const sgq_model *model);
  * replays it; the per-token inputs travel through a device step buffer. */
 int sgq_model_decode(sgq_model *model, uint32_t token, float *logits);
 int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
+/* Decode implementation (no counterpart in the reference, whose graph is one
+ * dispatch per operator, graph.rs:478-756): 0 = one kernel per operator
+ * (the _graph form captures them), 1 = one persistent cooperative launch
+ * per step whose workgroups meet at grid barriers and stream each GEMV's
+ * weights while waiting (the _graph form then launches it directly).
+ * Mode 1 fails with SGQ_ERR_VALIDATION when the shape or the device does not
+ * fit it. */
+int sgq_model_set_decode_mode(sgq_model *model, int mode);
+int sgq_model_decode_mode(const sgq_model *model);
+/* Waits for the context's stream; SGQ_ERR_HIP if a persistent step could not
+ * complete a grid barrier (its outputs are then undefined). */
+int sgq_model_status(sgq_model *model);
 /* Prefill (GpuModel::prefill, crates/sg-model/src/graph.rs:1451-1482): runs
  * the host tokens[0..n) at positions pos..pos+n-1 in chunks of
  * prefill_chunk, appends their K/V, advances the position, and writes the

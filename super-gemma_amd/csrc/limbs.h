@@ -100,7 +100,9 @@ __device__ __forceinline__ void limbs_from_values(const float (&v)[32], BlockLim
 // lane packs its 4 values into the nibbles they occupy in word (g & 3) of
 // every limb, lanes g and g^4 OR their halves, lanes g < 4 store word g and
 // lane 0 the scale.  Bit-identical to quantize_values (same amax, d, 1/d and
-// rint sequence per value).  All 8 lanes of a group must be active.
+// rint sequence per value).  All 8 lanes of a group must be active.  AGENT:
+// agent-scope stores, for a table read by other workgroups of one launch.
+template <bool AGENT = false>
 __device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *__restrict__ dst) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
@@ -125,11 +127,21 @@ __device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *
 #pragma unroll
     for (int l = 0; l < kLimbs; l++) word[l] |= (uint32_t)__shfl_xor((int)word[l], 4, 64);
     if (g < 4) {
+        if (AGENT) {
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) dst->q[l][g] = (int)word[l];
-        if (g == 0) {
-            dst->d = d * kLimbScale;
-            dst->pad[0] = dst->pad[1] = dst->pad[2] = 0;
+            for (int l = 0; l < kLimbs; l++)
+                __hip_atomic_store(&dst->q[l][g], (int)word[l], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (g == 0)
+                __hip_atomic_store(&dst->d, d * kLimbScale, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+#pragma unroll
+            for (int l = 0; l < kLimbs; l++) dst->q[l][g] = (int)word[l];
+            if (g == 0) {
+                dst->d = d * kLimbScale;
+                dst->pad[0] = dst->pad[1] = dst->pad[2] = 0;
+            }
         }
     }
 }

@@ -138,6 +138,9 @@ SIGNATURES = {
     "sgq_model_position": (U32, [P]),
     "sgq_model_decode": (I, [P, U32, P]),
     "sgq_model_decode_graph": (I, [P, U32, P]),
+    "sgq_model_set_decode_mode": (I, [P, I]),
+    "sgq_model_decode_mode": (I, [P]),
+    "sgq_model_status": (I, [P]),
     "sgq_model_fill_cache": (I, [P, U32, U64]),
     "sgq_model_prefill": (I, [P, C.POINTER(U32), U32, P]),
     "sgq_model_tensor": (I, [P, I, C.c_char_p, C.POINTER(P), C.POINTER(U64)]),
@@ -563,6 +566,19 @@ class Model:
         _need(logits, torch.float32, self.cfg.vocab, "logits")
         fn = lib().sgq_model_decode_graph if graph else lib().sgq_model_decode
         _check(fn(self._h, int(token), _ptr(logits)))
+
+    @property
+    def decode_mode(self) -> int:
+        """0: one kernel per operator; 1: one persistent launch per step."""
+        return int(lib().sgq_model_decode_mode(self._h))
+
+    @decode_mode.setter
+    def decode_mode(self, mode: int):
+        _check(lib().sgq_model_set_decode_mode(self._h, int(mode)))
+
+    def status(self):
+        """Wait for the stream; raises if a persistent step failed."""
+        _check(lib().sgq_model_status(self._h))
 
     def prefill(self, tokens, logits: Optional[torch.Tensor] = None):
         """Run a prompt (host token ids) through the model at the current
