@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // x by gemv_prep_x_kernel, or by a producer kernel that fuses it), so the
 // GEMV itself does no quantization and no LDS table.
 //
-// Each wave owns a private ring of kRStages LDS slots and streams exactly
+// Each wave owns a private ring of kGStages LDS slots and streams exactly
 // the row slices it reduces with global_load_lds_dwordx4 (a lane moves 16 B
 // straight into LDS; the data never occupies VGPRs, so ~5 slices per wave,
 // ~120 KB per CU, stay in flight without hurting occupancy).  A wave waits
@@ -169,7 +169,12 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // (one barrier per row).
 // ---------------------------------------------------------------------------
 constexpr int kRWG = 256;                       // 4 waves
-constexpr int kRLds = (kRWG / kWave) * kRStages * kRSlot + 64;  // 72 KB + 2×4 partials
+// Three slots (two slices in flight per wave, 12 MB over the chip) beat
+// deeper rings: with more in flight every wave's first slices arrive in one
+// burst and the waves then compute in lockstep while the stream idles
+// (measured at K=5376, N=21504: 14.1 us with 3 slots, 15.8 us with 6).
+constexpr int kGStages = 3;
+constexpr int kRLds = (kRWG / kWave) * kGStages * kRSlot + 64;  // 36 KB + 2×4 partials
 
 // Row r of the concatenated targets -> (matrix, local row).
 __device__ __forceinline__ int target_of(const GemvTargets &tg, int row, int *local) {
@@ -231,8 +236,8 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const int s = wave % S;              // K-slice of this wave
     const int rw = wave / S;             // row within the workgroup's row group
     const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
-    uint8_t *ring = gemv_smem + wave * (kRStages * kRSlot);
-    uint8_t *red = gemv_smem + (kRWG / kWave) * kRStages * kRSlot;  // [2][4] floats
+    uint8_t *ring = gemv_smem + wave * (kGStages * kRSlot);
+    uint8_t *red = gemv_smem + (kRWG / kWave) * kGStages * kRSlot;  // [2][4] floats
     const size_t row_bytes = (size_t)nb * 18;
     const int b0 = s * slice;
     const int slice_blocks = min(slice, nb - b0);
@@ -256,7 +261,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // real rounds are fetched, so no wave waits on loads it never uses
     const int rows_rounds = (n - blockIdx.x * P + G - 1) / G;
 #pragma unroll
-    for (int j = 0; j < kRStages - 1; j++)
+    for (int j = 0; j < kGStages - 1; j++)
         if (j < rows_rounds)
             issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
     asm volatile("" ::: "memory");
@@ -283,21 +288,18 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const uint32_t dshift = (lane & 1) ? 16u : 0u;
     for (int it = 0; it < rows_rounds; it++) {
         const int row = r0 + it * G;
-        if (it + kRStages - 1 < rows_rounds)
-            issue_slice(tg, ring + ((it + kRStages - 1) % kRStages) * kRSlot,
-                        row + (kRStages - 1) * G, n, row_bytes, slice_off, doff);
+        if (it + kGStages - 1 < rows_rounds)
+            issue_slice(tg, ring + ((it + kGStages - 1) % kGStages) * kRSlot,
+                        row + (kGStages - 1) * G, n, row_bytes, slice_off, doff);
         // wait for round `it`: the slices issued after it may stay in flight
-        static_assert(kRStages == 6, "the wait switch below covers 0..5 rounds ahead");
-        switch (min(kRStages - 1, rows_rounds - 1 - it)) {
-            case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 5)); break;
-            case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 4)); break;
-            case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 3)); break;
+        static_assert(kGStages == 3, "the wait switch below covers 0..2 rounds ahead");
+        switch (min(kGStages - 1, rows_rounds - 1 - it)) {
             case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 2)); break;
             case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 1)); break;
             default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
         }
         uint32_t wv[NBL][5];
-        lds_read_blocks<NBL>(ring + (it % kRStages) * kRSlot, boff, wv);
+        lds_read_blocks<NBL>(ring + (it % kGStages) * kRSlot, boff, wv);
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < NBL; i++) a += block_dot(wv[i], sel, dshift, L, i);
@@ -339,7 +341,7 @@ int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int
                 int slice) {
     if (int rc = ring_attr<NBL>()) return rc;
     const int P = (kRWG / kWave) / S;
-    int grid = device_info().cus * 2;  // two 72 KB workgroups per CU
+    int grid = device_info().cus * 2;  // two workgroups (8 waves) per CU
     const int max_grid = (n + P - 1) / P;
     if (grid > max_grid) grid = max_grid;
     hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL>), dim3(grid), dim3(kRWG), kRLds, st, tg, xl,
