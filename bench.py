@@ -269,7 +269,7 @@ class Decode:
         self.cfg = sgq.default_model_config(max_ctx=16384)
         self.model = sgq.Model(ctx, self.cfg)
         self.mode = mode
-        self.model.decode_mode = 1 if mode == "persistent" else 0
+        self.model.decode_mode = {"kernels": 0, "persistent": 1, "fused": 2}[mode]
         self.context = context
         self.model.fill_cache(context)
         self.logits = torch.empty(self.cfg.vocab, dtype=torch.float32, device="cuda")
@@ -397,7 +397,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--decode-mode", default="kernels", choices=["persistent", "kernels"],
+    ap.add_argument("--decode-mode", default="kernels", choices=["persistent", "kernels", "fused"],
                     help="decode workload: one persistent launch per step, or one kernel "
                          "per operator replayed as a hipGraph")
     ap.add_argument("--workload", default="decode",

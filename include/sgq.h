@@ -253,7 +253,10 @@ int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
  * dispatch per operator, graph.rs:478-756): 0 = one kernel per operator
  * (the _graph form captures them), 1 = one persistent cooperative launch
  * per step whose workgroups meet at grid barriers and stream each GEMV's
- * weights while waiting (the _graph form then launches it directly).
+ * weights while waiting (the _graph form then launches it directly),
+ * 2 = five launches per layer (QKV, attention, O, gate/up, down GEMVs) with
+ * the norms, residual updates, GeGLU and the split merge fused into them
+ * (the _graph form captures them).
  * Mode 1 fails with SGQ_ERR_VALIDATION when the shape or the device does not
  * fit it. */
 int sgq_model_set_decode_mode(sgq_model *model, int mode);

@@ -42,6 +42,9 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void st_agent(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 constexpr size_t attn_lds_bytes(int qpk, int wg) {
     return (size_t)wg * kHD + (size_t)qpk * wg * 4 + (size_t)wg * 8;
@@ -345,8 +348,9 @@ __device__ __forceinline__ void attn_split(
 // Merge of kv head `kvh`'s partials by the workgroup's first QPK·kHD
 // threads (thread (h, d)); all threads must call (one barrier when limbs
 // are written).  `out` and `limbs_out` may each be null; AGENT selects
-// agent-scope stores for the limbs (read by other workgroups of the same
-// launch).
+// agent-scope loads of the partials (written by other workgroups of the
+// same launch) and agent-scope stores for the limbs (read by other
+// workgroups of the same launch).
 template <int QPK, bool AGENT>
 __device__ __forceinline__ void attn_merge(const float *__restrict__ part, int n_splits, int kvh,
                                            float *__restrict__ out,
@@ -367,9 +371,12 @@ __device__ __forceinline__ void attn_merge(const float *__restrict__ part, int n
 #pragma unroll
             for (int u = 0; u < 16; u++) {
                 const float *r = ph_part + (size_t)(s0 + min(u, nb - 1)) * stride;
-                mv[u] = u < nb ? r[kHD] : kNegBig;
-                lv[u] = u < nb ? r[kHD + 1] : 0.f;
-                av[u] = u < nb ? r[d] : 0.f;
+                const float m_ = AGENT ? ld_agent(r + kHD) : r[kHD];
+                const float l_ = AGENT ? ld_agent(r + kHD + 1) : r[kHD + 1];
+                const float a_ = AGENT ? ld_agent(r + d) : r[d];
+                mv[u] = u < nb ? m_ : kNegBig;
+                lv[u] = u < nb ? l_ : 0.f;
+                av[u] = u < nb ? a_ : 0.f;
             }
             float Mn = M;
 #pragma unroll

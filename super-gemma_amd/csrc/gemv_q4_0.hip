@@ -174,7 +174,6 @@ constexpr int kRWG = 256;                       // 4 waves
 // burst and the waves then compute in lockstep while the stream idles
 // (measured at K=5376, N=21504: 14.1 us with 3 slots, 15.8 us with 6).
 constexpr int kGStages = 3;
-constexpr int kRLds = (kRWG / kWave) * kGStages * kRSlot + 64;  // 36 KB + 2×4 partials
 
 // Row r of the concatenated targets -> (matrix, local row).
 __device__ __forceinline__ int target_of(const GemvTargets &tg, int row, int *local) {
@@ -220,16 +219,106 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
     tg.y[j][local] = v;
 }
 
+// LDS of the streamed kernel: the wave rings, then 64 B of row partials,
+// 256 B of cross-wave scratch, then (prologues only) the x limb table.
+constexpr int kRingBytes = (kRWG / kWave) * kGStages * kRSlot;
+constexpr int kRedOff = kRingBytes;
+constexpr int kScrOff = kRedOff + 64;
+constexpr int kTabOff = kScrOff + 256;
+constexpr int kRLds = kTabOff;
+constexpr int kMaxTabBlocks = 3 * kWave;  // one slice: <= 192 blocks
+constexpr int kGegluUnits = 32;           // units (gate/up row pairs) per workgroup
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_write_f32x4(uint8_t *p, float4 v) {
+    const uint32_t a = (uint32_t)(uintptr_t)p;
+    const f32x4_t t = {v.x, v.y, v.z, v.w};
+    asm volatile("ds_write_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : : "v"(a), "v"(t) : "memory");
+}
+__device__ __forceinline__ float4 lds_read_f32x4(const uint8_t *p) {
+    const uint32_t a = (uint32_t)(uintptr_t)p;
+    f32x4_t v;
+    asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a) : "memory");
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void lds_write_u32(uint8_t *p, uint32_t v) {
+    const uint32_t a = (uint32_t)(uintptr_t)p;
+    asm volatile("ds_write_b32 %0, %1" : : "v"(a), "v"(v) : "memory");
+}
+// Workgroup barrier for LDS written with the asm stores above: waits for
+// this wave's LDS traffic only (vector memory, i.e. the weight DMA, keeps
+// streaming).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+}
+
+// Values passed through an empty asm: to the compiler they are defined here,
+// so a load behind them is waited for here (before the weight stream
+// starts) and not at their first use, where the compiler, which cannot
+// count the stream's LDS DMA together with ordinary loads, would wait for
+// everything in flight.
+__device__ __forceinline__ void settle(float &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void settle(uint32_t &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void settle(float4 &v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
+// An 8-lane group's limb block into an LDS table entry (BlockLimbs layout).
+__device__ __forceinline__ void limbs_block8_lds(const float4 v, int g, uint8_t *dst) {
+    uint32_t word[kLimbs];
+    const float d = limbs_words8(v, g, word);
+    if (g < 4) {
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) lds_write_u32(dst + (l * 4 + g) * 4, word[l]);
+        if (g == 0) lds_write_u32(dst + 64, __builtin_bit_cast(uint32_t, d));
+    }
+}
+
+__device__ __forceinline__ float gelu_tanh_g(float x) {
+    const float k = 0.7978845608028654f;
+    return 0.5f * x * (1.f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+// Sum of float4s over the workgroup in a fixed order (every workgroup that
+// sums the same inputs gets the same bits): lanes in DPP order, then the
+// four waves in order through `scr`.
+__device__ __forceinline__ float4 wg_sum4(float4 v, uint8_t *scr) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    v.x = wave_sum_dpp(v.x);
+    v.y = wave_sum_dpp(v.y);
+    v.z = wave_sum_dpp(v.z);
+    v.w = wave_sum_dpp(v.w);
+    if (lane == 0) lds_write_f32x4(scr + wave * 16, v);
+    lds_barrier();
+    float4 r = lds_read_f32x4(scr);
+#pragma unroll
+    for (int w = 1; w < kRWG / kWave; w++) {
+        const float4 t = lds_read_f32x4(scr + w * 16);
+        r.x += t.x, r.y += t.y, r.z += t.z, r.w += t.w;
+    }
+    lds_barrier();  // scr may be reused
+    return r;
+}
+
 // Rows of up to kGemvMaxTargets matrices sharing x (e.g. Q/K/V, gate/up) are
 // one concatenated row space: one launch, one x table.  Everything that
 // depends only on the wave (its K-slice, its rows, the DMA sources) is
 // computed in scalar registers; the VALU does the block dots and the DPP
 // reduction.  Lanes past the slice's last block read a genuine block of the
 // slot (block 0 or 1, so its scale is a finite f16) against zero limbs.
-template <int NBL>
+//
+// PRO/EPI select the fused prologue and epilogue (kPro*, kEpi*).  The
+// prologue's global loads are issued before the weight stream's first
+// slices (vector memory completes in order, so anything loaded after the
+// stream started would wait for it), and everything it puts in LDS goes
+// through asm accesses, so that the compiler, which cannot tell the table
+// from ring slots still being filled, does not drain the stream first.
+template <int NBL, int PRO, int EPI>
 __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
                                                               const BlockLimbs *__restrict__ xl,
-                                                              int n, int nb, int S, int slice) {
+                                                              int n, int nb, int S, int slice,
+                                                              GemvFuse fz) {
     extern __shared__ __align__(16) uint8_t gemv_smem[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -237,7 +326,9 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const int rw = wave / S;             // row within the workgroup's row group
     const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
     uint8_t *ring = gemv_smem + wave * (kGStages * kRSlot);
-    uint8_t *red = gemv_smem + (kRWG / kWave) * kGStages * kRSlot;  // [2][4] floats
+    uint8_t *red = gemv_smem + kRedOff;  // [2][4] floats
+    uint8_t *scr = gemv_smem + kScrOff;
+    uint8_t *tab = gemv_smem + kTabOff;
     const size_t row_bytes = (size_t)nb * 18;
     const int b0 = s * slice;
     const int slice_blocks = min(slice, nb - b0);
@@ -245,6 +336,8 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const int slice_bytes = slice_blocks * 18;
     const int G = gridDim.x * P;         // rows advanced per iteration by the grid
     const int r0 = blockIdx.x * P + rw;
+    constexpr int kUnitsPerWave = kGegluUnits / (kRWG / kWave);
+    const int u0 = blockIdx.x * kGegluUnits + wave * kUnitsPerWave;  // kEpiGeglu
 
     int doff[kRLoads];
 #pragma unroll
@@ -252,45 +345,243 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         const int off = (i * kWave + lane) * 16;
         doff[i] = off + 16 > slice_bytes ? 0 : off;
     }
-    // Ring prologue first, then the limbs: the compiler cannot order LDS DMA
-    // against ordinary loads and waits for everything (vmcnt(0)) before the
-    // first limb is used, so issuing the DMA first makes that one wait cover
-    // both round trips at once.  The empty asm keeps the limb loads after
-    // the DMA.
     // rounds of rows this workgroup owns (the same for all its waves); only
     // real rounds are fetched, so no wave waits on loads it never uses
-    const int rows_rounds = (n - blockIdx.x * P + G - 1) / G;
+    const int rows_rounds =
+        EPI == kEpiGeglu ? 2 * kUnitsPerWave : (n - blockIdx.x * P + G - 1) / G;
+    // the weight slice of round `it` into ring slot `slot`
+    auto issue = [&](int it) {
+        uint8_t *slot = ring + (it % kGStages) * kRSlot;
+        if (EPI == kEpiGeglu) {
+            const uint8_t *w = static_cast<const uint8_t *>((it & 1) ? tg.w[1] : tg.w[0]);
+            const uint8_t *src = w + (size_t)(u0 + (it >> 1)) * row_bytes + slice_off;
 #pragma unroll
-    for (int j = 0; j < kGStages - 1; j++)
-        if (j < rows_rounds)
-            issue_slice(tg, ring + j * kRSlot, r0 + j * G, n, row_bytes, slice_off, doff);
+            for (int i = 0; i < kRLoads; i++)
+                __builtin_amdgcn_global_load_lds((gvoid_t *)(src + doff[i]),
+                                                 (lvoid_t *)(slot + i * kWave * 16), 16, 0, 0);
+        } else {
+            issue_slice(tg, slot, r0 + it * G, n, row_bytes, slice_off, doff);
+        }
+    };
+
+    // ---- prologue loads (before the stream) --------------------------------
+    constexpr int kPB = (kMaxTabBlocks + 31) / 32;  // blocks per 8-lane group
+    const int grp = threadIdx.x >> 3, ge = threadIdx.x & 7;
+    float4 pv[kGemvMaxPartials / kRWG];
+    float4 av[kPB], bv[kPB], xo_in, xo_u;
+    uint32_t eq[kPB];  // kProEmbed: 4 nibble bytes of the lane's values
+    float ed[kPB];
+    const int H4 = nb * 8;  // float4s of x
+    const int per4 = (H4 + gridDim.x - 1) / gridDim.x;
+    const int xo_i = blockIdx.x * per4 + (int)threadIdx.x;  // this thread's x_out float4
+    const bool xo_on = fz.x_out != nullptr && (int)threadIdx.x < per4 && xo_i < H4;
+    // (branch-free: indices are clamped and the extra values ignored, so the
+    // compiler can count exactly which loads each later wait needs)
+    float s_pre = 1.f;
+    if (PRO == kProNorm) {
+#pragma unroll
+        for (int k = 0; k < kGemvMaxPartials / kRWG; k++) {
+            const int i = (int)threadIdx.x + k * kRWG;
+            pv[k] = fz.part[i < fz.np ? i : 0];
+        }
+#pragma unroll
+        for (int k = 0; k < kPB; k++) {
+            const int b = min(grp + 32 * k, nb - 1);
+            av[k] = reinterpret_cast<const float4 *>(fz.A)[b * 8 + ge];
+            bv[k] = reinterpret_cast<const float4 *>(fz.B)[b * 8 + ge];
+        }
+        if (fz.x_out) {  // uniform
+            const int i = xo_on ? xo_i : 0;
+            xo_in = reinterpret_cast<const float4 *>(fz.x_in)[i];
+            xo_u = reinterpret_cast<const float4 *>(fz.u)[i];
+        }
+        if (fz.scale) s_pre = *fz.scale;
+    } else if (PRO == kProEmbed) {
+        const uint8_t *er = fz.embd + (size_t)fz.step[4] * nb * 18;
+#pragma unroll
+        for (int k = 0; k < kPB; k++) {
+            const int b = min(grp + 32 * k, nb - 1);
+            const uint8_t *blk = er + b * 18;
+            const uint8_t *qs = blk + 2 + ((4 * ge) & 15);
+            ed[k] = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+            eq[k] = (uint32_t)qs[0] | ((uint32_t)qs[1] << 8) | ((uint32_t)qs[2] << 16) |
+                    ((uint32_t)qs[3] << 24);
+            av[k] = reinterpret_cast<const float4 *>(fz.w)[b * 8 + ge];
+        }
+    }
+    // kEpiResid: lane j holds the per-row inputs of round j
+    float ex = 0.f, ewp = 0.f, ewn = 0.f;
+    if (EPI == kEpiResid) {
+        int row = r0 + lane * G;
+        row = lane < rows_rounds && row < n ? row : 0;
+        ex = fz.x_res[row];
+        ewp = fz.w_post[row];
+        ewn = fz.w_next[row];
+    }
+
+    // The prologue's inputs are waited for before the stream starts (about
+    // one L2/MALL round trip), then turned into limbs while the first slices
+    // are in flight.
+    if (PRO != kProTable) {
+        if (PRO == kProNorm) {
+#pragma unroll
+            for (int k = 0; k < kGemvMaxPartials / kRWG; k++) settle(pv[k]);
+            if (fz.x_out) {
+                settle(xo_in);
+                settle(xo_u);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kPB; k++) {
+                settle(ed[k]);
+                settle(eq[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kPB; k++) {
+            settle(av[k]);
+            if (PRO == kProNorm) settle(bv[k]);
+        }
+        if (EPI == kEpiResid) {
+            settle(ex);
+            settle(ewp);
+            settle(ewn);
+        }
+    }
+
+    // ---- the stream starts ------------------------------------------------
+    // (unconditional: a missing round loads row 0, which keeps the number of
+    // loads in flight known to the compiler's wait counting)
+#pragma unroll
+    for (int j = 0; j < kGStages - 1; j++) issue(j);
     asm volatile("" ::: "memory");
-    // limbs for this lane's blocks, straight from the (L2-resident) table
+
     XLimbs<NBL> L;
     int boff[NBL];
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int lb = lane + kWave * i;
-        const bool valid = lb < slice_blocks;
-        boff[i] = valid ? lb * 18 - (lane & 1) * 2 : (lane & 1) * 16;
-        BlockLimbs t = valid ? xl[b0 + lb] : BlockLimbs{};
-#pragma unroll
-        for (int l = 0; l < kLimbs; l++)
-#pragma unroll
-            for (int w = 0; w < 4; w++) L.q[i][l][w] = t.q[l][w];
-        L.d[i] = t.d;
+        boff[i] = lb < slice_blocks ? lb * 18 - (lane & 1) * 2 : (lane & 1) * 16;
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    if (PRO == kProTable) {
+        // limbs for this lane's blocks, straight from the (L2-resident) table
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int lb = lane + kWave * i;
+            BlockLimbs t = lb < slice_blocks ? xl[b0 + lb] : BlockLimbs{};
+#pragma unroll
+            for (int l = 0; l < kLimbs; l++)
+#pragma unroll
+                for (int w = 0; w < 4; w++) L.q[i][l][w] = t.q[l][w];
+            L.d[i] = t.d;
+        }
+        // the DMA prologue was issued first, so this one wait covers both
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        if (EPI == kEpiResid) {
+            settle(ex);
+            settle(ewp);
+            settle(ewn);
+        }
+    } else {
+        float rb_s = 1.f;  // scale of the values that go into the table
+        float ra = 0.f, s_out = 1.f;
+        if (PRO == kProNorm) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < kGemvMaxPartials / kRWG; k++)
+                if ((int)threadIdx.x + k * kRWG < fz.np)  // past np: a clamped duplicate
+                    acc.x += pv[k].x, acc.y += pv[k].y, acc.z += pv[k].z, acc.w += pv[k].w;
+            const float4 P4 = wg_sum4(acc, scr);
+            const float K = (float)(nb * 32);
+            s_out = s_pre;
+            ra = 1.0f / sqrtf(P4.x / K + fz.eps);
+            const float sx = s_out * s_out * (P4.w + 2.f * ra * P4.y + ra * ra * P4.z);
+            const float rb = 1.0f / sqrtf(sx / K + fz.eps);
+            rb_s = rb * s_out;
+#pragma unroll
+            for (int k = 0; k < kPB; k++) {
+                const int b = grp + 32 * k;
+                if (b < nb) {
+                    const float4 v = make_float4((av[k].x + ra * bv[k].x) * rb_s,
+                                                 (av[k].y + ra * bv[k].y) * rb_s,
+                                                 (av[k].z + ra * bv[k].z) * rb_s,
+                                                 (av[k].w + ra * bv[k].w) * rb_s);
+                    limbs_block8_lds(v, ge, tab + b * 80);
+                }
+            }
+            if (xo_on)
+                reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
+                    make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
+                                s_out * (xo_in.z + ra * xo_u.z), s_out * (xo_in.w + ra * xo_u.w));
+        } else {  // kProEmbed
+            float4 x0[kPB];
+            float ss = 0.f;
+            const int sh = ge < 4 ? 0 : 4;
+#pragma unroll
+            for (int k = 0; k < kPB; k++) {
+                const int b = grp + 32 * k;
+                x0[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (b < nb) {
+                    float e[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        e[u] = ed[k] * (float)((int)((eq[k] >> (8 * u + sh)) & 15u) - 8) *
+                               fz.embed_scale;
+                    x0[k] = make_float4(e[0], e[1], e[2], e[3]);
+                    ss += x0[k].x * x0[k].x + x0[k].y * x0[k].y + x0[k].z * x0[k].z +
+                          x0[k].w * x0[k].w;
+                    const int i4 = b * 8 + ge;
+                    if (fz.x_out && i4 >= blockIdx.x * per4 && i4 < (blockIdx.x + 1) * per4)
+                        reinterpret_cast<float4 *>(fz.x_out)[i4] = x0[k];
+                }
+            }
+            const float4 t = wg_sum4(make_float4(ss, 0.f, 0.f, 0.f), scr);
+            const float r = 1.0f / sqrtf(t.x / (float)(nb * 32) + fz.eps);
+#pragma unroll
+            for (int k = 0; k < kPB; k++) {
+                const int b = grp + 32 * k;
+                if (b < nb) {
+                    const float4 v = make_float4(x0[k].x * r * av[k].x, x0[k].y * r * av[k].y,
+                                                 x0[k].z * r * av[k].z, x0[k].w * r * av[k].w);
+                    limbs_block8_lds(v, ge, tab + b * 80);
+                }
+            }
+        }
+        lds_barrier();
+        // this lane's blocks from the LDS table
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int lb = lane + kWave * i;
+            if (lb < slice_blocks) {
+                const uint8_t *e = tab + (b0 + lb) * 80;
+#pragma unroll
+                for (int l = 0; l < kLimbs; l++) {
+                    const float4 q = lds_read_f32x4(e + l * 16);
+                    L.q[i][l][0] = __builtin_bit_cast(int, q.x);
+                    L.q[i][l][1] = __builtin_bit_cast(int, q.y);
+                    L.q[i][l][2] = __builtin_bit_cast(int, q.z);
+                    L.q[i][l][3] = __builtin_bit_cast(int, q.w);
+                }
+                L.d[i] = lds_read_f32(e + 64);
+            } else {
+#pragma unroll
+                for (int l = 0; l < kLimbs; l++)
+#pragma unroll
+                    for (int w = 0; w < 4; w++) L.q[i][l][w] = 0;
+                L.d[i] = 0.f;
+            }
+        }
+    }
 
     // lb even: qs = bytes 2..17 of the window, d = low half of word 0;
     // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
     const uint32_t sel = (lane & 1) ? 0x07060504u : 0x05040302u;
     const uint32_t dshift = (lane & 1) ? 16u : 0u;
+    float p1 = 0.f, p2 = 0.f, p3 = 0.f, p4 = 0.f;  // kEpiResid partial sums
+    float gate = 0.f;                              // kEpiGeglu
     for (int it = 0; it < rows_rounds; it++) {
         const int row = r0 + it * G;
-        if (it + kGStages - 1 < rows_rounds)
-            issue_slice(tg, ring + ((it + kGStages - 1) % kGStages) * kRSlot,
-                        row + (kGStages - 1) * G, n, row_bytes, slice_off, doff);
+        if (it + kGStages - 1 < rows_rounds) issue(it + kGStages - 1);
         // wait for round `it`: the slices issued after it may stay in flight
         static_assert(kGStages == 3, "the wait switch below covers 0..2 rounds ahead");
         switch (min(kGStages - 1, rows_rounds - 1 - it)) {
@@ -304,48 +595,108 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
 #pragma unroll
         for (int i = 0; i < NBL; i++) a += block_dot(wv[i], sel, dshift, L, i);
         a = wave_sum_dpp(a);
-        if (S == 1) {
-            if (lane == 0 && row < n) store_row(tg, row, a);
-        } else if (tg.split_out) {
-            if (lane == 0 && row < n) tg.y[0][(size_t)s * n + row] = a;
-        } else {
+        if (EPI == kEpiGeglu) {
+            if ((it & 1) == 0) {
+                gate = a;
+            } else if (lane == 0) {
+                lds_write_u32(scr + (wave * kUnitsPerWave + (it >> 1)) * 4,
+                              __builtin_bit_cast(uint32_t, gelu_tanh_g(gate) * a));
+            }
+            continue;
+        }
+        bool have = true;
+        if (S > 1 && !(EPI == kEpiRows && tg.split_out)) {
             // one barrier per row: partials alternate between two slots, and
             // a slot is rewritten only after the next row's barrier, which
             // the reading wave reaches after its reads
             uint8_t *rb = red + (it & 1) * 16;
             if (lane == 0) lds_write_f32(rb + wave * 4, a);
             __builtin_amdgcn_s_barrier();
-            if (s == 0 && lane == 0 && row < n) {
+            have = s == 0;
+            if (have) {
                 float v = 0.f;
                 for (int q = 0; q < S; q++) v += lds_read_f32(rb + (rw * S + q) * 4);
-                store_row(tg, row, v);
+                a = v;
             }
+        }
+        if (!have || row >= n) continue;
+        if (EPI == kEpiResid) {
+            const float x = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), it));
+            const float wp = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ewp), it));
+            const float wn = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ewn), it));
+            const float u = a * wp;
+            p1 += a * a;
+            p2 += x * u;
+            p3 += u * u;
+            p4 += x * x;
+            if (lane == 0) {
+                fz.u_out[row] = u;
+                fz.A_out[row] = x * wn;
+                fz.B_out[row] = u * wn;
+            }
+        } else if (S == 1) {
+            if (lane == 0) store_row(tg, row, a);
+        } else if (tg.split_out) {
+            if (lane == 0) tg.y[0][(size_t)s * n + row] = a;
+        } else {
+            if (lane == 0) store_row(tg, row, a);
+        }
+    }
+    if (EPI == kEpiResid) {
+        // the workgroup's partial sums, waves in order
+        if (lane == 0) lds_write_f32x4(scr + wave * 16, make_float4(p1, p2, p3, p4));
+        lds_barrier();
+        if (threadIdx.x == 0) {
+            float4 r = lds_read_f32x4(scr);
+#pragma unroll
+            for (int w = 1; w < kRWG / kWave; w++) {
+                const float4 t = lds_read_f32x4(scr + w * 16);
+                r.x += t.x, r.y += t.y, r.z += t.z, r.w += t.w;
+            }
+            fz.part_out[blockIdx.x] = r;
+        }
+    } else if (EPI == kEpiGeglu) {
+        lds_barrier();
+        if (threadIdx.x < 8) {
+            const float4 h = lds_read_f32x4(scr + threadIdx.x * 16);
+            limbs_block8(h, (int)threadIdx.x, &fz.hl[blockIdx.x]);
         }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // nothing should be left; LDS is released at exit
 }
 
-template <int NBL>
+constexpr int lds_bytes(int pro, int nb) { return kRLds + (pro != kProTable ? nb * 80 : 0); }
+
+template <int NBL, int PRO, int EPI>
 int ring_attr() {
     static bool attr = false;
     if (!attr) {
-        SGQ_HIP(hipFuncSetAttribute((const void *)gemv_q4_0_ring_kernel<NBL>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, kRLds));
+        SGQ_HIP(hipFuncSetAttribute((const void *)gemv_q4_0_ring_kernel<NBL, PRO, EPI>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    lds_bytes(PRO, kMaxTabBlocks)));
         attr = true;
     }
     return SGQ_OK;
 }
 
-template <int NBL>
-int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n, int nb, int S,
-                int slice) {
-    if (int rc = ring_attr<NBL>()) return rc;
+int ring_grid(int n, int S, int epi) {
+    if (epi == kEpiGeglu) return n / kGegluUnits;
     const int P = (kRWG / kWave) / S;
     int grid = device_info().cus * 2;  // two workgroups (8 waves) per CU
     const int max_grid = (n + P - 1) / P;
-    if (grid > max_grid) grid = max_grid;
-    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL>), dim3(grid), dim3(kRWG), kRLds, st, tg, xl,
-                       n, nb, S, slice);
+    return grid > max_grid ? max_grid : grid;
+}
+
+template <int NBL, int PRO, int EPI>
+int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n, int nb, int S,
+                int slice, const GemvFuse &fz) {
+    if (int rc = ring_attr<NBL, PRO, EPI>()) return rc;
+    const int grid = ring_grid(n, S, EPI);
+    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL, PRO, EPI>), dim3(grid), dim3(kRWG),
+                       lds_bytes(PRO, nb), st, tg, xl, n, nb, S, slice, fz);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }
@@ -387,19 +738,88 @@ static bool ring_geometry(int nb, int *S_out, int *slice_out) {
     return true;
 }
 
-static int launch_ring_any(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n,
-                           int nb, int S, int slice) {
+template <int PRO, int EPI>
+static int launch_ring_nbl(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n,
+                           int nb, int S, int slice, const GemvFuse &fz) {
     const int nbl = (slice + kWave - 1) / kWave;
-    if (nbl == 1) return launch_ring<1>(st, tg, xl, n, nb, S, slice);
-    if (nbl == 2) return launch_ring<2>(st, tg, xl, n, nb, S, slice);
-    return launch_ring<3>(st, tg, xl, n, nb, S, slice);
+    if (nbl == 1) return launch_ring<1, PRO, EPI>(st, tg, xl, n, nb, S, slice, fz);
+    if (nbl == 2) return launch_ring<2, PRO, EPI>(st, tg, xl, n, nb, S, slice, fz);
+    return launch_ring<3, PRO, EPI>(st, tg, xl, n, nb, S, slice, fz);
+}
+
+static int launch_ring_any(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n,
+                           int nb, int S, int slice, int pro = kProTable, int epi = kEpiRows,
+                           const GemvFuse &fz = GemvFuse{}) {
+    if (pro == kProTable && epi == kEpiRows)
+        return launch_ring_nbl<kProTable, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProNorm && epi == kEpiRows)
+        return launch_ring_nbl<kProNorm, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProEmbed && epi == kEpiRows)
+        return launch_ring_nbl<kProEmbed, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProNorm && epi == kEpiGeglu)
+        return launch_ring_nbl<kProNorm, kEpiGeglu>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProTable && epi == kEpiResid)
+        return launch_ring_nbl<kProTable, kEpiResid>(st, tg, xl, n, nb, S, slice, fz);
+    return fail(SGQ_ERR_VALIDATION, "gemv (fused): prologue %d with epilogue %d not built", pro,
+                epi);
+}
+
+template <int PRO, int EPI>
+static int attr_nbl() {
+    int rc = ring_attr<1, PRO, EPI>();
+    if (!rc) rc = ring_attr<2, PRO, EPI>();
+    if (!rc) rc = ring_attr<3, PRO, EPI>();
+    return rc;
 }
 
 int gemv_prepare() {
-    int rc = ring_attr<1>();
-    if (!rc) rc = ring_attr<2>();
-    if (!rc) rc = ring_attr<3>();
+    int rc = attr_nbl<kProTable, kEpiRows>();
+    if (!rc) rc = attr_nbl<kProNorm, kEpiRows>();
+    if (!rc) rc = attr_nbl<kProEmbed, kEpiRows>();
+    if (!rc) rc = attr_nbl<kProNorm, kEpiGeglu>();
+    if (!rc) rc = attr_nbl<kProTable, kEpiResid>();
     return rc;
+}
+
+int gemv_fused_grid(uint32_t n, uint32_t k, int epi) {
+    int S, slice;
+    if (k % 256 != 0 || k == 0 || k > 65536 || !ring_geometry((int)(k / 32), &S, &slice)) return 0;
+    return ring_grid((int)n, S, epi);
+}
+
+int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k, int pro,
+                      int epi, const GemvFuse &fz) {
+    SGQ_CHECK(k % 256 == 0 && k > 0 && k <= 65536, "gemv (fused): k=%u must be a multiple of 256", k);
+    SGQ_CHECK(tg.count >= 1 && tg.count <= kGemvMaxTargets, "gemv (fused): %d targets", tg.count);
+    for (int j = 0; j < tg.count; j++)
+        SGQ_CHECK(((uintptr_t)tg.w[j] & 15) == 0, "gemv (fused): weights must be 16-byte aligned");
+    int S, slice;
+    const int nb = (int)(k / 32);
+    SGQ_CHECK(ring_geometry(nb, &S, &slice), "gemv (fused): k=%u outside the streamed geometry", k);
+    SGQ_CHECK(pro == kProTable || S == 1, "gemv (fused): prologues need k <= %d", kRSlot / 18 * 32);
+    SGQ_CHECK(pro != kProTable || xl != nullptr, "gemv (fused): no limb table");
+    SGQ_CHECK(pro != kProNorm || (fz.part && fz.np > 0 && fz.np <= kGemvMaxPartials && fz.A &&
+                                  fz.B && (!fz.x_out || (fz.x_in && fz.u))),
+              "gemv (fused): norm prologue inputs");
+    SGQ_CHECK(pro != kProEmbed || (fz.embd && fz.step && fz.w), "gemv (fused): embed inputs");
+    int n = tg.end[tg.count - 1];
+    if (epi == kEpiGeglu) {
+        SGQ_CHECK(tg.count == 2 && tg.end[0] > 0 && tg.end[1] == 2 * tg.end[0] &&
+                      tg.end[0] % kGegluUnits == 0 && fz.hl,
+                  "gemv (fused): GeGLU needs gate/up of equal rows, a multiple of %d", kGegluUnits);
+        n = tg.end[0];
+    }
+    if (epi == kEpiResid) {
+        SGQ_CHECK(tg.count == 1 && !tg.split_out && tg.softcap == 0.f && fz.x_res && fz.w_post &&
+                      fz.w_next && fz.u_out && fz.A_out && fz.B_out && fz.part_out,
+                  "gemv (fused): residual epilogue inputs");
+        const int G = ring_grid(n, S, epi) * ((kRWG / kWave) / S);
+        SGQ_CHECK((n + G - 1) / G <= kWave, "gemv (fused): more than %d rows per wave", kWave);
+    }
+    SGQ_CHECK(!tg.split_out || (tg.count == 1 && tg.softcap == 0.f && epi == kEpiRows),
+              "gemv (fused): split output needs one target and no softcap");
+    return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), n, nb, S, slice, pro, epi,
+                           fz);
 }
 
 int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k) {

@@ -102,8 +102,9 @@ __device__ __forceinline__ void limbs_from_values(const float (&v)[32], BlockLim
 // lane 0 the scale.  Bit-identical to quantize_values (same amax, d, 1/d and
 // rint sequence per value).  All 8 lanes of a group must be active.  AGENT:
 // agent-scope stores, for a table read by other workgroups of one launch.
-template <bool AGENT = false>
-__device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *__restrict__ dst) {
+// The limb words of an 8-lane group's block: lane g gets word (g & 3) of
+// every limb (valid in lanes g < 4) and the block scale.
+__device__ __forceinline__ float limbs_words8(const float4 v, int g, uint32_t (&word)[kLimbs]) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
@@ -112,7 +113,8 @@ __device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *
     const float id = d > 0.f ? 1.0f / d : 0.f;
     const float vals[4] = {v.x, v.y, v.z, v.w};
     const int hi = g >> 2;  // values 16..31 sit in the high nibble of each byte
-    uint32_t word[kLimbs] = {};
+#pragma unroll
+    for (int l = 0; l < kLimbs; l++) word[l] = 0u;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         float r = vals[e] * id;
@@ -126,6 +128,20 @@ __device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *
     }
 #pragma unroll
     for (int l = 0; l < kLimbs; l++) word[l] |= (uint32_t)__shfl_xor((int)word[l], 4, 64);
+    return d * kLimbScale;
+}
+
+// The same table entry computed by 8 consecutive lanes: lane group g = lane&7
+// holds values 4g..4g+3 of the block (a float4).  amax by xor-shuffles; each
+// lane packs its 4 values into the nibbles they occupy in word (g & 3) of
+// every limb, lanes g and g^4 OR their halves, lanes g < 4 store word g and
+// lane 0 the scale.  Bit-identical to quantize_values (same amax, d, 1/d and
+// rint sequence per value).  All 8 lanes of a group must be active.  AGENT:
+// agent-scope stores, for a table read by other workgroups of one launch.
+template <bool AGENT = false>
+__device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *__restrict__ dst) {
+    uint32_t word[kLimbs];
+    const float d = limbs_words8(v, g, word);
     if (g < 4) {
         if (AGENT) {
 #pragma unroll
@@ -133,13 +149,12 @@ __device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *
                 __hip_atomic_store(&dst->q[l][g], (int)word[l], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             if (g == 0)
-                __hip_atomic_store(&dst->d, d * kLimbScale, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&dst->d, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
 #pragma unroll
             for (int l = 0; l < kLimbs; l++) dst->q[l][g] = (int)word[l];
             if (g == 0) {
-                dst->d = d * kLimbScale;
+                dst->d = d;
                 dst->pad[0] = dst->pad[1] = dst->pad[2] = 0;
             }
         }

@@ -452,6 +452,15 @@ struct sgq_model {
     uint32_t pos = 0;
     sgq_graph *graph = nullptr;
     float *graph_logits = nullptr;
+    // fused decode (mode 2): the residual in two buffers (xa: entering a
+    // layer, xb: after attention), the residual epilogue's u/A/B rows and
+    // per-workgroup partial sums, and the limb tables of the attention
+    // output and of the GeGLU output
+    struct {
+        float *xb, *u, *a, *b;
+        float4 *part;
+        void *xl_o, *hl;
+    } fx{};
     // persistent decode (mode 1): device layer table, activation arena,
     // sync words and error flag; `pp` is filled except for the logits
     int mode = 0;
@@ -560,6 +569,103 @@ int record_step(sgq_model *m, float *logits) {
     return launch_gemv_limbs(st, head, xl, H);
 }
 
+// Fused decode step (mode 2): five launches per layer.
+//   QKV GEMV       prologue: the previous layer's post-FFN residual update and
+//                  this layer's input RMSNorm, from the down GEMV's partial
+//                  sums (layer 0: the embedding row); writes x (xa)
+//   attention      fused q/k/v post-projection and K/V append; the last
+//                  split of each kv head merges and writes the O limbs
+//   O GEMV         epilogue: u/A/B rows and partial sums for the post-
+//                  attention residual and the FFN norm
+//   gate/up GEMV   prologue: the post-attention residual (writes xb) and the
+//                  FFN norm; epilogue: GeGLU of 32-unit blocks -> limbs
+//   down GEMV      epilogue: u/A/B rows and partial sums for the post-FFN
+//                  residual and the next layer's (or the head's) norm
+// The tied head's GEMV takes the last layer's update in its prologue.
+// Norm statistics come from sums of per-row terms:
+//   Σ(x + r·u)² = Σx² + 2r·Σx·u + r²·Σu²,  r = 1/sqrt(Σo²/H + eps).
+int record_step_fused(sgq_model *m, float *logits) {
+    const sgq_model_config &c = m->cfg;
+    hipStream_t st = ctx_stream(m->ctx);
+    const int H = (int)c.hidden, F = (int)c.ffn, QD = (int)(c.n_q_heads * kHeadDim),
+              KD = (int)(c.n_kv_heads * kHeadDim);
+    const int np_o = gemv_fused_grid((uint32_t)H, (uint32_t)QD, kEpiResid);
+    const int np_d = gemv_fused_grid((uint32_t)H, (uint32_t)F, kEpiResid);
+    SGQ_CHECK(np_o > 0 && np_o <= kGemvMaxPartials && np_d > 0 && np_d <= kGemvMaxPartials,
+              "model (fused): partial sums %d / %d", np_o, np_d);
+    float *xa = m->x, *xb = m->fx.xb;
+    int rc;
+    const size_t nl = m->layers.size();
+    for (size_t li = 0; li < nl; li++) {
+        const LayerW &L = m->layers[li];
+        GemvTargets qkv{};
+        qkv.w[0] = L.wq, qkv.w[1] = L.wk, qkv.w[2] = L.wv;
+        qkv.y[0] = m->q_raw, qkv.y[1] = m->k_raw, qkv.y[2] = m->v_raw;
+        qkv.end[0] = QD, qkv.end[1] = QD + KD, qkv.end[2] = QD + 2 * KD;
+        qkv.count = L.wv ? 3 : 2;
+        GemvFuse pre{};
+        pre.eps = c.eps;
+        pre.x_out = xa;
+        int pro;
+        if (li == 0) {
+            pro = kProEmbed;
+            pre.embd = static_cast<const uint8_t *>(m->embd);
+            pre.step = m->step;
+            pre.embed_scale = sqrtf((float)H);
+            pre.w = L.attn_norm;
+        } else {
+            pro = kProNorm;
+            pre.part = m->fx.part, pre.np = np_d;
+            pre.A = m->fx.a, pre.B = m->fx.b, pre.u = m->fx.u, pre.x_in = xb;
+            pre.scale = m->layers[li - 1].out_scale;
+        }
+        if ((rc = launch_gemv_fused(st, qkv, nullptr, (uint32_t)H, pro, kEpiRows, pre))) return rc;
+        const float *v_src = L.wv ? m->v_raw : m->k_raw;
+        const int n_splits = L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 16;
+        if ((rc = launch_attn_decode_fused(
+                 st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
+                 m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
+                 L.global ? 0u : L.slots, L.kq, L.ks, L.vq, L.vs, (int)c.n_q_heads,
+                 (int)c.n_kv_heads, n_splits, c.attn_scale, nullptr, ctx_workspace(m->ctx),
+                 kWorkspaceBytes, m->fx.xl_o, true)))
+            return rc;
+        GemvTargets ot{};
+        ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
+        GemvFuse eo{};
+        eo.x_res = xa, eo.w_post = L.post_attn_norm, eo.w_next = L.ffn_norm;
+        eo.u_out = m->fx.u, eo.A_out = m->fx.a, eo.B_out = m->fx.b, eo.part_out = m->fx.part;
+        if ((rc = launch_gemv_fused(st, ot, m->fx.xl_o, (uint32_t)QD, kProTable, kEpiResid, eo)))
+            return rc;
+        GemvTargets gu{};
+        gu.w[0] = L.wg, gu.w[1] = L.wu, gu.y[0] = m->g, gu.y[1] = m->u;
+        gu.end[0] = F, gu.end[1] = 2 * F, gu.count = 2;
+        GemvFuse pg{};
+        pg.eps = c.eps;
+        pg.part = m->fx.part, pg.np = np_o;
+        pg.A = m->fx.a, pg.B = m->fx.b, pg.u = m->fx.u, pg.x_in = xa, pg.x_out = xb;
+        pg.hl = static_cast<BlockLimbs *>(m->fx.hl);
+        if ((rc = launch_gemv_fused(st, gu, nullptr, (uint32_t)H, kProNorm, kEpiGeglu, pg)))
+            return rc;
+        GemvTargets dt{};
+        dt.w[0] = L.wd, dt.y[0] = m->f, dt.end[0] = H, dt.count = 1;
+        GemvFuse ed{};
+        ed.x_res = xb, ed.w_post = L.post_ffw_norm;
+        ed.w_next = li + 1 < nl ? m->layers[li + 1].attn_norm : m->out_norm;
+        ed.u_out = m->fx.u, ed.A_out = m->fx.a, ed.B_out = m->fx.b, ed.part_out = m->fx.part;
+        if ((rc = launch_gemv_fused(st, dt, m->fx.hl, (uint32_t)F, kProTable, kEpiResid, ed)))
+            return rc;
+    }
+    GemvTargets head{};
+    head.w[0] = m->embd, head.y[0] = logits, head.end[0] = (int)c.vocab, head.count = 1;
+    head.softcap = c.final_softcap;
+    GemvFuse ph{};
+    ph.eps = c.eps;
+    ph.part = m->fx.part, ph.np = np_d;
+    ph.A = m->fx.a, ph.B = m->fx.b;
+    ph.scale = m->layers[nl - 1].out_scale;
+    return launch_gemv_fused(st, head, nullptr, (uint32_t)H, kProNorm, kEpiRows, ph);
+}
+
 }  // namespace
 
 extern "C" {
@@ -652,6 +758,15 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
     for (int i = 0; i < 10; i++)
         if ((rc = alloc(m, act_n[i] * 4, reinterpret_cast<void **>(acts[i])))) return fail_out(rc);
     if ((rc = alloc(m, std::max(H, F) / 32 * sizeof(BlockLimbs), &m->xl))) return fail_out(rc);
+    {
+        float **fb[] = {&m->fx.xb, &m->fx.u, &m->fx.a, &m->fx.b};
+        for (float **b : fb)
+            if ((rc = alloc(m, H * 4, reinterpret_cast<void **>(b)))) return fail_out(rc);
+        if ((rc = alloc(m, kGemvMaxPartials * sizeof(float4), reinterpret_cast<void **>(&m->fx.part))) ||
+            (rc = alloc(m, QD / 32 * sizeof(BlockLimbs), &m->fx.xl_o)) ||
+            (rc = alloc(m, F / 32 * sizeof(BlockLimbs), &m->fx.hl)))
+            return fail_out(rc);
+    }
     if ((rc = alloc(m, 64, reinterpret_cast<void **>(&m->step)))) return fail_out(rc);
     if ((rc = alloc(m, 2 * kHeadDim * 4, reinterpret_cast<void **>(&m->rope_cs))))
         return fail_out(rc);
@@ -702,7 +817,10 @@ int sgq_model_decode(sgq_model *m, uint32_t token, float *logits) {
     if (!m || !logits) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     int rc = write_step(m, token);
     if (rc) return rc;
-    if ((rc = m->mode == 1 ? persistent_step(m, logits) : record_step(m, logits))) return rc;
+    if ((rc = m->mode == 1   ? persistent_step(m, logits)
+               : m->mode == 2 ? record_step_fused(m, logits)
+                              : record_step(m, logits)))
+        return rc;
     m->pos++;
     return SGQ_OK;
 }
@@ -720,7 +838,7 @@ int sgq_model_decode_graph(sgq_model *m, uint32_t token, float *logits) {
             m->graph = nullptr;
         }
         if ((rc = sgq_graph_begin(m->ctx))) return rc;
-        rc = record_step(m, logits);
+        rc = m->mode == 2 ? record_step_fused(m, logits) : record_step(m, logits);
         sgq_graph *g = nullptr;
         const int rc2 = sgq_graph_end(m->ctx, &g);
         if (rc) {
@@ -820,9 +938,14 @@ static int persistent_setup(sgq_model *m) {
 
 int sgq_model_set_decode_mode(sgq_model *m, int mode) {
     if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
-    SGQ_CHECK(mode == 0 || mode == 1, "model: decode mode %d (0 kernels, 1 persistent)", mode);
+    SGQ_CHECK(mode >= 0 && mode <= 2, "model: decode mode %d (0 kernels, 1 persistent, 2 fused)",
+              mode);
     if (mode == 1 && !m->err)
         if (int rc = persistent_setup(m)) return rc;
+    if (mode != m->mode && m->graph) {  // a captured step belongs to one mode
+        sgq_graph_destroy(m->graph);
+        m->graph = nullptr;
+    }
     m->mode = mode;
     return SGQ_OK;
 }
@@ -1099,6 +1222,21 @@ int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr
         if (n == "token_embd") { *ptr = m->embd; *bytes = q4(c.vocab, H); return SGQ_OK; }
         if (n == "output_norm") { *ptr = m->out_norm; *bytes = H * 4; return SGQ_OK; }
         if (n == "x") { *ptr = m->x; *bytes = H * 4; return SGQ_OK; }
+        // decode-step activations (the last layer's, after a step)
+        const struct { const char *n; void *p; uint64_t b; } acts[] = {
+            {"q_raw", m->q_raw, QD * 4}, {"k_raw", m->k_raw, KD * 4}, {"v_raw", m->v_raw, KD * 4},
+            {"attn_out", m->attn, QD * 4}, {"x_mid", m->fx.xb, H * 4},
+            {"resid_u", m->fx.u, H * 4}, {"resid_a", m->fx.a, H * 4}, {"resid_b", m->fx.b, H * 4},
+            {"resid_partials", m->fx.part, kGemvMaxPartials * 16},
+            {"attn_out_limbs", m->fx.xl_o, QD / 32 * sizeof(BlockLimbs)},
+            {"ffn_limbs", m->fx.hl, F / 32 * sizeof(BlockLimbs)},
+        };
+        for (const auto &e : acts)
+            if (n == e.n) {
+                *ptr = e.p;
+                *bytes = e.b;
+                return SGQ_OK;
+            }
         return fail(SGQ_ERR_VALIDATION, "model: no global tensor '%s'", name);
     }
     SGQ_CHECK(layer < (int)m->layers.size(), "model: layer %d out of range", layer);

@@ -11,6 +11,7 @@
 namespace sgq {
 
 constexpr int kWave = 64;
+struct BlockLimbs;
 
 // Status plumbing: every entry point returns an sgq_status and leaves a
 // human-readable message in a thread-local buffer (sgq_last_error()).
@@ -70,6 +71,50 @@ int gemv_slices(uint32_t k);
 // Sets the streamed kernels' launch attributes (call before graph capture).
 int gemv_prepare();
 int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k);
+// Fused forms of the streamed GEMV (single K-slice for the prologues).
+// Prologue (what the GEMV's x limbs are computed from, inside the launch):
+//   kProTable  the limb table xl (written by an earlier kernel);
+//   kProNorm   f = rb·s·(A + ra·B) with ra = 1/sqrt(P1/K + eps),
+//              rb = 1/sqrt(s²(P4 + 2·ra·P2 + ra²·P3)/K + eps) from the np
+//              partial sums (P1..P4) an kEpiResid launch left in part, and
+//              x_out = s·(x_in + ra·u) (each workgroup writes a slice);
+//              s = *scale (1 when null).  That is the residual update
+//              x_out = (x_in + rmsnorm(o)∘w_post)·s followed by
+//              rmsnorm(x_out)∘w_next, with A = x_in∘w_next, u = o∘w_post,
+//              B = u∘w_next;
+//   kProEmbed  x0 = dequant(embd[step[4]])·embed_scale, f = rmsnorm(x0)∘w,
+//              x_out = x0 (sliced).
+// Epilogue (what is done with the output rows o):
+//   kEpiRows   stored to the targets (softcap, split_out as GemvTargets);
+//   kEpiResid  single target: per row u = o·w_post, A = x_res·w_next,
+//              B = u·w_next into u_out/A_out/B_out, and the workgroup's
+//              (Σo², Σx_res·u, Σu², Σx_res²) into part_out[workgroup];
+//   kEpiGeglu  targets gate (w[0]) and up (w[1]), n = units: workgroup b
+//              computes units [32b, 32b+32) and writes block b of the limbs
+//              of gelu_tanh(gate)·up into hl.
+enum { kProTable = 0, kProNorm = 1, kProEmbed = 2 };
+enum { kEpiRows = 0, kEpiResid = 1, kEpiGeglu = 2 };
+constexpr int kGemvMaxPartials = 1024;
+struct GemvFuse {
+    const float4 *part;
+    int np;
+    const float *A, *B, *u, *x_in, *scale;
+    float *x_out;
+    const uint8_t *embd;
+    const uint32_t *step;
+    float embed_scale;
+    const float *w;
+    float eps;
+    const float *x_res, *w_post, *w_next;
+    float *u_out, *A_out, *B_out;
+    float4 *part_out;
+    struct BlockLimbs *hl;
+};
+// Workgroups a fused launch uses (= the np its kEpiResid partials need).
+int gemv_fused_grid(uint32_t n, uint32_t k, int epi);
+int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k, int pro,
+                      int epi, const GemvFuse &fz);
+
 int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k);
 int launch_quant_q8_0(hipStream_t st, const float *x, uint16_t *scales, int8_t *quants,
                       uint64_t n_elems);
@@ -88,7 +133,9 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
                           size_t workspace_bytes, void *limbs_out = nullptr);
 // Sets the attention kernels' launch attributes (call before graph capture).
 int attn_prepare();
-// Decode attention with the step's q/k/v post-projection fused in: q, k
+// Decode attention with the step's q/k/v post-projection fused in (and,
+// with merge_in_launch, the split merge: limbs only, counters in the
+// workspace, which must start zeroed): q, k
 // and v_src are the raw projections (v_src may alias k_raw), rope_cs the
 // (cos, sin) table of the current position; appends the new K/V rows at the
 // current slot (pos % ring, or pos when ring == 0).  head_dim 128.
@@ -97,7 +144,8 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                              const float *rope_cs, float eps, const uint32_t *step, int step_word,
                              uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
                              int n_q, int n_kv, int n_splits, float scale, float *out,
-                             void *workspace, size_t workspace_bytes, void *limbs_out);
+                             void *workspace, size_t workspace_bytes, void *limbs_out,
+                             bool merge_in_launch = false);
 // Keys before q0 come from the cache (ring: slot = pos % ring), keys from q0
 // on from the chunk's pages ckq.. (row = pos - q0) when given, else the cache.
 int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,

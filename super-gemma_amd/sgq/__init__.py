@@ -569,7 +569,8 @@ class Model:
 
     @property
     def decode_mode(self) -> int:
-        """0: one kernel per operator; 1: one persistent launch per step."""
+        """0: one kernel per operator; 1: one persistent launch per step;
+        2: five fused launches per layer."""
         return int(lib().sgq_model_decode_mode(self._h))
 
     @decode_mode.setter
