@@ -124,7 +124,7 @@ int sgq_timer_stop(sgq_ctx *ctx, float *ms);
  * per row), x and y fp32.  Replaces gemv_q4_0_k{K} / gemv_q4_0_generic
  * (crates/sg-gpu/shaders/gemv_q4_0.wgsl:52-112).  k % 64 == 0, k <= 65536.
  * x enters the integer dot as four signed 4-bit limbs per value (error
- * <= 2.6e-5 of its 32-block's max |x|, below an f16 rounding of x). */
+ * <= 1.7e-5 of its 32-block's max |x|, below an f16 rounding of x). */
 int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_t n,
                   uint32_t k);
 

@@ -8,13 +8,13 @@
 //  * VALU, not the MFMA, is the scarce unit next to an 8 TB/s weight stream:
 //    at ~1 wave-instruction per 4 cycles per SIMD, an fp32 FMA form (nibble
 //    split, int->f32, FMA: ~2.4 ops/weight) takes as long as the stream.
-//    So x is split once per 32-block into four signed 4-bit limbs,
-//    x ≈ (amax/7)·(l1 + l2/14 + l3/14² + l4/14³), l ∈ [-7, 7]
-//    (|error| ≤ amax·2.6e-5), and the inner loop is v_dot8_i32_i4 on the
+//    So x is split once per 32-block into four signed 4-bit limbs, the
+//    base-16 digits of v = rint(x·(7/amax)·4096) (limbs.h; |error| ≤
+//    amax·1.7e-5), and the inner loop is v_dot8_i32_i4 on the
 //    weight nibbles themselves: qs ^ 0x88888888 turns every nibble q into
 //    the signed 4-bit value q-8, so one XOR per 8 weights is the whole
 //    unpack.  Per block: 4 perm + 4 xor + 16 dot8 + 3 Horner steps in one
-//    exact integer accumulator (|c| <= 1792·2955 < 2^23) + cvt + 2 mul.
+//    exact integer accumulator (|c| <= 32·8·28672 < 2^23) + cvt + 2 mul.
 //  * x limbs live in registers for the whole kernel: lane l of a wave always
 //    owns blocks l, l+64, l+128 of its K-slice.
 //  * Each lane reads its block as 20 bytes from a 4-byte-aligned address
@@ -253,6 +253,14 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
 }
 
+// A wave-uniform pointer in scalar registers.
+__device__ __forceinline__ const uint8_t *uni(const uint8_t *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+}
+
 // Values passed through an empty asm: to the compiler they are defined here,
 // so a load behind them is waited for here (before the weight stream
 // starts) and not at their first use, where the compiler, which cannot
@@ -364,6 +372,21 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         }
     };
 
+    // wave-uniform source of round `it`'s slice (past-the-end rows: row 0)
+    auto slice_src = [&](int it) -> const uint8_t * {
+        const uint8_t *src;
+        if (EPI == kEpiGeglu) {
+            const uint8_t *w = static_cast<const uint8_t *>((it & 1) ? tg.w[1] : tg.w[0]);
+            src = w + (size_t)(u0 + (it >> 1)) * row_bytes + slice_off;
+        } else {
+            const int row = r0 + it * G;
+            int local;
+            const int j = target_of(tg, row < n ? row : 0, &local);
+            src = static_cast<const uint8_t *>(tg.w[j]) + (size_t)local * row_bytes + slice_off;
+        }
+        return uni(src);
+    };
+
     // ---- prologue loads (before the stream) --------------------------------
     constexpr int kPB = (kMaxTabBlocks + 31) / 32;  // blocks per 8-lane group
     const int grp = threadIdx.x >> 3, ge = threadIdx.x & 7;
@@ -379,23 +402,77 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // compiler can count exactly which loads each later wait needs)
     float s_pre = 1.f;
     if (PRO == kProNorm) {
-#pragma unroll
-        for (int k = 0; k < kGemvMaxPartials / kRWG; k++) {
-            const int i = (int)threadIdx.x + k * kRWG;
-            pv[k] = fz.part[i < fz.np ? i : 0];
-        }
-#pragma unroll
-        for (int k = 0; k < kPB; k++) {
-            const int b = min(grp + 32 * k, nb - 1);
-            av[k] = reinterpret_cast<const float4 *>(fz.A)[b * 8 + ge];
-            bv[k] = reinterpret_cast<const float4 *>(fz.B)[b * 8 + ge];
-        }
-        if (fz.x_out) {  // uniform
-            const int i = xo_on ? xo_i : 0;
-            xo_in = reinterpret_cast<const float4 *>(fz.x_in)[i];
-            xo_u = reinterpret_cast<const float4 *>(fz.u)[i];
-        }
+        // Issued by asm, together with the stream's first two slices and a
+        // wait for just these loads (vmcnt = the 6 slice loads after them):
+        // the compiler never sees these loads, so it adds no wait of its own
+        // for the stream (it cannot count LDS DMA and ordinary loads
+        // together and would wait for everything).  Indices are clamped;
+        // values past the end are ignored below.
         if (fz.scale) s_pre = *fz.scale;
+        const float *A = fz.A, *B = fz.B;
+        const float *xi = fz.x_out ? fz.x_in : A, *xu = fz.x_out ? fz.u : A;
+        const uint32_t op0 = (uint32_t)min((int)threadIdx.x, fz.np - 1) * 16u;
+        const uint32_t op1 = (uint32_t)min((int)threadIdx.x + kRWG, fz.np - 1) * 16u;
+        const uint32_t ox = (uint32_t)(xo_on ? xo_i : 0) * 16u;
+        uint32_t ob[kPB];
+#pragma unroll
+        for (int k = 0; k < kPB; k++) ob[k] = (uint32_t)(min(grp + 32 * k, nb - 1) * 8 + ge) * 16u;
+        f32x4_t t0, t1, t2, t3;
+        asm volatile(
+            "global_load_dwordx4 %0, %4, %6\n"
+            "global_load_dwordx4 %1, %5, %6\n"
+            "global_load_dwordx4 %2, %7, %8\n"
+            "global_load_dwordx4 %3, %7, %9\n"
+            : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+            : "v"(op0), "v"(op1), "s"(fz.part), "v"(ox), "s"(xi), "s"(xu)
+            : "memory");
+        static_assert(kPB == 6 && kGemvMaxPartials == 2 * kRWG, "asm prologue layout");
+        f32x4_t a0, a1, a2, a3, a4, a5, c0, c1, c2, c3, c4, c5;
+        asm volatile(
+            "global_load_dwordx4 %0, %12, %18\n"
+            "global_load_dwordx4 %1, %13, %18\n"
+            "global_load_dwordx4 %2, %14, %18\n"
+            "global_load_dwordx4 %3, %15, %18\n"
+            "global_load_dwordx4 %4, %16, %18\n"
+            "global_load_dwordx4 %5, %17, %18\n"
+            "global_load_dwordx4 %6, %12, %19\n"
+            "global_load_dwordx4 %7, %13, %19\n"
+            "global_load_dwordx4 %8, %14, %19\n"
+            "global_load_dwordx4 %9, %15, %19\n"
+            "global_load_dwordx4 %10, %16, %19\n"
+            "global_load_dwordx4 %11, %17, %19\n"
+            : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(a3), "=&v"(a4), "=&v"(a5), "=&v"(c0),
+              "=&v"(c1), "=&v"(c2), "=&v"(c3), "=&v"(c4), "=&v"(c5)
+            : "v"(ob[0]), "v"(ob[1]), "v"(ob[2]), "v"(ob[3]), "v"(ob[4]), "v"(ob[5]), "s"(A),
+              "s"(B)
+            : "memory");
+        // the stream's first two slices, then the wait for the loads above
+        const uint8_t *src0 = slice_src(0), *src1 = slice_src(1);
+        const uint32_t l0 = (uint32_t)(uintptr_t)ring, l1 = l0 + kRSlot;
+        static_assert(kRLoads == 3 && kGStages == 3, "asm stream start layout");
+        asm volatile(
+            "s_mov_b32 m0, %0\n"
+            "global_load_lds_dwordx4 %4, %2\n"
+            "s_add_i32 m0, %0, 0x400\n"
+            "global_load_lds_dwordx4 %5, %2\n"
+            "s_add_i32 m0, %0, 0x800\n"
+            "global_load_lds_dwordx4 %6, %2\n"
+            "s_mov_b32 m0, %1\n"
+            "global_load_lds_dwordx4 %4, %3\n"
+            "s_add_i32 m0, %1, 0x400\n"
+            "global_load_lds_dwordx4 %5, %3\n"
+            "s_add_i32 m0, %1, 0x800\n"
+            "global_load_lds_dwordx4 %6, %3\n"
+            "s_waitcnt vmcnt(6)\n"
+            :
+            : "s"(l0), "s"(l1), "s"(src0), "s"(src1), "v"(doff[0]), "v"(doff[1]), "v"(doff[2])
+            : "memory", "m0", "scc");
+        auto f4 = [](f32x4_t v) { return make_float4(v.x, v.y, v.z, v.w); };
+        pv[0] = f4(t0), pv[1] = f4(t1), xo_in = f4(t2), xo_u = f4(t3);
+        av[0] = f4(a0), av[1] = f4(a1), av[2] = f4(a2), av[3] = f4(a3), av[4] = f4(a4),
+        av[5] = f4(a5);
+        bv[0] = f4(c0), bv[1] = f4(c1), bv[2] = f4(c2), bv[3] = f4(c3), bv[4] = f4(c4),
+        bv[5] = f4(c5);
     } else if (PRO == kProEmbed) {
         const uint8_t *er = fz.embd + (size_t)fz.step[4] * nb * 18;
 #pragma unroll
@@ -423,24 +500,13 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // one L2/MALL round trip), then turned into limbs while the first slices
     // are in flight.
     if (PRO != kProTable) {
-        if (PRO == kProNorm) {
-#pragma unroll
-            for (int k = 0; k < kGemvMaxPartials / kRWG; k++) settle(pv[k]);
-            if (fz.x_out) {
-                settle(xo_in);
-                settle(xo_u);
-            }
-        } else {
+        if (PRO == kProEmbed) {
 #pragma unroll
             for (int k = 0; k < kPB; k++) {
                 settle(ed[k]);
                 settle(eq[k]);
+                settle(av[k]);
             }
-        }
-#pragma unroll
-        for (int k = 0; k < kPB; k++) {
-            settle(av[k]);
-            if (PRO == kProNorm) settle(bv[k]);
         }
         if (EPI == kEpiResid) {
             settle(ex);
@@ -452,8 +518,10 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // ---- the stream starts ------------------------------------------------
     // (unconditional: a missing round loads row 0, which keeps the number of
     // loads in flight known to the compiler's wait counting)
+    if (PRO != kProNorm) {  // (kProNorm started it above)
 #pragma unroll
-    for (int j = 0; j < kGStages - 1; j++) issue(j);
+        for (int j = 0; j < kGStages - 1; j++) issue(j);
+    }
     asm volatile("" ::: "memory");
 
     XLimbs<NBL> L;

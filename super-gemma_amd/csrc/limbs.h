@@ -1,23 +1,27 @@
-// x limbs for the Q4_0 GEMV: each 32-block of an fp32 vector is split into
-// kLimbs signed 4-bit limbs, x ≈ (amax/7)·(l1 + l2/14 + l3/14² + l4/14³),
-// l ∈ [-7, 7] (|error| ≤ amax/7/14³/2 = amax·2.6e-5, below the 2^-12
-// relative rounding of an f16 activation), packed eight to a 32-bit word in
-// the nibble order of a Q4_0 qs word so that v_dot8_i32_i4 can take the
-// weights' nibbles as they are.  Shared by the GEMV and by the kernels
-// that produce its input (norms, GeGLU, attention output), which write the
-// limb table (BlockLimbs per block) directly.
+// x limbs for the Q4_0 GEMV: each value of a 32-block of an fp32 vector is
+// rounded to an integer v = rint(x·(7/amax)·4096), |v| <= 28672, and v is
+// written as four signed base-16 digits, v = 16³·l1 + 16²·l2 + 16·l3 + l4,
+// l ∈ [-8, 7]: with u = v + 0x8888 every nibble of u is a digit plus 8, so
+// the digits are the nibbles of u ^ 0x8888 read as signed 4-bit numbers.
+// x ≈ d·v with d = (amax/7)/4096 (|error| ≤ amax/57344 = amax·1.7e-5, below
+// the 2^-12 relative rounding of an f16 activation).  The limbs are packed
+// eight to a 32-bit word in the nibble order of a Q4_0 qs word so that
+// v_dot8_i32_i4 can take the weights' nibbles as they are.  Shared by the
+// GEMV and by the kernels that produce its input (norms, GeGLU, attention
+// output), which write the limb table (BlockLimbs per block) directly.
 #pragma once
 #include "sgq_internal.h"
 
 namespace sgq {
 
 constexpr int kLimbs = 4;
-constexpr float kLimbScale = 1.0f / 2744.0f;  // 14^-3
+constexpr float kLimbScale = 1.0f / 4096.0f;  // 16^-3
+constexpr int kLimbBias = 0x8888;              // Σ 8·16^k, k < 4
 
 template <int NBL>
 struct XLimbs {
     int q[NBL][kLimbs][4];  // i4 × 8 per word, in the nibble order of a qs word
-    float d[NBL];           // (amax/7) / 14^3: scale of the Horner-combined sum
+    float d[NBL];           // (amax/7) / 16^3: scale of the Horner-combined sum
 };
 
 // Per-block x limbs as stored in the table the streamed GEMV reads (80 B).
@@ -29,26 +33,30 @@ struct BlockLimbs {
 
 static_assert(sizeof(BlockLimbs) == SGQ_X_LIMBS_BYTES_PER_BLOCK, "limb table layout (sgq.h)");
 
+// The four digit nibbles (signed 4-bit, most significant limb in bits
+// 12..15) of a value already multiplied by (7/amax)·4096.
+__device__ __forceinline__ uint32_t limb_digits(float r) {
+    const int v = (int)__builtin_rintf(r);
+    return (uint32_t)(v + kLimbBias) ^ (uint32_t)kLimbBias;
+}
+
 template <int NBL>
 __device__ __forceinline__ void quantize_values(const float (&v)[32], XLimbs<NBL> &L, int i) {
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax * (1.0f / 7.0f);
-    const float id = d > 0.f ? 1.0f / d : 0.f;
+    const float id = d > 0.f ? 4096.0f * (1.0f / d) : 0.f;
     L.d[i] = d * kLimbScale;
     uint32_t word[kLimbs][4] = {};
 #pragma unroll
     for (int j = 0; j < 32; j++) {
-        float r = v[j] * id;
+        const uint32_t u = limb_digits(v[j] * id);
         const int w = (j & 15) >> 2;
         const int shift = 4 * (2 * (j & 3) + (j >> 4));
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) {
-            const float c = __builtin_rintf(r);
-            r = (r - c) * 14.f;
-            word[l][w] |= ((uint32_t)(int)c & 0xFu) << shift;
-        }
+        for (int l = 0; l < kLimbs; l++)
+            word[l][w] |= ((u >> (4 * (kLimbs - 1 - l))) & 0xFu) << shift;
     }
 #pragma unroll
     for (int l = 0; l < kLimbs; l++)
@@ -95,49 +103,48 @@ __device__ __forceinline__ void limbs_from_values(const float (&v)[32], BlockLim
     t.pad[0] = t.pad[1] = t.pad[2] = 0;
 }
 
-// The same table entry computed by 8 consecutive lanes: lane group g = lane&7
-// holds values 4g..4g+3 of the block (a float4).  amax by xor-shuffles; each
-// lane packs its 4 values into the nibbles they occupy in word (g & 3) of
-// every limb, lanes g and g^4 OR their halves, lanes g < 4 store word g and
-// lane 0 the scale.  Bit-identical to quantize_values (same amax, d, 1/d and
-// rint sequence per value).  All 8 lanes of a group must be active.  AGENT:
-// agent-scope stores, for a table read by other workgroups of one launch.
-// The limb words of an 8-lane group's block: lane g gets word (g & 3) of
-// every limb (valid in lanes g < 4) and the block scale.
+// DPP lane moves inside 8-lane groups (no LDS traffic): quad_perm swaps
+// for xor 1 and 2, row_half_mirror (lane i <- 7-i) to meet the other quad,
+// row_ror:12 (lane i <- i+4 within a 16-lane row) to fetch lane g+4's word.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float max8(float a) {
+    a = fmaxf(a, __builtin_bit_cast(float, dpp_mov<0xB1>(__builtin_bit_cast(uint32_t, a))));
+    a = fmaxf(a, __builtin_bit_cast(float, dpp_mov<0x4E>(__builtin_bit_cast(uint32_t, a))));
+    return fmaxf(a, __builtin_bit_cast(float, dpp_mov<0x141>(__builtin_bit_cast(uint32_t, a))));
+}
+
+// The limb words of an 8-lane group's block, where lane g = lane & 7 holds
+// values 4g..4g+3 (a float4): amax over the group, then each lane packs its
+// 4 values into the nibbles they occupy in word (g & 3) of every limb, and
+// lanes g < 4 OR in the other half from lane g+4.  Valid in lanes g < 4;
+// returns the block scale.  Bit-identical to quantize_values (same amax,
+// d, scale and rint per value).  All 8 lanes of a group must be active.
 __device__ __forceinline__ float limbs_words8(const float4 v, int g, uint32_t (&word)[kLimbs]) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float d = amax * (1.0f / 7.0f);
-    const float id = d > 0.f ? 1.0f / d : 0.f;
+    const float id = d > 0.f ? 4096.0f * (1.0f / d) : 0.f;
     const float vals[4] = {v.x, v.y, v.z, v.w};
     const int hi = g >> 2;  // values 16..31 sit in the high nibble of each byte
 #pragma unroll
     for (int l = 0; l < kLimbs; l++) word[l] = 0u;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        float r = vals[e] * id;
+        const uint32_t u = limb_digits(vals[e] * id);
         const int shift = 4 * (2 * e + hi);
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) {
-            const float c = __builtin_rintf(r);
-            r = (r - c) * 14.f;
-            word[l] |= ((uint32_t)(int)c & 0xFu) << shift;
-        }
+        for (int l = 0; l < kLimbs; l++) word[l] |= ((u >> (4 * (kLimbs - 1 - l))) & 0xFu) << shift;
     }
 #pragma unroll
-    for (int l = 0; l < kLimbs; l++) word[l] |= (uint32_t)__shfl_xor((int)word[l], 4, 64);
+    for (int l = 0; l < kLimbs; l++) word[l] |= dpp_mov<0x12C>(word[l]);  // row_ror:12
     return d * kLimbScale;
 }
 
-// The same table entry computed by 8 consecutive lanes: lane group g = lane&7
-// holds values 4g..4g+3 of the block (a float4).  amax by xor-shuffles; each
-// lane packs its 4 values into the nibbles they occupy in word (g & 3) of
-// every limb, lanes g and g^4 OR their halves, lanes g < 4 store word g and
-// lane 0 the scale.  Bit-identical to quantize_values (same amax, d, 1/d and
-// rint sequence per value).  All 8 lanes of a group must be active.  AGENT:
-// agent-scope stores, for a table read by other workgroups of one launch.
+// The table entry of an 8-lane group's block (limbs_words8): lanes g < 4
+// store word g of every limb, lane 0 the scale.  AGENT: agent-scope
+// stores, for a table read by other workgroups of one launch.
 template <bool AGENT = false>
 __device__ __forceinline__ void limbs_block8(const float4 v, int g, BlockLimbs *__restrict__ dst) {
     uint32_t word[kLimbs];

@@ -94,7 +94,7 @@ int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k);
 //              of gelu_tanh(gate)·up into hl.
 enum { kProTable = 0, kProNorm = 1, kProEmbed = 2 };
 enum { kEpiRows = 0, kEpiResid = 1, kEpiGeglu = 2 };
-constexpr int kGemvMaxPartials = 1024;
+constexpr int kGemvMaxPartials = 512;
 struct GemvFuse {
     const float4 *part;
     int np;

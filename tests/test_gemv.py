@@ -5,7 +5,7 @@ random_q4_0 weights, f64 reference over sampled rows, bit-determinism).
 Tolerance: fp32 output within 1e-3 relative (BASELINE) — asserted as
 |err| <= 1e-3*|want| + 3e-4*rms(want) per element, and the normwise error
 max|err|/max|want| <= 1e-4.  x enters the kernel as four 4-bit limbs
-(per-element error <= 2.6e-5 of its block's max |x|), so an output's error
+(per-element error <= 1.7e-5 of its block's max |x|), so an output's error
 is ~3e-5*rms(want) (1 sigma): four times below what the reference's own f16
 activation buffers cost its GEMV (2^-12 relative rounding per element).
 """

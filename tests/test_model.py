@@ -9,7 +9,7 @@ Q8_0 K/V pages.
 Tolerance on logits, per step: |err| <= 2e-3*|want| + 2e-3*max|want|
 elementwise, and top-1 agreement up to ties within that tolerance (the GPU's
 argmax scores within 2e-3*max|want| of the oracle's best).  The GPU differs from
-the oracle by the GEMV's x limbs (|err| <= 2.6e-5*amax per block), f32 vs f64
+the oracle by the GEMV's x limbs (|err| <= 1.7e-5*amax per block), f32 vs f64
 accumulation, and an occasional Q8_0 rounding flip of a K/V element or, in
 prefill, of an activation.
 """
