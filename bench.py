@@ -260,7 +260,7 @@ class Decode:
     decoder at an 8K-token context, replayed as one hipGraph per step."""
     kernel = "gemv_q4_0_ring_kernel"
 
-    def __init__(self, ctx, torch, context=8192, mode="kernels"):
+    def __init__(self, ctx, torch, context=8192, mode="fused"):
         import sgq
 
         self.ctx, self.torch, self.sgq = ctx, torch, sgq
@@ -308,6 +308,7 @@ class Decode:
                               "bytes_per_step": self.bytes},
             "config": {"workload": "decode step, bs=1, 8K context (BASELINE config 5), "
                                    "62-layer random-init decoder, hipGraph per step",
+                       "decode_mode": self.mode,
                        "n_layers": c.n_layers, "hidden": c.hidden, "ffn": c.ffn,
                        "n_q_heads": c.n_q_heads, "n_kv_heads": c.n_kv_heads, "head_dim": 128,
                        "vocab": c.vocab, "sliding_window": c.sliding_window,
@@ -397,9 +398,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--decode-mode", default="kernels", choices=["persistent", "kernels", "fused"],
-                    help="decode workload: one persistent launch per step, or one kernel "
-                         "per operator replayed as a hipGraph")
+    ap.add_argument("--decode-mode", default="fused", choices=["persistent", "kernels", "fused"],
+                    help="decode workload: five fused launches per layer (default) or one "
+                         "kernel per operator, each step replayed as a hipGraph; or one "
+                         "persistent launch per step")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",

@@ -224,7 +224,8 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
 constexpr int kRingBytes = (kRWG / kWave) * kGStages * kRSlot;
 constexpr int kRedOff = kRingBytes;
 constexpr int kScrOff = kRedOff + 64;
-constexpr int kTabOff = kScrOff + 256;
+constexpr int kRowsOff = kScrOff + 256;    // kEpiResid: row results, 256 floats
+constexpr int kTabOff = kRowsOff + 1024;
 constexpr int kRLds = kTabOff;
 constexpr int kMaxTabBlocks = 3 * kWave;  // one slice: <= 192 blocks
 constexpr int kGegluUnits = 32;           // units (gate/up row pairs) per workgroup
@@ -337,6 +338,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     uint8_t *red = gemv_smem + kRedOff;  // [2][4] floats
     uint8_t *scr = gemv_smem + kScrOff;
     uint8_t *tab = gemv_smem + kTabOff;
+    uint8_t *rows_s = gemv_smem + kRowsOff;
     const size_t row_bytes = (size_t)nb * 18;
     const int b0 = s * slice;
     const int slice_blocks = min(slice, nb - b0);
@@ -390,7 +392,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // ---- prologue loads (before the stream) --------------------------------
     constexpr int kPB = (kMaxTabBlocks + 31) / 32;  // blocks per 8-lane group
     const int grp = threadIdx.x >> 3, ge = threadIdx.x & 7;
-    float4 pv[kGemvMaxPartials / kRWG];
+    float4 pv[kGemvMaxPartials / kWave];
     float4 av[kPB], bv[kPB], xo_in, xo_u;
     uint32_t eq[kPB];  // kProEmbed: 4 nibble bytes of the lane's values
     float ed[kPB];
@@ -411,22 +413,41 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         if (fz.scale) s_pre = *fz.scale;
         const float *A = fz.A, *B = fz.B;
         const float *xi = fz.x_out ? fz.x_in : A, *xu = fz.x_out ? fz.u : A;
-        const uint32_t op0 = (uint32_t)min((int)threadIdx.x, fz.np - 1) * 16u;
-        const uint32_t op1 = (uint32_t)min((int)threadIdx.x + kRWG, fz.np - 1) * 16u;
+        // wave 0 reads all np partial sums (lane l: entries l + 64k) and
+        // hands their total to the others through LDS
+        uint32_t op[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) op[k] = (uint32_t)min(lane + kWave * k, fz.np - 1) * 16u;
         const uint32_t ox = (uint32_t)(xo_on ? xo_i : 0) * 16u;
         uint32_t ob[kPB];
 #pragma unroll
         for (int k = 0; k < kPB; k++) ob[k] = (uint32_t)(min(grp + 32 * k, nb - 1) * 8 + ge) * 16u;
-        f32x4_t t0, t1, t2, t3;
+        f32x4_t t0, t1, t2, t3, t4, t5, t6, t7, t8, t9;
+        if (wave == 0) {
+            asm volatile(
+                "global_load_dwordx4 %0, %8, %16\n"
+                "global_load_dwordx4 %1, %9, %16\n"
+                "global_load_dwordx4 %2, %10, %16\n"
+                "global_load_dwordx4 %3, %11, %16\n"
+                "global_load_dwordx4 %4, %12, %16\n"
+                "global_load_dwordx4 %5, %13, %16\n"
+                "global_load_dwordx4 %6, %14, %16\n"
+                "global_load_dwordx4 %7, %15, %16\n"
+                : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6),
+                  "=&v"(t7)
+                : "v"(op[0]), "v"(op[1]), "v"(op[2]), "v"(op[3]), "v"(op[4]), "v"(op[5]),
+                  "v"(op[6]), "v"(op[7]), "s"(fz.part)
+                : "memory");
+        } else {
+            t0 = t1 = t2 = t3 = t4 = t5 = t6 = t7 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
         asm volatile(
-            "global_load_dwordx4 %0, %4, %6\n"
-            "global_load_dwordx4 %1, %5, %6\n"
-            "global_load_dwordx4 %2, %7, %8\n"
-            "global_load_dwordx4 %3, %7, %9\n"
-            : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
-            : "v"(op0), "v"(op1), "s"(fz.part), "v"(ox), "s"(xi), "s"(xu)
+            "global_load_dwordx4 %0, %2, %3\n"
+            "global_load_dwordx4 %1, %2, %4\n"
+            : "=&v"(t8), "=&v"(t9)
+            : "v"(ox), "s"(xi), "s"(xu)
             : "memory");
-        static_assert(kPB == 6 && kGemvMaxPartials == 2 * kRWG, "asm prologue layout");
+        static_assert(kPB == 6 && kGemvMaxPartials == 8 * kWave, "asm prologue layout");
         f32x4_t a0, a1, a2, a3, a4, a5, c0, c1, c2, c3, c4, c5;
         asm volatile(
             "global_load_dwordx4 %0, %12, %18\n"
@@ -447,28 +468,14 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
               "s"(B)
             : "memory");
         // the stream's first two slices, then the wait for the loads above
-        const uint8_t *src0 = slice_src(0), *src1 = slice_src(1);
-        const uint32_t l0 = (uint32_t)(uintptr_t)ring, l1 = l0 + kRSlot;
-        static_assert(kRLoads == 3 && kGStages == 3, "asm stream start layout");
-        asm volatile(
-            "s_mov_b32 m0, %0\n"
-            "global_load_lds_dwordx4 %4, %2\n"
-            "s_add_i32 m0, %0, 0x400\n"
-            "global_load_lds_dwordx4 %5, %2\n"
-            "s_add_i32 m0, %0, 0x800\n"
-            "global_load_lds_dwordx4 %6, %2\n"
-            "s_mov_b32 m0, %1\n"
-            "global_load_lds_dwordx4 %4, %3\n"
-            "s_add_i32 m0, %1, 0x400\n"
-            "global_load_lds_dwordx4 %5, %3\n"
-            "s_add_i32 m0, %1, 0x800\n"
-            "global_load_lds_dwordx4 %6, %3\n"
-            "s_waitcnt vmcnt(6)\n"
-            :
-            : "s"(l0), "s"(l1), "s"(src0), "s"(src1), "v"(doff[0]), "v"(doff[1]), "v"(doff[2])
-            : "memory", "m0", "scc");
+        // (the 6 slice loads issued after them may stay in flight)
+        issue(0);
+        issue(1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 2));
         auto f4 = [](f32x4_t v) { return make_float4(v.x, v.y, v.z, v.w); };
-        pv[0] = f4(t0), pv[1] = f4(t1), xo_in = f4(t2), xo_u = f4(t3);
+        pv[0] = f4(t0), pv[1] = f4(t1), pv[2] = f4(t2), pv[3] = f4(t3), pv[4] = f4(t4),
+        pv[5] = f4(t5), pv[6] = f4(t6), pv[7] = f4(t7);
+        xo_in = f4(t8), xo_u = f4(t9);
         av[0] = f4(a0), av[1] = f4(a1), av[2] = f4(a2), av[3] = f4(a3), av[4] = f4(a4),
         av[5] = f4(a5);
         bv[0] = f4(c0), bv[1] = f4(c1), bv[2] = f4(c2), bv[3] = f4(c3), bv[4] = f4(c4),
@@ -556,10 +563,16 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         if (PRO == kProNorm) {
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int k = 0; k < kGemvMaxPartials / kRWG; k++)
-                if ((int)threadIdx.x + k * kRWG < fz.np)  // past np: a clamped duplicate
+            for (int k = 0; k < kGemvMaxPartials / kWave; k++)
+                if (lane + k * kWave < fz.np)  // past np: a clamped duplicate
                     acc.x += pv[k].x, acc.y += pv[k].y, acc.z += pv[k].z, acc.w += pv[k].w;
-            const float4 P4 = wg_sum4(acc, scr);
+            if (wave == 0) {
+                const float4 t = make_float4(wave_sum_dpp(acc.x), wave_sum_dpp(acc.y),
+                                             wave_sum_dpp(acc.z), wave_sum_dpp(acc.w));
+                if (lane == 0) lds_write_f32x4(scr, t);
+            }
+            lds_barrier();
+            const float4 P4 = lds_read_f32x4(scr);
             const float K = (float)(nb * 32);
             s_out = s_pre;
             ra = 1.0f / sqrtf(P4.x / K + fz.eps);
@@ -568,14 +581,14 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             rb_s = rb * s_out;
 #pragma unroll
             for (int k = 0; k < kPB; k++) {
-                const int b = grp + 32 * k;
-                if (b < nb) {
-                    const float4 v = make_float4((av[k].x + ra * bv[k].x) * rb_s,
-                                                 (av[k].y + ra * bv[k].y) * rb_s,
-                                                 (av[k].z + ra * bv[k].z) * rb_s,
-                                                 (av[k].w + ra * bv[k].w) * rb_s);
-                    limbs_block8_lds(v, ge, tab + b * 80);
-                }
+                // branch-free: groups past the last block redo the last block
+                // (same values into the same entry)
+                const int b = min(grp + 32 * k, nb - 1);
+                const float4 v = make_float4((av[k].x + ra * bv[k].x) * rb_s,
+                                             (av[k].y + ra * bv[k].y) * rb_s,
+                                             (av[k].z + ra * bv[k].z) * rb_s,
+                                             (av[k].w + ra * bv[k].w) * rb_s);
+                limbs_block8_lds(v, ge, tab + b * 80);
             }
             if (xo_on)
                 reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
@@ -616,28 +629,20 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             }
         }
         lds_barrier();
-        // this lane's blocks from the LDS table
+        // this lane's blocks from the LDS table (a lane past the slice reads
+        // the last entry and gets scale 0)
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
-            const int lb = lane + kWave * i;
-            if (lb < slice_blocks) {
-                const uint8_t *e = tab + (b0 + lb) * 80;
+            const uint8_t *e = tab + min(b0 + lane + kWave * i, nb - 1) * 80;
 #pragma unroll
-                for (int l = 0; l < kLimbs; l++) {
-                    const float4 q = lds_read_f32x4(e + l * 16);
-                    L.q[i][l][0] = __builtin_bit_cast(int, q.x);
-                    L.q[i][l][1] = __builtin_bit_cast(int, q.y);
-                    L.q[i][l][2] = __builtin_bit_cast(int, q.z);
-                    L.q[i][l][3] = __builtin_bit_cast(int, q.w);
-                }
-                L.d[i] = lds_read_f32(e + 64);
-            } else {
-#pragma unroll
-                for (int l = 0; l < kLimbs; l++)
-#pragma unroll
-                    for (int w = 0; w < 4; w++) L.q[i][l][w] = 0;
-                L.d[i] = 0.f;
+            for (int l = 0; l < kLimbs; l++) {
+                const float4 q = lds_read_f32x4(e + l * 16);
+                L.q[i][l][0] = __builtin_bit_cast(int, q.x);
+                L.q[i][l][1] = __builtin_bit_cast(int, q.y);
+                L.q[i][l][2] = __builtin_bit_cast(int, q.z);
+                L.q[i][l][3] = __builtin_bit_cast(int, q.w);
             }
+            L.d[i] = lane + kWave * i < slice_blocks ? lds_read_f32(e + 64) : 0.f;
         }
     }
 
@@ -645,7 +650,6 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     // lb odd: the window starts 2 bytes early, qs = words 1..4, d = high half.
     const uint32_t sel = (lane & 1) ? 0x07060504u : 0x05040302u;
     const uint32_t dshift = (lane & 1) ? 16u : 0u;
-    float p1 = 0.f, p2 = 0.f, p3 = 0.f, p4 = 0.f;  // kEpiResid partial sums
     float gate = 0.f;                              // kEpiGeglu
     for (int it = 0; it < rows_rounds; it++) {
         const int row = r0 + it * G;
@@ -672,6 +676,13 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             }
             continue;
         }
+        if (EPI == kEpiResid) {
+            // kept for the epilogue after the loop: slot (row group, round,
+            // K-slice), so the K-slices of a row need no barrier per row
+            if (lane == 0)
+                lds_write_u32(rows_s + ((rw * kWave + it) * S + s) * 4, __builtin_bit_cast(uint32_t, a));
+            continue;
+        }
         bool have = true;
         if (S > 1 && !(EPI == kEpiRows && tg.split_out)) {
             // one barrier per row: partials alternate between two slots, and
@@ -688,24 +699,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             }
         }
         if (!have || row >= n) continue;
-        if (EPI == kEpiResid) {
-            const float x = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), it));
-            const float wp = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ewp), it));
-            const float wn = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ewn), it));
-            const float u = a * wp;
-            p1 += a * a;
-            p2 += x * u;
-            p3 += u * u;
-            p4 += x * x;
-            if (lane == 0) {
-                fz.u_out[row] = u;
-                fz.A_out[row] = x * wn;
-                fz.B_out[row] = u * wn;
-            }
-        } else if (S == 1) {
+        if (S == 1) {
             if (lane == 0) store_row(tg, row, a);
         } else if (tg.split_out) {
             if (lane == 0) tg.y[0][(size_t)s * n + row] = a;
@@ -714,15 +708,31 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         }
     }
     if (EPI == kEpiResid) {
-        // the workgroup's partial sums, waves in order
-        if (lane == 0) lds_write_f32x4(scr + wave * 16, make_float4(p1, p2, p3, p4));
+        // lane j of the first wave of each row group finishes round j's row:
+        // the K-slices summed in order, u = o·w_post, A = x·w_next,
+        // B = u·w_next; then the partial sums (lanes in DPP order, waves in
+        // order)
+        lds_barrier();
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int row = r0 + lane * G;
+        if (s == 0 && lane < rows_rounds && row < n) {
+            float o = 0.f;
+            for (int q = 0; q < S; q++) o += lds_read_f32(rows_s + ((rw * kWave + lane) * S + q) * 4);
+            const float u = o * ewp;
+            fz.u_out[row] = u;
+            fz.A_out[row] = ex * ewn;
+            fz.B_out[row] = u * ewn;
+            t = make_float4(o * o, ex * u, u * u, ex * ex);
+        }
+        t = make_float4(wave_sum_dpp(t.x), wave_sum_dpp(t.y), wave_sum_dpp(t.z), wave_sum_dpp(t.w));
+        if (lane == 0) lds_write_f32x4(scr + wave * 16, t);
         lds_barrier();
         if (threadIdx.x == 0) {
             float4 r = lds_read_f32x4(scr);
 #pragma unroll
             for (int w = 1; w < kRWG / kWave; w++) {
-                const float4 t = lds_read_f32x4(scr + w * 16);
-                r.x += t.x, r.y += t.y, r.z += t.z, r.w += t.w;
+                const float4 q = lds_read_f32x4(scr + w * 16);
+                r.x += q.x, r.y += q.y, r.z += q.z, r.w += q.w;
             }
             fz.part_out[blockIdx.x] = r;
         }

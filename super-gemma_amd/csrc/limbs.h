@@ -33,11 +33,14 @@ struct BlockLimbs {
 
 static_assert(sizeof(BlockLimbs) == SGQ_X_LIMBS_BYTES_PER_BLOCK, "limb table layout (sgq.h)");
 
-// The four digit nibbles (signed 4-bit, most significant limb in bits
-// 12..15) of a value already multiplied by (7/amax)·4096.
-__device__ __forceinline__ uint32_t limb_digits(float r) {
-    const int v = (int)__builtin_rintf(r);
-    return (uint32_t)(v + kLimbBias) ^ (uint32_t)kLimbBias;
+// The biased value u = v + 0x8888 of x·(7/amax)·4096 (id = 4096/d with the
+// hardware reciprocal: its < 1 ulp error moves x·id by < 0.01, and the
+// table's scale is d itself, so it only shifts which way a value rounds):
+// one FMA, rint, convert (the bias is added before rounding; |v| <= 28672
+// keeps u in [6280, 63624], where a float still resolves 2^-8).  Nibble k
+// of u is digit k plus 8; XOR with 8 turns it into the signed 4-bit digit.
+__device__ __forceinline__ uint32_t limb_biased(float x, float id) {
+    return (uint32_t)(int)__builtin_rintf(__builtin_fmaf(x, id, (float)kLimbBias));
 }
 
 template <int NBL>
@@ -46,12 +49,12 @@ __device__ __forceinline__ void quantize_values(const float (&v)[32], XLimbs<NBL
 #pragma unroll
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax * (1.0f / 7.0f);
-    const float id = d > 0.f ? 4096.0f * (1.0f / d) : 0.f;
+    const float id = d > 0.f ? 4096.0f * __builtin_amdgcn_rcpf(d) : 0.f;
     L.d[i] = d * kLimbScale;
     uint32_t word[kLimbs][4] = {};
 #pragma unroll
     for (int j = 0; j < 32; j++) {
-        const uint32_t u = limb_digits(v[j] * id);
+        const uint32_t u = limb_biased(v[j], id) ^ (uint32_t)kLimbBias;
         const int w = (j & 15) >> 2;
         const int shift = 4 * (2 * (j & 3) + (j >> 4));
 #pragma unroll
@@ -117,26 +120,28 @@ __device__ __forceinline__ float max8(float a) {
 }
 
 // The limb words of an 8-lane group's block, where lane g = lane & 7 holds
-// values 4g..4g+3 (a float4): amax over the group, then each lane packs its
-// 4 values into the nibbles they occupy in word (g & 3) of every limb, and
-// lanes g < 4 OR in the other half from lane g+4.  Valid in lanes g < 4;
-// returns the block scale.  Bit-identical to quantize_values (same amax,
-// d, scale and rint per value).  All 8 lanes of a group must be active.
+// values 4g..4g+3 (a float4): amax over the group; each lane's four biased
+// values (16 nibbles) are transposed with two byte permutes so that limb l
+// of value e lands in byte e of word l (low nibble for g < 4, high nibble
+// for g >= 4), and lanes g < 4 OR in the other half from lane g+4.  Valid
+// in lanes g < 4; returns the block scale.  Bit-identical to
+// quantize_values (same amax, d, scale, FMA and rint per value).  All 8
+// lanes of a group must be active.
 __device__ __forceinline__ float limbs_words8(const float4 v, int g, uint32_t (&word)[kLimbs]) {
     const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float d = amax * (1.0f / 7.0f);
-    const float id = d > 0.f ? 4096.0f * (1.0f / d) : 0.f;
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    const int hi = g >> 2;  // values 16..31 sit in the high nibble of each byte
-#pragma unroll
-    for (int l = 0; l < kLimbs; l++) word[l] = 0u;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const uint32_t u = limb_digits(vals[e] * id);
-        const int shift = 4 * (2 * e + hi);
-#pragma unroll
-        for (int l = 0; l < kLimbs; l++) word[l] |= ((u >> (4 * (kLimbs - 1 - l))) & 0xFu) << shift;
-    }
+    const float id = d > 0.f ? 4096.0f * __builtin_amdgcn_rcpf(d) : 0.f;
+    const uint32_t u01 = limb_biased(v.x, id) | (limb_biased(v.y, id) << 16);
+    const uint32_t u23 = limb_biased(v.z, id) | (limb_biased(v.w, id) << 16);
+    // byte e of hi/lo = digits (3, 2) / (1, 0) of value e, high nibble first
+    const uint32_t hi = __builtin_amdgcn_perm(u23, u01, 0x07050301u);
+    const uint32_t lo = __builtin_amdgcn_perm(u23, u01, 0x06040200u);
+    const uint32_t sh = (uint32_t)(g >> 2) * 4u;  // values 16..31: high nibbles
+    const uint32_t m = 0x0F0F0F0Fu, flip = 0x08080808u;
+    word[0] = (((hi >> 4) & m) ^ flip) << sh;
+    word[1] = ((hi & m) ^ flip) << sh;
+    word[2] = (((lo >> 4) & m) ^ flip) << sh;
+    word[3] = ((lo & m) ^ flip) << sh;
 #pragma unroll
     for (int l = 0; l < kLimbs; l++) word[l] |= dpp_mov<0x12C>(word[l]);  // row_ror:12
     return d * kLimbScale;

@@ -22,11 +22,11 @@ __device__ __forceinline__ float block_dot(const uint32_t (&w)[5], uint32_t sel,
     for (int j = 0; j < 4; j++) t[j] = (int)(__builtin_amdgcn_perm(w[j + 1], w[j], sel) ^ 0x88888888u);
     // Horner over the limbs in one exact integer accumulator: the result is
     // Σ (q-8)·v with |v| <= 28672, so |c| <= 32·8·28672 < 2^23 (exact as
-    // f32), and every partial fits the 24-bit multiply.
+    // f32); ×16 is a shift.
     int ci = 0;
 #pragma unroll
     for (int l = 0; l < kLimbs; l++) {
-        if (l) ci = __mul24(ci, 16);
+        if (l) ci *= 16;
 #pragma unroll
         for (int j = 0; j < 4; j++) ci = __builtin_amdgcn_sdot8(t[j], L.q[i][l][j], ci, false);
     }
