@@ -1,31 +1,32 @@
-// Q8_0-KV split-K decode attention kernels and launchers; the work-item
-// bodies (attn_split, attn_merge) live in attn_body.h and are shared with
-// the persistent decode kernel.
-#include "attn_body.h"
+// Q8_0-KV split-K decode attention kernels and launchers.  The split work
+// item (attn_chunk, int8-MFMA QK) is in attn_mfma.h; the split merge
+// (attn_merge) in attn_body.h, shared with the persistent decode kernel.
+#include "attn_mfma.h"
 
 namespace sgq {
 namespace {
 
-template <int QPK, bool FUSED, int WG>
-__global__ __launch_bounds__(WG) void attn_decode_q8_kernel(
+template <int QPK, bool FUSED, int W>
+__global__ __launch_bounds__(W * kWave) void attn_decode_q8_kernel(
     const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
     const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
     const uint32_t *__restrict__ step, int step_word, uint32_t kv_len_direct, int n_kv,
-    int n_splits, float scale, float *__restrict__ part, AttnPost post) {
+    int n_splits, float scale, float *__restrict__ part, float *__restrict__ out,
+    BlockLimbs *__restrict__ limbs_out, AttnPost post) {
     const uint32_t kv_len = step ? step[step_word] : kv_len_direct;
-    attn_split<QPK, FUSED, WG>(q, kq, ks, vq, vs, kv_len, n_kv, n_splits, scale, part, post,
-                               blockIdx.x, blockIdx.y, 0u, FUSED ? step[0] : 0u);
+    attn_chunk<QPK, FUSED, W>(q, kq, ks, vq, vs, kv_len, n_kv, n_splits, scale, part, out,
+                              limbs_out, post, blockIdx.x, blockIdx.y, FUSED ? step[0] : 0u);
 }
 
 // The same with the merge done by the last split of each kv head to finish
 // (no second launch): every split stores its partial with agent-scope
-// stores (attn_split), waits for them, and bumps the kv head's counter; the
+// stores (attn_chunk), waits for them, and bumps the kv head's counter; the
 // one that sees n_splits-1 merges, reading the partials with agent-scope
 // loads, and resets the counter for the next launch.  The merge order is
 // still split order 0..S-1, so the result does not depend on which split
-// finished last.
-template <int QPK, int WG>
-__global__ __launch_bounds__(WG) void attn_decode_merge_kernel(
+// finished last.  With one split the workgroup writes the limbs itself.
+template <int QPK, int W>
+__global__ __launch_bounds__(W * kWave) void attn_decode_merge_kernel(
     const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
     const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
     const uint32_t *__restrict__ step, int step_word, int n_kv, int n_splits, float scale,
@@ -33,8 +34,9 @@ __global__ __launch_bounds__(WG) void attn_decode_merge_kernel(
     BlockLimbs *__restrict__ limbs_out) {
     __shared__ __align__(16) float o_s[QPK * kHD];
     __shared__ int last_s;
-    attn_split<QPK, true, WG>(nullptr, kq, ks, vq, vs, step[step_word], n_kv, n_splits, scale,
-                              part, post, blockIdx.x, blockIdx.y, 0u, step[0]);
+    attn_chunk<QPK, true, W>(nullptr, kq, ks, vq, vs, step[step_word], n_kv, n_splits, scale,
+                             part, nullptr, limbs_out, post, blockIdx.x, blockIdx.y, step[0]);
+    if (n_splits == 1) return;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -84,21 +86,24 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + kAttnPartOff);
     const int qpk = n_q / n_kv;
     dim3 grid(n_kv, n_splits);
-#define SGQ_ATTN(Q)                                                                               \
-    case Q:                                                                                       \
-        hipLaunchKernelGGL((attn_decode_q8_kernel<Q, false, kAWG>), grid, dim3(kAWG),             \
-                           attn_lds_bytes(Q, kAWG), st, q, kq, ks, vq, vs, step, step_word,       \
-                           kv_len, n_kv, n_splits, scale, part, AttnPost{});                      \
-        SGQ_HIP(hipGetLastError());                                                               \
-        hipLaunchKernelGGL(attn_merge_kernel<Q>, dim3(n_kv), dim3(Q * kHD), 0, st, part,          \
-                           n_splits, out, static_cast<BlockLimbs *>(limbs_out));                  \
-        break;
-    switch (qpk) {
-        SGQ_ATTN(1)
-        SGQ_ATTN(2)
-        default:
-            return fail(SGQ_ERR_VALIDATION, "attn_decode_q8: %d q heads per kv head unsupported",
-                        qpk);
+    SGQ_CHECK(qpk == 1 || qpk == 2, "attn_decode_q8: %d q heads per kv head unsupported", qpk);
+    BlockLimbs *lo = static_cast<BlockLimbs *>(limbs_out);
+    float *out1 = n_splits == 1 ? out : nullptr;
+    BlockLimbs *lo1 = n_splits == 1 ? lo : nullptr;
+#define SGQ_ATTN(Q, W)                                                                            \
+    hipLaunchKernelGGL((attn_decode_q8_kernel<Q, false, W>), grid, dim3(W * kWave), 0, st, q, kq, \
+                       ks, vq, vs, step, step_word, kv_len, n_kv, n_splits, scale, part, out1,    \
+                       lo1, AttnPost{})
+    if (qpk == 1) SGQ_ATTN(1, kAttnWaves);
+    else SGQ_ATTN(2, kAttnWaves);
+    SGQ_HIP(hipGetLastError());
+    if (n_splits > 1) {
+        if (qpk == 1)
+            hipLaunchKernelGGL(attn_merge_kernel<1>, dim3(n_kv), dim3(kHD), 0, st, part, n_splits,
+                               out, lo);
+        else
+            hipLaunchKernelGGL(attn_merge_kernel<2>, dim3(n_kv), dim3(2 * kHD), 0, st, part,
+                               n_splits, out, lo);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());
@@ -131,28 +136,35 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
     dim3 grid(n_kv, n_splits);
     unsigned *counters = reinterpret_cast<unsigned *>(static_cast<uint8_t *>(workspace) +
                                                       kAttnCounterOff);
-#define SGQ_ATTN(Q)                                                                               \
-    case Q:                                                                                       \
-        if (merge_in_launch) {                                                                    \
-            hipLaunchKernelGGL((attn_decode_merge_kernel<Q, kAWG>), grid, dim3(kAWG),             \
-                               attn_lds_bytes(Q, kAWG), st, kq, ks, vq, vs, step, step_word,      \
-                               n_kv, n_splits, scale, part, post, counters,                       \
-                               static_cast<BlockLimbs *>(limbs_out));                             \
-            break;                                                                                \
-        }                                                                                         \
-        hipLaunchKernelGGL((attn_decode_q8_kernel<Q, true, kAWG>), grid, dim3(kAWG),              \
-                           attn_lds_bytes(Q, kAWG), st, nullptr, kq, ks, vq, vs, step, step_word, \
-                           0u, n_kv, n_splits, scale, part, post);                                \
-        SGQ_HIP(hipGetLastError());                                                               \
-        hipLaunchKernelGGL(attn_merge_kernel<Q>, dim3(n_kv), dim3(Q * kHD), 0, st, part,          \
-                           n_splits, out, static_cast<BlockLimbs *>(limbs_out));                  \
-        break;
-    switch (n_q / n_kv) {
-        SGQ_ATTN(1)
-        SGQ_ATTN(2)
-        default:
-            return fail(SGQ_ERR_VALIDATION, "attn (fused): %d q heads per kv head unsupported",
-                        n_q / n_kv);
+    const int qpk = n_q / n_kv;
+    SGQ_CHECK(qpk == 1 || qpk == 2, "attn (fused): %d q heads per kv head unsupported", qpk);
+    BlockLimbs *lo = static_cast<BlockLimbs *>(limbs_out);
+    if (merge_in_launch) {
+#define SGQ_ATTN(Q, W)                                                                            \
+    hipLaunchKernelGGL((attn_decode_merge_kernel<Q, W>), grid, dim3(W * kWave), 0, st, kq, ks, vq, \
+                       vs, step, step_word, n_kv, n_splits, scale, part, post, counters, lo)
+        if (qpk == 1) SGQ_ATTN(1, kAttnWaves);
+        else SGQ_ATTN(2, kAttnWaves);
+#undef SGQ_ATTN
+        SGQ_HIP(hipGetLastError());
+        return SGQ_OK;
+    }
+    float *out1 = n_splits == 1 ? out : nullptr;
+    BlockLimbs *lo1 = n_splits == 1 ? lo : nullptr;
+#define SGQ_ATTN(Q, W)                                                                            \
+    hipLaunchKernelGGL((attn_decode_q8_kernel<Q, true, W>), grid, dim3(W * kWave), 0, st, nullptr, \
+                       kq, ks, vq, vs, step, step_word, 0u, n_kv, n_splits, scale, part, out1,    \
+                       lo1, post)
+    if (qpk == 1) SGQ_ATTN(1, kAttnWaves);
+    else SGQ_ATTN(2, kAttnWaves);
+    SGQ_HIP(hipGetLastError());
+    if (n_splits > 1) {
+        if (qpk == 1)
+            hipLaunchKernelGGL(attn_merge_kernel<1>, dim3(n_kv), dim3(kHD), 0, st, part, n_splits,
+                               out, lo);
+        else
+            hipLaunchKernelGGL(attn_merge_kernel<2>, dim3(n_kv), dim3(2 * kHD), 0, st, part,
+                               n_splits, out, lo);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());

@@ -44,6 +44,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 128, BN = 128, KB = 4;   // tile rows, cols, blocks per stage
 constexpr int ROWB = KB * 32 + 16;          // padded LDS row bytes (144)
 constexpr int kMWG = 256;
+#ifndef SGQ_MMQ_WG_PER_CU
+#define SGQ_MMQ_WG_PER_CU 2
+#endif
 
 struct Stage {
     int8_t a[BM * ROWB];      // activations, [row][k]
@@ -145,7 +148,7 @@ __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
     }
 }
 
-__global__ __launch_bounds__(kMWG, 2) void mmq_kernel(const uint8_t *__restrict__ W,
+__global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint8_t *__restrict__ W,
                                                       const int8_t *__restrict__ xq,
                                                       const uint16_t *__restrict__ xs,
                                                       float *__restrict__ out, int m, int n,

@@ -437,6 +437,13 @@ struct LayerW {
     uint32_t slots;
 };
 
+// Decode attention splits per kv head: 8 for a 1024-slot ring (one 32-slot
+// group per wave of the 4-wave workgroups), about 512 slots per workgroup
+// for a linear cache (measured best at 8K).
+static int decode_splits(const LayerW &L) {
+    return L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 8;
+}
+
 struct sgq_model {
     sgq_ctx *ctx;
     sgq_model_config cfg;
@@ -522,9 +529,7 @@ int record_step(sgq_model *m, float *logits) {
         qkv.count = L.wv ? 3 : 2;
         const float *v_src = L.wv ? m->v_raw : m->k_raw;
         if ((rc = launch_gemv_limbs(st, qkv, xl, H))) return rc;
-        // splits: 16 for a 1024-slot ring (64 slots per workgroup), about 512
-        // slots per workgroup for a linear cache (measured best)
-        const int n_splits = L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 16;
+        const int n_splits = decode_splits(L);
         if ((rc = launch_attn_decode_fused(
                  st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
                  m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
@@ -621,7 +626,7 @@ int record_step_fused(sgq_model *m, float *logits) {
         }
         if ((rc = launch_gemv_fused(st, qkv, nullptr, (uint32_t)H, pro, kEpiRows, pre))) return rc;
         const float *v_src = L.wv ? m->v_raw : m->k_raw;
-        const int n_splits = L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 16;
+        const int n_splits = decode_splits(L);
         if ((rc = launch_attn_decode_fused(
                  st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
                  m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
