@@ -63,7 +63,8 @@ __device__ __forceinline__ uint32_t unpack_hi(uint32_t q) {
 }
 
 struct Prefetch {
-    uint4 a[4];        // 64 activation bytes: row = tid/2, k-half = tid%2
+    v4i a[4];          // 64 activation bytes: row = tid/2, k-half = tid%2 (native
+                       // vectors: HIP's uint4 is a struct, copied through scratch)
     uint32_t w[9];     // two Q4_0 blocks (36 bytes): col = tid/2, blocks 2*(tid%2)+{0,1}
     uint16_t da[4];    // threads < 128: 4 block scales of row tid
 };
@@ -81,9 +82,9 @@ __device__ __forceinline__ void load_stage(Prefetch &pf, const int8_t *__restric
         for (int i = 0; i < 4; i++) {
             const int kk = kb + i * 16;
             if (gm < m && kk < b_end * 32)
-                pf.a[i] = *reinterpret_cast<const uint4 *>(xq + (size_t)gm * k + kk);
+                pf.a[i] = *reinterpret_cast<const v4i *>(xq + (size_t)gm * k + kk);
             else
-                pf.a[i] = make_uint4(0, 0, 0, 0);
+                pf.a[i] = v4i{0, 0, 0, 0};
         }
     }
     {   // weights: two blocks, 36 bytes, 4-aligned (b0 and the pair index are even)
@@ -112,13 +113,50 @@ __device__ __forceinline__ void load_stage(Prefetch &pf, const int8_t *__restric
     }
 }
 
+// Aligned shapes (m % BM == 0, n % BN == 0, nb % KB == 0): no bounds
+// checks; each thread's three sources are base pointers that advance by a
+// constant per stage, and the 4 block scales of a row are one 8-byte load.
+struct AlignedSrc {
+    const int8_t *a;      // row t/2 of the tile, byte 64·(t%2) of block 0
+    const uint32_t *w;    // column t/2, block 2·(t%2)
+    const uint2 *da;      // row t (t < BM): scales of blocks 0..3
+};
+
+__device__ __forceinline__ AlignedSrc aligned_src(const int8_t *__restrict__ xq,
+                                                  const uint16_t *__restrict__ xs,
+                                                  const uint8_t *__restrict__ W, int k, int nb,
+                                                  int m0, int n0) {
+    const int t = threadIdx.x;
+    AlignedSrc s;
+    s.a = xq + (size_t)(m0 + (t >> 1)) * k + (t & 1) * 64;
+    s.w = reinterpret_cast<const uint32_t *>(W + ((size_t)(n0 + (t >> 1)) * nb + 2 * (t & 1)) * 18);
+    s.da = reinterpret_cast<const uint2 *>(xs + (size_t)(m0 + (t & (BM - 1))) * nb);
+    return s;
+}
+
+__device__ __forceinline__ void load_stage_al(Prefetch &pf, const AlignedSrc &src, int b0) {
+    const v4i *a = reinterpret_cast<const v4i *>(src.a + b0 * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) pf.a[i] = a[i];
+    const uint32_t *w = src.w + (b0 * 18) / 4;  // b0 % 4 == 0: 72 B per stage
+#pragma unroll
+    for (int j = 0; j < 9; j++) pf.w[j] = __builtin_nontemporal_load(w + j);
+    if (threadIdx.x < BM) {
+        const uint2 d = src.da[b0 / 4];
+        pf.da[0] = (uint16_t)(d.x & 0xffffu);
+        pf.da[1] = (uint16_t)(d.x >> 16);
+        pf.da[2] = (uint16_t)(d.y & 0xffffu);
+        pf.da[3] = (uint16_t)(d.y >> 16);
+    }
+}
+
 __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
     const int t = threadIdx.x;
     {
         const int row = t >> 1, half = t & 1;
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            *reinterpret_cast<uint4 *>(&S.a[row * ROWB + half * 64 + i * 16]) = pf.a[i];
+            *reinterpret_cast<v4i *>(&S.a[row * ROWB + half * 64 + i * 16]) = pf.a[i];
     }
     {
         const int col = t >> 1, pair = t & 1;
@@ -148,6 +186,7 @@ __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
     }
 }
 
+template <bool AL>
 __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint8_t *__restrict__ W,
                                                       const int8_t *__restrict__ xq,
                                                       const uint16_t *__restrict__ xs,
@@ -187,16 +226,23 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
     // waits in registers for its LDS slot and stage s+2 is in flight; the
     // loop is unrolled by two so both prefetch sets stay in registers
     Prefetch pf0, pf1;
+    AlignedSrc src{};
+    if (AL) src = aligned_src(xq, xs, W, k, nb, m0, n0);
+    auto load = [&](Prefetch &pf, int b0) {
+        if (AL)
+            load_stage_al(pf, src, b0);
+        else
+            load_stage(pf, xq, xs, W, m, n, k, nb, m0, n0, b0, b_end);
+    };
     if (n_stages > 0) {
-        load_stage(pf0, xq, xs, W, m, n, k, nb, m0, n0, b_beg, b_end);
+        load(pf0, b_beg);
         store_stage(pf0, stages[0]);
     }
-    if (n_stages > 1) load_stage(pf1, xq, xs, W, m, n, k, nb, m0, n0, b_beg + KB, b_end);
+    if (n_stages > 1) load(pf1, b_beg + KB);
     __syncthreads();
 
     auto step = [&](int s, Prefetch &pl, Prefetch &ps) {
-        if (s + 2 < n_stages)
-            load_stage(pl, xq, xs, W, m, n, k, nb, m0, n0, b_beg + (s + 2) * KB, b_end);
+        if (s + 2 < n_stages) load(pl, b_beg + (s + 2) * KB);
         const Stage &S = stages[s & 1];
 #pragma unroll 1  // keeps the 4 live MFMA results + 64 accumulators within 256 VGPRs
         for (int blk = 0; blk < KB; blk++) {
@@ -247,11 +293,11 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int col = n0 + wn * 64 + j * 32 + r;
-            if (col >= n) continue;
+            if (!AL && col >= n) continue;
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int row = m0 + wm * 64 + i * 32 + 8 * (q / 4) + 4 * h + (q % 4);
-                if (row < m) dst[(size_t)row * n + col] = acc[i][j][q];
+                if (AL || row < m) dst[(size_t)row * n + col] = acc[i][j][q];
             }
         }
 }
@@ -289,15 +335,26 @@ int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const u
     static bool attr = false;
     const size_t lds = 2 * sizeof(Stage);
     if (!attr) {
-        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel,
+        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<true>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
     const int mt = (int)((m + BM - 1) / BM), nt = (int)((n + BN - 1) / BN);
     float *dst = split_k == 1 ? y : partials;
-    hipLaunchKernelGGL(mmq_kernel, dim3(mt * nt, split_k), dim3(kMWG), lds, st,
-                       static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k, mt,
-                       nt, (int)split_k);
+    // every split's block range is a multiple of KB when nb is (the split
+    // bounds are rounded down to KB)
+    const bool aligned = m % BM == 0 && n % BN == 0 && (k / 32) % KB == 0 &&
+                         ((uintptr_t)xs & 7) == 0;
+    if (aligned)
+        hipLaunchKernelGGL(mmq_kernel<true>, dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+                           static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k,
+                           mt, nt, (int)split_k);
+    else
+        hipLaunchKernelGGL(mmq_kernel<false>, dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+                           static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k,
+                           mt, nt, (int)split_k);
     SGQ_HIP(hipGetLastError());
     if (split_k > 1) {
         const uint64_t n4 = (uint64_t)m * n / 4;
