@@ -273,10 +273,14 @@ __device__ __forceinline__ void settle(float4 &v) {
     asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
-// An 8-lane group's limb block into an LDS table entry (BlockLimbs layout).
-__device__ __forceinline__ void limbs_block8_lds(const float4 v, int g, uint8_t *dst) {
-    uint32_t word[kLimbs];
-    const float d = limbs_words8(v, g, word);
+// An 8-lane group's limb block written as an LDS table entry (BlockLimbs
+// layout) from its words (limbs_words8).  The words of all of a thread's
+// blocks are computed before any of them is written: the asm stores are
+// scheduling barriers, and each block is a long dependent chain (max over
+// the group, reciprocal, rounding, byte transposes), so computing and
+// storing block by block would run the chains one after another.
+__device__ __forceinline__ void limb_words_to_lds(const uint32_t (&word)[kLimbs], float d, int g,
+                                                  uint8_t *dst) {
     if (g < 4) {
 #pragma unroll
         for (int l = 0; l < kLimbs; l++) lds_write_u32(dst + (l * 4 + g) * 4, word[l]);
@@ -579,17 +583,21 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             const float sx = s_out * s_out * (P4.w + 2.f * ra * P4.y + ra * ra * P4.z);
             const float rb = 1.0f / sqrtf(sx / K + fz.eps);
             rb_s = rb * s_out;
+            uint32_t wd[kPB][kLimbs];
+            float dd[kPB];
 #pragma unroll
             for (int k = 0; k < kPB; k++) {
-                // branch-free: groups past the last block redo the last block
-                // (same values into the same entry)
-                const int b = min(grp + 32 * k, nb - 1);
                 const float4 v = make_float4((av[k].x + ra * bv[k].x) * rb_s,
                                              (av[k].y + ra * bv[k].y) * rb_s,
                                              (av[k].z + ra * bv[k].z) * rb_s,
                                              (av[k].w + ra * bv[k].w) * rb_s);
-                limbs_block8_lds(v, ge, tab + b * 80);
+                dd[k] = limbs_words8(v, ge, wd[k]);
             }
+            // branch-free: groups past the last block redo the last block
+            // (same values into the same entry)
+#pragma unroll
+            for (int k = 0; k < kPB; k++)
+                limb_words_to_lds(wd[k], dd[k], ge, tab + min(grp + 32 * k, nb - 1) * 80);
             if (xo_on)
                 reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
                     make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
@@ -618,32 +626,61 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             }
             const float4 t = wg_sum4(make_float4(ss, 0.f, 0.f, 0.f), scr);
             const float r = 1.0f / sqrtf(t.x / (float)(nb * 32) + fz.eps);
+            uint32_t wd[kPB][kLimbs];
+            float dd[kPB];
 #pragma unroll
             for (int k = 0; k < kPB; k++) {
-                const int b = grp + 32 * k;
-                if (b < nb) {
-                    const float4 v = make_float4(x0[k].x * r * av[k].x, x0[k].y * r * av[k].y,
-                                                 x0[k].z * r * av[k].z, x0[k].w * r * av[k].w);
-                    limbs_block8_lds(v, ge, tab + b * 80);
-                }
+                const float4 v = make_float4(x0[k].x * r * av[k].x, x0[k].y * r * av[k].y,
+                                             x0[k].z * r * av[k].z, x0[k].w * r * av[k].w);
+                dd[k] = limbs_words8(v, ge, wd[k]);
             }
+#pragma unroll
+            for (int k = 0; k < kPB; k++)
+                if (grp + 32 * k < nb) limb_words_to_lds(wd[k], dd[k], ge, tab + (grp + 32 * k) * 80);
         }
         lds_barrier();
         // this lane's blocks from the LDS table (a lane past the slice reads
-        // the last entry and gets scale 0)
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const uint8_t *e = tab + min(b0 + lane + kWave * i, nb - 1) * 80;
-#pragma unroll
-            for (int l = 0; l < kLimbs; l++) {
-                const float4 q = lds_read_f32x4(e + l * 16);
-                L.q[i][l][0] = __builtin_bit_cast(int, q.x);
-                L.q[i][l][1] = __builtin_bit_cast(int, q.y);
-                L.q[i][l][2] = __builtin_bit_cast(int, q.z);
-                L.q[i][l][3] = __builtin_bit_cast(int, q.w);
-            }
-            L.d[i] = lane + kWave * i < slice_blocks ? lds_read_f32(e + 64) : 0.f;
-        }
+        // the last entry and gets scale 0): all reads issued, then one wait
+        // that names their registers (named variables, not an array of
+        // vectors, which has read back wrong components on this compiler)
+        static_assert(NBL <= 3 && kLimbs == 4, "table read layout");
+        f32x4_t r00 = {}, r01 = {}, r02 = {}, r03 = {}, r10 = {}, r11 = {}, r12 = {}, r13 = {},
+                r20 = {}, r21 = {}, r22 = {}, r23 = {};
+        float e0 = 0.f, e1 = 0.f, e2 = 0.f;
+        const uint32_t ta0 = (uint32_t)(uintptr_t)(tab + min(b0 + lane, nb - 1) * 80);
+        const uint32_t ta1 = (uint32_t)(uintptr_t)(tab + min(b0 + lane + kWave, nb - 1) * 80);
+        const uint32_t ta2 = (uint32_t)(uintptr_t)(tab + min(b0 + lane + 2 * kWave, nb - 1) * 80);
+#define SGQ_RDBLK(A, Q0, Q1, Q2, Q3, D)                                                      \
+    asm volatile("ds_read_b128 %0, %5\n ds_read_b128 %1, %5 offset:16\n"                      \
+                 "ds_read_b128 %2, %5 offset:32\n ds_read_b128 %3, %5 offset:48\n"            \
+                 "ds_read_b32 %4, %5 offset:64"                                              \
+                 : "=&v"(Q0), "=&v"(Q1), "=&v"(Q2), "=&v"(Q3), "=&v"(D)                       \
+                 : "v"(A)                                                                    \
+                 : "memory")
+        SGQ_RDBLK(ta0, r00, r01, r02, r03, e0);
+        if (NBL > 1) SGQ_RDBLK(ta1, r10, r11, r12, r13, e1);
+        if (NBL > 2) SGQ_RDBLK(ta2, r20, r21, r22, r23, e2);
+#undef SGQ_RDBLK
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(r00), "+v"(r01), "+v"(r02), "+v"(r03), "+v"(r10), "+v"(r11),
+                       "+v"(r12), "+v"(r13), "+v"(r20), "+v"(r21), "+v"(r22), "+v"(r23),
+                       "+v"(e0), "+v"(e1), "+v"(e2)
+                     :
+                     : "memory");
+        auto f4 = [](f32x4_t v) { return make_float4(v.x, v.y, v.z, v.w); };
+        auto put = [&](int i, float4 q0, float4 q1, float4 q2, float4 q3, float d) {
+#define SGQ_PUT(l, Q)                                     \
+    L.q[i][l][0] = __builtin_bit_cast(int, Q.x);          \
+    L.q[i][l][1] = __builtin_bit_cast(int, Q.y);          \
+    L.q[i][l][2] = __builtin_bit_cast(int, Q.z);          \
+    L.q[i][l][3] = __builtin_bit_cast(int, Q.w);
+            SGQ_PUT(0, q0) SGQ_PUT(1, q1) SGQ_PUT(2, q2) SGQ_PUT(3, q3)
+#undef SGQ_PUT
+            L.d[i] = lane + kWave * i < slice_blocks ? d : 0.f;
+        };
+        put(0, f4(r00), f4(r01), f4(r02), f4(r03), e0);
+        if (NBL > 1) put(1, f4(r10), f4(r11), f4(r12), f4(r13), e1);
+        if (NBL > 2) put(2, f4(r20), f4(r21), f4(r22), f4(r23), e2);
     }
 
     // lb even: qs = bytes 2..17 of the window, d = low half of word 0;
