@@ -19,6 +19,9 @@ batch of synthetic input, already resident in HBM:
           BASELINE config 4 prefill: 4096 queries, causal / sliding-1024.
   attn_decode_4k, attn_decode_32k, attn_decode_128k
           BASELINE config 4 decode over a 4K / 32K / 128K Q8_0 context.
+  head_q6k
+          the real checkpoint's tied Q6_K LM head (262144 x 5376, rows padded
+          to 4416 B) with the 30*tanh softcap (gemv_q6_k_logits).
 
 The timed region is bracketed by torch.cuda.synchronize() and measured with
 HIP events on the stream the kernels run on.  The cpu_baseline leg times the
@@ -206,6 +209,44 @@ class AttnDecode:
             "config": {"workload": f"attn_decode_q8 ctx {self.ctx_len}, 32q/16kv, hd 128, "
                                    f"{self.splits} splits, {self.copies} rotating caches "
                                    "(BASELINE config 4)", "bytes_per_launch": self.bytes},
+        }
+
+
+class HeadQ6K:
+    """The Q6_K tied LM head of the real checkpoint (gemv_q6_k_logits.wgsl):
+    262144 vocabulary rows x K=5376, rows padded to 4416 bytes, 30*tanh
+    softcap; 1.16 GB per launch, so it streams from HBM."""
+    kernel = "gemv_q6_k_kernel"
+
+    def __init__(self, ctx, torch, n=262144, k=5376, stride=4416):
+        self.ctx, self.torch = ctx, torch
+        self.n, self.k, self.stride = n, k, stride
+        self.w = torch.zeros(n * stride, dtype=torch.uint8, device="cuda")
+        # random bytes, then bounded sub-scales and small d (parity_logits.rs:31-51)
+        g = torch.Generator(device="cuda").manual_seed(61)
+        self.w.copy_(torch.randint(0, 256, (n * stride,), dtype=torch.uint8, device="cuda",
+                                   generator=g))
+        blk = self.w.view(n, stride)[:, :(k // 256) * 210].reshape(n, k // 256, 210)
+        blk[:, :, 192:208] = (blk[:, :, 192:208] & 15).to(torch.int16).sub(8).to(torch.int8).view(torch.uint8)
+        d = (torch.rand(n, k // 256, device="cuda", generator=g) * 1e-3).to(torch.float16)
+        blk[:, :, 208:210] = d.view(torch.uint8).view(n, k // 256, 2)
+        self.x = torch.empty(k, dtype=torch.float32, device="cuda")
+        ctx.fill_normal(self.x, seed=62)
+        self.y = torch.empty(n, dtype=torch.float32, device="cuda")
+        self.bytes = n * stride + k * 4 + n * 4
+
+    def step(self, i):
+        self.ctx.gemv_q6_k(self.w, self.stride, self.x, self.y, self.n, self.k, 30.0)
+
+    def result(self, ms_per_step):
+        gbs = self.bytes / (ms_per_step * 1e-3) / 1e9
+        return {
+            "value": gbs, "unit": "GB/s", "dtype": "q6_k weights, f16 x (from fp32), f32 dot",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "config": {"workload": f"gemv_q6_k_logits N={self.n} K={self.k} stride {self.stride} "
+                                   "(the real checkpoint's tied Q6_K head)",
+                       "bytes_per_launch": self.bytes},
         }
 
 
@@ -405,7 +446,7 @@ def main():
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
-                             "attn_decode_128k"])
+                             "attn_decode_128k", "head_q6k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -429,6 +470,8 @@ def main():
         wl = Gemv(ctx, torch)
     elif args.workload == "mmq":
         wl = Mmq(ctx, torch)
+    elif args.workload == "head_q6k":
+        wl = HeadQ6K(ctx, torch)
     elif args.workload == "attn_prefill":
         wl = AttnPrefill(ctx, torch)
     elif args.workload == "attn_prefill_sliding":

@@ -144,6 +144,17 @@ int sgq_x_limbs(sgq_ctx *ctx, const float *x, void *x_limbs, uint32_t k);
 int sgq_gemv_q4_0_limbs(sgq_ctx *ctx, uint32_t n_targets, const void *const *w, float *const *y,
                         const uint32_t *rows, const void *x_limbs, uint32_t k, float softcap);
 
+/* Q6_K LM head: y[n] = softcap·tanh((E[n×k]·x[k]) / softcap) (softcap <= 0:
+ * the raw dot).  Replaces gemv_q6_k_logits
+ * (crates/sg-gpu/shaders/gemv_q6_k_logits.wgsl:41-104; registry entry
+ * crates/sg-gpu/build.rs:322-327).  E holds rows of k/256 GGUF Q6_K
+ * super-blocks (210 B each, crates/sg-gguf/src/q6_k.rs:25-62) at a byte
+ * stride of row_stride (a multiple of 16; the reference pads 4410 -> 4416
+ * at k = 5376); x is fp32 and is rounded to f16, the reference's activation
+ * type; y fp32.  k % 256 == 0, k <= 6144; E 16-byte aligned. */
+int sgq_gemv_q6_k(sgq_ctx *ctx, const void *w, size_t row_stride, const float *x, float *y,
+                  uint32_t n, uint32_t k, float softcap);
+
 /* Q8_0 quantization of n fp32 values (n % 32 == 0) into f16 scales [n/32] and
  * int8 quants [n]: kv_quant_q8 (crates/sg-gpu/shaders/kv_quant_q8.wgsl:30-57),
  * d = amax*(1/127), q = round_ties_even(x/d) with an IEEE reciprocal. */

@@ -47,6 +47,10 @@ def lib():
             "sgo_q4_0_dequant_rows": (None, [P, SZ, SZ, P]),
             "sgo_random_q4_0": (U64, [U64, P, SZ]),
             "sgo_gemv_q4_0_rows": (None, [P, P, SZ, P, SZ, P]),
+            "sgo_q6_k_dequant_block": (None, [P, P]),
+            "sgo_q6_k_dequant_rows": (None, [P, SZ, SZ, SZ, P]),
+            "sgo_random_q6_k_rows": (U64, [U64, P, SZ, SZ, SZ]),
+            "sgo_gemv_q6_k_logits": (None, [P, SZ, P, SZ, SZ, C.c_double, P]),
             "sgo_dot_f64": (C.c_double, [P, P, SZ]),
             "sgo_matmul_q4_0": (None, [P, P, SZ, SZ, SZ, P, C.c_int]),
             "sgo_quant_q8_0": (None, [P, SZ, P, P]),
@@ -104,6 +108,12 @@ class Rng:
         self.state = lib().sgo_rng_u64_vec(self.state, _p(out), n)
         return out
 
+    def random_q6_k_rows(self, n_rows: int, k: int, row_stride: int) -> np.ndarray:
+        """parity_logits.rs:31-51 rows in a padded layout (row_stride bytes)."""
+        out = np.empty(n_rows * row_stride, np.uint8)
+        self.state = lib().sgo_random_q6_k_rows(self.state, _p(out), n_rows, k, row_stride)
+        return out
+
     def random_q4_0(self, n_blocks: int) -> np.ndarray:
         out = np.empty(n_blocks * 18, np.uint8)
         self.state = lib().sgo_random_q4_0(self.state, _p(out), n_blocks)
@@ -138,6 +148,25 @@ def q4_0_dequant(w: np.ndarray, n_rows: int, k: int) -> np.ndarray:
     out = np.empty((n_rows, k), np.float32)
     lib().sgo_q4_0_dequant_rows(_p(w), n_rows, k, _p(out))
     return out
+
+
+def q6_k_dequant(w: np.ndarray, n_rows: int, k: int, row_stride: int | None = None) -> np.ndarray:
+    """q6_k.rs:41-62 over rows of k/256 blocks at row_stride bytes."""
+    row_stride = row_stride or (k // 256) * 210
+    w = np.ascontiguousarray(w, np.uint8)
+    out = np.empty((n_rows, k), np.float32)
+    lib().sgo_q6_k_dequant_rows(_p(w), row_stride, n_rows, k, _p(out))
+    return out
+
+
+def gemv_q6_k_logits(w: np.ndarray, row_stride: int, x, n: int, k: int,
+                     softcap: float = 30.0) -> np.ndarray:
+    """parity_logits.rs:84-98: f64 dot per row, softcap*tanh(dot/softcap)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(n, np.float32)
+    lib().sgo_gemv_q6_k_logits(_p(w), row_stride, _p(x), n, k, float(softcap), _p(y))
+    return y
 
 
 def gemv_rows(w: np.ndarray, x: np.ndarray, k: int, rows) -> np.ndarray:

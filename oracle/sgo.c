@@ -170,6 +170,86 @@ uint64_t sgo_random_q4_0(uint64_t state, uint8_t *out, size_t n_blocks) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Q6_K — crates/sg-gguf/src/q6_k.rs:41-62 (ggml dequantize_row_q6_K)       */
+/* block: ql[128] low nibbles, qh[64] 2-bit highs, int8 scales[16], f16 d   */
+/* ------------------------------------------------------------------------ */
+
+#define Q6K_BLOCK_BYTES 210
+#define Q6K_WEIGHTS 256
+
+/* w = d * scale[sub] * (q - 32), one f32 product chain d*sc*q as in the
+ * reference (d widened to f32, sc and q converted to f32). */
+void sgo_q6_k_dequant_block(const uint8_t *blk, float *out) {
+    const uint8_t *ql0 = blk, *qh0 = blk + 128;
+    const int8_t *sc0 = (const int8_t *)(blk + 192);
+    const float d = sgo_f16_to_f32((uint16_t)(blk[208] | (blk[209] << 8)));
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *ql = ql0 + half * 64, *qh = qh0 + half * 32;
+        const int8_t *sc = sc0 + half * 8;
+        float *y = out + half * 128;
+        for (int l = 0; l < 32; l++) {
+            const int is = l / 16;
+            const int q1 = ((ql[l] & 0x0F) | ((qh[l] & 0x03) << 4)) - 32;
+            const int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 0x03) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 0x03) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 0x03) << 4)) - 32;
+            y[l] = d * (float)sc[is] * (float)q1;
+            y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+            y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+            y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
+    }
+}
+
+/* Rows of k/256 blocks at a byte stride (the GPU layout pads rows). */
+void sgo_q6_k_dequant_rows(const uint8_t *w, size_t row_stride, size_t n_rows, size_t k,
+                           float *out) {
+    const size_t nb = k / Q6K_WEIGHTS;
+    for (size_t r = 0; r < n_rows; r++)
+        for (size_t b = 0; b < nb; b++)
+            sgo_q6_k_dequant_block(w + r * row_stride + b * Q6K_BLOCK_BYTES,
+                                   out + r * k + b * Q6K_WEIGHTS);
+}
+
+/* random_q6k_rows (crates/sg-gpu/tests/parity_logits.rs:31-51): every byte
+ * of a row's blocks = next_u64() & 0xFF; then per block the 16 sub-scales
+ * become (s & 0x0F) - 8 and d = f16(f32() * 1e-3).  Padding stays 0. */
+uint64_t sgo_random_q6_k_rows(uint64_t state, uint8_t *out, size_t n_rows, size_t k,
+                              size_t row_stride) {
+    const size_t nb = k / Q6K_WEIGHTS, row_bytes = nb * Q6K_BLOCK_BYTES;
+    memset(out, 0, n_rows * row_stride);
+    for (size_t r = 0; r < n_rows; r++) {
+        uint8_t *row = out + r * row_stride;
+        for (size_t i = 0; i < row_bytes; i++) row[i] = (uint8_t)(sgo_rng_next(&state) & 0xff);
+        for (size_t b = 0; b < nb; b++) {
+            uint8_t *blk = row + b * Q6K_BLOCK_BYTES;
+            for (int s = 192; s < 208; s++) blk[s] = (uint8_t)(int8_t)((int)(blk[s] & 0x0F) - 8);
+            const uint16_t d = sgo_f32_to_f16(sgo_rng_f32(&state) * 1e-3f);
+            blk[208] = (uint8_t)(d & 0xff);
+            blk[209] = (uint8_t)(d >> 8);
+        }
+    }
+    return state;
+}
+
+/* gemv_q6_k_logits reference (crates/sg-gpu/tests/parity_logits.rs:84-98):
+ * f64 dot of each dequantized row with x, then softcap*tanh(dot/softcap)
+ * (softcap <= 0: the raw dot). */
+void sgo_gemv_q6_k_logits(const uint8_t *w, size_t row_stride, const float *x, size_t n,
+                          size_t k, double softcap, float *y) {
+    const size_t nb = k / Q6K_WEIGHTS;
+    float deq[Q6K_WEIGHTS];
+    for (size_t r = 0; r < n; r++) {
+        double dot = 0.0;
+        for (size_t b = 0; b < nb; b++) {
+            sgo_q6_k_dequant_block(w + r * row_stride + b * Q6K_BLOCK_BYTES, deq);
+            for (int j = 0; j < Q6K_WEIGHTS; j++) dot += (double)deq[j] * (double)x[b * Q6K_WEIGHTS + j];
+        }
+        y[r] = (float)(softcap > 0.0 ? softcap * tanh(dot / softcap) : dot);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* GEMV oracle: f64 dot over dequantized rows                               */
 /* (crates/sg-gpu/tests/parity_gemv.rs:37-55 reference_rows)                */
 /* ------------------------------------------------------------------------ */

@@ -74,6 +74,7 @@ using namespace sgq;
 
 enum class Kind {
     Gemv,          // gemv_q4_0_k{K} / gemv_q4_0_generic
+    GemvQ6kLogits, // gemv_q6_k_logits: K 5376, rows padded to 4416 B, softcap 30
     QuantQ8,       // kv_quant_q8
     DequantQ8,     // kv_dequant_q8
     AppendQ8,      // kv_append_global_q8 (linear) / kv_append_sliding_q8 (ring)
@@ -112,7 +113,7 @@ const char *const kNames[] = {
     "rmsnorm_256",  "rmsnorm_256_plus1",  "rmsnorm_128", "rmsnorm_128_plus1",
     "rope_sliding_q", "rope_sliding_k", "rope_global_q", "rope_global_k",
     "rope_hd128_sliding_q", "rope_hd128_sliding_k", "rope_hd128_global_q", "rope_hd128_global_k",
-    "geglu", "add_scaled",
+    "geglu", "add_scaled", "gemv_q6_k_logits",
 };
 
 // RoPE variants: (name, head_dim, rot_dims, n_heads).  The first four are
@@ -158,6 +159,13 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         }
         if (!parse_u32_after(name, "_k", &k->k)) return false;
         return name == "gemv_q4_0_k" + std::to_string(k->k) && k->k % 64 == 0 && k->k > 0;
+    }
+    if (name == "gemv_q6_k_logits") {  // crates/sg-gpu/build.rs:322-327
+        k->kind = Kind::GemvQ6kLogits;
+        k->info.bindings = 3;
+        k->k = 5376;        // BLOCKS_PER_ROW 21
+        k->param = 4416;    // ROW_WORDS 1104 × 4 bytes
+        return true;
     }
     if (name == "kv_quant_q8") {
         k->kind = Kind::QuantQ8;
@@ -399,6 +407,21 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             return launch_gemv_q4_0(st, p0, static_cast<const float *>(p1), static_cast<float *>(p2),
                                     n, k, ctx->workspace);
         }
+        case Kind::GemvQ6kLogits: {
+            // bindings: 0 padded Q6_K rows, 1 x (fp32 here; f16 in the
+            // reference), 2 logits; groups [N, 1, 1] (one per vocabulary row)
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            const uint32_t n = groups[0];
+            if (r0 && r0 < (uint64_t)n * kernel->param)
+                return fail(SGQ_ERR_VALIDATION, "%s: weights binding too small", kernel->name.c_str());
+            if (r1 && r1 < (uint64_t)kernel->k * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: x binding too small", kernel->name.c_str());
+            if (r2 && r2 < (uint64_t)n * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: logits binding too small", kernel->name.c_str());
+            return launch_gemv_q6_k(st, p0, kernel->param, static_cast<const float *>(p1),
+                                    static_cast<float *>(p2), n, kernel->k, 30.0f);
+        }
         case Kind::RmsNorm: {
             // bindings: 0 x, 1 w, 2 y; one workgroup per row (groups[0] rows)
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
@@ -586,6 +609,12 @@ int sgq_gemv_q4_0(sgq_ctx *ctx, const void *w, const float *x, float *y, uint32_
                   uint32_t k) {
     if (!ctx || !w || !x || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     return launch_gemv_q4_0(ctx->stream, w, x, y, n, k, ctx->workspace);
+}
+
+int sgq_gemv_q6_k(sgq_ctx *ctx, const void *w, size_t row_stride, const float *x, float *y,
+                  uint32_t n, uint32_t k, float softcap) {
+    if (!ctx || !w || !x || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_gemv_q6_k(ctx->stream, w, row_stride, x, y, n, k, softcap);
 }
 
 int sgq_x_limbs(sgq_ctx *ctx, const float *x, void *x_limbs, uint32_t k) {

@@ -71,6 +71,9 @@ int gemv_slices(uint32_t k);
 // Sets the streamed kernels' launch attributes (call before graph capture).
 int gemv_prepare();
 int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k);
+// Q6_K logits GEMV (gemv_q6_k.hip): rows at a 16-byte-multiple stride.
+int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const float *x, float *y,
+                     uint32_t n, uint32_t k, float softcap);
 // Fused forms of the streamed GEMV (single K-slice for the prologues).
 // Prologue (what the GEMV's x limbs are computed from, inside the launch):
 //   kProTable  the limb table xl (written by an earlier kernel);

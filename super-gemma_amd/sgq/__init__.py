@@ -119,6 +119,7 @@ SIGNATURES = {
     "sgq_timer_start": (I, [P]),
     "sgq_timer_stop": (I, [P, C.POINTER(C.c_float)]),
     "sgq_gemv_q4_0": (I, [P, P, P, P, U32, U32]),
+    "sgq_gemv_q6_k": (I, [P, P, C.c_size_t, P, P, U32, U32, C.c_float]),
     "sgq_x_limbs": (I, [P, P, P, U32]),
     "sgq_gemv_q4_0_limbs": (I, [P, U32, C.POINTER(P), C.POINTER(P), C.POINTER(U32), P, U32,
                                 C.c_float]),
@@ -299,6 +300,15 @@ class GpuContext:
         _need(x, torch.float32, k, "x")
         _need(y, torch.float32, n, "y")
         _check(lib().sgq_gemv_q4_0(self._h, _ptr(w), _ptr(x), _ptr(y), n, k))
+
+    def gemv_q6_k(self, w: torch.Tensor, row_stride: int, x: torch.Tensor, y: torch.Tensor,
+                  n: int, k: int, softcap: float = 30.0):
+        """Q6_K logits GEMV (gemv_q6_k_logits.wgsl): y = softcap·tanh(E·x/softcap)."""
+        _need(w, torch.uint8, n * row_stride, "w")
+        _need(x, torch.float32, k, "x")
+        _need(y, torch.float32, n, "y")
+        _check(lib().sgq_gemv_q6_k(self._h, _ptr(w), row_stride, _ptr(x), _ptr(y), n, k,
+                                   float(softcap)))
 
     X_LIMBS_BYTES_PER_BLOCK = 80
 

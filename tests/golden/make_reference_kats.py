@@ -84,6 +84,28 @@ kats = {
     # a[i][k] = (i+k)%7-3 and b[k][j] = (k*j)%11-5 (inputs; the expected C is
     # their integer product, which the test computes the same way).
     "coop_i8_tile": {"src": "crates/sg-gpu/tests/coop_i8_smoke.rs", "m": 16, "n": 16, "k": 16},
+    # crates/sg-gguf/src/q6_k.rs:92-124 dequantize_known_block: a block with
+    # ql = 0, qh = 0, scales = 1, d = 0.5 dequantizes to -16 everywhere; then
+    # edits of single bytes set weights 0 and 96 (weight 64 is unchanged).
+    "q6_k_known_block": {
+        "src": "crates/sg-gguf/src/q6_k.rs:92-124",
+        "d": 0.5, "scales": [1] * 16,
+        "all_zero_expect": -16.0,
+        "steps": [
+            {"set": {"ql": [[0, 0x0F]], "qh": [[0, 0x03]], "scales": [[0, 2]]},
+             "expect": [[0, 31.0], [64, -16.0]]},
+            {"set": {"ql": [[32, 0xA0]], "qh_or": [[0, 0xC0]], "scales": [[6, -3]]},
+             "expect": [[96, -39.0]]},
+        ],
+    },
+    # crates/sg-gguf/src/q6_k.rs:126-138 negative_scales_and_signed_range
+    "q6_k_negative_scales": {"src": "crates/sg-gguf/src/q6_k.rs:126-138", "d": 1.0,
+                             "ql": 0xFF, "qh": 0xFF, "scale": -128, "expect_all": -3968.0},
+    # crates/sg-gguf/src/q6_k.rs:25-38, 86-90: 210-byte blocks of 256 weights;
+    # crates/sg-gpu/build.rs:322-327 rows padded 4410 -> 4416 bytes (ROW_WORDS 1104)
+    "q6_k_block_bytes": {"src": "crates/sg-gguf/src/q6_k.rs:25-38,86-90; crates/sg-gpu/build.rs:322-327",
+                         "block_bytes": 210, "block_weights": 256, "row_bytes_k5376": 4410,
+                         "row_stride_k5376": 4416},
 }
 
 if __name__ == "__main__":

@@ -306,3 +306,90 @@ def test_add_scaled(oracle):
     a = np.array([1.0, 2.0], np.float32)
     b = np.array([3.0, -1.0], np.float32)
     assert list(oracle.add_scaled(a, b, 0.5)) == [2.0, 0.5]
+
+
+# --- Q6_K dequant (q6_k.rs:41-62) ---------------------------------------------
+def _q6_block(d, scales, ql=0, qh=0):
+    blk = np.zeros(210, np.uint8)
+    blk[:128] = ql
+    blk[128:192] = qh
+    blk[192:208] = np.array(scales, np.int8).view(np.uint8)
+    blk[208:210] = np.array([d], np.float16).view(np.uint8)
+    return blk
+
+
+def test_q6_k_known_block(oracle):
+    """q6_k.rs:92-124: all-zero quants give -16; single-byte edits move
+    weights 0 and 96 and leave weight 64."""
+    k = KATS["q6_k_known_block"]
+    blk = _q6_block(k["d"], k["scales"])
+    assert (oracle.q6_k_dequant(blk, 1, 256)[0] == k["all_zero_expect"]).all()
+    for step in k["steps"]:
+        for i, v in step["set"].get("ql", []):
+            blk[i] = v
+        for i, v in step["set"].get("qh", []):
+            blk[128 + i] = v
+        for i, v in step["set"].get("qh_or", []):
+            blk[128 + i] |= v
+        for i, v in step["set"].get("scales", []):
+            blk[192 + i] = np.array([v], np.int8).view(np.uint8)[0]
+        out = oracle.q6_k_dequant(blk, 1, 256)[0]
+        for i, v in step["expect"]:
+            assert out[i] == v, (i, out[i], v)
+
+
+def test_q6_k_negative_scales(oracle):
+    """q6_k.rs:126-138: q = 63 everywhere, scale -128, d = 1 -> -3968."""
+    k = KATS["q6_k_negative_scales"]
+    blk = _q6_block(k["d"], [k["scale"]] * 16, ql=k["ql"], qh=k["qh"])
+    assert (oracle.q6_k_dequant(blk, 1, 256)[0] == k["expect_all"]).all()
+    assert KATS["q6_k_block_bytes"]["block_bytes"] == 210
+
+
+def _q6_encode(q, scales, d):
+    """Inverse of the Q6_K layout, written from the other side: weight w of
+    the block sits in half h = w // 128, group g = (w % 128) // 32, lane
+    l = w % 32; its low nibble in ql[64h + l + 32(g & 1)] (high nibble when
+    g >= 2), its top two bits in qh[32h + l] at bit 2g; its scale is
+    scales[8h + l // 16 + 2g]."""
+    blk = np.zeros(210, np.uint8)
+    for w in range(256):
+        h, g, l = w // 128, (w % 128) // 32, w % 32
+        lo, hi = q[w] & 15, q[w] >> 4
+        qi = 64 * h + l + 32 * (g & 1)
+        blk[qi] |= lo << (4 if g >= 2 else 0)
+        blk[128 + 32 * h + l] |= hi << (2 * g)
+    blk[192:208] = np.array(scales, np.int8).view(np.uint8)
+    blk[208:210] = np.array([d], np.float16).view(np.uint8)
+    return blk
+
+
+def test_q6_k_layout_round_trip(oracle):
+    """Random 6-bit quants and sub-scales placed by the inverse layout come
+    back as d*scale*(q-32) with the sub-block of 16 weights each scale covers
+    (exact: small integers times an f16)."""
+    rs = np.random.default_rng(7)
+    for _ in range(20):
+        q = rs.integers(0, 64, 256)
+        sc = rs.integers(-128, 128, 16)
+        d = np.float16(rs.uniform(-2, 2))
+        out = oracle.q6_k_dequant(_q6_encode(q, sc, d), 1, 256)[0]
+        w = np.arange(256)
+        h, g, l = w // 128, (w % 128) // 32, w % 32
+        scale = sc[8 * h + l // 16 + 2 * g]
+        want = (np.float32(d) * scale.astype(np.float32)) * (q - 32).astype(np.float32)
+        assert np.array_equal(out, want.astype(np.float32))
+
+
+def test_q6_k_logits_oracle_matches_numpy(oracle):
+    """gemv_q6_k_logits oracle: f64 dot over the dequantized rows and the
+    30*tanh(v/30) softcap, against numpy on the same rows."""
+    rng = oracle.Rng(0xC6)
+    n, k, stride = 12, 5376, 4416
+    w = rng.random_q6_k_rows(n, k, stride)
+    x = oracle.through_f16(rng.f32_vec(k))
+    got = oracle.gemv_q6_k_logits(w, stride, x, n, k, 30.0)
+    deq = oracle.q6_k_dequant(w, n, k, stride).astype(np.float64)
+    want = 30.0 * np.tanh((deq @ x.astype(np.float64)) / 30.0)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+    assert (w.reshape(n, stride)[:, 4410:] == 0).all()
