@@ -51,17 +51,15 @@ __global__ __launch_bounds__(W * kWave) void attn_decode_merge_kernel(
 }
 
 // Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
-// out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s, both sums in
-// split order 0..S-1.  One workgroup per kv head, thread (h, d); the
-// kernel boundary after the split kernel makes the partials visible.
-// Optionally writes the x limbs of the output rows for the next GEMV.
-template <int QPK>
-__global__ __launch_bounds__(QPK * kHD) void attn_merge_kernel(const float *__restrict__ part,
-                                                               int n_splits,
-                                                               float *__restrict__ out,
-                                                               BlockLimbs *__restrict__ limbs_out) {
-    __shared__ __align__(16) float o_s[QPK * kHD];
-    attn_merge<QPK, false>(part, n_splits, blockIdx.x, out, limbs_out, o_s);
+// out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s.  One
+// 256-thread workgroup per query head (attn_merge_head); the kernel
+// boundary after the split kernel makes the partials visible.  Optionally
+// writes the x limbs of the output rows for the next GEMV.
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
+                                                         int n_splits, float *__restrict__ out,
+                                                         BlockLimbs *__restrict__ limbs_out) {
+    __shared__ float merge_s[kMergeSmem];
+    attn_merge_head<false>(part, n_splits, blockIdx.x, out, limbs_out, merge_s);
 }
 
 }  // namespace
@@ -73,7 +71,7 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
                           size_t workspace_bytes, void *limbs_out) {
     SGQ_CHECK(head_dim == kHD, "attn_decode_q8: head_dim %d unsupported (128)", head_dim);
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_decode_q8: n_q %% n_kv != 0");
-    SGQ_CHECK(n_splits >= 1 && n_splits <= 1024, "attn_decode_q8: n_splits %d out of range", n_splits);
+    SGQ_CHECK(n_splits >= 1 && n_splits <= kMergeMaxSplits, "attn_decode_q8: n_splits %d out of range", n_splits);
     SGQ_CHECK(step != nullptr || kv_len > 0, "attn_decode_q8: kv_len must be > 0");
     SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0 && ((uintptr_t)ks & 7) == 0 &&
                   ((uintptr_t)vs & 7) == 0,
@@ -98,12 +96,8 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     else SGQ_ATTN(2, kAttnWaves);
     SGQ_HIP(hipGetLastError());
     if (n_splits > 1) {
-        if (qpk == 1)
-            hipLaunchKernelGGL(attn_merge_kernel<1>, dim3(n_kv), dim3(kHD), 0, st, part, n_splits,
-                               out, lo);
-        else
-            hipLaunchKernelGGL(attn_merge_kernel<2>, dim3(n_kv), dim3(2 * kHD), 0, st, part,
-                               n_splits, out, lo);
+        hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q), dim3(256), 0, st, part, n_splits, out,
+                           lo);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());
@@ -123,7 +117,7 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
     SGQ_CHECK(!merge_in_launch || (limbs_out != nullptr && out == nullptr && n_kv <= kAttnMaxKv),
               "attn (fused): the in-launch merge writes limbs only");
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn (fused): n_q %% n_kv != 0");
-    SGQ_CHECK(n_splits >= 1 && n_splits <= 1024, "attn (fused): n_splits %d", n_splits);
+    SGQ_CHECK(n_splits >= 1 && n_splits <= kMergeMaxSplits, "attn (fused): n_splits %d", n_splits);
     SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 && ((uintptr_t)ks & 7) == 0 &&
                   ((uintptr_t)vs & 7) == 0,
               "attn (fused): misaligned cache");
@@ -159,12 +153,8 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
     else SGQ_ATTN(2, kAttnWaves);
     SGQ_HIP(hipGetLastError());
     if (n_splits > 1) {
-        if (qpk == 1)
-            hipLaunchKernelGGL(attn_merge_kernel<1>, dim3(n_kv), dim3(kHD), 0, st, part, n_splits,
-                               out, lo);
-        else
-            hipLaunchKernelGGL(attn_merge_kernel<2>, dim3(n_kv), dim3(2 * kHD), 0, st, part,
-                               n_splits, out, lo);
+        hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q), dim3(256), 0, st, part, n_splits, out,
+                           lo);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());
