@@ -375,9 +375,11 @@ def measured_traffic():
 def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
     """The dominant kernel, gemv_q4_0_ring_kernel, alone at K x N: x limbs
     made once, then `steps` single-matrix launches rotating over w_ptrs (so
-    each launch streams its weights from HBM), HIP events on the context's
-    stream around them.  Algorithmic bytes per launch: W (18 B per 32
-    weights) + the x limb table (80 B per 32 values) + y (fp32)."""
+    each launch streams its weights from HBM), recorded once as a hipGraph
+    and replayed with HIP events on the context's stream around the replay
+    (back-to-back launches without host gaps).  Algorithmic bytes per
+    launch: W (18 B per 32 weights) + the x limb table (80 B per 32 values)
+    + y (fp32)."""
     import ctypes as C
     import sgq
 
@@ -398,8 +400,12 @@ def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
             assert rc == 0, sgq.lib().sgq_last_error()
     run(len(w_ptrs))
     ctx.synchronize()
+    with sgq.GraphRecorder(ctx) as rec:
+        run(steps)
+    rec.graph.submit()  # warm replay
+    ctx.synchronize()
     ctx.timer_start()
-    run(steps)
+    rec.graph.submit()
     ms = ctx.timer_stop() / steps
     nbytes = q4_bytes(n, k) + (k // 32) * 80 + n * 4
     gbs = nbytes / (ms * 1e-3) / 1e9

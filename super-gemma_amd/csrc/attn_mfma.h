@@ -45,6 +45,22 @@ typedef int v4i_a __attribute__((ext_vector_type(4)));
 typedef int v16i_a __attribute__((ext_vector_type(16)));
 
 constexpr int kAttnWaves = 4;  // waves per workgroup
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+    return fmaxf(v, __builtin_bit_cast(float, t));
+}
+// Max over each 16-lane row, in every lane of the row.
+__device__ __forceinline__ float row_max_dpp(float v) {
+    v = dpp_max<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max<0x141>(v);  // row_half_mirror
+    return dpp_max<0x140>(v);  // row_mirror
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
 constexpr float kLimbBase = 254.f;
 
 // One wave's loads for a 32-slot group: lane (t, kh) takes bytes
@@ -258,12 +274,11 @@ __device__ __forceinline__ void attn_chunk(const float *__restrict__ q,
         const bool valid = tb + (uint32_t)c < t_end && hq < QPK;
         s = valid ? s * dh : kNegBig;
         // ---- online softmax per head (32-lane halves)
-        float mx = s;
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-        const float M0 = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 0));
-        const float M1 = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), 32));
+        // max over each 16-lane row on the VALU (DPP), then over the two
+        // rows of each head from lanes 0/16 and 32/48
+        const float mx = row_max_dpp(s);
+        const float M0 = fmaxf(readlane_f(mx, 0), readlane_f(mx, 16));
+        const float M1 = fmaxf(readlane_f(mx, 32), readlane_f(mx, 48));
         const float mn0 = fmaxf(m_run[0], M0), mn1 = fmaxf(m_run[1], M1);
         const float corr0 = __expf(m_run[0] - mn0), corr1 = __expf(m_run[1] - mn1);
         m_run[0] = mn0;

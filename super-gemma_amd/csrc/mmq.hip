@@ -222,70 +222,90 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[a][b][i] = 0.f;
 
-    // register prefetch two stages ahead: while stage s computes, stage s+1
-    // waits in registers for its LDS slot and stage s+2 is in flight; the
-    // loop is unrolled by two so both prefetch sets stay in registers
-    Prefetch pf0, pf1;
+    // register prefetch one stage ahead: stage s+1's global loads are in
+    // flight while stage s computes (four blocks of MFMAs and rescales),
+    // then go to the other LDS buffer
+    Prefetch pf;
     AlignedSrc src{};
     if (AL) src = aligned_src(xq, xs, W, k, nb, m0, n0);
-    auto load = [&](Prefetch &pf, int b0) {
+    auto load = [&](Prefetch &p, int b0) {
         if (AL)
-            load_stage_al(pf, src, b0);
+            load_stage_al(p, src, b0);
         else
-            load_stage(pf, xq, xs, W, m, n, k, nb, m0, n0, b0, b_end);
+            load_stage(p, xq, xs, W, m, n, k, nb, m0, n0, b0, b_end);
     };
     if (n_stages > 0) {
-        load(pf0, b_beg);
-        store_stage(pf0, stages[0]);
+        load(pf, b_beg);
+        store_stage(pf, stages[0]);
     }
-    if (n_stages > 1) load(pf1, b_beg + KB);
     __syncthreads();
 
-    auto step = [&](int s, Prefetch &pl, Prefetch &ps) {
-        if (s + 2 < n_stages) load(pl, b_beg + (s + 2) * KB);
-        const Stage &S = stages[s & 1];
-#pragma unroll 1  // keeps the 4 live MFMA results + 64 accumulators within 256 VGPRs
-        for (int blk = 0; blk < KB; blk++) {
-            v4i af[2], bf[2];
+    // LDS operands of one block: int8 fragments of the wave's two row and
+    // two column tiles, and the f16 scale bits of its rows and columns
+    struct Ops {
+        v4i af[2], bf[2];
+        uint32_t sa[2], sb[2];
+    };
+    auto ld_ops = [&](const Stage &S, int blk, Ops &o) {
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                af[i] = *reinterpret_cast<const v4i *>(
-                    &S.a[(wm * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
-                bf[i] = *reinterpret_cast<const v4i *>(
-                    &S.b[(wn * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
-            }
-            // scale operands: lane (r, h = 0) holds K term 0 = d of its row
-            // (A) / column (B); every other K term is zero
-            h8 as[2], bs[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const uint16_t da = h == 0 ? S.da[blk][wm * 64 + i * 32 + r] : (uint16_t)0;
-                const uint16_t dw = h == 0 ? S.dw[blk][wn * 64 + i * 32 + r] : (uint16_t)0;
-                as[i] = h8{};
-                bs[i] = h8{};
-                as[i][0] = __builtin_bit_cast(_Float16, da);
-                bs[i][0] = __builtin_bit_cast(_Float16, dw);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const v16i zero = {};
-                    const f32x16 fzero = {};
-                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
-                    const f32x16 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(as[i], bs[j], fzero, 0, 0, 0);
-#pragma unroll
-                    for (int q = 0; q < 16; q++)
-                        acc[i][j][q] = __builtin_fmaf((float)d[q], sc[q], acc[i][j][q]);
-                }
+        for (int i = 0; i < 2; i++) {
+            o.af[i] = *reinterpret_cast<const v4i *>(
+                &S.a[(wm * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
+            o.bf[i] = *reinterpret_cast<const v4i *>(
+                &S.b[(wn * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
+            o.sa[i] = S.da[blk][wm * 64 + i * 32 + r];
+            o.sb[i] = S.dw[blk][wn * 64 + i * 32 + r];
         }
-        if (s + 1 < n_stages) store_stage(ps, stages[(s + 1) & 1]);
+    };
+    // One block on the wave's 2×2 tiles.  Tile t's MFMAs are issued before
+    // tile t-1's rescale, so the matrix cores work while the VALU converts.
+    auto block = [&](const Ops &o) {
+        // scale operands: lane (r, h = 0) holds K term 0 = d of its row
+        // (A) / column (B); every other K term is zero
+        h8 as[2], bs[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            as[i] = __builtin_bit_cast(h8, v4i{h == 0 ? (int)o.sa[i] : 0, 0, 0, 0});
+            bs[i] = __builtin_bit_cast(h8, v4i{h == 0 ? (int)o.sb[i] : 0, 0, 0, 0});
+        }
+        v16i d[2];
+        f32x16 sc[2];
+        const v16i zero = {};
+        const f32x16 fzero = {};
+#pragma unroll
+        for (int t = 0; t <= 4; t++) {
+            if (t < 4) {
+                const int i = t >> 1, j = t & 1;
+                d[t & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.af[i], o.bf[j], zero, 0, 0, 0);
+                sc[t & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as[i], bs[j], fzero, 0, 0, 0);
+            }
+            if (t > 0) {
+                const int u = t - 1, i = u >> 1, j = u & 1;
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    acc[i][j][q] = __builtin_fmaf((float)d[u & 1][q], sc[u & 1][q], acc[i][j][q]);
+            }
+        }
+    };
+    auto step = [&](int s) {
+        if (s + 1 < n_stages) load(pf, b_beg + (s + 1) * KB);
+        const Stage &S = stages[s & 1];
+        // the next block's LDS operands load while this block computes
+        // (two blocks per iteration, so both operand sets keep fixed registers)
+        Ops cur;
+        ld_ops(S, 0, cur);
+#pragma unroll 1
+        for (int blk = 0; blk < KB; blk++) {
+            Ops nxt;
+            ld_ops(S, min(blk + 1, KB - 1), nxt);
+            asm volatile("" ::: "memory");  // keeps the reads above the block's MFMAs
+            block(cur);
+            cur = nxt;
+        }
+        if (s + 1 < n_stages) store_stage(pf, stages[(s + 1) & 1]);
         __syncthreads();
     };
-    for (int s = 0; s < n_stages; s += 2) {
-        step(s, pf0, pf1);
-        if (s + 1 < n_stages) step(s + 1, pf1, pf0);
-    }
+    for (int s = 0; s < n_stages; s++) step(s);
 
     float *dst = out + (size_t)z * m * n;
 #pragma unroll
