@@ -192,7 +192,9 @@ class AttnDecode:
         self.q = torch.empty(n_q * hd, dtype=torch.float32, device="cuda")
         ctx.fill_normal(self.q, seed=52)
         self.out = torch.empty_like(self.q)
-        self.splits = min(1024, max(16, ctx_len // 512))
+        # 512 slots per split, 16..128 splits (sweep: 4K flat from 16 to 32,
+        # 32K best at 64, 128K flat from 64 to 256)
+        self.splits = min(128, max(16, ctx_len // 512))
         self.bytes = ctx_len * n_kv * (2 * hd + 2 * (hd // 32) * 2) + 2 * n_q * hd * 4
 
     def step(self, i):
