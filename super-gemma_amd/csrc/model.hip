@@ -440,6 +440,14 @@ struct LayerW {
 // Decode attention splits per kv head: 8 for a 1024-slot ring (one 32-slot
 // group per wave of the 4-wave workgroups), about 512 slots per workgroup
 // for a linear cache (measured best at 8K).
+// The split merge of the fused decode runs as its own launch (queued behind
+// the split kernel it costs little; measured 1.7% faster per step than the
+// last split of each kv head merging in the split kernel, which adds a store
+// drain and a counter to every workgroup).  1 selects the in-launch merge.
+#ifndef SGQ_MERGE_IN_LAUNCH
+#define SGQ_MERGE_IN_LAUNCH 0
+#endif
+constexpr bool kMergeInLaunch = SGQ_MERGE_IN_LAUNCH;
 static int decode_splits(const LayerW &L) {
     return L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 8;
 }
@@ -574,12 +582,13 @@ int record_step(sgq_model *m, float *logits) {
     return launch_gemv_limbs(st, head, xl, H);
 }
 
-// Fused decode step (mode 2): five launches per layer.
+// Fused decode step (mode 2): six launches per layer.
 //   QKV GEMV       prologue: the previous layer's post-FFN residual update and
 //                  this layer's input RMSNorm, from the down GEMV's partial
 //                  sums (layer 0: the embedding row); writes x (xa)
-//   attention      fused q/k/v post-projection and K/V append; the last
-//                  split of each kv head merges and writes the O limbs
+//   attention      fused q/k/v post-projection and K/V append
+//   merge          the splits in split order -> the O GEMV's limbs (or, with
+//                  SGQ_MERGE_IN_LAUNCH, by the last split inside attention)
 //   O GEMV         epilogue: u/A/B rows and partial sums for the post-
 //                  attention residual and the FFN norm
 //   gate/up GEMV   prologue: the post-attention residual (writes xb) and the
@@ -632,7 +641,7 @@ int record_step_fused(sgq_model *m, float *logits) {
                  m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
                  L.global ? 0u : L.slots, L.kq, L.ks, L.vq, L.vs, (int)c.n_q_heads,
                  (int)c.n_kv_heads, n_splits, c.attn_scale, nullptr, ctx_workspace(m->ctx),
-                 kWorkspaceBytes, m->fx.xl_o, true)))
+                 kWorkspaceBytes, m->fx.xl_o, kMergeInLaunch)))
             return rc;
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;

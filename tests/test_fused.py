@@ -1,6 +1,6 @@
-"""Fused decode (sgq_model_set_decode_mode(model, 2)): five launches per
-layer, with the norms, residual updates, GeGLU and the attention merge moved
-into the GEMV prologues/epilogues and the attention launch.  Checked against
+"""Fused decode (sgq_model_set_decode_mode(model, 2)): six launches per
+layer, with the norms, residual updates and GeGLU moved into the GEMV
+prologues/epilogues and the q/k/v post-projection into the attention launch.  Checked against
 the oracle decoder (crates/sg-model/src/reference.rs:157-316 restated in
 oracle/model.py) on the same weights, at the tolerance of the
 kernel-per-operator path, plus graph replays, determinism and mode switches
