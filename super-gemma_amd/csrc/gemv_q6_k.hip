@@ -9,9 +9,9 @@
 //
 // Design (HBM-bound: 4416 B per row at k = 5376, 1.16 GB for the 262144-row
 // vocabulary):
-//  * One wave per row at a time.  A row is staged through registers into
-//    the wave's LDS slot (16-byte chunks, coalesced); the wave's next two
-//    rows are in flight while one is computed.
+//  * One wave per two rows at a time.  Rows are staged through registers
+//    into the wave's two LDS slots (16-byte chunks, coalesced); the wave's
+//    next two rows are in flight while two are computed.
 //  * Lane task (super-block sb, half h, lane-half j) covers 64 weights: the
 //    four 16-weight sub-blocks g = 0..3 that share ql bytes
 //    [64h + 16j, +16) / [64h + 32 + 16j, +16) and qh bytes [32h + 16j, +16).
@@ -108,13 +108,18 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
     _Float16 *xh = reinterpret_cast<_Float16 *>(q6_smem);  // k halves
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    // slots padded by 16 B: the scale reads of a row's last block may run 2 B past it
-    uint8_t *row = q6_smem + ((k * 2 + 15) & ~15) + wave * (stride + 16);
+    // two row slots per wave, each padded by 16 B: the scale reads of a
+    // row's last block may run 2 B past it
+    uint8_t *row0 = q6_smem + ((k * 2 + 15) & ~15) + wave * 2 * (stride + 16);
+    uint8_t *row1 = row0 + (stride + 16);
     const int nb = k / 256, ntask = 4 * nb, nchunks = (int)(stride / 16);
     const int G = gridDim.x * kQ6Waves;
     int r = blockIdx.x * kQ6Waves + wave;
 
-    // two rows in flight per wave: the row being computed came in two rounds ago
+    // a wave computes rows r and r + G together (2·4·nb tasks over its 64
+    // lanes: 168 at k = 5376, so lanes stay busy where one row's 84 tasks
+    // would leave 44 of them idle in the second round), while rows r + 2G
+    // and r + 3G load into the registers just emptied
     i32x4_t pa[kQ6Chunks], pb[kQ6Chunks];
     auto load = [&](i32x4_t (&pre)[kQ6Chunks], int rr) {
         if (rr >= n) return;
@@ -125,32 +130,44 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
             if (idx < nchunks) pre[c] = __builtin_nontemporal_load(src + idx);
         }
     };
-    load(pa, r);
-    load(pb, r + G);
-    for (int i = threadIdx.x; i < k; i += kQ6WG) xh[i] = (_Float16)x[i];
-    __syncthreads();
-
-    auto round = [&](i32x4_t (&pre)[kQ6Chunks], int rr) {
+    auto put = [&](const i32x4_t (&pre)[kQ6Chunks], uint8_t *row) {
 #pragma unroll
         for (int c = 0; c < kQ6Chunks; c++) {
             const int idx = lane + kWave * c;
             if (idx < nchunks) *reinterpret_cast<i32x4_t *>(row + 16 * idx) = pre[c];
         }
+    };
+    load(pa, r);
+    load(pb, r + G);
+    for (int i = threadIdx.x; i < k; i += kQ6WG) xh[i] = (_Float16)x[i];
+    __syncthreads();
+
+    for (; r < n; r += 2 * G) {
+        const int r1 = r + G;
+        const bool has1 = r1 < n;
+        put(pa, row0);
+        if (has1) put(pb, row1);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        load(pre, rr + 2 * G);  // lands two rounds from now
-        float acc = 0.f;
-        for (int t = lane; t < ntask; t += kWave)
-            acc += q6_task(row, xh, t >> 2, (t >> 1) & 1, t & 1);
-        acc = wave_sum_dpp(acc);
-        if (lane == 0) y[rr] = softcap > 0.f ? softcap * tanhf(acc / softcap) : acc;
-        __builtin_amdgcn_wave_barrier();  // this row's LDS reads before the next row's stores
-    };
-    for (; r < n; r += 2 * G) {
-        round(pa, r);
-        if (r + G >= n) break;
-        round(pb, r + G);
+        load(pa, r + 2 * G);  // land while these two rows compute
+        load(pb, r1 + 2 * G);
+        float acc0 = 0.f, acc1 = 0.f;
+        const int nt = has1 ? 2 * ntask : ntask;
+        for (int t = lane; t < nt; t += kWave) {
+            const bool second = t >= ntask;
+            const int u = second ? t - ntask : t;
+            const float v = q6_task(second ? row1 : row0, xh, u >> 2, (u >> 1) & 1, u & 1);
+            if (second) acc1 += v;
+            else acc0 += v;
+        }
+        acc0 = wave_sum_dpp(acc0);
+        acc1 = wave_sum_dpp(acc1);
+        if (lane == 0) {
+            y[r] = softcap > 0.f ? softcap * tanhf(acc0 / softcap) : acc0;
+            if (has1) y[r1] = softcap > 0.f ? softcap * tanhf(acc1 / softcap) : acc1;
+        }
+        __builtin_amdgcn_wave_barrier();  // these rows' LDS reads before the next rows' stores
     }
 }
 
@@ -166,8 +183,8 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const flo
               row_stride);
     SGQ_CHECK(((uintptr_t)w & 15) == 0, "gemv_q6_k: weights must be 16-byte aligned");
     SGQ_CHECK(n > 0, "gemv_q6_k: empty");
-    const size_t lds = ((size_t)k * 2 + 15) / 16 * 16 + (size_t)kQ6Waves * (row_stride + 16);
-    const int rows_per_wg = kQ6Waves;
+    const size_t lds = ((size_t)k * 2 + 15) / 16 * 16 + (size_t)kQ6Waves * 2 * (row_stride + 16);
+    const int rows_per_wg = 2 * kQ6Waves;
     // three workgroups (12 waves) per CU: the per-row work is a chain of LDS
     // reads and dependent VALU, so more waves hide more of it
     int grid = device_info().cus * 3;

@@ -437,9 +437,6 @@ struct LayerW {
     uint32_t slots;
 };
 
-// Decode attention splits per kv head: 8 for a 1024-slot ring (one 32-slot
-// group per wave of the 4-wave workgroups), about 512 slots per workgroup
-// for a linear cache (measured best at 8K).
 // The split merge of the fused decode runs as its own launch (queued behind
 // the split kernel it costs little; measured 1.7% faster per step than the
 // last split of each kv head merging in the split kernel, which adds a store
@@ -448,8 +445,20 @@ struct LayerW {
 #define SGQ_MERGE_IN_LAUNCH 0
 #endif
 constexpr bool kMergeInLaunch = SGQ_MERGE_IN_LAUNCH;
+
+// Decode attention splits per kv head: 16 for a 1024-slot ring (64 slots
+// per split; with the merge as its own launch, 16 and 32 measured equal and
+// 0.6% faster per step than 8, 4 was 2.3% slower), about 512 slots per
+// workgroup for a linear cache (measured best at 8K against 256 and 1024).
+#ifndef SGQ_SLIDING_SPLITS
+#define SGQ_SLIDING_SPLITS 16
+#endif
+#ifndef SGQ_GLOBAL_SLOTS_PER_SPLIT
+#define SGQ_GLOBAL_SLOTS_PER_SPLIT 512
+#endif
 static int decode_splits(const LayerW &L) {
-    return L.global ? (int)std::min(64u, std::max(8u, L.slots / 512)) : 8;
+    return L.global ? (int)std::min(64u, std::max(8u, L.slots / SGQ_GLOBAL_SLOTS_PER_SPLIT))
+                    : SGQ_SLIDING_SPLITS;
 }
 
 struct sgq_model {

@@ -126,7 +126,7 @@ def test_fused_full_width_matches_oracle(ctx, oracle):
 def test_fused_long_context_matches_oracle(ctx, oracle):
     """A full, wrapping 1024-slot ring and ~1030-position global layers
     (synthetic pages read back into the oracle's cache); 16 splits per
-    sliding kv head meet in the in-launch merge."""
+    sliding kv head meet in the merge."""
     import sgq
     from oracle.model import OracleDecoder
 
