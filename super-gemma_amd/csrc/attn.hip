@@ -62,6 +62,29 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     attn_merge_head<false>(part, n_splits, blockIdx.x, out, limbs_out, merge_s);
 }
 
+// The same merge for up to 16 splits: one workgroup per kv head, thread
+// (head, dim) loads all splits' (m, l, acc[dim]) in one batch and folds
+// them in split order (attn_merge): a single round trip.
+template <int QPK>
+__global__ __launch_bounds__(QPK * kHD) void attn_merge_fold_kernel(
+    const float *__restrict__ part, int n_splits, float *__restrict__ out,
+    BlockLimbs *__restrict__ limbs_out) {
+    __shared__ __align__(16) float o_s[QPK * kHD];
+    attn_merge<QPK, false>(part, n_splits, blockIdx.x, out, limbs_out, o_s);
+}
+
+void launch_merge(hipStream_t st, int qpk, int n_q, int n_kv, int n_splits, const float *part,
+                  float *out, BlockLimbs *lo) {
+    if (n_splits > 16)
+        hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q), dim3(256), 0, st, part, n_splits, out, lo);
+    else if (qpk == 1)
+        hipLaunchKernelGGL(attn_merge_fold_kernel<1>, dim3(n_kv), dim3(kHD), 0, st, part, n_splits,
+                           out, lo);
+    else
+        hipLaunchKernelGGL(attn_merge_fold_kernel<2>, dim3(n_kv), dim3(2 * kHD), 0, st, part,
+                           n_splits, out, lo);
+}
+
 }  // namespace
 
 int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
@@ -96,8 +119,7 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     else SGQ_ATTN(2, kAttnWaves);
     SGQ_HIP(hipGetLastError());
     if (n_splits > 1) {
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q), dim3(256), 0, st, part, n_splits, out,
-                           lo);
+        launch_merge(st, qpk, n_q, n_kv, n_splits, part, out, lo);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());
@@ -153,8 +175,7 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
     else SGQ_ATTN(2, kAttnWaves);
     SGQ_HIP(hipGetLastError());
     if (n_splits > 1) {
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q), dim3(256), 0, st, part, n_splits, out,
-                           lo);
+        launch_merge(st, qpk, n_q, n_kv, n_splits, part, out, lo);
     }
 #undef SGQ_ATTN
     SGQ_HIP(hipGetLastError());
