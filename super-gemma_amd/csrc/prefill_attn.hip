@@ -43,6 +43,15 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Bytes (sel picks two of the four) of a word of int8 quants -> their exact
+// f16 values: 1024 + (q + 128) by a permute against 0x64, then -1152.
+__device__ __forceinline__ h2 i8_pair_f16(uint32_t w, uint32_t sel) {
+    const h2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w ^ 0x80808080u, sel)) + bias;
+}
+
 struct KvSource {
     const int8_t *kq, *vq;      // cache pages
     const uint16_t *ks, *vs;
@@ -108,17 +117,25 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
                 const i32x4 *kp = reinterpret_cast<const i32x4 *>(kqb + row * kHD + 32 * blk);
                 const i32x4 *vp = reinterpret_cast<const i32x4 *>(vqb + row * kHD + 32 * blk);
                 const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
-                const float sk = f16_bits_to_f32(ksb[row * (kHD / 32) + blk]);
-                const float sv = f16_bits_to_f32(vsb[row * (kHD / 32) + blk]);
+                // q·d in f16 with one rounding, as (f16)(d·q) in f32 (the
+                // product of an int8 and an f16 is exact in both): four
+                // quants at a time become the f16 pairs 1024 + (q + 128) by a
+                // byte permute against 0x64, -1152 gives q exactly, and a
+                // packed f16 multiply applies d
+                const _Float16 sk = __builtin_bit_cast(_Float16, ksb[row * (kHD / 32) + blk]);
+                const _Float16 sv = __builtin_bit_cast(_Float16, vsb[row * (kHD / 32) + blk]);
+                const h2 dk = {sk, sk}, dv = {sv, sv};
                 const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
                 const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-                for (int w = 0; w < 8; w++)
-#pragma unroll
-                    for (int b = 0; b < 4; b++) {
-                        kv[4 * w + b] = (_Float16)(sk * (float)(int8_t)((kw[w] >> (8 * b)) & 0xff));
-                        vv[4 * w + b] = (_Float16)(sv * (float)(int8_t)((vw[w] >> (8 * b)) & 0xff));
-                    }
+                for (int w = 0; w < 8; w++) {
+                    const h2 k01 = i8_pair_f16((uint32_t)kw[w], 0x04010400u) * dk;
+                    const h2 k23 = i8_pair_f16((uint32_t)kw[w], 0x04030402u) * dk;
+                    const h2 v01 = i8_pair_f16((uint32_t)vw[w], 0x04010400u) * dv;
+                    const h2 v23 = i8_pair_f16((uint32_t)vw[w], 0x04030402u) * dv;
+                    kv[4 * w] = k01[0], kv[4 * w + 1] = k01[1], kv[4 * w + 2] = k23[0], kv[4 * w + 3] = k23[1];
+                    vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+                }
             } else {
 #pragma unroll
                 for (int j = 0; j < 32; j++) kv[j] = vv[j] = (_Float16)0.f;
