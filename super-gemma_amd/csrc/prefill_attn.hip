@@ -16,9 +16,10 @@
 //
 // Design (MFMA-bound: 4·hd flops per query-key pair against 2·hd·1 B of
 // K/V per key per query tile):
-//  * Workgroup = 4 waves = 128 queries of one query head; tiles of 64 keys.
-//    K and V of a tile are dequantized once into LDS (K as [key][dim],
-//    V transposed as [dim][key], rows padded) and used by all 128 queries.
+//  * Workgroup = 4 waves per query head of one kv head (GQA: 8 waves for
+//    two) = 128 queries of each; tiles of 64 keys.  K and V of a tile are
+//    dequantized once into LDS (K as [key][dim], V transposed as [dim][key],
+//    rows padded) and used by all of the workgroup's queries.
 //  * Each wave computes Sᵀ = K·Qᵀ for its 32 queries with
 //    v_mfma_f32_32x32x16_f16 (8 per 32 keys): in that layout lane l owns
 //    query column l%32, so the online softmax needs one cross-half shuffle,
@@ -60,15 +61,19 @@ struct KvSource {
     const uint16_t *cks, *cvs;
 };
 
-__global__ __launch_bounds__(256) void attn_prefill_kernel(
+template <int QPK>
+__global__ __launch_bounds__(256 * QPK) void attn_prefill_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
     int n_q, int n_kv, int window, float scale, int qtiles) {
     __shared__ __align__(16) _Float16 k_s[kKT][kKRow];
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
 
     const int tile = qtiles - 1 - (int)blockIdx.x;  // heaviest (latest) query tile first
-    const int qh = blockIdx.y, kvh = qh / (n_q / n_kv);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the QPK query heads of kv head blockIdx.y share the workgroup (and
+    // each K/V tile): waves 4h .. 4h+3 take query head h
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
+    const int qh = kvh * QPK + (tid >> 8);
     const int l32 = lane & 31, hh = lane >> 5;
 
     // this lane's query (column l32 of the wave's 32) and its Qᵀ operand:
@@ -102,7 +107,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 
     for (int kb = k_lo; kb <= k_hi; kb += kKT) {
         __syncthreads();  // the previous tile's LDS reads are done
-        {   // dequantize K and V of keys kb..kb+63: thread -> (key t/4, 32-block t%4)
+        if (tid < 256) {   // dequantize K and V of keys kb..kb+63: thread -> (key t/4, 32-block t%4)
             const int kk = tid >> 2, blk = tid & 3;
             const int key = kb + kk;
             _Float16 kv[32], vv[32];
@@ -242,8 +247,15 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
               "attn_prefill_q8: misaligned operand");
     const int qtiles = (n_tok + kQT - 1) / kQT;
     const KvSource src{kq, vq, ks, vs, ring, ckq, cvq, cks, cvs};
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(qtiles, n_q), dim3(256), 0, st, q, src, out,
-                       n_tok, q0, n_q, n_kv, window, scale, qtiles);
+    const int qpk = n_q / n_kv;
+    if (qpk == 2)
+        hipLaunchKernelGGL(attn_prefill_kernel<2>, dim3(qtiles, n_kv), dim3(512), 0, st, q, src,
+                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
+    else if (qpk == 1)
+        hipLaunchKernelGGL(attn_prefill_kernel<1>, dim3(qtiles, n_kv), dim3(256), 0, st, q, src,
+                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
+    else
+        return fail(SGQ_ERR_VALIDATION, "attn_prefill_q8: %d q heads per kv head unsupported", qpk);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }
