@@ -32,6 +32,10 @@
 namespace sgq {
 namespace {
 
+#ifndef SGQ_PREFILL_PAIR_HEADS
+#define SGQ_PREFILL_PAIR_HEADS 1
+#endif
+constexpr bool kPrefillPairHeads = SGQ_PREFILL_PAIR_HEADS;  // two query heads per workgroup
 constexpr int kHD = 128;
 constexpr int kQT = 128;           // queries per workgroup (4 waves × 32)
 constexpr int kKT = 64;            // keys per tile
@@ -61,19 +65,18 @@ struct KvSource {
     const uint16_t *cks, *cvs;
 };
 
-template <int QPK>
-__global__ __launch_bounds__(256 * QPK) void attn_prefill_kernel(
+template <int HPW>
+__global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
     int n_q, int n_kv, int window, float scale, int qtiles) {
     __shared__ __align__(16) _Float16 k_s[kKT][kKRow];
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
 
     const int tile = qtiles - 1 - (int)blockIdx.x;  // heaviest (latest) query tile first
-    // the QPK query heads of kv head blockIdx.y share the workgroup (and
-    // each K/V tile): waves 4h .. 4h+3 take query head h
-    const int kvh = blockIdx.y;
+    // HPW query heads (of one kv head) share the workgroup and each K/V
+    // tile: waves 4h .. 4h+3 take query head HPW·blockIdx.y + h
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;
-    const int qh = kvh * QPK + (tid >> 8);
+    const int qh = HPW * (int)blockIdx.y + (tid >> 8), kvh = qh / (n_q / n_kv);
     const int l32 = lane & 31, hh = lane >> 5;
 
     // this lane's query (column l32 of the wave's 32) and its Qᵀ operand:
@@ -248,14 +251,12 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
     const int qtiles = (n_tok + kQT - 1) / kQT;
     const KvSource src{kq, vq, ks, vs, ring, ckq, cvq, cks, cvs};
     const int qpk = n_q / n_kv;
-    if (qpk == 2)
-        hipLaunchKernelGGL(attn_prefill_kernel<2>, dim3(qtiles, n_kv), dim3(512), 0, st, q, src,
-                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
-    else if (qpk == 1)
-        hipLaunchKernelGGL(attn_prefill_kernel<1>, dim3(qtiles, n_kv), dim3(256), 0, st, q, src,
+    if (kPrefillPairHeads && qpk % 2 == 0)
+        hipLaunchKernelGGL(attn_prefill_kernel<2>, dim3(qtiles, n_q / 2), dim3(512), 0, st, q, src,
                            out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
     else
-        return fail(SGQ_ERR_VALIDATION, "attn_prefill_q8: %d q heads per kv head unsupported", qpk);
+        hipLaunchKernelGGL(attn_prefill_kernel<1>, dim3(qtiles, n_q), dim3(256), 0, st, q, src,
+                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }
