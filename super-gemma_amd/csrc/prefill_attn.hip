@@ -38,9 +38,10 @@ namespace {
 constexpr bool kPrefillPairHeads = SGQ_PREFILL_PAIR_HEADS;  // two query heads per workgroup
 constexpr int kHD = 128;
 constexpr int kQT = 128;           // queries per workgroup (4 waves × 32)
-constexpr int kKT = 64;            // keys per tile
+constexpr int kKT = 64;            // keys per compute tile
+constexpr int kLT = 2 * kKT;       // keys per LDS tile (two compute tiles per barrier pair)
 constexpr int kKRow = kHD + 8;     // K tile row in LDS (f16), padded
-constexpr int kVRow = kKT + 8;     // Vᵀ tile row in LDS (f16), padded
+constexpr int kVRow = kLT + 8;     // Vᵀ tile row in LDS (f16), padded
 constexpr float kNegBig = -3.0e38f;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -69,7 +70,7 @@ template <int HPW>
 __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
     int n_q, int n_kv, int window, float scale, int qtiles) {
-    __shared__ __align__(16) _Float16 k_s[kKT][kKRow];
+    __shared__ __align__(16) _Float16 k_s[kLT][kKRow];
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
 
     const int tile = qtiles - 1 - (int)blockIdx.x;  // heaviest (latest) query tile first
@@ -108,11 +109,12 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const int k_lo = window > 0 ? max(0, qpos_lo + 1 - window) : 0;
     const int k_hi = qpos_hi;
 
-    for (int kb = k_lo; kb <= k_hi; kb += kKT) {
+    for (int kl = k_lo; kl <= k_hi; kl += kLT) {
         __syncthreads();  // the previous tile's LDS reads are done
-        if (tid < 256) {   // dequantize K and V of keys kb..kb+63: thread -> (key t/4, 32-block t%4)
-            const int kk = tid >> 2, blk = tid & 3;
-            const int key = kb + kk;
+        // dequantize K and V of keys kl..kl+127: thread -> (key t/4, 32-block t%4)
+        for (int t = tid; t < kLT * 4; t += 256 * HPW) {
+            const int kk = t >> 2, blk = t & 3;
+            const int key = kl + kk;
             _Float16 kv[32], vv[32];
             if (key <= k_hi) {
                 const bool fresh = src.ckq != nullptr && key >= q0;
@@ -160,6 +162,10 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         }
         __syncthreads();
 
+#pragma unroll 1
+      for (int sub = 0; sub < 2; sub++) {
+        const int kb = kl + kKT * sub, ko = kKT * sub;  // compute tile: keys kb.., LDS rows ko..
+        if (kb > k_hi) break;
         // Sᵀ = K·Qᵀ for the tile's two 32-key halves
         f32x16 s[2];
 #pragma unroll
@@ -168,7 +174,7 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
             for (int i = 0; i < 16; i++) s[t2][i] = 0.f;
 #pragma unroll
             for (int c = 0; c < 8; c++) {
-                const h8 a = *reinterpret_cast<const h8 *>(&k_s[32 * t2 + l32][16 * c + 8 * hh]);
+                const h8 a = *reinterpret_cast<const h8 *>(&k_s[ko + 32 * t2 + l32][16 * c + 8 * hh]);
                 s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], s[t2], 0, 0, 0);
             }
         }
@@ -211,12 +217,13 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
             for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
                 for (int half = 0; half < 2; half++) {
-                    const _Float16 *vr = &vt_s[32 * d + l32][32 * t2 + 16 * half + 4 * hh];
+                    const _Float16 *vr = &vt_s[32 * d + l32][ko + 32 * t2 + 16 * half + 4 * hh];
                     const h4 lo = *reinterpret_cast<const h4 *>(vr);
                     const h4 hi = *reinterpret_cast<const h4 *>(vr + 8);
                     const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t2][half], o[d], 0, 0, 0);
                 }
+      }
     }
 
     if (!q_valid) return;
