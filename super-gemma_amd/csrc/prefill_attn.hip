@@ -39,7 +39,11 @@ constexpr bool kPrefillPairHeads = SGQ_PREFILL_PAIR_HEADS;  // two query heads p
 constexpr int kHD = 128;
 constexpr int kQT = 128;           // queries per workgroup (4 waves × 32)
 constexpr int kKT = 64;            // keys per compute tile
-constexpr int kLT = 2 * kKT;       // keys per LDS tile (two compute tiles per barrier pair)
+#ifndef SGQ_PF_SUBTILES
+#define SGQ_PF_SUBTILES 4
+#endif
+constexpr int kSub = SGQ_PF_SUBTILES;  // compute tiles per LDS tile (per barrier pair)
+constexpr int kLT = kSub * kKT;       // keys per LDS tile
 constexpr int kKRow = kHD + 8;     // K tile row in LDS (f16), padded
 constexpr int kVRow = kLT + 8;     // Vᵀ tile row in LDS (f16), padded
 constexpr float kNegBig = -3.0e38f;
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         __syncthreads();
 
 #pragma unroll 1
-      for (int sub = 0; sub < 2; sub++) {
+      for (int sub = 0; sub < kSub; sub++) {
         const int kb = kl + kKT * sub, ko = kKT * sub;  // compute tile: keys kb.., LDS rows ko..
         if (kb > k_hi) break;
         // Sᵀ = K·Qᵀ for the tile's two 32-key halves
