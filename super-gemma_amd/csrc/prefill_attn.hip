@@ -17,9 +17,10 @@
 // Design (MFMA-bound: 4·hd flops per query-key pair against 2·hd·1 B of
 // K/V per key per query tile):
 //  * Workgroup = 4 waves per query head of one kv head (GQA: 8 waves for
-//    two) = 128 queries of each; tiles of 64 keys.  K and V of a tile are
-//    dequantized once into LDS (K as [key][dim], V transposed as [dim][key],
-//    rows padded) and used by all of the workgroup's queries.
+//    two) = 128 queries of each.  K and V are dequantized by all threads
+//    into LDS tiles of kLT keys (K as [key][dim], V transposed as
+//    [dim][key], rows padded), used by all of the workgroup's queries, and
+//    computed as 64-key tiles: one barrier pair per LDS tile.
 //  * Each wave computes Sᵀ = K·Qᵀ for its 32 queries with
 //    v_mfma_f32_32x32x16_f16 (8 per 32 keys): in that layout lane l owns
 //    query column l%32, so the online softmax needs one cross-half shuffle,
