@@ -67,6 +67,8 @@ int sgq_buf_alloc(sgq_ctx *ctx, uint64_t bytes, void **dev_ptr);
 int sgq_buf_free(sgq_ctx *ctx, void *dev_ptr);
 int sgq_buf_upload(sgq_ctx *ctx, void *dst_dev, const void *src_host, uint64_t bytes);
 int sgq_buf_download(sgq_ctx *ctx, void *dst_host, const void *src_dev, uint64_t bytes);
+/* Zero-fill on the context stream.  Returns SGQ_ERR_VALIDATION while a graph
+   capture (sgq_graph_begin) is open: no memset is ever recorded into a graph. */
 int sgq_buf_fill_zero(sgq_ctx *ctx, void *dev_ptr, uint64_t bytes);
 
 /* ---- kernel registry: KernelBlob (crates/sg-gpu/src/kernel.rs:18-34) and
@@ -78,6 +80,31 @@ typedef struct {
     uint32_t subgroup_size;
 } sgq_kernel_info;
 
+/* Attention and KV-append variants (the reference's record_layer dispatches,
+ * crates/sg-model/src/graph.rs:560-656, at this build's geometry: Q8_0 K and
+ * V pages, head_dim 128, 32 query / 16 kv heads, window and ring 1024):
+ *   kv_append_global_q8 / kv_append_sliding_q8
+ *       0 src fp32 [n_tok × 2048], 1 scales, 2 quants, 3 step; slot =
+ *       step[0] + t (global) or (step[0] + t) % 1024 (sliding)
+ *   attn_decode_global_q8_hd128 / attn_decode_sliding_q8_hd128
+ *       0 q, 1 k_quants, 2 k_scales, 3 v_quants, 4 v_scales, 5 part, 6 step;
+ *       push {n_splits: u32, scale: f32}; groups [16, n_splits, 1];
+ *       kv_len = step[2] / step[1]  (attn_decode_global_q8k.wgsl:18-25)
+ *   attn_reduce_d128
+ *       0 part [32 × n_splits × 130], 1 out [32 × 128]; push n_splits;
+ *       groups [32, 1, 1]  (attn_reduce.wgsl:11-14)
+ *   attn_prefill_global_flash_q8_hd128
+ *       0 q fp32, 1..4 cache K/V pages, 5 out, 6 step; push f32 scale;
+ *       groups [32, ceil(M/16), 1]; q0 = step[3]
+ *       (attn_prefill_global_flash_sp_iq.wgsl:24-35)
+ *   attn_prefill_sliding_ring_q8_hd128
+ *       0 q, 1..4 ring K/V pages, 5..8 chunk K/V pages, 9 out, 10 step;
+ *       push f32 scale; groups [16, M, 1]  (attn_prefill_sliding_ring.wgsl:28-40)
+ * M (prefill) is the out binding's range / (32·128·4).  The reference's
+ * head_dim 256/512 f16-cache variants (attn_decode_sliding, attn_decode_global,
+ * attn_decode_global_q8k, attn_reduce_d256/d512, attn_prefill_sliding[_ring],
+ * attn_prefill_global_flash_sp_iq/_sp_q8, kv_append_sliding/global) return
+ * SGQ_ERR_UNKNOWN_KERNEL with the name of the form above to use. */
 int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
                       sgq_kernel_info *info);
 /* Number of registered variant names / the i-th one (for enumeration). */

@@ -26,8 +26,8 @@ the oracle round-trips each K/V row through Q8_0 before caching it.
 RoPE: NEOX, angles in f64 via cos_sin_table (crates/sg-model/src/rope.rs:
 27-48); global layers use divisor factors [1]*live + [1e30]*rest, which is
 how partial_rotary_factor materializes (rope.rs:13-16).
-Linear layers use the f64 Q4_0 GEMV (gemv_rows); everything is fp32 between
-ops, as in the reference.
+Linear layers use CpuModel::matmul's dequant_row + 8-lane f64 dot
+(matmul_q4_0); everything is fp32 between ops, as in the reference.
 """
 from __future__ import annotations
 
@@ -50,6 +50,9 @@ class OracleDecoder:
         self.k_cache = [[] for _ in range(L)]
         self.v_cache = [[] for _ in range(L)]
         self.pos = 0
+        # taps[(name, layer)] = the row(s) of the last forward, when a dict:
+        # "k_rope" and "v_norm" (reference.rs:153-155 tap names)
+        self.taps = None
         hd = cfg["head_dim"]
         live = int(round(cfg["global_rope_frac"] * hd / 2))
         self.global_factors = np.array([1.0] * live + [1e30] * (hd // 2 - live), np.float32)
@@ -73,9 +76,15 @@ class OracleDecoder:
         ge = self.c["global_every"]
         return layer % ge == ge - 1
 
+    # host threads of the row-parallel matmul (results do not depend on it)
+    threads = 8
+
     def _lin(self, name, layer, x, n_out):
+        """CpuModel::matmul over one token (reference.rs:402-444): the same
+        dequant_row + 8-lane dot_f64 as the prefill's multi-token matmul, so a
+        token-by-token decode reproduces a multi-token forward bit for bit."""
         k = x.size
-        return O.gemv_rows(self.w[(name, layer)], x, k, np.arange(n_out))
+        return O.matmul_q4_0(self.w[(name, layer)], x, 1, n_out, k, threads=self.threads)[0]
 
     def _q8_round_trip(self, row):
         s, q = O.quant_q8_0(row)
@@ -108,6 +117,8 @@ class OracleDecoder:
             k = O.rmsnorm(k_proj, w[("attn_k_norm", l)], hd, eps)
             k = O.rope(k, hd, hd, nkv, cs)
             v = O.rmsnorm(v, None, hd, eps)
+            if self.taps is not None:
+                self.taps[("k_rope", l)], self.taps[("v_norm", l)] = k, v
             self.k_cache[l].append(self._q8_round_trip(k))
             self.v_cache[l].append(self._q8_round_trip(v))
             ck = np.concatenate(self.k_cache[l])
@@ -127,7 +138,7 @@ class OracleDecoder:
             x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
         self.pos += 1
         xf = O.rmsnorm(x, w[("output_norm", -1)], H, eps)
-        logits = O.gemv_rows(emb, xf, H, np.arange(c["vocab"]))
+        logits = O.matmul_q4_0(emb, xf, 1, c["vocab"], H, threads=self.threads)[0]
         cap = np.float64(c["final_softcap"])
         return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
 
@@ -138,15 +149,24 @@ class OraclePrefill(OracleDecoder):
     round-tripped through Q8_0 (kv_quant_q8 semantics, per row, 32-blocks),
     as the reference quantizes activations before its int8 MMQs; attention
     is causal (window on sliding layers) over the cached positions plus the
-    chunk.  Decoding after it continues with the inherited decode()."""
+    chunk.  Decoding after it continues with the inherited decode().
+
+    ``q8_activations = False`` skips those activation round trips: the
+    forward is then ReferenceModel::forward over several tokens (f32
+    activations, reference.rs:157-316), which a token-by-token decode must
+    reproduce bit for bit (crates/sg-model/tests/cpu_reference.rs:84-92)."""
+
+    q8_activations = True
 
     def _q8rt(self, x2d):
+        if not self.q8_activations:
+            return np.ascontiguousarray(x2d, np.float32)
         s, q = O.quant_q8_0(np.ascontiguousarray(x2d, np.float32).reshape(-1))
         return O.dequant_q8_0(s, q).reshape(x2d.shape)
 
     def _mm(self, name, layer, x2d, n_out):
         M, K = x2d.shape
-        return O.matmul_q4_0(self.w[(name, layer)], x2d, M, n_out, K, threads=8)
+        return O.matmul_q4_0(self.w[(name, layer)], x2d, M, n_out, K, threads=self.threads)
 
     def prefill(self, tokens) -> np.ndarray:
         c, w = self.c, self.w
@@ -172,6 +192,8 @@ class OraclePrefill(OracleDecoder):
             q = O.rope(O.rmsnorm(q, w[("attn_q_norm", l)], hd, eps), hd, hd, nq, cs)
             k = O.rope(O.rmsnorm(k_proj, w[("attn_k_norm", l)], hd, eps), hd, hd, nkv, cs)
             v = O.rmsnorm(v, None, hd, eps)
+            if self.taps is not None:
+                self.taps[("k_rope", l)], self.taps[("v_norm", l)] = k, v
             for i in range(M):
                 self.k_cache[l].append(self._q8_round_trip(k[i]))
                 self.v_cache[l].append(self._q8_round_trip(v[i]))
@@ -189,7 +211,7 @@ class OraclePrefill(OracleDecoder):
             x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
         self.pos += M
         xf = O.rmsnorm(x[-1], w[("output_norm", -1)], H, eps)
-        logits = O.gemv_rows(emb, xf, H, np.arange(c["vocab"]))
+        logits = O.matmul_q4_0(emb, xf, 1, c["vocab"], H, threads=self.threads)[0]
         cap = np.float64(c["final_softcap"])
         return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
 

@@ -85,6 +85,9 @@ enum class Kind {
     Rope,          // rope_{sliding,global}_{q,k} (+ head_dim-128 forms)
     Geglu,         // geglu
     AddScaled,     // add_scaled (push: f32 scale)
+    AttnDecode,    // attn_decode_{sliding,global}_q8_hd128: groups [n_kv, n_splits]
+    AttnReduce,    // attn_reduce_d128: groups [n_q]
+    AttnPrefill,   // attn_prefill_{global_flash,sliding_ring}_q8_hd128
 };
 
 struct sgq_kernel {
@@ -114,6 +117,36 @@ const char *const kNames[] = {
     "rope_sliding_q", "rope_sliding_k", "rope_global_q", "rope_global_k",
     "rope_hd128_sliding_q", "rope_hd128_sliding_k", "rope_hd128_global_q", "rope_hd128_global_k",
     "geglu", "add_scaled", "gemv_q6_k_logits",
+    "kv_append_sliding_q8",
+    "attn_decode_sliding_q8_hd128", "attn_decode_global_q8_hd128", "attn_reduce_d128",
+    "attn_prefill_global_flash_q8_hd128", "attn_prefill_sliding_ring_q8_hd128",
+};
+
+// The benchmark geometry of the hd128 attention forms (32 query heads over
+// 16 kv heads of 128, sliding window and ring 1024), baked into the names as
+// the reference bakes HEAD_DIM / N_KV_HEADS / Q_PER_KV / WINDOW into its
+// variants (crates/sg-gpu/build.rs:331-430).
+constexpr uint32_t kAttnNQ = 32, kAttnNKv = 16, kAttnWindow = 1024;
+
+// Reference variants this build does not provide: the real checkpoint's
+// head_dim 256 (sliding) / 512 (global) geometry with f16 K/V caches
+// (crates/sg-gpu/build.rs:255-430, :2271).  Every cache here is Q8_0 and
+// every attention kernel head_dim 128; lookup names the form to use instead.
+struct Unbuilt {
+    const char *name, *use;
+};
+const Unbuilt kUnbuilt[] = {
+    {"attn_decode_sliding", "attn_decode_sliding_q8_hd128"},
+    {"attn_decode_global", "attn_decode_global_q8_hd128"},
+    {"attn_decode_global_q8k", "attn_decode_global_q8_hd128"},
+    {"attn_reduce_d256", "attn_reduce_d128"},
+    {"attn_reduce_d512", "attn_reduce_d128"},
+    {"attn_prefill_sliding", "attn_prefill_sliding_ring_q8_hd128"},
+    {"attn_prefill_sliding_ring", "attn_prefill_sliding_ring_q8_hd128"},
+    {"attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_q8_hd128"},
+    {"attn_prefill_global_flash_sp_q8", "attn_prefill_global_flash_q8_hd128"},
+    {"kv_append_sliding", "kv_append_sliding_q8"},
+    {"kv_append_global", "kv_append_global_q8"},
 };
 
 // RoPE variants: (name, head_dim, rot_dims, n_heads).  The first four are
@@ -177,10 +210,46 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         k->info.bindings = 3;
         return true;
     }
-    if (name == "kv_append_global_q8") {
+    if (name == "kv_append_global_q8" || name == "kv_append_sliding_q8") {
         k->kind = Kind::AppendQ8;
         k->info.bindings = 4;
-        k->param = 0;
+        k->param = name == "kv_append_sliding_q8" ? kAttnWindow : 0;  // ring slots
+        return true;
+    }
+    if (name == "attn_decode_sliding_q8_hd128" || name == "attn_decode_global_q8_hd128") {
+        // bindings: 0 q fp32 [n_q × 128], 1 k_quants, 2 k_scales, 3 v_quants,
+        // 4 v_scales (Q8_0 pages [slot × n_kv × 128]), 5 part fp32
+        // [n_q × n_splits × 130], 6 step; push {n_splits: u32, scale: f32};
+        // kv_len = step[1] (sliding ring) or step[2] (global)
+        k->kind = Kind::AttnDecode;
+        k->info = {{256, 1, 1}, 7, 8, 0};
+        k->k = kAttnNQ;
+        k->n = kAttnNKv;
+        k->param = name == "attn_decode_sliding_q8_hd128" ? 1 : 2;
+        return true;
+    }
+    if (name == "attn_reduce_d128") {
+        // bindings: 0 part, 1 out fp32 [n_q × 128]; push n_splits; groups [n_q]
+        k->kind = Kind::AttnReduce;
+        k->info = {{256, 1, 1}, 2, 4, 0};
+        k->k = kAttnNQ;
+        k->n = kAttnNKv;
+        return true;
+    }
+    if (name == "attn_prefill_global_flash_q8_hd128" ||
+        name == "attn_prefill_sliding_ring_q8_hd128") {
+        // global: 0 q fp32 [M × n_q × 128], 1 k_quants, 2 k_scales,
+        //   3 v_quants, 4 v_scales (linear cache holding the chunk's keys),
+        //   5 out fp32, 6 step; groups [n_q, ceil(M/16)]
+        // sliding: 0 q, 1..4 the ring's K/V pages, 5..8 the chunk's K/V
+        //   pages [M × n_kv × 128], 9 out, 10 step; groups [n_kv, M]
+        // push {scale: f32}; q0 = step[3]; M = out range / (n_q·128·4)
+        k->kind = Kind::AttnPrefill;
+        const bool ring = name == "attn_prefill_sliding_ring_q8_hd128";
+        k->info = {{256, 1, 1}, ring ? 11u : 7u, 4, 0};
+        k->k = kAttnNQ;
+        k->n = kAttnNKv;
+        k->param = ring ? kAttnWindow : 0;
         return true;
     }
     if (starts_with(name, "gemm_q4_0_i8_bb_pfd")) {
@@ -250,10 +319,11 @@ Registry &registry() {
 }
 
 // Binding table lookup with range check.
+constexpr uint32_t kMaxBindings = 16;
 struct Binds {
-    const sgq_binding *b[8] = {};
+    const sgq_binding *b[kMaxBindings] = {};
     int get(uint32_t i, void **p, uint64_t *range) const {
-        if (i >= 8 || !b[i]) return fail(SGQ_ERR_VALIDATION, "binding %u missing", i);
+        if (i >= kMaxBindings || !b[i]) return fail(SGQ_ERR_VALIDATION, "binding %u missing", i);
         *p = static_cast<uint8_t *>(b[i]->ptr) + b[i]->offset;
         *range = b[i]->range;
         return SGQ_OK;
@@ -342,6 +412,10 @@ int sgq_buf_download(sgq_ctx *ctx, void *dst_host, const void *src_dev, uint64_t
 
 int sgq_buf_fill_zero(sgq_ctx *ctx, void *dev_ptr, uint64_t bytes) {
     if (!ctx) return fail(SGQ_ERR_VALIDATION, "ctx is NULL");
+    // A memset node recorded into a graph has given wrong results on replays
+    // after the first on this hardware pool: refuse instead of capturing one.
+    if (ctx->capturing)
+        return fail(SGQ_ERR_VALIDATION, "sgq_buf_fill_zero: not allowed while a graph capture is open");
     SGQ_HIP(hipMemsetAsync(dev_ptr, 0, bytes, ctx->stream));
     return SGQ_OK;
 }
@@ -356,6 +430,12 @@ int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
                       sgq_kernel_info *info) {
     (void)ctx;
     if (!name || !out) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    for (const Unbuilt &u : kUnbuilt)
+        if (std::strcmp(name, u.name) == 0)
+            return fail(SGQ_ERR_UNKNOWN_KERNEL,
+                        "kernel variant '%s' (head_dim 256/512, f16 K/V) is not built: "
+                        "caches are Q8_0 at head_dim 128 here, use '%s'",
+                        name, u.use);
     auto *k = new sgq_kernel;
     if (!resolve(name, k)) {
         delete k;
@@ -381,7 +461,7 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
     if (push_bytes && !push) return fail(SGQ_ERR_VALIDATION, "push is NULL");
     Binds B;
     for (uint32_t i = 0; i < n_bindings; i++) {
-        if (bindings[i].binding >= 8 || bindings[i].binding >= kernel->info.bindings)
+        if (bindings[i].binding >= kMaxBindings || bindings[i].binding >= kernel->info.bindings)
             return fail(SGQ_ERR_VALIDATION, "%s: binding %u out of range",
                         kernel->name.c_str(), bindings[i].binding);
         B.b[bindings[i].binding] = &bindings[i];
@@ -523,6 +603,84 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             return launch_gemm_q4_0_q8(st, p0, static_cast<const int8_t *>(p1),
                                        static_cast<const uint16_t *>(p2), static_cast<float *>(p3),
                                        m, n, k, split, partials);
+        }
+        case Kind::AttnDecode: {
+            void *p5, *p6;
+            uint64_t r5, r6;
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)) ||
+                (rc = B.get(3, &p3, &r3)) || (rc = B.get(4, &p4, &r4)) || (rc = B.get(5, &p5, &r5)) ||
+                (rc = B.get(6, &p6, &r6)))
+                return rc;
+            uint32_t n_splits;
+            float scale;
+            std::memcpy(&n_splits, push, 4);
+            std::memcpy(&scale, static_cast<const uint8_t *>(push) + 4, 4);
+            const uint32_t nq = kernel->k, nkv = kernel->n;
+            if (groups[0] != nkv || groups[1] != n_splits || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, n_splits=%u, 1]",
+                            kernel->name.c_str(), nkv, n_splits);
+            if (r0 && r0 < (uint64_t)nq * 128 * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: q binding too small", kernel->name.c_str());
+            if (r5 && r5 < (uint64_t)nq * n_splits * 130 * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: part binding too small", kernel->name.c_str());
+            if (r6 && r6 < 16)
+                return fail(SGQ_ERR_VALIDATION, "%s: step binding too small", kernel->name.c_str());
+            return launch_attn_decode_parts(
+                st, static_cast<const float *>(p0), static_cast<const int8_t *>(p1),
+                static_cast<const uint16_t *>(p2), static_cast<const int8_t *>(p3),
+                static_cast<const uint16_t *>(p4), static_cast<const uint32_t *>(p6),
+                (int)kernel->param, (int)nq, (int)nkv, (int)n_splits, scale, static_cast<float *>(p5));
+        }
+        case Kind::AttnReduce: {
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1))) return rc;
+            uint32_t n_splits;
+            std::memcpy(&n_splits, push, 4);
+            const uint32_t nq = kernel->k;
+            if (groups[0] != nq || groups[1] != 1 || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, 1, 1]",
+                            kernel->name.c_str(), nq);
+            if ((r0 && r0 < (uint64_t)nq * n_splits * 130 * 4) || (r1 && r1 < (uint64_t)nq * 128 * 4))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            return launch_attn_reduce(st, static_cast<const float *>(p0), (int)nq, (int)kernel->n,
+                                      (int)n_splits, static_cast<float *>(p1));
+        }
+        case Kind::AttnPrefill: {
+            const bool ring = kernel->param != 0;
+            void *pp[11];
+            uint64_t rr[11];
+            for (uint32_t i = 0; i < kernel->info.bindings; i++)
+                if ((rc = B.get(i, &pp[i], &rr[i]))) return rc;
+            const uint32_t out_b = ring ? 9 : 5, step_b = ring ? 10 : 6;
+            const uint32_t nq = kernel->k, nkv = kernel->n;
+            if (!rr[out_b])
+                return fail(SGQ_ERR_VALIDATION, "%s: out range required (it gives M)",
+                            kernel->name.c_str());
+            const uint64_t m = rr[out_b] / ((uint64_t)nq * 128 * 4);
+            if (m == 0 || m >= (1u << 30) || rr[out_b] != m * nq * 128 * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: out range is not a whole number of tokens",
+                            kernel->name.c_str());
+            const uint64_t gy = ring ? m : (m + 15) / 16;
+            if (groups[0] != (ring ? nkv : nq) || groups[1] != gy || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, %llu, 1]",
+                            kernel->name.c_str(), ring ? nkv : nq, (unsigned long long)gy);
+            if (rr[0] && rr[0] < m * nq * 128 * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: q binding too small", kernel->name.c_str());
+            if (ring && ((rr[5] && rr[5] < m * nkv * 128) || (rr[7] && rr[7] < m * nkv * 128)))
+                return fail(SGQ_ERR_VALIDATION, "%s: chunk pages too small", kernel->name.c_str());
+            if (rr[step_b] && rr[step_b] < 16)
+                return fail(SGQ_ERR_VALIDATION, "%s: step binding too small", kernel->name.c_str());
+            float scale;
+            std::memcpy(&scale, push, 4);
+            return launch_attn_prefill_q8(
+                st, static_cast<const float *>(pp[0]), static_cast<const int8_t *>(pp[1]),
+                static_cast<const uint16_t *>(pp[2]), static_cast<const int8_t *>(pp[3]),
+                static_cast<const uint16_t *>(pp[4]), static_cast<float *>(pp[out_b]), (int)m, 0,
+                (int)nq, (int)nkv, 128, ring ? (int)kAttnWindow : 0, scale,
+                ring ? (int)kernel->param : 0, ring ? static_cast<const int8_t *>(pp[5]) : nullptr,
+                ring ? static_cast<const uint16_t *>(pp[6]) : nullptr,
+                ring ? static_cast<const int8_t *>(pp[7]) : nullptr,
+                ring ? static_cast<const uint16_t *>(pp[8]) : nullptr,
+                static_cast<const uint32_t *>(pp[step_b]));
         }
     }
     return fail(SGQ_ERR_LIBRARY, "unhandled kernel kind");

@@ -126,6 +126,43 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     return SGQ_OK;
 }
 
+int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
+                             const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
+                             const uint32_t *step, int step_word, int n_q, int n_kv, int n_splits,
+                             float scale, float *part) {
+    SGQ_CHECK(step != nullptr && part != nullptr, "attn_decode (parts): step and part required");
+    SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0 && (n_q / n_kv == 1 || n_q / n_kv == 2),
+              "attn_decode (parts): %d q heads over %d kv heads unsupported", n_q, n_kv);
+    SGQ_CHECK(n_splits >= 1 && n_splits <= kMergeMaxSplits,
+              "attn_decode (parts): n_splits %d out of range (1..%d)", n_splits, kMergeMaxSplits);
+    SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0 && ((uintptr_t)ks & 7) == 0 &&
+                  ((uintptr_t)vs & 7) == 0 && ((uintptr_t)part & 3) == 0,
+              "attn_decode (parts): misaligned operand");
+    dim3 grid(n_kv, n_splits);
+    if (n_q == n_kv)
+        hipLaunchKernelGGL((attn_decode_q8_kernel<1, false, kAttnWaves>), grid,
+                           dim3(kAttnWaves * kWave), 0, st, q, kq, ks, vq, vs, step, step_word, 0u,
+                           n_kv, n_splits, scale, part, nullptr, nullptr, AttnPost{});
+    else
+        hipLaunchKernelGGL((attn_decode_q8_kernel<2, false, kAttnWaves>), grid,
+                           dim3(kAttnWaves * kWave), 0, st, q, kq, ks, vq, vs, step, step_word, 0u,
+                           n_kv, n_splits, scale, part, nullptr, nullptr, AttnPost{});
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_attn_reduce(hipStream_t st, const float *part, int n_q, int n_kv, int n_splits,
+                       float *out) {
+    SGQ_CHECK(part != nullptr && out != nullptr, "attn_reduce: NULL operand");
+    SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0 && (n_q / n_kv == 1 || n_q / n_kv == 2),
+              "attn_reduce: %d q heads over %d kv heads unsupported", n_q, n_kv);
+    SGQ_CHECK(n_splits >= 1 && n_splits <= kMergeMaxSplits,
+              "attn_reduce: n_splits %d out of range (1..%d)", n_splits, kMergeMaxSplits);
+    launch_merge(st, n_q / n_kv, n_q, n_kv, n_splits, part, out, nullptr);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
 int attn_prepare() { return SGQ_OK; }  // all variants fit the default LDS limit
 
 int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_raw,

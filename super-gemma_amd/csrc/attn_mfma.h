@@ -95,10 +95,11 @@ __device__ __forceinline__ void attn_group_load(AttnGroup &g, const int8_t *__re
 }
 
 // The split work item of kv head kvh over the split's slots.  With
-// n_splits > 1 it writes the partial (acc, m, l) of its QPK query heads to
-// part (agent-scope stores, so a merge in the same launch may read them
-// after an atomic handoff); with one split it writes the normalised rows to
-// out and/or their x limbs to limbs_out (either may be null).  q is read
+// n_splits > 1, or with neither out nor limbs_out given, it writes the
+// partial (acc, m, l) of its QPK query heads to part (agent-scope stores, so
+// a merge in the same launch may read them after an atomic handoff);
+// otherwise (one split) it writes the normalised rows to out and/or their x
+// limbs to limbs_out.  q is read
 // from global memory unless FUSED, in which case the post-projection of
 // AttnPost runs first (and split 0 appends the new K/V row).  All W·64
 // threads call.
@@ -357,7 +358,7 @@ __device__ __forceinline__ void attn_chunk(const float *__restrict__ q,
             l = __builtin_fmaf(wml_s[w][oh][1], f, l);
         }
     }
-    if (n_splits > 1) {
+    if (n_splits > 1 || (out == nullptr && limbs_out == nullptr)) {
         if (ot) {
             const size_t rowp = ((size_t)(kvh * QPK + oh) * n_splits + split) * stride;
             st_agent(&part[rowp + d], a);

@@ -74,7 +74,8 @@ struct KvSource {
 template <int HPW>
 __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
-    int n_q, int n_kv, int window, float scale, int qtiles) {
+    int n_q, int n_kv, int window, float scale, int qtiles, const uint32_t *__restrict__ step) {
+    if (step) q0 = (int)step[3];
     __shared__ __align__(16) _Float16 k_s[kLT][kKRow];
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
 
@@ -246,7 +247,7 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
                            const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
                            int n_q, int n_kv, int head_dim, int window, float scale, int ring,
                            const int8_t *ckq, const uint16_t *cks, const int8_t *cvq,
-                           const uint16_t *cvs) {
+                           const uint16_t *cvs, const uint32_t *step) {
     SGQ_CHECK(head_dim == kHD, "attn_prefill_q8: head_dim %d unsupported (128)", head_dim);
     SGQ_CHECK(n_tok > 0 && q0 >= 0, "attn_prefill_q8: n_tok %d, q0 %d", n_tok, q0);
     SGQ_CHECK(n_kv > 0 && n_q > 0 && n_q % n_kv == 0, "attn_prefill_q8: n_q %% n_kv != 0");
@@ -265,10 +266,10 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
     const int qpk = n_q / n_kv;
     if (kPrefillPairHeads && qpk % 2 == 0)
         hipLaunchKernelGGL(attn_prefill_kernel<2>, dim3(qtiles, n_q / 2), dim3(512), 0, st, q, src,
-                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
+                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles, step);
     else
         hipLaunchKernelGGL(attn_prefill_kernel<1>, dim3(qtiles, n_q), dim3(256), 0, st, q, src,
-                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles);
+                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles, step);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }

@@ -134,6 +134,17 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
                           int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
                           int n_splits, float scale, float *out, void *workspace,
                           size_t workspace_bytes, void *limbs_out = nullptr);
+// The split kernel alone, reading kv_len from step[step_word] and writing
+// every split's partial (acc[128], m, l) per query head to part
+// [n_q × n_splits × 130] (attn_decode_global_q8k.wgsl's part layout); then
+// the merge of those partials in split order into out [n_q × 128]
+// (attn_reduce.wgsl:24-57).  head_dim 128, 1 or 2 query heads per kv head.
+int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
+                             const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
+                             const uint32_t *step, int step_word, int n_q, int n_kv, int n_splits,
+                             float scale, float *part);
+int launch_attn_reduce(hipStream_t st, const float *part, int n_q, int n_kv, int n_splits,
+                       float *out);
 // Sets the attention kernels' launch attributes (call before graph capture).
 int attn_prepare();
 // Decode attention with the step's q/k/v post-projection fused in (and,
@@ -151,11 +162,14 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                              bool merge_in_launch = false);
 // Keys before q0 come from the cache (ring: slot = pos % ring), keys from q0
 // on from the chunk's pages ckq.. (row = pos - q0) when given, else the cache.
+// With step non-null, q0 is read on the device from step[3] (the host value
+// is ignored), so a recorded graph replays with a new chunk position.
 int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
                            const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,
                            int n_q, int n_kv, int head_dim, int window, float scale, int ring = 0,
                            const int8_t *ckq = nullptr, const uint16_t *cks = nullptr,
-                           const int8_t *cvq = nullptr, const uint16_t *cvs = nullptr);
+                           const int8_t *cvq = nullptr, const uint16_t *cvs = nullptr,
+                           const uint32_t *step = nullptr);
 int launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *y, uint32_t rows,
                    uint32_t row_len, int plus_one, float eps);
 int launch_rope(hipStream_t st, float *xs, const float *cos_sin, uint64_t rows, uint32_t head_dim,

@@ -614,6 +614,15 @@ class Model:
         _check(lib().sgq_model_tensor(self._h, layer, name.encode(), C.byref(p), C.byref(b)))
         return p.value, b.value
 
+    def write_tensor(self, name: str, data, layer: int = -1):
+        """Overwrite a named device tensor with host bytes of exactly its size."""
+        import numpy as np
+        a = np.ascontiguousarray(data)
+        p, b = self.tensor_ptr(name, layer)
+        if a.nbytes != b:
+            raise ValidationError(6, f"{name}[{layer}]: {a.nbytes} bytes given, tensor has {b}")
+        _check(lib().sgq_buf_upload(self.ctx.handle, p, a.ctypes.data, b))
+
     def read_tensor(self, name: str, layer: int = -1, dtype=None):
         """Host copy (numpy) of a named device tensor."""
         import numpy as np

@@ -70,6 +70,34 @@ def test_registry_names_resolve_without_device():
     assert rc == 4 and b"unknown kernel" in L.sgq_last_error()
 
 
+def test_attention_variants_layouts_and_unbuilt_names():
+    """The record_layer attention / KV-append surface (crates/sg-model/src/
+    graph.rs:560-656) at head_dim 128 with Q8_0 K/V; the reference's hd
+    256/512 f16-cache names fail with UnknownKernel naming the form to use."""
+    import sgq
+
+    L = sgq.lib()
+    h = C.c_void_p()
+    info = sgq._Info()
+    want = {"kv_append_global_q8": (4, 0), "kv_append_sliding_q8": (4, 0),
+            "attn_decode_global_q8_hd128": (7, 8), "attn_decode_sliding_q8_hd128": (7, 8),
+            "attn_reduce_d128": (2, 4), "attn_prefill_global_flash_q8_hd128": (7, 4),
+            "attn_prefill_sliding_ring_q8_hd128": (11, 4)}
+    for n, (nb, pb) in want.items():
+        assert L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info)) == 0, n
+        assert (info.bindings, info.push_bytes) == (nb, pb), n
+    for n, use in [("attn_decode_global_q8k", "attn_decode_global_q8_hd128"),
+                   ("attn_decode_sliding", "attn_decode_sliding_q8_hd128"),
+                   ("attn_reduce_d512", "attn_reduce_d128"), ("attn_reduce_d256", "attn_reduce_d128"),
+                   ("attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_q8_hd128"),
+                   ("attn_prefill_sliding_ring", "attn_prefill_sliding_ring_q8_hd128"),
+                   ("kv_append_global", "kv_append_global_q8"),
+                   ("kv_append_sliding", "kv_append_sliding_q8")]:
+        rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
+        msg = L.sgq_last_error().decode()
+        assert rc == 4 and "not built" in msg and f"'{use}'" in msg, (n, msg)
+
+
 def test_ctx_create_without_device_reports_no_device():
     import torch
     import sgq

@@ -112,3 +112,38 @@ def test_attn_decode_bit_deterministic(ctx, oracle):
     c = _run(ctx, q, kq, ks, vq, vs, kv_len, n_q, n_kv, 7, 0.1)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert np.allclose(a, c, rtol=1e-5, atol=1e-6)
+
+
+def test_attn_decode_128k_sampled_heads(ctx, oracle):
+    """BASELINE config 4 at its longest context, 131072 slots (570 MB of Q8_0
+    K/V, generated and quantized on the device: the quantizer is bit-exact
+    against the oracle), 256 splits, scale 1.0; every head computed, six
+    heads (spanning both q heads of a kv head and the first/last kv head)
+    checked against the f64 oracle over the dequantized cache."""
+    n_q, n_kv, kv_len, splits = 32, 16, 131072, 256
+    print(f"attn decode 128K kv_len={kv_len} splits={splits}", flush=True)
+    n = kv_len * n_kv * HD
+    kv = []
+    for seed in (0x128A, 0x128B):
+        x = empty(n, torch.float32)
+        ctx.fill_normal(x, seed=seed)
+        s = empty(n // 32, torch.int16)
+        qn = empty(n, torch.int8)
+        ctx.quant_q8_0(x, s, qn)
+        del x
+        kv += [qn, s]
+    kq, ks, vq, vs = kv
+    rng = oracle.Rng(0x128C)
+    q = rng.f32_vec(n_q * HD) * np.float32(0.1)
+    out = empty(n_q * HD, torch.float32)
+    ctx.attn_decode_q8(dev(q), kq, ks, vq, vs, kv_len, n_q, n_kv, out, n_splits=splits, scale=1.0)
+    torch.cuda.synchronize()
+    got = host(out).reshape(n_q, HD)
+    assert np.isfinite(got).all()
+    kd = oracle.dequant_q8_0(host(ks, np.uint16), host(kq))
+    vd = oracle.dequant_q8_0(host(vs, np.uint16), host(vq))
+    heads = [0, 1, 14, 15, 30, 31]
+    want = np.stack([oracle.attention_head(q, kd, vd, 0, h, n_q, n_kv, HD, 1.0, 0, kv_len - 1)
+                     for h in heads])
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert_close(got[heads], want, 1e-3, 1e-4 * rms, "decode 128K")

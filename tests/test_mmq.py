@@ -183,3 +183,35 @@ def test_mmq_rejects_bad_split(ctx):
     y = empty(64 * 32, torch.float32)
     with pytest.raises(sgq.ValidationError):
         ctx.gemm_q4_0_q8(w, xq, xs, y, 64, 32, 64, 3, empty(3 * 64 * 32, torch.float32))
+
+
+@pytest.mark.parametrize("split", [1, 2, 4, 8])
+def test_mmq_config3_m2048(ctx, oracle, split):
+    """BASELINE config 3 at its stated M=2048 (K=21504, N=5376, X =
+    gelu(N(0,1))*N(0,1) -> Q8): split-K 1/2/4/8 against split 1 (normwise
+    <= 4e-6, fp32 reassociation) and 400 sampled outputs against the oracle,
+    including the four corners."""
+    print(f"mmq config 3 M=2048 split {split}", flush=True)
+    m, k, n = 2048, 21504, 5376
+    tw = empty(n * k // 32 * 18, torch.uint8)
+    ctx.fill_q4_0_random(tw, n * k // 32, seed=41, sigma=0.02)
+    g = empty(m * k, torch.float32)
+    u = empty(m * k, torch.float32)
+    ctx.fill_normal(g, seed=42)
+    ctx.fill_normal(u, seed=43)
+    x = (torch.nn.functional.gelu(g, approximate="tanh") * u).contiguous()
+    del g, u
+    xq_t, xs_t = _quant_on_gpu(ctx, x, m, k)
+    del x
+    y1 = empty(m * n, torch.float32)
+    ctx.gemm_q4_0_q8(tw, xq_t, xs_t, y1, m, n, k)
+    ys = empty(m * n, torch.float32)
+    part = empty(split * m * n, torch.float32) if split > 1 else None
+    ctx.gemm_q4_0_q8(tw, xq_t, xs_t, ys, m, n, k, split, part)
+    torch.cuda.synchronize()
+    assert rel_err(host(ys), host(y1)) <= 4e-6
+    gen = np.random.default_rng(100 + split)
+    ms = np.concatenate([gen.integers(0, m, 396), [0, 0, m - 1, m - 1]])
+    ns = np.concatenate([gen.integers(0, n, 396), [0, n - 1, 0, n - 1]])
+    _check_pairs(oracle, host(tw), host(xq_t), host(xs_t, np.uint16), host(ys).reshape(m, n), k,
+                 ms, ns, f"config 3 split {split}")
