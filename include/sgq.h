@@ -171,6 +171,17 @@ int sgq_x_limbs(sgq_ctx *ctx, const float *x, void *x_limbs, uint32_t k);
 int sgq_gemv_q4_0_limbs(sgq_ctx *ctx, uint32_t n_targets, const void *const *w, float *const *y,
                         const uint32_t *rows, const void *x_limbs, uint32_t k, float softcap);
 
+/* Allocation-free form of sgq_gemv_q4_0: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No context:
+ * work goes on `hip_stream` (NULL = the null stream), which must belong to the
+ * current device.  The x limb table lives in a library-owned device array of
+ * 192 KiB per device (kept until the process ends), so k <= 65536; larger k
+ * returns SGQ_ERR_VALIDATION.  Every call on one device shares that array:
+ * calls that overlap on one device (different streams, or threads) race. */
+int sgq_gemv_q4_0_noalloc(void *hip_stream, const void *w, const float *x, float *y, uint32_t n,
+                          uint32_t k);
+
 /* Q6_K LM head: y[n] = softcap·tanh((E[n×k]·x[k]) / softcap) (softcap <= 0:
  * the raw dot).  Replaces gemv_q6_k_logits
  * (crates/sg-gpu/shaders/gemv_q6_k_logits.wgsl:41-104; registry entry

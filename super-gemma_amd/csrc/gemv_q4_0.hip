@@ -21,6 +21,8 @@
 //    (even blocks start 4-aligned, odd blocks 2 bytes past); v_perm_b32
 //    realigns the 16 nibble bytes with a per-lane selector.
 //  * Row sums: butterfly over the wave (fixed order: deterministic).
+#include <mutex>
+
 #include "ring.h"
 
 namespace sgq {
@@ -1009,3 +1011,56 @@ int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, ui
 }
 
 }  // namespace sgq
+
+// ---------------------------------------------------------------------------
+// Allocation-free form of sgq_gemv_q4_0 for callers that cannot allocate
+// device memory (code under HIP graph capture, tight serving loops): the x
+// limb table lives in a file-scope device array instead of a context's
+// workspace.  The array's host-side name is not a device address; its
+// address is looked up once per device with hipGetSymbolAddress and only
+// that pointer is handed to kernels.
+// ---------------------------------------------------------------------------
+namespace sgq {
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = kGemvWorkspace;  // limbs for K <= 65536
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on its first use).
+int scratch_for_current_device(void **out) {
+    int dev = -1;
+    SGQ_HIP(hipGetDevice(&dev));
+    SGQ_CHECK(dev >= 0 && dev < kMaxDevices, "gemv_q4_0_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        SGQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        SGQ_CHECK(p != nullptr, "gemv_q4_0_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SGQ_OK;
+}
+
+}  // namespace
+}  // namespace sgq
+
+extern "C" int sgq_gemv_q4_0_noalloc(void *hip_stream, const void *w, const float *x, float *y,
+                                     uint32_t n, uint32_t k) {
+    using namespace sgq;
+    if (!w || !x || !y) return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_CHECK(k % 64 == 0 && k > 0 && k <= 65536,
+              "gemv_q4_0_noalloc: k=%u must be a positive multiple of 64 and <= 65536 "
+              "(the %zu-byte scratch array holds the x limbs of at most 65536 values)",
+              k, kNoAllocScratchBytes);
+    SGQ_CHECK((size_t)(k / 32) * sizeof(BlockLimbs) <= kNoAllocScratchBytes,
+              "gemv_q4_0_noalloc: k=%u needs %zu scratch bytes, %zu available", k,
+              (size_t)(k / 32) * sizeof(BlockLimbs), kNoAllocScratchBytes);
+    void *ws = nullptr;
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+    return launch_gemv_q4_0(static_cast<hipStream_t>(hip_stream), w, x, y, n, k, ws);
+}

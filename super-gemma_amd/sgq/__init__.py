@@ -107,6 +107,7 @@ SIGNATURES = {
     "sgq_buf_upload": (I, [P, P, P, U64]),
     "sgq_buf_download": (I, [P, P, P, U64]),
     "sgq_buf_fill_zero": (I, [P, P, U64]),
+    "sgq_gemv_q4_0_noalloc": (I, [P, P, P, P, U32, U32]),
     "sgq_kernel_lookup": (I, [P, C.c_char_p, C.POINTER(P), C.POINTER(_Info)]),
     "sgq_kernel_count": (U32, []),
     "sgq_kernel_name": (C.c_char_p, [U32]),
