@@ -75,7 +75,8 @@ class Gemv:
         gbs = self.bytes / (ms_per_step * 1e-3) / 1e9
         return {
             "value": gbs, "unit": "GB/s",
-            "dtype": "q4_0 weights, fp32 x/y (i4 dot8 on 4-limb x)",
+            "dtype": "q4_0 weights, fp32 x/y; x enters the i4 dot8 as 15-bit fixed point per "
+                     "32-block (4 limbs)",
             "roofline": ring_roofline(self.ctx, self.torch, [w.data_ptr() for w in self.w],
                                       self.k, self.n),
             "config": {"workload": self.name, "m": 1, "k": self.k, "n": self.n,
@@ -282,15 +283,34 @@ class Prefill:
         self.model.reset()
         self.model.prefill(self.tokens, self.logits)
 
+    def mmq_roofline(self):
+        """The dominant kernel alone: the MMQ at the prefill's gate/up shape
+        (M=4096, K=5376, N=21504), timed with HIP events over 10 launches."""
+        t = self.torch
+        m, k, n = self.n_tok, 5376, 21504
+        mm = Mmq(self.ctx, t, m=m, k=k, n=n, label="prefill gate/up shape")
+        mm.step(0)
+        self.ctx.synchronize()
+        self.ctx.timer_start()
+        for i in range(10):
+            mm.step(i)
+        ms = self.ctx.timer_stop() / 10
+        r = mm.result(ms)["roofline"]
+        r["kernel"] = f"mmq_kernel M={m} K={k} N={n} (int8 ops only)"
+        r["us_per_launch"] = ms * 1e3
+        del mm
+        return r
+
     def result(self, ms_per_step):
         tops = (self.mmq_ops + self.attn_flops) / (ms_per_step * 1e-3) / 1e12
         c = self.cfg
         return {
             "value": self.n_tok / (ms_per_step * 1e-3), "unit": "tok/s (prefill)",
             "dtype": "q4_0 weights x q8_0 activations (int8 MFMA), f16 attention",
-            "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS,
-                         "unit": "TOP/s", "frac": tops / INT8_PEAK_TOPS, "traffic": None,
-                         "note": "whole prefill: MMQ int8 ops + attention flops per second"},
+            "roofline": self.mmq_roofline(),
+            "whole_prefill_rate": {"achieved": tops, "unit": "TOP/s",
+                                   "note": "MMQ int8 ops + attention f16 flops per second "
+                                           "over the whole prefill (mixed units: no peak)"},
             "config": {"workload": f"prefill {self.n_tok} tokens from position 0, 62-layer "
                                    "random-init decoder (BASELINE config 5)",
                        "n_layers": c.n_layers, "hidden": c.hidden, "ffn": c.ffn,
@@ -344,7 +364,8 @@ class Decode:
         c = self.cfg
         return {
             "value": tok_s, "unit": "tok/s",
-            "dtype": "q4_0 weights, q8_0 kv, fp32 activations",
+            "dtype": "q4_0 weights x i4-limb activations (15-bit fixed point per 32-block) "
+                     "in every GEMV, q8_0 kv, fp32 elsewhere",
             "roofline": self.kernel_roofline(),
             "step_roofline": {"bound": "hbm", "achieved": step_gbs, "peak": HBM_PEAK_GBS,
                               "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS,
@@ -400,46 +421,151 @@ def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
             rc = lib.sgq_gemv_q4_0_limbs(ctx.handle, 1, wp, yp, rows, C.c_void_p(xl.data_ptr()),
                                          k, 0.0)
             assert rc == 0, sgq.lib().sgq_last_error()
-    run(len(w_ptrs))
-    ctx.synchronize()
-    with sgq.GraphRecorder(ctx) as rec:
-        run(steps)
-    rec.graph.submit()  # warm replay
-    ctx.synchronize()
-    ctx.timer_start()
-    rec.graph.submit()
-    ms = ctx.timer_stop() / steps
+    def full(m):  # the whole typed call: fp32 x -> limbs -> streamed kernel
+        for j in range(m):
+            rc = lib.sgq_gemv_q4_0(ctx.handle, C.c_void_p(w_ptrs[j % len(w_ptrs)]),
+                                   C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr()), n, k)
+            assert rc == 0, sgq.lib().sgq_last_error()
+
+    def timed(fn):
+        fn(len(w_ptrs))
+        ctx.synchronize()
+        with sgq.GraphRecorder(ctx) as rec:
+            fn(steps)
+        rec.graph.submit()  # warm replay
+        ctx.synchronize()
+        ctx.timer_start()
+        rec.graph.submit()
+        return ctx.timer_stop() / steps
+
+    ms = timed(run)
+    ms_full = timed(full)
     nbytes = q4_bytes(n, k) + (k // 32) * 80 + n * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
+    full_bytes = q4_bytes(n, k) + k * 4 + n * 4  # BASELINE's config-1 bytes (fp32 x in)
+    full_gbs = full_bytes / (ms_full * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic(),
             "kernel": f"gemv_q4_0_ring_kernel K={k} N={n}", "bytes_per_launch": nbytes,
-            "us_per_launch": ms * 1e3, "launches": steps}
+            "us_per_launch": ms * 1e3, "launches": steps,
+            "full_call": {"what": "sgq_gemv_q4_0 (fp32 x -> limb kernel -> streamed kernel)",
+                          "us_per_call": ms_full * 1e3, "achieved": full_gbs,
+                          "frac": full_gbs / HBM_PEAK_GBS, "bytes_per_call": full_bytes}}
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """Time the CPU restatement of CpuModel::matmul (dequant_row + 8-lane f64
-    dot, row-parallel) on BASELINE config 1, full size, on the host cores."""
-    import numpy as np
-    from oracle import oracle
+def measured_peaks(torch):
+    """Roofline denominators measured on this box (libsgq_probe.so, no memory
+    traffic for the MFMA probes): the dense int8 MFMA rate, the ceiling of an
+    exact per-32-block rescale (16 cvt + 16 FMA per int8 MFMA, and with the
+    f16 scale-product MFMA as the MMQ issues it), and a streaming HBM read of
+    4 GiB.  Each is the best of 3 launches timed with HIP events on torch's
+    current stream."""
+    import ctypes as C
 
-    k, n = 5376, 21504
-    threads = max(1, min(16, os.cpu_count() or 1))
-    rng = oracle.Rng(0xBA5E)
-    w = rng.random_q4_0(n * k // 32)
-    x = rng.f32_vec(k)
-    oracle.matmul_q4_0(w, x, 1, n, k, threads)  # warm
+    path = os.path.join(ROOT, "super-gemma_amd", "sgq", "libsgq_probe.so")
+    if not os.path.exists(path):
+        return None
+    P = C.CDLL(path)
+    P.sgqp_mfma.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
+    P.sgqp_mfma_count.restype = C.c_longlong
+    P.sgqp_mfma_count.argtypes = [C.c_int, C.c_int, C.c_int]
+    P.sgqp_hbm_read.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, C.c_void_p]
+    stream = torch.cuda.current_stream()
+    sp = C.c_void_p(stream.cuda_stream)
+
+    def best_ms(launch, reps=3):
+        launch()
+        best = None
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            launch()
+            e1.record(stream)
+            e1.synchronize()
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+        return best
+
+    out = {}
+    for label, mode, blocks, iters in (("int8_mfma", 0, 1024, 20000),
+                                       ("int8_mfma_cvt_fma_ceiling", 1, 512, 20000),
+                                       ("int8_mfma_cvt_fma_scale_mfma_ceiling", 2, 512, 20000)):
+        buf = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
+        ms = best_ms(lambda: P.sgqp_mfma(sp, mode, blocks, iters, C.c_void_p(buf.data_ptr())))
+        ops = P.sgqp_mfma_count(mode, blocks, iters) * 2.0 * 32 * 32 * 32
+        out[label + "_tops"] = ops / (ms * 1e-3) / 1e12
+    nbytes = 4 << 30
+    big = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    red = torch.empty(4096 * 256, dtype=torch.float32, device="cuda")
+    ms = best_ms(lambda: P.sgqp_hbm_read(sp, C.c_void_p(big.data_ptr()), nbytes, 4096,
+                                         C.c_void_p(red.data_ptr())))
+    out["hbm_read_gbs"] = nbytes / (ms * 1e-3) / 1e9
+    del big
+    out["note"] = ("int8 MFMA 32x32x32 only (16 waves/CU); the same with 16 cvt + 16 FMA "
+                   "per MFMA, and with the f16 scale MFMA too (8 waves/CU, the MMQ's "
+                   "occupancy); streaming read of 4 GiB")
+    return out
+
+
+def _time_reps(fn, budget_s):
+    fn()  # warm
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.matmul_q4_0(w, x, 1, n, k, threads)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
         if el > budget_s or reps >= 100000:
-            break
+            return reps, el
+
+
+def cpu_baseline(budget_s: float = 8.0):
+    """Time the CPU restatement of CpuModel::matmul (dequant_row + 8-lane f64
+    dot, row-parallel; reference.rs:402-475) on the host cores:
+      - config 1 (GEMV K=5376, N=21504) at full size on min(16, host CPUs)
+        threads, and on 1 thread;
+      - configs 2 and 3 (the same matmul over M tokens, as the reference's
+        CPU forward runs a prefill chunk) at reduced M, fitted as
+        t(M) = a + b*M from two M values and extrapolated linearly to the
+        configs' M (stated in the report)."""
+    import numpy as np
+    from oracle import oracle
+
+    try:
+        host_cpus = len(os.sched_getaffinity(0))
+    except AttributeError:
+        host_cpus = os.cpu_count() or 1
+    threads = max(1, min(16, host_cpus))
+    rng = oracle.Rng(0xBA5E)
+    k, n = 5376, 21504
+    w = rng.random_q4_0(n * k // 32)
+    x = rng.f32_vec(k)
+    reps, el = _time_reps(lambda: oracle.matmul_q4_0(w, x, 1, n, k, threads), budget_s)
     gbs = q4_bytes(n, k) * reps / el / 1e9
+    reps1, el1 = _time_reps(lambda: oracle.matmul_q4_0(w, x, 1, n, k, 1), budget_s / 2)
+    gbs1 = q4_bytes(n, k) * reps1 / el1 / 1e9
+
+    def mmq_extrapolated(m_full, k_, n_, ms=(4, 16)):
+        wq = rng.random_q4_0(n_ * k_ // 32)
+        xs = rng.f32_vec(max(ms) * k_)
+        t = []
+        for m in ms:
+            r, e = _time_reps(lambda: oracle.matmul_q4_0(wq, xs[:m * k_], m, n_, k_, threads),
+                              budget_s / 4)
+            t.append(e / r)
+        b = (t[1] - t[0]) / (ms[1] - ms[0])
+        a = t[0] - b * ms[0]
+        t_full = a + b * m_full
+        return {"m": m_full, "k": k_, "n": n_, "seconds": t_full,
+                "tops": 2.0 * m_full * n_ * k_ / t_full / 1e12,
+                "fit": f"t(M) = {a * 1e3:.1f} ms + {b * 1e3:.2f} ms * M from M = {ms[0]}, {ms[1]}"}
+
     return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"config 1 GEMV (K=5376, N=21504) full size, {reps} reps in {el:.1f} s, "
-                      f"C restatement of reference.rs:402-444 on {threads} threads"}
+            "host_cpus": host_cpus, "value_1_thread": gbs1,
+            "sample": f"config 1 GEMV (K=5376, N=21504) full size: {reps} reps in {el:.1f} s on "
+                      f"{threads} threads ({host_cpus} host CPUs), {reps1} reps in {el1:.1f} s on "
+                      "1 thread; C restatement of reference.rs:402-444",
+            "mmq_config2_extrapolated": mmq_extrapolated(512, 5376, 21504),
+            "mmq_config3_extrapolated": mmq_extrapolated(2048, 21504, 5376)}
 
 
 def main():
@@ -456,6 +582,8 @@ def main():
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k", "head_q6k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true",
+                    help="skip the measured MFMA / HBM peak probes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build runs on one GPU only "
@@ -516,8 +644,17 @@ def main():
         "config": res["config"],
         "roofline": res["roofline"],
         **({"step_roofline": res["step_roofline"]} if "step_roofline" in res else {}),
+        **({"whole_prefill_rate": res["whole_prefill_rate"]} if "whole_prefill_rate" in res
+           else {}),
         "kernel": wl.kernel,
     }
+    if not args.no_peaks:
+        out["measured_peaks"] = measured_peaks(torch)
+        if out["measured_peaks"] and out["roofline"].get("unit") == "TOP/s":
+            mp = out["measured_peaks"]
+            a = out["roofline"]["achieved"]
+            out["roofline"]["frac_of_measured_int8_peak"] = a / mp["int8_mfma_tops"]
+            out["roofline"]["frac_of_rescale_ceiling"] = a / mp["int8_mfma_cvt_fma_scale_mfma_ceiling_tops"]
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
