@@ -375,7 +375,7 @@ __device__ __forceinline__ void attn_chunk(const float *__restrict__ q,
     if (limbs_out == nullptr) return;
     __syncthreads();  // wacc_s reads done
     float *o_s = &wacc_s[0][0][0];
-    if (ot) o_s[tid] = res;
+    if (ot) o_s[oh * kHD + d] = res;  // thread tid holds dim d of head oh (not dim tid)
     __syncthreads();
     if (tid < QPK * kHD / 4) {
         const float4 v = *reinterpret_cast<const float4 *>(&o_s[4 * tid]);
