@@ -17,6 +17,8 @@ batch of synthetic input, already resident in HBM:
   splitk  BASELINE config 3: down-proj M=2048, K=21504, N=5376, split-K 4.
   attn_prefill, attn_prefill_sliding
           BASELINE config 4 prefill: 4096 queries, causal / sliding-1024.
+  attn_prefill_ipv
+          the same causal prefill with int8 PV over key-blocked V.
   attn_decode_4k, attn_decode_32k, attn_decode_128k
           BASELINE config 4 decode over a 4K / 32K / 128K Q8_0 context.
   head_q6k
@@ -131,8 +133,9 @@ class AttnPrefill:
     causal (window 0) or sliding-1024, over a Q8_0 cache of N(0,1) K/V."""
     kernel = "attn_prefill_kernel"
 
-    def __init__(self, ctx, torch, window=0, n_tok=4096):
+    def __init__(self, ctx, torch, window=0, n_tok=4096, ipv=False):
         self.ctx, self.torch, self.window, self.n_tok = ctx, torch, window, n_tok
+        self.ipv = ipv
         n_q, n_kv, hd = 32, 16, 128
         self.n_q, self.n_kv = n_q, n_kv
         kv = torch.empty(n_tok * n_kv * hd, dtype=torch.float32, device="cuda")
@@ -143,23 +146,35 @@ class AttnPrefill:
         ctx.fill_normal(kv, seed=41)
         ctx.quant_q8_0(kv, self.ks, self.kq)
         ctx.fill_normal(kv, seed=42)
-        ctx.quant_q8_0(kv, self.vs, self.vq)
+        if ipv:  # V with key-blocked scales (int8 PV)
+            self.vs_kb = torch.empty(((n_tok + 31) // 32) * n_kv * hd, dtype=torch.int16,
+                                     device="cuda")
+            ctx.kv_append_v_q8(kv, n_tok, n_kv * hd, 0, self.vq, self.vs_kb)
+        else:
+            ctx.quant_q8_0(kv, self.vs, self.vq)
         self.q = torch.empty(n_tok * n_q * hd, dtype=torch.float32, device="cuda")
         ctx.fill_normal(self.q, seed=43)
         self.out = torch.empty_like(self.q)
         pairs = sum(min(i + 1, window) if window else i + 1 for i in range(n_tok))
         self.flops = 4.0 * hd * n_q * pairs  # QK^T and PV, 2 flops per MAC
-        self.name = (f"attn_prefill_q8 {n_tok} queries, 32q/16kv, hd 128, "
-                     f"{'sliding-%d' % window if window else 'causal'} (BASELINE config 4)")
+        self.name = (f"attn_prefill_{'ipv' if ipv else 'q8'} {n_tok} queries, 32q/16kv, hd 128, "
+                     f"{'sliding-%d' % window if window else 'causal'} (BASELINE config 4)"
+                     + (", int8 PV with key-blocked V" if ipv else ""))
 
     def step(self, i):
+        if self.ipv:
+            self.ctx.attn_prefill_ipv(self.q, self.kq, self.ks, self.vq, self.vs_kb, self.n_tok, 0,
+                                      self.n_q, self.n_kv, self.out)
+            return
         self.ctx.attn_prefill_q8(self.q, self.kq, self.ks, self.vq, self.vs, self.n_tok, 0,
                                  self.n_q, self.n_kv, self.out, window=self.window)
 
     def result(self, ms_per_step):
         tf = self.flops / (ms_per_step * 1e-3) / 1e12
         return {
-            "value": tf, "unit": "TFLOP/s", "dtype": "f16 MFMA (K/V dequantized from Q8_0), fp32 acc",
+            "value": tf, "unit": "TFLOP/s",
+            "dtype": ("f16 MFMA QK, int8 MFMA PV (P quantized per 32-key block), fp32 acc"
+                      if self.ipv else "f16 MFMA (K/V dequantized from Q8_0), fp32 acc"),
             "roofline": {"bound": "mfma", "achieved": tf, "peak": F16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": tf / F16_PEAK_TFLOPS, "traffic": None},
             "config": {"workload": self.name, "flops_per_launch": self.flops},
@@ -579,6 +594,7 @@ def main():
                          "persistent launch per step")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
+                             "attn_prefill_ipv",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k", "head_q6k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -610,6 +626,8 @@ def main():
         wl = HeadQ6K(ctx, torch)
     elif args.workload == "attn_prefill":
         wl = AttnPrefill(ctx, torch)
+    elif args.workload == "attn_prefill_ipv":
+        wl = AttnPrefill(ctx, torch, ipv=True)
     elif args.workload == "attn_prefill_sliding":
         wl = AttnPrefill(ctx, torch, window=1024)
     elif args.workload.startswith("attn_decode_"):

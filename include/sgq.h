@@ -100,6 +100,11 @@ typedef struct {
  *   attn_prefill_sliding_ring_q8_hd128
  *       0 q, 1..4 ring K/V pages, 5..8 chunk K/V pages, 9 out, 10 step;
  *       push f32 scale; groups [16, M, 1]  (attn_prefill_sliding_ring.wgsl:28-40)
+ *   kv_append_global_v_q8  (kv_append_global_v_q8.wgsl:19-25)
+ *       0 src fp32, 1 key-blocked scales, 2 quants, 3 step (pos = step[0])
+ *   attn_prefill_global_flash_ipv_hd128  (attn_prefill_global_flash_sp_ipv.wgsl:24-35)
+ *       0 q fp32, 1 k_quants, 2 k_scales, 3 v_quants, 4 key-blocked v_scales,
+ *       5 out, 6 step; push f32 scale; groups [32, ceil(M/16), 1]
  * M (prefill) is the out binding's range / (32·128·4).  The reference's
  * head_dim 256/512 f16-cache variants (attn_decode_sliding, attn_decode_global,
  * attn_decode_global_q8k, attn_reduce_d256/d512, attn_prefill_sliding[_ring],
@@ -245,6 +250,27 @@ int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
  * y; groups [rows]), rope_{sliding,global}_{q,k} and the head_dim-128 forms
  * rope_hd128_{sliding,global}_{q,k} (bindings xs, cos_sin), geglu (gate,
  * up, y), add_scaled (a, b, y; push f32 scale). */
+/* V quantized in 32-KEY blocks per column and appended at rows pos ..
+ * pos+n_tokens-1 (kv_append_global_v_q8, crates/sg-gpu/shaders/
+ * kv_append_global_v_q8.wgsl:32-75): src fp32 [n_tokens × row_len]; quants
+ * [slot × row_len] int8 (the layout of the K pages); scales f16
+ * [slot/32 × row_len], one per (32-key block, column), the kv_quant_q8 rule
+ * over the block's live rows.  pos must be a multiple of 32. */
+int sgq_kv_append_v_q8(sgq_ctx *ctx, const float *src, uint32_t n_tokens, uint32_t row_len,
+                       uint32_t pos, int8_t *v_quants, uint16_t *v_scales);
+/* Prefill attention with int8 PV (attn_prefill_global_flash_sp_ipv,
+ * crates/sg-gpu/shaders/attn_prefill_global_flash_sp_ipv.wgsl:1-20,
+ * :134-210): causal over a linear Q8_0 cache holding positions
+ * 0..q0+n_tokens-1, K pages as sgq_attn_prefill_q8, V quants with the
+ * key-blocked scales of sgq_kv_append_v_q8.  P is quantized per (query,
+ * 32-key block) in the kernel and the softmax denominator sums the
+ * dequantized P; head_dim 128. */
+int sgq_attn_prefill_ipv(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
+                         const uint16_t *k_scales, const int8_t *v_quants,
+                         const uint16_t *v_scales_kb, uint32_t n_tokens, uint32_t q0,
+                         uint32_t n_q_heads, uint32_t n_kv_heads, uint32_t head_dim, float scale,
+                         float *out);
+
 /* rmsnorm.wgsl:24-61: y = x·rsqrt(mean(x²)+eps)·w per row of row_len
  * (w + 1 when plus_one; w NULL = weightless). */
 int sgq_rmsnorm(sgq_ctx *ctx, const float *x, const float *w, float *y, uint32_t rows,

@@ -56,6 +56,9 @@ def lib():
             "sgo_quant_q8_0": (None, [P, SZ, P, P]),
             "sgo_q8_quant_div": (None, [P, SZ, P, P, P]),
             "sgo_q8_quant_v": (None, [P, SZ, SZ, SZ, P, P, P]),
+            "sgo_kv_append_v_q8": (None, [P, SZ, SZ, SZ, P, P]),
+            "sgo_attention_head_ipv": (None, [P, P, P, SZ, SZ, SZ, SZ, SZ, C.c_double, SZ, SZ,
+                                              P]),
             "sgo_dequant_q8_0_f16": (None, [P, P, SZ, P]),
             "sgo_dequant_q8_0": (None, [P, P, SZ, P]),
             "sgo_block_dot_q4_q8": (C.c_int32, [P, P]),
@@ -224,6 +227,23 @@ def q8_quant_v(v, keys, n_kv_heads, head_dim):
     return q, s, d
 
 
+def kv_append_v_q8(src, n_tok, row, pos, quants, scales):
+    """kv_append_global_v_q8.wgsl:32-75 into (quants int8 [slots*row],
+    scales uint16 [slot_blocks*row]), in place."""
+    src = np.ascontiguousarray(src, np.float32)
+    assert quants.flags["C_CONTIGUOUS"] and scales.flags["C_CONTIGUOUS"]
+    assert quants.dtype == np.int8 and scales.dtype == np.uint16
+    assert quants.size >= (pos + n_tok) * row and scales.size >= ((pos + n_tok + 31) // 32) * row
+    lib().sgo_kv_append_v_q8(_p(src), n_tok, row, pos, _p(quants), _p(scales))
+
+
+def dequant_v_keyblocked(quants, scales, keys, row):
+    """Dequantize key-blocked V: x[t, c] = f16 scale[t//32, c] * q[t, c]."""
+    q = np.asarray(quants, np.int8)[:keys * row].reshape(keys, row).astype(np.float32)
+    s = f16_bits_to_f32(np.asarray(scales, np.uint16)[:((keys + 31) // 32) * row]).reshape(-1, row)
+    return (q * s[np.arange(keys) // 32]).astype(np.float32).reshape(-1)
+
+
 def dequant_q8_0(scales, quants) -> np.ndarray:
     scales = np.ascontiguousarray(scales, np.uint16)
     quants = np.ascontiguousarray(quants, np.int8)
@@ -341,6 +361,16 @@ def attention_head(q, k, v, i, qh, n_q_heads, n_kv_heads, head_dim, scale, t0, t
     out = np.empty(head_dim, np.float32)
     lib().sgo_attention_head(_p(q), _p(k), _p(v), i, qh, n_q_heads, n_kv_heads, head_dim,
                              scale, t0, t1, _p(out))
+    return out
+
+
+def attention_head_ipv(q, k, v, i, qh, n_q_heads, n_kv_heads, head_dim, scale, t0, t1):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty(head_dim, np.float32)
+    lib().sgo_attention_head_ipv(_p(q), _p(k), _p(v), i, qh, n_q_heads, n_kv_heads, head_dim,
+                                 scale, t0, t1, _p(out))
     return out
 
 

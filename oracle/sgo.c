@@ -616,6 +616,85 @@ void sgo_attention_head(const float *q, const float *k, const float *v, size_t i
     free(sc);
 }
 
+/* attention_head with the int8-PV quantization of
+ * attn_prefill_global_flash_sp_ipv.wgsl:134-181: P = exp(s - max) is
+ * quantized per 32-KEY block (blocks of absolute key index t/32, restricted
+ * to [t0, t1]): d = amax*(1/127) in f32, id = 1/d, scale f16(d),
+ * q = clamp(round(p*id)), p~ = f16(d)*q; the denominator sums the
+ * dequantized p~ as the numerator does (ipv.wgsl:157-177); V is the
+ * dequantized key-blocked V the kernel multiplies. */
+void sgo_attention_head_ipv(const float *q, const float *k, const float *v, size_t i, size_t qh,
+                            size_t n_q_heads, size_t n_kv_heads, size_t head_dim, double scale,
+                            size_t t0, size_t t1, float *out) {
+    size_t kvh = qh / (n_q_heads / n_kv_heads);
+    const float *qrow = q + (i * n_q_heads + qh) * head_dim;
+    size_t n = t1 - t0 + 1;
+    double *sc = (double *)malloc(n * sizeof(double));
+    double mx = -INFINITY;
+    for (size_t t = t0; t <= t1; t++) {
+        const float *krow = k + (t * n_kv_heads + kvh) * head_dim;
+        double dot = 0.0;
+        for (size_t d = 0; d < head_dim; d++) dot += (double)qrow[d] * (double)krow[d];
+        sc[t - t0] = dot * scale;
+        if (sc[t - t0] > mx) mx = sc[t - t0];
+    }
+    for (size_t j = 0; j < n; j++) sc[j] = (double)(float)exp(sc[j] - mx);
+    const float inv127 = 1.0f / 127.0f;
+    for (size_t b0 = t0 / 32 * 32; b0 <= t1; b0 += 32) {
+        size_t lo = b0 > t0 ? b0 : t0, hi = b0 + 31 < t1 ? b0 + 31 : t1;
+        float amax = 0.0f;
+        for (size_t t = lo; t <= hi; t++) {
+            float p = (float)sc[t - t0];
+            amax = p > amax ? p : amax;
+        }
+        float d = amax * inv127;
+        float id = d > 0.0f ? 1.0f / d : 0.0f;
+        float dd = sgo_f16_to_f32(sgo_f32_to_f16(d));
+        for (size_t t = lo; t <= hi; t++) {
+            int qi = (int)rintf((float)sc[t - t0] * id);
+            if (qi < -128) qi = -128;
+            if (qi > 127) qi = 127;
+            sc[t - t0] = (double)dd * (double)qi;
+        }
+    }
+    double denom = 0.0;
+    for (size_t j = 0; j < n; j++) denom += sc[j];
+    for (size_t d = 0; d < head_dim; d++) {
+        double acc = 0.0;
+        for (size_t t = t0; t <= t1; t++)
+            acc += sc[t - t0] * (double)v[(t * n_kv_heads + kvh) * head_dim + d];
+        out[d] = denom > 0.0 ? (float)(acc / denom) : 0.0f;
+    }
+    free(sc);
+}
+
+/* kv_append_global_v_q8.wgsl:32-75: append n_tok rows of V (fp32 [n_tok x
+ * row], row = n_kv*hd) at positions pos.. (pos a multiple of 32) quantized
+ * in 32-KEY blocks per column: global key block kb = pos/32 + t/32, one f16
+ * scale per (kb, col) into scales[kb*row + col] (d = amax*(1/127), id = 1/d
+ * of the unrounded d, round half to even), quants at [(pos+t)*row + col].
+ * A short final block is quantized over its live rows. */
+void sgo_kv_append_v_q8(const float *src, size_t n_tok, size_t row, size_t pos, int8_t *quants,
+                        uint16_t *scales) {
+    const float inv127 = 1.0f / 127.0f;
+    for (size_t tb = 0; tb * 32 < n_tok; tb++) {
+        size_t k0 = tb * 32, k1 = k0 + 32 < n_tok ? k0 + 32 : n_tok;
+        size_t kb = pos / 32 + tb;
+        for (size_t c = 0; c < row; c++) {
+            float amax = 0.0f;
+            for (size_t t = k0; t < k1; t++) {
+                float a = fabsf(src[t * row + c]);
+                amax = a > amax ? a : amax;
+            }
+            float d = amax * inv127;
+            float id = d > 0.0f ? 1.0f / d : 0.0f;
+            scales[kb * row + c] = sgo_f32_to_f16(d);
+            for (size_t t = k0; t < k1; t++)
+                quants[(pos + t) * row + c] = (int8_t)(int)rintf(src[t * row + c] * id);
+        }
+    }
+}
+
 /* attention (crates/sg-model/src/reference.rs:482-530): causal, optionally
  * windowed GQA over a linear cache; query t sits at q0+t and sees keys
  * [max(0, q0+t+1-window), q0+t]. window == 0 means no window. */

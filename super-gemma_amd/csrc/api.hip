@@ -88,6 +88,8 @@ enum class Kind {
     AttnDecode,    // attn_decode_{sliding,global}_q8_hd128: groups [n_kv, n_splits]
     AttnReduce,    // attn_reduce_d128: groups [n_q]
     AttnPrefill,   // attn_prefill_{global_flash,sliding_ring}_q8_hd128
+    AttnPrefillIpv,  // attn_prefill_global_flash_ipv_hd128 (int8 PV, key-blocked V)
+    AppendVQ8,     // kv_append_global_v_q8 (V in 32-key blocks per column)
 };
 
 struct sgq_kernel {
@@ -120,6 +122,7 @@ const char *const kNames[] = {
     "kv_append_sliding_q8",
     "attn_decode_sliding_q8_hd128", "attn_decode_global_q8_hd128", "attn_reduce_d128",
     "attn_prefill_global_flash_q8_hd128", "attn_prefill_sliding_ring_q8_hd128",
+    "kv_append_global_v_q8", "attn_prefill_global_flash_ipv_hd128",
 };
 
 // The benchmark geometry of the hd128 attention forms (32 query heads over
@@ -214,6 +217,27 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         k->kind = Kind::AppendQ8;
         k->info.bindings = 4;
         k->param = name == "kv_append_sliding_q8" ? kAttnWindow : 0;  // ring slots
+        return true;
+    }
+    if (name == "kv_append_global_v_q8") {
+        // bindings: 0 src fp32 [n_tok × row], 1 scales f16 [block × row],
+        // 2 quants [slot × row], 3 step (pos = step[0], a multiple of 32);
+        // row = groups.y·32 when groups.y > 1, else 2048 (16 kv heads × 128,
+        // also the real checkpoint's 4 global kv heads × 512)
+        k->kind = Kind::AppendVQ8;
+        k->info.bindings = 4;
+        return true;
+    }
+    if (name == "attn_prefill_global_flash_ipv_hd128") {
+        // 0 q fp32 [M × 32 × 128], 1 k_quants, 2 k_scales (Q8_0 pages), 3 v
+        // quants [slot × 16 × 128], 4 v scales key-blocked [slot/32 × 16 ×
+        // 128], 5 out, 6 step; push {scale: f32}; groups [32, ceil(M/16)];
+        // causal, q0 = step[3], keys 0..q0+M-1 in the linear cache
+        // (attn_prefill_global_flash_sp_ipv.wgsl:24-35)
+        k->kind = Kind::AttnPrefillIpv;
+        k->info = {{256, 1, 1}, 7, 4, 0};
+        k->k = kAttnNQ;
+        k->n = kAttnNKv;
         return true;
     }
     if (name == "attn_decode_sliding_q8_hd128" || name == "attn_decode_global_q8_hd128") {
@@ -604,6 +628,43 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                                        static_cast<const uint16_t *>(p2), static_cast<float *>(p3),
                                        m, n, k, split, partials);
         }
+        case Kind::AppendVQ8: {
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)) ||
+                (rc = B.get(3, &p3, &r3)))
+                return rc;
+            const uint32_t row = groups[1] > 1 ? groups[1] * 32 : 2048;
+            if (!r0) return fail(SGQ_ERR_VALIDATION, "kv_append_global_v_q8: src range required");
+            const uint32_t ntok = (uint32_t)(r0 / 4 / row);
+            return launch_kv_append_v_q8(st, static_cast<const float *>(p0),
+                                         static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2),
+                                         static_cast<const uint32_t *>(p3), 0, ntok, row);
+        }
+        case Kind::AttnPrefillIpv: {
+            void *pp[7];
+            uint64_t rr[7];
+            for (uint32_t i = 0; i < 7; i++)
+                if ((rc = B.get(i, &pp[i], &rr[i]))) return rc;
+            const uint32_t nq = kernel->k, nkv = kernel->n;
+            if (!rr[5])
+                return fail(SGQ_ERR_VALIDATION, "%s: out range required (it gives M)",
+                            kernel->name.c_str());
+            const uint64_t m = rr[5] / ((uint64_t)nq * 128 * 4);
+            if (m == 0 || m >= (1u << 30) || rr[5] != m * nq * 128 * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: out range is not a whole number of tokens",
+                            kernel->name.c_str());
+            if (groups[0] != nq || groups[1] != (m + 15) / 16 || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, %llu, 1]",
+                            kernel->name.c_str(), nq, (unsigned long long)((m + 15) / 16));
+            if ((rr[0] && rr[0] < m * nq * 128 * 4) || (rr[6] && rr[6] < 16))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            float scale;
+            std::memcpy(&scale, push, 4);
+            return launch_attn_prefill_ipv(
+                st, static_cast<const float *>(pp[0]), static_cast<const int8_t *>(pp[1]),
+                static_cast<const uint16_t *>(pp[2]), static_cast<const int8_t *>(pp[3]),
+                static_cast<const uint16_t *>(pp[4]), static_cast<float *>(pp[5]), (int)m, 0,
+                (int)nq, (int)nkv, 128, scale, static_cast<const uint32_t *>(pp[6]));
+        }
         case Kind::AttnDecode: {
             void *p5, *p6;
             uint64_t r5, r6;
@@ -813,6 +874,27 @@ int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
     return launch_attn_prefill_q8(ctx->stream, q, k_quants, k_scales, v_quants, v_scales, out,
                                   (int)n_tokens, (int)q0, (int)n_q_heads, (int)n_kv_heads,
                                   (int)head_dim, (int)window, scale);
+}
+
+int sgq_kv_append_v_q8(sgq_ctx *ctx, const float *src, uint32_t n_tokens, uint32_t row_len,
+                       uint32_t pos, int8_t *v_quants, uint16_t *v_scales) {
+    if (!ctx || (n_tokens && (!src || !v_quants || !v_scales)))
+        return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    return launch_kv_append_v_q8(ctx->stream, src, v_scales, v_quants, nullptr, pos, n_tokens,
+                                 row_len);
+}
+
+int sgq_attn_prefill_ipv(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
+                         const uint16_t *k_scales, const int8_t *v_quants,
+                         const uint16_t *v_scales_kb, uint32_t n_tokens, uint32_t q0,
+                         uint32_t n_q_heads, uint32_t n_kv_heads, uint32_t head_dim, float scale,
+                         float *out) {
+    if (!ctx || !q || !k_quants || !k_scales || !v_quants || !v_scales_kb || !out)
+        return fail(SGQ_ERR_VALIDATION, "NULL argument");
+    SGQ_CHECK(n_tokens < (1u << 30) && q0 < (1u << 30), "attn_prefill_ipv: size out of range");
+    return launch_attn_prefill_ipv(ctx->stream, q, k_quants, k_scales, v_quants, v_scales_kb, out,
+                                   (int)n_tokens, (int)q0, (int)n_q_heads, (int)n_kv_heads,
+                                   (int)head_dim, scale, nullptr);
 }
 
 int sgq_rmsnorm(sgq_ctx *ctx, const float *x, const float *w, float *y, uint32_t rows,

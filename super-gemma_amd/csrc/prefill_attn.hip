@@ -53,6 +53,8 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int v4i_p __attribute__((ext_vector_type(4)));
+typedef int v16i_p __attribute__((ext_vector_type(16)));
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -71,13 +73,26 @@ struct KvSource {
     const uint16_t *cks, *cvs;
 };
 
-template <int HPW>
+// IPV (int8 PV, attn_prefill_global_flash_sp_ipv.wgsl): V stays int8 in LDS
+// (transposed, [dim][key]) with its key-blocked scales, P is quantized per
+// (query, 32-key block) and Oᵀ += Vᵀ·Pᵀ runs as one v_mfma_i32_32x32x32_i8
+// per block and 32 dims, rescaled by p_scale ⊗ v_scale; linear cache,
+// causal, no window (tiles start at key 0, so every 32-key MFMA block is a
+// V scale block).
+constexpr int kVRowB = kLT + 16;   // int8 Vᵀ tile row (IPV), padded
+static_assert(kHD * kVRowB + (kLT / 32) * kHD * 4 <= kHD * kVRow * 2, "IPV tiles fit the Vᵀ LDS");
+
+template <int HPW, bool IPV = false>
 __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
     int n_q, int n_kv, int window, float scale, int qtiles, const uint32_t *__restrict__ step) {
     if (step) q0 = (int)step[3];
     __shared__ __align__(16) _Float16 k_s[kLT][kKRow];
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
+    // IPV views of the Vᵀ tile: int8 Vᵀ, then the tile's V scales [block][dim]
+    int8_t(*vt8)[kVRowB] = reinterpret_cast<int8_t(*)[kVRowB]>(&vt_s[0][0]);
+    float(*vsc)[kHD] = reinterpret_cast<float(*)[kHD]>(reinterpret_cast<int8_t *>(&vt_s[0][0]) +
+                                                       kHD * kVRowB);
 
     const int tile = qtiles - 1 - (int)blockIdx.x;  // heaviest (latest) query tile first
     // HPW query heads (of one kv head) share the workgroup and each K/V
@@ -139,7 +154,8 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
                 // byte permute against 0x64, -1152 gives q exactly, and a
                 // packed f16 multiply applies d
                 const _Float16 sk = __builtin_bit_cast(_Float16, ksb[row * (kHD / 32) + blk]);
-                const _Float16 sv = __builtin_bit_cast(_Float16, vsb[row * (kHD / 32) + blk]);
+                const _Float16 sv =
+                    IPV ? (_Float16)1.f : __builtin_bit_cast(_Float16, vsb[row * (kHD / 32) + blk]);
                 const h2 dk = {sk, sk}, dv = {sv, sv};
                 const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
                 const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
@@ -163,8 +179,23 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
                 for (int e = 0; e < 8; e++) t[e] = kv[8 * j + e];
                 *reinterpret_cast<h8 *>(&k_s[kk][32 * blk + 8 * j]) = t;
             }
+            if (IPV) {
+                // the raw quants (exact as f16 with a unit scale), transposed
 #pragma unroll
-            for (int j = 0; j < 32; j++) vt_s[32 * blk + j][kk] = vv[j];
+                for (int j = 0; j < 32; j++) vt8[32 * blk + j][kk] = (int8_t)(int)(float)vv[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 32; j++) vt_s[32 * blk + j][kk] = vv[j];
+            }
+        }
+        if (IPV) {  // the tile's key-blocked V scales, [block][dim]
+            for (int t = tid; t < (kLT / 32) * kHD; t += 256 * HPW) {
+                const int b = t / kHD, dim = t % kHD;
+                const int key0 = kl + 32 * b;
+                vsc[b][dim] = key0 <= k_hi
+                                  ? f16_bits_to_f32(src.vs[((size_t)(key0 / 32) * n_kv + kvh) * kHD + dim])
+                                  : 0.f;
+            }
         }
         __syncthreads();
 
@@ -200,15 +231,49 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         const float corr = __expf(m_run - mx);
         float rs = 0.f;
         h8 pb[2][2];
+        v4i_p pq[2];     // IPV: P quants of block t2 (K order: this lane's 16 keys)
+        float pd[2];     // IPV: their f16-rounded scale
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
+        for (int t2 = 0; t2 < 2; t2++) {
+            float pf[16];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float v = s[t2][i];
-                const float p = v > kNegBig ? __expf(v - mx) : 0.f;
-                rs += p;
-                pb[t2][i / 8][i % 8] = (_Float16)p;
+                pf[i] = v > kNegBig ? __expf(v - mx) : 0.f;
             }
+            if (!IPV) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    rs += pf[i];
+                    pb[t2][i / 8][i % 8] = (_Float16)pf[i];
+                }
+            } else {
+                // Q8 of P over the block's 32 keys (16 here, 16 in lane ^ 32):
+                // d = amax/127, q = round(p/d), the denominator sums f16(d)·q
+                // (attn_prefill_global_flash_sp_ipv.wgsl:157-177)
+                float amax = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) amax = fmaxf(amax, pf[i]);
+                amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+                const float dq = amax * (1.0f / 127.0f);
+                const float id = dq > 0.f ? 1.0f / dq : 0.f;
+                const float dd = f16_bits_to_f32(f32_to_f16_bits(dq));
+                int qs = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int qi = min(127, (int)__builtin_rintf(pf[4 * j + e] * id));
+                        qs += qi;
+                        w |= (uint32_t)(qi & 0xff) << (8 * e);
+                    }
+                    pq[t2][j] = (int)w;
+                }
+                pd[t2] = dd;
+                rs += dd * (float)qs;
+            }
+        }
         rs += __shfl_xor(rs, 32, kWave);
         l_run = l_run * corr + rs;
         m_run = mx;
@@ -216,6 +281,36 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         for (int d = 0; d < 4; d++)
 #pragma unroll
             for (int i = 0; i < 16; i++) o[d][i] *= corr;
+        if (IPV) {
+            // Oᵀ += Vᵀ·Pᵀ per 32-key block: A row = dim 32d + l32 with this
+            // lane's keys 8j + 4hh .. +3 (j = 0..3, the order of pq), B column =
+            // this lane's query; then ×(v_scale[dim]·p_scale)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++) {
+                const int kbase = ko + 32 * t2;
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const int8_t *vr = &vt8[32 * d + l32][kbase + 4 * hh];
+                    const v4i_p a = {*reinterpret_cast<const int *>(vr),
+                                     *reinterpret_cast<const int *>(vr + 8),
+                                     *reinterpret_cast<const int *>(vr + 16),
+                                     *reinterpret_cast<const int *>(vr + 24)};
+                    const v16i_p dot =
+                        __builtin_amdgcn_mfma_i32_32x32x32_i8(a, pq[t2], v16i_p{}, 0, 0, 0);
+                    const float *vs_row = &vsc[kbase / 32][32 * d + 4 * hh];
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const float4 sv = *reinterpret_cast<const float4 *>(vs_row + 8 * g);
+                        const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            o[d][4 * g + e] = __builtin_fmaf((float)dot[4 * g + e], svv[e] * pd[t2],
+                                                             o[d][4 * g + e]);
+                    }
+                }
+            }
+            continue;
+        }
         // Oᵀ += Vᵀ·Pᵀ: key chunk (t2, half) = keys 32t2 + 16half + {4hh..+3, 8+4hh..+3}
 #pragma unroll
         for (int d = 0; d < 4; d++)
@@ -242,6 +337,28 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
 }
 
 }  // namespace
+
+int launch_attn_prefill_ipv(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
+                            const int8_t *vq, const uint16_t *vs_kb, float *out, int n_tok, int q0,
+                            int n_q, int n_kv, int head_dim, float scale, const uint32_t *step) {
+    SGQ_CHECK(head_dim == kHD, "attn_prefill_ipv: head_dim %d unsupported (128)", head_dim);
+    SGQ_CHECK(n_tok > 0 && q0 >= 0, "attn_prefill_ipv: n_tok %d, q0 %d", n_tok, q0);
+    SGQ_CHECK(n_kv > 0 && n_q > 0 && n_q % n_kv == 0, "attn_prefill_ipv: n_q %% n_kv != 0");
+    SGQ_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 &&
+                  ((uintptr_t)ks & 1) == 0 && ((uintptr_t)vs_kb & 1) == 0,
+              "attn_prefill_ipv: misaligned operand");
+    const int qtiles = (n_tok + kQT - 1) / kQT;
+    const KvSource src{kq, vq, ks, vs_kb, 0, nullptr, nullptr, nullptr, nullptr};
+    const int qpk = n_q / n_kv;
+    if (kPrefillPairHeads && qpk % 2 == 0)
+        hipLaunchKernelGGL((attn_prefill_kernel<2, true>), dim3(qtiles, n_q / 2), dim3(512), 0, st,
+                           q, src, out, n_tok, q0, n_q, n_kv, 0, scale, qtiles, step);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<1, true>), dim3(qtiles, n_q), dim3(256), 0, st, q,
+                           src, out, n_tok, q0, n_q, n_kv, 0, scale, qtiles, step);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
 
 int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
                            const int8_t *vq, const uint16_t *vs, float *out, int n_tok, int q0,

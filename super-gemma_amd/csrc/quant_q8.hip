@@ -78,6 +78,34 @@ __global__ __launch_bounds__(kQWG) void kv_append_q8_kernel(const float4 *__rest
     }
 }
 
+// Key-blocked V append (kv_append_global_v_q8.wgsl:32-75): thread (key
+// block tb, column c) quantizes column c over the block's live rows with the
+// kv_quant_q8 rule and writes scale (pos/32 + tb, c) and the block's quants
+// at rows pos + t.  Neighbouring threads take neighbouring columns, so every
+// load and store is coalesced across the wave.
+__global__ __launch_bounds__(kQWG) void kv_append_v_q8_kernel(const float *__restrict__ src,
+                                                              uint16_t *__restrict__ scales,
+                                                              int8_t *__restrict__ quants,
+                                                              const uint32_t *__restrict__ step,
+                                                              uint32_t pos_direct,
+                                                              uint32_t n_tok, uint32_t row) {
+    const uint32_t pos = step ? step[0] : pos_direct;
+    const uint64_t n_items = (uint64_t)((n_tok + 31) / 32) * row;
+    for (uint64_t i = (uint64_t)blockIdx.x * kQWG + threadIdx.x; i < n_items;
+         i += (uint64_t)gridDim.x * kQWG) {
+        const uint32_t tb = (uint32_t)(i / row), c = (uint32_t)(i % row);
+        const uint32_t k0 = 32 * tb, k1 = min(k0 + 32u, n_tok);
+        float amax = 0.f;
+        for (uint32_t t = k0; t < k1; t++) amax = fmaxf(amax, fabsf(src[(size_t)t * row + c]));
+        const float d = amax * (1.0f / 127.0f);
+        const float id = d > 0.f ? 1.0f / d : 0.f;
+        scales[(size_t)(pos / 32 + tb) * row + c] = f32_to_f16_bits(d);
+        for (uint32_t t = k0; t < k1; t++)
+            quants[(size_t)(pos + t) * row + c] =
+                (int8_t)(int)__builtin_rintf(src[(size_t)t * row + c] * id);
+    }
+}
+
 int grid_for(uint64_t n4) {
     uint64_t g = (n4 + kQWG - 1) / kQWG;
     const uint64_t cap = (uint64_t)device_info().cus * 8;
@@ -125,6 +153,19 @@ int launch_kv_append_q8(hipStream_t st, const float *src, uint16_t *scales, int8
     hipLaunchKernelGGL(kv_append_q8_kernel, dim3(grid_for(n4)), dim3(kQWG), 0, st,
                        reinterpret_cast<const float4 *>(src), scales,
                        reinterpret_cast<int *>(quants), step, n4, row_len / 4, ring);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_kv_append_v_q8(hipStream_t st, const float *src, uint16_t *scales, int8_t *quants,
+                          const uint32_t *step, uint32_t pos, uint32_t n_tokens, uint32_t row_len) {
+    SGQ_CHECK(row_len > 0, "kv_append_v_q8: empty row");
+    SGQ_CHECK(step != nullptr || pos % 32 == 0,
+              "kv_append_v_q8: pos %u must be a multiple of 32 (32-key blocks)", pos);
+    if (n_tokens == 0) return SGQ_OK;
+    const uint64_t items = (uint64_t)((n_tokens + 31) / 32) * row_len;
+    hipLaunchKernelGGL(kv_append_v_q8_kernel, dim3(grid_for(items)), dim3(kQWG), 0, st, src, scales,
+                       quants, step, pos, n_tokens, row_len);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }

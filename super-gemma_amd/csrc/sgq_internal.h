@@ -126,6 +126,17 @@ int launch_dequant_q8_0(hipStream_t st, const uint16_t *scales, const int8_t *qu
 int launch_kv_append_q8(hipStream_t st, const float *src, uint16_t *scales, int8_t *quants,
                         const uint32_t *step, uint32_t n_tokens, uint32_t row_len,
                         uint32_t ring);
+// V quantized in 32-KEY blocks per column (kv_append_global_v_q8.wgsl):
+// rows [n_tokens × row_len] appended at pos (step[0] when step is given;
+// a multiple of 32), scales [block × row_len] f16.
+int launch_kv_append_v_q8(hipStream_t st, const float *src, uint16_t *scales, int8_t *quants,
+                          const uint32_t *step, uint32_t pos, uint32_t n_tokens, uint32_t row_len);
+// Prefill attention with int8 PV (attn_prefill_global_flash_sp_ipv.wgsl):
+// causal over a linear Q8_0 cache with key-blocked V scales vs_kb
+// [ceil(keys/32) × n_kv × 128]; q0 from step[3] when step is given.
+int launch_attn_prefill_ipv(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
+                            const int8_t *vq, const uint16_t *vs_kb, float *out, int n_tok, int q0,
+                            int n_q, int n_kv, int head_dim, float scale, const uint32_t *step);
 int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
                         float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
                         float *partials);

@@ -108,6 +108,8 @@ SIGNATURES = {
     "sgq_buf_download": (I, [P, P, P, U64]),
     "sgq_buf_fill_zero": (I, [P, P, U64]),
     "sgq_gemv_q4_0_noalloc": (I, [P, P, P, P, U32, U32]),
+    "sgq_kv_append_v_q8": (I, [P, P, U32, U32, U32, P, P]),
+    "sgq_attn_prefill_ipv": (I, [P, P, P, P, P, P, U32, U32, U32, U32, U32, C.c_float, P]),
     "sgq_kernel_lookup": (I, [P, C.c_char_p, C.POINTER(P), C.POINTER(_Info)]),
     "sgq_kernel_count": (U32, []),
     "sgq_kernel_name": (C.c_char_p, [U32]),
@@ -369,6 +371,30 @@ class GpuContext:
             scale = 1.0 / head_dim ** 0.5
         _check(lib().sgq_attn_decode_q8(self._h, _ptr(q), _ptr(kq), _ptr(ks), _ptr(vq), _ptr(vs),
                                         kv_len, n_q, n_kv, head_dim, n_splits, scale, _ptr(out)))
+
+    def kv_append_v_q8(self, src, n_tok, row, pos, vq, vs):
+        """Key-blocked V append (sgq_kv_append_v_q8)."""
+        _need(src, torch.float32, n_tok * row, "src")
+        _need(vq, torch.int8, (pos + n_tok) * row, "v_quants")
+        _need(vs, (torch.uint16, torch.int16, torch.float16), ((pos + n_tok + 31) // 32) * row,
+              "v_scales")
+        _check(lib().sgq_kv_append_v_q8(self._h, _ptr(src), n_tok, row, pos, _ptr(vq), _ptr(vs)))
+
+    def attn_prefill_ipv(self, q, kq, ks, vq, vs_kb, n_tok, q0, n_q, n_kv, out, scale=None,
+                         head_dim=128):
+        """Causal prefill attention with int8 PV over a linear cache of
+        positions 0..q0+n_tok-1 (V scales key-blocked)."""
+        n_slots = q0 + n_tok
+        _need(q, torch.float32, n_tok * n_q * head_dim, "q")
+        _need(out, torch.float32, n_tok * n_q * head_dim, "out")
+        _need(kq, torch.int8, n_slots * n_kv * head_dim, "k_quants")
+        _need(vq, torch.int8, n_slots * n_kv * head_dim, "v_quants")
+        _need(vs_kb, (torch.uint16, torch.int16, torch.float16),
+              ((n_slots + 31) // 32) * n_kv * head_dim, "v_scales")
+        sc = 1.0 / head_dim ** 0.5 if scale is None else scale
+        _check(lib().sgq_attn_prefill_ipv(self._h, _ptr(q), _ptr(kq), _ptr(ks), _ptr(vq),
+                                          _ptr(vs_kb), n_tok, q0, n_q, n_kv, head_dim, sc,
+                                          _ptr(out)))
 
     def attn_prefill_q8(self, q, kq, ks, vq, vs, n_tok, q0, n_q, n_kv, out, window=0,
                         scale=None, head_dim=128):

@@ -393,3 +393,76 @@ def test_q6_k_logits_oracle_matches_numpy(oracle):
     want = 30.0 * np.tanh((deq @ x.astype(np.float64)) / 30.0)
     assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
     assert (w.reshape(n, stride)[:, 4410:] == 0).all()
+
+
+# --- int8 PV: key-blocked V append and block-quantized P ----------------------
+def test_kv_append_v_q8_is_quant_q8_0_per_key_block_column(oracle):
+    """kv_append_global_v_q8.wgsl:32-75: every (32-key block, column) is the
+    kv_quant_q8 rule (quant_q8_0, pinned above) over that column's live keys,
+    placed at key-block pos/32 + t/32; the quants keep the [key x row]
+    layout; a short final block covers its live keys (q8_quant_v layout,
+    mod.rs:98-134)."""
+    rng = oracle.Rng(0xA7E)
+    n_tok, row, pos = 45, 64, 64
+    src = oracle.through_f16(rng.f32_vec(n_tok * row))
+    slots = pos + n_tok + 19
+    quants = np.zeros(slots * row, np.int8)
+    scales = np.zeros(((slots + 31) // 32) * row, np.uint16)
+    oracle.kv_append_v_q8(src, n_tok, row, pos, quants, scales)
+    x = src.reshape(n_tok, row)
+    qq = quants.reshape(slots, row)
+    ss = scales.reshape(-1, row)
+    for c in (0, 5, 63):
+        for tb in range(2):
+            seg = x[tb * 32:(tb + 1) * 32, c]
+            pad = np.zeros(32, np.float32)
+            pad[:len(seg)] = seg
+            s2, q2 = oracle.quant_q8_0(pad)
+            assert ss[pos // 32 + tb, c] == s2.reshape(-1)[0]
+            assert np.array_equal(qq[pos + tb * 32:pos + tb * 32 + len(seg), c], q2.reshape(-1)[:len(seg)])
+    assert not qq[:pos].any() and not qq[pos + n_tok:].any()
+    assert not ss[:pos // 32].any()
+    # same layout as q8_quant_v wherever the division and multiply scale rules agree
+    qv, sv, _ = oracle.q8_quant_v(src, n_tok, 1, row)
+    agree = sv.reshape(-1, row) == ss[pos // 32:pos // 32 + 2]
+    assert agree.mean() > 0.9
+    deq = oracle.dequant_v_keyblocked(quants[pos * row:], scales[(pos // 32) * row:], n_tok, row)
+    assert np.allclose(deq.reshape(n_tok, row), x, atol=np.abs(x).max() / 127)
+
+
+def test_attention_ipv_kats_and_bound(oracle):
+    """Block-quantized P (attn_prefill_global_flash_sp_ipv.wgsl:134-181):
+    identical keys -> every p is 1 -> q = 127 everywhere -> the mean of V, as
+    the exact softmax (reference.rs:572-586); one dominant key per block and
+    the others at p ~ 1e-3 -> those round to q = 0 and vanish from numerator
+    AND denominator (the reference sums the dequantized P), so the output is
+    the dominant key's V exactly; random inputs stay within the quantization
+    bound of the exact softmax."""
+    hd, n = 32, 64
+    k = np.zeros(n * hd, np.float32)
+    v = np.tile(np.arange(n, dtype=np.float32)[:, None] * 0.25, (1, hd)).reshape(-1)
+    q = np.ones(hd, np.float32)
+    out = oracle.attention_head_ipv(q, k, v, 0, 0, 1, 1, hd, 0.1, 0, n - 1)
+    assert np.allclose(out, v.reshape(n, hd)[:, 0].mean(), rtol=1e-6)
+    # window of 40 keys across two blocks (8..47): blocks restricted to the window
+    out = oracle.attention_head_ipv(q, k, v, 0, 0, 1, 1, hd, 0.1, 8, 47)
+    assert np.allclose(out, v.reshape(n, hd)[8:48, 0].mean(), rtol=1e-6)
+    # dominant key: scores 0 for key 5, log(1e-3) for the rest of its block
+    k2 = np.zeros((32, hd), np.float32)
+    q2 = np.zeros(hd, np.float32)
+    q2[0] = 1.0
+    k2[:, 0] = np.float32(np.log(1e-3))
+    k2[5, 0] = 0.0
+    v2 = (np.arange(32 * hd, dtype=np.float32) % 7).reshape(32, hd)
+    out = oracle.attention_head_ipv(q2, k2.reshape(-1), v2.reshape(-1), 0, 0, 1, 1, hd, 1.0, 0, 31)
+    assert np.array_equal(out, v2[5])
+    exact = oracle.attention_head(q2, k2.reshape(-1), v2.reshape(-1), 0, 0, 1, 1, hd, 1.0, 0, 31)
+    assert np.abs(exact - v2[5]).max() > 1e-3
+    # random: within ~1/127 of max|v| of the exact softmax
+    rng = oracle.Rng(0x1B7)
+    L, nq, nkv, hd = 200, 4, 2, 64
+    qr, kr, vr = rng.f32_vec(nq * hd), rng.f32_vec(L * nkv * hd), rng.f32_vec(L * nkv * hd)
+    for h in range(nq):
+        a = oracle.attention_head_ipv(qr, kr, vr, 0, h, nq, nkv, hd, 0.125, 0, L - 1)
+        b = oracle.attention_head(qr, kr, vr, 0, h, nq, nkv, hd, 0.125, 0, L - 1)
+        assert 0 < np.abs(a - b).max() <= np.abs(vr).max() / 127
