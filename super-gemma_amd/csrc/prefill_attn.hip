@@ -87,8 +87,10 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
     int n_q, int n_kv, int window, float scale, int qtiles, const uint32_t *__restrict__ step) {
     if (step) q0 = (int)step[3];
-    __shared__ __align__(16) _Float16 k_s[kLT][kKRow];
+    // Vᵀ first: its reads (32 per compute tile) then address with immediate
+    // offsets below 64 KiB
     __shared__ __align__(16) _Float16 vt_s[kHD][kVRow];
+    __shared__ __align__(16) _Float16 k_s[kLT][kKRow];
     // IPV views of the Vᵀ tile: int8 Vᵀ, then the tile's V scales [block][dim]
     int8_t(*vt8)[kVRowB] = reinterpret_cast<int8_t(*)[kVRowB]>(&vt_s[0][0]);
     float(*vsc)[kHD] = reinterpret_cast<float(*)[kHD]>(reinterpret_cast<int8_t *>(&vt_s[0][0]) +
@@ -106,6 +108,9 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
     const int my_q = tile * kQT + wave * 32 + l32;
     const bool q_valid = my_q < n_tok;
     const int qp = q0 + my_q;  // its position
+    // scores come out of the MFMA in log2 units: q carries scale·log2(e),
+    // so the softmax exponentials are plain exp2 (v_exp_f32)
+    const float qscale = scale * 1.44269504088896341f;
     h8 qb[8];
     {
         const float *qr = q + ((size_t)(q_valid ? my_q : 0) * n_q + qh) * kHD + 8 * hh;
@@ -115,7 +120,7 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
             const float4 b = *reinterpret_cast<const float4 *>(qr + 16 * c + 4);
             const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] : 0.f);
+            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] * qscale : 0.f);
         }
     }
     f32x16 o[4];
@@ -206,41 +211,74 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         // Sᵀ = K·Qᵀ for the tile's two 32-key halves
         f32x16 s[2];
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++) {
+        for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
             for (int i = 0; i < 16; i++) s[t2][i] = 0.f;
+        // the two halves' MFMA chains interleaved: consecutive MFMAs independent
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
+        for (int c = 0; c < 8; c++)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++) {
                 const h8 a = *reinterpret_cast<const h8 *>(&k_s[ko + 32 * t2 + l32][16 * c + 8 * hh]);
                 s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], s[t2], 0, 0, 0);
             }
-        }
-        // mask, scale and the online softmax for this lane's query
+        // mask and the online softmax for this lane's query.  A tile whose
+        // keys all precede the wave's first query (and, with a window, all
+        // lie inside the last query's window) needs no mask: the test is
+        // wave-uniform, and keys past the chunk's end (zero rows of the last
+        // LDS tile) never pass it.
+        const int wq_lo = q0 + tile * kQT + wave * 32;
+        const bool full = kb + kKT - 1 <= wq_lo && (window <= 0 || kb > wq_lo + 31 - window);
         float mx = m_run;
+        if (full) {
 #pragma unroll
-        for (int t2 = 0; t2 < 2; t2++)
+            for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int key = kb + 32 * t2 + 8 * (i / 4) + 4 * hh + (i % 4);
-                const bool ok = q_valid && key <= qp && (window <= 0 || key > qp - window);
-                const float v = ok ? s[t2][i] * scale : kNegBig;
-                s[t2][i] = v;
-                mx = fmaxf(mx, v);
-            }
+                for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[t2][i]);
+        } else {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = kb + 32 * t2 + 8 * (i / 4) + 4 * hh + (i % 4);
+                    const bool ok = q_valid && key <= qp && (window <= 0 || key > qp - window);
+                    const float v = ok ? s[t2][i] : kNegBig;
+                    s[t2][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float corr = __expf(m_run - mx);
+        // lazy rescale: the reference max moves only when the tile's max
+        // exceeds it by more than 2^8 (p <= 256, exact in f16's range), so
+        // the accumulator's rescale is usually skipped; the normalisation by
+        // l at the end is unchanged (same reference max in numerator and
+        // denominator)
+        if (!(mx > m_run + 8.0f)) mx = m_run;
+        const float corr = __builtin_amdgcn_exp2f(m_run - mx);
         float rs = 0.f;
         h8 pb[2][2];
         v4i_p pq[2];     // IPV: P quants of block t2 (K order: this lane's 16 keys)
         float pd[2];     // IPV: their f16-rounded scale
+        // p = 2^(s - max); masked scores give 0 (a lane whose keys so far are
+        // all masked has mx = kNegBig, where 2^(s - mx) alone would give 1)
+        float pfa[2][16];
+        if (full) {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) pfa[t2][i] = __builtin_amdgcn_exp2f(s[t2][i] - mx);
+        } else {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float v = s[t2][i];
+                    pfa[t2][i] = v > kNegBig ? __builtin_amdgcn_exp2f(v - mx) : 0.f;
+                }
+        }
 #pragma unroll
         for (int t2 = 0; t2 < 2; t2++) {
-            float pf[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float v = s[t2][i];
-                pf[i] = v > kNegBig ? __expf(v - mx) : 0.f;
-            }
+            const float(&pf)[16] = pfa[t2];
             if (!IPV) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
@@ -277,10 +315,12 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         rs += __shfl_xor(rs, 32, kWave);
         l_run = l_run * corr + rs;
         m_run = mx;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
 #pragma unroll
-        for (int d = 0; d < 4; d++)
+            for (int d = 0; d < 4; d++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) o[d][i] *= corr;
+                for (int i = 0; i < 16; i++) o[d][i] *= corr;
+        }
         if (IPV) {
             // Oᵀ += Vᵀ·Pᵀ per 32-key block: A row = dim 32d + l32 with this
             // lane's keys 8j + 4hh .. +3 (j = 0..3, the order of pq), B column =
@@ -312,12 +352,13 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
             continue;
         }
         // Oᵀ += Vᵀ·Pᵀ: key chunk (t2, half) = keys 32t2 + 16half + {4hh..+3, 8+4hh..+3}
+        // dim tiles innermost: consecutive MFMAs accumulate into different o[d]
 #pragma unroll
-        for (int d = 0; d < 4; d++)
+        for (int t2 = 0; t2 < 2; t2++)
 #pragma unroll
-            for (int t2 = 0; t2 < 2; t2++)
+            for (int half = 0; half < 2; half++)
 #pragma unroll
-                for (int half = 0; half < 2; half++) {
+                for (int d = 0; d < 4; d++) {
                     const _Float16 *vr = &vt_s[32 * d + l32][ko + 32 * t2 + 16 * half + 4 * hh];
                     const h4 lo = *reinterpret_cast<const h4 *>(vr);
                     const h4 hi = *reinterpret_cast<const h4 *>(vr + 8);

@@ -9,7 +9,9 @@
 //              into fp32 accumulators: the ceiling of any kernel that
 //              rescales every block's exact i32 dot on the VALU;
 //      mode 2  mode 1 plus the v_mfma_f32_32x32x16_f16 that forms the
-//              block's d_a x d_w scale outer product (the MMQ's structure).
+//              block's d_a x d_w scale outer product (the MMQ's structure);
+//      mode 3  the block dot on the f16 matrix cores (exact), the scale
+//              MFMA and one FMA per output element, software-pipelined.
 //    Ops counted: 2*32*32*32 per int8 MFMA.
 //  * sgqp_hbm_read: a streaming read of a large buffer (16-byte loads,
 //    grid-stride), summed so that nothing is elided: the achievable HBM
@@ -23,6 +25,39 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// mode 3: the block dot on the f16 matrix cores (int8 and q-8 values are
+// exact f16 integers, a 32-term dot is exact in the f32 accumulator: two
+// v_mfma_f32_32x32x16_f16 per block), the scale MFMA, and one FMA per output
+// element; the MFMAs of block b+1 are issued before block b's FMAs.
+__global__ __launch_bounds__(256) void mfma_f16dot_probe_kernel(int iters, int *__restrict__ out) {
+    const int t = threadIdx.x;
+    const h8 a0 = __builtin_bit_cast(h8, v4i{0x3c003c00 + t, 0x40004000, 0x3c00bc00, t});
+    const h8 a1 = __builtin_bit_cast(h8, v4i{0x3c00 + t, 0x4000, 0xbc00, t * 3});
+    const h8 sa = __builtin_bit_cast(h8, v4i{0x3c00 + (t & 7), 0, 0, 0});
+    const h8 sb = __builtin_bit_cast(h8, v4i{0x3800 + (t & 3), 0, 0, 0});
+    const f32x16 fzero = {};
+    f32x16 acc0 = {}, acc1 = {};
+    f32x16 d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, a1, fzero, 0, 0, 0);
+    d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, a0, d0, 0, 0, 0);
+    f32x16 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, sb, fzero, 0, 0, 0);
+    for (int i = 0; i < iters; i++) {
+        f32x16 d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, a0, fzero, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, a1, d1, 0, 0, 0);
+        const f32x16 s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sb, sa, fzero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc0[q] = __builtin_fmaf(d0[q], s0[q], acc0[q]);
+        d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, a1, fzero, 0, 0, 0);
+        d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, a0, d0, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, sb, fzero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc1[q] = __builtin_fmaf(d1[q], s1[q], acc1[q]);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) s += acc0[q] + acc1[q];
+    out[blockIdx.x * blockDim.x + t] = __float_as_int(s);
+}
 
 template <int MODE>
 __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int *__restrict__ out) {
@@ -103,6 +138,8 @@ int sgqp_mfma(void *stream, int mode, int blocks, int iters, int *out) {
         hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(blocks), dim3(256), 0, st, iters, out);
     else if (mode == 2)
         hipLaunchKernelGGL(mfma_probe_kernel<2>, dim3(blocks), dim3(256), 0, st, iters, out);
+    else if (mode == 3)
+        hipLaunchKernelGGL(mfma_f16dot_probe_kernel, dim3(blocks), dim3(256), 0, st, iters, out);
     else
         return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
@@ -111,7 +148,7 @@ int sgqp_mfma(void *stream, int mode, int blocks, int iters, int *out) {
 // Int8 MFMAs one launch of sgqp_mfma issues (for the ops count).
 long long sgqp_mfma_count(int mode, int blocks, int iters) {
     const long long waves = (long long)blocks * 4;
-    return waves * iters * (mode == 0 ? 4 : 2);
+    return waves * iters * (mode == 0 ? 4 : 2);  // mode 3: 2 blocks of 32x32x32 per iteration
 }
 
 // Reads `bytes` (a multiple of 16, 16-byte aligned) from `buf`; out:

@@ -11,8 +11,9 @@ flash_sp_ipv: q0 in {0, 200}, Q8 K, key-blocked V from q8_quant_v) and
   and K to f16 for QK (as the f16-PV prefill) and quantizes P against the
   running max (the oracle: the final max), so a block's f16 P scale may round
   differently (2^-11): bar |err| <= 2e-3*|want| + 2e-3*max|want| and
-  normwise 2e-3, with the oracle's q and K rounded to f16 as the kernel's
-  QK operands are (P's quantization turns score noise into whole steps).  Against the full-precision softmax the P quantization
+  normwise 2e-3, with the oracle's q (times scale·log2(e), the kernel's
+  score units) and K rounded to f16 as the kernel's QK operands are (P's
+  quantization turns score noise into whole steps).  Against the full-precision softmax the P quantization
   itself costs up to ~1/127 of max|v| (the reference bounds its own kernel
   at 4e-2 absolute); that error is printed, not asserted.
 """
@@ -77,7 +78,11 @@ def _want(oracle, q, kd, vd, rows, q0, n_q, n_kv, scale, ipv=True):
     oracle must see the same scores, not just close ones."""
     f = oracle.attention_head_ipv if ipv else oracle.attention_head
     if ipv:
-        q, kd = oracle.through_f16(q), oracle.through_f16(kd)
+        # the kernel rounds q·scale·log2(e) to f16 (its scores are in log2
+        # units); the same rounding, undone in f32, gives the oracle its q
+        c = np.float32(scale) * np.float32(1.44269504088896341)
+        q = (oracle.through_f16(np.asarray(q, np.float32) * c) / c).astype(np.float32)
+        kd = oracle.through_f16(kd)
     out = np.empty((len(rows), n_q, HD), np.float32)
     for r, i in enumerate(rows):
         for h in range(n_q):
