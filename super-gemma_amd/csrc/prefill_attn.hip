@@ -46,7 +46,13 @@ constexpr int kKT = 64;            // keys per compute tile
 constexpr int kSub = SGQ_PF_SUBTILES;  // compute tiles per LDS tile (per barrier pair)
 constexpr int kLT = kSub * kKT;       // keys per LDS tile
 constexpr int kKRow = kHD + 8;     // K tile row in LDS (f16), padded
-constexpr int kVRow = kLT + 8;     // Vᵀ tile row in LDS (f16), padded
+// Vᵀ tile row in LDS (f16): 130 dwords, so the 32 rows one PV read spans
+// start 2 banks apart (conflict-free 8-byte reads).  Columns are swizzled in
+// units of 4 keys (8 bytes): unit u of a row of dim block b is stored at
+// u ^ 8b, so the four blocks' row writes of one key range (the rows 32b + j
+// share their bank offset) land on disjoint banks.
+constexpr int kVRow = kLT + 4;
+__device__ __forceinline__ int vt_col(int key, int b) { return ((key >> 2) ^ (8 * b)) * 4 + (key & 3); }
 constexpr float kNegBig = -3.0e38f;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -137,60 +143,76 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
 
     for (int kl = k_lo; kl <= k_hi; kl += kLT) {
         __syncthreads();  // the previous tile's LDS reads are done
-        // dequantize K and V of keys kl..kl+127: thread -> (key t/4, 32-block t%4)
-        for (int t = tid; t < kLT * 4; t += 256 * HPW) {
-            const int kk = t >> 2, blk = t & 3;
-            const int key = kl + kk;
-            _Float16 kv[32], vv[32];
-            if (key <= k_hi) {
-                const bool fresh = src.ckq != nullptr && key >= q0;
-                const int slot = fresh ? key - q0 : src.ring ? key % src.ring : key;
-                const size_t row = (size_t)slot * n_kv + kvh;
-                const int8_t *kqb = fresh ? src.ckq : src.kq;
-                const int8_t *vqb = fresh ? src.cvq : src.vq;
-                const uint16_t *ksb = fresh ? src.cks : src.ks;
-                const uint16_t *vsb = fresh ? src.cvs : src.vs;
-                const i32x4 *kp = reinterpret_cast<const i32x4 *>(kqb + row * kHD + 32 * blk);
-                const i32x4 *vp = reinterpret_cast<const i32x4 *>(vqb + row * kHD + 32 * blk);
-                const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
-                // q·d in f16 with one rounding, as (f16)(d·q) in f32 (the
-                // product of an int8 and an f16 is exact in both): four
-                // quants at a time become the f16 pairs 1024 + (q + 128) by a
-                // byte permute against 0x64, -1152 gives q exactly, and a
-                // packed f16 multiply applies d
-                const _Float16 sk = __builtin_bit_cast(_Float16, ksb[row * (kHD / 32) + blk]);
-                const _Float16 sv =
-                    IPV ? (_Float16)1.f : __builtin_bit_cast(_Float16, vsb[row * (kHD / 32) + blk]);
-                const h2 dk = {sk, sk}, dv = {sv, sv};
-                const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-                const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        // dequantize K and V of the tile's keys: thread -> (key pair t/4,
+        // 32-block t%4): four lanes read a key's whole 128-byte row, and a
+        // Vᵀ row write packs both keys of the pair into one dword (16
+        // consecutive dwords per block, the blocks 8 dwords apart)
+        for (int t = tid; t < kLT * 2; t += 256 * HPW) {
+            const int blk = t & 3, pair = t >> 2;
+            uint32_t vpk[32];
 #pragma unroll
-                for (int w = 0; w < 8; w++) {
-                    const h2 k01 = i8_pair_f16((uint32_t)kw[w], 0x04010400u) * dk;
-                    const h2 k23 = i8_pair_f16((uint32_t)kw[w], 0x04030402u) * dk;
-                    const h2 v01 = i8_pair_f16((uint32_t)vw[w], 0x04010400u) * dv;
-                    const h2 v23 = i8_pair_f16((uint32_t)vw[w], 0x04030402u) * dv;
-                    kv[4 * w] = k01[0], kv[4 * w + 1] = k01[1], kv[4 * w + 2] = k23[0], kv[4 * w + 3] = k23[1];
-                    vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+            for (int e = 0; e < 2; e++) {
+                const int kk = 2 * pair + e;
+                const int key = kl + kk;
+                _Float16 kv[32], vv[32];
+                if (key <= k_hi) {
+                    const bool fresh = src.ckq != nullptr && key >= q0;
+                    const int slot = fresh ? key - q0 : src.ring ? key % src.ring : key;
+                    const size_t row = (size_t)slot * n_kv + kvh;
+                    const int8_t *kqb = fresh ? src.ckq : src.kq;
+                    const int8_t *vqb = fresh ? src.cvq : src.vq;
+                    const uint16_t *ksb = fresh ? src.cks : src.ks;
+                    const uint16_t *vsb = fresh ? src.cvs : src.vs;
+                    const i32x4 *kp = reinterpret_cast<const i32x4 *>(kqb + row * kHD + 32 * blk);
+                    const i32x4 *vp = reinterpret_cast<const i32x4 *>(vqb + row * kHD + 32 * blk);
+                    const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+                    // q·d in f16 with one rounding, as (f16)(d·q) in f32 (the
+                    // product of an int8 and an f16 is exact in both): four
+                    // quants at a time become the f16 pairs 1024 + (q + 128)
+                    // by a byte permute against 0x64, -1152 gives q exactly,
+                    // and a packed f16 multiply applies d
+                    const _Float16 sk = __builtin_bit_cast(_Float16, ksb[row * (kHD / 32) + blk]);
+                    const _Float16 sv = IPV ? (_Float16)1.f
+                                            : __builtin_bit_cast(_Float16, vsb[row * (kHD / 32) + blk]);
+                    const h2 dk = {sk, sk}, dv = {sv, sv};
+                    const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                    const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                    for (int w = 0; w < 8; w++) {
+                        const h2 k01 = i8_pair_f16((uint32_t)kw[w], 0x04010400u) * dk;
+                        const h2 k23 = i8_pair_f16((uint32_t)kw[w], 0x04030402u) * dk;
+                        const h2 v01 = i8_pair_f16((uint32_t)vw[w], 0x04010400u) * dv;
+                        const h2 v23 = i8_pair_f16((uint32_t)vw[w], 0x04030402u) * dv;
+                        kv[4 * w] = k01[0], kv[4 * w + 1] = k01[1], kv[4 * w + 2] = k23[0], kv[4 * w + 3] = k23[1];
+                        vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 32; j++) kv[j] = vv[j] = (_Float16)0.f;
                 }
-            } else {
 #pragma unroll
-                for (int j = 0; j < 32; j++) kv[j] = vv[j] = (_Float16)0.f;
-            }
+                for (int j = 0; j < 4; j++) {
+                    h8 kt;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                h8 t;
+                    for (int q8 = 0; q8 < 8; q8++) kt[q8] = kv[8 * j + q8];
+                    *reinterpret_cast<h8 *>(&k_s[kk][32 * blk + 8 * j]) = kt;
+                }
 #pragma unroll
-                for (int e = 0; e < 8; e++) t[e] = kv[8 * j + e];
-                *reinterpret_cast<h8 *>(&k_s[kk][32 * blk + 8 * j]) = t;
+                for (int j = 0; j < 32; j++) {
+                    // IPV: the raw quants (exact as f16 with a unit scale) as bytes
+                    const uint32_t bits = IPV ? (uint32_t)((int)(float)vv[j] & 0xff)
+                                              : (uint32_t)__builtin_bit_cast(uint16_t, vv[j]);
+                    vpk[j] = e == 0 ? bits : vpk[j] | (bits << (IPV ? 8 : 16));
+                }
             }
             if (IPV) {
-                // the raw quants (exact as f16 with a unit scale), transposed
 #pragma unroll
-                for (int j = 0; j < 32; j++) vt8[32 * blk + j][kk] = (int8_t)(int)(float)vv[j];
+                for (int j = 0; j < 32; j++)
+                    *reinterpret_cast<uint16_t *>(&vt8[32 * blk + j][2 * pair]) = (uint16_t)vpk[j];
             } else {
 #pragma unroll
-                for (int j = 0; j < 32; j++) vt_s[32 * blk + j][kk] = vv[j];
+                for (int j = 0; j < 32; j++)
+                    *reinterpret_cast<uint32_t *>(&vt_s[32 * blk + j][vt_col(2 * pair, blk)]) = vpk[j];
             }
         }
         if (IPV) {  // the tile's key-blocked V scales, [block][dim]
@@ -359,9 +381,9 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
             for (int half = 0; half < 2; half++)
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
-                    const _Float16 *vr = &vt_s[32 * d + l32][ko + 32 * t2 + 16 * half + 4 * hh];
-                    const h4 lo = *reinterpret_cast<const h4 *>(vr);
-                    const h4 hi = *reinterpret_cast<const h4 *>(vr + 8);
+                    const int c0 = ko + 32 * t2 + 16 * half + 4 * hh;
+                    const h4 lo = *reinterpret_cast<const h4 *>(&vt_s[32 * d + l32][vt_col(c0, d)]);
+                    const h4 hi = *reinterpret_cast<const h4 *>(&vt_s[32 * d + l32][vt_col(c0 + 8, d)]);
                     const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t2][half], o[d], 0, 0, 0);
                 }
