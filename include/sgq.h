@@ -305,6 +305,16 @@ typedef struct {
     uint32_t global_k_eq_v; /* 1: global layers take V from the K projection */
     uint32_t prefill_chunk; /* tokens per prefill chunk (its buffers are sized by it) */
     uint64_t seed;
+    /* The real checkpoint's per-kind geometry (crates/sg-gguf/src/desc.rs:
+     * 66-93): global layers' head_dim and kv heads (0: as the sliding
+     * layers'), and a Q6_K token embedding / tied head (q6_k.rs:25-62)
+     * instead of Q4_0.  Any of them, or head_dim != 128, selects the
+     * any-geometry attention (decode modes 2 and 3 only; see
+     * sgq_model_set_decode_mode). */
+    uint32_t head_dim_global;
+    uint32_t n_kv_heads_global;
+    uint32_t embed_q6k;
+    uint32_t reserved;
 } sgq_model_config;
 
 /* The benchmark shape: 62 layers, hidden 5376, ffn 21504, 32 q / 16 kv heads
@@ -331,7 +341,13 @@ int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
  * weights while waiting (the _graph form then launches it directly),
  * 2 = five launches per layer (QKV, attention, O, gate/up, down GEMVs) with
  * the norms, residual updates, GeGLU and the split merge fused into them
- * (the _graph form captures them).
+ * (the _graph form captures them), 3 = one kernel per operator at any
+ * supported geometry: head_dim 128/256/512 per layer kind, 1/2/4/8 query
+ * heads per kv head, Q4_0 or Q6_K embedding (the real checkpoint's shape;
+ * attention on the VALU).  Models of another geometry than the benchmark's
+ * (head_dim 128 everywhere, <= 2 q heads per kv head, Q4_0 embedding) run in
+ * mode 2 (the default for them: the fused GEMVs around the any-geometry
+ * attention) or mode 3; their prefill runs as successive mode-3 steps.
  * Mode 1 fails with SGQ_ERR_VALIDATION when the shape or the device does not
  * fit it. */
 int sgq_model_set_decode_mode(sgq_model *model, int mode);

@@ -53,9 +53,14 @@ class OracleDecoder:
         # taps[(name, layer)] = the row(s) of the last forward, when a dict:
         # "k_rope" and "v_norm" (reference.rs:153-155 tap names)
         self.taps = None
-        hd = cfg["head_dim"]
-        live = int(round(cfg["global_rope_frac"] * hd / 2))
-        self.global_factors = np.array([1.0] * live + [1e30] * (hd // 2 - live), np.float32)
+        # kv_source(layer, pos, k_row, v_row) -> (k_row, v_row): the Q8_0
+        # round-tripped rows decode() caches, replaceable by the caller (a
+        # test hands in the device's own pages, so that a rounding flip of a
+        # quant near a rounding boundary does not make the two caches differ)
+        self.kv_source = None
+        hd_g = cfg.get("head_dim_global") or cfg["head_dim"]
+        live = int(round(cfg["global_rope_frac"] * hd_g / 2))
+        self.global_factors = np.array([1.0] * live + [1e30] * (hd_g // 2 - live), np.float32)
 
     def preload_cache(self, pages: dict, n_tokens: int):
         """Start from a filled context: ``pages[(layer, "k"|"v")]`` = (scales,
@@ -63,8 +68,8 @@ class OracleDecoder:
         slot p; ring layers at slot p % slots (positions older than the ring
         are never attended)."""
         c = self.c
-        hd, nkv = c["head_dim"], c["n_kv_heads"]
         for l in range(c["n_layers"]):
+            hd, nkv = self.geometry(l)
             for kind, cache in (("k", self.k_cache), ("v", self.v_cache)):
                 sc, q = pages[(l, kind)]
                 rows = O.dequant_q8_0(sc, q).reshape(-1, nkv * hd)
@@ -75,6 +80,40 @@ class OracleDecoder:
     def is_global(self, layer: int) -> bool:
         ge = self.c["global_every"]
         return layer % ge == ge - 1
+
+    def geometry(self, layer: int):
+        """(head_dim, n_kv_heads) of the layer's kind: the global kind may
+        differ (the real checkpoint: sliding 256 x 16, global 512 x 4;
+        crates/sg-gguf/src/desc.rs:66-93)."""
+        c = self.c
+        if self.is_global(layer):
+            return (c.get("head_dim_global") or c["head_dim"],
+                    c.get("n_kv_heads_global") or c["n_kv_heads"])
+        return c["head_dim"], c["n_kv_heads"]
+
+    def _embed_rows(self, tokens):
+        """Dequantized embedding rows: Q4_0, or Q6_K rows at the device's
+        padded stride (q6_k.rs:41-62)."""
+        c, H = self.c, self.c["hidden"]
+        emb = self.w[("token_embd", -1)]
+        if c.get("embed_q6k"):
+            stride = ((H // 256) * 210 + 15) // 16 * 16
+            return np.stack([O.q6_k_dequant(emb[t * stride:(t + 1) * stride], 1, H, stride)[0]
+                             for t in tokens])
+        rb = (H // 32) * 18
+        return np.stack([O.q4_0_dequant(emb[t * rb:(t + 1) * rb], 1, H)[0] for t in tokens])
+
+    def _head(self, xf):
+        """Tied LM head with the softcap (reference.rs:307-316)."""
+        c, H = self.c, self.c["hidden"]
+        emb = self.w[("token_embd", -1)]
+        if c.get("embed_q6k"):
+            stride = ((H // 256) * 210 + 15) // 16 * 16
+            logits = O.gemv_q6_k_logits(emb, stride, xf, c["vocab"], H, softcap=0.0)
+        else:
+            logits = O.matmul_q4_0(emb, xf, 1, c["vocab"], H, threads=self.threads)[0]
+        cap = np.float64(c["final_softcap"])
+        return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
 
     # host threads of the row-parallel matmul (results do not depend on it)
     threads = 8
@@ -92,15 +131,15 @@ class OracleDecoder:
 
     def decode(self, token: int) -> np.ndarray:
         c, w = self.c, self.w
-        H, F, hd = c["hidden"], c["ffn"], c["head_dim"]
-        nq, nkv = c["n_q_heads"], c["n_kv_heads"]
+        H, F = c["hidden"], c["ffn"]
+        nq = c["n_q_heads"]
         eps = c["eps"]
-        emb = w[("token_embd", -1)]
-        row = O.q4_0_dequant(emb[token * (H // 32) * 18:(token + 1) * (H // 32) * 18], 1, H)[0]
+        row = self._embed_rows([token])[0]
         x = (row * np.float32(math.sqrt(H))).astype(np.float32)
         pos = self.pos
         for l in range(c["n_layers"]):
             glob = self.is_global(l)
+            hd, nkv = self.geometry(l)
             xn = O.rmsnorm(x, w[("attn_norm", l)], H, eps)
             q = self._lin("attn_q", l, xn, nq * hd)
             k_proj = self._lin("attn_k", l, xn, nkv * hd)
@@ -119,8 +158,11 @@ class OracleDecoder:
             v = O.rmsnorm(v, None, hd, eps)
             if self.taps is not None:
                 self.taps[("k_rope", l)], self.taps[("v_norm", l)] = k, v
-            self.k_cache[l].append(self._q8_round_trip(k))
-            self.v_cache[l].append(self._q8_round_trip(v))
+            kr, vr = self._q8_round_trip(k), self._q8_round_trip(v)
+            if self.kv_source is not None:
+                kr, vr = self.kv_source(l, pos, kr, vr)
+            self.k_cache[l].append(kr)
+            self.v_cache[l].append(vr)
             ck = np.concatenate(self.k_cache[l])
             cv = np.concatenate(self.v_cache[l])
             window = None if glob else c["sliding_window"]
@@ -138,9 +180,7 @@ class OracleDecoder:
             x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
         self.pos += 1
         xf = O.rmsnorm(x, w[("output_norm", -1)], H, eps)
-        logits = O.matmul_q4_0(emb, xf, 1, c["vocab"], H, threads=self.threads)[0]
-        cap = np.float64(c["final_softcap"])
-        return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
+        return self._head(xf)
 
 
 class OraclePrefill(OracleDecoder):
@@ -170,20 +210,20 @@ class OraclePrefill(OracleDecoder):
 
     def prefill(self, tokens) -> np.ndarray:
         c, w = self.c, self.w
-        H, F, hd = c["hidden"], c["ffn"], c["head_dim"]
-        nq, nkv = c["n_q_heads"], c["n_kv_heads"]
+        H, F = c["hidden"], c["ffn"]
+        nq = c["n_q_heads"]
         eps = c["eps"]
         M = len(tokens)
         q0 = self.pos
-        emb = w[("token_embd", -1)]
-        rb = (H // 32) * 18
-        x = np.stack([O.q4_0_dequant(emb[t * rb:(t + 1) * rb], 1, H)[0] for t in tokens])
+        x = self._embed_rows(tokens)
         x = (x * np.float32(math.sqrt(H))).astype(np.float32)
         pos = np.arange(q0, q0 + M, dtype=np.uint32)
-        cs_sl = O.cos_sin_table(pos, hd, c["rope_theta_sliding"])
-        cs_gl = O.cos_sin_table(pos, hd, c["rope_theta_global"], self.global_factors)
+        hd_g = c.get("head_dim_global") or c["head_dim"]
+        cs_sl = O.cos_sin_table(pos, c["head_dim"], c["rope_theta_sliding"])
+        cs_gl = O.cos_sin_table(pos, hd_g, c["rope_theta_global"], self.global_factors)
         for l in range(c["n_layers"]):
             glob = self.is_global(l)
+            hd, nkv = self.geometry(l)
             xn = self._q8rt(O.rmsnorm(x, w[("attn_norm", l)], H, eps))
             q = self._mm("attn_q", l, xn, nq * hd)
             k_proj = self._mm("attn_k", l, xn, nkv * hd)
@@ -211,9 +251,7 @@ class OraclePrefill(OracleDecoder):
             x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
         self.pos += M
         xf = O.rmsnorm(x[-1], w[("output_norm", -1)], H, eps)
-        logits = O.matmul_q4_0(emb, xf, 1, c["vocab"], H, threads=self.threads)[0]
-        cap = np.float64(c["final_softcap"])
-        return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
+        return self._head(xf)
 
 
 LAYER_TENSORS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",

@@ -1,0 +1,372 @@
+// Decode attention over a Q8_0 KV cache at any head_dim in {128, 256, 512}
+// and 1..8 query heads per kv head: the released checkpoint's geometry
+// (sliding layers 16 kv heads of 256, global layers 4 kv heads of 512 under
+// 32 query heads; crates/sg-gguf/src/desc.rs:66-93), which the int8-MFMA
+// kernel (attn_mfma.h: head_dim 128, <= 2 heads per kv head) does not cover.
+//
+// Semantics as attn_decode_global_q8k.wgsl:41-112 / attn_reduce.wgsl:24-57:
+// s_t = scale·q_h·k_t over a split's slots, softmax per split, partials
+// (acc, m, l) per (query head, split), merged over the splits in split order.
+// The post-projection before it (q/k norms with weights, the weightless v
+// norm, NEOX RoPE, the Q8_0 append; rmsnorm.wgsl:24-61, rope.wgsl:35-52,
+// kv_append_global_q8.wgsl:29-60) is one launch of its own.
+//
+// Three launches per layer:
+//  * post-projection: one wave per head row (q heads, then k, then v);
+//    lane j holds float4 j (and j + 64 at head_dim 512); the NEOX partner
+//    of float4 j is j ± head_dim/8, a lane shuffle or the lane's other
+//    float4; q goes out in fp32, k and v as Q8_0 into the cache slot;
+//  * attention: workgroup = (kv head, split of 64 slots), 4 waves.  Scores:
+//    lane = slot, wave = a quarter of the head's dims (the quarter's K bytes
+//    in 16-byte loads, q from LDS as wave-uniform broadcasts), quarters
+//    summed in order.  Softmax over the 64 slots per head (one wave per
+//    head).  PV: wave = a quarter of the dims, lane = 1 or 2 dims (head_dim
+//    128: two lanes per dim over odd and even slots), the split's V rows read
+//    slot by slot (a wave reads 64 or 128 contiguous bytes of a row);
+//    splits past the current kv length exit at once;
+//  * merge: workgroup = (query head, 64 dims), splits folded in order up to
+//    the current kv length; writes fp32 rows and/or the O projection's x
+//    limbs (32-blocks, limbs.h).
+#include <algorithm>
+
+#include "limbs.h"
+#include "q8.h"
+
+namespace sgq {
+namespace {
+
+constexpr int kGSlots = 64;  // slots per split
+constexpr float kGNegBig = -3.0e38f;
+
+template <int HD>
+__global__ __launch_bounds__(64) void attn_postproj_generic_kernel(
+    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
+    const float *__restrict__ v_src, const float *__restrict__ q_norm,
+    const float *__restrict__ k_norm, const float2 *__restrict__ cs, float eps,
+    const uint32_t *__restrict__ step, uint32_t ring, int n_q, int n_kv, float *__restrict__ q_out,
+    uint16_t *__restrict__ ks, int *__restrict__ kq, uint16_t *__restrict__ vs,
+    int *__restrict__ vq) {
+    constexpr int NF = HD / 4;               // float4s per head row
+    constexpr int NV = (NF + 63) / 64;       // float4s per lane
+    const int lane = threadIdx.x, b = blockIdx.x;
+    const int kind = b < n_q ? 0 : (b < n_q + n_kv ? 1 : 2);
+    const int head = kind == 0 ? b : (kind == 1 ? b - n_q : b - n_q - n_kv);
+    const float *src = (kind == 0 ? q_raw : (kind == 1 ? k_raw : v_src)) + (size_t)head * HD;
+    const float *w = kind == 0 ? q_norm : (kind == 1 ? k_norm : nullptr);
+    float4 x[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int j = lane + 64 * v;
+        x[v] = j < NF ? reinterpret_cast<const float4 *>(src)[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
+    }
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int j = lane + 64 * v;
+        float4 wt = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (w && j < NF) wt = reinterpret_cast<const float4 *>(w)[j];
+        x[v] = make_float4(x[v].x * inv * wt.x, x[v].y * inv * wt.y, x[v].z * inv * wt.z,
+                           x[v].w * inv * wt.w);
+    }
+    if (kind != 2) {
+        // NEOX: dim i pairs with i + HD/2 (float4 j with j + NF/2)
+        float4 pr[NV];
+        if (NV == 1) {
+            const int pj = lane < NF / 2 ? lane + NF / 2 : lane - NF / 2;
+            const int src_lane = pj < 64 ? pj : 0;
+            pr[0] = make_float4(__shfl(x[0].x, src_lane, kWave), __shfl(x[0].y, src_lane, kWave),
+                                __shfl(x[0].z, src_lane, kWave), __shfl(x[0].w, src_lane, kWave));
+        } else {
+#pragma unroll
+            for (int v = 0; v < NV; v++) pr[v] = x[NV - 1 - v];  // NF = 128: j ± 64
+        }
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int j = lane + 64 * v;
+            if (j >= NF) continue;
+            const bool lo = j < NF / 2;
+            const int i0 = (lo ? j : j - NF / 2) * 4;  // pair index of the float4's first dim
+            const float sg = lo ? -1.f : 1.f;
+            const float2 c0 = cs[i0], c1 = cs[i0 + 1], c2 = cs[i0 + 2], c3 = cs[i0 + 3];
+            x[v] = make_float4(x[v].x * c0.x + sg * pr[v].x * c0.y,
+                               x[v].y * c1.x + sg * pr[v].y * c1.y,
+                               x[v].z * c2.x + sg * pr[v].z * c2.y,
+                               x[v].w * c3.x + sg * pr[v].w * c3.y);
+        }
+    }
+    if (kind == 0) {
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int j = lane + 64 * v;
+            if (j < NF) reinterpret_cast<float4 *>(q_out + (size_t)head * HD)[j] = x[v];
+        }
+        return;
+    }
+    const uint32_t pos = step[0];
+    const size_t slot = ring ? pos % ring : pos;
+    uint16_t *sc = kind == 1 ? ks : vs;
+    int *qt = kind == 1 ? kq : vq;
+    const size_t e0 = slot * (size_t)n_kv * HD + (size_t)head * HD;  // row start, elements
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int j = lane + 64 * v;
+        if (j < NF) {  // whole 8-lane groups (NF is a multiple of 8)
+            int qv;
+            quant_lane(x[v], j & 7, &sc[(e0 + 4 * j) / 32], &qv);
+            qt[(e0 + 4 * j) / 4] = qv;
+        }
+    }
+}
+
+template <int HD, int QPK>
+__global__ __launch_bounds__(256) void attn_generic_kernel(
+    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
+    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
+    const uint32_t *__restrict__ step, int step_word, int n_kv, int n_splits, float scale,
+    float *__restrict__ part) {
+    constexpr int NB = HD / 32;   // Q8 blocks per row
+    constexpr int DW = HD / 4;    // dims per wave (a quarter of the head)
+    constexpr int PB = DW / 32;   // Q8 blocks per quarter
+    constexpr int ND = DW >= 64 ? DW / 64 : 1;  // PV dims per lane
+    constexpr int SG = DW >= 64 ? 1 : 64 / DW;  // PV slot groups across a wave's lanes
+    __shared__ float q_s[QPK][HD];
+    __shared__ float sp_s[4][QPK][kGSlots];
+    __shared__ float p_s[QPK][kGSlots];
+    __shared__ float ml_s[QPK][2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const uint32_t kv_len = step[step_word];
+    const uint32_t t0 = (uint32_t)split * kGSlots;
+    if (t0 >= kv_len) return;  // the merge folds only the live splits
+    const int n = (int)min((uint32_t)kGSlots, kv_len - t0);
+
+    for (int i = tid; i < QPK * HD; i += 256)
+        q_s[i / HD][i % HD] = q[((size_t)kvh * QPK + i / HD) * HD + i % HD] * scale;
+    __syncthreads();
+
+    // ---- scores: lane = slot, wave = dims [wave·DW, wave·DW + DW)
+    {
+        float acc[QPK];
+#pragma unroll
+        for (int h = 0; h < QPK; h++) acc[h] = 0.f;
+        if (lane < n) {
+            const size_t row = (size_t)(t0 + lane) * n_kv + kvh;
+            const int8_t *kr = kq + row * HD + wave * DW;
+            const uint16_t *sr = ks + row * NB + wave * PB;
+#pragma unroll
+            for (int b = 0; b < PB; b++) {
+                const float d = f16_bits_to_f32(sr[b]);
+                const int4 w0 = reinterpret_cast<const int4 *>(kr + 32 * b)[0];
+                const int4 w1 = reinterpret_cast<const int4 *>(kr + 32 * b)[1];
+                const int ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                float kf[32];
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) kf[4 * j + e] = (float)(int8_t)(ww[j] >> (8 * e));
+#pragma unroll
+                for (int h = 0; h < QPK; h++) {
+                    const float *qh = &q_s[h][wave * DW + 32 * b];
+                    float dot = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 32; j++) dot = __builtin_fmaf(qh[j], kf[j], dot);
+                    acc[h] = __builtin_fmaf(d, dot, acc[h]);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < QPK; h++) sp_s[wave][h][lane] = acc[h];
+    }
+    __syncthreads();
+
+    // ---- softmax per head over the split: wave w takes heads w, w + 4
+    for (int h = wave; h < QPK; h += 4) {
+        const float s = lane < n ? ((sp_s[0][h][lane] + sp_s[1][h][lane]) + sp_s[2][h][lane]) +
+                                       sp_s[3][h][lane]
+                                 : kGNegBig;
+        float m = s;
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+        const float p = lane < n ? __expf(s - m) : 0.f;
+        float l = p;
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, kWave);
+        p_s[h][lane] = p;
+        if (lane == 0) ml_s[h][0] = m, ml_s[h][1] = l;
+    }
+    __syncthreads();
+
+    // ---- PV: wave = dims [wave·DW, wave·DW + DW), lane = ND dims (SG slot groups)
+    const int sg = SG == 1 ? 0 : lane / DW;
+    const int dl = SG == 1 ? lane : lane % DW;
+    const int d0 = wave * DW + dl * ND;
+    float acc[QPK][ND];
+#pragma unroll
+    for (int h = 0; h < QPK; h++)
+#pragma unroll
+        for (int e = 0; e < ND; e++) acc[h][e] = 0.f;
+#pragma unroll 4
+    for (int i = sg; i < n; i += SG) {
+        const size_t row = (size_t)(t0 + i) * n_kv + kvh;
+        const float sc = f16_bits_to_f32(vs[row * NB + d0 / 32]);
+        float v[ND];
+        if (ND == 2) {
+            const uint32_t w2 = *reinterpret_cast<const uint16_t *>(vq + row * HD + d0);
+            v[0] = sc * (float)(int8_t)(w2 & 0xff);
+            v[ND - 1] = sc * (float)(int8_t)(w2 >> 8);
+        } else {
+            v[0] = sc * (float)vq[row * HD + d0];
+        }
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            const float p = p_s[h][i];
+#pragma unroll
+            for (int e = 0; e < ND; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
+        }
+    }
+    if (SG == 2) {
+#pragma unroll
+        for (int h = 0; h < QPK; h++)
+#pragma unroll
+            for (int e = 0; e < ND; e++) acc[h][e] += __shfl_xor(acc[h][e], 32, kWave);
+    }
+    constexpr int stride = HD + 2;
+#pragma unroll
+    for (int h = 0; h < QPK; h++) {
+        float *pr = part + ((size_t)(kvh * QPK + h) * n_splits + split) * stride;
+        if (sg == 0) {
+#pragma unroll
+            for (int e = 0; e < ND; e++) pr[d0 + e] = acc[h][e];
+        }
+        if (tid == 0) {
+            pr[HD] = ml_s[h][0];
+            pr[HD + 1] = ml_s[h][1];
+        }
+    }
+}
+
+// out[h][d] = Σ_s a_s e^(m_s − M) / Σ_s l_s e^(m_s − M) over the live splits
+// in order; fp32 rows to out and/or the x limbs of the row to xl.
+template <int HD>
+__global__ __launch_bounds__(64) void attn_generic_merge_kernel(
+    const float *__restrict__ part, const uint32_t *__restrict__ step, int step_word,
+    int n_splits, float *__restrict__ out, BlockLimbs *__restrict__ xl) {
+    constexpr int stride = HD + 2;
+    __shared__ float o_s[64];
+    const int h = blockIdx.x, lane = threadIdx.x, d = blockIdx.y * 64 + lane;
+    const uint32_t kv_len = step[step_word];
+    const int n_act = min(n_splits, (int)((kv_len + kGSlots - 1) / kGSlots));
+    const float *ph = part + (size_t)h * n_splits * stride;
+    float M = kGNegBig;
+    for (int s = lane; s < n_act; s += 64) M = fmaxf(M, ph[(size_t)s * stride + HD]);
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, kWave));
+    float a = 0.f, l = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < n_act; s++) {
+        const float *pr = ph + (size_t)s * stride;
+        const float f = __expf(pr[HD] - M);
+        a = __builtin_fmaf(pr[d], f, a);
+        l = __builtin_fmaf(pr[HD + 1], f, l);
+    }
+    const float o = l > 0.f ? a / l : 0.f;
+    if (out) out[(size_t)h * HD + d] = o;
+    if (xl) {
+        o_s[lane] = o;
+        __syncthreads();
+        if (lane < 16) {  // two 32-blocks: 8-lane groups of float4s
+            const float4 v = reinterpret_cast<const float4 *>(o_s)[lane];
+            limbs_block8(v, lane & 7, xl + ((size_t)h * HD + blockIdx.y * 64) / 32 + (lane >> 3));
+        }
+    }
+}
+
+}  // namespace
+
+int attn_generic_splits(uint32_t slots) {
+    return (int)std::max<uint32_t>(1u, (slots + kGSlots - 1) / kGSlots);
+}
+
+int launch_attn_postproj_generic(hipStream_t st, const float *q_raw, const float *k_raw,
+                                 const float *v_src, const float *q_norm, const float *k_norm,
+                                 const float *cos_sin, float eps, const uint32_t *step,
+                                 uint32_t ring, int n_q, int n_kv, int head_dim, float *q_out,
+                                 uint16_t *ks, int8_t *kq, uint16_t *vs, int8_t *vq) {
+    SGQ_CHECK(q_raw && k_raw && v_src && q_norm && k_norm && cos_sin && step && q_out && ks &&
+                  kq && vs && vq,
+              "attn_postproj: NULL operand");
+    SGQ_CHECK(n_q > 0 && n_kv > 0, "attn_postproj: %d q heads / %d kv heads", n_q, n_kv);
+    SGQ_CHECK(((uintptr_t)q_raw & 15) == 0 && ((uintptr_t)k_raw & 15) == 0 &&
+                  ((uintptr_t)v_src & 15) == 0 && ((uintptr_t)q_out & 15) == 0 &&
+                  ((uintptr_t)kq & 3) == 0 && ((uintptr_t)vq & 3) == 0,
+              "attn_postproj: misaligned buffers");
+    const dim3 grid(n_q + 2 * n_kv);
+    const float2 *cs = reinterpret_cast<const float2 *>(cos_sin);
+#define SGQ_PP(HD)                                                                                \
+    hipLaunchKernelGGL(attn_postproj_generic_kernel<HD>, grid, dim3(64), 0, st, q_raw, k_raw,     \
+                       v_src, q_norm, k_norm, cs, eps, step, ring, n_q, n_kv, q_out, ks,          \
+                       reinterpret_cast<int *>(kq), vs, reinterpret_cast<int *>(vq))
+    switch (head_dim) {
+        case 128: SGQ_PP(128); break;
+        case 256: SGQ_PP(256); break;
+        case 512: SGQ_PP(512); break;
+        default: return fail(SGQ_ERR_VALIDATION, "attn_postproj: head_dim %d (128/256/512)", head_dim);
+    }
+#undef SGQ_PP
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
+                               const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
+                               const uint32_t *step, int step_word, int n_q, int n_kv,
+                               int head_dim, int n_splits, float scale, float *part, float *out,
+                               void *xl) {
+    SGQ_CHECK(q && kq && ks && vq && vs && step && part && (out || xl),
+              "attn_generic: NULL operand");
+    SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_generic: n_q %% n_kv != 0");
+    const int qpk = n_q / n_kv;
+    SGQ_CHECK(n_splits >= 1 && n_splits <= 65535, "attn_generic: n_splits %d", n_splits);
+    SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0,
+              "attn_generic: misaligned cache");
+    dim3 grid(n_kv, n_splits);
+#define SGQ_G(HD, Q)                                                                             \
+    hipLaunchKernelGGL((attn_generic_kernel<HD, Q>), grid, dim3(256), 0, st, q, kq, ks, vq, vs,  \
+                       step, step_word, n_kv, n_splits, scale, part)
+#define SGQ_GQ(HD)                                                      \
+    switch (qpk) {                                                      \
+        case 1: SGQ_G(HD, 1); break;                                    \
+        case 2: SGQ_G(HD, 2); break;                                    \
+        case 4: SGQ_G(HD, 4); break;                                    \
+        case 8: SGQ_G(HD, 8); break;                                    \
+        default: return fail(SGQ_ERR_VALIDATION, "attn_generic: %d q heads per kv head", qpk); \
+    }
+    switch (head_dim) {
+        case 128: SGQ_GQ(128); break;
+        case 256: SGQ_GQ(256); break;
+        case 512: SGQ_GQ(512); break;
+        default: return fail(SGQ_ERR_VALIDATION, "attn_generic: head_dim %d (128/256/512)", head_dim);
+    }
+#undef SGQ_GQ
+#undef SGQ_G
+    SGQ_HIP(hipGetLastError());
+    BlockLimbs *xt = static_cast<BlockLimbs *>(xl);
+    const dim3 mg(n_q, head_dim / 64);
+    switch (head_dim) {
+        case 128:
+            hipLaunchKernelGGL(attn_generic_merge_kernel<128>, mg, dim3(64), 0, st, part, step,
+                               step_word, n_splits, out, xt);
+            break;
+        case 256:
+            hipLaunchKernelGGL(attn_generic_merge_kernel<256>, mg, dim3(64), 0, st, part, step,
+                               step_word, n_splits, out, xt);
+            break;
+        default:
+            hipLaunchKernelGGL(attn_generic_merge_kernel<512>, mg, dim3(64), 0, st, part, step,
+                               step_word, n_splits, out, xt);
+    }
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+}  // namespace sgq

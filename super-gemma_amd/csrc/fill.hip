@@ -54,6 +54,34 @@ __global__ void fill_normal_kernel(float *__restrict__ x, uint64_t n, uint64_t s
     }
 }
 
+// Q6_K rows at a byte stride (q6_k.rs:25-62 block layout: ql[128], qh[64],
+// int8 sub-scales[16], f16 d; parity_logits.rs:31-51's distribution: random
+// quant bytes, sub-scales in [-8, 7], d = f16(N(0,1)·1e-3)); row padding
+// zeroed.  Thread per (row, block).
+__global__ void fill_q6k_kernel(uint8_t *__restrict__ w, uint64_t n_rows, int nb,
+                                uint64_t row_stride, uint64_t seed) {
+    const uint64_t n_items = n_rows * (uint64_t)nb;
+    for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items;
+         it += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = it / nb;
+        const int b = (int)(it % nb);
+        uint8_t *blk = w + r * row_stride + (uint64_t)b * 210;
+        for (int j = 0; j < 208; j += 8) {
+            const uint64_t h = splitmix64(seed ^ ((it * 27 + j / 8) * 0xD1B54A32D192ED03ull));
+            for (int e = 0; e < 8 && j + e < 208; e++) {
+                const uint8_t byte = (uint8_t)(h >> (8 * e));
+                blk[j + e] = j + e >= 192 ? (uint8_t)(int8_t)((int)(byte & 15) - 8) : byte;
+            }
+        }
+        const uint16_t d = f32_to_f16_bits(
+            normal_from(splitmix64(seed ^ ((it * 27 + 26) * 0xD1B54A32D192ED03ull))) * 1e-3f);
+        blk[208] = (uint8_t)(d & 0xff);
+        blk[209] = (uint8_t)(d >> 8);
+        if (b == nb - 1)
+            for (uint64_t p = (uint64_t)nb * 210; p < row_stride; p++) w[r * row_stride + p] = 0;
+    }
+}
+
 int fill_grid(uint64_t n) {
     uint64_t g = (n + 255) / 256;
     const uint64_t cap = (uint64_t)device_info().cus * 16;
@@ -76,6 +104,18 @@ int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, floa
     if (n == 0) return SGQ_OK;
     hipLaunchKernelGGL(fill_normal_kernel, dim3(fill_grid(n)), dim3(256), 0, st, x, n, seed, mean,
                        sigma);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_fill_q6k(hipStream_t st, void *w, uint64_t n_rows, uint32_t k, uint64_t row_stride,
+                    uint64_t seed) {
+    SGQ_CHECK(k % 256 == 0 && row_stride >= (uint64_t)(k / 256) * 210,
+              "fill_q6k: k %u, row stride %llu", k, (unsigned long long)row_stride);
+    const uint64_t items = n_rows * (k / 256);
+    if (items == 0) return SGQ_OK;
+    hipLaunchKernelGGL(fill_q6k_kernel, dim3(fill_grid(items)), dim3(256), 0, st,
+                       static_cast<uint8_t *>(w), n_rows, (int)(k / 256), row_stride, seed);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }

@@ -117,6 +117,104 @@ __global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__res
     }
 }
 
+// The same with a Q6_K embedding row at a byte stride (q6_k.rs:41-62: value
+// 128h + 32w + l of a 256-weight block is d·sc[l/16 + 2w + 8h]·q, q the
+// 6-bit quant from ql's low (w even) or high (w odd) nibble of byte
+// 64h + l (+32 for w = 1, 3) and 2 bits of qh[32h + l], minus 32).
+__global__ __launch_bounds__(kRowWG) void embed_q6k_norm_kernel(
+    const uint8_t *__restrict__ E, uint64_t row_stride, const uint32_t *__restrict__ step,
+    int hidden, float scale, const float *__restrict__ w, float eps, float *__restrict__ x,
+    BlockLimbs *__restrict__ xl) {
+    __shared__ float red[kRowWG / kWave];
+    const int n4 = hidden / 4, t = threadIdx.x;
+    const uint8_t *er = E + (size_t)step[4] * row_stride;
+    float4 v[kRowV];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            const int j0 = 4 * i;                       // first of four consecutive values
+            const uint8_t *blk = er + (j0 / 256) * 210;
+            const int j = j0 % 256, h = j / 128, r = j % 128, wq = r / 32, l0 = r % 32;
+            const float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
+            const float ds = d * (float)(int8_t)blk[192 + 8 * h + l0 / 16 + 2 * wq];
+            const uint8_t *ql = blk + 64 * h + (wq & 1) * 32;
+            const uint8_t *qh = blk + 128 + 32 * h;
+            float e[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int l = l0 + u;
+                const int lo = wq < 2 ? (ql[l] & 15) : (ql[l] >> 4);
+                const int q = (lo | (((qh[l] >> (2 * wq)) & 3) << 4)) - 32;
+                e[u] = ds * (float)q * scale;
+            }
+            v[k] = make_float4(e[0], e[1], e[2], e[3]);
+            reinterpret_cast<float4 *>(x)[i] = v[k];
+            ss += sumsq4(v[k]);
+        }
+    }
+    ss = wg_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+#pragma unroll
+    for (int k = 0; k < kRowV; k++) {
+        const int i = t + k * kRowWG;
+        if (i < n4) {
+            const float4 wv = reinterpret_cast<const float4 *>(w)[i];
+            const float4 y = make_float4(v[k].x * inv * wv.x, v[k].y * inv * wv.y,
+                                         v[k].z * inv * wv.z, v[k].w * inv * wv.w);
+            limbs_block8(y, i & 7, &xl[i >> 3]);
+        }
+    }
+}
+
+// RoPE tables of the step's position for both layer kinds at their own
+// head_dim (rope.rs:27-48 with f64 angles): [sliding: hd_s/2 pairs][global:
+// hd_g/2 pairs] of (cos, sin); global pairs past live_g use divisor 1e30.
+// The fused step's norm of the residual from a kEpiResid launch's partial
+// sums (the GEMV's kProNorm prologue, written out for a head that is not a
+// Q4_0 GEMV): with P = Σ of the np partials (Σo², Σx·u, Σu², Σx²),
+// ra = 1/sqrt(P0/H + eps), rb = 1/sqrt(s²(P3 + 2·ra·P1 + ra²·P2)/H + eps),
+// y = (A + ra·B)·rb·s with A = x·w_next, B = u·w_next the GEMV's rows.
+__global__ __launch_bounds__(kRowWG) void norm_from_partials_kernel(
+    const float4 *__restrict__ part, int np, const float *__restrict__ A,
+    const float *__restrict__ B, const float *__restrict__ scale, int hidden, float eps,
+    float *__restrict__ y) {
+    __shared__ float red[kRowWG / kWave];
+    const int t = threadIdx.x;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = t; i < np; i += kRowWG)
+        acc.x += part[i].x, acc.y += part[i].y, acc.z += part[i].z, acc.w += part[i].w;
+    float P[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        P[k] = wg_sum(P[k], red);
+        __syncthreads();  // red is reused by the next sum
+    }
+    const float P0 = P[0], P1 = P[1], P2 = P[2], P3 = P[3];
+    const float s = scale ? *scale : 1.f, K = (float)hidden;
+    const float ra = 1.0f / sqrtf(P0 / K + eps);
+    const float rb = 1.0f / sqrtf(s * s * (P3 + 2.f * ra * P1 + ra * ra * P2) / K + eps);
+    const float rs = rb * s;
+    for (int i = t; i < hidden; i += kRowWG) y[i] = (A[i] + ra * B[i]) * rs;
+}
+
+__global__ void rope_table_generic_kernel(const uint32_t *__restrict__ step,
+                                          float *__restrict__ cs, int hd_s, int hd_g,
+                                          float theta_s, float theta_g, int live_g) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int ps = hd_s / 2, pg = hd_g / 2;
+    if (t >= ps + pg) return;
+    const bool glob = t >= ps;
+    const int i = glob ? t - ps : t;
+    const int hd = glob ? hd_g : hd_s;
+    const double theta = glob ? (double)theta_g : (double)theta_s;
+    const double factor = glob && i >= live_g ? 1e30 : 1.0;
+    const double ang = (double)step[0] * pow(theta, -2.0 * (double)i / (double)hd) / factor;
+    cs[2 * t] = (float)cos(ang);
+    cs[2 * t + 1] = (float)sin(ang);
+}
+
 // post-attention: x += rmsnorm(o, w_post);            xl = limbs(rmsnorm(x, w_next))
 // post-FFN:       x = (x + rmsnorm(o, w_post))·scale;  xl = limbs(rmsnorm(x, w_next))
 // o arrives as n_parts K-slice partials (o = Σ_s o[s·hidden + i], s in order).
@@ -435,6 +533,7 @@ struct LayerW {
     int8_t *kq, *vq;
     uint16_t *ks, *vs;
     uint32_t slots;
+    uint32_t hd, n_kv;  // this layer kind's head_dim and kv heads
 };
 
 // The split merge of the fused decode runs as its own launch (queued behind
@@ -473,6 +572,14 @@ struct sgq_model {
     void *xl;  // limb table (largest K)
     uint32_t *step;
     float *rope_cs;  // [2 kinds][head_dim/2][cos, sin] of the current position
+    // mode 3 (any geometry): per-kind RoPE tables [hd_s/2 + hd_g/2][cos, sin],
+    // post-norm k and v rows, attention split partials, the final-normed x
+    // for a Q6_K head; embd_stride = bytes per embedding row (Q6_K rows are
+    // padded to 16 bytes, as the reference uploads them)
+    bool generic = false;
+    uint64_t embd_stride = 0;
+    float *rope_g = nullptr, *kx = nullptr, *vx = nullptr, *part_g = nullptr, *xf = nullptr;
+    float *logits_tmp = nullptr;
     uint32_t pos = 0;
     sgq_graph *graph = nullptr;
     float *graph_logits = nullptr;
@@ -591,6 +698,84 @@ int record_step(sgq_model *m, float *logits) {
     return launch_gemv_limbs(st, head, xl, H);
 }
 
+// Decode step at any supported geometry (mode 3): the kernel-per-operator
+// sequence of record_step with each layer kind's own head_dim and kv heads
+// (the real checkpoint: sliding 16 × 256, global 4 × 512 under 32 query
+// heads, desc.rs:66-93), the q/k/v post-projection as separate norm, RoPE
+// and Q8_0-append launches, the VALU split-K attention (attn_generic.hip),
+// and a Q4_0 or Q6_K tied head.  `head` false skips the logits (prefill's
+// inner tokens).
+int record_step_generic(sgq_model *m, float *logits, bool head) {
+    const sgq_model_config &c = m->cfg;
+    hipStream_t st = ctx_stream(m->ctx);
+    const int H = (int)c.hidden, F = (int)c.ffn, nq = (int)c.n_q_heads;
+    const int hd_s = (int)c.head_dim;
+    BlockLimbs *xl = static_cast<BlockLimbs *>(m->xl);
+    int rc;
+    if (c.embed_q6k)
+        hipLaunchKernelGGL(embed_q6k_norm_kernel, dim3(1), dim3(kRowWG), 0, st,
+                           static_cast<const uint8_t *>(m->embd), m->embd_stride, m->step, H,
+                           sqrtf((float)H), m->layers[0].attn_norm, c.eps, m->x, xl);
+    else
+        hipLaunchKernelGGL(embed_norm_kernel, dim3(1), dim3(kRowWG), 0, st,
+                           static_cast<const uint8_t *>(m->embd), m->step, H, sqrtf((float)H),
+                           m->layers[0].attn_norm, c.eps, m->x, xl);
+    SGQ_HIP(hipGetLastError());
+    for (size_t li = 0; li < m->layers.size(); li++) {
+        const LayerW &L = m->layers[li];
+        const int hd = (int)L.hd, nkv = (int)L.n_kv, QD = nq * hd, KD = nkv * hd;
+        GemvTargets qkv{};
+        qkv.w[0] = L.wq, qkv.w[1] = L.wk, qkv.w[2] = L.wv;
+        qkv.y[0] = m->q_raw, qkv.y[1] = m->k_raw, qkv.y[2] = m->v_raw;
+        qkv.end[0] = QD, qkv.end[1] = QD + KD, qkv.end[2] = QD + 2 * KD;
+        qkv.count = L.wv ? 3 : 2;
+        if ((rc = launch_gemv_limbs(st, qkv, xl, H))) return rc;
+        const float *v_src = L.wv ? m->v_raw : m->k_raw;
+        // q/k norms with weights, weightless v norm, NEOX RoPE, Q8_0 append;
+        // then attention, merged into the O projection's limbs
+        const float *cs = m->rope_g + (L.global ? hd_s : 0);
+        if ((rc = launch_attn_postproj_generic(st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
+                                               cs, c.eps, m->step, L.global ? 0u : L.slots, nq,
+                                               nkv, hd, m->q, L.ks, L.kq, L.vs, L.vq)) ||
+            (rc = launch_attn_decode_generic(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step,
+                                             L.global ? 2 : 1, nq, nkv, hd,
+                                             attn_generic_splits(L.slots), c.attn_scale,
+                                             m->part_g, m->attn, xl)))
+            return rc;
+        GemvTargets ot{};
+        ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
+        if ((rc = launch_gemv_limbs(st, ot, xl, QD))) return rc;
+        hipLaunchKernelGGL(residual_norm_kernel<1>, dim3(1), dim3(kRowWG), 0, st, m->o,
+                           L.post_attn_norm, m->x, (const float *)nullptr, L.ffn_norm, H, c.eps, xl);
+        SGQ_HIP(hipGetLastError());
+        GemvTargets gu{};
+        gu.w[0] = L.wg, gu.w[1] = L.wu, gu.y[0] = m->g, gu.y[1] = m->u;
+        gu.end[0] = F, gu.end[1] = 2 * F, gu.count = 2;
+        if ((rc = launch_gemv_limbs(st, gu, xl, H))) return rc;
+        hipLaunchKernelGGL(geglu_limbs_kernel, dim3((F / 4 + 255) / 256), dim3(256), 0, st, m->g,
+                           m->u, F, xl);
+        SGQ_HIP(hipGetLastError());
+        GemvTargets dt{};
+        dt.w[0] = L.wd, dt.y[0] = m->f, dt.end[0] = H, dt.count = 1;
+        if ((rc = launch_gemv_limbs(st, dt, xl, F))) return rc;
+        const float *w_next =
+            li + 1 < m->layers.size() ? m->layers[li + 1].attn_norm : m->out_norm;
+        hipLaunchKernelGGL(residual_norm_kernel<1>, dim3(1), dim3(kRowWG), 0, st, m->f,
+                           L.post_ffw_norm, m->x, L.out_scale, w_next, H, c.eps, xl);
+        SGQ_HIP(hipGetLastError());
+    }
+    if (!head) return SGQ_OK;
+    if (c.embed_q6k) {
+        if ((rc = launch_rmsnorm(st, m->x, m->out_norm, m->xf, 1, (uint32_t)H, 0, c.eps))) return rc;
+        return launch_gemv_q6_k(st, m->embd, m->embd_stride, m->xf, logits, c.vocab, (uint32_t)H,
+                                c.final_softcap);
+    }
+    GemvTargets hd_t{};
+    hd_t.w[0] = m->embd, hd_t.y[0] = logits, hd_t.end[0] = (int)c.vocab, hd_t.count = 1;
+    hd_t.softcap = c.final_softcap;
+    return launch_gemv_limbs(st, hd_t, xl, H);
+}
+
 // Fused decode step (mode 2): six launches per layer.
 //   QKV GEMV       prologue: the previous layer's post-FFN residual update and
 //                  this layer's input RMSNorm, from the down GEMV's partial
@@ -610,17 +795,17 @@ int record_step(sgq_model *m, float *logits) {
 int record_step_fused(sgq_model *m, float *logits) {
     const sgq_model_config &c = m->cfg;
     hipStream_t st = ctx_stream(m->ctx);
-    const int H = (int)c.hidden, F = (int)c.ffn, QD = (int)(c.n_q_heads * kHeadDim),
-              KD = (int)(c.n_kv_heads * kHeadDim);
-    const int np_o = gemv_fused_grid((uint32_t)H, (uint32_t)QD, kEpiResid);
+    const int H = (int)c.hidden, F = (int)c.ffn, nq = (int)c.n_q_heads;
     const int np_d = gemv_fused_grid((uint32_t)H, (uint32_t)F, kEpiResid);
-    SGQ_CHECK(np_o > 0 && np_o <= kGemvMaxPartials && np_d > 0 && np_d <= kGemvMaxPartials,
-              "model (fused): partial sums %d / %d", np_o, np_d);
+    SGQ_CHECK(np_d > 0 && np_d <= kGemvMaxPartials, "model (fused): partial sums %d", np_d);
     float *xa = m->x, *xb = m->fx.xb;
     int rc;
     const size_t nl = m->layers.size();
     for (size_t li = 0; li < nl; li++) {
         const LayerW &L = m->layers[li];
+        const int hd = (int)L.hd, nkv = (int)L.n_kv, QD = nq * hd, KD = nkv * hd;
+        const int np_o = gemv_fused_grid((uint32_t)H, (uint32_t)QD, kEpiResid);
+        SGQ_CHECK(np_o > 0 && np_o <= kGemvMaxPartials, "model (fused): partial sums %d", np_o);
         GemvTargets qkv{};
         qkv.w[0] = L.wq, qkv.w[1] = L.wk, qkv.w[2] = L.wv;
         qkv.y[0] = m->q_raw, qkv.y[1] = m->k_raw, qkv.y[2] = m->v_raw;
@@ -630,7 +815,18 @@ int record_step_fused(sgq_model *m, float *logits) {
         pre.eps = c.eps;
         pre.x_out = xa;
         int pro;
-        if (li == 0) {
+        const void *qkv_xl = nullptr;
+        if (li == 0 && c.embed_q6k) {
+            // Q6_K embedding row: its own launch writes x and the norm's limbs
+            hipLaunchKernelGGL(embed_q6k_norm_kernel, dim3(1), dim3(kRowWG), 0, st,
+                               static_cast<const uint8_t *>(m->embd), m->embd_stride, m->step, H,
+                               sqrtf((float)H), L.attn_norm, c.eps, xa,
+                               static_cast<BlockLimbs *>(m->xl));
+            SGQ_HIP(hipGetLastError());
+            pro = kProTable;
+            qkv_xl = m->xl;
+            pre = GemvFuse{};
+        } else if (li == 0) {
             pro = kProEmbed;
             pre.embd = static_cast<const uint8_t *>(m->embd);
             pre.step = m->step;
@@ -642,16 +838,27 @@ int record_step_fused(sgq_model *m, float *logits) {
             pre.A = m->fx.a, pre.B = m->fx.b, pre.u = m->fx.u, pre.x_in = xb;
             pre.scale = m->layers[li - 1].out_scale;
         }
-        if ((rc = launch_gemv_fused(st, qkv, nullptr, (uint32_t)H, pro, kEpiRows, pre))) return rc;
+        if ((rc = launch_gemv_fused(st, qkv, qkv_xl, (uint32_t)H, pro, kEpiRows, pre))) return rc;
         const float *v_src = L.wv ? m->v_raw : m->k_raw;
-        const int n_splits = decode_splits(L);
-        if ((rc = launch_attn_decode_fused(
-                 st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
-                 m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
-                 L.global ? 0u : L.slots, L.kq, L.ks, L.vq, L.vs, (int)c.n_q_heads,
-                 (int)c.n_kv_heads, n_splits, c.attn_scale, nullptr, ctx_workspace(m->ctx),
-                 kWorkspaceBytes, m->fx.xl_o, kMergeInLaunch)))
+        if (m->generic) {
+            const float *cs = m->rope_g + (L.global ? c.head_dim : 0);
+            if ((rc = launch_attn_postproj_generic(st, m->q_raw, m->k_raw, v_src, L.q_norm,
+                                                   L.k_norm, cs, c.eps, m->step,
+                                                   L.global ? 0u : L.slots, nq, nkv, hd, m->q,
+                                                   L.ks, L.kq, L.vs, L.vq)) ||
+                (rc = launch_attn_decode_generic(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step,
+                                                 L.global ? 2 : 1, nq, nkv, hd,
+                                                 attn_generic_splits(L.slots), c.attn_scale,
+                                                 m->part_g, nullptr, m->fx.xl_o)))
+                return rc;
+        } else if ((rc = launch_attn_decode_fused(
+                        st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
+                        m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
+                        L.global ? 0u : L.slots, L.kq, L.ks, L.vq, L.vs, nq, nkv,
+                        decode_splits(L), c.attn_scale, nullptr, ctx_workspace(m->ctx),
+                        kWorkspaceBytes, m->fx.xl_o, kMergeInLaunch))) {
             return rc;
+        }
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
         GemvFuse eo{};
@@ -677,6 +884,15 @@ int record_step_fused(sgq_model *m, float *logits) {
         ed.u_out = m->fx.u, ed.A_out = m->fx.a, ed.B_out = m->fx.b, ed.part_out = m->fx.part;
         if ((rc = launch_gemv_fused(st, dt, m->fx.hl, (uint32_t)F, kProTable, kEpiResid, ed)))
             return rc;
+    }
+    if (c.embed_q6k) {
+        // the last layer's residual update and the output norm from the down
+        // GEMV's partial sums, then the Q6_K head over the fp32 row
+        hipLaunchKernelGGL(norm_from_partials_kernel, dim3(1), dim3(kRowWG), 0, st, m->fx.part,
+                           np_d, m->fx.a, m->fx.b, m->layers[nl - 1].out_scale, H, c.eps, m->xf);
+        SGQ_HIP(hipGetLastError());
+        return launch_gemv_q6_k(st, m->embd, m->embd_stride, m->xf, logits, c.vocab, (uint32_t)H,
+                                c.final_softcap);
     }
     GemvTargets head{};
     head.w[0] = m->embd, head.y[0] = logits, head.end[0] = (int)c.vocab, head.count = 1;
@@ -720,14 +936,26 @@ void sgq_model_default_config(sgq_model_config *c) {
 int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out) {
     if (!ctx || !cfg || !out) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     const sgq_model_config &c = *cfg;
-    SGQ_CHECK(c.head_dim == kHeadDim, "model: head_dim must be 128");
-    SGQ_CHECK(c.hidden % 256 == 0 && c.ffn % 256 == 0 && (c.n_q_heads * kHeadDim) % 256 == 0,
+    // per-kind geometry: sliding (head_dim, n_kv_heads) and global
+    const uint32_t hd_s = c.head_dim, hd_g = c.head_dim_global ? c.head_dim_global : c.head_dim;
+    const uint32_t kv_s = c.n_kv_heads, kv_g = c.n_kv_heads_global ? c.n_kv_heads_global : c.n_kv_heads;
+    const bool generic = hd_s != kHeadDim || hd_g != kHeadDim || kv_g != kv_s || c.embed_q6k;
+    auto ok_hd = [](uint32_t hd) { return hd == 128 || hd == 256 || hd == 512; };
+    auto ok_qpk = [&](uint32_t kv) {
+        if (kv == 0 || c.n_q_heads % kv) return false;
+        const uint32_t r = c.n_q_heads / kv;
+        return generic ? (r == 1 || r == 2 || r == 4 || r == 8) : r <= 2;
+    };
+    SGQ_CHECK(ok_hd(hd_s) && ok_hd(hd_g), "model: head_dim %u / %u (128, 256 or 512)", hd_s, hd_g);
+    SGQ_CHECK(ok_qpk(kv_s) && ok_qpk(kv_g),
+              "model: %u q heads over %u / %u kv heads (1 or 2 per kv head at the benchmark "
+              "geometry, 1/2/4/8 otherwise)", c.n_q_heads, kv_s, kv_g);
+    SGQ_CHECK(c.hidden % 256 == 0 && c.ffn % 256 == 0 && (c.n_q_heads * hd_s) % 256 == 0,
               "model: hidden, ffn and q_dim must be multiples of 256");
-    SGQ_CHECK(c.n_kv_heads > 0 && c.n_q_heads % c.n_kv_heads == 0 &&
-                  c.n_q_heads / c.n_kv_heads <= 2,
-              "model: 1 or 2 q heads per kv head");
     SGQ_CHECK(c.hidden <= 16384, "model: hidden above 16384 (row kernels)");
-    SGQ_CHECK(c.ffn <= 65536 && c.n_q_heads * kHeadDim <= 65536, "model: GEMV K above 65536");
+    SGQ_CHECK(c.ffn <= 65536 && c.n_q_heads * std::max(hd_s, hd_g) <= 65536,
+              "model: GEMV K above 65536");
+    SGQ_CHECK(!c.embed_q6k || c.hidden <= 6144, "model: Q6_K head needs hidden <= 6144");
     SGQ_CHECK(c.n_layers >= 1 && c.vocab >= 1 && c.max_ctx >= 1 && c.sliding_window >= 1,
               "model: empty dimension");
     SGQ_CHECK(c.global_every >= 1, "model: global_every must be >= 1");
@@ -740,29 +968,44 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
     auto *m = new sgq_model;
     m->ctx = ctx;
     m->cfg = c;
-    const size_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim,
-                 KD = c.n_kv_heads * kHeadDim;
+    m->generic = generic;
+    m->mode = generic ? 2 : 0;
+    const size_t H = c.hidden, F = c.ffn;
+    const size_t QD_max = c.n_q_heads * std::max(hd_s, hd_g),
+                 KD_max = std::max<size_t>((size_t)kv_s * hd_s, (size_t)kv_g * hd_g);
     int rc = SGQ_OK;
     auto fail_out = [&](int r) {
         sgq_model_destroy(m);
         return r;
     };
     uint64_t s = c.seed;
-    if ((rc = q4_tensor(m, c.vocab, H, mix(s, 1), &m->embd))) return fail_out(rc);
+    if (c.embed_q6k) {
+        m->embd_stride = ((H / 256) * 210 + 15) / 16 * 16;
+        if ((rc = alloc(m, c.vocab * m->embd_stride, &m->embd)) ||
+            (rc = launch_fill_q6k(ctx_stream(ctx), m->embd, c.vocab, (uint32_t)H, m->embd_stride,
+                                  mix(s, 1))))
+            return fail_out(rc);
+    } else {
+        m->embd_stride = (H / 32) * 18;
+        if ((rc = q4_tensor(m, c.vocab, H, mix(s, 1), &m->embd))) return fail_out(rc);
+    }
     if ((rc = f32_tensor(m, H, mix(s, 2), 1.0f, 0.1f, &m->out_norm))) return fail_out(rc);
     m->layers.resize(c.n_layers);
     for (uint32_t li = 0; li < c.n_layers; li++) {
         LayerW &L = m->layers[li];
         const uint64_t ls = mix(s, 1000 + li);
         L.global = (li % c.global_every) == c.global_every - 1;
+        L.hd = L.global ? hd_g : hd_s;
+        L.n_kv = L.global ? kv_g : kv_s;
+        const size_t QD = c.n_q_heads * L.hd, KD = (size_t)L.n_kv * L.hd;
         if ((rc = q4_tensor(m, QD, H, mix(ls, 1), &L.wq)) || (rc = q4_tensor(m, KD, H, mix(ls, 2), &L.wk)) ||
             (!(L.global && c.global_k_eq_v) && (rc = q4_tensor(m, KD, H, mix(ls, 3), &L.wv))) ||
             (rc = q4_tensor(m, H, QD, mix(ls, 4), &L.wo)) ||
             (rc = q4_tensor(m, F, H, mix(ls, 5), &L.wg)) || (rc = q4_tensor(m, F, H, mix(ls, 6), &L.wu)) ||
             (rc = q4_tensor(m, H, F, mix(ls, 7), &L.wd)) ||
             (rc = f32_tensor(m, H, mix(ls, 8), 1.f, 0.1f, &L.attn_norm)) ||
-            (rc = f32_tensor(m, kHeadDim, mix(ls, 9), 1.f, 0.1f, &L.q_norm)) ||
-            (rc = f32_tensor(m, kHeadDim, mix(ls, 10), 1.f, 0.1f, &L.k_norm)) ||
+            (rc = f32_tensor(m, L.hd, mix(ls, 9), 1.f, 0.1f, &L.q_norm)) ||
+            (rc = f32_tensor(m, L.hd, mix(ls, 10), 1.f, 0.1f, &L.k_norm)) ||
             (rc = f32_tensor(m, H, mix(ls, 11), 1.f, 0.1f, &L.post_attn_norm)) ||
             (rc = f32_tensor(m, H, mix(ls, 12), 1.f, 0.1f, &L.ffn_norm)) ||
             (rc = f32_tensor(m, H, mix(ls, 13), 1.f, 0.1f, &L.post_ffw_norm)) ||
@@ -777,22 +1020,34 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
             return fail_out(rc);
     }
     float **acts[] = {&m->x, &m->q_raw, &m->k_raw, &m->v_raw, &m->q, &m->attn, &m->o, &m->g, &m->u, &m->f};
-    const size_t act_n[] = {H, QD, KD, KD, QD, QD, H, F, F, 4 * H};  // f: up to 4 K-slices
+    const size_t act_n[] = {H, QD_max, KD_max, KD_max, QD_max, QD_max, H, F, F, 4 * H};  // f: up to 4 K-slices
     for (int i = 0; i < 10; i++)
         if ((rc = alloc(m, act_n[i] * 4, reinterpret_cast<void **>(acts[i])))) return fail_out(rc);
-    if ((rc = alloc(m, std::max(H, F) / 32 * sizeof(BlockLimbs), &m->xl))) return fail_out(rc);
+    if ((rc = alloc(m, std::max({H, F, QD_max}) / 32 * sizeof(BlockLimbs), &m->xl))) return fail_out(rc);
     {
         float **fb[] = {&m->fx.xb, &m->fx.u, &m->fx.a, &m->fx.b};
         for (float **b : fb)
             if ((rc = alloc(m, H * 4, reinterpret_cast<void **>(b)))) return fail_out(rc);
         if ((rc = alloc(m, kGemvMaxPartials * sizeof(float4), reinterpret_cast<void **>(&m->fx.part))) ||
-            (rc = alloc(m, QD / 32 * sizeof(BlockLimbs), &m->fx.xl_o)) ||
+            (rc = alloc(m, QD_max / 32 * sizeof(BlockLimbs), &m->fx.xl_o)) ||
             (rc = alloc(m, F / 32 * sizeof(BlockLimbs), &m->fx.hl)))
             return fail_out(rc);
     }
     if ((rc = alloc(m, 64, reinterpret_cast<void **>(&m->step)))) return fail_out(rc);
     if ((rc = alloc(m, 2 * kHeadDim * 4, reinterpret_cast<void **>(&m->rope_cs))))
         return fail_out(rc);
+    {   // mode 3 buffers
+        uint32_t max_splits = 1;
+        for (const LayerW &L : m->layers) max_splits = std::max<uint32_t>(max_splits, attn_generic_splits(L.slots));
+        if ((rc = alloc(m, (hd_s + hd_g) * 4, reinterpret_cast<void **>(&m->rope_g))) ||
+            (rc = alloc(m, KD_max * 4, reinterpret_cast<void **>(&m->kx))) ||
+            (rc = alloc(m, KD_max * 4, reinterpret_cast<void **>(&m->vx))) ||
+            (rc = alloc(m, (size_t)c.n_q_heads * max_splits * (std::max(hd_s, hd_g) + 2) * 4,
+                        reinterpret_cast<void **>(&m->part_g))) ||
+            (rc = alloc(m, H * 4, reinterpret_cast<void **>(&m->xf))) ||
+            (rc = alloc(m, (size_t)c.vocab * 4, reinterpret_cast<void **>(&m->logits_tmp))))
+            return fail_out(rc);
+    }
     if (hipStreamSynchronize(ctx_stream(ctx)) != hipSuccess) return fail_out(fail(SGQ_ERR_HIP, "init sync"));
     *out = m;
     return SGQ_OK;
@@ -826,6 +1081,14 @@ static int write_step(sgq_model *m, uint32_t token) {
                        (int)lroundf(c.global_rope_frac * kHeadDim / 2),
                        m->mode == 1 ? m->sync : nullptr, m->n_sync);
     SGQ_HIP(hipGetLastError());
+    if (m->mode == 3 || m->generic) {
+        const int hd_s = (int)c.head_dim, hd_g = (int)(c.head_dim_global ? c.head_dim_global : c.head_dim);
+        hipLaunchKernelGGL(rope_table_generic_kernel, dim3((hd_s / 2 + hd_g / 2 + 255) / 256),
+                           dim3(256), 0, ctx_stream(m->ctx), m->step, m->rope_g, hd_s, hd_g,
+                           c.rope_theta_sliding, c.rope_theta_global,
+                           (int)lroundf(c.global_rope_frac * hd_g / 2));
+        SGQ_HIP(hipGetLastError());
+    }
     return SGQ_OK;
 }
 
@@ -842,6 +1105,7 @@ int sgq_model_decode(sgq_model *m, uint32_t token, float *logits) {
     if (rc) return rc;
     if ((rc = m->mode == 1   ? persistent_step(m, logits)
                : m->mode == 2 ? record_step_fused(m, logits)
+               : m->mode == 3 ? record_step_generic(m, logits, true)
                               : record_step(m, logits)))
         return rc;
     m->pos++;
@@ -861,7 +1125,9 @@ int sgq_model_decode_graph(sgq_model *m, uint32_t token, float *logits) {
             m->graph = nullptr;
         }
         if ((rc = sgq_graph_begin(m->ctx))) return rc;
-        rc = m->mode == 2 ? record_step_fused(m, logits) : record_step(m, logits);
+        rc = m->mode == 2   ? record_step_fused(m, logits)
+             : m->mode == 3 ? record_step_generic(m, logits, true)
+                            : record_step(m, logits);
         sgq_graph *g = nullptr;
         const int rc2 = sgq_graph_end(m->ctx, &g);
         if (rc) {
@@ -961,8 +1227,11 @@ static int persistent_setup(sgq_model *m) {
 
 int sgq_model_set_decode_mode(sgq_model *m, int mode) {
     if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
-    SGQ_CHECK(mode >= 0 && mode <= 2, "model: decode mode %d (0 kernels, 1 persistent, 2 fused)",
-              mode);
+    SGQ_CHECK(mode >= 0 && mode <= 3,
+              "model: decode mode %d (0 kernels, 1 persistent, 2 fused, 3 any geometry)", mode);
+    SGQ_CHECK(!m->generic || mode >= 2,
+              "model: this geometry (head_dim %u/%u, Q6_K embedding %u) runs in modes 2 and 3 only",
+              m->cfg.head_dim, m->cfg.head_dim_global, m->cfg.embed_q6k);
     if (mode == 1 && !m->err)
         if (int rc = persistent_setup(m)) return rc;
     if (mode != m->mode && m->graph) {  // a captured step belongs to one mode
@@ -993,15 +1262,16 @@ int sgq_model_fill_cache(sgq_model *m, uint32_t n_tokens, uint64_t seed) {
     if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
     const sgq_model_config &c = m->cfg;
     SGQ_CHECK(n_tokens <= c.max_ctx, "model: fill_cache %u > max_ctx %u", n_tokens, c.max_ctx);
-    const size_t KD = (size_t)c.n_kv_heads * kHeadDim;
     hipStream_t st = ctx_stream(m->ctx);
     size_t most = 0;
-    for (const LayerW &L : m->layers) most = std::max(most, (size_t)std::min(n_tokens, L.slots));
+    for (const LayerW &L : m->layers)
+        most = std::max(most, (size_t)std::min(n_tokens, L.slots) * L.n_kv * L.hd);
     float *tmp = nullptr;
-    if (most) SGQ_HIP(hipMalloc(&tmp, most * KD * 4));
+    if (most) SGQ_HIP(hipMalloc(&tmp, most * 4));
     int rc = SGQ_OK;
     for (size_t li = 0; li < m->layers.size() && !rc; li++) {
         const LayerW &L = m->layers[li];
+        const size_t KD = (size_t)L.n_kv * L.hd;
         const size_t rows = std::min(n_tokens, L.slots);
         if (!rows) continue;
         for (int kv = 0; kv < 2 && !rc; kv++) {
@@ -1140,6 +1410,19 @@ int sgq_model_prefill(sgq_model *m, const uint32_t *tokens, uint32_t n_tokens, f
     for (uint32_t i = 0; i < n_tokens; i++)
         SGQ_CHECK(tokens[i] < c.vocab, "model: token %u at %u >= vocab %u", tokens[i], i, c.vocab);
     int rc;
+    if (m->generic) {
+        // any-geometry models: the prompt as successive decode steps (mode 3),
+        // logits of the last token only
+        for (uint32_t i = 0; i < n_tokens; i++) {
+            const bool last = i + 1 == n_tokens;
+            if ((rc = write_step(m, tokens[i])) ||
+                (rc = record_step_generic(m, last && logits ? logits : m->logits_tmp,
+                                          last && logits)))
+                return rc;
+            m->pos++;
+        }
+        return SGQ_OK;
+    }
     if (!m->pf.chunk && (rc = pf_alloc(m))) return rc;
     hipStream_t st = ctx_stream(m->ctx);
     uint32_t M = 0;
@@ -1167,35 +1450,38 @@ int sgq_model_prefill(sgq_model *m, const uint32_t *tokens, uint32_t n_tokens, f
 int sgq_model_load_gguf(sgq_model *m, const sgq_gguf *g) {
     if (!m || !g) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     const sgq_model_config &c = m->cfg;
-    const uint64_t H = c.hidden, F = c.ffn, QD = (uint64_t)c.n_q_heads * kHeadDim,
-                   KD = (uint64_t)c.n_kv_heads * kHeadDim;
+    const uint64_t H = c.hidden, F = c.ffn;
+    // the tensor table of crates/sg-gguf/src/desc.rs:150-193 at this model's
+    // geometry: per-kind q/kv dims and norm lengths, attn_v absent on layers
+    // that share K=V, token_embd Q4_0 or Q6_K (type 14)
+    constexpr uint32_t kQ6K = 14;
     struct Want {
         std::string name;
         const char *model_name;
         int layer;
-        uint32_t type;  // 0 F32, 2 Q4_0
+        uint32_t type;  // 0 F32, 2 Q4_0, 14 Q6_K
         uint64_t d0, d1;
-        bool optional;
     };
-    std::vector<Want> want = {{"token_embd.weight", "token_embd", -1, 2, H, c.vocab, false},
-                              {"output_norm.weight", "output_norm", -1, 0, H, 1, false}};
+    std::vector<Want> want = {{"token_embd.weight", "token_embd", -1, c.embed_q6k ? kQ6K : 2u, H, c.vocab},
+                              {"output_norm.weight", "output_norm", -1, 0, H, 1}};
     for (uint32_t l = 0; l < c.n_layers; l++) {
+        const LayerW &L = m->layers[l];
+        const uint64_t QD = (uint64_t)c.n_q_heads * L.hd, KD = (uint64_t)L.n_kv * L.hd;
         const std::string b = "blk." + std::to_string(l) + ".";
-        const bool kv_shared = m->layers[l].wv == nullptr;
-        want.push_back({b + "attn_q.weight", "attn_q", (int)l, 2, H, QD, false});
-        want.push_back({b + "attn_k.weight", "attn_k", (int)l, 2, H, KD, false});
-        if (!kv_shared) want.push_back({b + "attn_v.weight", "attn_v", (int)l, 2, H, KD, false});
-        want.push_back({b + "attn_output.weight", "attn_output", (int)l, 2, QD, H, false});
-        want.push_back({b + "attn_q_norm.weight", "attn_q_norm", (int)l, 0, kHeadDim, 1, false});
-        want.push_back({b + "attn_k_norm.weight", "attn_k_norm", (int)l, 0, kHeadDim, 1, false});
-        want.push_back({b + "attn_norm.weight", "attn_norm", (int)l, 0, H, 1, false});
-        want.push_back({b + "post_attention_norm.weight", "post_attention_norm", (int)l, 0, H, 1, false});
-        want.push_back({b + "ffn_norm.weight", "ffn_norm", (int)l, 0, H, 1, false});
-        want.push_back({b + "post_ffw_norm.weight", "post_ffw_norm", (int)l, 0, H, 1, false});
-        want.push_back({b + "ffn_gate.weight", "ffn_gate", (int)l, 2, H, F, false});
-        want.push_back({b + "ffn_up.weight", "ffn_up", (int)l, 2, H, F, false});
-        want.push_back({b + "ffn_down.weight", "ffn_down", (int)l, 2, F, H, false});
-        want.push_back({b + "layer_output_scale.weight", "layer_output_scale", (int)l, 0, 1, 1, false});
+        want.push_back({b + "attn_q.weight", "attn_q", (int)l, 2, H, QD});
+        want.push_back({b + "attn_k.weight", "attn_k", (int)l, 2, H, KD});
+        if (L.wv) want.push_back({b + "attn_v.weight", "attn_v", (int)l, 2, H, KD});
+        want.push_back({b + "attn_output.weight", "attn_output", (int)l, 2, QD, H});
+        want.push_back({b + "attn_q_norm.weight", "attn_q_norm", (int)l, 0, L.hd, 1});
+        want.push_back({b + "attn_k_norm.weight", "attn_k_norm", (int)l, 0, L.hd, 1});
+        want.push_back({b + "attn_norm.weight", "attn_norm", (int)l, 0, H, 1});
+        want.push_back({b + "post_attention_norm.weight", "post_attention_norm", (int)l, 0, H, 1});
+        want.push_back({b + "ffn_norm.weight", "ffn_norm", (int)l, 0, H, 1});
+        want.push_back({b + "post_ffw_norm.weight", "post_ffw_norm", (int)l, 0, H, 1});
+        want.push_back({b + "ffn_gate.weight", "ffn_gate", (int)l, 2, H, F});
+        want.push_back({b + "ffn_up.weight", "ffn_up", (int)l, 2, H, F});
+        want.push_back({b + "ffn_down.weight", "ffn_down", (int)l, 2, F, H});
+        want.push_back({b + "layer_output_scale.weight", "layer_output_scale", (int)l, 0, 1, 1});
     }
     // Check everything before writing anything.
     std::vector<sgq_gguf_tensor> found(want.size());
@@ -1213,11 +1499,12 @@ int sgq_model_load_gguf(sgq_model *m, const sgq_gguf *g) {
     sgq_gguf_tensor rf;
     if (sgq_gguf_tensor_find(g, "rope_freqs.weight", &rf) == SGQ_OK) {
         // divisor factors of the global layers' partial rotation (rope.rs:13-16)
-        const int live = (int)lroundf(c.global_rope_frac * kHeadDim / 2);
-        SGQ_CHECK(rf.type == 0 && rf.dims[0] == kHeadDim / 2 && rf.n_dims == 1,
-                  "gguf: rope_freqs.weight must be F32 [%d]", kHeadDim / 2);
+        const int half = (int)(c.head_dim_global ? c.head_dim_global : c.head_dim) / 2;
+        const int live = (int)lroundf(c.global_rope_frac * half);
+        SGQ_CHECK(rf.type == 0 && rf.dims[0] == (uint64_t)half && rf.n_dims == 1,
+                  "gguf: rope_freqs.weight must be F32 [%d]", half);
         const float *f = static_cast<const float *>(rf.data);
-        for (int i = 0; i < kHeadDim / 2; i++)
+        for (int i = 0; i < half; i++)
             SGQ_CHECK(i < live ? f[i] == 1.0f : f[i] >= 1e20f,
                       "gguf: rope_freqs.weight[%d] = %g does not match global_rope_frac", i, f[i]);
     }
@@ -1226,6 +1513,16 @@ int sgq_model_load_gguf(sgq_model *m, const sgq_gguf *g) {
         void *dst;
         uint64_t bytes;
         if (int rc = sgq_model_tensor(m, want[i].layer, want[i].model_name, &dst, &bytes)) return rc;
+        if (want[i].type == kQ6K) {
+            // GGUF rows are k/256·210 bytes; the device rows are padded
+            const uint64_t row = (H / 256) * 210;
+            SGQ_CHECK(found[i].bytes == row * c.vocab, "gguf: token_embd is %llu bytes, not %llu",
+                      (unsigned long long)found[i].bytes, (unsigned long long)(row * c.vocab));
+            SGQ_HIP(hipMemsetAsync(dst, 0, bytes, st));
+            SGQ_HIP(hipMemcpy2DAsync(dst, m->embd_stride, found[i].data, row, row, c.vocab,
+                                     hipMemcpyHostToDevice, st));
+            continue;
+        }
         SGQ_CHECK(bytes == found[i].bytes, "gguf: tensor '%s' is %llu bytes, the model's %llu",
                   want[i].name.c_str(), (unsigned long long)found[i].bytes, (unsigned long long)bytes);
         SGQ_HIP(hipMemcpyAsync(dst, found[i].data, bytes, hipMemcpyHostToDevice, st));
@@ -1238,11 +1535,15 @@ int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr
                      uint64_t *bytes) {
     if (!m || !name || !ptr || !bytes) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     const sgq_model_config &c = m->cfg;
-    const size_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim;
+    const uint32_t hd_max = std::max(c.head_dim, c.head_dim_global);
+    const size_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * hd_max;
+    size_t KD = 0;
+    for (const LayerW &L : m->layers) KD = std::max(KD, (size_t)L.n_kv * L.hd);
     auto q4 = [](size_t r, size_t k) { return (uint64_t)(r * (k / 32) * 18); };
     std::string n(name);
     if (layer < 0) {
-        if (n == "token_embd") { *ptr = m->embd; *bytes = q4(c.vocab, H); return SGQ_OK; }
+        // token_embd: Q4_0 rows, or Q6_K rows padded to embd_stride bytes
+        if (n == "token_embd") { *ptr = m->embd; *bytes = (uint64_t)c.vocab * m->embd_stride; return SGQ_OK; }
         if (n == "output_norm") { *ptr = m->out_norm; *bytes = H * 4; return SGQ_OK; }
         if (n == "x") { *ptr = m->x; *bytes = H * 4; return SGQ_OK; }
         // decode-step activations (the last layer's, after a step)
@@ -1265,12 +1566,14 @@ int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr
     SGQ_CHECK(layer < (int)m->layers.size(), "model: layer %d out of range", layer);
     const LayerW &L = m->layers[layer];
     struct E { const char *n; void *p; uint64_t b; };
-    const uint64_t kvn = (uint64_t)L.slots * KD;
+    const size_t hd = L.hd;
+    const size_t QDl = c.n_q_heads * hd, KDl = (size_t)L.n_kv * hd;
+    const uint64_t kvn = (uint64_t)L.slots * KDl;
     const E table[] = {
-        {"attn_q", L.wq, q4(QD, H)}, {"attn_k", L.wk, q4(KD, H)}, {"attn_v", L.wv, q4(KD, H)},
-        {"attn_output", L.wo, q4(H, QD)}, {"ffn_gate", L.wg, q4(F, H)}, {"ffn_up", L.wu, q4(F, H)},
+        {"attn_q", L.wq, q4(QDl, H)}, {"attn_k", L.wk, q4(KDl, H)}, {"attn_v", L.wv, q4(KDl, H)},
+        {"attn_output", L.wo, q4(H, QDl)}, {"ffn_gate", L.wg, q4(F, H)}, {"ffn_up", L.wu, q4(F, H)},
         {"ffn_down", L.wd, q4(H, F)}, {"attn_norm", L.attn_norm, H * 4},
-        {"attn_q_norm", L.q_norm, kHeadDim * 4}, {"attn_k_norm", L.k_norm, kHeadDim * 4},
+        {"attn_q_norm", L.q_norm, hd * 4}, {"attn_k_norm", L.k_norm, hd * 4},
         {"post_attention_norm", L.post_attn_norm, H * 4}, {"ffn_norm", L.ffn_norm, H * 4},
         {"post_ffw_norm", L.post_ffw_norm, H * 4}, {"layer_output_scale", L.out_scale, 4},
         {"k_quants", L.kq, kvn}, {"v_quants", L.vq, kvn}, {"k_scales", L.ks, kvn / 16},

@@ -156,6 +156,25 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
                              float scale, float *part);
 int launch_attn_reduce(hipStream_t st, const float *part, int n_q, int n_kv, int n_splits,
                        float *out);
+// Decode attention at head_dim 128/256/512 and 1/2/4/8 query heads per kv
+// head (attn_generic.hip).  Post-projection: q/k norms (weights q_norm,
+// k_norm), weightless v norm, NEOX RoPE of q and k with cos_sin [head_dim/2
+// pairs], q -> q_out [n_q × head_dim], k and v quantized (Q8_0) into slot
+// step[0] (mod ring when ring > 0).  Attention: splits of 64 slots
+// (attn_generic_splits(slots) of them cover a cache of `slots`), kv_len =
+// step[step_word], partials in part [n_q × n_splits × (head_dim+2)], merged
+// in split order into out [n_q × head_dim] and/or the x limbs xl.
+int attn_generic_splits(uint32_t slots);
+int launch_attn_postproj_generic(hipStream_t st, const float *q_raw, const float *k_raw,
+                                 const float *v_src, const float *q_norm, const float *k_norm,
+                                 const float *cos_sin, float eps, const uint32_t *step,
+                                 uint32_t ring, int n_q, int n_kv, int head_dim, float *q_out,
+                                 uint16_t *ks, int8_t *kq, uint16_t *vs, int8_t *vq);
+int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
+                               const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
+                               const uint32_t *step, int step_word, int n_q, int n_kv,
+                               int head_dim, int n_splits, float scale, float *part, float *out,
+                               void *xl);
 // Sets the attention kernels' launch attributes (call before graph capture).
 int attn_prepare();
 // Decode attention with the step's q/k/v post-projection fused in (and,
@@ -191,6 +210,9 @@ int launch_add_scaled(hipStream_t st, const float *a, const float *b, float *y, 
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);
+// Random Q6_K rows (k/256 blocks of 210 B) at a byte stride, padding zeroed.
+int launch_fill_q6k(hipStream_t st, void *w, uint64_t n_rows, uint32_t k, uint64_t row_stride,
+                    uint64_t seed);
 
 }  // namespace sgq
 

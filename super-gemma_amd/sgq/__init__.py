@@ -80,7 +80,9 @@ class ModelConfig(C.Structure):
         "sliding_window", "global_every", "max_ctx")] + [(n, C.c_float) for n in (
         "rope_theta_sliding", "rope_theta_global", "global_rope_frac", "eps", "attn_scale",
         "final_softcap", "weight_sigma")] + [("global_k_eq_v", C.c_uint32),
-                                             ("prefill_chunk", C.c_uint32), ("seed", C.c_uint64)]
+                                             ("prefill_chunk", C.c_uint32), ("seed", C.c_uint64)] + [
+        (n, C.c_uint32) for n in ("head_dim_global", "n_kv_heads_global", "embed_q6k",
+                                  "reserved")]
 
     def as_dict(self):
         return {n: getattr(self, n) for n, _ in self._fields_}

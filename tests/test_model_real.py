@@ -1,0 +1,291 @@
+"""GPU parity: the decoder at the real checkpoint's geometry (scope row f3)
+against the CPU oracle decoder, and GGUF files with its tensor table.
+
+Geometry of crates/sg-gguf/src/desc.rs:66-93 at a small width: 32 query
+heads; sliding layers 16 kv heads of 256; global layers 4 kv heads of 512
+with K=V (no attn_v tensor); the tied embedding / LM head in Q6_K
+(q6_k.rs:25-62, rows padded to 16 bytes on the device as the reference
+uploads them); rope_freqs of 256 factors for the global layers' partial
+rotation.  These models decode in mode 2 (the fused GEMVs of the
+benchmark's step around the any-geometry attention: post-projection, VALU
+split attention at head_dim 256/512 with 2 or 8 query heads per kv head, a
+merge into the O projection's limbs; the Q6_K head after a norm from the
+down GEMV's partial sums) or mode 3 (one kernel per operator), and prefill
+as successive mode-3 decode steps.  Bar: the logits bar of tests/test_model.py;
+the head rounds x to f16 (gemv_q6_k_logits semantics), the oracle uses the
+fp32 x in an f64 dot.  The oracle attends the device's K/V pages after
+checking them against its own Q8_0 rows (_device_kv).
+"""
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from _util import empty, host
+from test_model import _check_logits, _weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _device_kv(model, oracle, flips):
+    """OracleDecoder.kv_source: the device's dequantized K/V rows of (layer,
+    position), after checking them against the oracle's own Q8_0 rows.  Per
+    32-element block: the f16 scales agree within one ulp (amax/127 sits
+    near a rounding boundary when the GPU's and the oracle's inputs differ
+    by float noise; such a block then differs everywhere, by at most a step
+    and 127 scale ulps); in blocks whose scales agree, every element within
+    one step (a quant flips where the inputs straddle a rounding boundary).
+    The counts (flipped quants, blocks with another scale) are a loose
+    sanity bound only: the noise grows with depth and position (up to ~27%
+    of a row's blocks and ~1.5% of its quants at 520 positions).  At this
+    geometry one flip moves a score by a whole step, and the 4-kv-head,
+    head_dim-512 attention amplifies it past the logits bar (the oracle
+    against itself with 2e-5 relative noise on every linear output: up to
+    1.8e-2 with its own Q8 pages, 4e-4 with shared ones), so the oracle
+    attends the device's pages."""
+    def src(layer, pos, k_row, v_row):
+        L = model.cfg
+        glob = layer % L.global_every == L.global_every - 1
+        hd = L.head_dim_global if glob else L.head_dim
+        nkv = L.n_kv_heads_global if glob else L.n_kv_heads
+        slots = L.max_ctx if glob else min(L.sliding_window, L.max_ctx)
+        slot = pos if glob else pos % slots
+        row = nkv * hd
+        out = []
+        for kind, mine in (("k", k_row), ("v", v_row)):
+            q = model.read_tensor(f"{kind}_quants", layer, np.int8).reshape(slots, row)[slot]
+            sc = model.read_tensor(f"{kind}_scales", layer, np.uint16).reshape(slots, row // 32)[slot]
+            dev = oracle.dequant_q8_0(sc, q)
+            # the oracle's block scale: its largest |q| is 127
+            mine_sc = np.abs(mine.reshape(-1, 32)).max(axis=1) / np.float32(127)
+            mine_bits = mine_sc.astype(np.float16).view(np.uint16)
+            ulps = np.abs(mine_bits.astype(np.int32) - sc.astype(np.int32))
+            assert (ulps <= 1).all(), (kind, layer, pos, ulps.max())
+            same = np.repeat(ulps == 0, 32)
+            step = np.repeat(oracle.f16_bits_to_f32(sc), 32)
+            diff = np.abs(dev - mine)
+            # one step, plus 127 scale ulps (2^-10 relative) where the scales differ
+            tol = step * np.where(same, 1.0001, 1.0001 + 127.0 / 1024)
+            assert (diff <= tol + 1e-30).all(), (kind, layer, pos, (diff / step).max())
+            flips.append(int((diff[same] > 0).sum()))
+            assert flips[-1] <= row // 10, (kind, layer, pos, flips[-1])
+            assert (~same).sum() <= row // 2, (kind, layer, pos, int((~same).sum()) // 32)
+            out.append(dev)
+        return out[0], out[1]
+    return src
+
+
+def _real_cfg(sgq, **kw):
+    base = dict(n_layers=6, hidden=512, ffn=1024, n_q_heads=32, n_kv_heads=16, head_dim=256,
+                head_dim_global=512, n_kv_heads_global=4, embed_q6k=1, vocab=1024,
+                sliding_window=4, global_every=3, max_ctx=24, seed=0x31B)
+    base.update(kw)
+    return sgq.default_model_config(**base)
+
+
+@pytest.mark.parametrize("mode", [2, 3])
+def test_real_geometry_decode_matches_oracle(ctx, oracle, mode):
+    """6 layers (4 sliding with a 4-slot ring, 2 global), 10 steps: the ring
+    wraps twice and the global layers grow."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print(f"real geometry decode, mode {mode}", flush=True)
+    cfg = _real_cfg(sgq)
+    model = sgq.Model(ctx, cfg)
+    assert model.decode_mode == 2
+    model.decode_mode = mode
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    flips = []
+    ref.kv_source = _device_kv(model, oracle, flips)
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([1, 1023, 5, 5, 100, 0, 999, 42, 7, 3]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    for bad in (0, 1):  # the head_dim-128 kernels only
+        with pytest.raises(sgq.ValidationError):
+            model.decode_mode = bad
+    model.close()
+
+
+@pytest.mark.parametrize("mode", [2, 3])
+def test_real_geometry_long_context_matches_oracle(ctx, oracle, mode):
+    """A full 256-slot sliding ring that wraps (4 splits of 64 slots) and
+    global layers over ~520 positions (9 splits, the last one partial):
+    synthetic K/V pages (sgq_model_fill_cache) read back into the oracle."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print(f"real geometry long context, mode {mode}", flush=True)
+    cfg = _real_cfg(sgq, sliding_window=256, max_ctx=600, seed=0x31E)
+    model = sgq.Model(ctx, cfg)
+    model.decode_mode = mode
+    model.fill_cache(517)
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    pages = {}
+    for l in range(cfg.n_layers):
+        for kind in ("k", "v"):
+            pages[(l, kind)] = (model.read_tensor(f"{kind}_scales", l, np.uint16),
+                                model.read_tensor(f"{kind}_quants", l, np.int8))
+    ref.preload_cache(pages, 517)
+    ref.kv_source = _device_kv(model, oracle, [])
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([11, 900, 2, 77]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
+
+
+def test_real_geometry_prefill_graph_and_decode(ctx, oracle):
+    """Prefill (successive decode steps) then decode, against the oracle's
+    token-by-token decode; the recorded graph replays the step bit for bit."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print("real geometry prefill + graph", flush=True)
+    # no ring wrap inside the prompt: the oracle reads the device's pages of
+    # every prompt position after the whole prefill
+    cfg = _real_cfg(sgq, seed=0x31C, sliding_window=24)
+    model = sgq.Model(ctx, cfg)
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    ref.kv_source = _device_kv(model, oracle, [])
+    toks = [3, 14, 159, 265, 358, 979]
+    logits = empty(cfg.vocab, torch.float32)
+    model.prefill(toks, logits)
+    torch.cuda.synchronize()
+    for t in toks:
+        want = ref.decode(t)
+    _check_logits(host(logits), want, "prefill")
+    eager = sgq.Model(ctx, cfg)
+    eager.prefill(toks)
+    s = torch.cuda.Stream()
+    ctx.set_stream(s)
+    try:
+        a = empty(cfg.vocab, torch.float32)
+        for i, t in enumerate([7, 77, 777]):
+            model.decode(t, logits, graph=True)
+            eager.decode(t, a)
+            ctx.synchronize()
+            g, e = host(logits), host(a)
+            assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), f"replay {i}"
+            _check_logits(g, ref.decode(t), f"graph {i}")
+    finally:
+        ctx.set_stream(None)
+    model.close()
+    eager.close()
+
+
+def test_benchmark_geometry_mode3_matches_oracle(ctx, oracle):
+    """Mode 3 at the benchmark's geometry (head_dim 128, Q4_0 head) is the same
+    model as modes 0 and 2: checked against the oracle."""
+    import sgq
+    from oracle.model import OracleDecoder
+    from test_model import _small_cfg
+
+    print("benchmark geometry in mode 3", flush=True)
+    cfg = _small_cfg(sgq, seed=0x3E)
+    model = sgq.Model(ctx, cfg)
+    model.decode_mode = 3
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([1, 2047, 5, 100, 0, 1999]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
+
+
+def _write_real_gguf(path, cfg, oracle, seed):
+    """The reference's tensor table (desc.rs:150-193) at cfg's geometry: Q6_K
+    token_embd (unpadded rows), rope_freqs [head_dim_global/2], no attn_v on
+    global layers."""
+    from _gguf import write_gguf
+
+    rng = oracle.Rng(seed)
+    H, F = cfg.hidden, cfg.ffn
+    row = (H // 256) * 210
+    emb = rng.random_q6_k_rows(cfg.vocab, H, row).tobytes()
+
+    def q4(k, n):
+        return rng.random_q4_0(n * k // 32).tobytes()
+
+    def f32(n):
+        return (np.float32(1.0) + np.float32(0.1) * rng.f32_vec(n)).astype(np.float32).tobytes()
+
+    half = cfg.head_dim_global // 2
+    live = int(round(cfg.global_rope_frac * half))
+    t = [("token_embd.weight", [H, cfg.vocab], "Q6_K", emb),
+         ("output_norm.weight", [H], "F32", f32(H)),
+         ("rope_freqs.weight", [half], "F32",
+          np.array([1.0] * live + [1e30] * (half - live), np.float32).tobytes())]
+    for l in range(cfg.n_layers):
+        glob = l % cfg.global_every == cfg.global_every - 1
+        hd = cfg.head_dim_global if glob else cfg.head_dim
+        nkv = cfg.n_kv_heads_global if glob else cfg.n_kv_heads
+        QD, KD = cfg.n_q_heads * hd, nkv * hd
+        b = f"blk.{l}."
+        t += [(b + "attn_q.weight", [H, QD], "Q4_0", q4(H, QD)),
+              (b + "attn_k.weight", [H, KD], "Q4_0", q4(H, KD))]
+        if not glob:
+            t.append((b + "attn_v.weight", [H, KD], "Q4_0", q4(H, KD)))
+        t += [(b + "attn_output.weight", [QD, H], "Q4_0", q4(QD, H)),
+              (b + "attn_q_norm.weight", [hd], "F32", f32(hd)),
+              (b + "attn_k_norm.weight", [hd], "F32", f32(hd)),
+              (b + "attn_norm.weight", [H], "F32", f32(H)),
+              (b + "post_attention_norm.weight", [H], "F32", f32(H)),
+              (b + "ffn_norm.weight", [H], "F32", f32(H)),
+              (b + "post_ffw_norm.weight", [H], "F32", f32(H)),
+              (b + "ffn_gate.weight", [H, F], "Q4_0", q4(H, F)),
+              (b + "ffn_up.weight", [H, F], "Q4_0", q4(H, F)),
+              (b + "ffn_down.weight", [F, H], "Q4_0", q4(F, H)),
+              (b + "layer_output_scale.weight", [1], "F32", struct.pack("<f", 0.9))]
+    write_gguf(path, [("general.architecture", "str", "gemma4")], t)
+    return {name: blob for name, _, _, blob in t}
+
+
+def test_real_geometry_gguf_loads_and_decodes(ctx, oracle, tmp_path):
+    """A GGUF with the real checkpoint's tensor table loads (Q6_K rows land at
+    the padded device stride, every other tensor byte for byte) and the model
+    then decodes the file's weights as the oracle does; a file of the
+    benchmark geometry is refused by this model."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print("real geometry gguf", flush=True)
+    cfg = _real_cfg(sgq, seed=0x31D)
+    path = tmp_path / "real.gguf"
+    blobs = _write_real_gguf(path, cfg, oracle, 0x99)
+    model = sgq.Model(ctx, cfg)
+    g = sgq.Gguf(str(path))
+    model.load_gguf(g)
+    H = cfg.hidden
+    row, stride = (H // 256) * 210, ((H // 256) * 210 + 15) // 16 * 16
+    dev_emb = model.read_tensor("token_embd").reshape(cfg.vocab, stride)
+    assert dev_emb[:, :row].tobytes() == blobs["token_embd.weight"]
+    assert not dev_emb[:, row:].any()
+    assert model.read_tensor("attn_q", 2).tobytes() == blobs["blk.2.attn_q.weight"]
+    assert model.read_tensor("attn_k_norm", 5).tobytes() == blobs["blk.5.attn_k_norm.weight"]
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    ref.kv_source = _device_kv(model, oracle, [])
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([3, 1000, 17, 4]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), f"gguf {i}")
+    g.close()
+    # a benchmark-geometry file (head_dim 128 everywhere, Q4_0 embedding)
+    from test_model import _small_cfg, _write_model_gguf
+
+    small = tmp_path / "small.gguf"
+    _write_model_gguf(small, _small_cfg(sgq, hidden=512), oracle, 0x66)
+    with pytest.raises(sgq.ValidationError):
+        model.load_gguf(sgq.Gguf(str(small)))
+    model.close()

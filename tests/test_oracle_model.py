@@ -45,17 +45,27 @@ def _cfg(**kw):
 
 def _weights(c, seed=0x51DE, sigma_scale=1.0):
     """Q4_0 matrices from the reference generator (d = |N(0,0.02)|), norm
-    weights around 1, layer_output_scale 1."""
+    weights around 1, layer_output_scale 1; per-kind geometry and a Q6_K
+    embedding (padded rows) when the config asks for them."""
     rng = O.Rng(seed)
-    H, F, hd = c["hidden"], c["ffn"], c["head_dim"]
-    qd, kd = c["n_q_heads"] * hd, c["n_kv_heads"] * hd
-    shapes = {"attn_q": (qd, H), "attn_k": (kd, H), "attn_v": (kd, H), "attn_output": (H, qd),
-              "ffn_gate": (F, H), "ffn_up": (F, H), "ffn_down": (H, F)}
-    norms = {"attn_norm": H, "attn_q_norm": hd, "attn_k_norm": hd,
-             "post_attention_norm": H, "ffn_norm": H, "post_ffw_norm": H}
-    w = {("token_embd", -1): rng.random_q4_0(c["vocab"] * H // 32),
+    H, F = c["hidden"], c["ffn"]
+    if c.get("embed_q6k"):
+        stride = ((H // 256) * 210 + 15) // 16 * 16
+        emb = rng.random_q6_k_rows(c["vocab"], H, stride)
+    else:
+        emb = rng.random_q4_0(c["vocab"] * H // 32)
+    w = {("token_embd", -1): emb,
          ("output_norm", -1): (1.0 + 0.1 * rng.f32_vec(H)).astype(np.float32)}
     for l in range(c["n_layers"]):
+        ge = c["global_every"]
+        glob = l % ge == ge - 1
+        hd = (c.get("head_dim_global") or c["head_dim"]) if glob else c["head_dim"]
+        nkv = (c.get("n_kv_heads_global") or c["n_kv_heads"]) if glob else c["n_kv_heads"]
+        qd, kd = c["n_q_heads"] * hd, nkv * hd
+        shapes = {"attn_q": (qd, H), "attn_k": (kd, H), "attn_v": (kd, H), "attn_output": (H, qd),
+                  "ffn_gate": (F, H), "ffn_up": (F, H), "ffn_down": (H, F)}
+        norms = {"attn_norm": H, "attn_q_norm": hd, "attn_k_norm": hd,
+                 "post_attention_norm": H, "ffn_norm": H, "post_ffw_norm": H}
         for name in LAYER_TENSORS:
             if name in shapes:
                 n, k = shapes[name]
@@ -255,3 +265,68 @@ def test_sliding_window_boundary_and_global_reach():
     far[0] = 300
     _, gf = _prefill(cg, w, far)
     assert np.abs(gf - gb).max() > 1e-4
+
+
+def _real_cfg(**kw):
+    """The real checkpoint's geometry (crates/sg-gguf/src/desc.rs:66-93) at a
+    small width: 32 q heads, sliding 16 kv x 256, global 4 kv x 512, K=V on
+    global layers, Q6_K embedding / tied head."""
+    c = _cfg(n_layers=3, hidden=512, ffn=512, n_q_heads=32, n_kv_heads=16, head_dim=256,
+             head_dim_global=512, n_kv_heads_global=4, embed_q6k=1, vocab=256,
+             global_every=3, sliding_window=3)
+    c.update(kw)
+    return c
+
+
+def test_real_geometry_forward_invariants():
+    """cpu_reference.rs:25-93 at the real per-kind geometry: decode ==
+    prefill bit for bit, K != V on the global layer, logits sane; and the
+    embedding scale, output norm and softcap closed form through the Q6_K
+    tied head with zero post norms."""
+    c = _real_cfg()
+    w = _weights(c)
+    _, a = _prefill(c, w, TOKENS)
+    d = OracleDecoder(c, w)
+    for t in TOKENS:
+        e = d.decode(t)
+    assert a.view(np.uint32).tolist() == e.view(np.uint32).tolist()
+    p = OraclePrefill(c, w)
+    p.q8_activations = False
+    p.taps = {}
+    logits = p.prefill(TOKENS)
+    assert np.isfinite(logits).all() and (np.abs(logits) <= 30.0).all()
+    assert logits.max() - logits.min() > 1.0
+    k, v = p.taps[("k_rope", 2)], p.taps[("v_norm", 2)]
+    assert k.shape == (len(TOKENS), 4 * 512)
+    assert (np.abs(k - v) > 1e-3).sum() > k.size // 2
+    # zero post norms: logits = cap*tanh(E . rmsnorm(x0 * prod(s)) / cap), E the
+    # dequantized Q6_K rows (independent numpy dequant of the block layout)
+    c0 = _real_cfg(eps=1.0)
+    w0 = _weights(c0, seed=0x66)
+    for l in range(c0["n_layers"]):
+        w0[("post_attention_norm", l)] = np.zeros(c0["hidden"], np.float32)
+        w0[("post_ffw_norm", l)] = np.zeros(c0["hidden"], np.float32)
+        w0[("layer_output_scale", l)] = np.array([0.5], np.float32)
+    H = c0["hidden"]
+    stride = ((H // 256) * 210 + 15) // 16 * 16
+    raw = w0[("token_embd", -1)].reshape(c0["vocab"], stride)[:, :(H // 256) * 210]
+    blk = raw.reshape(c0["vocab"], H // 256, 210).astype(np.int64)
+    ql, qh, sc = blk[..., :128], blk[..., 128:192], blk[..., 192:208].astype(np.int8)
+    dd = raw.reshape(c0["vocab"], H // 256, 210)[..., 208:210].copy().view(np.float16)[..., 0]
+    E = np.zeros((c0["vocab"], H // 256, 256))
+    for h in range(2):
+        for l in range(32):
+            qs = [(ql[..., 64 * h + l] & 15) | ((qh[..., 32 * h + l] & 3) << 4),
+                  (ql[..., 64 * h + l + 32] & 15) | (((qh[..., 32 * h + l] >> 2) & 3) << 4),
+                  (ql[..., 64 * h + l] >> 4) | (((qh[..., 32 * h + l] >> 4) & 3) << 4),
+                  (ql[..., 64 * h + l + 32] >> 4) | (((qh[..., 32 * h + l] >> 6) & 3) << 4)]
+            for j in range(4):
+                E[..., 128 * h + 32 * j + l] = (dd.astype(np.float64) *
+                                                sc[..., 8 * h + l // 16 + 2 * j] * (qs[j] - 32))
+    E = E.reshape(c0["vocab"], H)
+    tok = 17
+    x = E[tok] * np.sqrt(H) * 0.5 ** c0["n_layers"]
+    xn = x / np.sqrt(np.mean(x * x) + 1.0) * w0[("output_norm", -1)].astype(np.float64)
+    want = 30.0 * np.tanh(E @ xn / 30.0)
+    got = OracleDecoder(c0, w0).decode(tok)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=2e-5)
