@@ -56,9 +56,11 @@ class Gemv:
     name = "gemv_q4_0 K=5376 N=21504 (BASELINE config 1), 8 rotating weight copies"
     kernel = "gemv_q4_0_ring_kernel"
 
-    def __init__(self, ctx, torch):
+    def __init__(self, ctx, torch, n=21504):
         self.ctx, self.torch = ctx, torch
-        self.k, self.n = 5376, 21504
+        self.k, self.n = 5376, n
+        if n != 21504:
+            self.name = f"gemv_q4_0 K=5376 N={n} (row-count sweep around config 1), 8 rotating copies"
         self.copies = 8
         nbytes = q4_bytes(self.n, self.k)
         self.w = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(self.copies)]
@@ -662,6 +664,9 @@ def main():
                              "attn_prefill_ipv",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k", "head_q6k"])
+    ap.add_argument("--gemv-rows", type=int, default=21504,
+                    help="gemv workload: rows N (config 1 is 21504; other values sweep the "
+                         "per-launch fixed cost against the streaming rate)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true",
                     help="skip the measured MFMA / HBM peak probes")
@@ -686,7 +691,7 @@ def main():
     elif args.workload == "prefill":
         wl = Prefill(ctx, torch)
     elif args.workload == "gemv":
-        wl = Gemv(ctx, torch)
+        wl = Gemv(ctx, torch, n=args.gemv_rows)
     elif args.workload == "mmq":
         wl = Mmq(ctx, torch)
     elif args.workload == "head_q6k":
