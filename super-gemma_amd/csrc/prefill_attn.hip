@@ -411,6 +411,203 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         for (int i = 0; i < 16; i++) orow[32 * d + 8 * (i / 4) + 4 * hh + (i % 4)] = o[d][i] * inv;
 }
 
+// Prefill attention at head_dim 256 / 512 (the released checkpoint's
+// sliding and global layers; crates/sg-gguf/src/desc.rs:66-93), same
+// semantics as above.  One query head per workgroup of 8 waves; a query
+// tile of 32 is served by D = HD/128 waves.  Each of them computes the
+// tile's full-width scores Sᵀ = K·Qᵀ (Q from LDS, so no wave holds a whole
+// 512-dim query in registers), runs the same online softmax (the D copies
+// are identical instruction for instruction), and accumulates Oᵀ for its own
+// 128 dims, so no scores cross waves.  K/V LDS tiles hold KT = 16384/HD keys
+// (dequantized by all threads as in the head_dim-128 kernel); compute tiles
+// are 32 keys.
+template <int HD>
+__global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
+    const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
+    int n_q, int n_kv, int window, float scale, int qtiles) {
+    constexpr int D = HD / 128;        // waves per query tile
+    constexpr int QTW = 8 / D;         // query tiles per workgroup
+    constexpr int QW = 32 * QTW;       // queries per workgroup
+    constexpr int KT = 16384 / HD;     // keys per LDS tile
+    constexpr int NB = HD / 32;        // Q8 blocks per row
+    constexpr int QRow = HD + 8, KRow = HD + 8, VRow = KT + 8;
+    __shared__ __align__(16) _Float16 q_s[QW][QRow];
+    __shared__ __align__(16) _Float16 k_s[KT][KRow];
+    __shared__ __align__(16) _Float16 vt_s[HD][VRow];
+
+    int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+    if (gridDim.y % 8 == 0) {  // XCD-aware order, as in attn_prefill_kernel
+        const int L = bx + by * qtiles, per = (int)gridDim.y / 8, idx = L >> 3;
+        by = (L & 7) * per + idx % per;
+        bx = idx / per;
+    }
+    const int tile = qtiles - 1 - bx;  // heaviest (latest) query tile first
+    const int qh = by, kvh = qh / (n_q / n_kv);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qt = wave / D, ds = wave % D;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int my_q = tile * QW + qt * 32 + l32;
+    const bool q_valid = my_q < n_tok;
+    const int qp = q0 + my_q;
+
+    // the workgroup's queries, pre-scaled (scores in log2 units), as f16
+    const float qscale = scale * 1.44269504088896341f;
+    for (int i = tid; i < QW * (HD / 4); i += 512) {
+        const int r = i / (HD / 4), c4 = i % (HD / 4);
+        const int qi = tile * QW + r;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (qi < n_tok) v = *reinterpret_cast<const float4 *>(q + ((size_t)qi * n_q + qh) * HD + 4 * c4);
+        const h4 hv = {(_Float16)(v.x * qscale), (_Float16)(v.y * qscale), (_Float16)(v.z * qscale),
+                       (_Float16)(v.w * qscale)};
+        *reinterpret_cast<h4 *>(&q_s[r][4 * c4]) = hv;
+    }
+
+    f32x16 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[d][i] = 0.f;
+    float m_run = kNegBig, l_run = 0.f;
+
+    const int qpos_lo = q0 + tile * QW;
+    const int qpos_hi = q0 + min((tile + 1) * QW, n_tok) - 1;
+    const int k_lo = window > 0 ? max(0, qpos_lo + 1 - window) : 0;
+    const int k_hi = qpos_hi;
+    const int wq_lo = q0 + tile * QW + qt * 32;
+
+    for (int kl = k_lo; kl <= k_hi; kl += KT) {
+        __syncthreads();  // the previous tile's LDS reads (and the q tile writes) are done
+        // dequantize: item = (key pair, 32-block)
+        for (int t = tid; t < (KT / 2) * NB; t += 512) {
+            const int blk = t % NB, pair = t / NB;
+            uint32_t vpk[32];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int kk = 2 * pair + e, key = kl + kk;
+                _Float16 kv[32], vv[32];
+                if (key <= k_hi) {
+                    const bool fresh = src.ckq != nullptr && key >= q0;
+                    const int slot = fresh ? key - q0 : src.ring ? key % src.ring : key;
+                    const size_t row = (size_t)slot * n_kv + kvh;
+                    const int8_t *kqb = fresh ? src.ckq : src.kq;
+                    const int8_t *vqb = fresh ? src.cvq : src.vq;
+                    const uint16_t *ksb = fresh ? src.cks : src.ks;
+                    const uint16_t *vsb = fresh ? src.cvs : src.vs;
+                    const i32x4 *kp = reinterpret_cast<const i32x4 *>(kqb + row * HD + 32 * blk);
+                    const i32x4 *vp = reinterpret_cast<const i32x4 *>(vqb + row * HD + 32 * blk);
+                    const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+                    const _Float16 sk = __builtin_bit_cast(_Float16, ksb[row * NB + blk]);
+                    const _Float16 sv = __builtin_bit_cast(_Float16, vsb[row * NB + blk]);
+                    const h2 dk = {sk, sk}, dv = {sv, sv};
+                    const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                    const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                    for (int w = 0; w < 8; w++) {
+                        const h2 k01 = i8_pair_f16((uint32_t)kw[w], 0x04010400u) * dk;
+                        const h2 k23 = i8_pair_f16((uint32_t)kw[w], 0x04030402u) * dk;
+                        const h2 v01 = i8_pair_f16((uint32_t)vw[w], 0x04010400u) * dv;
+                        const h2 v23 = i8_pair_f16((uint32_t)vw[w], 0x04030402u) * dv;
+                        kv[4 * w] = k01[0], kv[4 * w + 1] = k01[1], kv[4 * w + 2] = k23[0], kv[4 * w + 3] = k23[1];
+                        vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 32; j++) kv[j] = vv[j] = (_Float16)0.f;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    h8 kt;
+#pragma unroll
+                    for (int q8 = 0; q8 < 8; q8++) kt[q8] = kv[8 * j + q8];
+                    *reinterpret_cast<h8 *>(&k_s[kk][32 * blk + 8 * j]) = kt;
+                }
+#pragma unroll
+                for (int j = 0; j < 32; j++) {
+                    const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, vv[j]);
+                    vpk[j] = e == 0 ? bits : vpk[j] | (bits << 16);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+                *reinterpret_cast<uint32_t *>(&vt_s[32 * blk + j][2 * pair]) = vpk[j];
+        }
+        __syncthreads();
+
+#pragma unroll 1
+        for (int ko = 0; ko < KT; ko += 32) {
+            const int kb = kl + ko;
+            if (kb > k_hi) break;
+            // Sᵀ over the full head width, two independent MFMA chains
+            f32x16 s0, s1;
+#pragma unroll
+            for (int i = 0; i < 16; i++) s0[i] = s1[i] = 0.f;
+#pragma unroll
+            for (int c = 0; c < HD / 16; c += 2) {
+                const h8 a0 = *reinterpret_cast<const h8 *>(&k_s[ko + l32][16 * c + 8 * hh]);
+                const h8 b0 = *reinterpret_cast<const h8 *>(&q_s[qt * 32 + l32][16 * c + 8 * hh]);
+                const h8 a1 = *reinterpret_cast<const h8 *>(&k_s[ko + l32][16 * c + 16 + 8 * hh]);
+                const h8 b1 = *reinterpret_cast<const h8 *>(&q_s[qt * 32 + l32][16 * c + 16 + 8 * hh]);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, s1, 0, 0, 0);
+            }
+            f32x16 s;
+#pragma unroll
+            for (int i = 0; i < 16; i++) s[i] = s0[i] + s1[i];
+            const bool full = kb + 31 <= wq_lo && (window <= 0 || kb > wq_lo + 31 - window);
+            float mx = m_run;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                if (!full) {
+                    const int key = kb + 8 * (i / 4) + 4 * hh + (i % 4);
+                    const bool ok = q_valid && key <= qp && (window <= 0 || key > qp - window);
+                    s[i] = ok ? s[i] : kNegBig;
+                }
+                mx = fmaxf(mx, s[i]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            if (!(mx > m_run + 8.0f)) mx = m_run;
+            const float corr = __builtin_amdgcn_exp2f(m_run - mx);
+            float rs = 0.f;
+            h8 pb[2];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float p = full || s[i] > kNegBig ? __builtin_amdgcn_exp2f(s[i] - mx) : 0.f;
+                rs += p;
+                pb[i / 8][i % 8] = (_Float16)p;
+            }
+            rs += __shfl_xor(rs, 32, kWave);
+            l_run = l_run * corr + rs;
+            m_run = mx;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+#pragma unroll
+                for (int d = 0; d < 4; d++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) o[d][i] *= corr;
+            }
+            // Oᵀ (this wave's 128 dims) += Vᵀ·Pᵀ over the tile's two 16-key halves
+#pragma unroll
+            for (int half = 0; half < 2; half++)
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const int row = 128 * ds + 32 * d + l32;
+                    const int c0 = ko + 16 * half + 4 * hh;
+                    const h4 lo = *reinterpret_cast<const h4 *>(&vt_s[row][c0]);
+                    const h4 hi = *reinterpret_cast<const h4 *>(&vt_s[row][c0 + 8]);
+                    const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[half], o[d], 0, 0, 0);
+                }
+        }
+    }
+
+    if (!q_valid) return;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    float *orow = out + ((size_t)my_q * n_q + qh) * HD + 128 * ds;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) orow[32 * d + 8 * (i / 4) + 4 * hh + (i % 4)] = o[d][i] * inv;
+}
+
 }  // namespace
 
 int launch_attn_prefill_ipv(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
@@ -440,7 +637,8 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
                            int n_q, int n_kv, int head_dim, int window, float scale, int ring,
                            const int8_t *ckq, const uint16_t *cks, const int8_t *cvq,
                            const uint16_t *cvs, const uint32_t *step) {
-    SGQ_CHECK(head_dim == kHD, "attn_prefill_q8: head_dim %d unsupported (128)", head_dim);
+    SGQ_CHECK(head_dim == kHD || head_dim == 256 || head_dim == 512,
+              "attn_prefill_q8: head_dim %d unsupported (128, 256, 512)", head_dim);
     SGQ_CHECK(n_tok > 0 && q0 >= 0, "attn_prefill_q8: n_tok %d, q0 %d", n_tok, q0);
     SGQ_CHECK(n_kv > 0 && n_q > 0 && n_q % n_kv == 0, "attn_prefill_q8: n_q %% n_kv != 0");
     SGQ_CHECK(window >= 0 && ring >= 0, "attn_prefill_q8: negative window or ring");
@@ -453,8 +651,23 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
     SGQ_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 &&
                   ((uintptr_t)ks & 1) == 0 && ((uintptr_t)vs & 1) == 0,
               "attn_prefill_q8: misaligned operand");
-    const int qtiles = (n_tok + kQT - 1) / kQT;
     const KvSource src{kq, vq, ks, vs, ring, ckq, cvq, cks, cvs};
+    if (head_dim != kHD) {
+        SGQ_CHECK(step == nullptr, "attn_prefill_q8: head_dim %d needs q0 from the host", head_dim);
+        SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0,
+                  "attn_prefill_q8: misaligned cache");
+        const int qw = head_dim == 256 ? 128 : 64;  // queries per workgroup
+        const int qt = (n_tok + qw - 1) / qw;
+        if (head_dim == 256)
+            hipLaunchKernelGGL(attn_prefill_wide_kernel<256>, dim3(qt, n_q), dim3(512), 0, st, q, src,
+                               out, n_tok, q0, n_q, n_kv, window, scale, qt);
+        else
+            hipLaunchKernelGGL(attn_prefill_wide_kernel<512>, dim3(qt, n_q), dim3(512), 0, st, q, src,
+                               out, n_tok, q0, n_q, n_kv, window, scale, qt);
+        SGQ_HIP(hipGetLastError());
+        return SGQ_OK;
+    }
+    const int qtiles = (n_tok + kQT - 1) / kQT;
     const int qpk = n_q / n_kv;
     if (kPrefillPairHeads && qpk % 2 == 0)
         hipLaunchKernelGGL(attn_prefill_kernel<2>, dim3(qtiles, n_q / 2), dim3(512), 0, st, q, src,

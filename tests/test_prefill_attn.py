@@ -109,3 +109,36 @@ def test_attn_prefill_is_bit_deterministic(ctx, oracle):
     a = _run(ctx, q, kq, ks, vq, vs, n_tok, 0, n_q, n_kv, 0, 0.1)
     b = _run(ctx, q, kq, ks, vq, vs, n_tok, 0, n_q, n_kv, 0, 0.1)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("hd,n_tok,q0,window,n_q,n_kv", [
+    (256, 1, 0, 0, 32, 16), (256, 300, 0, 0, 32, 16), (256, 150, 77, 64, 32, 16),
+    (256, 200, 0, 100, 4, 2), (512, 1, 0, 0, 32, 4), (512, 130, 0, 0, 32, 4),
+    (512, 100, 41, 0, 32, 4), (512, 70, 5, 33, 8, 1)])
+def test_attn_prefill_wide_head_dims_match_oracle(ctx, oracle, hd, n_tok, q0, window, n_q, n_kv):
+    """head_dim 256 / 512 (the released checkpoint's sliding and global
+    layers: 32 q heads over 16 kv heads of 256, or over 4 kv heads of 512),
+    every row and head against the f64 oracle at the same bar."""
+    print(f"prefill attn hd={hd} n_tok={n_tok} q0={q0} window={window} heads={n_q}/{n_kv}",
+          flush=True)
+    rng = oracle.Rng(0xD1DE + hd + n_tok + q0 + window)
+    n_slots = q0 + n_tok
+    k = rng.f32_vec(n_slots * n_kv * hd)
+    v = rng.f32_vec(n_slots * n_kv * hd)
+    ks, kq = oracle.quant_q8_0(k)
+    vs, vq = oracle.quant_q8_0(v)
+    q = rng.f32_vec(n_tok * n_q * hd)
+    kd, vd = oracle.dequant_q8_0(ks, kq), oracle.dequant_q8_0(vs, vq)
+    scale = 1.0 / np.sqrt(hd)
+    out = empty(n_tok * n_q * hd, torch.float32)
+    ctx.attn_prefill_q8(dev(q), dev(kq), dev(ks), dev(vq), dev(vs), n_tok, q0, n_q, n_kv, out,
+                        window=window, scale=scale, head_dim=hd)
+    torch.cuda.synchronize()
+    got = host(out).reshape(n_tok, n_q, hd)
+    want = np.empty_like(got)
+    for i in range(n_tok):
+        p = q0 + i
+        t0 = max(0, p + 1 - window) if window else 0
+        for h in range(n_q):
+            want[i, h] = oracle.attention_head(q, kd, vd, i, h, n_q, n_kv, hd, scale, t0, p)
+    _check(got, want, f"prefill hd={hd} n_tok={n_tok} q0={q0} w={window}")
