@@ -276,25 +276,36 @@ class Prefill:
     last-token logits.  value = prompt tokens per second."""
     kernel = "mmq_kernel"
 
-    def __init__(self, ctx, torch, n_tok=4096):
+    def __init__(self, ctx, torch, n_tok=4096, real=False):
         import numpy as np
         import sgq
 
-        self.ctx, self.torch, self.n_tok = ctx, torch, n_tok
+        self.ctx, self.torch, self.n_tok, self.real = ctx, torch, n_tok, real
         self.stream = torch.cuda.Stream()
         ctx.set_stream(self.stream)
-        self.cfg = sgq.default_model_config(max_ctx=n_tok, prefill_chunk=n_tok)
+        if real:  # the released checkpoint's geometry (crates/sg-gguf/src/desc.rs:66-93)
+            self.cfg = sgq.default_model_config(
+                n_layers=60, global_every=6, head_dim=256, head_dim_global=512, n_kv_heads=16,
+                n_kv_heads_global=4, embed_q6k=1, max_ctx=n_tok, prefill_chunk=n_tok)
+        else:
+            self.cfg = sgq.default_model_config(max_ctx=n_tok, prefill_chunk=n_tok)
         self.model = sgq.Model(ctx, self.cfg)
         self.tokens = np.random.default_rng(11).integers(0, self.cfg.vocab, n_tok).astype(np.uint32)
         self.logits = torch.empty(self.cfg.vocab, dtype=torch.float32, device="cuda")
         c = self.cfg
-        H, F, QD, KD = c.hidden, c.ffn, c.n_q_heads * 128, c.n_kv_heads * 128
-        n_glob = sum(1 for l in range(c.n_layers) if l % c.global_every == c.global_every - 1)
-        per_layer = 2 * n_tok * H * (QD + KD + F + F) + 2 * n_tok * QD * H + 2 * n_tok * F * H
-        self.mmq_ops = c.n_layers * per_layer + (c.n_layers - n_glob) * 2 * n_tok * H * KD
-        attn = lambda w: 4.0 * 128 * c.n_q_heads * sum(min(i + 1, w) if w else i + 1
-                                                     for i in range(n_tok))
-        self.attn_flops = (c.n_layers - n_glob) * attn(c.sliding_window) + n_glob * attn(0)
+        H, F = c.hidden, c.ffn
+        self.mmq_ops, self.attn_flops = 0, 0.0
+        for l in range(c.n_layers):
+            glob = l % c.global_every == c.global_every - 1
+            hd = (c.head_dim_global or c.head_dim) if glob else c.head_dim
+            nkv = (c.n_kv_heads_global or c.n_kv_heads) if glob else c.n_kv_heads
+            QD, KD = c.n_q_heads * hd, nkv * hd
+            kv_proj = KD if glob and c.global_k_eq_v else 2 * KD
+            self.mmq_ops += 2 * n_tok * H * (QD + kv_proj + 2 * F) + 2 * n_tok * QD * H \
+                + 2 * n_tok * F * H
+            w = 0 if glob else c.sliding_window
+            self.attn_flops += 4.0 * hd * c.n_q_heads * sum(min(i + 1, w) if w else i + 1
+                                                            for i in range(n_tok))
 
     def step(self, i):
         self.model.reset()
@@ -328,8 +339,11 @@ class Prefill:
             "whole_prefill_rate": {"achieved": tops, "unit": "TOP/s",
                                    "note": "MMQ int8 ops + attention f16 flops per second "
                                            "over the whole prefill (mixed units: no peak)"},
-            "config": {"workload": f"prefill {self.n_tok} tokens from position 0, 62-layer "
-                                   "random-init decoder (BASELINE config 5)",
+            "config": {"workload": (f"prefill {self.n_tok} tokens from position 0, released-"
+                                    "checkpoint geometry (60 layers, head_dim 256/512, 16/4 kv "
+                                    "heads, Q6_K embedding/head), random init") if self.real else
+                                   (f"prefill {self.n_tok} tokens from position 0, 62-layer "
+                                    "random-init decoder (BASELINE config 5)"),
                        "n_layers": c.n_layers, "hidden": c.hidden, "ffn": c.ffn,
                        "mmq_ops": self.mmq_ops, "attn_flops": self.attn_flops},
         }
@@ -660,7 +674,7 @@ def main():
                          "kernel per operator, each step replayed as a hipGraph; or one "
                          "persistent launch per step")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_real", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
+                    choices=["decode", "decode_real", "prefill_real", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_ipv",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k", "head_q6k"])
@@ -681,15 +695,17 @@ def main():
 
     ctx = sgq.GpuContext(0)
     if args.steps is None:
-        args.steps = {"decode": 100, "decode_real": 50, "prefill": 5}.get(args.workload, 200)
+        args.steps = {"decode": 100, "decode_real": 50, "prefill": 5, "prefill_real": 3}.get(args.workload, 200)
     if args.warmup is None:
-        args.warmup = {"decode": 10, "decode_real": 5, "prefill": 1}.get(args.workload, 20)
+        args.warmup = {"decode": 10, "decode_real": 5, "prefill": 1, "prefill_real": 1}.get(args.workload, 20)
     if args.workload == "decode":
         wl = Decode(ctx, torch, mode=args.decode_mode)
     elif args.workload == "decode_real":
         wl = DecodeReal(ctx, torch, mode="kernels" if args.decode_mode == "kernels" else "fused")
     elif args.workload == "prefill":
         wl = Prefill(ctx, torch)
+    elif args.workload == "prefill_real":
+        wl = Prefill(ctx, torch, real=True)
     elif args.workload == "gemv":
         wl = Gemv(ctx, torch, n=args.gemv_rows)
     elif args.workload == "mmq":

@@ -347,7 +347,8 @@ int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
  * attention on the VALU).  Models of another geometry than the benchmark's
  * (head_dim 128 everywhere, <= 2 q heads per kv head, Q4_0 embedding) run in
  * mode 2 (the default for them: the fused GEMVs around the any-geometry
- * attention) or mode 3; their prefill runs as successive mode-3 steps.
+ * attention) or mode 3; their prefill is the chunked MMQ driver at their
+ * per-layer widths (head_dim 256/512 prefill attention).
  * Mode 1 fails with SGQ_ERR_VALIDATION when the shape or the device does not
  * fit it. */
 int sgq_model_set_decode_mode(sgq_model *model, int mode);

@@ -51,7 +51,8 @@ class OracleDecoder:
         self.v_cache = [[] for _ in range(L)]
         self.pos = 0
         # taps[(name, layer)] = the row(s) of the last forward, when a dict:
-        # "k_rope" and "v_norm" (reference.rs:153-155 tap names)
+        # "k_rope" and "v_norm" (reference.rs:153-155 tap names); prefill also
+        # leaves ("x_out", -1), the residual rows after the last layer
         self.taps = None
         # kv_source(layer, pos, k_row, v_row) -> (k_row, v_row): the Q8_0
         # round-tripped rows decode() caches, replaceable by the caller (a
@@ -235,8 +236,11 @@ class OraclePrefill(OracleDecoder):
             if self.taps is not None:
                 self.taps[("k_rope", l)], self.taps[("v_norm", l)] = k, v
             for i in range(M):
-                self.k_cache[l].append(self._q8_round_trip(k[i]))
-                self.v_cache[l].append(self._q8_round_trip(v[i]))
+                kr, vr = self._q8_round_trip(k[i]), self._q8_round_trip(v[i])
+                if self.kv_source is not None:
+                    kr, vr = self.kv_source(l, q0 + i, kr, vr)
+                self.k_cache[l].append(kr)
+                self.v_cache[l].append(vr)
             ck = np.concatenate(self.k_cache[l])
             cv = np.concatenate(self.v_cache[l])
             window = None if glob else c["sliding_window"]
@@ -250,6 +254,8 @@ class OraclePrefill(OracleDecoder):
             x = (x + O.rmsnorm(f, w[("post_ffw_norm", l)], H, eps)).astype(np.float32)
             x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
         self.pos += M
+        if self.taps is not None:
+            self.taps[("x_out", -1)] = x
         xf = O.rmsnorm(x[-1], w[("output_norm", -1)], H, eps)
         return self._head(xf)
 

@@ -121,6 +121,26 @@ __global__ __launch_bounds__(kRowWG) void embed_norm_kernel(const uint8_t *__res
 // 128h + 32w + l of a 256-weight block is d·sc[l/16 + 2w + 8h]·q, q the
 // 6-bit quant from ql's low (w even) or high (w odd) nibble of byte
 // 64h + l (+32 for w = 1, 3) and 2 bits of qh[32h + l], minus 32).
+// Values j0..j0+3 (j0 % 4 == 0) of a Q6_K row (q6_k.rs:41-62: 256-value
+// super-blocks of ql[128], qh[64], int8 scales[16], f16 d), times `scale`.
+__device__ __forceinline__ float4 q6k_quad(const uint8_t *__restrict__ er, int j0, float scale) {
+    const uint8_t *blk = er + (j0 / 256) * 210;
+    const int j = j0 % 256, h = j / 128, r = j % 128, wq = r / 32, l0 = r % 32;
+    const float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
+    const float ds = d * (float)(int8_t)blk[192 + 8 * h + l0 / 16 + 2 * wq];
+    const uint8_t *ql = blk + 64 * h + (wq & 1) * 32;
+    const uint8_t *qh = blk + 128 + 32 * h;
+    float e[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int l = l0 + u;
+        const int lo = wq < 2 ? (ql[l] & 15) : (ql[l] >> 4);
+        const int q = (lo | (((qh[l] >> (2 * wq)) & 3) << 4)) - 32;
+        e[u] = ds * (float)q * scale;
+    }
+    return make_float4(e[0], e[1], e[2], e[3]);
+}
+
 __global__ __launch_bounds__(kRowWG) void embed_q6k_norm_kernel(
     const uint8_t *__restrict__ E, uint64_t row_stride, const uint32_t *__restrict__ step,
     int hidden, float scale, const float *__restrict__ w, float eps, float *__restrict__ x,
@@ -134,21 +154,8 @@ __global__ __launch_bounds__(kRowWG) void embed_q6k_norm_kernel(
     for (int k = 0; k < kRowV; k++) {
         const int i = t + k * kRowWG;
         if (i < n4) {
-            const int j0 = 4 * i;                       // first of four consecutive values
-            const uint8_t *blk = er + (j0 / 256) * 210;
-            const int j = j0 % 256, h = j / 128, r = j % 128, wq = r / 32, l0 = r % 32;
-            const float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
-            const float ds = d * (float)(int8_t)blk[192 + 8 * h + l0 / 16 + 2 * wq];
-            const uint8_t *ql = blk + 64 * h + (wq & 1) * 32;
-            const uint8_t *qh = blk + 128 + 32 * h;
-            float e[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int l = l0 + u;
-                const int lo = wq < 2 ? (ql[l] & 15) : (ql[l] >> 4);
-                const int q = (lo | (((qh[l] >> (2 * wq)) & 3) << 4)) - 32;
-                e[u] = ds * (float)q * scale;
-            }
+            const float4 e4 = q6k_quad(er, 4 * i, scale);
+            const float e[4] = {e4.x, e4.y, e4.z, e4.w};
             v[k] = make_float4(e[0], e[1], e[2], e[3]);
             reinterpret_cast<float4 *>(x)[i] = v[k];
             ss += sumsq4(v[k]);
@@ -326,16 +333,19 @@ __global__ void model_step_kernel(uint32_t *step, uint32_t a, uint32_t b, uint32
 
 // RoPE tables of positions q0..q0+M-1 for both layer kinds, f64 angles as
 // in model_step_kernel; layout [kind][token][pair][cos, sin].
-__global__ void pf_rope_table_kernel(float *__restrict__ cs, int q0, int M, float theta_s,
-                                     float theta_g, int live_g) {
+__global__ void pf_rope_table_kernel(float *__restrict__ cs, int q0, int M, int hd_s, int hd_g,
+                                     float theta_s, float theta_g, int live_g) {
+    // sliding table [M][hd_s/2] (cos, sin), then the global one [M][hd_g/2]
     const int t = blockIdx.x * 256 + threadIdx.x;
-    const int half = kHeadDim / 2;
-    if (t >= 2 * M * half) return;
-    const int kind = t / (M * half), r = t % (M * half);
+    const int hs = hd_s / 2, hg = hd_g / 2;
+    if (t >= M * (hs + hg)) return;
+    const int kind = t >= M * hs;
+    const int r = kind ? t - M * hs : t, half = kind ? hg : hs;
     const int tok = r / half, i = r % half;
     const double theta = kind ? (double)theta_g : (double)theta_s;
     const double factor = kind && i >= live_g ? 1e30 : 1.0;
-    const double ang = (double)(q0 + tok) * pow(theta, -2.0 * (double)i / (double)kHeadDim) / factor;
+    const double ang =
+        (double)(q0 + tok) * pow(theta, -2.0 * (double)i / (double)(kind ? hd_g : hd_s)) / factor;
     cs[2 * t] = (float)cos(ang);
     cs[2 * t + 1] = (float)sin(ang);
 }
@@ -375,6 +385,33 @@ __global__ __launch_bounds__(kPfWG) void pf_embed_norm_q8_kernel(
         const float4 v = make_float4(e[0], e[1], e[2], e[3]);
         xr[i] = v;
         ss += e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
+    }
+    const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+    int *qr = reinterpret_cast<int *>(xq + (size_t)row * H);
+    for (int i = t; i < n4; i += kPfWG) {
+        const float4 v = xr[i], wv = reinterpret_cast<const float4 *>(w)[i];
+        const float4 y = make_float4(v.x * inv * wv.x, v.y * inv * wv.y, v.z * inv * wv.z,
+                                     v.w * inv * wv.w);
+        int q;
+        quant_lane(y, i & 7, &xs[(size_t)row * (H / 32) + (i >> 3)], &q);
+        qr[i] = q;
+    }
+}
+
+// The same for a Q6_K embedding (rows at the device's padded stride).
+__global__ __launch_bounds__(kPfWG) void pf_embed_q6k_norm_q8_kernel(
+    const uint8_t *__restrict__ E, uint64_t row_stride, const uint32_t *__restrict__ tokens, int H,
+    float scale, const float *__restrict__ w, float eps, float *__restrict__ x,
+    int8_t *__restrict__ xq, uint16_t *__restrict__ xs) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, t = threadIdx.x, n4 = H / 4;
+    const uint8_t *er = E + (size_t)tokens[row] * row_stride;
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * H);
+    float ss = 0.f;
+    for (int i = t; i < n4; i += kPfWG) {
+        const float4 v = q6k_quad(er, 4 * i, scale);
+        xr[i] = v;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
     int *qr = reinterpret_cast<int *>(xq + (size_t)row * H);
@@ -446,16 +483,17 @@ __global__ __launch_bounds__(256) void pf_geglu_q8_kernel(const float4 *__restri
 // Per (token, head): q -> rmsnorm(q_norm) + RoPE (fp32 out); k -> rmsnorm
 // (k_norm) + RoPE -> Q8_0 into the chunk's K pages; v -> weightless rmsnorm
 // -> Q8_0 into the chunk's V pages.  Grid [M, n_q + 2 n_kv], 128 threads.
-__global__ __launch_bounds__(kHeadDim) void pf_qkv_post_kernel(
+template <int HD>
+__global__ __launch_bounds__(HD) void pf_qkv_post_kernel(
     const float *__restrict__ q_raw, const float *__restrict__ k_raw,
     const float *__restrict__ v_src, const float *__restrict__ wq_norm,
     const float *__restrict__ wk_norm, const float *__restrict__ cs, int n_q, int n_kv,
     float eps, float *__restrict__ q_out, int8_t *__restrict__ ckq, uint16_t *__restrict__ cks,
     int8_t *__restrict__ cvq, uint16_t *__restrict__ cvs) {
-    __shared__ float row[kHeadDim];
-    __shared__ float red[2];
+    __shared__ float row[HD];
+    __shared__ float red[HD / 64];
     const int tok = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
-    const int QD = n_q * kHeadDim, KD = n_kv * kHeadDim;
+    const int QD = n_q * HD, KD = n_kv * HD;
     int kind, head;  // 0 q, 1 k, 2 v
     if (h < n_q) {
         kind = 0, head = h;
@@ -465,31 +503,34 @@ __global__ __launch_bounds__(kHeadDim) void pf_qkv_post_kernel(
         kind = 2, head = h - n_q - n_kv;
     }
     const float *src = kind == 0 ? q_raw + (size_t)tok * QD : (kind == 1 ? k_raw : v_src) + (size_t)tok * KD;
-    float v = src[head * kHeadDim + t];
+    float v = src[head * HD + t];
     float ss = v * v;
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
-    const float inv = 1.0f / sqrtf((red[0] + red[1]) / (float)kHeadDim + eps);
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < HD / 64; w++) tot += red[w];
+    const float inv = 1.0f / sqrtf(tot / (float)HD + eps);
     v = v * inv * (kind == 0 ? wq_norm[t] : kind == 1 ? wk_norm[t] : 1.f);
     row[t] = v;
     __syncthreads();
     if (kind < 2) {
-        const int i = t % (kHeadDim / 2);
-        const float c = cs[((size_t)tok * (kHeadDim / 2) + i) * 2];
-        const float sn = cs[((size_t)tok * (kHeadDim / 2) + i) * 2 + 1];
-        const float a = row[i], b = row[i + kHeadDim / 2];
-        v = t < kHeadDim / 2 ? a * c - b * sn : b * c + a * sn;
+        const int i = t % (HD / 2);
+        const float c = cs[((size_t)tok * (HD / 2) + i) * 2];
+        const float sn = cs[((size_t)tok * (HD / 2) + i) * 2 + 1];
+        const float a = row[i], b = row[i + HD / 2];
+        v = t < HD / 2 ? a * c - b * sn : b * c + a * sn;
     }
     if (kind == 0) {
-        q_out[(size_t)tok * QD + head * kHeadDim + t] = v;
+        q_out[(size_t)tok * QD + head * HD + t] = v;
         return;
     }
     float amax = fabsf(v);
     for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
     const float d = amax * (1.0f / 127.0f);
     const float id = d > 0.f ? 1.0f / d : 0.f;
-    const size_t e = ((size_t)tok * n_kv + head) * kHeadDim + t;
+    const size_t e = ((size_t)tok * n_kv + head) * HD + t;
     (kind == 1 ? ckq : cvq)[e] = (int8_t)(int)__builtin_rintf(v * id);
     if ((t & 31) == 0) (kind == 1 ? cks : cvs)[e / 32] = f32_to_f16_bits(d);
 }
@@ -1305,15 +1346,20 @@ constexpr size_t kPfPartialFloats = 1024ull * 128 * 128;  // >= split·m·n for 
 
 int pf_alloc(sgq_model *m) {
     const sgq_model_config &c = m->cfg;
-    const size_t C = c.prefill_chunk, H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim,
-                 KD = c.n_kv_heads * kHeadDim;
+    const size_t C = c.prefill_chunk, H = c.hidden, F = c.ffn;
+    size_t QD = 0, KD = 0, HD2 = 0;  // widest layer; both kinds' rope pairs
+    for (const LayerW &L : m->layers) {
+        QD = std::max<size_t>(QD, (size_t)c.n_q_heads * L.hd);
+        KD = std::max<size_t>(KD, (size_t)L.n_kv * L.hd);
+    }
+    HD2 = c.head_dim + (c.head_dim_global ? c.head_dim_global : c.head_dim);
     auto &p = m->pf;
     void **f32s[] = {(void **)&p.x, (void **)&p.q_raw, (void **)&p.k_raw, (void **)&p.v_raw,
                      (void **)&p.q, (void **)&p.attn, (void **)&p.o, (void **)&p.g,
                      (void **)&p.u, (void **)&p.f, (void **)&p.part, (void **)&p.head_in,
                      (void **)&p.rope};
     const size_t f32n[] = {C * H, C * QD, C * KD, C * KD, C * QD, C * QD, C * H, C * F, C * F,
-                           C * H, kPfPartialFloats, H, 2 * C * kHeadDim};
+                           C * H, kPfPartialFloats, H, C * HD2};
     int rc;
     for (int i = 0; i < 13; i++)
         if ((rc = alloc(m, f32n[i] * 4, f32s[i]))) return rc;
@@ -1338,32 +1384,45 @@ int pf_chunk(sgq_model *m, uint32_t M, uint32_t q0) {
     const sgq_model_config &c = m->cfg;
     hipStream_t st = ctx_stream(m->ctx);
     auto &p = m->pf;
-    const uint32_t H = c.hidden, F = c.ffn, QD = c.n_q_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim;
+    const uint32_t H = c.hidden, F = c.ffn, nq = c.n_q_heads;
+    const int hd_s = (int)c.head_dim, hd_g = (int)(c.head_dim_global ? c.head_dim_global : c.head_dim);
     int rc;
-    const int live = (int)lroundf(c.global_rope_frac * kHeadDim / 2);
-    hipLaunchKernelGGL(pf_rope_table_kernel, dim3((2 * M * (kHeadDim / 2) + 255) / 256), dim3(256),
-                       0, st, p.rope, (int)q0, (int)M, c.rope_theta_sliding, c.rope_theta_global,
-                       live);
-    hipLaunchKernelGGL(pf_embed_norm_q8_kernel, dim3(M), dim3(kPfWG), 0, st,
-                       static_cast<const uint8_t *>(m->embd), p.tok, (int)H, sqrtf((float)H),
-                       m->layers[0].attn_norm, c.eps, p.x, p.xq, p.xs);
+    const int live = (int)lroundf(c.global_rope_frac * hd_g / 2);
+    hipLaunchKernelGGL(pf_rope_table_kernel, dim3((M * (hd_s / 2 + hd_g / 2) + 255) / 256),
+                       dim3(256), 0, st, p.rope, (int)q0, (int)M, hd_s, hd_g, c.rope_theta_sliding,
+                       c.rope_theta_global, live);
+    if (c.embed_q6k)
+        hipLaunchKernelGGL(pf_embed_q6k_norm_q8_kernel, dim3(M), dim3(kPfWG), 0, st,
+                           static_cast<const uint8_t *>(m->embd), m->embd_stride, p.tok, (int)H,
+                           sqrtf((float)H), m->layers[0].attn_norm, c.eps, p.x, p.xq, p.xs);
+    else
+        hipLaunchKernelGGL(pf_embed_norm_q8_kernel, dim3(M), dim3(kPfWG), 0, st,
+                           static_cast<const uint8_t *>(m->embd), p.tok, (int)H, sqrtf((float)H),
+                           m->layers[0].attn_norm, c.eps, p.x, p.xq, p.xs);
     SGQ_HIP(hipGetLastError());
     for (size_t li = 0; li < m->layers.size(); li++) {
         const LayerW &L = m->layers[li];
+        const uint32_t hd = L.hd, nkv = L.n_kv, QD = nq * hd, KD = nkv * hd;
         if ((rc = mmq(m, st, L.wq, p.xq, p.xs, p.q_raw, M, QD, H)) ||
             (rc = mmq(m, st, L.wk, p.xq, p.xs, p.k_raw, M, KD, H)))
             return rc;
         if (L.wv && (rc = mmq(m, st, L.wv, p.xq, p.xs, p.v_raw, M, KD, H))) return rc;
-        const float *rope = p.rope + (L.global ? (size_t)M * kHeadDim : 0);
-        hipLaunchKernelGGL(pf_qkv_post_kernel, dim3(M, c.n_q_heads + 2 * c.n_kv_heads),
-                           dim3(kHeadDim), 0, st, p.q_raw, p.k_raw, L.wv ? p.v_raw : p.k_raw,
-                           L.q_norm, L.k_norm, rope, (int)c.n_q_heads, (int)c.n_kv_heads, c.eps,
-                           p.q, p.ckq, p.cks, p.cvq, p.cvs);
+        const float *rope = p.rope + (L.global ? (size_t)M * hd_s : 0);
+        const float *v_src = L.wv ? p.v_raw : p.k_raw;
+        const dim3 pg(M, nq + 2 * nkv);
+#define SGQ_PF_POST(HDV)                                                                          \
+    hipLaunchKernelGGL(pf_qkv_post_kernel<HDV>, pg, dim3(HDV), 0, st, p.q_raw, p.k_raw, v_src,     \
+                       L.q_norm, L.k_norm, rope, (int)nq, (int)nkv, c.eps, p.q, p.ckq, p.cks,     \
+                       p.cvq, p.cvs)
+        if (hd == 128) SGQ_PF_POST(128);
+        else if (hd == 256) SGQ_PF_POST(256);
+        else SGQ_PF_POST(512);
+#undef SGQ_PF_POST
         SGQ_HIP(hipGetLastError());
         const int ring = L.global ? 0 : (int)L.slots;
         const int window = L.global ? 0 : (int)std::min(c.sliding_window, L.slots);
         if ((rc = launch_attn_prefill_q8(st, p.q, L.kq, L.ks, L.vq, L.vs, p.attn, (int)M, (int)q0,
-                                         (int)c.n_q_heads, (int)c.n_kv_heads, kHeadDim, window,
+                                         (int)nq, (int)nkv, (int)hd, window,
                                          c.attn_scale, ring, p.ckq, p.cks, p.cvq, p.cvs)))
             return rc;
         {
@@ -1410,19 +1469,6 @@ int sgq_model_prefill(sgq_model *m, const uint32_t *tokens, uint32_t n_tokens, f
     for (uint32_t i = 0; i < n_tokens; i++)
         SGQ_CHECK(tokens[i] < c.vocab, "model: token %u at %u >= vocab %u", tokens[i], i, c.vocab);
     int rc;
-    if (m->generic) {
-        // any-geometry models: the prompt as successive decode steps (mode 3),
-        // logits of the last token only
-        for (uint32_t i = 0; i < n_tokens; i++) {
-            const bool last = i + 1 == n_tokens;
-            if ((rc = write_step(m, tokens[i])) ||
-                (rc = record_step_generic(m, last && logits ? logits : m->logits_tmp,
-                                          last && logits)))
-                return rc;
-            m->pos++;
-        }
-        return SGQ_OK;
-    }
     if (!m->pf.chunk && (rc = pf_alloc(m))) return rc;
     hipStream_t st = ctx_stream(m->ctx);
     uint32_t M = 0;
@@ -1436,9 +1482,12 @@ int sgq_model_prefill(sgq_model *m, const uint32_t *tokens, uint32_t n_tokens, f
     if (logits) {  // the last token's logits: output norm, limbs, tied head with softcap
         const uint32_t H = c.hidden;
         if ((rc = launch_rmsnorm(st, m->pf.x + (size_t)(M - 1) * H, m->out_norm, m->pf.head_in, 1, H, 0,
-                                 c.eps)) ||
-            (rc = launch_quant_limbs(st, m->pf.head_in, m->xl, H)))
+                                 c.eps)))
             return rc;
+        if (c.embed_q6k)
+            return launch_gemv_q6_k(st, m->embd, m->embd_stride, m->pf.head_in, logits, c.vocab, H,
+                                    c.final_softcap);
+        if ((rc = launch_quant_limbs(st, m->pf.head_in, m->xl, H))) return rc;
         GemvTargets head{};
         head.w[0] = m->embd, head.y[0] = logits, head.end[0] = (int)c.vocab, head.count = 1;
         head.softcap = c.final_softcap;
@@ -1561,6 +1610,12 @@ int sgq_model_tensor(const sgq_model *m, int layer, const char *name, void **ptr
                 *bytes = e.b;
                 return SGQ_OK;
             }
+        if (n == "prefill_x") {  // residual rows of the last prefill chunk
+            SGQ_CHECK(m->pf.chunk, "model: no prefill has run (prefill_x)");
+            *ptr = m->pf.x;
+            *bytes = (size_t)m->pf.chunk * H * 4;
+            return SGQ_OK;
+        }
         return fail(SGQ_ERR_VALIDATION, "model: no global tensor '%s'", name);
     }
     SGQ_CHECK(layer < (int)m->layers.size(), "model: layer %d out of range", layer);

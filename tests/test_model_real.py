@@ -11,7 +11,8 @@ benchmark's step around the any-geometry attention: post-projection, VALU
 split attention at head_dim 256/512 with 2 or 8 query heads per kv head, a
 merge into the O projection's limbs; the Q6_K head after a norm from the
 down GEMV's partial sums) or mode 3 (one kernel per operator), and prefill
-as successive mode-3 decode steps.  Bar: the logits bar of tests/test_model.py;
+in chunks through the int8 MMQs and the head_dim 256/512 prefill attention.
+Bar: the logits bar of tests/test_model.py (prefill: _check_prefill_logits);
 the head rounds x to f16 (gemv_q6_k_logits semantics), the oracle uses the
 fp32 x in an f64 dot.  The oracle attends the device's K/V pages after
 checking them against its own Q8_0 rows (_device_kv).
@@ -28,7 +29,7 @@ from test_model import _check_logits, _weights
 pytestmark = pytest.mark.gpu
 
 
-def _device_kv(model, oracle, flips):
+def _device_kv(model, oracle, flips, loose=False):
     """OracleDecoder.kv_source: the device's dequantized K/V rows of (layer,
     position), after checking them against the oracle's own Q8_0 rows.  Per
     32-element block: the f16 scales agree within one ulp (amax/127 sits
@@ -43,7 +44,9 @@ def _device_kv(model, oracle, flips):
     head_dim-512 attention amplifies it past the logits bar (the oracle
     against itself with 2e-5 relative noise on every linear output: up to
     1.8e-2 with its own Q8 pages, 4e-4 with shared ones), so the oracle
-    attends the device's pages."""
+    attends the device's pages.  ``loose``: after a prefill with Q8_0
+    activations the rows only have to agree within 10% of their largest
+    element (activation flips upstream move them by more than a step)."""
     def src(layer, pos, k_row, v_row):
         L = model.cfg
         glob = layer % L.global_every == L.global_every - 1
@@ -57,6 +60,12 @@ def _device_kv(model, oracle, flips):
             q = model.read_tensor(f"{kind}_quants", layer, np.int8).reshape(slots, row)[slot]
             sc = model.read_tensor(f"{kind}_scales", layer, np.uint16).reshape(slots, row // 32)[slot]
             dev = oracle.dequant_q8_0(sc, q)
+            if loose:
+                # after a prefill with Q8_0 activations (see _check_prefill_logits)
+                err = float(np.abs(dev - mine).max() / max(np.abs(mine).max(), 1e-30))
+                assert err <= 0.1, (kind, layer, pos, err)
+                out.append(dev)
+                continue
             # the oracle's block scale: its largest |q| is 127
             mine_sc = np.abs(mine.reshape(-1, 32)).max(axis=1) / np.float32(127)
             mine_bits = mine_sc.astype(np.float16).view(np.uint16)
@@ -74,6 +83,23 @@ def _device_kv(model, oracle, flips):
             out.append(dev)
         return out[0], out[1]
     return src
+
+
+def _check_prefill_logits(got, want):
+    """The prefill bar at this geometry.  Every linear layer of the prefill
+    sees Q8_0 activations, and the GPU's and the oracle's inputs to each
+    quantization differ by float noise (f32 MMQ sums against f64 dots): a
+    quant near a rounding boundary then flips, and one flip moves the logits
+    by up to ~1e-2 here.  The oracle against itself with 1e-6 relative noise
+    before each Q8_0 round trip spreads its logits by up to ~6e-3
+    (tests/test_oracle_model.py::test_q8_activation_noise_spread).  So: max
+    error within 2e-2 of the largest logit, and the GPU's top token within
+    that of the oracle's best."""
+    top = float(np.abs(want).max())
+    err = float(np.abs(got - want).max())
+    assert err <= 2e-2 * top, ("prefill logits", err / top)
+    g, w_ = int(np.argmax(got)), int(np.argmax(want))
+    assert want[g] >= want[w_] - 2e-2 * top, f"prefill top-1 differs: {g} vs {w_}"
 
 
 def _real_cfg(sgq, **kw):
@@ -142,26 +168,28 @@ def test_real_geometry_long_context_matches_oracle(ctx, oracle, mode):
 
 
 def test_real_geometry_prefill_graph_and_decode(ctx, oracle):
-    """Prefill (successive decode steps) then decode, against the oracle's
-    token-by-token decode; the recorded graph replays the step bit for bit."""
+    """Chunked prefill (two chunks: 16 + 5 tokens, the second attending the
+    first's cached keys and its own pages; int8 MMQs on Q8_0 activations,
+    head_dim 256/512 prefill attention) against the oracle's prefill with
+    the same Q8_0 activation round trips, then graph decode steps; the
+    recorded graph replays the step bit for bit."""
     import sgq
-    from oracle.model import OracleDecoder
+    from oracle.model import OraclePrefill
 
     print("real geometry prefill + graph", flush=True)
     # no ring wrap inside the prompt: the oracle reads the device's pages of
     # every prompt position after the whole prefill
-    cfg = _real_cfg(sgq, seed=0x31C, sliding_window=24)
+    cfg = _real_cfg(sgq, seed=0x31C, sliding_window=24, max_ctx=32, prefill_chunk=16)
     model = sgq.Model(ctx, cfg)
     d = cfg.as_dict()
-    ref = OracleDecoder(d, _weights(model, d))
-    ref.kv_source = _device_kv(model, oracle, [])
-    toks = [3, 14, 159, 265, 358, 979]
+    ref = OraclePrefill(d, _weights(model, d))
+    ref.kv_source = _device_kv(model, oracle, [], loose=True)
+    toks = [3, 14, 159, 265, 358, 979, 323, 846, 264, 338, 327, 950, 288, 419, 716, 939, 937,
+            510, 582, 97, 494]
     logits = empty(cfg.vocab, torch.float32)
     model.prefill(toks, logits)
     torch.cuda.synchronize()
-    for t in toks:
-        want = ref.decode(t)
-    _check_logits(host(logits), want, "prefill")
+    _check_prefill_logits(host(logits), ref.prefill(toks))
     eager = sgq.Model(ctx, cfg)
     eager.prefill(toks)
     s = torch.cuda.Stream()
