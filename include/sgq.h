@@ -238,7 +238,8 @@ int sgq_attn_decode_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
  * (slot = position) and must hold positions 0..q0+n_tokens-1 (the chunk's
  * own K/V included).  Query at position p attends keys k <= p, and with
  * window > 0 only k > p - window.  K/V are dequantized to f16 and P is
- * rounded to f16 as in the reference; accumulation fp32.  head_dim 128;
+ * rounded to f16 as in the reference; accumulation fp32.  head_dim 128, or
+ * 256 / 512 (the released checkpoint's sliding and global layers);
  * out [n_tokens × n_q_heads × head_dim] fp32. */
 int sgq_attn_prefill_q8(sgq_ctx *ctx, const float *q, const int8_t *k_quants,
                         const uint16_t *k_scales, const int8_t *v_quants, const uint16_t *v_scales,
