@@ -535,6 +535,89 @@ __global__ __launch_bounds__(HD) void pf_qkv_post_kernel(
     if ((t & 31) == 0) (kind == 1 ? cks : cvs)[e / 32] = f32_to_f16_bits(d);
 }
 
+// The same at head_dim 256 / 512: one wave per (token, head row), lane j
+// holding float4 j (and j + 64), the NEOX partner float4 j ± HD/8 a lane
+// shuffle (256) or the lane's other float4 (512), and the Q8_0 quantization
+// of 8-lane groups (quant_lane): four rows per 256-thread workgroup.
+template <int HD>
+__global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
+    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
+    const float *__restrict__ v_src, const float *__restrict__ wq_norm,
+    const float *__restrict__ wk_norm, const float *__restrict__ cs, int n_q, int n_kv, int M,
+    float eps, float *__restrict__ q_out, int8_t *__restrict__ ckq, uint16_t *__restrict__ cks,
+    int8_t *__restrict__ cvq, uint16_t *__restrict__ cvs) {
+    constexpr int NF = HD / 4, NV = NF / 64;
+    static_assert(NV == 1 || NV == 2, "head_dim 256 or 512");
+    const int lane = threadIdx.x & 63;
+    const int R = n_q + 2 * n_kv;
+    const long rid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (rid >= (long)M * R) return;  // whole waves
+    const int tok = (int)(rid / R), h = (int)(rid % R);
+    const int kind = h < n_q ? 0 : (h < n_q + n_kv ? 1 : 2);
+    const int head = kind == 0 ? h : (kind == 1 ? h - n_q : h - n_q - n_kv);
+    const int QD = n_q * HD, KD = n_kv * HD;
+    const float *src = (kind == 0 ? q_raw + (size_t)tok * QD
+                                  : (kind == 1 ? k_raw : v_src) + (size_t)tok * KD) +
+                       (size_t)head * HD;
+    const float *w = kind == 0 ? wq_norm : (kind == 1 ? wk_norm : nullptr);
+    float4 x[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        x[v] = reinterpret_cast<const float4 *>(src)[lane + 64 * v];
+        ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
+    }
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const float4 wt = w ? reinterpret_cast<const float4 *>(w)[lane + 64 * v]
+                            : make_float4(1.f, 1.f, 1.f, 1.f);
+        x[v] = make_float4(x[v].x * inv * wt.x, x[v].y * inv * wt.y, x[v].z * inv * wt.z,
+                           x[v].w * inv * wt.w);
+    }
+    if (kind < 2) {
+        float4 pr[NV];
+        if (NV == 1) {
+            const int pl = lane ^ 32;  // float4 j ± 32 = NF/2
+            pr[0] = make_float4(__shfl(x[0].x, pl, kWave), __shfl(x[0].y, pl, kWave),
+                                __shfl(x[0].z, pl, kWave), __shfl(x[0].w, pl, kWave));
+        } else {
+#pragma unroll
+            for (int v = 0; v < NV; v++) pr[v] = x[NV - 1 - v];
+        }
+        const float2 *tc = reinterpret_cast<const float2 *>(cs) + (size_t)tok * (HD / 2);
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const int j = lane + 64 * v;
+            const bool lo = j < NF / 2;
+            const int i0 = (lo ? j : j - NF / 2) * 4;
+            const float sg = lo ? -1.f : 1.f;
+            const float2 c0 = tc[i0], c1 = tc[i0 + 1], c2 = tc[i0 + 2], c3 = tc[i0 + 3];
+            x[v] = make_float4(x[v].x * c0.x + sg * pr[v].x * c0.y,
+                               x[v].y * c1.x + sg * pr[v].y * c1.y,
+                               x[v].z * c2.x + sg * pr[v].z * c2.y,
+                               x[v].w * c3.x + sg * pr[v].w * c3.y);
+        }
+    }
+    if (kind == 0) {
+#pragma unroll
+        for (int v = 0; v < NV; v++)
+            reinterpret_cast<float4 *>(q_out + (size_t)tok * QD + (size_t)head * HD)[lane + 64 * v] = x[v];
+        return;
+    }
+    const size_t e0 = ((size_t)tok * n_kv + head) * HD;
+    int *qt = reinterpret_cast<int *>(kind == 1 ? ckq : cvq);
+    uint16_t *sc = kind == 1 ? cks : cvs;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int j = lane + 64 * v;
+        int qv;
+        quant_lane(x[v], j & 7, &sc[(e0 + 4 * j) / 32], &qv);
+        qt[(e0 + 4 * j) / 4] = qv;
+    }
+}
+
 // Append the chunk's K/V pages (rows i = position - q0) to a cache: slot
 // q0+i, or (q0+i) mod ring — then only the last `ring` rows, so no two
 // threads write one slot.  Thread = one 16-byte quant chunk of a row (and one
@@ -1410,14 +1493,18 @@ int pf_chunk(sgq_model *m, uint32_t M, uint32_t q0) {
         const float *rope = p.rope + (L.global ? (size_t)M * hd_s : 0);
         const float *v_src = L.wv ? p.v_raw : p.k_raw;
         const dim3 pg(M, nq + 2 * nkv);
-#define SGQ_PF_POST(HDV)                                                                          \
-    hipLaunchKernelGGL(pf_qkv_post_kernel<HDV>, pg, dim3(HDV), 0, st, p.q_raw, p.k_raw, v_src,     \
-                       L.q_norm, L.k_norm, rope, (int)nq, (int)nkv, c.eps, p.q, p.ckq, p.cks,     \
-                       p.cvq, p.cvs)
-        if (hd == 128) SGQ_PF_POST(128);
-        else if (hd == 256) SGQ_PF_POST(256);
-        else SGQ_PF_POST(512);
-#undef SGQ_PF_POST
+        const unsigned wrows = (unsigned)(((long)M * (nq + 2 * nkv) + 3) / 4);
+#define SGQ_PF_WIDE(HDV)                                                                           \
+    hipLaunchKernelGGL(pf_qkv_post_wide_kernel<HDV>, dim3(wrows), dim3(256), 0, st, p.q_raw,      \
+                       p.k_raw, v_src, L.q_norm, L.k_norm, rope, (int)nq, (int)nkv, (int)M, c.eps, \
+                       p.q, p.ckq, p.cks, p.cvq, p.cvs)
+        if (hd == 128)
+            hipLaunchKernelGGL(pf_qkv_post_kernel<128>, pg, dim3(128), 0, st, p.q_raw, p.k_raw, v_src,
+                               L.q_norm, L.k_norm, rope, (int)nq, (int)nkv, c.eps, p.q, p.ckq, p.cks,
+                               p.cvq, p.cvs);
+        else if (hd == 256) SGQ_PF_WIDE(256);
+        else SGQ_PF_WIDE(512);
+#undef SGQ_PF_WIDE
         SGQ_HIP(hipGetLastError());
         const int ring = L.global ? 0 : (int)L.slots;
         const int window = L.global ? 0 : (int)std::min(c.sliding_window, L.slots);
