@@ -20,9 +20,9 @@
 //    lane = slot, wave = a quarter of the head's dims (the quarter's K bytes
 //    in 16-byte loads, q from LDS as wave-uniform broadcasts), quarters
 //    summed in order.  Softmax over the 64 slots per head (one wave per
-//    head).  PV: wave = a quarter of the dims, lane = 1 or 2 dims (head_dim
-//    128: two lanes per dim over odd and even slots), the split's V rows read
-//    slot by slot (a wave reads 64 or 128 contiguous bytes of a row);
+//    head).  PV: wave = 16 of the split's slots, lane = head_dim/64
+//    consecutive dims (a wave reads whole V rows), all 16 V words of a lane
+//    issued at once; the waves' sums are added in LDS in wave order;
 //    splits past the current kv length exit at once;
 //  * merge: workgroup = (query head, 64 dims), splits folded in order up to
 //    the current kv length; writes fp32 rows and/or the O projection's x
@@ -130,8 +130,6 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(
     constexpr int NB = HD / 32;   // Q8 blocks per row
     constexpr int DW = HD / 4;    // dims per wave (a quarter of the head)
     constexpr int PB = DW / 32;   // Q8 blocks per quarter
-    constexpr int ND = DW >= 64 ? DW / 64 : 1;  // PV dims per lane
-    constexpr int SG = DW >= 64 ? 1 : 64 / DW;  // PV slot groups across a wave's lanes
     __shared__ float q_s[QPK][HD];
     __shared__ float sp_s[4][QPK][kGSlots];
     __shared__ float p_s[QPK][kGSlots];
@@ -197,51 +195,106 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(
     }
     __syncthreads();
 
-    // ---- PV: wave = dims [wave·DW, wave·DW + DW), lane = ND dims (SG slot groups)
-    const int sg = SG == 1 ? 0 : lane / DW;
-    const int dl = SG == 1 ? lane : lane % DW;
-    const int d0 = wave * DW + dl * ND;
-    float acc[QPK][ND];
-#pragma unroll
-    for (int h = 0; h < QPK; h++)
-#pragma unroll
-        for (int e = 0; e < ND; e++) acc[h][e] = 0.f;
-#pragma unroll 4
-    for (int i = sg; i < n; i += SG) {
-        const size_t row = (size_t)(t0 + i) * n_kv + kvh;
-        const float sc = f16_bits_to_f32(vs[row * NB + d0 / 32]);
-        float v[ND];
-        if (ND == 2) {
-            const uint32_t w2 = *reinterpret_cast<const uint16_t *>(vq + row * HD + d0);
-            v[0] = sc * (float)(int8_t)(w2 & 0xff);
-            v[ND - 1] = sc * (float)(int8_t)(w2 >> 8);
-        } else {
-            v[0] = sc * (float)vq[row * HD + d0];
+    if constexpr (QPK * HD <= 1024) {
+        // ---- PV: wave w = slots 16w .. 16w+15, lane = DPL consecutive dims (the
+        // whole head across the wave), all 16 V words issued before the FMAs;
+        // the four waves' sums then meet in LDS, added in wave order
+        constexpr int DPL = HD / 64;  // dims per lane: 2, 4, 8
+        float acc[QPK][DPL];
+    #pragma unroll
+        for (int h = 0; h < QPK; h++)
+    #pragma unroll
+            for (int e = 0; e < DPL; e++) acc[h][e] = 0.f;
+        {
+            const int d0 = lane * DPL;
+            uint32_t vw[16][(DPL + 3) / 4];
+            float vsc[16];
+    #pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int slot = 16 * wave + i;
+                const size_t row = (size_t)(t0 + min(slot, n - 1)) * n_kv + kvh;
+                const int8_t *vr = vq + row * HD + d0;
+                if (DPL == 2) {
+                    vw[i][0] = *reinterpret_cast<const uint16_t *>(vr);
+                } else if (DPL == 4) {
+                    vw[i][0] = *reinterpret_cast<const uint32_t *>(vr);
+                } else {
+                    const uint2 t2 = *reinterpret_cast<const uint2 *>(vr);
+                    vw[i][0] = t2.x;
+                    vw[i][(DPL + 3) / 4 - 1] = t2.y;
+                }
+                vsc[i] = f16_bits_to_f32(vs[row * NB + d0 / 32]);
+            }
+    #pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int slot = 16 * wave + i;
+                if (slot < n) {  // wave-uniform
+                    float v[DPL];
+    #pragma unroll
+                    for (int e = 0; e < DPL; e++)
+                        v[e] = vsc[i] * (float)(int8_t)(vw[i][e / 4] >> (8 * (e % 4)));
+    #pragma unroll
+                    for (int h = 0; h < QPK; h++) {
+                        const float p = p_s[h][slot];
+    #pragma unroll
+                        for (int e = 0; e < DPL; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
+                    }
+                }
+            }
         }
-#pragma unroll
-        for (int h = 0; h < QPK; h++) {
-            const float p = p_s[h][i];
-#pragma unroll
-            for (int e = 0; e < ND; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
+        __shared__ float red_s[4][QPK][HD];
+    #pragma unroll
+        for (int h = 0; h < QPK; h++)
+    #pragma unroll
+            for (int e = 0; e < DPL; e++) red_s[wave][h][lane * DPL + e] = acc[h][e];
+        __syncthreads();
+        constexpr int stride = HD + 2;
+        for (int i = tid; i < QPK * HD; i += 256) {
+            const int h = i / HD, d = i % HD;
+            const float a = ((red_s[0][h][d] + red_s[1][h][d]) + red_s[2][h][d]) + red_s[3][h][d];
+            part[((size_t)(kvh * QPK + h) * n_splits + split) * stride + d] = a;
         }
-    }
-    if (SG == 2) {
+        if (tid < QPK) {
+            float *pr = part + ((size_t)(kvh * QPK + tid) * n_splits + split) * stride;
+            pr[HD] = ml_s[tid][0];
+            pr[HD + 1] = ml_s[tid][1];
+        }
+    } else {
+        // ---- PV for wide groups (QPK·HD > 1024, where the LDS reduction
+        // above costs more than it saves): wave = dims [wave·DW, wave·DW +
+        // DW), lane = 2 of them, over all the split's slots
+        constexpr int ND = DW / 64;
+        const int d0 = wave * DW + lane * ND;
+        float acc[QPK][ND];
 #pragma unroll
         for (int h = 0; h < QPK; h++)
 #pragma unroll
-            for (int e = 0; e < ND; e++) acc[h][e] += __shfl_xor(acc[h][e], 32, kWave);
-    }
-    constexpr int stride = HD + 2;
+            for (int e = 0; e < ND; e++) acc[h][e] = 0.f;
+#pragma unroll 4
+        for (int i = 0; i < n; i++) {
+            const size_t row = (size_t)(t0 + i) * n_kv + kvh;
+            const float sc = f16_bits_to_f32(vs[row * NB + d0 / 32]);
+            // ND = 2: one 2-byte word; ND = 1 (head_dim 256): one byte
+            const uint32_t w2 = ND == 2 ? *reinterpret_cast<const uint16_t *>(vq + row * HD + d0)
+                                        : (uint32_t)(uint8_t)vq[row * HD + d0];
+            const float v[2] = {sc * (float)(int8_t)(w2 & 0xff), sc * (float)(int8_t)(w2 >> 8)};
 #pragma unroll
-    for (int h = 0; h < QPK; h++) {
-        float *pr = part + ((size_t)(kvh * QPK + h) * n_splits + split) * stride;
-        if (sg == 0) {
+            for (int h = 0; h < QPK; h++) {
+                const float p = p_s[h][i];
+#pragma unroll
+                for (int e = 0; e < ND; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
+            }
+        }
+        constexpr int stride = HD + 2;
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            float *pr = part + ((size_t)(kvh * QPK + h) * n_splits + split) * stride;
 #pragma unroll
             for (int e = 0; e < ND; e++) pr[d0 + e] = acc[h][e];
-        }
-        if (tid == 0) {
-            pr[HD] = ml_s[h][0];
-            pr[HD + 1] = ml_s[h][1];
+            if (tid == 0) {
+                pr[HD] = ml_s[h][0];
+                pr[HD + 1] = ml_s[h][1];
+            }
         }
     }
 }
@@ -327,7 +380,7 @@ int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_generic: n_q %% n_kv != 0");
     const int qpk = n_q / n_kv;
     SGQ_CHECK(n_splits >= 1 && n_splits <= 65535, "attn_generic: n_splits %d", n_splits);
-    SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0,
+    SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 7) == 0,
               "attn_generic: misaligned cache");
     dim3 grid(n_kv, n_splits);
 #define SGQ_G(HD, Q)                                                                             \

@@ -209,6 +209,29 @@ def test_real_geometry_prefill_graph_and_decode(ctx, oracle):
     eager.close()
 
 
+@pytest.mark.parametrize("mode", [2, 3])
+def test_other_kv_groupings_decode_matches_oracle(ctx, oracle, mode):
+    """The any-geometry attention's other PV forms: head_dim 256 with 8
+    query heads per kv head (one dim per lane over all slots) and head_dim
+    512 with 4 (two dims per lane), 8 steps with a wrapping 4-slot ring."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print(f"kv groupings 8 / 4, mode {mode}", flush=True)
+    cfg = _real_cfg(sgq, n_kv_heads=4, n_kv_heads_global=8, seed=0x31F)
+    model = sgq.Model(ctx, cfg)
+    model.decode_mode = mode
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    ref.kv_source = _device_kv(model, oracle, [])
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([1, 1023, 5, 5, 100, 0, 999, 42]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
+
+
 def test_benchmark_geometry_mode3_matches_oracle(ctx, oracle):
     """Mode 3 at the benchmark's geometry (head_dim 128, Q4_0 head) is the same
     model as modes 0 and 2: checked against the oracle."""
