@@ -256,14 +256,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
 }
 
-// A wave-uniform pointer in scalar registers.
-__device__ __forceinline__ const uint8_t *uni(const uint8_t *p) {
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
-}
-
 // Values passed through an empty asm: to the compiler they are defined here,
 // so a load behind them is waited for here (before the weight stream
 // starts) and not at their first use, where the compiler, which cannot
@@ -378,21 +370,6 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         } else {
             issue_slice(tg, slot, r0 + it * G, n, row_bytes, slice_off, doff);
         }
-    };
-
-    // wave-uniform source of round `it`'s slice (past-the-end rows: row 0)
-    auto slice_src = [&](int it) -> const uint8_t * {
-        const uint8_t *src;
-        if (EPI == kEpiGeglu) {
-            const uint8_t *w = static_cast<const uint8_t *>((it & 1) ? tg.w[1] : tg.w[0]);
-            src = w + (size_t)(u0 + (it >> 1)) * row_bytes + slice_off;
-        } else {
-            const int row = r0 + it * G;
-            int local;
-            const int j = target_of(tg, row < n ? row : 0, &local);
-            src = static_cast<const uint8_t *>(tg.w[j]) + (size_t)local * row_bytes + slice_off;
-        }
-        return uni(src);
     };
 
     // ---- prologue loads (before the stream) --------------------------------
