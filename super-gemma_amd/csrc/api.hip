@@ -457,8 +457,9 @@ int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
     for (const Unbuilt &u : kUnbuilt)
         if (std::strcmp(name, u.name) == 0)
             return fail(SGQ_ERR_UNKNOWN_KERNEL,
-                        "kernel variant '%s' (head_dim 256/512, f16 K/V) is not built: "
-                        "caches are Q8_0 at head_dim 128 here, use '%s'",
+                        "kernel variant '%s' (f16 q / K / V pages) is not built: caches "
+                        "are Q8_0 here (head_dim 128 by name: '%s'; head_dim 256/512 "
+                        "through the typed entry points and the model driver)",
                         name, u.use);
     auto *k = new sgq_kernel;
     if (!resolve(name, k)) {
