@@ -72,6 +72,22 @@ __device__ __forceinline__ h2 i8_pair_f16(uint32_t w, uint32_t sel) {
     return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w ^ 0x80808080u, sel)) + bias;
 }
 
+// A pointer pinned in scalar registers: stops the compiler from turning a
+// per-lane choice between two kernel-argument pointers into a vector load
+// of the chosen pointer (a dependent load before every K/V fetch).
+template <typename T>
+__device__ __forceinline__ T *sgpr_ptr(T *p) {
+    asm volatile("" : "+s"(p));
+    return p;
+}
+// A load through the global address space (global_load, counted by vmcnt
+// only; the generic pointer sgpr_ptr returns would give a flat load, which
+// every LDS wait also waits for).
+template <typename T>
+__device__ __forceinline__ T gload(const T *p) {
+    return *(const __attribute__((address_space(1))) T *)(p);
+}
+
 struct KvSource {
     const int8_t *kq, *vq;      // cache pages
     const uint16_t *ks, *vs;
@@ -411,6 +427,258 @@ __global__ __launch_bounds__(256 * HPW) void attn_prefill_kernel(
         for (int i = 0; i < 16; i++) orow[32 * d + 8 * (i / 4) + 4 * hh + (i % 4)] = o[d][i] * inv;
 }
 
+// Warp-specialized form of the f16 path (the one the launchers use;
+// attn_prefill_kernel serves the int8-PV form): the 8 waves of
+// attn_prefill_kernel compute, and 4 more waves (producers)
+// dequantize the next 128-key tile into the other of two LDS buffers
+// meanwhile, so that the dequant VALU and LDS writes run beside the matrix
+// cores instead of between two barriers (3 waves per SIMD: two computing, one
+// staging).  One barrier per tile.  The per-tile math and the Vᵀ swizzle
+// are those of attn_prefill_kernel.
+constexpr int kWLT = 128;           // keys per LDS tile
+constexpr int kWSub = kWLT / kKT;   // compute tiles per LDS tile
+constexpr int kWVRow = kWLT + 4;    // Vᵀ row: 66 dwords, rows 2 banks apart
+
+template <int HPW>
+__global__ __launch_bounds__(256 * HPW + 256) void attn_prefill_ws_kernel(
+    const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
+    int n_q, int n_kv, int window, float scale, int qtiles, const uint32_t *__restrict__ step) {
+    if (step) q0 = (int)step[3];
+    __shared__ __align__(16) _Float16 vt_s[2][kHD][kWVRow];
+    __shared__ __align__(16) _Float16 k_s[2][kWLT][kKRow];
+
+    int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+    if (gridDim.y % 8 == 0) {  // XCD-aware order, as in attn_prefill_kernel
+        const int L = bx + by * qtiles, per = (int)gridDim.y / 8, idx = L >> 3;
+        by = (L & 7) * per + idx % per;
+        bx = idx / per;
+    }
+    const int tile = qtiles - 1 - bx;  // heaviest (latest) query tile first
+    const int tid = threadIdx.x;
+    const bool producer = tid >= 256 * HPW;
+    const int lane = tid & 63, wave = (tid >> 6) & 3;
+    const int qh = HPW * by + (producer ? 0 : tid >> 8), kvh = (HPW * by) / (n_q / n_kv);
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int qpos_lo = q0 + tile * kQT;
+    const int qpos_hi = q0 + min((tile + 1) * kQT, n_tok) - 1;
+    const int k_lo = window > 0 ? max(0, qpos_lo + 1 - window) : 0;
+    const int k_hi = qpos_hi;
+    const int n_t = (k_hi - k_lo) / kWLT + 1;
+
+    // ---- producers: key pair t/4, 32-block t%4 of a 128-key tile per thread;
+    // tile i+2's quants are loaded into registers before tile i+1 is
+    // dequantized, so their latency overlaps the dequant and the barrier
+    if (producer) {
+        struct Raw {
+            i32x4 k[2][2], v[2][2];  // [key of the pair][16-byte half of the block]
+            uint16_t sk[2], sv[2];
+        };
+        const int t = tid - 256 * HPW;
+        const int blk = t & 3, pair = t >> 2;
+        // kernel-argument pointers pinned in scalar registers (a per-lane
+        // choice between them then costs no dependent pointer load)
+        const int8_t *const kq_c = sgpr_ptr(src.kq), *const vq_c = sgpr_ptr(src.vq);
+        const uint16_t *const ks_c = sgpr_ptr(src.ks), *const vs_c = sgpr_ptr(src.vs);
+        const bool has_chunk = src.ckq != nullptr;
+        const int8_t *const kq_f = has_chunk ? sgpr_ptr(src.ckq) : kq_c;
+        const int8_t *const vq_f = has_chunk ? sgpr_ptr(src.cvq) : vq_c;
+        const uint16_t *const ks_f = has_chunk ? sgpr_ptr(src.cks) : ks_c;
+        const uint16_t *const vs_f = has_chunk ? sgpr_ptr(src.cvs) : vs_c;
+        const int ring = src.ring;
+        auto fetch = [&](int kl, Raw &r) {
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int key = min(kl + 2 * pair + e, k_hi);  // past k_hi: zeroed below
+                const bool fresh = has_chunk && key >= q0;
+                const int slot = fresh ? key - q0 : ring ? key % ring : key;
+                const size_t row = (size_t)slot * n_kv + kvh;
+                const i32x4 *kp = reinterpret_cast<const i32x4 *>((fresh ? kq_f : kq_c) + row * kHD + 32 * blk);
+                const i32x4 *vp = reinterpret_cast<const i32x4 *>((fresh ? vq_f : vq_c) + row * kHD + 32 * blk);
+                r.k[e][0] = gload(kp);
+                r.k[e][1] = gload(kp + 1);
+                r.v[e][0] = gload(vp);
+                r.v[e][1] = gload(vp + 1);
+                r.sk[e] = gload((fresh ? ks_f : ks_c) + row * (kHD / 32) + blk);
+                r.sv[e] = gload((fresh ? vs_f : vs_c) + row * (kHD / 32) + blk);
+            }
+        };
+        auto stage = [&](int kl, const Raw &r, int buf) {
+            uint32_t vpk[32];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int kk = 2 * pair + e;
+                const bool live = kl + kk <= k_hi;
+                const _Float16 sk = live ? __builtin_bit_cast(_Float16, r.sk[e]) : (_Float16)0.f;
+                const _Float16 sv = live ? __builtin_bit_cast(_Float16, r.sv[e]) : (_Float16)0.f;
+                const h2 dk = {sk, sk}, dv = {sv, sv};
+                const int kw[8] = {r.k[e][0].x, r.k[e][0].y, r.k[e][0].z, r.k[e][0].w,
+                                   r.k[e][1].x, r.k[e][1].y, r.k[e][1].z, r.k[e][1].w};
+                const int vw[8] = {r.v[e][0].x, r.v[e][0].y, r.v[e][0].z, r.v[e][0].w,
+                                   r.v[e][1].x, r.v[e][1].y, r.v[e][1].z, r.v[e][1].w};
+                _Float16 kv[32], vv[32];
+#pragma unroll
+                for (int w = 0; w < 8; w++) {
+                    const h2 k01 = i8_pair_f16((uint32_t)kw[w], 0x04010400u) * dk;
+                    const h2 k23 = i8_pair_f16((uint32_t)kw[w], 0x04030402u) * dk;
+                    const h2 v01 = i8_pair_f16((uint32_t)vw[w], 0x04010400u) * dv;
+                    const h2 v23 = i8_pair_f16((uint32_t)vw[w], 0x04030402u) * dv;
+                    kv[4 * w] = k01[0], kv[4 * w + 1] = k01[1], kv[4 * w + 2] = k23[0], kv[4 * w + 3] = k23[1];
+                    vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    h8 kt;
+#pragma unroll
+                    for (int q8 = 0; q8 < 8; q8++) kt[q8] = kv[8 * j + q8];
+                    *reinterpret_cast<h8 *>(&k_s[buf][kk][32 * blk + 8 * j]) = kt;
+                }
+#pragma unroll
+                for (int j = 0; j < 32; j++) {
+                    const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, vv[j]);
+                    vpk[j] = e == 0 ? bits : vpk[j] | (bits << 16);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+                *reinterpret_cast<uint32_t *>(&vt_s[buf][32 * blk + j][vt_col(2 * pair, blk)]) = vpk[j];
+        };
+        Raw ra, rb;
+        fetch(k_lo, ra);
+        if (n_t > 1) fetch(k_lo + kWLT, rb);
+        stage(k_lo, ra, 0);
+        __syncthreads();
+        // iteration it stages tile it+1 (in rb or ra by parity) and first
+        // fetches tile it+2 into the other set
+#pragma unroll 1
+        for (int it = 0; it < n_t; it += 2) {
+            if (it + 1 < n_t) {
+                if (it + 2 < n_t) fetch(k_lo + (it + 2) * kWLT, ra);
+                stage(k_lo + (it + 1) * kWLT, rb, 1);
+            }
+            __syncthreads();
+            if (it + 1 >= n_t) break;
+            if (it + 2 < n_t) {
+                if (it + 3 < n_t) fetch(k_lo + (it + 3) * kWLT, rb);
+                stage(k_lo + (it + 2) * kWLT, ra, 0);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+
+    // ---- consumers (the 8 waves of attn_prefill_kernel)
+    const int my_q = tile * kQT + wave * 32 + l32;
+    const bool q_valid = my_q < n_tok;
+    const int qp = q0 + my_q;
+    const float qscale = scale * 1.44269504088896341f;
+    h8 qb[8];
+    {
+        const float *qr = q + ((size_t)(q_valid ? my_q : 0) * n_q + qh) * kHD + 8 * hh;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 a = *reinterpret_cast<const float4 *>(qr + 16 * c);
+            const float4 b = *reinterpret_cast<const float4 *>(qr + 16 * c + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] * qscale : 0.f);
+        }
+    }
+    f32x16 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[d][i] = 0.f;
+    float m_run = kNegBig, l_run = 0.f;
+    const int wq_lo = q0 + tile * kQT + wave * 32;
+
+    __syncthreads();  // tile 0 staged
+#pragma unroll 1
+    for (int it = 0; it < n_t; it++) {
+        const int kl = k_lo + it * kWLT, buf = it & 1;
+#pragma unroll 1
+        for (int sub = 0; sub < kWSub; sub++) {
+            const int kb = kl + kKT * sub, ko = kKT * sub;
+            if (kb > k_hi) break;
+            f32x16 s[2];
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) s[t2][i] = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+#pragma unroll
+                for (int t2 = 0; t2 < 2; t2++) {
+                    const h8 a = *reinterpret_cast<const h8 *>(&k_s[buf][ko + 32 * t2 + l32][16 * c + 8 * hh]);
+                    s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], s[t2], 0, 0, 0);
+                }
+            const bool full = kb + kKT - 1 <= wq_lo && (window <= 0 || kb > wq_lo + 31 - window);
+            float mx = m_run;
+            if (full) {
+#pragma unroll
+                for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[t2][i]);
+            } else {
+#pragma unroll
+                for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const int key = kb + 32 * t2 + 8 * (i / 4) + 4 * hh + (i % 4);
+                        const bool ok = q_valid && key <= qp && (window <= 0 || key > qp - window);
+                        const float v = ok ? s[t2][i] : kNegBig;
+                        s[t2][i] = v;
+                        mx = fmaxf(mx, v);
+                    }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            if (!(mx > m_run + 8.0f)) mx = m_run;
+            const float corr = __builtin_amdgcn_exp2f(m_run - mx);
+            float rs = 0.f;
+            h8 pb[2][2];
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float v = s[t2][i];
+                    const float p = full || v > kNegBig ? __builtin_amdgcn_exp2f(v - mx) : 0.f;
+                    rs += p;
+                    pb[t2][i / 8][i % 8] = (_Float16)p;
+                }
+            rs += __shfl_xor(rs, 32, kWave);
+            l_run = l_run * corr + rs;
+            m_run = mx;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+#pragma unroll
+                for (int d = 0; d < 4; d++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) o[d][i] *= corr;
+            }
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++)
+#pragma unroll
+                for (int half = 0; half < 2; half++)
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        const int c0 = ko + 32 * t2 + 16 * half + 4 * hh;
+                        const h4 lo = *reinterpret_cast<const h4 *>(&vt_s[buf][32 * d + l32][vt_col(c0, d)]);
+                        const h4 hi = *reinterpret_cast<const h4 *>(&vt_s[buf][32 * d + l32][vt_col(c0 + 8, d)]);
+                        const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t2][half], o[d], 0, 0, 0);
+                    }
+        }
+        __syncthreads();  // this tile read; the producers have staged the next
+    }
+
+    if (!q_valid) return;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    float *orow = out + ((size_t)my_q * n_q + qh) * kHD;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) orow[32 * d + 8 * (i / 4) + 4 * hh + (i % 4)] = o[d][i] * inv;
+}
+
 // Prefill attention at head_dim 256 / 512 (the released checkpoint's
 // sliding and global layers; crates/sg-gguf/src/desc.rs:66-93), same
 // semantics as above.  One query head per workgroup of 8 waves; a query
@@ -670,10 +938,10 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
     const int qtiles = (n_tok + kQT - 1) / kQT;
     const int qpk = n_q / n_kv;
     if (kPrefillPairHeads && qpk % 2 == 0)
-        hipLaunchKernelGGL(attn_prefill_kernel<2>, dim3(qtiles, n_q / 2), dim3(512), 0, st, q, src,
-                           out, n_tok, q0, n_q, n_kv, window, scale, qtiles, step);
+        hipLaunchKernelGGL(attn_prefill_ws_kernel<2>, dim3(qtiles, n_q / 2), dim3(768), 0, st, q,
+                           src, out, n_tok, q0, n_q, n_kv, window, scale, qtiles, step);
     else
-        hipLaunchKernelGGL(attn_prefill_kernel<1>, dim3(qtiles, n_q), dim3(256), 0, st, q, src,
+        hipLaunchKernelGGL(attn_prefill_ws_kernel<1>, dim3(qtiles, n_q), dim3(512), 0, st, q, src,
                            out, n_tok, q0, n_q, n_kv, window, scale, qtiles, step);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
