@@ -38,22 +38,20 @@ namespace {
 constexpr int kGSlots = 64;  // slots per split
 constexpr float kGNegBig = -3.0e38f;
 
+// (GenericPost is declared in sgq_internal.h)
+
+// One head row in one wave: RMSNorm (weight w, or none), then NEOX RoPE
+// with cs when w_rope; lane j holds float4 j (and j + 64 at head_dim 512),
+// the partner float4 j ± head_dim/8 a lane shuffle or the lane's other
+// float4.  Lanes past the row (head_dim 128: lanes 32..63) hold zeros.
 template <int HD>
-__global__ __launch_bounds__(64) void attn_postproj_generic_kernel(
-    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
-    const float *__restrict__ v_src, const float *__restrict__ q_norm,
-    const float *__restrict__ k_norm, const float2 *__restrict__ cs, float eps,
-    const uint32_t *__restrict__ step, uint32_t ring, int n_q, int n_kv, float *__restrict__ q_out,
-    uint16_t *__restrict__ ks, int *__restrict__ kq, uint16_t *__restrict__ vs,
-    int *__restrict__ vq) {
-    constexpr int NF = HD / 4;               // float4s per head row
-    constexpr int NV = (NF + 63) / 64;       // float4s per lane
-    const int lane = threadIdx.x, b = blockIdx.x;
-    const int kind = b < n_q ? 0 : (b < n_q + n_kv ? 1 : 2);
-    const int head = kind == 0 ? b : (kind == 1 ? b - n_q : b - n_q - n_kv);
-    const float *src = (kind == 0 ? q_raw : (kind == 1 ? k_raw : v_src)) + (size_t)head * HD;
-    const float *w = kind == 0 ? q_norm : (kind == 1 ? k_norm : nullptr);
-    float4 x[NV];
+__device__ __forceinline__ void norm_rope_row(const float *__restrict__ src,
+                                              const float *__restrict__ w,
+                                              const float2 *__restrict__ cs, float eps,
+                                              bool w_rope, int lane,
+                                              float4 (&x)[(HD / 4 + 63) / 64]) {
+    constexpr int NF = HD / 4;
+    constexpr int NV = (NF + 63) / 64;
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < NV; v++) {
@@ -71,62 +69,37 @@ __global__ __launch_bounds__(64) void attn_postproj_generic_kernel(
         x[v] = make_float4(x[v].x * inv * wt.x, x[v].y * inv * wt.y, x[v].z * inv * wt.z,
                            x[v].w * inv * wt.w);
     }
-    if (kind != 2) {
-        // NEOX: dim i pairs with i + HD/2 (float4 j with j + NF/2)
-        float4 pr[NV];
-        if (NV == 1) {
-            const int pj = lane < NF / 2 ? lane + NF / 2 : lane - NF / 2;
-            const int src_lane = pj < 64 ? pj : 0;
-            pr[0] = make_float4(__shfl(x[0].x, src_lane, kWave), __shfl(x[0].y, src_lane, kWave),
-                                __shfl(x[0].z, src_lane, kWave), __shfl(x[0].w, src_lane, kWave));
-        } else {
+    if (!w_rope) return;
+    float4 pr[NV];
+    if (NV == 1) {
+        const int pj = lane < NF / 2 ? lane + NF / 2 : lane - NF / 2;
+        const int src_lane = pj < 64 ? pj : 0;
+        pr[0] = make_float4(__shfl(x[0].x, src_lane, kWave), __shfl(x[0].y, src_lane, kWave),
+                            __shfl(x[0].z, src_lane, kWave), __shfl(x[0].w, src_lane, kWave));
+    } else {
 #pragma unroll
-            for (int v = 0; v < NV; v++) pr[v] = x[NV - 1 - v];  // NF = 128: j ± 64
-        }
-#pragma unroll
-        for (int v = 0; v < NV; v++) {
-            const int j = lane + 64 * v;
-            if (j >= NF) continue;
-            const bool lo = j < NF / 2;
-            const int i0 = (lo ? j : j - NF / 2) * 4;  // pair index of the float4's first dim
-            const float sg = lo ? -1.f : 1.f;
-            const float2 c0 = cs[i0], c1 = cs[i0 + 1], c2 = cs[i0 + 2], c3 = cs[i0 + 3];
-            x[v] = make_float4(x[v].x * c0.x + sg * pr[v].x * c0.y,
-                               x[v].y * c1.x + sg * pr[v].y * c1.y,
-                               x[v].z * c2.x + sg * pr[v].z * c2.y,
-                               x[v].w * c3.x + sg * pr[v].w * c3.y);
-        }
+        for (int v = 0; v < NV; v++) pr[v] = x[NV - 1 - v];  // NF = 128: j ± 64
     }
-    if (kind == 0) {
-#pragma unroll
-        for (int v = 0; v < NV; v++) {
-            const int j = lane + 64 * v;
-            if (j < NF) reinterpret_cast<float4 *>(q_out + (size_t)head * HD)[j] = x[v];
-        }
-        return;
-    }
-    const uint32_t pos = step[0];
-    const size_t slot = ring ? pos % ring : pos;
-    uint16_t *sc = kind == 1 ? ks : vs;
-    int *qt = kind == 1 ? kq : vq;
-    const size_t e0 = slot * (size_t)n_kv * HD + (size_t)head * HD;  // row start, elements
 #pragma unroll
     for (int v = 0; v < NV; v++) {
         const int j = lane + 64 * v;
-        if (j < NF) {  // whole 8-lane groups (NF is a multiple of 8)
-            int qv;
-            quant_lane(x[v], j & 7, &sc[(e0 + 4 * j) / 32], &qv);
-            qt[(e0 + 4 * j) / 4] = qv;
-        }
+        if (j >= NF) continue;
+        const bool lo = j < NF / 2;
+        const int i0 = (lo ? j : j - NF / 2) * 4;  // pair index of the float4's first dim
+        const float sg = lo ? -1.f : 1.f;
+        const float2 c0 = cs[i0], c1 = cs[i0 + 1], c2 = cs[i0 + 2], c3 = cs[i0 + 3];
+        x[v] = make_float4(x[v].x * c0.x + sg * pr[v].x * c0.y, x[v].y * c1.x + sg * pr[v].y * c1.y,
+                           x[v].z * c2.x + sg * pr[v].z * c2.y, x[v].w * c3.x + sg * pr[v].w * c3.y);
     }
 }
 
 template <int HD, int QPK>
 __global__ __launch_bounds__(256) void attn_generic_kernel(
-    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
-    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
-    const uint32_t *__restrict__ step, int step_word, int n_kv, int n_splits, float scale,
-    float *__restrict__ part) {
+    // the cache pages are not __restrict__: with post set this kernel writes
+    // the new slot's rows and reads them back after a barrier
+    const float *__restrict__ q, const int8_t *kq, const uint16_t *ks, const int8_t *vq,
+    const uint16_t *vs, const uint32_t *__restrict__ step, int step_word, int n_kv, int n_splits,
+    float scale, float *__restrict__ part, GenericPost post) {
     constexpr int NB = HD / 32;   // Q8 blocks per row
     constexpr int DW = HD / 4;    // dims per wave (a quarter of the head)
     constexpr int PB = DW / 32;   // Q8 blocks per quarter
@@ -141,8 +114,48 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(
     if (t0 >= kv_len) return;  // the merge folds only the live splits
     const int n = (int)min((uint32_t)kGSlots, kv_len - t0);
 
-    for (int i = tid; i < QPK * HD; i += 256)
-        q_s[i / HD][i % HD] = q[((size_t)kvh * QPK + i / HD) * HD + i % HD] * scale;
+    if (post.q_raw == nullptr) {
+        for (int i = tid; i < QPK * HD; i += 256)
+            q_s[i / HD][i % HD] = q[((size_t)kvh * QPK + i / HD) * HD + i % HD] * scale;
+    } else {
+        // the post-projection in every split: this kv head's query heads
+        // (norm, RoPE, pre-scaled) into LDS; the split holding the new slot
+        // also writes the new K/V rows to the cache (norms, RoPE of k, Q8_0),
+        // which its own score and PV loops then read after the barrier
+        constexpr int NF = HD / 4, NV = (NF + 63) / 64;
+        for (int h = wave; h < QPK; h += 4) {
+            float4 x[NV];
+            norm_rope_row<HD>(post.q_raw + ((size_t)kvh * QPK + h) * HD, post.q_norm, post.cs,
+                              post.eps, true, lane, x);
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const int j = lane + 64 * v;
+                if (j < NF)
+                    *reinterpret_cast<float4 *>(&q_s[h][4 * j]) =
+                        make_float4(x[v].x * scale, x[v].y * scale, x[v].z * scale, x[v].w * scale);
+            }
+        }
+        const uint32_t pos = step[0];
+        const uint32_t slot = post.ring ? pos % post.ring : pos;
+        if (slot - t0 < (uint32_t)n && wave < 2) {
+            float4 x[NV];
+            norm_rope_row<HD>((wave == 0 ? post.k_raw : post.v_src) + (size_t)kvh * HD,
+                              wave == 0 ? post.k_norm : nullptr, post.cs, post.eps, wave == 0,
+                              lane, x);
+            const size_t e0 = ((size_t)slot * n_kv + kvh) * HD;  // row start, elements
+            uint16_t *sc = wave == 0 ? post.ks_w : post.vs_w;
+            int *qt = reinterpret_cast<int *>(wave == 0 ? post.kq_w : post.vq_w);
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const int j = lane + 64 * v;
+                if (j < NF) {  // whole 8-lane groups (NF is a multiple of 8)
+                    int qv;
+                    quant_lane(x[v], j & 7, &sc[(e0 + 4 * j) / 32], &qv);
+                    qt[(e0 + 4 * j) / 4] = qv;
+                }
+            }
+        }
+    }
     __syncthreads();
 
     // ---- scores: lane = slot, wave = dims [wave·DW, wave·DW + DW)
@@ -270,19 +283,32 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(
         for (int h = 0; h < QPK; h++)
 #pragma unroll
             for (int e = 0; e < ND; e++) acc[h][e] = 0.f;
-#pragma unroll 4
-        for (int i = 0; i < n; i++) {
-            const size_t row = (size_t)(t0 + i) * n_kv + kvh;
-            const float sc = f16_bits_to_f32(vs[row * NB + d0 / 32]);
-            // ND = 2: one 2-byte word; ND = 1 (head_dim 256): one byte
-            const uint32_t w2 = ND == 2 ? *reinterpret_cast<const uint16_t *>(vq + row * HD + d0)
-                                        : (uint32_t)(uint8_t)vq[row * HD + d0];
-            const float v[2] = {sc * (float)(int8_t)(w2 & 0xff), sc * (float)(int8_t)(w2 >> 8)};
+        // 32 slots' V words and scales are issued before their FMAs (two
+        // round trips for a full split instead of one per few slots)
+        constexpr int VB = 32;
+        for (int i0 = 0; i0 < n; i0 += VB) {
+            uint32_t vw[VB];
+            float vsc[VB];
 #pragma unroll
-            for (int h = 0; h < QPK; h++) {
-                const float p = p_s[h][i];
+            for (int u = 0; u < VB; u++) {
+                const size_t row = (size_t)(t0 + min(i0 + u, n - 1)) * n_kv + kvh;
+                vsc[u] = f16_bits_to_f32(vs[row * NB + d0 / 32]);
+                // ND = 2: one 2-byte word; ND = 1 (head_dim 256): one byte
+                vw[u] = ND == 2 ? *reinterpret_cast<const uint16_t *>(vq + row * HD + d0)
+                                : (uint32_t)(uint8_t)vq[row * HD + d0];
+            }
 #pragma unroll
-                for (int e = 0; e < ND; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
+            for (int u = 0; u < VB; u++) {
+                if (i0 + u < n) {  // wave-uniform
+                    const float v[2] = {vsc[u] * (float)(int8_t)(vw[u] & 0xff),
+                                        vsc[u] * (float)(int8_t)(vw[u] >> 8)};
+#pragma unroll
+                    for (int h = 0; h < QPK; h++) {
+                        const float p = p_s[h][i0 + u];
+#pragma unroll
+                        for (int e = 0; e < ND; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
+                    }
+                }
             }
         }
         constexpr int stride = HD + 2;
@@ -299,38 +325,74 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(
     }
 }
 
-// out[h][d] = Σ_s a_s e^(m_s − M) / Σ_s l_s e^(m_s − M) over the live splits
-// in order; fp32 rows to out and/or the x limbs of the row to xl.
+// out[h][d] = Σ_s a_s e^(m_s − M) / Σ_s l_s e^(m_s − M) over the live splits;
+// fp32 rows to out and/or the x limbs of the row to xl.  Workgroup (h, 64
+// dims), wave w folds the w-th quarter of the splits in 16-split batches
+// (all loads of a batch issued together, running max rescaled per batch),
+// and wave 0 adds the four (M, a, l) in wave order: a fixed order, so the
+// result is bit-reproducible.
 template <int HD>
-__global__ __launch_bounds__(64) void attn_generic_merge_kernel(
+__global__ __launch_bounds__(256) void attn_generic_merge_kernel(
     const float *__restrict__ part, const uint32_t *__restrict__ step, int step_word,
     int n_splits, float *__restrict__ out, BlockLimbs *__restrict__ xl) {
-    constexpr int stride = HD + 2;
-    __shared__ float o_s[64];
-    const int h = blockIdx.x, lane = threadIdx.x, d = blockIdx.y * 64 + lane;
+    constexpr int stride = HD + 2, B = 16;
+    __shared__ float red_s[3][4][64];
+    __shared__ __align__(16) float o_s[64];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int d = blockIdx.y * 64 + lane;
     const uint32_t kv_len = step[step_word];
     const int n_act = min(n_splits, (int)((kv_len + kGSlots - 1) / kGSlots));
+    const int per = (n_act + 3) / 4, s0 = wave * per, s1 = min(n_act, s0 + per);
     const float *ph = part + (size_t)h * n_splits * stride;
-    float M = kGNegBig;
-    for (int s = lane; s < n_act; s += 64) M = fmaxf(M, ph[(size_t)s * stride + HD]);
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, kWave));
-    float a = 0.f, l = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < n_act; s++) {
-        const float *pr = ph + (size_t)s * stride;
-        const float f = __expf(pr[HD] - M);
-        a = __builtin_fmaf(pr[d], f, a);
-        l = __builtin_fmaf(pr[HD + 1], f, l);
-    }
-    const float o = l > 0.f ? a / l : 0.f;
-    if (out) out[(size_t)h * HD + d] = o;
-    if (xl) {
-        o_s[lane] = o;
-        __syncthreads();
-        if (lane < 16) {  // two 32-blocks: 8-lane groups of float4s
-            const float4 v = reinterpret_cast<const float4 *>(o_s)[lane];
-            limbs_block8(v, lane & 7, xl + ((size_t)h * HD + blockIdx.y * 64) / 32 + (lane >> 3));
+    float M = kGNegBig, a = 0.f, l = 0.f;
+    for (int sb = s0; sb < s1; sb += B) {
+        float mv[B], lv[B], av[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const bool live = sb + u < s1;
+            const float *pr = ph + (size_t)(live ? sb + u : s0) * stride;
+            mv[u] = live ? pr[HD] : kGNegBig;
+            lv[u] = live ? pr[HD + 1] : 0.f;
+            av[u] = live ? pr[d] : 0.f;
         }
+        float Mb = M;
+#pragma unroll
+        for (int u = 0; u < B; u++) Mb = fmaxf(Mb, mv[u]);
+        const float r = __expf(M - Mb);
+        a *= r;
+        l *= r;
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const float f = __expf(mv[u] - Mb);
+            a = __builtin_fmaf(av[u], f, a);
+            l = __builtin_fmaf(lv[u], f, l);
+        }
+        M = Mb;
+    }
+    red_s[0][wave][lane] = M;
+    red_s[1][wave][lane] = a;
+    red_s[2][wave][lane] = l;
+    __syncthreads();
+    if (wave == 0) {
+        float Mt = red_s[0][0][lane];
+#pragma unroll
+        for (int w = 1; w < 4; w++) Mt = fmaxf(Mt, red_s[0][w][lane]);
+        float A = 0.f, Lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = __expf(red_s[0][w][lane] - Mt);
+            A = __builtin_fmaf(red_s[1][w][lane], f, A);
+            Lt = __builtin_fmaf(red_s[2][w][lane], f, Lt);
+        }
+        const float o = Lt > 0.f ? A / Lt : 0.f;
+        if (out) out[(size_t)h * HD + d] = o;
+        o_s[lane] = o;
+    }
+    if (!xl) return;
+    __syncthreads();
+    if (tid < 16) {  // two 32-blocks: 8-lane groups of float4s
+        const float4 v = reinterpret_cast<const float4 *>(o_s)[tid];
+        limbs_block8(v, tid & 7, xl + ((size_t)h * HD + blockIdx.y * 64) / 32 + (tid >> 3));
     }
 }
 
@@ -340,43 +402,24 @@ int attn_generic_splits(uint32_t slots) {
     return (int)std::max<uint32_t>(1u, (slots + kGSlots - 1) / kGSlots);
 }
 
-int launch_attn_postproj_generic(hipStream_t st, const float *q_raw, const float *k_raw,
-                                 const float *v_src, const float *q_norm, const float *k_norm,
-                                 const float *cos_sin, float eps, const uint32_t *step,
-                                 uint32_t ring, int n_q, int n_kv, int head_dim, float *q_out,
-                                 uint16_t *ks, int8_t *kq, uint16_t *vs, int8_t *vq) {
-    SGQ_CHECK(q_raw && k_raw && v_src && q_norm && k_norm && cos_sin && step && q_out && ks &&
-                  kq && vs && vq,
-              "attn_postproj: NULL operand");
-    SGQ_CHECK(n_q > 0 && n_kv > 0, "attn_postproj: %d q heads / %d kv heads", n_q, n_kv);
-    SGQ_CHECK(((uintptr_t)q_raw & 15) == 0 && ((uintptr_t)k_raw & 15) == 0 &&
-                  ((uintptr_t)v_src & 15) == 0 && ((uintptr_t)q_out & 15) == 0 &&
-                  ((uintptr_t)kq & 3) == 0 && ((uintptr_t)vq & 3) == 0,
-              "attn_postproj: misaligned buffers");
-    const dim3 grid(n_q + 2 * n_kv);
-    const float2 *cs = reinterpret_cast<const float2 *>(cos_sin);
-#define SGQ_PP(HD)                                                                                \
-    hipLaunchKernelGGL(attn_postproj_generic_kernel<HD>, grid, dim3(64), 0, st, q_raw, k_raw,     \
-                       v_src, q_norm, k_norm, cs, eps, step, ring, n_q, n_kv, q_out, ks,          \
-                       reinterpret_cast<int *>(kq), vs, reinterpret_cast<int *>(vq))
-    switch (head_dim) {
-        case 128: SGQ_PP(128); break;
-        case 256: SGQ_PP(256); break;
-        case 512: SGQ_PP(512); break;
-        default: return fail(SGQ_ERR_VALIDATION, "attn_postproj: head_dim %d (128/256/512)", head_dim);
-    }
-#undef SGQ_PP
-    SGQ_HIP(hipGetLastError());
-    return SGQ_OK;
-}
-
 int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
                                const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
                                const uint32_t *step, int step_word, int n_q, int n_kv,
                                int head_dim, int n_splits, float scale, float *part, float *out,
-                               void *xl) {
-    SGQ_CHECK(q && kq && ks && vq && vs && step && part && (out || xl),
+                               void *xl, const GenericPost *post) {
+    SGQ_CHECK((q || post) && kq && ks && vq && vs && step && part && (out || xl),
               "attn_generic: NULL operand");
+    GenericPost gp{};
+    if (post) {
+        gp = *post;
+        SGQ_CHECK(gp.q_raw && gp.k_raw && gp.v_src && gp.q_norm && gp.k_norm && gp.cs && gp.kq_w &&
+                      gp.ks_w && gp.vq_w && gp.vs_w,
+                  "attn_generic: incomplete post-projection operands");
+        SGQ_CHECK(((uintptr_t)gp.q_raw & 15) == 0 && ((uintptr_t)gp.k_raw & 15) == 0 &&
+                      ((uintptr_t)gp.v_src & 15) == 0 && ((uintptr_t)gp.kq_w & 3) == 0 &&
+                      ((uintptr_t)gp.vq_w & 3) == 0,
+                  "attn_generic: misaligned post-projection operands");
+    }
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_generic: n_q %% n_kv != 0");
     const int qpk = n_q / n_kv;
     SGQ_CHECK(n_splits >= 1 && n_splits <= 65535, "attn_generic: n_splits %d", n_splits);
@@ -385,7 +428,7 @@ int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
     dim3 grid(n_kv, n_splits);
 #define SGQ_G(HD, Q)                                                                             \
     hipLaunchKernelGGL((attn_generic_kernel<HD, Q>), grid, dim3(256), 0, st, q, kq, ks, vq, vs,  \
-                       step, step_word, n_kv, n_splits, scale, part)
+                       step, step_word, n_kv, n_splits, scale, part, gp)
 #define SGQ_GQ(HD)                                                      \
     switch (qpk) {                                                      \
         case 1: SGQ_G(HD, 1); break;                                    \
@@ -407,15 +450,15 @@ int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
     const dim3 mg(n_q, head_dim / 64);
     switch (head_dim) {
         case 128:
-            hipLaunchKernelGGL(attn_generic_merge_kernel<128>, mg, dim3(64), 0, st, part, step,
+            hipLaunchKernelGGL(attn_generic_merge_kernel<128>, mg, dim3(256), 0, st, part, step,
                                step_word, n_splits, out, xt);
             break;
         case 256:
-            hipLaunchKernelGGL(attn_generic_merge_kernel<256>, mg, dim3(64), 0, st, part, step,
+            hipLaunchKernelGGL(attn_generic_merge_kernel<256>, mg, dim3(256), 0, st, part, step,
                                step_word, n_splits, out, xt);
             break;
         default:
-            hipLaunchKernelGGL(attn_generic_merge_kernel<512>, mg, dim3(64), 0, st, part, step,
+            hipLaunchKernelGGL(attn_generic_merge_kernel<512>, mg, dim3(256), 0, st, part, step,
                                step_word, n_splits, out, xt);
     }
     SGQ_HIP(hipGetLastError());

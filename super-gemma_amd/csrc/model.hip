@@ -855,16 +855,16 @@ int record_step_generic(sgq_model *m, float *logits, bool head) {
         qkv.count = L.wv ? 3 : 2;
         if ((rc = launch_gemv_limbs(st, qkv, xl, H))) return rc;
         const float *v_src = L.wv ? m->v_raw : m->k_raw;
-        // q/k norms with weights, weightless v norm, NEOX RoPE, Q8_0 append;
-        // then attention, merged into the O projection's limbs
+        // attention with the post-projection fused in (q/k norms with
+        // weights, weightless v norm, NEOX RoPE, Q8_0 append), merged into
+        // the O projection's limbs
         const float *cs = m->rope_g + (L.global ? hd_s : 0);
-        if ((rc = launch_attn_postproj_generic(st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
-                                               cs, c.eps, m->step, L.global ? 0u : L.slots, nq,
-                                               nkv, hd, m->q, L.ks, L.kq, L.vs, L.vq)) ||
-            (rc = launch_attn_decode_generic(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step,
+        const GenericPost post{m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm, (const float2 *)cs,
+                               c.eps, L.global ? 0u : L.slots, L.kq, L.vq, L.ks, L.vs};
+        if ((rc = launch_attn_decode_generic(st, nullptr, L.kq, L.ks, L.vq, L.vs, m->step,
                                              L.global ? 2 : 1, nq, nkv, hd,
                                              attn_generic_splits(L.slots), c.attn_scale,
-                                             m->part_g, m->attn, xl)))
+                                             m->part_g, m->attn, xl, &post)))
             return rc;
         GemvTargets ot{};
         ot.w[0] = L.wo, ot.y[0] = m->o, ot.end[0] = H, ot.count = 1;
@@ -966,14 +966,13 @@ int record_step_fused(sgq_model *m, float *logits) {
         const float *v_src = L.wv ? m->v_raw : m->k_raw;
         if (m->generic) {
             const float *cs = m->rope_g + (L.global ? c.head_dim : 0);
-            if ((rc = launch_attn_postproj_generic(st, m->q_raw, m->k_raw, v_src, L.q_norm,
-                                                   L.k_norm, cs, c.eps, m->step,
-                                                   L.global ? 0u : L.slots, nq, nkv, hd, m->q,
-                                                   L.ks, L.kq, L.vs, L.vq)) ||
-                (rc = launch_attn_decode_generic(st, m->q, L.kq, L.ks, L.vq, L.vs, m->step,
+            const GenericPost post{m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,
+                                   (const float2 *)cs, c.eps, L.global ? 0u : L.slots,
+                                   L.kq, L.vq, L.ks, L.vs};
+            if ((rc = launch_attn_decode_generic(st, nullptr, L.kq, L.ks, L.vq, L.vs, m->step,
                                                  L.global ? 2 : 1, nq, nkv, hd,
                                                  attn_generic_splits(L.slots), c.attn_scale,
-                                                 m->part_g, nullptr, m->fx.xl_o)))
+                                                 m->part_g, nullptr, m->fx.xl_o, &post)))
                 return rc;
         } else if ((rc = launch_attn_decode_fused(
                         st, m->q_raw, m->k_raw, v_src, L.q_norm, L.k_norm,

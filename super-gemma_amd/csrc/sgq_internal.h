@@ -157,24 +157,30 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
 int launch_attn_reduce(hipStream_t st, const float *part, int n_q, int n_kv, int n_splits,
                        float *out);
 // Decode attention at head_dim 128/256/512 and 1/2/4/8 query heads per kv
-// head (attn_generic.hip).  Post-projection: q/k norms (weights q_norm,
-// k_norm), weightless v norm, NEOX RoPE of q and k with cos_sin [head_dim/2
-// pairs], q -> q_out [n_q × head_dim], k and v quantized (Q8_0) into slot
-// step[0] (mod ring when ring > 0).  Attention: splits of 64 slots
+// head (attn_generic.hip).  q [n_q × head_dim] ready, or with post the
+// post-projection fused in (GenericPost).  Attention: splits of 64 slots
 // (attn_generic_splits(slots) of them cover a cache of `slots`), kv_len =
 // step[step_word], partials in part [n_q × n_splits × (head_dim+2)], merged
 // in split order into out [n_q × head_dim] and/or the x limbs xl.
 int attn_generic_splits(uint32_t slots);
-int launch_attn_postproj_generic(hipStream_t st, const float *q_raw, const float *k_raw,
-                                 const float *v_src, const float *q_norm, const float *k_norm,
-                                 const float *cos_sin, float eps, const uint32_t *step,
-                                 uint32_t ring, int n_q, int n_kv, int head_dim, float *q_out,
-                                 uint16_t *ks, int8_t *kq, uint16_t *vs, int8_t *vq);
+// The q/k/v post-projection fused into the attention (q/k norms with
+// weights q_norm / k_norm, weightless v norm, NEOX RoPE of q and k with cs
+// [head_dim/2 pairs], the new K/V rows quantized (Q8_0) into slot step[0],
+// mod ring when ring > 0): q_raw [n_q × head_dim], k_raw / v_src
+// [n_kv × head_dim], and writable views of the cache pages.
+struct GenericPost {
+    const float *q_raw, *k_raw, *v_src, *q_norm, *k_norm;
+    const float2 *cs;
+    float eps;
+    uint32_t ring;
+    int8_t *kq_w, *vq_w;
+    uint16_t *ks_w, *vs_w;
+};
 int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
                                const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
                                const uint32_t *step, int step_word, int n_q, int n_kv,
                                int head_dim, int n_splits, float scale, float *part, float *out,
-                               void *xl);
+                               void *xl, const GenericPost *post = nullptr);
 // Sets the attention kernels' launch attributes (call before graph capture).
 int attn_prepare();
 // Decode attention with the step's q/k/v post-projection fused in (and,
