@@ -682,13 +682,20 @@ __global__ __launch_bounds__(256 * HPW + 256) void attn_prefill_ws_kernel(
 // Prefill attention at head_dim 256 / 512 (the released checkpoint's
 // sliding and global layers; crates/sg-gguf/src/desc.rs:66-93), same
 // semantics as above.  One query head per workgroup of 8 waves; a query
-// tile of 32 is served by D = HD/128 waves.  Each of them computes the
-// tile's full-width scores Sᵀ = K·Qᵀ (Q from LDS, so no wave holds a whole
-// 512-dim query in registers), runs the same online softmax (the D copies
-// are identical instruction for instruction), and accumulates Oᵀ for its own
-// 128 dims, so no scores cross waves.  K/V LDS tiles hold KT = 16384/HD keys
-// (dequantized by all threads as in the head_dim-128 kernel); compute tiles
-// are 32 keys.
+// tile of 32 is served by D = HD/128 waves, wave ds owning dims [128·ds,
+// 128·ds + 128): its slice of the queries sits in registers (as in the
+// head_dim-128 kernel), it computes the partial scores Sᵀ = K·Qᵀ of a
+// 32-key tile over its dims, and the D partials meet
+// through LDS, summed in slice order, so that the D waves hold
+// bit-identical scores, run the same online softmax and accumulate Oᵀ for
+// their own dims.  Per tile, two barriers:
+//   QK(t) → partials out → barrier → K(t+1) and V(t+1) staged (V double-
+//   buffered), quants of t+2 issued → partials summed, softmax, PV(t) →
+//   barrier.
+// Every thread dequantizes one item per tile: two keys × head_dim/32 dims.
+// The Vᵀ rows carry a pad of 16 dwords per 16 rows, so the item writes
+// (rows 8 or 16 apart within a wave) and the PV reads are free of bank
+// conflicts.
 template <int HD>
 __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
@@ -696,12 +703,18 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     constexpr int D = HD / 128;        // waves per query tile
     constexpr int QTW = 8 / D;         // query tiles per workgroup
     constexpr int QW = 32 * QTW;       // queries per workgroup
-    constexpr int KT = 16384 / HD;     // keys per LDS tile
+    constexpr int KT = 32;             // keys per tile
     constexpr int NB = HD / 32;        // Q8 blocks per row
-    constexpr int QRow = HD + 8, KRow = HD + 8, VRow = KT + 8;
-    __shared__ __align__(16) _Float16 q_s[QW][QRow];
+    constexpr int NP = KT / 2;         // key pairs per tile
+    constexpr int CW = HD / 32;        // dims per dequant item (8 or 16)
+    constexpr int KRow = HD + 8;       // halves
+    constexpr int VS = NP + 4;         // Vᵀ row stride, dwords
+    constexpr int VBuf = HD * VS + (HD / 16) * NP;  // dwords per Vᵀ buffer
+    static_assert(NP * (HD / CW) == 512, "one dequant item per thread");
     __shared__ __align__(16) _Float16 k_s[KT][KRow];
-    __shared__ __align__(16) _Float16 vt_s[HD][VRow];
+    __shared__ __align__(16) uint32_t vt_s[2][VBuf];
+    __shared__ __align__(16) float4 ex_s[8][4][64];  // partial scores [wave][i/4][lane]
+    auto vt_at = [](int row, int col) { return row * VS + (row >> 4) * NP + col; };
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
     if (gridDim.y % 8 == 0) {  // XCD-aware order, as in attn_prefill_kernel
@@ -718,16 +731,20 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     const bool q_valid = my_q < n_tok;
     const int qp = q0 + my_q;
 
-    // the workgroup's queries, pre-scaled (scores in log2 units), as f16
+    // this lane's query (column l32) on the wave's dims, pre-scaled (scores
+    // in log2 units), as the f16 B operand: dims 128·ds + 16c + 8hh .. +7
     const float qscale = scale * 1.44269504088896341f;
-    for (int i = tid; i < QW * (HD / 4); i += 512) {
-        const int r = i / (HD / 4), c4 = i % (HD / 4);
-        const int qi = tile * QW + r;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (qi < n_tok) v = *reinterpret_cast<const float4 *>(q + ((size_t)qi * n_q + qh) * HD + 4 * c4);
-        const h4 hv = {(_Float16)(v.x * qscale), (_Float16)(v.y * qscale), (_Float16)(v.z * qscale),
-                       (_Float16)(v.w * qscale)};
-        *reinterpret_cast<h4 *>(&q_s[r][4 * c4]) = hv;
+    h8 qb[8];
+    {
+        const float *qr = q + ((size_t)(q_valid ? my_q : 0) * n_q + qh) * HD + 128 * ds + 8 * hh;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 a = *reinterpret_cast<const float4 *>(qr + 16 * c);
+            const float4 b = *reinterpret_cast<const float4 *>(qr + 16 * c + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] * qscale : 0.f);
+        }
     }
 
     f32x16 o[4];
@@ -743,84 +760,109 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     const int k_hi = qpos_hi;
     const int wq_lo = q0 + tile * QW + qt * 32;
 
-    for (int kl = k_lo; kl <= k_hi; kl += KT) {
-        __syncthreads();  // the previous tile's LDS reads (and the q tile writes) are done
-        // dequantize: item = (key pair, 32-block)
-        for (int t = tid; t < (KT / 2) * NB; t += 512) {
-            const int blk = t % NB, pair = t / NB;
-            uint32_t vpk[32];
+    // dequant item of this thread: keys 2·pair, 2·pair + 1 of the tile,
+    // dims CW·chunk .. +CW-1
+    const int pair = tid % NP, chunk = tid / NP;
+    const int dim0 = CW * chunk, blk = dim0 >> 5;
+    const int8_t *const kq_c = sgpr_ptr(src.kq), *const vq_c = sgpr_ptr(src.vq);
+    const uint16_t *const ks_c = sgpr_ptr(src.ks), *const vs_c = sgpr_ptr(src.vs);
+    const bool has_chunk = src.ckq != nullptr;
+    const int8_t *const kq_f = has_chunk ? sgpr_ptr(src.ckq) : kq_c;
+    const int8_t *const vq_f = has_chunk ? sgpr_ptr(src.cvq) : vq_c;
+    const uint16_t *const ks_f = has_chunk ? sgpr_ptr(src.cks) : ks_c;
+    const uint16_t *const vs_f = has_chunk ? sgpr_ptr(src.cvs) : vs_c;
+    const int ring = src.ring;
+    typedef int raw_t __attribute__((ext_vector_type(CW / 4)));
+    raw_t rk[2], rv[2];
+    uint16_t rsk[2], rsv[2];
+    auto fetch = [&](int kl) {
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int kk = 2 * pair + e, key = kl + kk;
-                _Float16 kv[32], vv[32];
-                if (key <= k_hi) {
-                    const bool fresh = src.ckq != nullptr && key >= q0;
-                    const int slot = fresh ? key - q0 : src.ring ? key % src.ring : key;
-                    const size_t row = (size_t)slot * n_kv + kvh;
-                    const int8_t *kqb = fresh ? src.ckq : src.kq;
-                    const int8_t *vqb = fresh ? src.cvq : src.vq;
-                    const uint16_t *ksb = fresh ? src.cks : src.ks;
-                    const uint16_t *vsb = fresh ? src.cvs : src.vs;
-                    const i32x4 *kp = reinterpret_cast<const i32x4 *>(kqb + row * HD + 32 * blk);
-                    const i32x4 *vp = reinterpret_cast<const i32x4 *>(vqb + row * HD + 32 * blk);
-                    const i32x4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
-                    const _Float16 sk = __builtin_bit_cast(_Float16, ksb[row * NB + blk]);
-                    const _Float16 sv = __builtin_bit_cast(_Float16, vsb[row * NB + blk]);
-                    const h2 dk = {sk, sk}, dv = {sv, sv};
-                    const int kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-                    const int vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-                    for (int w = 0; w < 8; w++) {
-                        const h2 k01 = i8_pair_f16((uint32_t)kw[w], 0x04010400u) * dk;
-                        const h2 k23 = i8_pair_f16((uint32_t)kw[w], 0x04030402u) * dk;
-                        const h2 v01 = i8_pair_f16((uint32_t)vw[w], 0x04010400u) * dv;
-                        const h2 v23 = i8_pair_f16((uint32_t)vw[w], 0x04030402u) * dv;
-                        kv[4 * w] = k01[0], kv[4 * w + 1] = k01[1], kv[4 * w + 2] = k23[0], kv[4 * w + 3] = k23[1];
-                        vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 32; j++) kv[j] = vv[j] = (_Float16)0.f;
-                }
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    h8 kt;
-#pragma unroll
-                    for (int q8 = 0; q8 < 8; q8++) kt[q8] = kv[8 * j + q8];
-                    *reinterpret_cast<h8 *>(&k_s[kk][32 * blk + 8 * j]) = kt;
-                }
-#pragma unroll
-                for (int j = 0; j < 32; j++) {
-                    const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, vv[j]);
-                    vpk[j] = e == 0 ? bits : vpk[j] | (bits << 16);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 32; j++)
-                *reinterpret_cast<uint32_t *>(&vt_s[32 * blk + j][2 * pair]) = vpk[j];
+        for (int e = 0; e < 2; e++) {
+            const int key = min(kl + 2 * pair + e, k_hi);  // past k_hi: zeroed when staged
+            const bool fresh = has_chunk && key >= q0;
+            const int slot = fresh ? key - q0 : ring ? key % ring : key;
+            const size_t row = (size_t)slot * n_kv + kvh;
+            rk[e] = gload(reinterpret_cast<const raw_t *>((fresh ? kq_f : kq_c) + row * HD + dim0));
+            rv[e] = gload(reinterpret_cast<const raw_t *>((fresh ? vq_f : vq_c) + row * HD + dim0));
+            rsk[e] = gload((fresh ? ks_f : ks_c) + row * NB + blk);
+            rsv[e] = gload((fresh ? vs_f : vs_c) + row * NB + blk);
         }
-        __syncthreads();
-
-#pragma unroll 1
-        for (int ko = 0; ko < KT; ko += 32) {
-            const int kb = kl + ko;
-            if (kb > k_hi) break;
-            // Sᵀ over the full head width, two independent MFMA chains
-            f32x16 s0, s1;
+    };
+    auto stage = [&](int kl, uint32_t *vt) {
+        constexpr int NW = CW / 4;  // quant words per key
+        uint32_t vpk[CW];
 #pragma unroll
-            for (int i = 0; i < 16; i++) s0[i] = s1[i] = 0.f;
+        for (int e = 0; e < 2; e++) {
+            const int kk = 2 * pair + e;
+            const bool live = kl + kk <= k_hi;
+            const _Float16 sk = live ? __builtin_bit_cast(_Float16, rsk[e]) : (_Float16)0.f;
+            const _Float16 sv = live ? __builtin_bit_cast(_Float16, rsv[e]) : (_Float16)0.f;
+            const h2 dk = {sk, sk}, dv = {sv, sv};
+            h8 kt[NW / 2];
+            _Float16 vv[CW];
 #pragma unroll
-            for (int c = 0; c < HD / 16; c += 2) {
-                const h8 a0 = *reinterpret_cast<const h8 *>(&k_s[ko + l32][16 * c + 8 * hh]);
-                const h8 b0 = *reinterpret_cast<const h8 *>(&q_s[qt * 32 + l32][16 * c + 8 * hh]);
-                const h8 a1 = *reinterpret_cast<const h8 *>(&k_s[ko + l32][16 * c + 16 + 8 * hh]);
-                const h8 b1 = *reinterpret_cast<const h8 *>(&q_s[qt * 32 + l32][16 * c + 16 + 8 * hh]);
-                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, s1, 0, 0, 0);
+            for (int w = 0; w < NW; w++) {
+                const h2 k01 = i8_pair_f16((uint32_t)rk[e][w], 0x04010400u) * dk;
+                const h2 k23 = i8_pair_f16((uint32_t)rk[e][w], 0x04030402u) * dk;
+                const h2 v01 = i8_pair_f16((uint32_t)rv[e][w], 0x04010400u) * dv;
+                const h2 v23 = i8_pair_f16((uint32_t)rv[e][w], 0x04030402u) * dv;
+                kt[w / 2][4 * (w & 1)] = k01[0], kt[w / 2][4 * (w & 1) + 1] = k01[1];
+                kt[w / 2][4 * (w & 1) + 2] = k23[0], kt[w / 2][4 * (w & 1) + 3] = k23[1];
+                vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
             }
-            f32x16 s;
 #pragma unroll
-            for (int i = 0; i < 16; i++) s[i] = s0[i] + s1[i];
+            for (int h = 0; h < NW / 2; h++) *reinterpret_cast<h8 *>(&k_s[kk][dim0 + 8 * h]) = kt[h];
+#pragma unroll
+            for (int j = 0; j < CW; j++) {
+                const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, vv[j]);
+                vpk[j] = e == 0 ? bits : vpk[j] | (bits << 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < CW; j++) vt[vt_at(dim0 + j, pair)] = vpk[j];
+    };
+
+    fetch(k_lo);
+    stage(k_lo, vt_s[0]);
+    if (k_lo + KT <= k_hi) fetch(k_lo + KT);
+    __syncthreads();
+    int buf = 0;
+    for (int kl = k_lo; kl <= k_hi; kl += KT) {
+        // partial Sᵀ of the tile over this wave's 128 dims, two MFMA chains
+        f32x16 s0, s1;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s0[i] = s1[i] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; c += 2) {
+            const h8 a0 = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 8 * hh]);
+            const h8 a1 = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 16 + 8 * hh]);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qb[c], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qb[c + 1], s1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            ex_s[wave][j][lane] = make_float4(s0[4 * j] + s1[4 * j], s0[4 * j + 1] + s1[4 * j + 1],
+                                              s0[4 * j + 2] + s1[4 * j + 2], s0[4 * j + 3] + s1[4 * j + 3]);
+        __syncthreads();  // the partials visible; K(t) fully read
+        if (kl + KT <= k_hi) {  // stage t+1 (V into the other buffer), fetch t+2
+            stage(kl + KT, vt_s[buf ^ 1]);
+            if (kl + 2 * KT <= k_hi) fetch(kl + 2 * KT);
+        }
+        // the D partials in slice order: the same bits in every wave of the tile
+        f32x16 s;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float4 t = ex_s[qt * D][j][lane];
+#pragma unroll
+            for (int d2 = 1; d2 < D; d2++) {
+                const float4 u = ex_s[qt * D + d2][j][lane];
+                t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+            }
+            s[4 * j] = t.x, s[4 * j + 1] = t.y, s[4 * j + 2] = t.z, s[4 * j + 3] = t.w;
+        }
+        const uint32_t *vt = vt_s[buf];
+        {
+            const int kb = kl;
             const bool full = kb + 31 <= wq_lo && (window <= 0 || kb > wq_lo + 31 - window);
             float mx = m_run;
 #pragma unroll
@@ -852,19 +894,22 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
 #pragma unroll
                     for (int i = 0; i < 16; i++) o[d][i] *= corr;
             }
-            // Oᵀ (this wave's 128 dims) += Vᵀ·Pᵀ over the tile's two 16-key halves
+            // Oᵀ (this wave's 128 dims) += Vᵀ·Pᵀ over the group's two 16-key halves
 #pragma unroll
-            for (int half = 0; half < 2; half++)
+            for (int hf = 0; hf < 2; hf++)
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
                     const int row = 128 * ds + 32 * d + l32;
-                    const int c0 = ko + 16 * half + 4 * hh;
-                    const h4 lo = *reinterpret_cast<const h4 *>(&vt_s[row][c0]);
-                    const h4 hi = *reinterpret_cast<const h4 *>(&vt_s[row][c0 + 8]);
-                    const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[half], o[d], 0, 0, 0);
+                    const int c0 = (16 * hf + 4 * hh) / 2;  // dword column (key pair)
+                    const uint2 lo = *reinterpret_cast<const uint2 *>(&vt[vt_at(row, c0)]);
+                    const uint2 hi = *reinterpret_cast<const uint2 *>(&vt[vt_at(row, c0 + 4)]);
+                    const h4 l4 = __builtin_bit_cast(h4, lo), h4v = __builtin_bit_cast(h4, hi);
+                    const h8 a = {l4[0], l4[1], l4[2], l4[3], h4v[0], h4v[1], h4v[2], h4v[3]};
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[hf], o[d], 0, 0, 0);
                 }
         }
+        buf ^= 1;
+        __syncthreads();  // V(t) and the slots read; K(t+1), V(t+1) visible
     }
 
     if (!q_valid) return;
