@@ -592,14 +592,14 @@ def measured_peaks(torch):
         out[label + "_tops"] = ops / (ms * 1e-3) / 1e12
     nbytes = 4 << 30
     big = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
-    red = torch.empty(4096 * 256, dtype=torch.float32, device="cuda")
-    ms = best_ms(lambda: P.sgqp_hbm_read(sp, C.c_void_p(big.data_ptr()), nbytes, 4096,
+    red = torch.empty(1024 * 256, dtype=torch.float32, device="cuda")
+    ms = best_ms(lambda: P.sgqp_hbm_read(sp, C.c_void_p(big.data_ptr()), nbytes, 1024,
                                          C.c_void_p(red.data_ptr())))
     out["hbm_read_gbs"] = nbytes / (ms * 1e-3) / 1e9
     del big
     out["note"] = ("int8 MFMA 32x32x32 only (16 waves/CU); the same with 16 cvt + 16 FMA "
                    "per MFMA, and with the f16 scale MFMA too (8 waves/CU, the MMQ's "
-                   "occupancy); streaming read of 4 GiB")
+                   "occupancy); streaming read of 4 GiB (64 KB chunks, nontemporal 16-byte loads)")
     return out
 
 

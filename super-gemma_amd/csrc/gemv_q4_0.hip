@@ -201,7 +201,8 @@ __device__ __forceinline__ void issue_slice(const GemvTargets &tg, uint8_t *slot
 #pragma unroll
     for (int i = 0; i < kRLoads; i++)
         __builtin_amdgcn_global_load_lds((gvoid_t *)(src + doff[i]),
-                                         (lvoid_t *)(slot + i * kWave * 16), 16, 0, 0);
+                                         (lvoid_t *)(slot + i * kWave * 16), 16, 0,
+                                         kStreamPolicy);
 }
 
 // x (fp32, nb blocks of 32) -> limb table, one thread per block.
@@ -366,7 +367,8 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
 #pragma unroll
             for (int i = 0; i < kRLoads; i++)
                 __builtin_amdgcn_global_load_lds((gvoid_t *)(src + doff[i]),
-                                                 (lvoid_t *)(slot + i * kWave * 16), 16, 0, 0);
+                                                 (lvoid_t *)(slot + i * kWave * 16), 16, 0,
+                                         kStreamPolicy);
         } else {
             issue_slice(tg, slot, r0 + it * G, n, row_bytes, slice_off, doff);
         }

@@ -204,7 +204,8 @@ __device__ __forceinline__ void issue(const Stage &st, const Ptrs &pt, const Wav
 #pragma unroll
     for (int i = 0; i < kRLoads; i++)
         __builtin_amdgcn_global_load_lds((gvoid_t *)(src + g.doff[i]),
-                                         (lvoid_t *)(slot + i * kWave * 16), 16, 0, 0);
+                                         (lvoid_t *)(slot + i * kWave * 16), 16, 0,
+                                         kStreamPolicy);
 }
 
 // Issue the first min(npf, rounds) ring slices of a stage (the prefetch

@@ -42,6 +42,11 @@ constexpr int kRSlot = kRLoads * kWave * 16;    // 3072 B: row slice <= 170 bloc
 // s_waitcnt immediate for gfx9: wait until at most `n` vector-memory ops are
 // outstanding (vmcnt bits [3:0] and [15:14]); expcnt/lgkmcnt left at "any".
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+// Cache policy of the weight stream's LDS DMA: nontemporal (the `nt` bit).
+// Weights are read once per step, and a streaming read of 2 GiB through
+// the same per-wave 3-slot ring runs at 6.8 TB/s with it against 5.9
+// without (2048 workgroups; with 16-byte register loads: 7.1 against 6.2).
+constexpr int kStreamPolicy = 2;
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
 

@@ -26,7 +26,9 @@ from typing import Optional, Sequence
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libsgq.so")
+# SGQ_LIB_PATH names another build of the same library (e.g. an A/B variant);
+# by default the in-tree libsgq.so next to this file.
+LIB_PATH = os.environ.get("SGQ_LIB_PATH") or os.path.join(_HERE, "libsgq.so")
 
 SGQ_OK = 0
 ERRORS = {
