@@ -480,65 +480,16 @@ __global__ __launch_bounds__(256) void pf_geglu_q8_kernel(const float4 *__restri
     hq[i] = q;
 }
 
+
 // Per (token, head): q -> rmsnorm(q_norm) + RoPE (fp32 out); k -> rmsnorm
 // (k_norm) + RoPE -> Q8_0 into the chunk's K pages; v -> weightless rmsnorm
-// -> Q8_0 into the chunk's V pages.  Grid [M, n_q + 2 n_kv], 128 threads.
-template <int HD>
-__global__ __launch_bounds__(HD) void pf_qkv_post_kernel(
-    const float *__restrict__ q_raw, const float *__restrict__ k_raw,
-    const float *__restrict__ v_src, const float *__restrict__ wq_norm,
-    const float *__restrict__ wk_norm, const float *__restrict__ cs, int n_q, int n_kv,
-    float eps, float *__restrict__ q_out, int8_t *__restrict__ ckq, uint16_t *__restrict__ cks,
-    int8_t *__restrict__ cvq, uint16_t *__restrict__ cvs) {
-    __shared__ float row[HD];
-    __shared__ float red[HD / 64];
-    const int tok = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
-    const int QD = n_q * HD, KD = n_kv * HD;
-    int kind, head;  // 0 q, 1 k, 2 v
-    if (h < n_q) {
-        kind = 0, head = h;
-    } else if (h < n_q + n_kv) {
-        kind = 1, head = h - n_q;
-    } else {
-        kind = 2, head = h - n_q - n_kv;
-    }
-    const float *src = kind == 0 ? q_raw + (size_t)tok * QD : (kind == 1 ? k_raw : v_src) + (size_t)tok * KD;
-    float v = src[head * HD + t];
-    float ss = v * v;
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
-    if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < HD / 64; w++) tot += red[w];
-    const float inv = 1.0f / sqrtf(tot / (float)HD + eps);
-    v = v * inv * (kind == 0 ? wq_norm[t] : kind == 1 ? wk_norm[t] : 1.f);
-    row[t] = v;
-    __syncthreads();
-    if (kind < 2) {
-        const int i = t % (HD / 2);
-        const float c = cs[((size_t)tok * (HD / 2) + i) * 2];
-        const float sn = cs[((size_t)tok * (HD / 2) + i) * 2 + 1];
-        const float a = row[i], b = row[i + HD / 2];
-        v = t < HD / 2 ? a * c - b * sn : b * c + a * sn;
-    }
-    if (kind == 0) {
-        q_out[(size_t)tok * QD + head * HD + t] = v;
-        return;
-    }
-    float amax = fabsf(v);
-    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
-    const float d = amax * (1.0f / 127.0f);
-    const float id = d > 0.f ? 1.0f / d : 0.f;
-    const size_t e = ((size_t)tok * n_kv + head) * HD + t;
-    (kind == 1 ? ckq : cvq)[e] = (int8_t)(int)__builtin_rintf(v * id);
-    if ((t & 31) == 0) (kind == 1 ? cks : cvs)[e / 32] = f32_to_f16_bits(d);
-}
-
-// The same at head_dim 256 / 512: one wave per (token, head row), lane j
-// holding float4 j (and j + 64), the NEOX partner float4 j ± HD/8 a lane
-// shuffle (256) or the lane's other float4 (512), and the Q8_0 quantization
-// of 8-lane groups (quant_lane): four rows per 256-thread workgroup.
+// -> Q8_0 into the chunk's V pages.
+// At head_dim 128 / 256 / 512: LPR = min(64, head_dim/4)
+// lanes per (token, head row) (half a wave at 128, a whole wave at 256 and
+// 512), lane j holding float4 j (and j + 64 at 512), the NEOX partner
+// float4 j ± HD/8 a lane shuffle within the row's lanes (128, 256) or the
+// lane's other float4 (512), and the Q8_0 quantization of 8-lane groups
+// (quant_lane): 4·(64/LPR) rows per 256-thread workgroup, no barriers.
 template <int HD>
 __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
     const float *__restrict__ q_raw, const float *__restrict__ k_raw,
@@ -546,12 +497,15 @@ __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
     const float *__restrict__ wk_norm, const float *__restrict__ cs, int n_q, int n_kv, int M,
     float eps, float *__restrict__ q_out, int8_t *__restrict__ ckq, uint16_t *__restrict__ cks,
     int8_t *__restrict__ cvq, uint16_t *__restrict__ cvs) {
-    constexpr int NF = HD / 4, NV = NF / 64;
-    static_assert(NV == 1 || NV == 2, "head_dim 256 or 512");
-    const int lane = threadIdx.x & 63;
+    constexpr int NF = HD / 4;                  // float4s per row
+    constexpr int LPR = NF < 64 ? NF : 64;      // lanes per row
+    constexpr int RPW = 64 / LPR;               // rows per wave
+    constexpr int NV = NF / LPR;                // float4s per lane
+    static_assert(NV == 1 || NV == 2, "head_dim 128, 256 or 512");
+    const int lane = threadIdx.x & 63, sub = lane % LPR;
     const int R = n_q + 2 * n_kv;
-    const long rid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (rid >= (long)M * R) return;  // whole waves
+    const long rid = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+    if (rid >= (long)M * R) return;  // whole rows (a row's lanes share a wave)
     const int tok = (int)(rid / R), h = (int)(rid % R);
     const int kind = h < n_q ? 0 : (h < n_q + n_kv ? 1 : 2);
     const int head = kind == 0 ? h : (kind == 1 ? h - n_q : h - n_q - n_kv);
@@ -564,14 +518,14 @@ __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < NV; v++) {
-        x[v] = reinterpret_cast<const float4 *>(src)[lane + 64 * v];
+        x[v] = reinterpret_cast<const float4 *>(src)[sub + LPR * v];
         ss += x[v].x * x[v].x + x[v].y * x[v].y + x[v].z * x[v].z + x[v].w * x[v].w;
     }
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    for (int o = LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
     const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
 #pragma unroll
     for (int v = 0; v < NV; v++) {
-        const float4 wt = w ? reinterpret_cast<const float4 *>(w)[lane + 64 * v]
+        const float4 wt = w ? reinterpret_cast<const float4 *>(w)[sub + LPR * v]
                             : make_float4(1.f, 1.f, 1.f, 1.f);
         x[v] = make_float4(x[v].x * inv * wt.x, x[v].y * inv * wt.y, x[v].z * inv * wt.z,
                            x[v].w * inv * wt.w);
@@ -579,7 +533,7 @@ __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
     if (kind < 2) {
         float4 pr[NV];
         if (NV == 1) {
-            const int pl = lane ^ 32;  // float4 j ± 32 = NF/2
+            const int pl = lane ^ (NF / 2);  // float4 j ± NF/2, within the row's lanes
             pr[0] = make_float4(__shfl(x[0].x, pl, kWave), __shfl(x[0].y, pl, kWave),
                                 __shfl(x[0].z, pl, kWave), __shfl(x[0].w, pl, kWave));
         } else {
@@ -589,7 +543,7 @@ __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
         const float2 *tc = reinterpret_cast<const float2 *>(cs) + (size_t)tok * (HD / 2);
 #pragma unroll
         for (int v = 0; v < NV; v++) {
-            const int j = lane + 64 * v;
+            const int j = sub + LPR * v;
             const bool lo = j < NF / 2;
             const int i0 = (lo ? j : j - NF / 2) * 4;
             const float sg = lo ? -1.f : 1.f;
@@ -603,7 +557,7 @@ __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
     if (kind == 0) {
 #pragma unroll
         for (int v = 0; v < NV; v++)
-            reinterpret_cast<float4 *>(q_out + (size_t)tok * QD + (size_t)head * HD)[lane + 64 * v] = x[v];
+            reinterpret_cast<float4 *>(q_out + (size_t)tok * QD + (size_t)head * HD)[sub + LPR * v] = x[v];
         return;
     }
     const size_t e0 = ((size_t)tok * n_kv + head) * HD;
@@ -611,7 +565,7 @@ __global__ __launch_bounds__(256) void pf_qkv_post_wide_kernel(
     uint16_t *sc = kind == 1 ? cks : cvs;
 #pragma unroll
     for (int v = 0; v < NV; v++) {
-        const int j = lane + 64 * v;
+        const int j = sub + LPR * v;
         int qv;
         quant_lane(x[v], j & 7, &sc[(e0 + 4 * j) / 32], &qv);
         qt[(e0 + 4 * j) / 4] = qv;
@@ -1491,16 +1445,15 @@ int pf_chunk(sgq_model *m, uint32_t M, uint32_t q0) {
         if (L.wv && (rc = mmq(m, st, L.wv, p.xq, p.xs, p.v_raw, M, KD, H))) return rc;
         const float *rope = p.rope + (L.global ? (size_t)M * hd_s : 0);
         const float *v_src = L.wv ? p.v_raw : p.k_raw;
-        const dim3 pg(M, nq + 2 * nkv);
-        const unsigned wrows = (unsigned)(((long)M * (nq + 2 * nkv) + 3) / 4);
+        const long prow = (long)M * (nq + 2 * nkv);  // (token, head row) pairs
 #define SGQ_PF_WIDE(HDV)                                                                           \
-    hipLaunchKernelGGL(pf_qkv_post_wide_kernel<HDV>, dim3(wrows), dim3(256), 0, st, p.q_raw,      \
+    hipLaunchKernelGGL(pf_qkv_post_wide_kernel<HDV>,                                             \
+                       dim3((unsigned)((prow + 4 * (HDV == 128 ? 2 : 1) - 1) /                     \
+                                       (4 * (HDV == 128 ? 2 : 1)))),                              \
+                       dim3(256), 0, st, p.q_raw,                                                 \
                        p.k_raw, v_src, L.q_norm, L.k_norm, rope, (int)nq, (int)nkv, (int)M, c.eps, \
                        p.q, p.ckq, p.cks, p.cvq, p.cvs)
-        if (hd == 128)
-            hipLaunchKernelGGL(pf_qkv_post_kernel<128>, pg, dim3(128), 0, st, p.q_raw, p.k_raw, v_src,
-                               L.q_norm, L.k_norm, rope, (int)nq, (int)nkv, c.eps, p.q, p.ckq, p.cks,
-                               p.cvq, p.cvs);
+        if (hd == 128) SGQ_PF_WIDE(128);
         else if (hd == 256) SGQ_PF_WIDE(256);
         else SGQ_PF_WIDE(512);
 #undef SGQ_PF_WIDE
