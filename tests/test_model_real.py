@@ -209,6 +209,46 @@ def test_real_geometry_prefill_graph_and_decode(ctx, oracle):
     eager.close()
 
 
+def test_real_geometry_prefill_ring_wrap_matches_one_chunk(ctx, oracle):
+    """A 21-token prompt through an 8-slot sliding ring in chunks of 8 and of
+    4: the later chunks read the ring (wrapped: early positions leave it as
+    later ones arrive) together with their own chunk pages, at head_dim 256
+    (ring) and 512 (linear cache).  Against the same prompt in one chunk
+    (every key from the chunk's pages) on a model with the same weights:
+    the same Q8_0 rows, and with at most 21 keys per query every query's
+    keys sit in one 32-key attention tile in all three runs, so the logits
+    agree bit for bit (a wrong slot moves them by O(1): swapping two prompt
+    tokens moves them by 1.7× the largest logit); then two decode steps
+    from each cache, also bit for bit."""
+    import sgq
+
+    print("real geometry prefill ring wrap", flush=True)
+    toks = [3, 14, 159, 265, 358, 979, 323, 846, 264, 338, 327, 950, 288, 419, 716, 939, 937,
+            510, 582, 97, 494]
+    models, outs = [], []
+    for chunk in (32, 8, 4):
+        cfg = _real_cfg(sgq, seed=0x31D, sliding_window=8, max_ctx=40, prefill_chunk=chunk)
+        m = sgq.Model(ctx, cfg)
+        lg = empty(cfg.vocab, torch.float32)
+        m.prefill(toks, lg)
+        torch.cuda.synchronize()
+        models.append(m)
+        outs.append(host(lg))
+    for c, o in zip((8, 4), outs[1:]):
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), f"chunk {c}"
+    for i, t in enumerate([7, 77]):
+        got = []
+        for m in models:
+            lg = empty(m.cfg.vocab, torch.float32)
+            m.decode(t, lg)
+            torch.cuda.synchronize()
+            got.append(host(lg))
+        for c, g in zip((8, 4), got[1:]):
+            assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32)), f"decode {i}, chunk {c}"
+    for m in models:
+        m.close()
+
+
 @pytest.mark.parametrize("mode", [2, 3])
 def test_other_kv_groupings_decode_matches_oracle(ctx, oracle, mode):
     """The any-geometry attention's other PV forms: head_dim 256 with 8
