@@ -167,6 +167,39 @@ def test_real_geometry_long_context_matches_oracle(ctx, oracle, mode):
     model.close()
 
 
+@pytest.mark.parametrize("mode", [2, 3])
+def test_real_geometry_8k_context_matches_oracle(ctx, oracle, mode):
+    """The benchmark's context at this geometry: an 8192-position cache
+    (sgq_model_fill_cache) under a full 1024-slot sliding ring (16 splits)
+    and a global layer at head_dim 512 with 8 query heads per kv head over
+    8193+ positions (129 live splits of 64 slots, the merge over all of
+    them), then decode steps against the oracle reading the device's
+    pages."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print(f"real geometry 8K context, mode {mode}", flush=True)
+    cfg = _real_cfg(sgq, n_layers=3, sliding_window=1024, max_ctx=8200, seed=0x31F)
+    model = sgq.Model(ctx, cfg)
+    model.decode_mode = mode
+    model.fill_cache(8192)
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    pages = {}
+    for l in range(cfg.n_layers):
+        for kind in ("k", "v"):
+            pages[(l, kind)] = (model.read_tensor(f"{kind}_scales", l, np.uint16),
+                                model.read_tensor(f"{kind}_quants", l, np.int8))
+    ref.preload_cache(pages, 8192)
+    ref.kv_source = _device_kv(model, oracle, [])
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([5, 600]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
+
+
 def test_real_geometry_prefill_graph_and_decode(ctx, oracle):
     """Chunked prefill (two chunks: 16 + 5 tokens, the second attending the
     first's cached keys and its own pages; int8 MMQs on Q8_0 activations,
