@@ -200,6 +200,35 @@ def test_real_geometry_8k_context_matches_oracle(ctx, oracle, mode):
     model.close()
 
 
+def test_real_geometry_long_prompt_decode_continues_prefill(ctx, oracle):
+    """A 1099-token prompt in chunks of 512 (the third chunk starts past the
+    1024-slot sliding window, so the ring has wrapped) followed by one
+    decode step, against the same 1100 tokens prefilled on a model with the
+    same weights: the decode step reads the prefill's ring and global
+    pages and must give the last position's logits to the prefill bar
+    (decode runs its GEMVs on 15-bit activations where the prefill's MMQs
+    take Q8_0 ones, hence that bar) with the same top-1."""
+    import sgq
+
+    print("real geometry long prompt: decode continues prefill", flush=True)
+    rng = np.random.default_rng(0x5107)
+    cfg = _real_cfg(sgq, n_layers=3, sliding_window=1024, max_ctx=1200, prefill_chunk=512,
+                    seed=0x320)
+    toks = [int(t) for t in rng.integers(0, cfg.vocab, 1100)]
+    a = sgq.Model(ctx, cfg)
+    la = empty(cfg.vocab, torch.float32)
+    a.prefill(toks[:-1])
+    a.decode(toks[-1], la)
+    b = sgq.Model(ctx, cfg)
+    lb = empty(cfg.vocab, torch.float32)
+    b.prefill(toks, lb)
+    torch.cuda.synchronize()
+    assert a.position == b.position == 1100
+    _check_prefill_logits(host(la), host(lb))
+    a.close()
+    b.close()
+
+
 def test_real_geometry_prefill_graph_and_decode(ctx, oracle):
     """Chunked prefill (two chunks: 16 + 5 tokens, the second attending the
     first's cached keys and its own pages; int8 MMQs on Q8_0 activations,
