@@ -204,6 +204,36 @@ def test_model_prefill_matches_oracle_then_decodes(ctx, oracle, chunk, n_tok):
     model.close()
 
 
+def test_model_prefill_past_window_matches_oracle(ctx, oracle):
+    """A 1100-token prompt in chunks of 512 at the benchmark's 1024-slot
+    sliding window: the third chunk (positions 1024..1099) reads keys from
+    the wrapped ring (slots = position mod 1024) over several 128-key LDS
+    tiles together with its own pages, and the global layers from the
+    linear cache; last-token logits vs the oracle's chunked prefill, then
+    2 decode steps from the caches the prefill filled."""
+    import sgq
+    from oracle.model import OraclePrefill
+
+    print("model prefill past the window", flush=True)
+    cfg = _small_cfg(sgq, sliding_window=1024, max_ctx=1200, prefill_chunk=512, seed=0x1100)
+    model = sgq.Model(ctx, cfg)
+    d = cfg.as_dict()
+    ref = OraclePrefill(d, _weights(model, d))
+    toks = np.random.default_rng(0x1100).integers(0, cfg.vocab, 1100)
+    logits = empty(cfg.vocab, torch.float32)
+    model.prefill(toks, logits)
+    torch.cuda.synchronize()
+    want = None
+    for c0 in range(0, len(toks), 512):
+        want = ref.prefill(toks[c0:c0 + 512])
+    _check_logits(host(logits), want, "prefill")
+    for i, t in enumerate([5, 900]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), f"after prefill {i}")
+    model.close()
+
+
 def test_model_prefill_full_width(ctx, oracle):
     """The benchmark widths at 2 layers, a 300-token prompt in one chunk."""
     import sgq
