@@ -26,7 +26,8 @@ FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-mcode-object-version=5",
-    # Packed FP32 (v_pk_*_f32) stays off on this pool; see DESIGN.md.
+    # Packed FP32 (v_pk_*_f32) stays off: some of its forms have given wrong
+    # results on this hardware pool without an error.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-command-line-argument",
