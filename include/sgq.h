@@ -105,11 +105,28 @@ typedef struct {
  *   attn_prefill_global_flash_ipv_hd128  (attn_prefill_global_flash_sp_ipv.wgsl:24-35)
  *       0 q fp32, 1 k_quants, 2 k_scales, 3 v_quants, 4 key-blocked v_scales,
  *       5 out, 6 step; push f32 scale; groups [32, ceil(M/16), 1]
- * M (prefill) is the out binding's range / (32·128·4).  The reference's
- * head_dim 256/512 f16-cache variants (attn_decode_sliding, attn_decode_global,
- * attn_decode_global_q8k, attn_reduce_d256/d512, attn_prefill_sliding[_ring],
- * attn_prefill_global_flash_sp_iq/_sp_q8, kv_append_sliding/global) return
- * SGQ_ERR_UNKNOWN_KERNEL with the name of the form above to use. */
+ * M (prefill) is the out binding's range / (32·128·4).
+ * The real checkpoint's decode side over f16 pages (crates/sg-gpu/build.rs:
+ * 255-394; record_layer, crates/sg-model/src/graph.rs:572-650), 32 q heads:
+ *   attn_decode_sliding   head_dim 256, 16 kv heads; 0 q f16 [32 × 256],
+ *       1 K ring f16 [slot × 16 × 256], 2 V ring f16, 3 part fp32
+ *       [32 × n_splits × 258], 4 step; kv_len = step[1]
+ *   attn_decode_global    head_dim 512, 4 kv heads, the same bindings;
+ *       kv_len = step[2]
+ *   attn_decode_global_q8k  0 q, 1 k_quants i8 [slot × 4 × 512], 2 k_scales
+ *       f16 [slot × 4 × 16], 3 V f16, 4 part, 5 step
+ *       (all three: push {n_splits: u32, scale: f32}; groups [n_kv, n_splits,
+ *       1]; split s covers the s-th ceil(kv_len/n_splits) slots;
+ *       attn_decode_sliding.wgsl:16-50)
+ *   attn_reduce_d256 / attn_reduce_d512  0 part, 1 out f16 [32 × HD]; push
+ *       n_splits; groups [32, 1, 1]  (attn_reduce.wgsl:14-30)
+ *   kv_append_sliding / kv_append_global  0 src f16 [n_tok × ROW], 1 dst f16
+ *       [slot × ROW], 2 step; ROW 4096 into the 1024-slot ring (slot =
+ *       (step[0] + t) mod 1024) / 2048 linear; groups cover n_tok·ROW
+ *       elements at 256 a group  (kv_append.wgsl:15-35)
+ * The reference's prefill over f16 pages (attn_prefill_sliding[_ring],
+ * attn_prefill_global_flash_sp_iq/_sp_q8) returns SGQ_ERR_UNKNOWN_KERNEL
+ * with the name of the Q8_0 form above to use. */
 int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
                       sgq_kernel_info *info);
 /* Number of registered variant names / the i-th one (for enumeration). */

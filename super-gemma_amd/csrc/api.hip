@@ -90,6 +90,9 @@ enum class Kind {
     AttnPrefill,   // attn_prefill_{global_flash,sliding_ring}_q8_hd128
     AttnPrefillIpv,  // attn_prefill_global_flash_ipv_hd128 (int8 PV, key-blocked V)
     AppendVQ8,     // kv_append_global_v_q8 (V in 32-key blocks per column)
+    AttnDecodePages,  // attn_decode_{sliding,global,global_q8k}: f16 q / V pages
+    AttnReducePages,  // attn_reduce_d{256,512}: f16 rows out
+    AppendF16,     // kv_append_{sliding,global}: f16 rows
 };
 
 struct sgq_kernel {
@@ -123,6 +126,8 @@ const char *const kNames[] = {
     "attn_decode_sliding_q8_hd128", "attn_decode_global_q8_hd128", "attn_reduce_d128",
     "attn_prefill_global_flash_q8_hd128", "attn_prefill_sliding_ring_q8_hd128",
     "kv_append_global_v_q8", "attn_prefill_global_flash_ipv_hd128",
+    "attn_decode_sliding", "attn_decode_global", "attn_decode_global_q8k",
+    "attn_reduce_d256", "attn_reduce_d512", "kv_append_sliding", "kv_append_global",
 };
 
 // The benchmark geometry of the hd128 attention forms (32 query heads over
@@ -131,25 +136,22 @@ const char *const kNames[] = {
 // variants (crates/sg-gpu/build.rs:331-430).
 constexpr uint32_t kAttnNQ = 32, kAttnNKv = 16, kAttnWindow = 1024;
 
+// The real checkpoint's decode-side variants over f16 pages (crates/sg-gpu/
+// build.rs:255-394): head_dim 256 sliding (16 kv heads, 2 q heads each,
+// ring 1024) and 512 global (4 kv heads, 8 q heads each, K = V rows).
+constexpr uint32_t kRealNQ = 32, kSlNKv = 16, kGlNKv = 4;
+
 // Reference variants this build does not provide: the real checkpoint's
-// head_dim 256 (sliding) / 512 (global) geometry with f16 K/V caches
-// (crates/sg-gpu/build.rs:255-430, :2271).  Every cache here is Q8_0 and
-// every attention kernel head_dim 128; lookup names the form to use instead.
+// prefill attention over f16 pages (crates/sg-gpu/build.rs:395-430).  The
+// prefill here runs over Q8_0 pages; lookup names the form to use instead.
 struct Unbuilt {
     const char *name, *use;
 };
 const Unbuilt kUnbuilt[] = {
-    {"attn_decode_sliding", "attn_decode_sliding_q8_hd128"},
-    {"attn_decode_global", "attn_decode_global_q8_hd128"},
-    {"attn_decode_global_q8k", "attn_decode_global_q8_hd128"},
-    {"attn_reduce_d256", "attn_reduce_d128"},
-    {"attn_reduce_d512", "attn_reduce_d128"},
     {"attn_prefill_sliding", "attn_prefill_sliding_ring_q8_hd128"},
     {"attn_prefill_sliding_ring", "attn_prefill_sliding_ring_q8_hd128"},
     {"attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_q8_hd128"},
     {"attn_prefill_global_flash_sp_q8", "attn_prefill_global_flash_q8_hd128"},
-    {"kv_append_sliding", "kv_append_sliding_q8"},
-    {"kv_append_global", "kv_append_global_q8"},
 };
 
 // RoPE variants: (name, head_dim, rot_dims, n_heads).  The first four are
@@ -250,6 +252,43 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         k->k = kAttnNQ;
         k->n = kAttnNKv;
         k->param = name == "attn_decode_sliding_q8_hd128" ? 1 : 2;
+        return true;
+    }
+    if (name == "attn_decode_sliding" || name == "attn_decode_global" ||
+        name == "attn_decode_global_q8k") {
+        // f16: 0 q f16 [32 × HD], 1 k pages, 2 v pages f16 [slot × n_kv × HD],
+        //   3 part fp32 [32 × n_splits × (HD + 2)], 4 step
+        // q8k: 1 k_quants i8, 2 k_scales f16 [slot × n_kv × HD/32], 3 v f16,
+        //   4 part, 5 step
+        // push {n_splits: u32, scale: f32}; groups [n_kv, n_splits, 1];
+        // kv_len = step[1] (sliding) or step[2] (global)
+        // (attn_decode_sliding.wgsl:16-50, attn_decode_global_q8k.wgsl)
+        const bool q8k = name == "attn_decode_global_q8k";
+        const bool sl = name == "attn_decode_sliding";
+        k->kind = Kind::AttnDecodePages;
+        k->info = {{256, 1, 1}, q8k ? 6u : 5u, 8, 0};
+        k->k = sl ? 256 : 512;          // head_dim
+        k->n = sl ? kSlNKv : kGlNKv;    // kv heads
+        k->param = (sl ? 1 : 2) | (q8k ? 4 : 0);  // step word, Q8_0 K
+        return true;
+    }
+    if (name == "attn_reduce_d256" || name == "attn_reduce_d512") {
+        // 0 part, 1 out f16 [32 × HD]; push n_splits; groups [32, 1, 1]
+        // (attn_reduce.wgsl:14-30)
+        k->kind = Kind::AttnReducePages;
+        k->info = {{256, 1, 1}, 2, 4, 0};
+        k->k = name == "attn_reduce_d256" ? 256 : 512;
+        return true;
+    }
+    if (name == "kv_append_sliding" || name == "kv_append_global") {
+        // 0 src f16 [n_tok × ROW], 1 dst f16 [slot × ROW], 2 step; groups
+        // cover n_tok × ROW elements at 256 per group; ROW 4096 (sliding,
+        // ring 1024) or 2048 (global, linear) (kv_append.wgsl:15-35)
+        k->kind = Kind::AppendF16;
+        k->info = {{256, 1, 1}, 3, 0, 0};
+        const bool sl = name == "kv_append_sliding";
+        k->k = sl ? kSlNKv * 256 : kGlNKv * 512;  // row halves
+        k->param = sl ? kAttnWindow : 0;          // ring slots
         return true;
     }
     if (name == "attn_reduce_d128") {
@@ -457,9 +496,10 @@ int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
     for (const Unbuilt &u : kUnbuilt)
         if (std::strcmp(name, u.name) == 0)
             return fail(SGQ_ERR_UNKNOWN_KERNEL,
-                        "kernel variant '%s' (f16 q / K / V pages) is not built: caches "
-                        "are Q8_0 here (head_dim 128 by name: '%s'; head_dim 256/512 "
-                        "through the typed entry points and the model driver)",
+                        "kernel variant '%s' (prefill over f16 pages) is not built: "
+                        "prefill runs over Q8_0 pages here (head_dim 128 by name: '%s'; "
+                        "head_dim 256/512 through the typed entry points and the model "
+                        "driver)",
                         name, u.use);
     auto *k = new sgq_kernel;
     if (!resolve(name, k)) {
@@ -705,6 +745,71 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                 return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
             return launch_attn_reduce(st, static_cast<const float *>(p0), (int)nq, (int)kernel->n,
                                       (int)n_splits, static_cast<float *>(p1));
+        }
+        case Kind::AttnDecodePages: {
+            const bool q8k = kernel->param & 4;
+            const uint32_t nb = kernel->info.bindings;
+            void *pp[6];
+            uint64_t rr[6];
+            for (uint32_t i = 0; i < nb; i++)
+                if ((rc = B.get(i, &pp[i], &rr[i]))) return rc;
+            uint32_t n_splits;
+            float scale;
+            std::memcpy(&n_splits, push, 4);
+            std::memcpy(&scale, static_cast<const uint8_t *>(push) + 4, 4);
+            const uint32_t hd = kernel->k, nkv = kernel->n;
+            if (n_splits == 0 || groups[0] != nkv || groups[1] != n_splits || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, n_splits=%u, 1]",
+                            kernel->name.c_str(), nkv, n_splits);
+            const uint32_t part_b = nb - 2, step_b = nb - 1;
+            if (rr[0] && rr[0] < (uint64_t)kRealNQ * hd * 2)
+                return fail(SGQ_ERR_VALIDATION, "%s: q binding too small", kernel->name.c_str());
+            if (rr[part_b] && rr[part_b] < (uint64_t)kRealNQ * n_splits * (hd + 2) * 4)
+                return fail(SGQ_ERR_VALIDATION, "%s: part binding too small", kernel->name.c_str());
+            if (rr[step_b] && rr[step_b] < 12)
+                return fail(SGQ_ERR_VALIDATION, "%s: step binding too small", kernel->name.c_str());
+            return launch_attn_decode_pages(
+                st, static_cast<const uint16_t *>(pp[0]), pp[1],
+                q8k ? static_cast<const uint16_t *>(pp[2]) : nullptr,
+                static_cast<const uint16_t *>(pp[q8k ? 3 : 2]), static_cast<float *>(pp[part_b]),
+                static_cast<const uint32_t *>(pp[step_b]), (int)(kernel->param & 3), (int)hd,
+                (int)kRealNQ, (int)nkv, (int)n_splits, scale);
+        }
+        case Kind::AttnReducePages: {
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1))) return rc;
+            uint32_t n_splits;
+            std::memcpy(&n_splits, push, 4);
+            const uint32_t hd = kernel->k;
+            if (n_splits == 0 || groups[0] != kRealNQ || groups[1] != 1 || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, 1, 1], n_splits > 0",
+                            kernel->name.c_str(), kRealNQ);
+            if ((r0 && r0 < (uint64_t)kRealNQ * n_splits * (hd + 2) * 4) ||
+                (r1 && r1 < (uint64_t)kRealNQ * hd * 2))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            return launch_attn_reduce_pages(st, static_cast<const float *>(p0), (int)kRealNQ,
+                                            (int)hd, (int)n_splits, static_cast<uint16_t *>(p1));
+        }
+        case Kind::AppendF16: {
+            if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
+                return rc;
+            const uint32_t row = kernel->k;
+            if (!r0 || r0 % ((uint64_t)row * 2))
+                return fail(SGQ_ERR_VALIDATION, "%s: src range must be whole rows of %u halves",
+                            kernel->name.c_str(), row);
+            const uint64_t n_tok = r0 / ((uint64_t)row * 2);
+            if ((uint64_t)groups[0] * groups[1] * groups[2] * 256 < n_tok * row)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups cover fewer than %llu elements",
+                            kernel->name.c_str(), (unsigned long long)(n_tok * row));
+            if (kernel->param && n_tok > kernel->param)
+                return fail(SGQ_ERR_VALIDATION, "%s: %llu rows exceed the %u-slot ring",
+                            kernel->name.c_str(), (unsigned long long)n_tok, kernel->param);
+            if ((r1 && r1 < (uint64_t)(kernel->param ? kernel->param : n_tok) * row * 2) ||
+                (r2 && r2 < 4))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            return launch_kv_append_f16(st, static_cast<const uint16_t *>(p0),
+                                        static_cast<uint16_t *>(p1),
+                                        static_cast<const uint32_t *>(p2), (uint32_t)n_tok, row,
+                                        kernel->param);
         }
         case Kind::AttnPrefill: {
             const bool ring = kernel->param != 0;

@@ -154,6 +154,23 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
                              const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
                              const uint32_t *step, int step_word, int n_q, int n_kv, int n_splits,
                              float scale, float *part);
+// Decode attention over f16 pages (or Q8_0 K with f16 V) for the released
+// checkpoint's names (attn_pages.hip): q f16 [n_q × head_dim], pages
+// [slot × n_kv × head_dim], k_scales non-null selects Q8_0 K (f16 scale per
+// 32 dims); kv_len = step[step_word]; split s covers the s-th chunk of
+// ceil(kv_len / n_splits) slots; partials [n_q × n_splits × (head_dim + 2)].
+// Built: head_dim 256 with 2 q heads per kv head (f16 K), 512 with 8 (f16
+// or Q8_0 K).
+int launch_attn_decode_pages(hipStream_t st, const uint16_t *q, const void *k,
+                             const uint16_t *k_scales, const uint16_t *v, float *part,
+                             const uint32_t *step, int step_word, int head_dim, int n_q, int n_kv,
+                             int n_splits, float scale);
+// Their merge in split order into f16 rows [n_q × head_dim] (256 / 512).
+int launch_attn_reduce_pages(hipStream_t st, const float *part, int n_q, int head_dim,
+                             int n_splits, uint16_t *out);
+// f16 rows [n_tok × row] into pages at slot step[0] + t (mod ring if ring > 0).
+int launch_kv_append_f16(hipStream_t st, const uint16_t *src, uint16_t *dst,
+                         const uint32_t *step, uint32_t n_tok, uint32_t row, uint32_t ring);
 int launch_attn_reduce(hipStream_t st, const float *part, int n_q, int n_kv, int n_splits,
                        float *out);
 // Decode attention at head_dim 128/256/512 and 1/2/4/8 query heads per kv

@@ -72,8 +72,10 @@ def test_registry_names_resolve_without_device():
 
 def test_attention_variants_layouts_and_unbuilt_names():
     """The record_layer attention / KV-append surface (crates/sg-model/src/
-    graph.rs:560-656) at head_dim 128 with Q8_0 K/V; the reference's hd
-    256/512 f16-cache names fail with UnknownKernel naming the form to use."""
+    graph.rs:560-656): head_dim 128 with Q8_0 K/V, and the real checkpoint's
+    decode side over f16 pages with the reference's binding and push layout
+    (crates/sg-gpu/build.rs:255-394); its prefill over f16 pages fails with
+    UnknownKernel naming the form to use."""
     import sgq
 
     L = sgq.lib()
@@ -82,17 +84,17 @@ def test_attention_variants_layouts_and_unbuilt_names():
     want = {"kv_append_global_q8": (4, 0), "kv_append_sliding_q8": (4, 0),
             "attn_decode_global_q8_hd128": (7, 8), "attn_decode_sliding_q8_hd128": (7, 8),
             "attn_reduce_d128": (2, 4), "attn_prefill_global_flash_q8_hd128": (7, 4),
-            "attn_prefill_sliding_ring_q8_hd128": (11, 4)}
+            "attn_prefill_sliding_ring_q8_hd128": (11, 4),
+            "attn_decode_sliding": (5, 8), "attn_decode_global": (5, 8),
+            "attn_decode_global_q8k": (6, 8), "attn_reduce_d256": (2, 4),
+            "attn_reduce_d512": (2, 4), "kv_append_sliding": (3, 0), "kv_append_global": (3, 0)}
     for n, (nb, pb) in want.items():
         assert L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info)) == 0, n
         assert (info.bindings, info.push_bytes) == (nb, pb), n
-    for n, use in [("attn_decode_global_q8k", "attn_decode_global_q8_hd128"),
-                   ("attn_decode_sliding", "attn_decode_sliding_q8_hd128"),
-                   ("attn_reduce_d512", "attn_reduce_d128"), ("attn_reduce_d256", "attn_reduce_d128"),
-                   ("attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_q8_hd128"),
-                   ("attn_prefill_sliding_ring", "attn_prefill_sliding_ring_q8_hd128"),
-                   ("kv_append_global", "kv_append_global_q8"),
-                   ("kv_append_sliding", "kv_append_sliding_q8")]:
+    for n, use in [("attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_q8_hd128"),
+                   ("attn_prefill_global_flash_sp_q8", "attn_prefill_global_flash_q8_hd128"),
+                   ("attn_prefill_sliding", "attn_prefill_sliding_ring_q8_hd128"),
+                   ("attn_prefill_sliding_ring", "attn_prefill_sliding_ring_q8_hd128")]:
         rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
         msg = L.sgq_last_error().decode()
         assert rc == 4 and "not built" in msg and f"'{use}'" in msg, (n, msg)
