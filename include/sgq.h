@@ -124,9 +124,24 @@ typedef struct {
  *       [slot × ROW], 2 step; ROW 4096 into the 1024-slot ring (slot =
  *       (step[0] + t) mod 1024) / 2048 linear; groups cover n_tok·ROW
  *       elements at 256 a group  (kv_append.wgsl:15-35)
- * The reference's prefill over f16 pages (attn_prefill_sliding[_ring],
- * attn_prefill_global_flash_sp_iq/_sp_q8) returns SGQ_ERR_UNKNOWN_KERNEL
- * with the name of the Q8_0 form above to use. */
+ * Its prefill (crates/sg-gpu/build.rs:395-438, :2206-2292; record_prefill_
+ * layer, graph.rs:1176-1225); push {scale: f32}; q0 = step[3]; out f16
+ * [M × 32 × HD]; M = groups.y (grid [n_kv, M, 1]) or 16·groups.y (grid
+ * [32, M/16, 1]):
+ *   attn_prefill_sliding       hd 256, window 1024, [16, M]; 0 q f16, 1 K f16
+ *       [pos × 16 × 256], 2 V f16, 3 out, 4 step
+ *   attn_prefill_sliding_ring  hd 256, window 1024, [16, M]; 0 q, 1 K ring,
+ *       2 V ring (1024 slots, before this chunk's append), 3 chunk K, 4 chunk
+ *       V [M × 16 × 256], 5 out, 6 step
+ *   attn_prefill_global        hd 512 causal, [4, M]; bindings as _sliding
+ *   attn_prefill_global_flash / _flash_sp   hd 512 causal, [32, M/16]; the same
+ *   attn_prefill_global_flash_sp_q8  [32, M/16]; 0 q f16, 1 k_quants, 2 k_scales,
+ *       3 v_quants, 4 v_scales, 5 out, 6 step (K/V dequantized to f16)
+ *   attn_prefill_global_flash_sp_iq  [32, M/16]; 0 q_i8, 1 q_scales f16
+ *       [M × 32 × 16], 2 k_quants, 3 k_scales, 4 V f16, 5 out, 6 step (score
+ *       = sum over 32-dim blocks of q_scale·k_scale·integer dot)
+ * attn_prefill_global_flash_sp_ipv[_bcast] (int8 PV at head_dim 512) return
+ * SGQ_ERR_UNKNOWN_KERNEL naming attn_prefill_global_flash_sp_iq. */
 int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
                       sgq_kernel_info *info);
 /* Number of registered variant names / the i-th one (for enumeration). */

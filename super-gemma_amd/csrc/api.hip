@@ -93,6 +93,7 @@ enum class Kind {
     AttnDecodePages,  // attn_decode_{sliding,global,global_q8k}: f16 q / V pages
     AttnReducePages,  // attn_reduce_d{256,512}: f16 rows out
     AppendF16,     // kv_append_{sliding,global}: f16 rows
+    AttnPrefillPages,  // attn_prefill_{sliding[_ring],global[_flash[_sp[_q8,_iq]]]}
 };
 
 struct sgq_kernel {
@@ -128,6 +129,9 @@ const char *const kNames[] = {
     "kv_append_global_v_q8", "attn_prefill_global_flash_ipv_hd128",
     "attn_decode_sliding", "attn_decode_global", "attn_decode_global_q8k",
     "attn_reduce_d256", "attn_reduce_d512", "kv_append_sliding", "kv_append_global",
+    "attn_prefill_sliding", "attn_prefill_sliding_ring", "attn_prefill_global",
+    "attn_prefill_global_flash", "attn_prefill_global_flash_sp", "attn_prefill_global_flash_sp_q8",
+    "attn_prefill_global_flash_sp_iq",
 };
 
 // The benchmark geometry of the hd128 attention forms (32 query heads over
@@ -141,17 +145,35 @@ constexpr uint32_t kAttnNQ = 32, kAttnNKv = 16, kAttnWindow = 1024;
 // ring 1024) and 512 global (4 kv heads, 8 q heads each, K = V rows).
 constexpr uint32_t kRealNQ = 32, kSlNKv = 16, kGlNKv = 4;
 
-// Reference variants this build does not provide: the real checkpoint's
-// prefill attention over f16 pages (crates/sg-gpu/build.rs:395-430).  The
-// prefill here runs over Q8_0 pages; lookup names the form to use instead.
+// Reference variants this build does not provide: the int8-PV prefill at
+// head_dim 512 (crates/sg-gpu/build.rs:2293-2335); lookup names the form to
+// use instead.
 struct Unbuilt {
     const char *name, *use;
 };
 const Unbuilt kUnbuilt[] = {
-    {"attn_prefill_sliding", "attn_prefill_sliding_ring_q8_hd128"},
-    {"attn_prefill_sliding_ring", "attn_prefill_sliding_ring_q8_hd128"},
-    {"attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_q8_hd128"},
-    {"attn_prefill_global_flash_sp_q8", "attn_prefill_global_flash_q8_hd128"},
+    {"attn_prefill_global_flash_sp_ipv", "attn_prefill_global_flash_sp_iq"},
+    {"attn_prefill_global_flash_sp_ipv_bcast", "attn_prefill_global_flash_sp_iq"},
+};
+
+// The real checkpoint's prefill attention variants (crates/sg-gpu/build.rs:
+// 395-438, :2206-2292): head_dim, kv heads, page format (the kernel's
+// PfFmt: 1 Q8_0 K/V with f16 q, 2 f16 pages, 3 int8 q and Q8_0 K with f16
+// V), window, ring, bindings, and the grid form: per token [n_kv, M] or per
+// 16-query tile [32, M/16].
+struct PrefillVariant {
+    const char *name;
+    uint32_t head_dim, n_kv, fmt, window, ring, bindings;
+    bool per_token;
+};
+const PrefillVariant kPrefill[] = {
+    {"attn_prefill_sliding", 256, kSlNKv, 2, kAttnWindow, 0, 5, true},
+    {"attn_prefill_sliding_ring", 256, kSlNKv, 2, kAttnWindow, kAttnWindow, 7, true},
+    {"attn_prefill_global", 512, kGlNKv, 2, 0, 0, 5, true},
+    {"attn_prefill_global_flash", 512, kGlNKv, 2, 0, 0, 5, false},
+    {"attn_prefill_global_flash_sp", 512, kGlNKv, 2, 0, 0, 5, false},
+    {"attn_prefill_global_flash_sp_q8", 512, kGlNKv, 1, 0, 0, 7, false},
+    {"attn_prefill_global_flash_sp_iq", 512, kGlNKv, 3, 0, 0, 7, false},
 };
 
 // RoPE variants: (name, head_dim, rot_dims, n_heads).  The first four are
@@ -291,6 +313,19 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         k->param = sl ? kAttnWindow : 0;          // ring slots
         return true;
     }
+    for (uint32_t i = 0; i < sizeof kPrefill / sizeof kPrefill[0]; i++)
+        if (name == kPrefill[i].name) {
+            // per-token grids: [n_kv, M, 1], M = groups.y; flash grids:
+            // [32, M/16, 1], M = 16·groups.y; push {scale: f32}; q0 = step[3]
+            // f16 (5): 0 q, 1 K, 2 V, 3 out, 4 step
+            // ring (7): 0 q, 1 K ring, 2 V ring, 3 chunk K, 4 chunk V, 5 out, 6 step
+            // q8 (7): 0 q f16, 1 k_quants, 2 k_scales, 3 v_quants, 4 v_scales, 5 out, 6 step
+            // iq (7): 0 q_i8, 1 q_scales, 2 k_quants, 3 k_scales, 4 V f16, 5 out, 6 step
+            k->kind = Kind::AttnPrefillPages;
+            k->info = {{64, 1, 1}, kPrefill[i].bindings, 4, 0};
+            k->param = i;
+            return true;
+        }
     if (name == "attn_reduce_d128") {
         // bindings: 0 part, 1 out fp32 [n_q × 128]; push n_splits; groups [n_q]
         k->kind = Kind::AttnReduce;
@@ -496,10 +531,8 @@ int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
     for (const Unbuilt &u : kUnbuilt)
         if (std::strcmp(name, u.name) == 0)
             return fail(SGQ_ERR_UNKNOWN_KERNEL,
-                        "kernel variant '%s' (prefill over f16 pages) is not built: "
-                        "prefill runs over Q8_0 pages here (head_dim 128 by name: '%s'; "
-                        "head_dim 256/512 through the typed entry points and the model "
-                        "driver)",
+                        "kernel variant '%s' (int8 PV at head_dim 512) is not built: "
+                        "use '%s' (f16 PV)",
                         name, u.use);
     auto *k = new sgq_kernel;
     if (!resolve(name, k)) {
@@ -810,6 +843,52 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                                         static_cast<uint16_t *>(p1),
                                         static_cast<const uint32_t *>(p2), (uint32_t)n_tok, row,
                                         kernel->param);
+        }
+        case Kind::AttnPrefillPages: {
+            const PrefillVariant &pv = kPrefill[kernel->param];
+            void *pp[7];
+            uint64_t rr[7];
+            for (uint32_t i = 0; i < pv.bindings; i++)
+                if ((rc = B.get(i, &pp[i], &rr[i]))) return rc;
+            const uint32_t hd = pv.head_dim, nkv = pv.n_kv, nb = pv.bindings;
+            const uint32_t gx = pv.per_token ? nkv : kRealNQ;
+            if (groups[0] != gx || groups[1] == 0 || groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, %s, 1]",
+                            kernel->name.c_str(), gx, pv.per_token ? "M" : "M/16");
+            const uint64_t m = pv.per_token ? groups[1] : 16ull * groups[1];
+            if (m >= (1u << 24))
+                return fail(SGQ_ERR_VALIDATION, "%s: M %llu too large", kernel->name.c_str(),
+                            (unsigned long long)m);
+            const uint64_t row = (uint64_t)kRealNQ * hd;  // q / out elements per query
+            const bool iq = pv.fmt == 3, ring = pv.ring != 0;
+            if ((rr[nb - 2] && rr[nb - 2] < m * row * 2) || (rr[nb - 1] && rr[nb - 1] < 16) ||
+                (rr[0] && rr[0] < m * row * (iq ? 1 : 2)) ||
+                (iq && rr[1] && rr[1] < m * row / 32 * 2))
+                return fail(SGQ_ERR_VALIDATION, "%s: binding too small for M=%llu",
+                            kernel->name.c_str(), (unsigned long long)m);
+            const uint64_t kv_row = (uint64_t)nkv * hd * 2;
+            if (ring && ((rr[1] && rr[1] < pv.ring * kv_row) || (rr[2] && rr[2] < pv.ring * kv_row) ||
+                         (rr[3] && rr[3] < m * kv_row) || (rr[4] && rr[4] < m * kv_row)))
+                return fail(SGQ_ERR_VALIDATION, "%s: ring or chunk pages too small",
+                            kernel->name.c_str());
+            float scale;
+            std::memcpy(&scale, push, 4);
+            const void *q = pp[0], *k, *v, *ck = nullptr, *cv = nullptr;
+            const uint16_t *qs = nullptr, *ks = nullptr, *vs = nullptr;
+            if (iq) {
+                qs = static_cast<const uint16_t *>(pp[1]);
+                k = pp[2], ks = static_cast<const uint16_t *>(pp[3]), v = pp[4];
+            } else if (pv.fmt == 1) {
+                k = pp[1], ks = static_cast<const uint16_t *>(pp[2]);
+                v = pp[3], vs = static_cast<const uint16_t *>(pp[4]);
+            } else {
+                k = pp[1], v = pp[2];
+                if (ring) ck = pp[3], cv = pp[4];
+            }
+            return launch_attn_prefill_pages(st, (int)pv.fmt, q, qs, k, ks, v, vs, (int)pv.ring, ck, cv,
+                                             nullptr, nullptr, pp[nb - 2], (int)m,
+                                             static_cast<const uint32_t *>(pp[nb - 1]), (int)kRealNQ,
+                                             (int)nkv, (int)hd, (int)pv.window, scale);
         }
         case Kind::AttnPrefill: {
             const bool ring = kernel->param != 0;

@@ -692,28 +692,54 @@ __global__ __launch_bounds__(256 * HPW + 256) void attn_prefill_ws_kernel(
 //   QK(t) → partials out → barrier → K(t+1) and V(t+1) staged (V double-
 //   buffered), quants of t+2 issued → partials summed, softmax, PV(t) →
 //   barrier.
-// Every thread dequantizes one item per tile: two keys × head_dim/32 dims.
+// Every thread stages one item per tile: two keys × head_dim/32 dims.
 // The Vᵀ rows carry a pad of 16 dwords per 16 rows, so the item writes
 // (rows 8 or 16 apart within a wave) and the PV reads are free of bank
 // conflicts.
-template <int HD>
+//
+// Page formats (FMT), one kernel body:
+//   kPfQ8   fp32 q, Q8_0 K and V dequantized to f16 in LDS, fp32 out, q0
+//           from the host (the model driver's prefill)
+//   kPfQ8H  f16 q, Q8_0 K and V as above, f16 out, q0 = step[3]
+//           (attn_prefill_global_flash_sp_q8.wgsl)
+//   kPfF16  f16 q, K and V f16 pages, f16 out, q0 = step[3]
+//           (attn_prefill_sliding[_ring].wgsl, attn_prefill_global[_flash
+//           [_sp]].wgsl)
+//   kPfIQ   int8 q with f16 scales per 32 dims, K as Q8_0 quants with its
+//           scales, V f16, f16 out, q0 = step[3]: the score is the sum over
+//           32-dim blocks of q_scale·k_scale·(exact integer dot)
+//           (attn_prefill_global_flash_sp_iq.wgsl:94-125).  The integer
+//           dot runs on the f16 MFMA over the quants' exact f16 values
+//           (|products| < 2^14, block sums < 2^24: exact in fp32).
+// Except for kPfQ8, q enters the MFMA as its exact f16 values and the
+// scores are scaled afterwards.
+enum PfFmt { kPfQ8 = 0, kPfQ8H = 1, kPfF16 = 2, kPfIQ = 3 };
+
+template <int HD, int FMT>
 __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
-    const float *__restrict__ q, KvSource src, float *__restrict__ out, int n_tok, int q0,
-    int n_q, int n_kv, int window, float scale, int qtiles) {
+    const void *__restrict__ qv, const uint16_t *__restrict__ q_scales, KvSource src,
+    void *__restrict__ outv, int n_tok, int q0_host, const uint32_t *__restrict__ step, int n_q,
+    int n_kv, int window, float scale, int qtiles) {
+    constexpr bool QF32 = FMT == kPfQ8, QI8 = FMT == kPfIQ;
+    constexpr bool KQ8 = FMT == kPfQ8 || FMT == kPfQ8H;  // dequantized into LDS
+    constexpr bool KF16 = FMT == kPfF16, KRAW = FMT == kPfIQ;
+    constexpr bool VF16 = FMT == kPfF16 || FMT == kPfIQ;
+    constexpr bool O16 = FMT != kPfQ8;
     constexpr int D = HD / 128;        // waves per query tile
     constexpr int QTW = 8 / D;         // query tiles per workgroup
     constexpr int QW = 32 * QTW;       // queries per workgroup
     constexpr int KT = 32;             // keys per tile
-    constexpr int NB = HD / 32;        // Q8 blocks per row
+    constexpr int NB = HD / 32;        // 32-dim blocks per row
     constexpr int NP = KT / 2;         // key pairs per tile
-    constexpr int CW = HD / 32;        // dims per dequant item (8 or 16)
+    constexpr int CW = HD / 32;        // dims per staging item (8 or 16)
     constexpr int KRow = HD + 8;       // halves
     constexpr int VS = NP + 4;         // Vᵀ row stride, dwords
     constexpr int VBuf = HD * VS + (HD / 16) * NP;  // dwords per Vᵀ buffer
-    static_assert(NP * (HD / CW) == 512, "one dequant item per thread");
+    static_assert(NP * (HD / CW) == 512, "one staging item per thread");
     __shared__ __align__(16) _Float16 k_s[KT][KRow];
     __shared__ __align__(16) uint32_t vt_s[2][VBuf];
     __shared__ __align__(16) float4 ex_s[8][4][64];  // partial scores [wave][i/4][lane]
+    __shared__ __align__(16) float ksc_s[KRAW ? NB : 1][KT];  // kPfIQ: k scales [block][key]
     auto vt_at = [](int row, int col) { return row * VS + (row >> 4) * NP + col; };
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
@@ -722,6 +748,7 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
         by = (L & 7) * per + idx % per;
         bx = idx / per;
     }
+    const int q0 = QF32 ? q0_host : (int)step[3];
     const int tile = qtiles - 1 - bx;  // heaviest (latest) query tile first
     const int qh = by, kvh = qh / (n_q / n_kv);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -731,19 +758,45 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     const bool q_valid = my_q < n_tok;
     const int qp = q0 + my_q;
 
-    // this lane's query (column l32) on the wave's dims, pre-scaled (scores
-    // in log2 units), as the f16 B operand: dims 128·ds + 16c + 8hh .. +7
+    // this lane's query (column l32) on the wave's dims as the f16 B
+    // operand: dims 128·ds + 16c + 8hh .. +7.  kPfQ8: pre-scaled (scores in
+    // log2 units); otherwise exact, with the scale applied to the scores.
     const float qscale = scale * 1.44269504088896341f;
     h8 qb[8];
+    float qsb[KRAW ? 4 : 1];  // kPfIQ: q scale · qscale of the wave's 4 blocks
     {
-        const float *qr = q + ((size_t)(q_valid ? my_q : 0) * n_q + qh) * HD + 128 * ds + 8 * hh;
+        const size_t qoff = ((size_t)(q_valid ? my_q : 0) * n_q + qh) * HD + 128 * ds + 8 * hh;
+        if constexpr (QF32) {
+            const float *qr = static_cast<const float *>(qv) + qoff;
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const float4 a = *reinterpret_cast<const float4 *>(qr + 16 * c);
-            const float4 b = *reinterpret_cast<const float4 *>(qr + 16 * c + 4);
-            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            for (int c = 0; c < 8; c++) {
+                const float4 a = *reinterpret_cast<const float4 *>(qr + 16 * c);
+                const float4 b = *reinterpret_cast<const float4 *>(qr + 16 * c + 4);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] * qscale : 0.f);
+                for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(q_valid ? v[e] * qscale : 0.f);
+            }
+        } else if constexpr (QI8) {
+            const int8_t *qr = static_cast<const int8_t *>(qv) + qoff;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(qr + 16 * c);
+                const h2 a = i8_pair_f16(w.x, 0x04010400u), b = i8_pair_f16(w.x, 0x04030402u);
+                const h2 e2 = i8_pair_f16(w.y, 0x04010400u), f = i8_pair_f16(w.y, 0x04030402u);
+                const h8 t = {a[0], a[1], b[0], b[1], e2[0], e2[1], f[0], f[1]};
+                qb[c] = q_valid ? t : h8{};
+            }
+            const uint16_t *qs = q_scales + ((size_t)(q_valid ? my_q : 0) * n_q + qh) * NB + 4 * ds;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                qsb[b] = q_valid ? (float)__builtin_bit_cast(_Float16, qs[b]) * qscale : 0.f;
+        } else {
+            const uint16_t *qr = static_cast<const uint16_t *>(qv) + qoff;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const h8 t = __builtin_bit_cast(h8, *reinterpret_cast<const uint4 *>(qr + 16 * c));
+                qb[c] = q_valid ? t : h8{};
+            }
         }
     }
 
@@ -760,20 +813,24 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     const int k_hi = qpos_hi;
     const int wq_lo = q0 + tile * QW + qt * 32;
 
-    // dequant item of this thread: keys 2·pair, 2·pair + 1 of the tile,
+    // staging item of this thread: keys 2·pair, 2·pair + 1 of the tile,
     // dims CW·chunk .. +CW-1
     const int pair = tid % NP, chunk = tid / NP;
     const int dim0 = CW * chunk, blk = dim0 >> 5;
-    const int8_t *const kq_c = sgpr_ptr(src.kq), *const vq_c = sgpr_ptr(src.vq);
+    constexpr int EK = KF16 ? 2 : 1, EV = VF16 ? 2 : 1;  // bytes per K / V element
+    const char *const kq_c = sgpr_ptr(reinterpret_cast<const char *>(src.kq));
+    const char *const vq_c = sgpr_ptr(reinterpret_cast<const char *>(src.vq));
     const uint16_t *const ks_c = sgpr_ptr(src.ks), *const vs_c = sgpr_ptr(src.vs);
     const bool has_chunk = src.ckq != nullptr;
-    const int8_t *const kq_f = has_chunk ? sgpr_ptr(src.ckq) : kq_c;
-    const int8_t *const vq_f = has_chunk ? sgpr_ptr(src.cvq) : vq_c;
+    const char *const kq_f = has_chunk ? sgpr_ptr(reinterpret_cast<const char *>(src.ckq)) : kq_c;
+    const char *const vq_f = has_chunk ? sgpr_ptr(reinterpret_cast<const char *>(src.cvq)) : vq_c;
     const uint16_t *const ks_f = has_chunk ? sgpr_ptr(src.cks) : ks_c;
     const uint16_t *const vs_f = has_chunk ? sgpr_ptr(src.cvs) : vs_c;
     const int ring = src.ring;
-    typedef int raw_t __attribute__((ext_vector_type(CW / 4)));
-    raw_t rk[2], rv[2];
+    typedef int kraw_t __attribute__((ext_vector_type(CW * EK / 4)));
+    typedef int vraw_t __attribute__((ext_vector_type(CW * EV / 4)));
+    kraw_t rk[2];
+    vraw_t rv[2];
     uint16_t rsk[2], rsv[2];
     auto fetch = [&](int kl) {
 #pragma unroll
@@ -782,36 +839,65 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
             const bool fresh = has_chunk && key >= q0;
             const int slot = fresh ? key - q0 : ring ? key % ring : key;
             const size_t row = (size_t)slot * n_kv + kvh;
-            rk[e] = gload(reinterpret_cast<const raw_t *>((fresh ? kq_f : kq_c) + row * HD + dim0));
-            rv[e] = gload(reinterpret_cast<const raw_t *>((fresh ? vq_f : vq_c) + row * HD + dim0));
-            rsk[e] = gload((fresh ? ks_f : ks_c) + row * NB + blk);
-            rsv[e] = gload((fresh ? vs_f : vs_c) + row * NB + blk);
+            rk[e] = gload(reinterpret_cast<const kraw_t *>((fresh ? kq_f : kq_c) + (row * HD + dim0) * EK));
+            rv[e] = gload(reinterpret_cast<const vraw_t *>((fresh ? vq_f : vq_c) + (row * HD + dim0) * EV));
+            if constexpr (!KF16) rsk[e] = gload((fresh ? ks_f : ks_c) + row * NB + blk);
+            if constexpr (!VF16) rsv[e] = gload((fresh ? vs_f : vs_c) + row * NB + blk);
         }
     };
     auto stage = [&](int kl, uint32_t *vt) {
-        constexpr int NW = CW / 4;  // quant words per key
         uint32_t vpk[CW];
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             const int kk = 2 * pair + e;
             const bool live = kl + kk <= k_hi;
-            const _Float16 sk = live ? __builtin_bit_cast(_Float16, rsk[e]) : (_Float16)0.f;
-            const _Float16 sv = live ? __builtin_bit_cast(_Float16, rsv[e]) : (_Float16)0.f;
-            const h2 dk = {sk, sk}, dv = {sv, sv};
-            h8 kt[NW / 2];
+            h8 kt[CW / 8];
             _Float16 vv[CW];
+            if constexpr (KF16) {
 #pragma unroll
-            for (int w = 0; w < NW; w++) {
-                const h2 k01 = i8_pair_f16((uint32_t)rk[e][w], 0x04010400u) * dk;
-                const h2 k23 = i8_pair_f16((uint32_t)rk[e][w], 0x04030402u) * dk;
-                const h2 v01 = i8_pair_f16((uint32_t)rv[e][w], 0x04010400u) * dv;
-                const h2 v23 = i8_pair_f16((uint32_t)rv[e][w], 0x04030402u) * dv;
-                kt[w / 2][4 * (w & 1)] = k01[0], kt[w / 2][4 * (w & 1) + 1] = k01[1];
-                kt[w / 2][4 * (w & 1) + 2] = k23[0], kt[w / 2][4 * (w & 1) + 3] = k23[1];
-                vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+                for (int h = 0; h < CW / 8; h++) {
+                    const int4 w = {rk[e][4 * h], rk[e][4 * h + 1], rk[e][4 * h + 2], rk[e][4 * h + 3]};
+                    kt[h] = live ? __builtin_bit_cast(h8, w) : h8{};
+                }
+            } else {
+                const _Float16 sk = KQ8 && live ? __builtin_bit_cast(_Float16, rsk[e]) : (_Float16)1.f;
+                const h2 dk = {sk, sk};
+#pragma unroll
+                for (int w = 0; w < CW / 4; w++) {
+                    h2 k01 = i8_pair_f16((uint32_t)rk[e][w], 0x04010400u);
+                    h2 k23 = i8_pair_f16((uint32_t)rk[e][w], 0x04030402u);
+                    if constexpr (KQ8) k01 *= dk, k23 *= dk;
+                    kt[w / 2][4 * (w & 1)] = k01[0], kt[w / 2][4 * (w & 1) + 1] = k01[1];
+                    kt[w / 2][4 * (w & 1) + 2] = k23[0], kt[w / 2][4 * (w & 1) + 3] = k23[1];
+                }
+                if (!live)
+#pragma unroll
+                    for (int h = 0; h < CW / 8; h++) kt[h] = h8{};
+                if constexpr (KRAW)
+                    if (dim0 % 32 == 0)
+                        ksc_s[blk][kk] = live ? (float)__builtin_bit_cast(_Float16, rsk[e]) : 0.f;
+            }
+            if constexpr (VF16) {
+#pragma unroll
+                for (int w = 0; w < CW / 2; w++) {
+                    const int word = rv[e][w];  // a plain value: bit_cast of a vector
+                                                // element reads element 0
+                    const h2 p = __builtin_bit_cast(h2, word);
+                    vv[2 * w] = live ? p[0] : (_Float16)0.f;
+                    vv[2 * w + 1] = live ? p[1] : (_Float16)0.f;
+                }
+            } else {
+                const _Float16 sv = live ? __builtin_bit_cast(_Float16, rsv[e]) : (_Float16)0.f;
+                const h2 dv = {sv, sv};
+#pragma unroll
+                for (int w = 0; w < CW / 4; w++) {
+                    const h2 v01 = i8_pair_f16((uint32_t)rv[e][w], 0x04010400u) * dv;
+                    const h2 v23 = i8_pair_f16((uint32_t)rv[e][w], 0x04030402u) * dv;
+                    vv[4 * w] = v01[0], vv[4 * w + 1] = v01[1], vv[4 * w + 2] = v23[0], vv[4 * w + 3] = v23[1];
+                }
             }
 #pragma unroll
-            for (int h = 0; h < NW / 2; h++) *reinterpret_cast<h8 *>(&k_s[kk][dim0 + 8 * h]) = kt[h];
+            for (int h = 0; h < CW / 8; h++) *reinterpret_cast<h8 *>(&k_s[kk][dim0 + 8 * h]) = kt[h];
 #pragma unroll
             for (int j = 0; j < CW; j++) {
                 const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, vv[j]);
@@ -828,16 +914,43 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     __syncthreads();
     int buf = 0;
     for (int kl = k_lo; kl <= k_hi; kl += KT) {
-        // partial Sᵀ of the tile over this wave's 128 dims, two MFMA chains
+        // partial Sᵀ of the tile over this wave's 128 dims
         f32x16 s0, s1;
 #pragma unroll
         for (int i = 0; i < 16; i++) s0[i] = s1[i] = 0.f;
+        if constexpr (KRAW) {
+            // per 32-dim block: the exact integer dot, then q_scale·k_scale
 #pragma unroll
-        for (int c = 0; c < 8; c += 2) {
-            const h8 a0 = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 8 * hh]);
-            const h8 a1 = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 16 + 8 * hh]);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qb[c], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qb[c + 1], s1, 0, 0, 0);
+            for (int b = 0; b < 4; b++) {
+                f32x16 t;
+#pragma unroll
+                for (int i = 0; i < 16; i++) t[i] = 0.f;
+#pragma unroll
+                for (int c = 2 * b; c < 2 * b + 2; c++) {
+                    const h8 a = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 8 * hh]);
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], t, 0, 0, 0);
+                }
+                const float *kb = ksc_s[4 * ds + b];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 k4 = *reinterpret_cast<const float4 *>(kb + 8 * j + 4 * hh);
+                    const float kv4[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int i = 4 * j + r;
+                        if (b & 1) s1[i] = __builtin_fmaf(qsb[b] * kv4[r], t[i], s1[i]);
+                        else s0[i] = __builtin_fmaf(qsb[b] * kv4[r], t[i], s0[i]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; c += 2) {
+                const h8 a0 = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 8 * hh]);
+                const h8 a1 = *reinterpret_cast<const h8 *>(&k_s[l32][128 * ds + 16 * c + 16 + 8 * hh]);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qb[c], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qb[c + 1], s1, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -860,6 +973,9 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
             }
             s[4 * j] = t.x, s[4 * j + 1] = t.y, s[4 * j + 2] = t.z, s[4 * j + 3] = t.w;
         }
+        if constexpr (!QF32 && !KRAW)
+#pragma unroll
+            for (int i = 0; i < 16; i++) s[i] *= qscale;
         const uint32_t *vt = vt_s[buf];
         {
             const int kb = kl;
@@ -914,11 +1030,17 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
 
     if (!q_valid) return;
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-    float *orow = out + ((size_t)my_q * n_q + qh) * HD + 128 * ds;
+    const size_t obase = ((size_t)my_q * n_q + qh) * HD + 128 * ds;
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) orow[32 * d + 8 * (i / 4) + 4 * hh + (i % 4)] = o[d][i] * inv;
+        for (int i = 0; i < 16; i++) {
+            const size_t at = obase + 32 * d + 8 * (i / 4) + 4 * hh + (i % 4);
+            if constexpr (O16)
+                static_cast<uint16_t *>(outv)[at] = __builtin_bit_cast(uint16_t, (_Float16)(o[d][i] * inv));
+            else
+                static_cast<float *>(outv)[at] = o[d][i] * inv;
+        }
 }
 
 }  // namespace
@@ -971,12 +1093,16 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
                   "attn_prefill_q8: misaligned cache");
         const int qw = head_dim == 256 ? 128 : 64;  // queries per workgroup
         const int qt = (n_tok + qw - 1) / qw;
+        const uint32_t *no_step = nullptr;
+        const uint16_t *no_qs = nullptr;
         if (head_dim == 256)
-            hipLaunchKernelGGL(attn_prefill_wide_kernel<256>, dim3(qt, n_q), dim3(512), 0, st, q, src,
-                               out, n_tok, q0, n_q, n_kv, window, scale, qt);
+            hipLaunchKernelGGL((attn_prefill_wide_kernel<256, kPfQ8>), dim3(qt, n_q), dim3(512), 0,
+                               st, q, no_qs, src, out, n_tok, q0, no_step, n_q, n_kv, window, scale,
+                               qt);
         else
-            hipLaunchKernelGGL(attn_prefill_wide_kernel<512>, dim3(qt, n_q), dim3(512), 0, st, q, src,
-                               out, n_tok, q0, n_q, n_kv, window, scale, qt);
+            hipLaunchKernelGGL((attn_prefill_wide_kernel<512, kPfQ8>), dim3(qt, n_q), dim3(512), 0,
+                               st, q, no_qs, src, out, n_tok, q0, no_step, n_q, n_kv, window, scale,
+                               qt);
         SGQ_HIP(hipGetLastError());
         return SGQ_OK;
     }
@@ -988,6 +1114,48 @@ int launch_attn_prefill_q8(hipStream_t st, const float *q, const int8_t *kq, con
     else
         hipLaunchKernelGGL(attn_prefill_ws_kernel<1>, dim3(qtiles, n_q), dim3(512), 0, st, q, src,
                            out, n_tok, q0, n_q, n_kv, window, scale, qtiles, step);
+    SGQ_HIP(hipGetLastError());
+    return SGQ_OK;
+}
+
+int launch_attn_prefill_pages(hipStream_t st, int fmt, const void *q, const uint16_t *q_scales,
+                              const void *k, const uint16_t *k_scales, const void *v,
+                              const uint16_t *v_scales, int ring, const void *ck, const void *cv,
+                              const uint16_t *cks, const uint16_t *cvs, void *out, int n_tok,
+                              const uint32_t *step, int n_q, int n_kv, int head_dim, int window,
+                              float scale) {
+    SGQ_CHECK(fmt == kPfQ8H || fmt == kPfF16 || fmt == kPfIQ, "attn_prefill_pages: format %d", fmt);
+    SGQ_CHECK(head_dim == 256 || head_dim == 512, "attn_prefill_pages: head_dim %d (256, 512)",
+              head_dim);
+    SGQ_CHECK(q && k && v && out && step, "attn_prefill_pages: NULL operand");
+    SGQ_CHECK(n_tok > 0 && n_kv > 0 && n_q > 0 && n_q % n_kv == 0,
+              "attn_prefill_pages: n_tok %d, n_q %d, n_kv %d", n_tok, n_q, n_kv);
+    SGQ_CHECK(fmt != kPfIQ || (q_scales && k_scales), "attn_prefill_pages: int8 q needs the scales");
+    SGQ_CHECK(fmt != kPfQ8H || (k_scales && v_scales), "attn_prefill_pages: Q8_0 pages need scales");
+    SGQ_CHECK(window >= 0 && ring >= 0 && (ring == 0 || (ck && cv && window <= ring)),
+              "attn_prefill_pages: a ring needs the chunk's pages and a window within it");
+    SGQ_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 &&
+                  ((uintptr_t)ck & 15) == 0 && ((uintptr_t)cv & 15) == 0,
+              "attn_prefill_pages: misaligned operand");
+    const KvSource src{static_cast<const int8_t *>(k), static_cast<const int8_t *>(v), k_scales,
+                       v_scales, ring, static_cast<const int8_t *>(ck),
+                       static_cast<const int8_t *>(cv), cks, cvs};
+    const int qw = head_dim == 256 ? 128 : 64;  // queries per workgroup
+    const int qt = (n_tok + qw - 1) / qw;
+    const dim3 grid(qt, n_q);
+#define SGQ_PF_PAGES(HD, F)                                                                     \
+    hipLaunchKernelGGL((attn_prefill_wide_kernel<HD, F>), grid, dim3(512), 0, st, q, q_scales, src, \
+                       out, n_tok, 0, step, n_q, n_kv, window, scale, qt)
+    if (head_dim == 256) {
+        if (fmt == kPfQ8H) SGQ_PF_PAGES(256, kPfQ8H);
+        else if (fmt == kPfF16) SGQ_PF_PAGES(256, kPfF16);
+        else SGQ_PF_PAGES(256, kPfIQ);
+    } else {
+        if (fmt == kPfQ8H) SGQ_PF_PAGES(512, kPfQ8H);
+        else if (fmt == kPfF16) SGQ_PF_PAGES(512, kPfF16);
+        else SGQ_PF_PAGES(512, kPfIQ);
+    }
+#undef SGQ_PF_PAGES
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }

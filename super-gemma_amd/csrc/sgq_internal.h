@@ -154,6 +154,18 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
                              const uint16_t *ks, const int8_t *vq, const uint16_t *vs,
                              const uint32_t *step, int step_word, int n_q, int n_kv, int n_splits,
                              float scale, float *part);
+// Prefill attention at head_dim 256/512 over the reference's page formats
+// (prefill_attn.hip, PfFmt): fmt 1 f16 q with Q8_0 K/V (k_scales/v_scales),
+// 2 f16 q/K/V, 3 int8 q (q_scales) with Q8_0 K and f16 V; f16 out
+// [n_tok × n_q × head_dim]; q0 = step[3]; window 0 = causal; ring > 0:
+// keys before q0 from the ring (slot = pos mod ring), from q0 on from the
+// chunk's pages ck/cv (rows = pos - q0; Q8_0 formats: cks/cvs scales).
+int launch_attn_prefill_pages(hipStream_t st, int fmt, const void *q, const uint16_t *q_scales,
+                              const void *k, const uint16_t *k_scales, const void *v,
+                              const uint16_t *v_scales, int ring, const void *ck, const void *cv,
+                              const uint16_t *cks, const uint16_t *cvs, void *out, int n_tok,
+                              const uint32_t *step, int n_q, int n_kv, int head_dim, int window,
+                              float scale);
 // Decode attention over f16 pages (or Q8_0 K with f16 V) for the released
 // checkpoint's names (attn_pages.hip): q f16 [n_q × head_dim], pages
 // [slot × n_kv × head_dim], k_scales non-null selects Q8_0 K (f16 scale per

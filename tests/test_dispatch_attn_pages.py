@@ -219,3 +219,146 @@ def test_pages_names_validate_groups_and_ranges(ctx):
         ctx.dispatch(app, _bind(sgq, empty(2 * 4096, torch.int16), empty(RING * 4096, torch.int16),
                                 step), b"", [16, 1, 1])
     ctx.synchronize()
+
+
+# --- prefill over the reference's page formats ------------------------------
+# attn_prefill_sliding[_ring] (hd256, 16 kv heads, window 1024, ring 1024),
+# attn_prefill_global[_flash[_sp]] (hd512, 4 kv heads, causal, f16 pages),
+# _sp_q8 (f16 q, Q8_0 K and V dequantized to f16, as that shader does) and
+# _sp_iq (int8 q and Q8_0 K: score = sum over blocks of q_scale·k_scale·
+# integer dot; f16 V).  q0 = step[3].  Bar: the typed prefill tests' (|err| <=
+# 2e-3·|want| + 1e-3·max|want|, normwise 1e-3) plus the f16 rounding of the
+# output (2^-11 of max|want|): normwise 1.5e-3.  Cache slots the kernel must
+# not read hold f16 NaN.
+F16_NAN = np.uint16(0x7E00)
+PREFILL = {  # name: (head_dim, n_kv, window, per-token grid)
+    "attn_prefill_sliding": (256, 16, 1024, True),
+    "attn_prefill_sliding_ring": (256, 16, 1024, True),
+    "attn_prefill_global": (512, 4, 0, True),
+    "attn_prefill_global_flash": (512, 4, 0, False),
+    "attn_prefill_global_flash_sp": (512, 4, 0, False),
+    "attn_prefill_global_flash_sp_q8": (512, 4, 0, False),
+    "attn_prefill_global_flash_sp_iq": (512, 4, 0, False),
+}
+
+
+def _prefill_check(got, want, what):
+    top = float(np.abs(want).max())
+    assert_close(got, want, 2e-3, 1.5e-3 * top, what)
+    err = float(np.abs(got.astype(np.float64) - want).max()) / top
+    assert err <= 1.5e-3, (what, err)
+
+
+def _prefill_by_name(ctx, name, binds, m, scale):
+    import sgq
+
+    hd, nkv, _, per_token = PREFILL[name]
+    k = ctx.load_kernel(name)
+    groups = [nkv, m, 1] if per_token else [NQ, m // 16, 1]
+    ctx.dispatch_blocking(k, [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(binds)],
+                          struct.pack("<f", scale), groups)
+
+
+@pytest.mark.parametrize("name,q0,m", [
+    ("attn_prefill_sliding", 1200, 100), ("attn_prefill_sliding", 0, 37),
+    ("attn_prefill_sliding_ring", 1500, 160), ("attn_prefill_sliding_ring", 0, 64),
+    ("attn_prefill_sliding_ring", 700, 1), ("attn_prefill_sliding_ring", 1000, 90),
+    ("attn_prefill_global", 300, 50), ("attn_prefill_global_flash", 0, 128),
+    ("attn_prefill_global_flash_sp", 77, 48), ("attn_prefill_global_flash_sp_q8", 200, 64),
+    ("attn_prefill_global_flash_sp_iq", 0, 256), ("attn_prefill_global_flash_sp_iq", 333, 32),
+])
+def test_prefill_pages_by_name_matches_oracle(ctx, oracle, name, q0, m):
+    hd, nkv, window, _ = PREFILL[name]
+    print(f"dispatch {name} q0={q0} M={m}", flush=True)
+    rng = oracle.Rng(0x9F + q0 + 7 * m + hd)
+    n = q0 + m
+    qf = rng.f32_vec(m * NQ * hd)
+    kf = rng.f32_vec(n * nkv * hd)
+    vf = rng.f32_vec(n * nkv * hd)
+    scale = 1.0 if name.endswith("_iq") else 1.0 / np.sqrt(hd)
+    row = nkv * hd
+    step = _step(ctx, q0, 0, 0, q0)
+    out = torch.full((m * NQ * hd,), 0x7E00, dtype=torch.int16, device="cuda")
+
+    def nan_padded(bits, rows):  # cache rows past position n - 1 hold NaN
+        full = np.full(rows * row, F16_NAN, np.uint16)
+        full[:bits.size] = bits
+        return full
+
+    if name.endswith("_iq") or name.endswith("_q8"):
+        ks, kq = oracle.quant_q8_0(kf)
+        if name.endswith("_iq"):
+            qs, qq = oracle.quant_q8_0(qf)
+            qd = oracle.dequant_q8_0(qs, qq)
+            kd = oracle.dequant_q8_0(ks, kq)
+            vb = oracle.f32_to_f16_bits(vf)
+            vd = oracle.f16_bits_to_f32(vb)
+            binds = [dev(qq), dev(qs), dev(kq), dev(ks), dev(nan_padded(vb, n + 40)), out, step]
+        else:
+            q16 = oracle.f32_to_f16_bits(qf)
+            qd = oracle.f16_bits_to_f32(q16)
+            vs, vq = oracle.quant_q8_0(vf)
+            kd, vd = oracle.dequant_q8_0_f16(ks, kq), oracle.dequant_q8_0_f16(vs, vq)
+            binds = [dev(q16), dev(kq), dev(ks), dev(vq), dev(vs), out, step]
+    else:
+        q16, kb, vb = (oracle.f32_to_f16_bits(x) for x in (qf, kf, vf))
+        qd, kd, vd = (oracle.f16_bits_to_f32(x) for x in (q16, kb, vb))
+        if name.endswith("_ring"):
+            kr = np.full(RING * row, F16_NAN, np.uint16)
+            vr = kr.copy()
+            for p in range(max(0, q0 - RING), q0):  # the ring before this chunk's append
+                sl = (p % RING) * row
+                kr[sl:sl + row], vr[sl:sl + row] = kb[p * row:(p + 1) * row], vb[p * row:(p + 1) * row]
+            binds = [dev(q16), dev(kr), dev(vr), dev(kb[q0 * row:]), dev(vb[q0 * row:]), out, step]
+        else:
+            binds = [dev(q16), dev(nan_padded(kb, n + 40)), dev(nan_padded(vb, n + 40)), out, step]
+    _prefill_by_name(ctx, name, binds, m, scale)
+    got = oracle.f16_bits_to_f32(host(out, np.uint16)).reshape(m, NQ, hd)
+    want = oracle.attention(qd, kd, vd, m, q0, NQ, nkv, hd, window, scale)
+    _prefill_check(got, want, f"{name} q0={q0} M={m}")
+
+
+def test_prefill_sliding_ring_equals_linear_view(ctx, oracle):
+    """The two-range form (history from the pre-append ring, the chunk from
+    its own pages) and the linear form over the same positions attend the
+    same keys in the same order: bit-identical outputs."""
+    hd, nkv, q0, m = 256, 16, 2100, 200
+    row = nkv * hd
+    rng = oracle.Rng(0x2A9)
+    q16 = oracle.f32_to_f16_bits(rng.f32_vec(m * NQ * hd))
+    kb = oracle.f32_to_f16_bits(rng.f32_vec((q0 + m) * row))
+    vb = oracle.f32_to_f16_bits(rng.f32_vec((q0 + m) * row))
+    kr = np.empty(RING * row, np.uint16)
+    vr = np.empty(RING * row, np.uint16)
+    for p in range(q0 - RING, q0):
+        sl = (p % RING) * row
+        kr[sl:sl + row], vr[sl:sl + row] = kb[p * row:(p + 1) * row], vb[p * row:(p + 1) * row]
+    step = _step(ctx, q0, 0, 0, q0)
+    a = empty(m * NQ * hd, torch.int16)
+    b = empty(m * NQ * hd, torch.int16)
+    _prefill_by_name(ctx, "attn_prefill_sliding_ring",
+                     [dev(q16), dev(kr), dev(vr), dev(kb[q0 * row:]), dev(vb[q0 * row:]), a, step],
+                     m, 0.0625)
+    _prefill_by_name(ctx, "attn_prefill_sliding", [dev(q16), dev(kb), dev(vb), b, step], m, 0.0625)
+    assert np.array_equal(host(a), host(b))
+
+
+def test_prefill_pages_names_validate(ctx):
+    import sgq
+
+    k = ctx.load_kernel("attn_prefill_global_flash_sp_iq")
+    q = empty(64 * NQ * 512 // 2, torch.int16)
+    bad = [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(
+        [q, q, q, q, q, empty(64 * NQ * 512, torch.int16), _step(ctx, 0, 0, 0, 0)])]
+    with pytest.raises(sgq.ValidationError):  # groups.x is the query head count
+        ctx.dispatch(k, bad, struct.pack("<f", 1.0), [4, 4, 1])
+    with pytest.raises(sgq.ValidationError):  # out holds 64 rows, groups ask for 80
+        ctx.dispatch(k, bad, struct.pack("<f", 1.0), [NQ, 5, 1])
+    ring = ctx.load_kernel("attn_prefill_sliding_ring")
+    small = empty(100 * 16 * 256, torch.int16)
+    with pytest.raises(sgq.ValidationError):  # a ring of 100 slots
+        ctx.dispatch(ring, [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(
+            [empty(8 * NQ * 256, torch.int16), small, small, small, small,
+             empty(8 * NQ * 256, torch.int16), _step(ctx, 0, 0, 0, 0)])],
+                     struct.pack("<f", 1.0), [16, 8, 1])
+    ctx.synchronize()
