@@ -232,6 +232,87 @@ class AttnDecode:
         }
 
 
+class AttnPages:
+    """The released checkpoint's decode attention by name over f16 pages, as
+    the reference's record_layer dispatches it (crates/sg-model/src/graph.rs:
+    572-650): attn_decode_global_q8k (Q8_0 K, f16 V, head_dim 512, 4 kv
+    heads, 32 splits) or attn_decode_sliding (f16 K/V, head_dim 256, 16 kv
+    heads, the full 1024-slot ring, 16 splits), then its attn_reduce.  One
+    graph replays the pair over rotating caches (>= 512 MB) so the pages
+    stream from HBM; a step is one replay, reported per pair."""
+    kernel = "attn_decode_pages_kernel"
+
+    def __init__(self, ctx, torch, kind="global_q8k", ctx_len=8192):
+        import struct
+        import sgq
+
+        self.ctx, self.torch, self.kind, self.ctx_len = ctx, torch, kind, ctx_len
+        if kind == "sliding":
+            hd, n_kv, self.splits, word = 256, 16, 16, 1
+        else:
+            hd, n_kv, self.splits, word = 512, 4, 32, 2
+        n_q, row = 32, n_kv * hd
+        k_bytes = ctx_len * row * (1 + 2 / 32) if kind == "global_q8k" else ctx_len * row * 2
+        self.bytes = int(k_bytes + ctx_len * row * 2)
+        self.copies = max(1, (512 << 20) // self.bytes)
+        tmp = torch.empty(ctx_len * row, dtype=torch.float32, device="cuda")
+        q = torch.empty(n_q * hd, dtype=torch.float32, device="cuda")
+        ctx.fill_normal(q, seed=60)
+        q16 = q.half().view(torch.int16)
+        step = torch.zeros(8, dtype=torch.int32, device="cuda")
+        kvs = [ctx_len - 1, ctx_len if word == 1 else 0, ctx_len if word == 2 else 0, 0]
+        ctx.step_write(step, sgq.StepState(*kvs))
+        part = torch.empty(n_q * self.splits * (hd + 2), dtype=torch.float32, device="cuda")
+        out = torch.empty(n_q * hd, dtype=torch.int16, device="cuda")
+        attn = ctx.load_kernel(f"attn_decode_{kind}")
+        red = ctx.load_kernel(f"attn_reduce_d{hd}")
+        self.pages = []
+        for c in range(self.copies):
+            ctx.fill_normal(tmp, seed=61 + 2 * c)
+            if kind == "global_q8k":
+                kq = torch.empty(tmp.numel(), dtype=torch.int8, device="cuda")
+                ks = torch.empty(tmp.numel() // 32, dtype=torch.int16, device="cuda")
+                ctx.quant_q8_0(tmp, ks, kq)
+                kb = (kq, ks)
+            else:
+                kb = (tmp.half().view(torch.int16),)
+            ctx.fill_normal(tmp, seed=62 + 2 * c)
+            self.pages.append((kb, tmp.half().view(torch.int16)))
+        del tmp
+        torch.cuda.synchronize()
+        self.stream = torch.cuda.Stream()
+        ctx.set_stream(self.stream)
+
+        def bind(*ts):
+            return [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(ts)]
+
+        with sgq.GraphRecorder(ctx) as rec:
+            for kb, v in self.pages:
+                ctx.dispatch(attn, bind(q16, *kb, v, part, step),
+                             struct.pack("<If", self.splits, 1.0), [n_kv, self.splits, 1])
+                ctx.dispatch(red, bind(part, out), struct.pack("<I", self.splits), [n_q, 1, 1])
+        self.graph = rec.graph
+        self.hd, self.n_kv = hd, n_kv
+
+    def step(self, i):
+        self.graph.submit()
+
+    def result(self, ms_per_step):
+        ms = ms_per_step / self.copies
+        gbs = self.bytes / (ms * 1e-3) / 1e9
+        return {
+            "value": gbs, "unit": "GB/s",
+            "dtype": "f16 q / V" + (", Q8_0 K" if self.kind == "global_q8k" else ", f16 K")
+                     + "; fp32 MFMA accumulation, f16 out",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "config": {"workload": f"attn_decode_{self.kind} + attn_reduce_d{self.hd} by name, "
+                                   f"{self.ctx_len} slots, 32 q / {self.n_kv} kv heads, "
+                                   f"{self.splits} splits, {self.copies} rotating caches",
+                       "bytes_per_launch": self.bytes, "us_per_pair": ms * 1e3},
+        }
+
+
 class HeadQ6K:
     """The Q6_K tied LM head of the real checkpoint (gemv_q6_k_logits.wgsl):
     262144 vocabulary rows x K=5376, rows padded to 4416 bytes, 30*tanh
@@ -677,7 +758,8 @@ def main():
                     choices=["decode", "decode_real", "prefill_real", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_ipv",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
-                             "attn_decode_128k", "head_q6k"])
+                             "attn_decode_128k", "head_q6k", "attn_pages_sliding",
+                             "attn_pages_q8k_4k", "attn_pages_q8k_8k", "attn_pages_q8k_32k"])
     ap.add_argument("--gemv-rows", type=int, default=21504,
                     help="gemv workload: rows N (config 1 is 21504; other values sweep the "
                          "per-launch fixed cost against the streaming rate)")
@@ -718,6 +800,11 @@ def main():
         wl = AttnPrefill(ctx, torch, ipv=True)
     elif args.workload == "attn_prefill_sliding":
         wl = AttnPrefill(ctx, torch, window=1024)
+    elif args.workload == "attn_pages_sliding":
+        wl = AttnPages(ctx, torch, "sliding", 1024)
+    elif args.workload.startswith("attn_pages_q8k_"):
+        wl = AttnPages(ctx, torch, "global_q8k",
+                       {"4k": 4096, "8k": 8192, "32k": 32768}[args.workload[15:]])
     elif args.workload.startswith("attn_decode_"):
         wl = AttnDecode(ctx, torch, {"4k": 4096, "32k": 32768, "128k": 131072}[args.workload[12:]])
     else:

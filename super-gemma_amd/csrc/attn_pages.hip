@@ -18,12 +18,22 @@
 // empty split: acc 0, m -3e38, l 0).  The model driver keeps Q8_0 K and V
 // (csrc/attn_generic.hip); these serve callers that hold f16 pages.
 //
-// Design: one 256-thread workgroup per (kv head, split) walks its chunk in
-// tiles of 64 slots: scores with lane = slot and wave = a quarter of the
-// dims (q in LDS), the tile's max and exponentials per head (one wave per
-// head), then PV with each thread owning head_dim/256 dims of every query
-// head, all 64 V values of a tile issued before their FMAs, and the running
-// (m, l) rescale applied per tile.
+// Design (MFMA; the reference's grid gives 128-256 workgroups, so each
+// must use its CU well): one workgroup of head_dim/32 waves per (kv head,
+// split) walks its chunk in tiles of 64 slots, with v_mfma_f32_32x32x16_f16
+// for both products (query heads padded to the 32 MFMA columns):
+//  * Sᵀ = K·Qᵀ: wave w takes slot block w & 1 (32 slots) and 64 dims; K
+//    goes from HBM straight into the A operand (16 bytes a lane), q sits in
+//    registers as the B operand.  f16 products are exact and Q8_0 quants
+//    enter as their exact f16 values, each 32-dim block accumulated on its
+//    own; the partials meet in LDS and are summed in dim order (times the
+//    block's k scale for Q8_0) by one wave per query head, which runs the
+//    tile's online-softmax step;
+//  * Oᵀ = Vᵀ·Pᵀ: the V tile is staged in LDS (rows padded so the transposed
+//    reads of rows 8 apart fall on other banks), wave w owns dims
+//    [32w, 32w + 32) of every query head, and P enters as two f16 parts
+//    (p = hi + lo, 22 bits) so the PV keeps fp32 accuracy;
+//  * the next tile's K and V are loaded while this one is computed.
 #include "sgq_internal.h"
 
 namespace sgq {
@@ -36,90 +46,159 @@ __device__ __forceinline__ float h2f(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
+typedef _Float16 ph8 __attribute__((ext_vector_type(8)));
+typedef float pf16x __attribute__((ext_vector_type(16)));
+
+// 8 int8 quants (two words) -> their exact f16 values.
+__device__ __forceinline__ ph8 i8x8_f16(uint32_t w0, uint32_t w1) {
+    ph8 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        r[e] = (_Float16)(float)(int8_t)(w0 >> (8 * e));
+        r[4 + e] = (_Float16)(float)(int8_t)(w1 >> (8 * e));
+    }
+    return r;
+}
+
 template <int HD, int QPK, bool KQ8>
-__global__ __launch_bounds__(256) void attn_decode_pages_kernel(
+__global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
     const uint16_t *__restrict__ q16, const void *__restrict__ kp,
     const uint16_t *__restrict__ k_scales, const uint16_t *__restrict__ v16,
     float *__restrict__ part, const uint32_t *__restrict__ step, int step_word, int n_kv,
     int n_splits, float scale) {
-    constexpr int DW = HD / 4;    // score dims per wave
-    constexpr int PB = DW / 32;   // 32-dim blocks per wave
-    constexpr int ND = HD / 256;  // PV dims per thread
-    __shared__ float q_s[QPK][HD];
-    __shared__ float sp_s[4][QPK][kPTile];
-    __shared__ float p_s[QPK][kPTile];
+    constexpr int NW = HD / 32;            // waves = PV dim blocks
+    constexpr int NT = NW * 64;            // threads
+    constexpr int NDG = NW / 2;            // score dim groups of 64 per slot block
+    constexpr int NG = KQ8 ? 2 * NDG : NDG;  // score partials per slot
+    constexpr int VP = HD + 8;             // V tile row pitch, halves
+    constexpr int NU = kPTile * HD / 8 / NT;  // uint4 of V per thread per tile (4)
+    static_assert(QPK <= 32 && NU == 4, "layout");
+    __shared__ __align__(16) _Float16 vs_s[kPTile][VP];
+    __shared__ float sp_s[NG][QPK][kPTile];
+    __shared__ __align__(16) _Float16 ph_s[QPK][kPTile], pl_s[QPK][kPTile];
     __shared__ float m_s[QPK], l_s[QPK], corr_s[QPK];
+    __shared__ __align__(16) uint32_t ks_s[KQ8 ? kPTile : 1][8];  // Q8_0 block scales per slot
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
     const int kvh = blockIdx.x, split = blockIdx.y;
     const uint32_t kv_len = step[step_word];
     const uint32_t chunk = (kv_len + (uint32_t)n_splits - 1) / (uint32_t)n_splits;
     const uint32_t t_begin = min((uint32_t)split * chunk, kv_len);
     const uint32_t t_end = min(t_begin + chunk, kv_len);
+    const size_t kv_row = (size_t)n_kv * HD;  // elements per slot
+    const int sb = wave & 1, dg = wave >> 1;  // score role
+    const bool hcol = l32 < QPK;              // this lane's MFMA column is a real head
 
-    for (int i = tid; i < QPK * HD; i += 256)
-        q_s[i / HD][i % HD] = h2f(q16[((size_t)kvh * QPK + i / HD) * HD + i % HD]);
+    // q of head l32 on the wave's 64 score dims, as four B operands
+    ph8 qb[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint4 w = hcol ? *reinterpret_cast<const uint4 *>(
+                                   q16 + ((size_t)kvh * QPK + l32) * HD + 64 * dg + 16 * c + 8 * hh)
+                             : make_uint4(0, 0, 0, 0);
+        qb[c] = __builtin_bit_cast(ph8, w);
+    }
     if (tid < QPK) m_s[tid] = kPNegBig, l_s[tid] = 0.f;
-    float acc[QPK][ND];
+    pf16x acc;
 #pragma unroll
-    for (int h = 0; h < QPK; h++)
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
+
+    // K (A operands) and V (staging words) of a tile, loaded ahead
+    // (vector values, not arrays: arrays assigned on two paths stay in scratch)
+    constexpr int KW = KQ8 ? 2 : 4;  // K words per A operand
+    typedef uint32_t kv_t __attribute__((ext_vector_type(4 * KW)));
+    typedef uint32_t vv_t __attribute__((ext_vector_type(4 * NU)));
+    typedef uint32_t sv_t __attribute__((ext_vector_type(8)));
+    kv_t kr;
+    vv_t vr;
+    sv_t ksr;  // Q8_0: the 16 block scales of slot `lane` (wave 0)
+    auto load_tile = [&](uint32_t t0) __attribute__((always_inline)) {
+        const int n = (int)min((uint32_t)kPTile, t_end - t0);
+        const size_t krow = (size_t)(t0 + min(32 * sb + l32, n - 1)) * n_kv + kvh;
 #pragma unroll
-        for (int e = 0; e < ND; e++) acc[h][e] = 0.f;
+        for (int c = 0; c < 4; c++) {
+            const size_t off = krow * HD + 64 * dg + 16 * c + 8 * hh;
+            if constexpr (KQ8) {
+                const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const int8_t *>(kp) + off);
+                kr[2 * c] = w.x, kr[2 * c + 1] = w.y;
+            } else {
+                const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(kp) + off);
+                kr[4 * c] = w.x, kr[4 * c + 1] = w.y, kr[4 * c + 2] = w.z, kr[4 * c + 3] = w.w;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NU; j++) {
+            const int u = tid + j * NT, sl = u / (HD / 8), c8 = u % (HD / 8);
+            const uint4 w = *reinterpret_cast<const uint4 *>(
+                v16 + (size_t)(t0 + min(sl, n - 1)) * kv_row + (size_t)kvh * HD + 8 * c8);
+            vr[4 * j] = w.x, vr[4 * j + 1] = w.y, vr[4 * j + 2] = w.z, vr[4 * j + 3] = w.w;
+        }
+        if constexpr (KQ8)
+            if (wave == 0) {
+                const uint4 *kss = reinterpret_cast<const uint4 *>(
+                    k_scales + ((size_t)(t0 + min(lane, n - 1)) * n_kv + kvh) * (HD / 32));
+                const uint4 a = kss[0], b = kss[1];
+                ksr[0] = a.x, ksr[1] = a.y, ksr[2] = a.z, ksr[3] = a.w;
+                ksr[4] = b.x, ksr[5] = b.y, ksr[6] = b.z, ksr[7] = b.w;
+            }
+    };
+    if (t_begin < t_end) load_tile(t_begin);
     __syncthreads();
 
     for (uint32_t t0 = t_begin; t0 < t_end; t0 += kPTile) {
         const int n = (int)min((uint32_t)kPTile, t_end - t0);
-        // ---- scores of the tile's slots (lane = slot), this wave's dims
-        float a[QPK];
+        // ---- V into LDS; partial Sᵀ of the wave's slot block and dims
 #pragma unroll
-        for (int h = 0; h < QPK; h++) a[h] = 0.f;
-        if (lane < n) {
-            const size_t row = (size_t)(t0 + lane) * n_kv + kvh;
+        for (int j = 0; j < NU; j++) {
+            const int u = tid + j * NT, sl = u / (HD / 8), c8 = u % (HD / 8);
+            *reinterpret_cast<uint4 *>(&vs_s[sl][8 * c8]) =
+                make_uint4(vr[4 * j], vr[4 * j + 1], vr[4 * j + 2], vr[4 * j + 3]);
+        }
+        if constexpr (KQ8)
+            if (wave == 0) {
+                *reinterpret_cast<uint4 *>(&ks_s[lane][0]) = make_uint4(ksr[0], ksr[1], ksr[2], ksr[3]);
+                *reinterpret_cast<uint4 *>(&ks_s[lane][4]) = make_uint4(ksr[4], ksr[5], ksr[6], ksr[7]);
+            }
+        pf16x d0, d1;
 #pragma unroll
-            for (int b = 0; b < PB; b++) {
-                const int d0 = wave * DW + 32 * b;
-                float kf[32];
-                float d = 1.f;
-                if (KQ8) {
-                    const int8_t *kr = static_cast<const int8_t *>(kp) + row * HD + d0;
-                    const int4 w0 = reinterpret_cast<const int4 *>(kr)[0];
-                    const int4 w1 = reinterpret_cast<const int4 *>(kr)[1];
-                    const int ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        for (int i = 0; i < 16; i++) d0[i] = d1[i] = 0.f;
 #pragma unroll
-                    for (int j = 0; j < 8; j++)
+        for (int c = 0; c < 4; c++) {
+            ph8 a;
+            if constexpr (KQ8) a = i8x8_f16(kr[2 * c], kr[2 * c + 1]);
+            else a = __builtin_bit_cast(ph8, make_uint4(kr[4 * c], kr[4 * c + 1], kr[4 * c + 2], kr[4 * c + 3]));
+            if (KQ8 && c >= 2) d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], d1, 0, 0, 0);
+            else d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[c], d0, 0, 0, 0);
+        }
+        if (hcol)
 #pragma unroll
-                        for (int e = 0; e < 4; e++) kf[4 * j + e] = (float)(int8_t)(ww[j] >> (8 * e));
-                    d = h2f(k_scales[row * (HD / 32) + d0 / 32]);
+            for (int i = 0; i < 16; i++) {
+                const int slot = 32 * sb + 8 * (i / 4) + 4 * hh + (i % 4);
+                if constexpr (KQ8) {
+                    sp_s[2 * dg][l32][slot] = d0[i];
+                    sp_s[2 * dg + 1][l32][slot] = d1[i];
                 } else {
-                    const uint4 *kr = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(kp) +
-                                                                      row * HD + d0);
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const uint4 w = kr[c];
-                        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            kf[8 * c + 2 * e] = h2f((uint16_t)(ww[e] & 0xffffu));
-                            kf[8 * c + 2 * e + 1] = h2f((uint16_t)(ww[e] >> 16));
-                        }
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < QPK; h++) {
-                    float dot = 0.f;
-#pragma unroll
-                    for (int j = 0; j < 32; j++) dot = __builtin_fmaf(q_s[h][d0 + j], kf[j], dot);
-                    a[h] = KQ8 ? __builtin_fmaf(d, dot, a[h]) : a[h] + dot;
+                    sp_s[dg][l32][slot] = d0[i];
                 }
             }
-        }
-#pragma unroll
-        for (int h = 0; h < QPK; h++) sp_s[wave][h][lane] = a[h];
+        if (t0 + kPTile < t_end) load_tile(t0 + kPTile);  // the next tile, in flight
         __syncthreads();
-        // ---- the tile's softmax step per head (wave w: heads w, w + 4)
-        for (int h = wave; h < QPK; h += 4) {
-            const float s = lane < n ? (((sp_s[0][h][lane] + sp_s[1][h][lane]) + sp_s[2][h][lane]) +
-                                        sp_s[3][h][lane]) * scale
-                                     : kPNegBig;
+        // ---- the tile's softmax step, one wave per query head (lane = slot)
+        if (wave < QPK) {
+            const int h = wave;
+            float sum = 0.f;
+            if constexpr (KQ8) {
+                const uint4 ka = *reinterpret_cast<const uint4 *>(&ks_s[lane][0]);
+                const uint4 kb = *reinterpret_cast<const uint4 *>(&ks_s[lane][4]);
+                const uint32_t kw[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+#pragma unroll
+                for (int g = 0; g < NG; g++)
+                    sum = __builtin_fmaf(h2f((uint16_t)(kw[g / 2] >> (16 * (g & 1)))), sp_s[g][h][lane], sum);
+            } else {
+#pragma unroll
+                for (int g = 0; g < NG; g++) sum += sp_s[g][h][lane];
+            }
+            const float s = lane < n ? sum * scale : kPNegBig;
             float mt = s;
             for (int o = 32; o > 0; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, kWave));
             const float m_old = m_s[h];
@@ -127,7 +206,9 @@ __global__ __launch_bounds__(256) void attn_decode_pages_kernel(
             const float p = lane < n ? expf(s - m_new) : 0.f;
             float ps = p;
             for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o, kWave);
-            p_s[h][lane] = p;
+            const _Float16 phi = (_Float16)p;
+            ph_s[h][lane] = phi;
+            pl_s[h][lane] = (_Float16)(p - (float)phi);
             if (lane == 0) {
                 const float corr = expf(m_old - m_new);  // the first tile: exp(-3e38 - m) = 0
                 corr_s[h] = corr;
@@ -136,73 +217,64 @@ __global__ __launch_bounds__(256) void attn_decode_pages_kernel(
             }
         }
         __syncthreads();
-        // ---- PV: this thread's ND dims of every query head
+        // ---- Oᵀ(dims 32·wave.., heads) += Vᵀ·Pᵀ over the tile's 64 slots
         {
-            uint32_t vw[kPTile];
+            const float c = corr_s[hcol ? l32 : 0];
 #pragma unroll
-            for (int i = 0; i < kPTile; i++) {
-                const size_t row = (size_t)(t0 + min(i, n - 1)) * n_kv + kvh;
-                const uint16_t *vr = v16 + row * HD + tid * ND;
-                vw[i] = ND == 2 ? *reinterpret_cast<const uint32_t *>(vr) : (uint32_t)vr[0];
-            }
+            for (int i = 0; i < 16; i++) acc[i] *= c;
 #pragma unroll
-            for (int h = 0; h < QPK; h++) {
-                const float c = corr_s[h];
+            for (int c4 = 0; c4 < 4; c4++) {
+                const int s0 = 16 * c4 + 8 * hh;
+                ph8 a;
 #pragma unroll
-                for (int e = 0; e < ND; e++) acc[h][e] *= c;
-            }
-#pragma unroll
-            for (int i = 0; i < kPTile; i++) {
-                if (i < n) {  // workgroup-uniform
-                    float v[ND];
-#pragma unroll
-                    for (int e = 0; e < ND; e++) v[e] = h2f((uint16_t)(vw[i] >> (16 * e)));
-#pragma unroll
-                    for (int h = 0; h < QPK; h++) {
-                        const float p = p_s[h][i];
-#pragma unroll
-                        for (int e = 0; e < ND; e++) acc[h][e] = __builtin_fmaf(p, v[e], acc[h][e]);
-                    }
-                }
+                for (int e = 0; e < 8; e++) a[e] = vs_s[s0 + e][32 * wave + l32];
+                const ph8 bh = hcol ? *reinterpret_cast<const ph8 *>(&ph_s[l32][s0]) : ph8{};
+                const ph8 bl = hcol ? *reinterpret_cast<const ph8 *>(&pl_s[l32][s0]) : ph8{};
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, acc, 0, 0, 0);
             }
         }
-        __syncthreads();  // p_s / sp_s are rewritten by the next tile
+        __syncthreads();  // vs_s, sp_s and the P tiles are rewritten by the next tile
     }
 
     constexpr int stride = HD + 2;
+    if (hcol) {
+        float *pp = part + ((size_t)(kvh * QPK + l32) * n_splits + split) * stride + 32 * wave;
 #pragma unroll
-    for (int h = 0; h < QPK; h++) {
-        float *pr = part + ((size_t)(kvh * QPK + h) * n_splits + split) * stride;
-#pragma unroll
-        for (int e = 0; e < ND; e++) pr[tid * ND + e] = acc[h][e];
-        if (tid == 0) {
-            pr[HD] = m_s[h];
-            pr[HD + 1] = l_s[h];
-        }
+        for (int i = 0; i < 16; i++) pp[8 * (i / 4) + 4 * hh + (i % 4)] = acc[i];
+    }
+    if (tid < QPK) {
+        float *pp = part + ((size_t)(kvh * QPK + tid) * n_splits + split) * stride;
+        pp[HD] = m_s[tid];
+        pp[HD + 1] = l_s[tid];
     }
 }
 
-// The split merge in split order, as attn_reduce.wgsl:33-56 folds it:
-// m' = max(m, m_s), acc = acc·e^(m - m') + acc_s·e^(m_s - m'), l likewise;
-// out = f16(acc / l).  One 256-thread workgroup per query head.
+// The split merge (attn_reduce.wgsl:33-56 folds the splits in order with a
+// running max; the same sum, weighted by exp(m_s - max over all splits)):
+// out = f16(sum_s e^(m_s - M)·acc_s / sum_s e^(m_s - M)·l_s).  The global
+// max first, then independent weighted loads.  One 256-thread workgroup per
+// query head.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_reduce_pages_kernel(const float *__restrict__ part,
                                                                  int n_splits,
                                                                  uint16_t *__restrict__ out) {
     constexpr int ND = HD / 256, stride = HD + 2;
     const int h = blockIdx.x, tid = threadIdx.x;
-    float m = kPNegBig, l = 0.f, acc[ND];
+    const float *ph = part + (size_t)h * n_splits * stride;
+    float m = kPNegBig;
+#pragma unroll 8
+    for (int s = 0; s < n_splits; s++) m = fmaxf(m, ph[(size_t)s * stride + HD]);
+    float l = 0.f, acc[ND];
 #pragma unroll
     for (int e = 0; e < ND; e++) acc[e] = 0.f;
+#pragma unroll 8
     for (int s = 0; s < n_splits; s++) {
-        const float *pr = part + ((size_t)h * n_splits + s) * stride;
-        const float ms = pr[HD], ls = pr[HD + 1];
-        const float m_new = fmaxf(m, ms);
-        const float ca = expf(m - m_new), cb = expf(ms - m_new);
+        const float *pr = ph + (size_t)s * stride;
+        const float w = expf(pr[HD] - m);
+        l = __builtin_fmaf(w, pr[HD + 1], l);
 #pragma unroll
-        for (int e = 0; e < ND; e++) acc[e] = acc[e] * ca + pr[tid * ND + e] * cb;
-        l = l * ca + ls * cb;
-        m = m_new;
+        for (int e = 0; e < ND; e++) acc[e] = __builtin_fmaf(w, pr[tid * ND + e], acc[e]);
     }
 #pragma unroll
     for (int e = 0; e < ND; e++)
@@ -237,13 +309,13 @@ int launch_attn_decode_pages(hipStream_t st, const uint16_t *q, const void *k,
     const int qpk = n_q / n_kv;
     const dim3 grid(n_kv, n_splits);
     if (head_dim == 256 && qpk == 2 && !k_scales)
-        hipLaunchKernelGGL((attn_decode_pages_kernel<256, 2, false>), grid, dim3(256), 0, st, q, k,
+        hipLaunchKernelGGL((attn_decode_pages_kernel<256, 2, false>), grid, dim3(512), 0, st, q, k,
                            k_scales, v, part, step, step_word, n_kv, n_splits, scale);
     else if (head_dim == 512 && qpk == 8 && !k_scales)
-        hipLaunchKernelGGL((attn_decode_pages_kernel<512, 8, false>), grid, dim3(256), 0, st, q, k,
+        hipLaunchKernelGGL((attn_decode_pages_kernel<512, 8, false>), grid, dim3(1024), 0, st, q, k,
                            k_scales, v, part, step, step_word, n_kv, n_splits, scale);
     else if (head_dim == 512 && qpk == 8 && k_scales)
-        hipLaunchKernelGGL((attn_decode_pages_kernel<512, 8, true>), grid, dim3(256), 0, st, q, k,
+        hipLaunchKernelGGL((attn_decode_pages_kernel<512, 8, true>), grid, dim3(1024), 0, st, q, k,
                            k_scales, v, part, step, step_word, n_kv, n_splits, scale);
     else
         return fail(SGQ_ERR_VALIDATION,
