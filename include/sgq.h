@@ -140,8 +140,11 @@ typedef struct {
  *   attn_prefill_global_flash_sp_iq  [32, M/16]; 0 q_i8, 1 q_scales f16
  *       [M × 32 × 16], 2 k_quants, 3 k_scales, 4 V f16, 5 out, 6 step (score
  *       = sum over 32-dim blocks of q_scale·k_scale·integer dot)
- * attn_prefill_global_flash_sp_ipv[_bcast] (int8 PV at head_dim 512) return
- * SGQ_ERR_UNKNOWN_KERNEL naming attn_prefill_global_flash_sp_iq. */
+ *   attn_prefill_global_flash_sp_ipv / _ipv_bcast  [32, M/16]; 0 q_i8,
+ *       1 q_scales, 2 k_quants, 3 k_scales, 4 v_quants, 5 key-blocked v_scales
+ *       f16 [pos/32 × 4 × 512], 6 out, 7 step (P quantized per query and
+ *       32-key block; attn_prefill_global_flash_sp_ipv.wgsl:134-210)
+ * Any other name returns SGQ_ERR_UNKNOWN_KERNEL. */
 int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
                       sgq_kernel_info *info);
 /* Number of registered variant names / the i-th one (for enumeration). */

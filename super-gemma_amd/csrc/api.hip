@@ -131,7 +131,8 @@ const char *const kNames[] = {
     "attn_reduce_d256", "attn_reduce_d512", "kv_append_sliding", "kv_append_global",
     "attn_prefill_sliding", "attn_prefill_sliding_ring", "attn_prefill_global",
     "attn_prefill_global_flash", "attn_prefill_global_flash_sp", "attn_prefill_global_flash_sp_q8",
-    "attn_prefill_global_flash_sp_iq",
+    "attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_sp_ipv",
+    "attn_prefill_global_flash_sp_ipv_bcast",
 };
 
 // The benchmark geometry of the hd128 attention forms (32 query heads over
@@ -145,22 +146,12 @@ constexpr uint32_t kAttnNQ = 32, kAttnNKv = 16, kAttnWindow = 1024;
 // ring 1024) and 512 global (4 kv heads, 8 q heads each, K = V rows).
 constexpr uint32_t kRealNQ = 32, kSlNKv = 16, kGlNKv = 4;
 
-// Reference variants this build does not provide: the int8-PV prefill at
-// head_dim 512 (crates/sg-gpu/build.rs:2293-2335); lookup names the form to
-// use instead.
-struct Unbuilt {
-    const char *name, *use;
-};
-const Unbuilt kUnbuilt[] = {
-    {"attn_prefill_global_flash_sp_ipv", "attn_prefill_global_flash_sp_iq"},
-    {"attn_prefill_global_flash_sp_ipv_bcast", "attn_prefill_global_flash_sp_iq"},
-};
-
 // The real checkpoint's prefill attention variants (crates/sg-gpu/build.rs:
-// 395-438, :2206-2292): head_dim, kv heads, page format (the kernel's
+// 395-438, :2206-2335): head_dim, kv heads, page format (the kernel's
 // PfFmt: 1 Q8_0 K/V with f16 q, 2 f16 pages, 3 int8 q and Q8_0 K with f16
-// V), window, ring, bindings, and the grid form: per token [n_kv, M] or per
-// 16-query tile [32, M/16].
+// V, 4 the same with int8 V under key-blocked scales and int8 P), window,
+// ring, bindings, and the grid form: per token [n_kv, M] or per 16-query
+// tile [32, M/16].
 struct PrefillVariant {
     const char *name;
     uint32_t head_dim, n_kv, fmt, window, ring, bindings;
@@ -174,6 +165,8 @@ const PrefillVariant kPrefill[] = {
     {"attn_prefill_global_flash_sp", 512, kGlNKv, 2, 0, 0, 5, false},
     {"attn_prefill_global_flash_sp_q8", 512, kGlNKv, 1, 0, 0, 7, false},
     {"attn_prefill_global_flash_sp_iq", 512, kGlNKv, 3, 0, 0, 7, false},
+    {"attn_prefill_global_flash_sp_ipv", 512, kGlNKv, 4, 0, 0, 8, false},
+    {"attn_prefill_global_flash_sp_ipv_bcast", 512, kGlNKv, 4, 0, 0, 8, false},
 };
 
 // RoPE variants: (name, head_dim, rot_dims, n_heads).  The first four are
@@ -321,6 +314,8 @@ bool resolve(const std::string &name, sgq_kernel *k) {
             // ring (7): 0 q, 1 K ring, 2 V ring, 3 chunk K, 4 chunk V, 5 out, 6 step
             // q8 (7): 0 q f16, 1 k_quants, 2 k_scales, 3 v_quants, 4 v_scales, 5 out, 6 step
             // iq (7): 0 q_i8, 1 q_scales, 2 k_quants, 3 k_scales, 4 V f16, 5 out, 6 step
+            // ipv (8): 0 q_i8, 1 q_scales, 2 k_quants, 3 k_scales, 4 v_quants, 5 key-blocked
+            //   v_scales [slot/32 × n_kv × HD], 6 out, 7 step
             k->kind = Kind::AttnPrefillPages;
             k->info = {{64, 1, 1}, kPrefill[i].bindings, 4, 0};
             k->param = i;
@@ -528,12 +523,6 @@ int sgq_kernel_lookup(sgq_ctx *ctx, const char *name, const sgq_kernel **out,
                       sgq_kernel_info *info) {
     (void)ctx;
     if (!name || !out) return fail(SGQ_ERR_VALIDATION, "NULL argument");
-    for (const Unbuilt &u : kUnbuilt)
-        if (std::strcmp(name, u.name) == 0)
-            return fail(SGQ_ERR_UNKNOWN_KERNEL,
-                        "kernel variant '%s' (int8 PV at head_dim 512) is not built: "
-                        "use '%s' (f16 PV)",
-                        name, u.use);
     auto *k = new sgq_kernel;
     if (!resolve(name, k)) {
         delete k;
@@ -846,8 +835,8 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
         }
         case Kind::AttnPrefillPages: {
             const PrefillVariant &pv = kPrefill[kernel->param];
-            void *pp[7];
-            uint64_t rr[7];
+            void *pp[8];
+            uint64_t rr[8];
             for (uint32_t i = 0; i < pv.bindings; i++)
                 if ((rc = B.get(i, &pp[i], &rr[i]))) return rc;
             const uint32_t hd = pv.head_dim, nkv = pv.n_kv, nb = pv.bindings;
@@ -860,7 +849,7 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                 return fail(SGQ_ERR_VALIDATION, "%s: M %llu too large", kernel->name.c_str(),
                             (unsigned long long)m);
             const uint64_t row = (uint64_t)kRealNQ * hd;  // q / out elements per query
-            const bool iq = pv.fmt == 3, ring = pv.ring != 0;
+            const bool iq = pv.fmt == 3 || pv.fmt == 4, ring = pv.ring != 0;
             if ((rr[nb - 2] && rr[nb - 2] < m * row * 2) || (rr[nb - 1] && rr[nb - 1] < 16) ||
                 (rr[0] && rr[0] < m * row * (iq ? 1 : 2)) ||
                 (iq && rr[1] && rr[1] < m * row / 32 * 2))
@@ -878,6 +867,7 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             if (iq) {
                 qs = static_cast<const uint16_t *>(pp[1]);
                 k = pp[2], ks = static_cast<const uint16_t *>(pp[3]), v = pp[4];
+                if (pv.fmt == 4) vs = static_cast<const uint16_t *>(pp[5]);
             } else if (pv.fmt == 1) {
                 k = pp[1], ks = static_cast<const uint16_t *>(pp[2]);
                 v = pp[3], vs = static_cast<const uint16_t *>(pp[4]);

@@ -711,18 +711,26 @@ __global__ __launch_bounds__(256 * HPW + 256) void attn_prefill_ws_kernel(
 //           (attn_prefill_global_flash_sp_iq.wgsl:94-125).  The integer
 //           dot runs on the f16 MFMA over the quants' exact f16 values
 //           (|products| < 2^14, block sums < 2^24: exact in fp32).
+//   kPfIPV  as kPfIQ for q and K; V int8 with key-blocked f16 scales (one per
+//           32 keys and column, kv_append_global_v_q8.wgsl:32-75), causal
+//           only, so every 32-key tile is one V scale block; P is quantized
+//           per (query, tile): d = amax/127, q = min(127, rint(p/d)), the
+//           denominator sums f16(d)·q; Oᵀ += (Vᵀ_q·Pᵀ_q)·v_scale[dim]·f16(d),
+//           the integer dot exact on the f16 MFMA
+//           (attn_prefill_global_flash_sp_ipv.wgsl:134-210)
 // Except for kPfQ8, q enters the MFMA as its exact f16 values and the
 // scores are scaled afterwards.
-enum PfFmt { kPfQ8 = 0, kPfQ8H = 1, kPfF16 = 2, kPfIQ = 3 };
+enum PfFmt { kPfQ8 = 0, kPfQ8H = 1, kPfF16 = 2, kPfIQ = 3, kPfIPV = 4 };
 
 template <int HD, int FMT>
 __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     const void *__restrict__ qv, const uint16_t *__restrict__ q_scales, KvSource src,
     void *__restrict__ outv, int n_tok, int q0_host, const uint32_t *__restrict__ step, int n_q,
     int n_kv, int window, float scale, int qtiles) {
-    constexpr bool QF32 = FMT == kPfQ8, QI8 = FMT == kPfIQ;
+    constexpr bool VKB = FMT == kPfIPV;  // int8 V, key-blocked scales, int8 P
+    constexpr bool QF32 = FMT == kPfQ8, QI8 = FMT == kPfIQ || VKB;
     constexpr bool KQ8 = FMT == kPfQ8 || FMT == kPfQ8H;  // dequantized into LDS
-    constexpr bool KF16 = FMT == kPfF16, KRAW = FMT == kPfIQ;
+    constexpr bool KF16 = FMT == kPfF16, KRAW = FMT == kPfIQ || VKB;
     constexpr bool VF16 = FMT == kPfF16 || FMT == kPfIQ;
     constexpr bool O16 = FMT != kPfQ8;
     constexpr int D = HD / 128;        // waves per query tile
@@ -739,7 +747,8 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     __shared__ __align__(16) _Float16 k_s[KT][KRow];
     __shared__ __align__(16) uint32_t vt_s[2][VBuf];
     __shared__ __align__(16) float4 ex_s[8][4][64];  // partial scores [wave][i/4][lane]
-    __shared__ __align__(16) float ksc_s[KRAW ? NB : 1][KT];  // kPfIQ: k scales [block][key]
+    __shared__ __align__(16) float ksc_s[KRAW ? NB : 1][KT];  // int8 QK: k scales [block][key]
+    __shared__ __align__(16) float vsk_s[VKB ? 2 : 1][VKB ? HD : 1];  // the tile's V scales
     auto vt_at = [](int row, int col) { return row * VS + (row >> 4) * NP + col; };
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
@@ -832,6 +841,7 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     kraw_t rk[2];
     vraw_t rv[2];
     uint16_t rsk[2], rsv[2];
+    float rvk = 0.f;  // kPfIPV: the V scale of column tid for the tile's key block
     auto fetch = [&](int kl) {
 #pragma unroll
         for (int e = 0; e < 2; e++) {
@@ -842,10 +852,17 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
             rk[e] = gload(reinterpret_cast<const kraw_t *>((fresh ? kq_f : kq_c) + (row * HD + dim0) * EK));
             rv[e] = gload(reinterpret_cast<const vraw_t *>((fresh ? vq_f : vq_c) + (row * HD + dim0) * EV));
             if constexpr (!KF16) rsk[e] = gload((fresh ? ks_f : ks_c) + row * NB + blk);
-            if constexpr (!VF16) rsv[e] = gload((fresh ? vs_f : vs_c) + row * NB + blk);
+            if constexpr (!VF16 && !VKB) rsv[e] = gload((fresh ? vs_f : vs_c) + row * NB + blk);
         }
+        if constexpr (VKB)
+            if (tid < HD)
+                rvk = (float)__builtin_bit_cast(
+                    _Float16, gload(vs_c + ((size_t)(kl / 32) * n_kv + kvh) * HD + tid));
     };
-    auto stage = [&](int kl, uint32_t *vt) {
+    auto stage = [&](int kl, int vb) {
+        uint32_t *vt = vt_s[vb];
+        if constexpr (VKB)
+            if (tid < HD) vsk_s[vb][tid] = rvk;
         uint32_t vpk[CW];
 #pragma unroll
         for (int e = 0; e < 2; e++) {
@@ -887,7 +904,10 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
                     vv[2 * w + 1] = live ? p[1] : (_Float16)0.f;
                 }
             } else {
-                const _Float16 sv = live ? __builtin_bit_cast(_Float16, rsv[e]) : (_Float16)0.f;
+                // kPfIPV: the quants themselves (exact f16), scaled after the dot
+                const _Float16 sv = !live ? (_Float16)0.f
+                                    : VKB ? (_Float16)1.f
+                                          : __builtin_bit_cast(_Float16, rsv[e]);
                 const h2 dv = {sv, sv};
 #pragma unroll
                 for (int w = 0; w < CW / 4; w++) {
@@ -909,7 +929,7 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
     };
 
     fetch(k_lo);
-    stage(k_lo, vt_s[0]);
+    stage(k_lo, 0);
     if (k_lo + KT <= k_hi) fetch(k_lo + KT);
     __syncthreads();
     int buf = 0;
@@ -958,7 +978,7 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
                                               s0[4 * j + 2] + s1[4 * j + 2], s0[4 * j + 3] + s1[4 * j + 3]);
         __syncthreads();  // the partials visible; K(t) fully read
         if (kl + KT <= k_hi) {  // stage t+1 (V into the other buffer), fetch t+2
-            stage(kl + KT, vt_s[buf ^ 1]);
+            stage(kl + KT, buf ^ 1);
             if (kl + 2 * KT <= k_hi) fetch(kl + 2 * KT);
         }
         // the D partials in slice order: the same bits in every wave of the tile
@@ -995,11 +1015,33 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
             const float corr = __builtin_amdgcn_exp2f(m_run - mx);
             float rs = 0.f;
             h8 pb[2];
+            float pdd = 0.f;  // kPfIPV: f16(d) of the tile's P quants
+            if constexpr (VKB) {
+                float pf[16], amax = 0.f;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float p = full || s[i] > kNegBig ? __builtin_amdgcn_exp2f(s[i] - mx) : 0.f;
-                rs += p;
-                pb[i / 8][i % 8] = (_Float16)p;
+                for (int i = 0; i < 16; i++) {
+                    pf[i] = full || s[i] > kNegBig ? __builtin_amdgcn_exp2f(s[i] - mx) : 0.f;
+                    amax = fmaxf(amax, pf[i]);
+                }
+                amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));  // the other 16 keys
+                const float dq = amax * (1.0f / 127.0f);
+                const float id = dq > 0.f ? 1.0f / dq : 0.f;
+                pdd = (float)(_Float16)dq;
+                int qsum = 0;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int qi = min(127, (int)__builtin_rintf(pf[i] * id));
+                    qsum += qi;
+                    pb[i / 8][i % 8] = (_Float16)(float)qi;
+                }
+                rs = pdd * (float)qsum;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float p = full || s[i] > kNegBig ? __builtin_amdgcn_exp2f(s[i] - mx) : 0.f;
+                    rs += p;
+                    pb[i / 8][i % 8] = (_Float16)p;
+                }
             }
             rs += __shfl_xor(rs, 32, kWave);
             l_run = l_run * corr + rs;
@@ -1011,18 +1053,40 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
                     for (int i = 0; i < 16; i++) o[d][i] *= corr;
             }
             // Oᵀ (this wave's 128 dims) += Vᵀ·Pᵀ over the group's two 16-key halves
-#pragma unroll
-            for (int hf = 0; hf < 2; hf++)
+            auto v_operand = [&](int hf, int d) __attribute__((always_inline)) {
+                const int row = 128 * ds + 32 * d + l32;
+                const int c0 = (16 * hf + 4 * hh) / 2;  // dword column (key pair)
+                const uint2 lo = *reinterpret_cast<const uint2 *>(&vt[vt_at(row, c0)]);
+                const uint2 hi = *reinterpret_cast<const uint2 *>(&vt[vt_at(row, c0 + 4)]);
+                const h4 l4 = __builtin_bit_cast(h4, lo), h4v = __builtin_bit_cast(h4, hi);
+                return h8{l4[0], l4[1], l4[2], l4[3], h4v[0], h4v[1], h4v[2], h4v[3]};
+            };
+            if constexpr (VKB) {
+                // per dim chunk: the tile's exact integer dot, then ×v_scale[dim]·f16(d)
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
-                    const int row = 128 * ds + 32 * d + l32;
-                    const int c0 = (16 * hf + 4 * hh) / 2;  // dword column (key pair)
-                    const uint2 lo = *reinterpret_cast<const uint2 *>(&vt[vt_at(row, c0)]);
-                    const uint2 hi = *reinterpret_cast<const uint2 *>(&vt[vt_at(row, c0 + 4)]);
-                    const h4 l4 = __builtin_bit_cast(h4, lo), h4v = __builtin_bit_cast(h4, hi);
-                    const h8 a = {l4[0], l4[1], l4[2], l4[3], h4v[0], h4v[1], h4v[2], h4v[3]};
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[hf], o[d], 0, 0, 0);
+                    f32x16 t;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) t[i] = 0.f;
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_operand(0, d), pb[0], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_operand(1, d), pb[1], t, 0, 0, 0);
+                    const float *vsr = &vsk_s[buf][128 * ds + 32 * d + 4 * hh];
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const float4 sv = *reinterpret_cast<const float4 *>(vsr + 8 * g);
+                        const float svv[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            o[d][4 * g + e] = __builtin_fmaf(t[4 * g + e], svv[e] * pdd, o[d][4 * g + e]);
+                    }
                 }
+            } else {
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+                    for (int d = 0; d < 4; d++)
+                        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v_operand(hf, d), pb[hf], o[d], 0, 0, 0);
+            }
         }
         buf ^= 1;
         __syncthreads();  // V(t) and the slots read; K(t+1), V(t+1) visible
@@ -1124,13 +1188,17 @@ int launch_attn_prefill_pages(hipStream_t st, int fmt, const void *q, const uint
                               const uint16_t *cks, const uint16_t *cvs, void *out, int n_tok,
                               const uint32_t *step, int n_q, int n_kv, int head_dim, int window,
                               float scale) {
-    SGQ_CHECK(fmt == kPfQ8H || fmt == kPfF16 || fmt == kPfIQ, "attn_prefill_pages: format %d", fmt);
+    SGQ_CHECK(fmt == kPfQ8H || fmt == kPfF16 || fmt == kPfIQ || fmt == kPfIPV,
+              "attn_prefill_pages: format %d", fmt);
+    SGQ_CHECK(fmt != kPfIPV || (window == 0 && ring == 0 && v_scales),
+              "attn_prefill_pages: int8 PV is causal over a linear cache with key-blocked V scales");
     SGQ_CHECK(head_dim == 256 || head_dim == 512, "attn_prefill_pages: head_dim %d (256, 512)",
               head_dim);
     SGQ_CHECK(q && k && v && out && step, "attn_prefill_pages: NULL operand");
     SGQ_CHECK(n_tok > 0 && n_kv > 0 && n_q > 0 && n_q % n_kv == 0,
               "attn_prefill_pages: n_tok %d, n_q %d, n_kv %d", n_tok, n_q, n_kv);
-    SGQ_CHECK(fmt != kPfIQ || (q_scales && k_scales), "attn_prefill_pages: int8 q needs the scales");
+    SGQ_CHECK((fmt != kPfIQ && fmt != kPfIPV) || (q_scales && k_scales),
+              "attn_prefill_pages: int8 q needs the scales");
     SGQ_CHECK(fmt != kPfQ8H || (k_scales && v_scales), "attn_prefill_pages: Q8_0 pages need scales");
     SGQ_CHECK(window >= 0 && ring >= 0 && (ring == 0 || (ck && cv && window <= ring)),
               "attn_prefill_pages: a ring needs the chunk's pages and a window within it");
@@ -1149,11 +1217,13 @@ int launch_attn_prefill_pages(hipStream_t st, int fmt, const void *q, const uint
     if (head_dim == 256) {
         if (fmt == kPfQ8H) SGQ_PF_PAGES(256, kPfQ8H);
         else if (fmt == kPfF16) SGQ_PF_PAGES(256, kPfF16);
-        else SGQ_PF_PAGES(256, kPfIQ);
+        else if (fmt == kPfIQ) SGQ_PF_PAGES(256, kPfIQ);
+        else SGQ_PF_PAGES(256, kPfIPV);
     } else {
         if (fmt == kPfQ8H) SGQ_PF_PAGES(512, kPfQ8H);
         else if (fmt == kPfF16) SGQ_PF_PAGES(512, kPfF16);
-        else SGQ_PF_PAGES(512, kPfIQ);
+        else if (fmt == kPfIQ) SGQ_PF_PAGES(512, kPfIQ);
+        else SGQ_PF_PAGES(512, kPfIPV);
     }
 #undef SGQ_PF_PAGES
     SGQ_HIP(hipGetLastError());

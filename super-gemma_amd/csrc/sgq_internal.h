@@ -156,7 +156,8 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
                              float scale, float *part);
 // Prefill attention at head_dim 256/512 over the reference's page formats
 // (prefill_attn.hip, PfFmt): fmt 1 f16 q with Q8_0 K/V (k_scales/v_scales),
-// 2 f16 q/K/V, 3 int8 q (q_scales) with Q8_0 K and f16 V; f16 out
+// 2 f16 q/K/V, 3 int8 q (q_scales) with Q8_0 K and f16 V, 4 the same with int8 V
+// under key-blocked v_scales (causal, linear cache) and int8 P; f16 out
 // [n_tok × n_q × head_dim]; q0 = step[3]; window 0 = causal; ring > 0:
 // keys before q0 from the ring (slot = pos mod ring), from q0 on from the
 // chunk's pages ck/cv (rows = pos - q0; Q8_0 formats: cks/cvs scales).

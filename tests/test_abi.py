@@ -74,8 +74,8 @@ def test_attention_variants_layouts_and_unbuilt_names():
     """The record_layer attention / KV-append surface (crates/sg-model/src/
     graph.rs:560-656): head_dim 128 with Q8_0 K/V, and the real checkpoint's
     decode side over f16 pages with the reference's binding and push layout
-    (crates/sg-gpu/build.rs:255-438, :2206-2292); the int8-PV prefill at
-    head_dim 512 fails with UnknownKernel naming the form to use."""
+    (crates/sg-gpu/build.rs:255-438, :2206-2335); a name outside the
+    registry fails with UnknownKernel."""
     import sgq
 
     L = sgq.lib()
@@ -91,15 +91,14 @@ def test_attention_variants_layouts_and_unbuilt_names():
             "attn_prefill_sliding": (5, 4), "attn_prefill_sliding_ring": (7, 4),
             "attn_prefill_global": (5, 4), "attn_prefill_global_flash": (5, 4),
             "attn_prefill_global_flash_sp": (5, 4), "attn_prefill_global_flash_sp_q8": (7, 4),
-            "attn_prefill_global_flash_sp_iq": (7, 4)}
+            "attn_prefill_global_flash_sp_iq": (7, 4), "attn_prefill_global_flash_sp_ipv": (8, 4),
+            "attn_prefill_global_flash_sp_ipv_bcast": (8, 4)}
     for n, (nb, pb) in want.items():
         assert L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info)) == 0, n
         assert (info.bindings, info.push_bytes) == (nb, pb), n
-    for n, use in [("attn_prefill_global_flash_sp_ipv", "attn_prefill_global_flash_sp_iq"),
-                   ("attn_prefill_global_flash_sp_ipv_bcast", "attn_prefill_global_flash_sp_iq")]:
-        rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
-        msg = L.sgq_last_error().decode()
-        assert rc == 4 and "not built" in msg and f"'{use}'" in msg, (n, msg)
+    rc = L.sgq_kernel_lookup(None, b"attn_prefill_global_flash_sp_ipv_hd64", C.byref(h),
+                             C.byref(info))
+    assert rc == 4 and b"unknown kernel" in L.sgq_last_error()
 
 
 def test_ctx_create_without_device_reports_no_device():

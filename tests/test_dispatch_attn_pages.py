@@ -226,7 +226,9 @@ def test_pages_names_validate_groups_and_ranges(ctx):
 # attn_prefill_global[_flash[_sp]] (hd512, 4 kv heads, causal, f16 pages),
 # _sp_q8 (f16 q, Q8_0 K and V dequantized to f16, as that shader does) and
 # _sp_iq (int8 q and Q8_0 K: score = sum over blocks of q_scale·k_scale·
-# integer dot; f16 V).  q0 = step[3].  Bar: the typed prefill tests' (|err| <=
+# integer dot; f16 V), _sp_ipv[_bcast] (the same with int8 V under key-blocked
+# scales and P quantized per query and 32-key block; oracle attention_head_ipv).
+# q0 = step[3].  Bar: the typed prefill tests' (|err| <=
 # 2e-3·|want| + 1e-3·max|want|, normwise 1e-3) plus the f16 rounding of the
 # output (2^-11 of max|want|): normwise 1.5e-3.  Cache slots the kernel must
 # not read hold f16 NaN.
@@ -239,6 +241,8 @@ PREFILL = {  # name: (head_dim, n_kv, window, per-token grid)
     "attn_prefill_global_flash_sp": (512, 4, 0, False),
     "attn_prefill_global_flash_sp_q8": (512, 4, 0, False),
     "attn_prefill_global_flash_sp_iq": (512, 4, 0, False),
+    "attn_prefill_global_flash_sp_ipv": (512, 4, 0, False),
+    "attn_prefill_global_flash_sp_ipv_bcast": (512, 4, 0, False),
 }
 
 
@@ -316,6 +320,44 @@ def test_prefill_pages_by_name_matches_oracle(ctx, oracle, name, q0, m):
     got = oracle.f16_bits_to_f32(host(out, np.uint16)).reshape(m, NQ, hd)
     want = oracle.attention(qd, kd, vd, m, q0, NQ, nkv, hd, window, scale)
     _prefill_check(got, want, f"{name} q0={q0} M={m}")
+
+
+@pytest.mark.parametrize("name,q0,m", [
+    ("attn_prefill_global_flash_sp_ipv", 0, 128), ("attn_prefill_global_flash_sp_ipv", 200, 64),
+    ("attn_prefill_global_flash_sp_ipv_bcast", 37, 32),
+])
+def test_prefill_ipv_by_name_matches_oracle(ctx, oracle, name, q0, m):
+    """int8 PV at head_dim 512 against oracle.attention_head_ipv on the same
+    dequantized q, K and key-blocked V (the scores are exact here, as the
+    int8 QK is).  P is quantized against the running max in the kernel and the
+    final max in the oracle, so a block's f16 P scale may round differently
+    (2^-11): the int8-PV bar of the head_dim-128 test (2e-3) plus the f16
+    output rounding.  V-scale rows past the last key hold f16 NaN."""
+    hd, nkv = 512, 4
+    print(f"dispatch {name} q0={q0} M={m}", flush=True)
+    rng = oracle.Rng(0x1F5 + q0 + m)
+    n, row = q0 + m, nkv * hd
+    qs, qq = oracle.quant_q8_0(rng.f32_vec(m * NQ * hd))
+    ks, kq = oracle.quant_q8_0(rng.f32_vec(n * row))
+    vq = np.zeros(n * row, np.int8)
+    vs = np.zeros(((n + 31) // 32) * row, np.uint16)
+    oracle.kv_append_v_q8(rng.f32_vec(n * row), n, row, 0, vq, vs)
+    qd, kd = oracle.dequant_q8_0(qs, qq), oracle.dequant_q8_0(ks, kq)
+    vd = oracle.dequant_v_keyblocked(vq, vs, n, row)
+    vs_pad = np.concatenate([vs, np.full(2 * row, F16_NAN, np.uint16)])
+    out = torch.full((m * NQ * hd,), 0x7E00, dtype=torch.int16, device="cuda")
+    scale = 1.0 / np.sqrt(hd)
+    _prefill_by_name(ctx, name, [dev(qq), dev(qs), dev(kq), dev(ks), dev(vq), dev(vs_pad), out,
+                                 _step(ctx, q0, 0, 0, q0)], m, scale)
+    got = oracle.f16_bits_to_f32(host(out, np.uint16)).reshape(m, NQ, hd)
+    want = np.empty_like(got)
+    for i in range(m):
+        for h in range(NQ):
+            want[i, h] = oracle.attention_head_ipv(qd, kd, vd, i, h, NQ, nkv, hd, scale, 0, q0 + i)
+    top = float(np.abs(want).max())
+    assert_close(got, want, 2e-3, 2.5e-3 * top, f"{name} q0={q0} M={m}")
+    err = float(np.abs(got.astype(np.float64) - want).max()) / top
+    assert err <= 2.5e-3, (name, err)
 
 
 def test_prefill_sliding_ring_equals_linear_view(ctx, oracle):
