@@ -112,3 +112,30 @@ def test_ctx_create_without_device_reports_no_device():
     assert rc == 3  # NoDevice: callers skip, as GpuContext::new's error does
     with pytest.raises(sgq.NoDevice):
         sgq.GpuContext(0)
+
+
+# Every variant the reference's model loads (crates/sg-model/src/graph.rs,
+# GraphKernels::load: its load("...") calls).
+MODEL_VARIANTS = [
+    "add_scaled", "attn_decode_global_q8k", "attn_decode_sliding",
+    "attn_prefill_global_flash_sp_iq", "attn_prefill_sliding_ring", "attn_reduce_d256",
+    "attn_reduce_d512", "geglu", "gemm_q4_0_i8_bb_pfd4", "gemm_q4_0_i8_swz_m4n1_k5376_n16384",
+    "gemm_q4_0_i8_swz_m4n1_k5376_n2048", "gemm_q4_0_i8_swz_m4n1_k5376_n21504",
+    "gemm_q4_0_i8_swz_m4n1_k5376_n4096", "gemm_q4_0_i8_swz_m4n1_k5376_n8192",
+    "gemm_q4_0_i8_swz_m4n1_k8192_n5376", "gemm_q4_0_i8_swz_m4n1_s1_k16384_n5376",
+    "gemv_q4_0_k16384", "gemv_q4_0_k21504", "gemv_q4_0_k5376", "gemv_q4_0_k8192",
+    "gemv_q6_k_logits", "kv_append_global", "kv_append_global_q8", "kv_append_sliding",
+    "kv_quant_q8", "rmsnorm_256", "rmsnorm_512", "rmsnorm_5376", "rope_global_k",
+    "rope_global_q", "rope_sliding_k", "rope_sliding_q",
+]
+
+
+def test_every_variant_the_reference_model_loads_resolves():
+    import sgq
+
+    L = sgq.lib()
+    h = C.c_void_p()
+    info = sgq._Info()
+    for n in MODEL_VARIANTS:
+        rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
+        assert rc == 0, (n, L.sgq_last_error())
