@@ -444,7 +444,7 @@ class Decode:
         self.cfg = sgq.default_model_config(max_ctx=16384)
         self.model = sgq.Model(ctx, self.cfg)
         self.mode = mode
-        self.model.decode_mode = {"kernels": 0, "persistent": 1, "fused": 2}[mode]
+        self.model.decode_mode = {"kernels": 0, "fused": 2}[mode]
         self.context = context
         self.model.fill_cache(context)
         self.logits = torch.empty(self.cfg.vocab, dtype=torch.float32, device="cuda")
@@ -750,10 +750,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--decode-mode", default="fused", choices=["persistent", "kernels", "fused"],
+    ap.add_argument("--decode-mode", default="fused", choices=["kernels", "fused"],
                     help="decode workload: five fused launches per layer (default) or one "
-                         "kernel per operator, each step replayed as a hipGraph; or one "
-                         "persistent launch per step")
+                         "kernel per operator, each step replayed as a hipGraph")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "decode_real", "prefill_real", "prefill", "gemv", "mmq", "splitk", "attn_prefill",
                              "attn_prefill_ipv",

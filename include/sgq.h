@@ -372,10 +372,7 @@ int sgq_model_decode(sgq_model *model, uint32_t token, float *logits);
 int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
 /* Decode implementation (no counterpart in the reference, whose graph is one
  * dispatch per operator, graph.rs:478-756): 0 = one kernel per operator
- * (the _graph form captures them), 1 = one persistent cooperative launch
- * per step whose workgroups meet at grid barriers and stream each GEMV's
- * weights while waiting (the _graph form then launches it directly),
- * 2 = five launches per layer (QKV, attention, O, gate/up, down GEMVs) with
+ * (the _graph form captures them), 2 = five launches per layer (QKV, attention, O, gate/up, down GEMVs) with
  * the norms, residual updates, GeGLU and the split merge fused into them
  * (the _graph form captures them), 3 = one kernel per operator at any
  * supported geometry: head_dim 128/256/512 per layer kind, 1/2/4/8 query
@@ -385,12 +382,11 @@ int sgq_model_decode_graph(sgq_model *model, uint32_t token, float *logits);
  * mode 2 (the default for them: the fused GEMVs around the any-geometry
  * attention) or mode 3; their prefill is the chunked MMQ driver at their
  * per-layer widths (head_dim 256/512 prefill attention).
- * Mode 1 fails with SGQ_ERR_VALIDATION when the shape or the device does not
- * fit it. */
+ * Mode 1 (a persistent one-launch step, measured slower) is not built and
+ * fails with SGQ_ERR_VALIDATION. */
 int sgq_model_set_decode_mode(sgq_model *model, int mode);
 int sgq_model_decode_mode(const sgq_model *model);
-/* Waits for the context's stream; SGQ_ERR_HIP if a persistent step could not
- * complete a grid barrier (its outputs are then undefined). */
+/* Waits for the context's stream. */
 int sgq_model_status(sgq_model *model);
 /* Prefill (GpuModel::prefill, crates/sg-model/src/graph.rs:1451-1482): runs
  * the host tokens[0..n) at positions pos..pos+n-1 in chunks of

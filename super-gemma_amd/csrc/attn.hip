@@ -1,6 +1,6 @@
 // Q8_0-KV split-K decode attention kernels and launchers.  The split work
 // item (attn_chunk, int8-MFMA QK) is in attn_mfma.h; the split merge
-// (attn_merge) in attn_body.h, shared with the persistent decode kernel.
+// (attn_merge) in attn_body.h.
 #include "attn_mfma.h"
 
 namespace sgq {

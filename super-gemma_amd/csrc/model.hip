@@ -37,7 +37,6 @@
 #include <vector>
 
 #include "limbs.h"
-#include "persist.h"
 #include "q8.h"
 
 struct sgq_model;
@@ -310,13 +309,10 @@ __global__ __launch_bounds__(256) void geglu_limbs_kernel(const float *__restric
 // (crates/sg-model/src/rope.rs:27-48): pair i of 64 turns by
 // pos·theta^(-2i/128)/factor_i; global layers use the divisor factors
 // [1 × live, 1e30 × rest] (rope.rs:13-16), so pairs past `live` barely move.
-// Also clears the persistent kernel's n_sync sync words (null: none).
 __global__ void model_step_kernel(uint32_t *step, uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                   uint32_t e, float *rope_cs, float theta_s, float theta_g,
-                                  int live_g, unsigned *sync, int n_sync) {
+                                  int live_g) {
     const uint32_t t = threadIdx.x;
-    if (sync)
-        for (int i = (int)t; i < n_sync; i += (int)blockDim.x) sync[i] = 0u;
     if (t < 5) step[t] = t == 0 ? a : t == 1 ? b : t == 2 ? c : t == 3 ? d : e;
     if (t < kHeadDim) {
         const int kind = t / (kHeadDim / 2), i = t % (kHeadDim / 2);
@@ -670,14 +666,7 @@ struct sgq_model {
         float4 *part;
         void *xl_o, *hl;
     } fx{};
-    // persistent decode (mode 1): device layer table, activation arena,
-    // sync words and error flag; `pp` is filled except for the logits
-    int mode = 0;
-    PParams pp{};
-    unsigned *sync = nullptr;
-    int n_sync = 0;
-    int *err = nullptr;
-    int grid = 0;
+    int mode = 0;  // 0 kernel per operator, 2 fused, 3 any geometry
     // prefill chunk buffers (allocated at the first prefill, `chunk` rows)
     struct {
         uint32_t chunk = 0;
@@ -1155,8 +1144,7 @@ static int write_step(sgq_model *m, uint32_t token) {
     hipLaunchKernelGGL(model_step_kernel, dim3(1), dim3(kHeadDim), 0, ctx_stream(m->ctx), m->step,
                        m->pos, kv_sl, m->pos + 1, m->pos, token, m->rope_cs,
                        c.rope_theta_sliding, c.rope_theta_global,
-                       (int)lroundf(c.global_rope_frac * kHeadDim / 2),
-                       m->mode == 1 ? m->sync : nullptr, m->n_sync);
+                       (int)lroundf(c.global_rope_frac * kHeadDim / 2));
     SGQ_HIP(hipGetLastError());
     if (m->mode == 3 || m->generic) {
         const int hd_s = (int)c.head_dim, hd_g = (int)(c.head_dim_global ? c.head_dim_global : c.head_dim);
@@ -1169,19 +1157,11 @@ static int write_step(sgq_model *m, uint32_t token) {
     return SGQ_OK;
 }
 
-static int persistent_step(sgq_model *m, float *logits) {
-    PParams p = m->pp;
-    p.logits = logits;
-    return launch_decode_persistent(ctx_stream(m->ctx), p, (int)(m->cfg.n_q_heads / m->cfg.n_kv_heads),
-                                    m->grid);
-}
-
 int sgq_model_decode(sgq_model *m, uint32_t token, float *logits) {
     if (!m || !logits) return fail(SGQ_ERR_VALIDATION, "NULL argument");
     int rc = write_step(m, token);
     if (rc) return rc;
-    if ((rc = m->mode == 1   ? persistent_step(m, logits)
-               : m->mode == 2 ? record_step_fused(m, logits)
+    if ((rc = m->mode == 2   ? record_step_fused(m, logits)
                : m->mode == 3 ? record_step_generic(m, logits, true)
                               : record_step(m, logits)))
         return rc;
@@ -1191,7 +1171,6 @@ int sgq_model_decode(sgq_model *m, uint32_t token, float *logits) {
 
 int sgq_model_decode_graph(sgq_model *m, uint32_t token, float *logits) {
     if (!m || !logits) return fail(SGQ_ERR_VALIDATION, "NULL argument");
-    if (m->mode == 1) return sgq_model_decode(m, token, logits);  // one launch per step already
     SGQ_CHECK(ctx_stream(m->ctx) != nullptr,
               "model: graph decode needs a non-null stream (sgq_ctx_set_stream)");
     int rc = write_step(m, token);
@@ -1220,97 +1199,14 @@ int sgq_model_decode_graph(sgq_model *m, uint32_t token, float *logits) {
     return SGQ_OK;
 }
 
-// Persistent decode: geometry checks, the device layer table, the arena.
-static int persistent_setup(sgq_model *m) {
-    const sgq_model_config &c = m->cfg;
-    const int H = (int)c.hidden, F = (int)c.ffn, QD = (int)(c.n_q_heads * kHeadDim),
-              KD = (int)(c.n_kv_heads * kHeadDim);
-    const int qpk = (int)(c.n_q_heads / c.n_kv_heads);
-    if (int rc = persist_prepare(qpk)) return rc;
-    int coop = 0, dev = 0;
-    SGQ_HIP(hipGetDevice(&dev));
-    SGQ_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-    SGQ_CHECK(coop, "persistent decode: no cooperative launch on this device");
-    const int G = device_info().cus;
-    PParams &p = m->pp;
-    auto geo = [&](int K, int *S, int *slice) -> int {
-        *S = gemv_slices((uint32_t)K);
-        SGQ_CHECK(*S >= 1, "persistent decode: K %d outside the streamed GEMV geometry", K);
-        *slice = (K / 32 + *S - 1) / *S;
-        SGQ_CHECK(*slice <= 3 * kWave && *slice * 18 <= 3 * kWave * 16,
-                  "persistent decode: K %d slice too long", K);
-        return SGQ_OK;
-    };
-    if (int rc = geo(H, &p.s_h, &p.slice_h)) return rc;
-    if (int rc = geo(QD, &p.s_q, &p.slice_q)) return rc;
-    if (int rc = geo(F, &p.s_f, &p.slice_f)) return rc;
-    // the O projection is prefetched whole into 3 ring slots during attention
-    const int units_per_round = G * (8 / p.s_q);
-    SGQ_CHECK((H + units_per_round - 1) / units_per_round <= 3,
-              "persistent decode: O projection rows %d exceed 3 ring rounds", H);
-    p.n_splits = std::min(64, G / (int)c.n_kv_heads);
-    SGQ_CHECK(p.n_splits >= 1, "persistent decode: %u kv heads > %d workgroups", c.n_kv_heads, G);
-    p.H = H, p.F = F, p.QD = QD, p.KD = KD, p.n_kv = (int)c.n_kv_heads, p.vocab = (int)c.vocab;
-    p.n_layers = (int)c.n_layers;
-    p.eps = c.eps, p.attn_scale = c.attn_scale, p.softcap = c.final_softcap;
-    p.embed_scale = sqrtf((float)H);
-    p.embd = static_cast<const uint8_t *>(m->embd);
-    p.out_norm = m->out_norm;
-    p.step = m->step;
-    p.rope_cs = m->rope_cs;
-    // arena: one region per layer plus the head's
-    PArena &A = p.ar;
-    size_t off = 0;
-    auto take = [&](size_t bytes) {
-        const size_t o = off;
-        off += (bytes + 255) / 256 * 256;
-        return o;
-    };
-    const size_t bl = sizeof(BlockLimbs);
-    A.x = take((size_t)H * 4), A.xl_attn = take((size_t)H / 32 * bl), A.ss_attn = take((size_t)H / 32 * 4);
-    A.qkv = take((size_t)(QD + 2 * KD) * 4);
-    A.part = take((size_t)c.n_q_heads * p.n_splits * (kHeadDim + 2) * 4);
-    A.xl_o = take((size_t)QD / 32 * bl);
-    A.y = take((size_t)H * 4), A.xm = take((size_t)H * 4);
-    A.xl_ffn = take((size_t)H / 32 * bl), A.ss_ffn = take((size_t)H / 32 * 4);
-    A.h = take((size_t)F * 4), A.xl_h = take((size_t)F / 32 * bl), A.d = take((size_t)H * 4);
-    A.stride = off;
-    void *arena = nullptr, *layers = nullptr, *sync = nullptr, *err = nullptr;
-    if (int rc = alloc(m, A.stride * (c.n_layers + 1), &arena)) return rc;
-    m->n_sync = kSyncMergeOff + (int)(c.n_layers * c.n_kv_heads);
-    if (int rc = alloc(m, (size_t)m->n_sync * 4, &sync)) return rc;
-    if (int rc = alloc(m, 256, &err)) return rc;
-    std::vector<PLayer> pl(c.n_layers);
-    for (uint32_t l = 0; l < c.n_layers; l++) {
-        const LayerW &L = m->layers[l];
-        pl[l] = PLayer{L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd, L.attn_norm, L.q_norm, L.k_norm,
-                       L.post_attn_norm, L.ffn_norm, L.post_ffw_norm, L.out_scale, L.kq, L.vq,
-                       L.ks, L.vs, L.slots, L.global ? 1 : 0};
-    }
-    if (int rc = alloc(m, pl.size() * sizeof(PLayer), &layers)) return rc;
-    hipStream_t st = ctx_stream(m->ctx);
-    SGQ_HIP(hipMemcpyAsync(layers, pl.data(), pl.size() * sizeof(PLayer), hipMemcpyHostToDevice, st));
-    SGQ_HIP(hipMemsetAsync(err, 0, 256, st));
-    SGQ_HIP(hipStreamSynchronize(st));
-    p.layers = static_cast<const PLayer *>(layers);
-    p.arena = static_cast<uint8_t *>(arena);
-    p.sync = static_cast<unsigned *>(sync);
-    p.err = static_cast<int *>(err);
-    m->sync = p.sync;
-    m->err = p.err;
-    m->grid = G;
-    return SGQ_OK;
-}
-
 int sgq_model_set_decode_mode(sgq_model *m, int mode) {
     if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
-    SGQ_CHECK(mode >= 0 && mode <= 3,
-              "model: decode mode %d (0 kernels, 1 persistent, 2 fused, 3 any geometry)", mode);
+    SGQ_CHECK(mode == 0 || mode == 2 || mode == 3,
+              "model: decode mode %d (0 kernels, 2 fused, 3 any geometry; 1, a persistent "
+              "one-launch step, measured slower and was removed)", mode);
     SGQ_CHECK(!m->generic || mode >= 2,
               "model: this geometry (head_dim %u/%u, Q6_K embedding %u) runs in modes 2 and 3 only",
               m->cfg.head_dim, m->cfg.head_dim_global, m->cfg.embed_q6k);
-    if (mode == 1 && !m->err)
-        if (int rc = persistent_setup(m)) return rc;
     if (mode != m->mode && m->graph) {  // a captured step belongs to one mode
         sgq_graph_destroy(m->graph);
         m->graph = nullptr;
@@ -1323,15 +1219,7 @@ int sgq_model_decode_mode(const sgq_model *m) { return m ? m->mode : -1; }
 
 int sgq_model_status(sgq_model *m) {
     if (!m) return fail(SGQ_ERR_VALIDATION, "NULL model");
-    hipStream_t st = ctx_stream(m->ctx);
-    SGQ_HIP(hipStreamSynchronize(st));
-    if (!m->err) return SGQ_OK;
-    int e = 0;
-    SGQ_HIP(hipMemcpy(&e, m->err, 4, hipMemcpyDeviceToHost));
-    if (e) {
-        SGQ_HIP(hipMemset(m->err, 0, 4));
-        return fail(SGQ_ERR_HIP, "persistent decode: a grid barrier did not complete");
-    }
+    SGQ_HIP(hipStreamSynchronize(ctx_stream(m->ctx)));
     return SGQ_OK;
 }
 

@@ -610,8 +610,8 @@ class Model:
 
     @property
     def decode_mode(self) -> int:
-        """0: one kernel per operator; 1: one persistent launch per step;
-        2: five fused launches per layer."""
+        """0: one kernel per operator; 2: five fused launches per layer;
+        3: one kernel per operator at any supported geometry."""
         return int(lib().sgq_model_decode_mode(self._h))
 
     @decode_mode.setter
@@ -619,7 +619,7 @@ class Model:
         _check(lib().sgq_model_set_decode_mode(self._h, int(mode)))
 
     def status(self):
-        """Wait for the stream; raises if a persistent step failed."""
+        """Wait for the stream."""
         _check(lib().sgq_model_status(self._h))
 
     def prefill(self, tokens, logits: Optional[torch.Tensor] = None):

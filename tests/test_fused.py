@@ -84,8 +84,8 @@ def test_fused_graph_replays_match_eager(ctx):
 
 
 def test_fused_mode_switch_mid_context(ctx, oracle):
-    """Kernel-per-operator, fused and persistent steps on one context: every
-    step matches the oracle."""
+    """Kernel-per-operator and fused steps on one context: every step matches
+    the oracle; decode mode 1 (the removed persistent step) is refused."""
     import sgq
     from oracle.model import OracleDecoder
 
@@ -96,7 +96,9 @@ def test_fused_mode_switch_mid_context(ctx, oracle):
     ref = OracleDecoder(d, _weights(model, d))
     logits = empty(cfg.vocab, torch.float32)
     with _side_stream(ctx):
-        for i, (t, mode) in enumerate([(9, 0), (8, 2), (7, 2), (6, 0), (5, 2), (4, 1), (3, 2)]):
+        with pytest.raises(sgq.ValidationError):
+            model.decode_mode = 1
+        for i, (t, mode) in enumerate([(9, 0), (8, 2), (7, 2), (6, 0), (5, 2), (4, 0), (3, 2)]):
             model.decode_mode = mode
             model.decode(t, logits, graph=bool(i & 1))
             model.status()
