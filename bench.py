@@ -14,7 +14,8 @@ batch of synthetic input, already resident in HBM:
           8 weight copies (520 MB > the 256 MB MALL) so every launch streams
           its weights from HBM.
   mmq     BASELINE config 2: Q4_0×Q8 int8-MFMA GEMM M=512, K=5376, N=21504.
-  splitk  BASELINE config 3: down-proj M=2048, K=21504, N=5376, split-K 4.
+  splitk  BASELINE config 3: down-proj M=2048, K=21504, N=5376, split-K 4
+          (--split-k 1/2/4/8).
   attn_prefill, attn_prefill_sliding
           BASELINE config 4 prefill: 4096 queries, causal / sliding-1024.
   attn_prefill_ipv
@@ -759,6 +760,8 @@ def main():
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k", "head_q6k", "attn_pages_sliding",
                              "attn_pages_q8k_4k", "attn_pages_q8k_8k", "attn_pages_q8k_32k"])
+    ap.add_argument("--split-k", type=int, default=4, choices=[1, 2, 4, 8],
+                    help="splitk workload: K split (BASELINE config 3 sweeps 1/2/4/8)")
     ap.add_argument("--gemv-rows", type=int, default=21504,
                     help="gemv workload: rows N (config 1 is 21504; other values sweep the "
                          "per-launch fixed cost against the streaming rate)")
@@ -807,7 +810,7 @@ def main():
     elif args.workload.startswith("attn_decode_"):
         wl = AttnDecode(ctx, torch, {"4k": 4096, "32k": 32768, "128k": 131072}[args.workload[12:]])
     else:
-        wl = Mmq(ctx, torch, m=2048, k=21504, n=5376, split=4, label="BASELINE config 3")
+        wl = Mmq(ctx, torch, m=2048, k=21504, n=5376, split=args.split_k, label="BASELINE config 3")
     torch.cuda.synchronize()
     for i in range(args.warmup):
         wl.step(i)
