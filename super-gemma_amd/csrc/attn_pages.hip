@@ -304,8 +304,9 @@ int launch_attn_decode_pages(hipStream_t st, const uint16_t *q, const void *k,
     SGQ_CHECK(q && k && v && part && step, "attn_decode_pages: NULL operand");
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn_decode_pages: n_q %% n_kv != 0");
     SGQ_CHECK(n_splits >= 1 && n_splits <= 65535, "attn_decode_pages: n_splits %d", n_splits);
-    SGQ_CHECK(((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 3) == 0,
-              "attn_decode_pages: misaligned pages");
+    SGQ_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 &&
+                  ((uintptr_t)k_scales & 15) == 0,
+              "attn_decode_pages: q, the pages and the K scales must be 16-byte aligned");
     const int qpk = n_q / n_kv;
     const dim3 grid(n_kv, n_splits);
     if (head_dim == 256 && qpk == 2 && !k_scales)
