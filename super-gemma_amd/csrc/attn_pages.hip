@@ -112,7 +112,7 @@ __global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
     kv_t kr;
     vv_t vr;
     sv_t ksr;  // Q8_0: the 16 block scales of slot `lane` (wave 0)
-    auto load_tile = [&](uint32_t t0) __attribute__((always_inline)) {
+    auto load_k = [&](uint32_t t0) __attribute__((always_inline)) {
         const int n = (int)min((uint32_t)kPTile, t_end - t0);
         const size_t krow = (size_t)(t0 + min(32 * sb + l32, n - 1)) * n_kv + kvh;
 #pragma unroll
@@ -126,13 +126,6 @@ __global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
                 kr[4 * c] = w.x, kr[4 * c + 1] = w.y, kr[4 * c + 2] = w.z, kr[4 * c + 3] = w.w;
             }
         }
-#pragma unroll
-        for (int j = 0; j < NU; j++) {
-            const int u = tid + j * NT, sl = u / (HD / 8), c8 = u % (HD / 8);
-            const uint4 w = *reinterpret_cast<const uint4 *>(
-                v16 + (size_t)(t0 + min(sl, n - 1)) * kv_row + (size_t)kvh * HD + 8 * c8);
-            vr[4 * j] = w.x, vr[4 * j + 1] = w.y, vr[4 * j + 2] = w.z, vr[4 * j + 3] = w.w;
-        }
         if constexpr (KQ8)
             if (wave == 0) {
                 const uint4 *kss = reinterpret_cast<const uint4 *>(
@@ -142,7 +135,20 @@ __global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
                 ksr[4] = b.x, ksr[5] = b.y, ksr[6] = b.z, ksr[7] = b.w;
             }
     };
-    if (t_begin < t_end) load_tile(t_begin);
+    auto load_v = [&](uint32_t t0) __attribute__((always_inline)) {
+        const int n = (int)min((uint32_t)kPTile, t_end - t0);
+#pragma unroll
+        for (int j = 0; j < NU; j++) {
+            const int u = tid + j * NT, sl = u / (HD / 8), c8 = u % (HD / 8);
+            const uint4 w = *reinterpret_cast<const uint4 *>(
+                v16 + (size_t)(t0 + min(sl, n - 1)) * kv_row + (size_t)kvh * HD + 8 * c8);
+            vr[4 * j] = w.x, vr[4 * j + 1] = w.y, vr[4 * j + 2] = w.z, vr[4 * j + 3] = w.w;
+        }
+    };
+    if (t_begin < t_end) {
+        load_k(t_begin);
+        load_v(t_begin);
+    }
     __syncthreads();
 
     for (uint32_t t0 = t_begin; t0 < t_end; t0 += kPTile) {
@@ -154,6 +160,8 @@ __global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
             *reinterpret_cast<uint4 *>(&vs_s[sl][8 * c8]) =
                 make_uint4(vr[4 * j], vr[4 * j + 1], vr[4 * j + 2], vr[4 * j + 3]);
         }
+        // the next tile's V as soon as this one's registers are free
+        if (t0 + kPTile < t_end) load_v(t0 + kPTile);
         if constexpr (KQ8)
             if (wave == 0) {
                 *reinterpret_cast<uint4 *>(&ks_s[lane][0]) = make_uint4(ksr[0], ksr[1], ksr[2], ksr[3]);
@@ -181,7 +189,7 @@ __global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
                     sp_s[dg][l32][slot] = d0[i];
                 }
             }
-        if (t0 + kPTile < t_end) load_tile(t0 + kPTile);  // the next tile, in flight
+        if (t0 + kPTile < t_end) load_k(t0 + kPTile);  // the next tile's K, in flight
         __syncthreads();
         // ---- the tile's softmax step, one wave per query head (lane = slot)
         if (wave < QPK) {
