@@ -111,6 +111,35 @@ def test_decode_pages_by_name_matches_oracle(ctx, oracle, kind, kv_len, splits):
             assert abs(l - lw) <= 1e-4 * lw, (h, s, l, lw)
 
 
+def test_decode_pages_long_context_many_tiles(ctx, oracle):
+    """attn_decode_global_q8k at 32768 slots over the reference's 32 splits:
+    16 tiles of 64 slots per split, so the running max and the rescale of
+    the accumulator are exercised across many tiles; keys drift upward along
+    the context (k·(1 + t/8192)) so that later tiles keep raising the max.
+    Sampled heads against the oracle at the decode bar."""
+    kind, kv_len, splits = "global_q8k", 32768, 32
+    hd, nkv, _ = GEOM[kind]
+    print(f"dispatch attn_decode_{kind} kv_len={kv_len} splits={splits}", flush=True)
+    rng = oracle.Rng(0x32C)
+    q16 = oracle.f32_to_f16_bits(rng.f32_vec(NQ * hd))
+    qf = oracle.f16_bits_to_f32(q16)
+    k = rng.f32_vec(kv_len * nkv * hd).reshape(kv_len, -1)
+    k *= (1.0 + np.arange(kv_len, dtype=np.float32) / 8192.0)[:, None]
+    ks, kq = oracle.quant_q8_0(k.reshape(-1))
+    kf = oracle.dequant_q8_0(ks, kq)
+    vb = oracle.f32_to_f16_bits(rng.f32_vec(kv_len * nkv * hd))
+    vf = oracle.f16_bits_to_f32(vb)
+    scale = 1.0 / np.sqrt(hd)
+    part, out = _decode(ctx, kind, dev(q16), (dev(kq), dev(ks)), dev(vb),
+                        _step(ctx, kv_len - 1, 0, kv_len), splits, scale)
+    got = oracle.f16_bits_to_f32(host(out, np.uint16)).reshape(NQ, hd)
+    heads = [0, 7, 8, 19, 31]
+    want = np.stack([oracle.attention_head(qf, kf, vf, 0, h, NQ, nkv, hd, scale, 0, kv_len - 1)
+                     for h in heads])
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    assert_close(got[heads], want, 1e-3, 1e-4 * rms, "attn_decode_global_q8k 32K")
+
+
 def test_decode_pages_head_mapping_isolates_kv_heads(ctx, oracle):
     """V constant per kv head (value = kv head index + 1): every query head's
     output is exactly its own kv head's value whatever the softmax weights,
