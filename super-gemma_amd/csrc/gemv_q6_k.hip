@@ -118,9 +118,10 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
 
     // a wave computes rows r and r + G together (2·4·nb tasks over its 64
     // lanes: 168 at k = 5376, so lanes stay busy where one row's 84 tasks
-    // would leave 44 of them idle in the second round), while rows r + 2G
-    // and r + 3G load into the registers just emptied
-    i32x4_t pa[kQ6Chunks], pb[kQ6Chunks];
+    // would leave 44 of them idle in the second round), while the next two
+    // pairs of rows are in flight: register sets (pa, pb) and (pc, pd) take
+    // turns, each refilled two iterations ahead as soon as it is in LDS
+    i32x4_t pa[kQ6Chunks], pb[kQ6Chunks], pc[kQ6Chunks], pd[kQ6Chunks];
     auto load = [&](i32x4_t (&pre)[kQ6Chunks], int rr) {
         if (rr >= n) return;
         const i32x4_t *src = reinterpret_cast<const i32x4_t *>(W + (size_t)rr * stride);
@@ -137,21 +138,18 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
             if (idx < nchunks) *reinterpret_cast<i32x4_t *>(row + 16 * idx) = pre[c];
         }
     };
-    load(pa, r);
-    load(pb, r + G);
-    for (int i = threadIdx.x; i < k; i += kQ6WG) xh[i] = (_Float16)x[i];
-    __syncthreads();
-
-    for (; r < n; r += 2 * G) {
-        const int r1 = r + G;
+    // rows rr and rr + G from (A, B); A and B then load rows rr + 4G, rr + 5G
+    auto step = [&](i32x4_t (&A)[kQ6Chunks], i32x4_t (&B)[kQ6Chunks], int rr)
+        __attribute__((always_inline)) {
+        const int r1 = rr + G;
         const bool has1 = r1 < n;
-        put(pa, row0);
-        if (has1) put(pb, row1);
+        put(A, row0);
+        if (has1) put(B, row1);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        load(pa, r + 2 * G);  // land while these two rows compute
-        load(pb, r1 + 2 * G);
+        load(A, rr + 4 * G);  // land while the next pairs compute
+        load(B, r1 + 4 * G);
         float acc0 = 0.f, acc1 = 0.f;
         const int nt = has1 ? 2 * ntask : ntask;
         for (int t = lane; t < nt; t += kWave) {
@@ -164,10 +162,22 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
         acc0 = wave_sum_dpp(acc0);
         acc1 = wave_sum_dpp(acc1);
         if (lane == 0) {
-            y[r] = softcap > 0.f ? softcap * tanhf(acc0 / softcap) : acc0;
+            y[rr] = softcap > 0.f ? softcap * tanhf(acc0 / softcap) : acc0;
             if (has1) y[r1] = softcap > 0.f ? softcap * tanhf(acc1 / softcap) : acc1;
         }
         __builtin_amdgcn_wave_barrier();  // these rows' LDS reads before the next rows' stores
+    };
+    load(pa, r);
+    load(pb, r + G);
+    load(pc, r + 2 * G);
+    load(pd, r + 3 * G);
+    for (int i = threadIdx.x; i < k; i += kQ6WG) xh[i] = (_Float16)x[i];
+    __syncthreads();
+
+    for (; r < n; r += 4 * G) {
+        step(pa, pb, r);
+        if (r + 2 * G >= n) break;
+        step(pc, pd, r + 2 * G);
     }
 }
 
