@@ -33,7 +33,9 @@
 //    reads of rows 8 apart fall on other banks), wave w owns dims
 //    [32w, 32w + 32) of every query head, and P enters as two f16 parts
 //    (p = hi + lo, 22 bits) so the PV keeps fp32 accuracy;
-//  * the next tile's K and V are loaded while this one is computed.
+//  * the next tile's V is requested as soon as this tile's V is in LDS
+//    (before the scores), its K after the score MFMAs have consumed this
+//    tile's K registers.
 #include "sgq_internal.h"
 
 namespace sgq {
