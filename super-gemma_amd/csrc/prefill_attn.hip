@@ -12,7 +12,10 @@
 // position, or position mod ring for a sliding ring), keys from q0 on from
 // the chunk's own pages (row = position - q0) when those are given, else
 // from the cache too.  They are dequantized to f16 as in the reference's
-// _sp_q8 variant; P is rounded to f16 for PV, as in the reference.
+// _sp_q8 variant; P is rounded to f16 for PV, as in the reference.  The
+// head_dim-256/512 kernel (attn_prefill_wide_kernel, below) also reads the
+// reference's other page formats: f16 K/V, int8 q with Q8_0 K, int8 V with
+// key-blocked scales (PfFmt).
 //
 // Design (MFMA-bound: 4·hd flops per query-key pair against 2·hd·1 B of
 // K/V per key per query tile):
