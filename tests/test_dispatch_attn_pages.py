@@ -433,3 +433,59 @@ def test_prefill_pages_names_validate(ctx):
              empty(8 * NQ * 256, torch.int16), _step(ctx, 0, 0, 0, 0)])],
                      struct.pack("<f", 1.0), [16, 8, 1])
     ctx.synchronize()
+
+
+def test_prefill_ring_graph_replay_with_step_q0(ctx, oracle):
+    """record_prefill_layer's use (graph.rs:1176-1190): attn_prefill_sliding_ring
+    recorded once into a graph and replayed for two chunks, the step buffer
+    rewritten with each chunk's q0 and the pages refilled between replays;
+    every replay equals an eager dispatch of the same chunk bit for bit and
+    the oracle at the prefill bar."""
+    import sgq
+
+    hd, nkv, m = 256, 16, 48
+    row = nkv * hd
+    name = "attn_prefill_sliding_ring"
+    k = ctx.load_kernel(name)
+    tq = empty(m * NQ * hd, torch.int16)
+    tkr = empty(RING * row, torch.int16)
+    tvr = empty(RING * row, torch.int16)
+    tkc = empty(m * row, torch.int16)
+    tvc = empty(m * row, torch.int16)
+    out = empty(m * NQ * hd, torch.int16)
+    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    binds = [tq, tkr, tvr, tkc, tvc, out, step]
+    B = [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(binds)]
+    push = struct.pack("<f", 0.0625)
+    s = torch.cuda.Stream()
+    ctx.set_stream(s)
+    try:
+        with sgq.GraphRecorder(ctx) as rec:
+            ctx.dispatch(k, B, push, [nkv, m, 1])
+        for q0 in (1200, 37):
+            print(f"graph replay {name} q0={q0}", flush=True)
+            rng = oracle.Rng(0x6A + q0)
+            q16 = oracle.f32_to_f16_bits(rng.f32_vec(m * NQ * hd))
+            kb = oracle.f32_to_f16_bits(rng.f32_vec((q0 + m) * row))
+            vb = oracle.f32_to_f16_bits(rng.f32_vec((q0 + m) * row))
+            kr = np.zeros(RING * row, np.uint16)
+            vr = np.zeros(RING * row, np.uint16)
+            for p in range(max(0, q0 - RING), q0):
+                sl = (p % RING) * row
+                kr[sl:sl + row], vr[sl:sl + row] = kb[p * row:(p + 1) * row], vb[p * row:(p + 1) * row]
+            for t, a in ((tq, q16), (tkr, kr), (tvr, vr), (tkc, kb[q0 * row:]), (tvc, vb[q0 * row:])):
+                t.copy_(torch.from_numpy(a.view(np.int16)).to("cuda"))
+            ctx.step_write(step, sgq.StepState(q0, 0, 0, q0))
+            ctx.synchronize()
+            rec.graph.submit()
+            ctx.synchronize()
+            got = host(out).copy()
+            ctx.dispatch_blocking(k, B, push, [nkv, m, 1])
+            assert np.array_equal(got, host(out)), q0
+            want = oracle.attention(*(oracle.f16_bits_to_f32(x) for x in (q16, kb, vb)), m, q0, NQ,
+                                    nkv, hd, 1024, 0.0625)
+            _prefill_check(oracle.f16_bits_to_f32(got.view(np.uint16)).reshape(m, NQ, hd), want,
+                           f"graph replay q0={q0}")
+            torch.randn(1024, device="cuda").sum().item()  # unrelated eager work
+    finally:
+        ctx.set_stream(None)
