@@ -489,3 +489,45 @@ def test_prefill_ring_graph_replay_with_step_q0(ctx, oracle):
             torch.randn(1024, device="cuda").sum().item()  # unrelated eager work
     finally:
         ctx.set_stream(None)
+
+
+def test_chunked_sliding_prefill_attend_then_append(ctx, oracle):
+    """The sliding layer's prefill order in record_prefill_layer
+    (graph.rs:1176-1190): per chunk, attn_prefill_sliding_ring over the ring
+    as it stands before the chunk's append plus the chunk's own pages, then
+    kv_append_sliding of the chunk's K and V.  Three chunks of 400 tokens
+    (the ring wraps during the third); every chunk's rows, on sampled query
+    heads, against the oracle over the linear positions at the prefill bar."""
+    import sgq
+
+    hd, nkv, m, chunks = 256, 16, 400, 3
+    row = nkv * hd
+    rng = oracle.Rng(0xC4C)
+    total = m * chunks
+    kb = oracle.f32_to_f16_bits(rng.f32_vec(total * row))
+    vb = oracle.f32_to_f16_bits(rng.f32_vec(total * row))
+    kf, vf = oracle.f16_bits_to_f32(kb), oracle.f16_bits_to_f32(vb)
+    attn = ctx.load_kernel("attn_prefill_sliding_ring")
+    app = ctx.load_kernel("kv_append_sliding")
+    ring_k = torch.zeros(RING * row, dtype=torch.int16, device="cuda")
+    ring_v = torch.zeros(RING * row, dtype=torch.int16, device="cuda")
+    out = empty(m * NQ * hd, torch.int16)
+    B = sgq.BufferBinding.buffer
+    for c in range(chunks):
+        q0 = c * m
+        print(f"chunked sliding prefill chunk {c} q0={q0}", flush=True)
+        q16 = oracle.f32_to_f16_bits(rng.f32_vec(m * NQ * hd))
+        ck, cv = dev(kb[q0 * row:(q0 + m) * row]), dev(vb[q0 * row:(q0 + m) * row])
+        step = _step(ctx, q0, 0, 0, q0)
+        ctx.dispatch(attn, [B(0, dev(q16)), B(1, ring_k), B(2, ring_v), B(3, ck), B(4, cv), B(5, out),
+                            B(6, step)], struct.pack("<f", 0.0625), [nkv, m, 1])
+        groups = [m * row // 256, 1, 1]
+        ctx.dispatch(app, [B(0, ck), B(1, ring_k), B(2, step)], b"", groups)
+        ctx.dispatch_blocking(app, [B(0, cv), B(1, ring_v), B(2, step)], b"", groups)
+        got = oracle.f16_bits_to_f32(host(out, np.uint16)).reshape(m, NQ, hd)
+        qf = oracle.f16_bits_to_f32(q16)
+        heads = [0, 9, 22, 23]  # sampled query heads (23: the second of kv head 11)
+        want = np.stack([np.stack([oracle.attention_head(qf, kf, vf, i, h, NQ, nkv, hd, 0.0625,
+                                                         max(0, q0 + i + 1 - 1024), q0 + i)
+                                   for h in heads]) for i in range(m)])
+        _prefill_check(got[:, heads], want, f"chunk {c}")
