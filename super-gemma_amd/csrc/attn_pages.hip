@@ -262,30 +262,65 @@ __global__ __launch_bounds__(HD * 2) void attn_decode_pages_kernel(
 
 // The split merge (attn_reduce.wgsl:33-56 folds the splits in order with a
 // running max; the same sum, weighted by exp(m_s - max over all splits)):
-// out = f16(sum_s e^(m_s - M)·acc_s / sum_s e^(m_s - M)·l_s).  The global
-// max first, then independent weighted loads.  One 256-thread workgroup per
-// query head.
+// out = f16(sum_s e^(m_s - M)·acc_s / sum_s e^(m_s - M)·l_s).  One 256-thread
+// workgroup per query head: wave 0 loads every split's (m, l) at once (a
+// lane per split, up to 64 at a time), takes the max over the wave and
+// leaves the weights in LDS; then every thread folds its dims over the
+// splits in order, all loads of a batch of 16 issued together.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_reduce_pages_kernel(const float *__restrict__ part,
                                                                  int n_splits,
                                                                  uint16_t *__restrict__ out) {
     constexpr int ND = HD / 256, stride = HD + 2;
-    const int h = blockIdx.x, tid = threadIdx.x;
+    __shared__ float w_s[64];
+    __shared__ float l_s[1];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const float *ph = part + (size_t)h * n_splits * stride;
-    float m = kPNegBig;
-#pragma unroll 8
-    for (int s = 0; s < n_splits; s++) m = fmaxf(m, ph[(size_t)s * stride + HD]);
-    float l = 0.f, acc[ND];
+    float acc[ND];
 #pragma unroll
     for (int e = 0; e < ND; e++) acc[e] = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < n_splits; s++) {
-        const float *pr = ph + (size_t)s * stride;
-        const float w = expf(pr[HD] - m);
-        l = __builtin_fmaf(w, pr[HD + 1], l);
+    float M = kPNegBig;  // wave 0: the max over all splits so far (chunks of 64)
+    float lsum = 0.f;
+    for (int s0 = 0; s0 < n_splits; s0 += 64) {
+        const int cnt = min(64, n_splits - s0);
+        if (tid < 64) {
+            const float m = lane < cnt ? ph[(size_t)(s0 + lane) * stride + HD] : kPNegBig;
+            const float l = lane < cnt ? ph[(size_t)(s0 + lane) * stride + HD + 1] : 0.f;
+            float mx = m;
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+            const float Mn = fmaxf(M, mx);
+            const float r = expf(M - Mn);  // rescale of the chunks before
+            const float w = lane < cnt ? expf(m - Mn) : 0.f;
+            float lw = w * l;
+            for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o, kWave);
+            lsum = lsum * r + lw;
+            M = Mn;
+            w_s[lane] = w;
+            if (lane == 0) l_s[0] = r;
+        }
+        __syncthreads();
+        const float r = l_s[0];
 #pragma unroll
-        for (int e = 0; e < ND; e++) acc[e] = __builtin_fmaf(w, pr[tid * ND + e], acc[e]);
+        for (int e = 0; e < ND; e++) acc[e] *= r;
+        for (int b = 0; b < cnt; b += 16) {
+            float v[16][ND];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+#pragma unroll
+                for (int e = 0; e < ND; e++)
+                    v[u][e] = b + u < cnt ? ph[(size_t)(s0 + b + u) * stride + tid * ND + e] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const float w = b + u < cnt ? w_s[b + u] : 0.f;
+#pragma unroll
+                for (int e = 0; e < ND; e++) acc[e] = __builtin_fmaf(w, v[u][e], acc[e]);
+            }
+        }
+        __syncthreads();  // w_s rewritten by the next chunk
     }
+    if (tid == 0) l_s[0] = lsum;
+    __syncthreads();
+    const float l = l_s[0];
 #pragma unroll
     for (int e = 0; e < ND; e++)
         out[(size_t)h * HD + tid * ND + e] = __builtin_bit_cast(uint16_t, (_Float16)(acc[e] / l));
