@@ -802,8 +802,10 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             uint32_t n_splits;
             std::memcpy(&n_splits, push, 4);
             const uint32_t hd = kernel->k;
-            if (n_splits == 0 || groups[0] != kRealNQ || groups[1] != 1 || groups[2] != 1)
-                return fail(SGQ_ERR_VALIDATION, "%s: groups must be [%u, 1, 1], n_splits > 0",
+            if (n_splits == 0 || n_splits > 65535 || groups[0] != kRealNQ || groups[1] != 1 ||
+                groups[2] != 1)
+                return fail(SGQ_ERR_VALIDATION,
+                            "%s: groups must be [%u, 1, 1], 0 < n_splits <= 65535",
                             kernel->name.c_str(), kRealNQ);
             if ((r0 && r0 < (uint64_t)kRealNQ * n_splits * (hd + 2) * 4) ||
                 (r1 && r1 < (uint64_t)kRealNQ * hd * 2))

@@ -76,6 +76,9 @@ def _decode(ctx, kind, tq, kbind, tv, step, splits, scale):
     ("sliding", 1024, 16), ("sliding", 333, 5), ("sliding", 1, 1), ("sliding", 7, 16),
     ("global", 4096, 32), ("global", 100, 32), ("global", 65, 3),
     ("global_q8k", 4096, 32), ("global_q8k", 2000, 32), ("global_q8k", 1, 1),
+    # more splits than the merge reads per pass (64): chunks rescaled to a
+    # running max, a ragged last chunk, empty splits at the end
+    ("sliding", 1024, 130), ("global", 4096, 200),
 ])
 def test_decode_pages_by_name_matches_oracle(ctx, oracle, kind, kv_len, splits):
     hd, nkv, word = GEOM[kind]
@@ -241,6 +244,10 @@ def test_pages_names_validate_groups_and_ranges(ctx):
     with pytest.raises(sgq.ValidationError):  # out too small for hd256 rows
         ctx.dispatch(red, _bind(sgq, part, empty(NQ * 128, torch.int16)),
                      struct.pack("<I", 4), [NQ, 1, 1])
+    for bad in (0, 70000):  # split counts past the decode grid's limit
+        with pytest.raises(sgq.ValidationError):
+            ctx.dispatch(red, _bind(sgq, part, empty(NQ * 256, torch.int16)),
+                         struct.pack("<I", bad), [NQ, 1, 1])
     app = ctx.load_kernel("kv_append_sliding")
     with pytest.raises(sgq.ValidationError):  # a partial row
         ctx.dispatch(app, _bind(sgq, empty(100, torch.int16), kv, step), b"", [1, 1, 1])
