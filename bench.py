@@ -314,6 +314,90 @@ class AttnPages:
         }
 
 
+class AttnPrefillPages:
+    """The released checkpoint's prefill attention by name, as the
+    reference's record_prefill_layer dispatches it (crates/sg-model/src/
+    graph.rs:1176-1225) for a 4096-token prompt from position 0 (q0 =
+    step[3] = 0): attn_prefill_global_flash_sp_iq (int8 q with f16 scales,
+    Q8_0 K, f16 V, head_dim 512, 4 kv heads, causal; groups [32, M/16, 1]) or
+    attn_prefill_sliding_ring (f16 q / K / V, head_dim 256, 16 kv heads,
+    window 1024: the ring holds the slots before the chunk, the chunk's own
+    K/V come from its pages; groups [16, M, 1]).  One dispatch per step,
+    replayed from a graph."""
+    kernel = "attn_prefill_wide_kernel"
+
+    def __init__(self, ctx, torch, kind="global_flash_sp_iq", n_tok=4096):
+        import struct
+        import sgq
+
+        self.ctx, self.kind, self.n_tok = ctx, kind, n_tok
+        n_q = 32
+        if kind == "sliding_ring":
+            hd, n_kv, window, scale = 256, 16, 1024, 1.0 / (256 ** 0.5)
+        else:
+            hd, n_kv, window, scale = 512, 4, 0, 1.0
+        self.hd, self.n_kv, self.window = hd, n_kv, window
+        row = n_kv * hd
+        f = torch.empty(n_tok * max(n_q * hd, row), dtype=torch.float32, device="cuda")
+
+        def normal(n, seed):
+            ctx.fill_normal(f[:n], seed=seed)
+            return f[:n]
+
+        step = torch.zeros(8, dtype=torch.int32, device="cuda")
+        ctx.step_write(step, sgq.StepState(0, 0, 0, 0))
+        out = torch.empty(n_tok * n_q * hd, dtype=torch.int16, device="cuda")
+        if kind == "sliding_ring":
+            q16 = normal(n_tok * n_q * hd, 70).half().view(torch.int16)
+            ring_k = torch.zeros(1024 * row, dtype=torch.int16, device="cuda")
+            ring_v = torch.zeros_like(ring_k)
+            ck = normal(n_tok * row, 71).half().view(torch.int16)
+            cv = normal(n_tok * row, 72).half().view(torch.int16)
+            binds = [q16, ring_k, ring_v, ck, cv, out, step]
+            groups = [n_kv, n_tok, 1]
+        else:
+            qq = torch.empty(n_tok * n_q * hd, dtype=torch.int8, device="cuda")
+            qs = torch.empty(qq.numel() // 32, dtype=torch.int16, device="cuda")
+            ctx.quant_q8_0(normal(qq.numel(), 73), qs, qq)
+            kq = torch.empty(n_tok * row, dtype=torch.int8, device="cuda")
+            ks = torch.empty(kq.numel() // 32, dtype=torch.int16, device="cuda")
+            ctx.quant_q8_0(normal(kq.numel(), 74), ks, kq)
+            v16 = normal(n_tok * row, 75).half().view(torch.int16)
+            binds = [qq, qs, kq, ks, v16, out, step]
+            groups = [n_q, n_tok // 16, 1]
+        del f
+        self._keep = binds
+        torch.cuda.synchronize()
+        self.stream = torch.cuda.Stream()
+        ctx.set_stream(self.stream)
+        k = ctx.load_kernel(f"attn_prefill_{kind}")
+        with sgq.GraphRecorder(ctx) as rec:
+            ctx.dispatch(k, [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(binds)],
+                         struct.pack("<f", scale), groups)
+        self.graph = rec.graph
+        pairs = sum(min(i + 1, window) if window else i + 1 for i in range(n_tok))
+        self.flops = 4.0 * hd * n_q * pairs  # QK^T and PV, 2 flops per MAC
+
+    def step(self, i):
+        self.graph.submit()
+
+    def result(self, ms_per_step):
+        tf = self.flops / (ms_per_step * 1e-3) / 1e12
+        iq = self.kind != "sliding_ring"
+        return {
+            "value": tf, "unit": "TFLOP/s",
+            "dtype": ("int8 q / Q8_0 K as exact f16 on the f16 MFMA (block dots scaled), f16 V"
+                      if iq else "f16 q / K / V") + "; fp32 acc, f16 out",
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tf / F16_PEAK_TFLOPS, "traffic": None},
+            "config": {"workload": f"attn_prefill_{self.kind} by name, {self.n_tok} queries "
+                                   f"from position 0, 32 q / {self.n_kv} kv heads, head_dim "
+                                   f"{self.hd}, " + (f"window {self.window}" if self.window
+                                                     else "causal"),
+                       "flops_per_launch": self.flops},
+        }
+
+
 class HeadQ6K:
     """The Q6_K tied LM head of the real checkpoint (gemv_q6_k_logits.wgsl):
     262144 vocabulary rows x K=5376, rows padded to 4416 bytes, 30*tanh
@@ -759,7 +843,8 @@ def main():
                              "attn_prefill_ipv",
                              "attn_prefill_sliding", "attn_decode_4k", "attn_decode_32k",
                              "attn_decode_128k", "head_q6k", "attn_pages_sliding",
-                             "attn_pages_q8k_4k", "attn_pages_q8k_8k", "attn_pages_q8k_32k"])
+                             "attn_pages_q8k_4k", "attn_pages_q8k_8k", "attn_pages_q8k_32k",
+                             "attn_prefill_pages_iq", "attn_prefill_pages_sliding"])
     ap.add_argument("--split-k", type=int, default=4, choices=[1, 2, 4, 8],
                     help="splitk workload: K split (BASELINE config 3 sweeps 1/2/4/8)")
     ap.add_argument("--gemv-rows", type=int, default=21504,
@@ -802,6 +887,10 @@ def main():
         wl = AttnPrefill(ctx, torch, ipv=True)
     elif args.workload == "attn_prefill_sliding":
         wl = AttnPrefill(ctx, torch, window=1024)
+    elif args.workload == "attn_prefill_pages_iq":
+        wl = AttnPrefillPages(ctx, torch, "global_flash_sp_iq")
+    elif args.workload == "attn_prefill_pages_sliding":
+        wl = AttnPrefillPages(ctx, torch, "sliding_ring")
     elif args.workload == "attn_pages_sliding":
         wl = AttnPages(ctx, torch, "sliding", 1024)
     elif args.workload.startswith("attn_pages_q8k_"):
