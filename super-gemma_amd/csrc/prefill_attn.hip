@@ -1003,16 +1003,19 @@ __global__ __launch_bounds__(512) void attn_prefill_wide_kernel(
         {
             const int kb = kl;
             const bool full = kb + 31 <= wq_lo && (window <= 0 || kb > wq_lo + 31 - window);
-            float mx = m_run;
+            // the mask as one uniform branch (inside the max loop it became a
+            // taken branch per element on every unmasked tile)
+            if (!full) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                if (!full) {
+                for (int i = 0; i < 16; i++) {
                     const int key = kb + 8 * (i / 4) + 4 * hh + (i % 4);
                     const bool ok = q_valid && key <= qp && (window <= 0 || key > qp - window);
                     s[i] = ok ? s[i] : kNegBig;
                 }
-                mx = fmaxf(mx, s[i]);
             }
+            float mx = m_run;
+#pragma unroll
+            for (int i = 0; i < 16; i++) mx = fmaxf(mx, s[i]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
             if (!(mx > m_run + 8.0f)) mx = m_run;
             const float corr = __builtin_amdgcn_exp2f(m_run - mx);
