@@ -60,6 +60,73 @@ def test_config5_decode_8k_matches_oracle(ctx, oracle):
     model.close()
 
 
+class _side_stream:
+    """Graph capture needs a non-null stream: run the block on a side one."""
+
+    def __init__(self, ctx):
+        self.ctx, self.s = ctx, torch.cuda.Stream()
+
+    def __enter__(self):
+        self.ctx.set_stream(self.s)
+        return self.s
+
+    def __exit__(self, *exc):
+        self.ctx.synchronize()
+        self.ctx.set_stream(None)
+
+
+@pytest.mark.timeout(600)
+def test_config5_fused_graph_decode_8k_matches_oracle(ctx, oracle):
+    """The benchmarked path itself: decode mode 2 (fused GEMV prologues and
+    epilogues, 16-split attention with its merges), replayed as one hipGraph
+    per step on a side stream, 62 layers over an 8192-slot context; three
+    steps at full logits width against the oracle."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print("config 5: 62 layers, fused hipGraph decode at 8K vs oracle", flush=True)
+    cfg = _cfg5(sgq, max_ctx=8200)
+    with _side_stream(ctx):
+        model = sgq.Model(ctx, cfg)
+        model.decode_mode = 2
+        model.fill_cache(8192)
+        ctx.synchronize()
+        ref = _oracle(OracleDecoder, model, cfg)
+        ref.preload_cache(_pages(model, cfg.n_layers), 8192)
+        logits = empty(cfg.vocab, torch.float32)
+        for i, t in enumerate([262143, 4242, 17]):
+            model.decode(t, logits, graph=True)
+            ctx.synchronize()
+            print(f"  step {i}: oracle", flush=True)
+            _check_logits(host(logits), ref.decode(t), f"config 5 fused graph step {i}")
+        model.close()
+
+
+@pytest.mark.timeout(600)
+def test_config5_fused_graph_after_prefill_matches_oracle(ctx, oracle):
+    """A 12-token prefill through all 62 layers, then decode mode 2 as hipGraph
+    replays from the caches the prefill filled, against the oracle."""
+    import sgq
+    from oracle.model import OraclePrefill
+
+    print("config 5: 62 layers, prefill then fused hipGraph decode vs oracle", flush=True)
+    cfg = _cfg5(sgq, max_ctx=64)
+    with _side_stream(ctx):
+        model = sgq.Model(ctx, cfg)
+        ref = _oracle(OraclePrefill, model, cfg)
+        toks = np.random.default_rng(56).integers(0, cfg.vocab, 12)
+        logits = empty(cfg.vocab, torch.float32)
+        model.prefill(toks, logits)
+        ctx.synchronize()
+        _check_logits(host(logits), ref.prefill(toks), "config 5 prefill (fused run)")
+        model.decode_mode = 2
+        for i, t in enumerate([99, 262000]):
+            model.decode(t, logits, graph=True)
+            ctx.synchronize()
+            _check_logits(host(logits), ref.decode(t), f"config 5 fused graph after prefill {i}")
+        model.close()
+
+
 @pytest.mark.timeout(600)
 def test_config5_prefill_matches_oracle_then_decodes(ctx, oracle):
     import sgq
