@@ -11,8 +11,17 @@
  *     Variant names, binding order, push-constant layout and group counts are
  *     the reference's (crates/sg-gpu/build.rs VARIANTS), so a forward graph
  *     that records `load_kernel(name)` + `dispatch(...)` drives this library
- *     unchanged.  Activation buffers hold fp32 where the reference held f16;
- *     Q4_0 weights and Q8_0 pages are byte-identical formats.
+ *     unchanged.  Under the reference's names, activation buffers hold f16
+ *     as the reference's shaders bind them (gemv_q4_0.wgsl:18-19,
+ *     rmsnorm.wgsl:14-16, rope.wgsl:26, geglu.wgsl:7-9, add_scaled.wgsl:12-14,
+ *     gemm_q4_0_i8.wgsl:63, kv_quant_q8.wgsl:24, kv_dequant_q8.wgsl:11,
+ *     kv_append_global_q8.wgsl:19, kv_append_global_v_q8.wgsl:20,
+ *     gemv_q6_k_logits.wgsl:19); the same kernel over fp32 activations is
+ *     NAME_f32 (e.g. gemv_q4_0_k5376_f32, rmsnorm_5376_f32, geglu_f32,
+ *     gemm_q4_0_i8_bb_pfd4_f32).  Families with no reference counterpart
+ *     (the head_dim-128 attention and RoPE forms, kv_append_sliding_q8, the
+ *     split-K MMQ) take fp32 and no suffix.  Q4_0 weights and Q8_0 pages are
+ *     byte-identical formats.
  *
  *  2. Typed entry points (sgq_gemv_q4_0, sgq_gemm_q4_0_q8, ...) that compute
  *     their own launch geometry; the name dispatch routes to the same code.
@@ -84,8 +93,10 @@ typedef struct {
  * crates/sg-model/src/graph.rs:560-656, at this build's geometry: Q8_0 K and
  * V pages, head_dim 128, 32 query / 16 kv heads, window and ring 1024):
  *   kv_append_global_q8 / kv_append_sliding_q8
- *       0 src fp32 [n_tok × 2048], 1 scales, 2 quants, 3 step; slot =
- *       step[0] + t (global) or (step[0] + t) % 1024 (sliding)
+ *       0 src [n_tok × ROW] (f16 for kv_append_global_q8, fp32 for its
+ *       _f32 form and for kv_append_sliding_q8; whole rows), 1 scales,
+ *       2 quants, 3 step; slot = step[0] + t (global) or (step[0] + t) % 1024
+ *       (sliding); ROW = groups.y·32 when groups.y > 1, else 2048
  *   attn_decode_global_q8_hd128 / attn_decode_sliding_q8_hd128
  *       0 q, 1 k_quants, 2 k_scales, 3 v_quants, 4 v_scales, 5 part, 6 step;
  *       push {n_splits: u32, scale: f32}; groups [16, n_splits, 1];
@@ -101,7 +112,10 @@ typedef struct {
  *       0 q, 1..4 ring K/V pages, 5..8 chunk K/V pages, 9 out, 10 step;
  *       push f32 scale; groups [16, M, 1]  (attn_prefill_sliding_ring.wgsl:28-40)
  *   kv_append_global_v_q8  (kv_append_global_v_q8.wgsl:19-25)
- *       0 src fp32, 1 key-blocked scales, 2 quants, 3 step (pos = step[0])
+ *       0 src f16 (fp32 for _f32) [n_tok × ROW], whole rows, 1 key-blocked
+ *       scales [ceil(n_tok/32) × ROW], 2 quants [n_tok × ROW], 3 step
+ *       (pos = step[0], a multiple of 32); ROW = groups.y·32 when
+ *       groups.y > 1, else 2048
  *   attn_prefill_global_flash_ipv_hd128  (attn_prefill_global_flash_sp_ipv.wgsl:24-35)
  *       0 q fp32, 1 k_quants, 2 k_scales, 3 v_quants, 4 key-blocked v_scales,
  *       5 out, 6 step; push f32 scale; groups [32, ceil(M/16), 1]

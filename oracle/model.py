@@ -116,6 +116,11 @@ class OracleDecoder:
         cap = np.float64(c["final_softcap"])
         return (cap * np.tanh(logits.astype(np.float64) / cap)).astype(np.float32)
 
+    def _embed(self, token: int) -> np.ndarray:
+        """The residual row a decode step starts from (reference.rs:163-172)."""
+        row = self._embed_rows([token])[0]
+        return (row * np.float32(math.sqrt(self.c["hidden"]))).astype(np.float32)
+
     # host threads of the row-parallel matmul (results do not depend on it)
     threads = 8
 
@@ -130,36 +135,46 @@ class OracleDecoder:
         s, q = O.quant_q8_0(row)
         return O.dequant_q8_0(s, q)
 
+    def _act(self, x):
+        """Storage of an activation buffer between two operators: fp32 here
+        (reference.rs); F16Graph rounds to f16 as the GPU graph's buffers do."""
+        return x
+
+    def _cache_rows(self, layer, k, v):
+        """The K/V rows a layer's cache holds for the new position: Q8_0 round
+        trips of both (the page format the oracle's caches model)."""
+        return self._q8_round_trip(k), self._q8_round_trip(v)
+
     def decode(self, token: int) -> np.ndarray:
         c, w = self.c, self.w
         H, F = c["hidden"], c["ffn"]
         nq = c["n_q_heads"]
         eps = c["eps"]
-        row = self._embed_rows([token])[0]
-        x = (row * np.float32(math.sqrt(H))).astype(np.float32)
+        x = self._embed(token)
         pos = self.pos
+        A = self._act
         for l in range(c["n_layers"]):
             glob = self.is_global(l)
             hd, nkv = self.geometry(l)
-            xn = O.rmsnorm(x, w[("attn_norm", l)], H, eps)
-            q = self._lin("attn_q", l, xn, nq * hd)
-            k_proj = self._lin("attn_k", l, xn, nkv * hd)
+            xn = A(O.rmsnorm(x, w[("attn_norm", l)], H, eps))
+            q = A(self._lin("attn_q", l, xn, nq * hd))
+            k_proj = A(self._lin("attn_k", l, xn, nkv * hd))
             if glob and c["global_k_eq_v"]:
                 v = k_proj.copy()
             else:
-                v = self._lin("attn_v", l, xn, nkv * hd)
+                v = A(self._lin("attn_v", l, xn, nkv * hd))
             if glob:
                 cs = O.cos_sin_table([pos], hd, c["rope_theta_global"], self.global_factors)
             else:
                 cs = O.cos_sin_table([pos], hd, c["rope_theta_sliding"])
-            q = O.rmsnorm(q, w[("attn_q_norm", l)], hd, eps)
-            q = O.rope(q, hd, hd, nq, cs)
-            k = O.rmsnorm(k_proj, w[("attn_k_norm", l)], hd, eps)
-            k = O.rope(k, hd, hd, nkv, cs)
-            v = O.rmsnorm(v, None, hd, eps)
+            q = A(O.rmsnorm(q, w[("attn_q_norm", l)], hd, eps))
+            q = A(O.rope(q, hd, hd, nq, cs))
+            k = A(O.rmsnorm(k_proj, w[("attn_k_norm", l)], hd, eps))
+            k = A(O.rope(k, hd, hd, nkv, cs))
+            v = A(O.rmsnorm(v, None, hd, eps))
             if self.taps is not None:
                 self.taps[("k_rope", l)], self.taps[("v_norm", l)] = k, v
-            kr, vr = self._q8_round_trip(k), self._q8_round_trip(v)
+            kr, vr = self._cache_rows(l, k, v)
             if self.kv_source is not None:
                 kr, vr = self.kv_source(l, pos, kr, vr)
             self.k_cache[l].append(kr)
@@ -167,21 +182,41 @@ class OracleDecoder:
             ck = np.concatenate(self.k_cache[l])
             cv = np.concatenate(self.v_cache[l])
             window = None if glob else c["sliding_window"]
-            a = O.attention(q, ck, cv, 1, pos, nq, nkv, hd, window, c["attn_scale"]).reshape(-1)
-            o = self._lin("attn_output", l, a, H)
-            o = O.rmsnorm(o, w[("post_attention_norm", l)], H, eps)
-            x = (x + o).astype(np.float32)
-            fn = O.rmsnorm(x, w[("ffn_norm", l)], H, eps)
-            g = self._lin("ffn_gate", l, fn, F)
-            u = self._lin("ffn_up", l, fn, F)
-            h = O.geglu(g, u)
-            f = self._lin("ffn_down", l, h, H)
-            f = O.rmsnorm(f, w[("post_ffw_norm", l)], H, eps)
+            a = A(O.attention(q, ck, cv, 1, pos, nq, nkv, hd, window, c["attn_scale"]).reshape(-1))
+            o = A(self._lin("attn_output", l, a, H))
+            o = A(O.rmsnorm(o, w[("post_attention_norm", l)], H, eps))
+            x = A((x + o).astype(np.float32))
+            fn = A(O.rmsnorm(x, w[("ffn_norm", l)], H, eps))
+            g = A(self._lin("ffn_gate", l, fn, F))
+            u = A(self._lin("ffn_up", l, fn, F))
+            h = A(O.geglu(g, u))
+            f = A(self._lin("ffn_down", l, h, H))
+            f = A(O.rmsnorm(f, w[("post_ffw_norm", l)], H, eps))
             x = (x + f).astype(np.float32)
-            x = (x * w[("layer_output_scale", l)][0]).astype(np.float32)
+            x = A((x * w[("layer_output_scale", l)][0]).astype(np.float32))
+            if self.taps is not None:
+                self.taps[("x_layer", l)] = x
         self.pos += 1
         xf = O.rmsnorm(x, w[("output_norm", -1)], H, eps)
         return self._head(xf)
+
+
+class F16Graph(OracleDecoder):
+    """The decode forward as the reference's GPU graph stores it
+    (crates/sg-model/src/graph.rs:478-729): every activation buffer between
+    two operators is f16 (graph.rs:282-313), so each operator's fp32 result
+    is rounded to f16 before the next reads it; the caches hold K and V as
+    record_layer appends them: f16 rows on sliding layers, Q8_0 K and f16 V
+    on global layers (graph.rs:581-611).  Operators themselves are the
+    oracle's (f32/f64, reference.rs)."""
+
+    def _act(self, x):
+        return O.through_f16(x)
+
+    def _cache_rows(self, layer, k, v):
+        if self.is_global(layer):
+            return self._q8_round_trip(k), v.copy()
+        return k.copy(), v.copy()
 
 
 class OraclePrefill(OracleDecoder):

@@ -102,6 +102,9 @@ struct sgq_kernel {
     sgq_kernel_info info;
     uint32_t k = 0, n = 0;  // baked dims (0 = from push/bindings)
     uint32_t param = 0;     // split factor, ring length, ...
+    // activation type: f16 (the reference's) under the reference's names,
+    // fp32 under the same names with the suffix _f32
+    bool f16 = false;
 };
 
 namespace {
@@ -133,6 +136,13 @@ const char *const kNames[] = {
     "attn_prefill_global_flash", "attn_prefill_global_flash_sp", "attn_prefill_global_flash_sp_q8",
     "attn_prefill_global_flash_sp_iq", "attn_prefill_global_flash_sp_ipv",
     "attn_prefill_global_flash_sp_ipv_bcast",
+    // the same kernels over fp32 activations
+    "gemv_q4_0_k5376_f32", "gemv_q4_0_k8192_f32", "gemv_q4_0_k16384_f32", "gemv_q4_0_k21504_f32",
+    "gemv_q4_0_k4096_f32", "gemv_q4_0_generic_f32", "kv_quant_q8_f32", "kv_dequant_q8_f32",
+    "kv_append_global_q8_f32", "kv_append_global_v_q8_f32",
+    "gemm_q4_0_i8_swz_m4n1_k5376_n21504_f32", "gemm_q4_0_i8_bb_pfd4_f32",
+    "rmsnorm_5376_f32", "rmsnorm_256_f32", "rmsnorm_512_f32", "rope_sliding_q_f32",
+    "rope_global_q_f32", "geglu_f32", "add_scaled_f32", "gemv_q6_k_logits_f32",
 };
 
 // The benchmark geometry of the hd128 attention forms (32 query heads over
@@ -199,8 +209,9 @@ bool parse_u32_after(const std::string &s, const std::string &key, uint32_t *out
 
 bool starts_with(const std::string &s, const char *p) { return s.rfind(p, 0) == 0; }
 
-// Build the registry entry for `name`, or return false if it is unknown.
-bool resolve(const std::string &name, sgq_kernel *k) {
+// Build the registry entry for `name` (without an _f32 suffix), or return
+// false if it is unknown.
+bool resolve_base(const std::string &name, sgq_kernel *k) {
     k->name = name;
     k->info = {{64, 1, 1}, 0, 0, 0};
     if (starts_with(name, "gemv_q4_0_")) {
@@ -237,7 +248,7 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         return true;
     }
     if (name == "kv_append_global_v_q8") {
-        // bindings: 0 src fp32 [n_tok × row], 1 scales f16 [block × row],
+        // bindings: 0 src f16 (fp32: _f32) [n_tok × row], 1 scales f16 [block × row],
         // 2 quants [slot × row], 3 step (pos = step[0], a multiple of 32);
         // row = groups.y·32 when groups.y > 1, else 2048 (16 kv heads × 128,
         // also the real checkpoint's 4 global kv heads × 512)
@@ -397,6 +408,39 @@ bool resolve(const std::string &name, sgq_kernel *k) {
         return k->k % 64 == 0 && k->n > 0;
     }
     return false;
+}
+
+// Kernels that exist for both activation types: the reference's names
+// take f16 activations as its shaders do; NAME_f32 is the same kernel over
+// fp32 activations.  The families of our own (head_dim-128 forms, the
+// split-K MMQ, the ring Q8 append) are fp32 only and take no suffix.
+bool dual_type(const sgq_kernel &k) {
+    switch (k.kind) {
+        case Kind::Gemv:
+        case Kind::GemvQ6kLogits:
+        case Kind::RmsNorm:
+        case Kind::Geglu:
+        case Kind::AddScaled:
+        case Kind::QuantQ8:
+        case Kind::DequantQ8:
+        case Kind::GemmI8:
+        case Kind::GemmI8Down:
+        case Kind::AppendVQ8: return true;
+        case Kind::Rope: return k.k != 128;
+        case Kind::AppendQ8: return k.param == 0;  // kv_append_global_q8
+        default: return false;
+    }
+}
+
+bool resolve(const std::string &full, sgq_kernel *k) {
+    static const std::string sfx = "_f32";
+    const bool f32 = full.size() > sfx.size() &&
+                     full.compare(full.size() - sfx.size(), sfx.size(), sfx) == 0;
+    if (!resolve_base(f32 ? full.substr(0, full.size() - sfx.size()) : full, k)) return false;
+    k->name = full;
+    if (!dual_type(*k)) return !f32;
+    k->f16 = !f32;
+    return true;
 }
 
 struct Registry {
@@ -565,27 +609,34 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             uint32_t k = kernel->k;
             if (!k) std::memcpy(&k, push, 4);
             const uint32_t n = groups[0];
+            const uint64_t es = kernel->f16 ? 2 : 4;
             if (r0 && r0 < (uint64_t)n * (k / 32) * 18)
                 return fail(SGQ_ERR_VALIDATION, "%s: weights binding too small", kernel->name.c_str());
-            if (r1 && r1 < (uint64_t)k * 4)
+            if (r1 && r1 < (uint64_t)k * es)
                 return fail(SGQ_ERR_VALIDATION, "%s: x binding too small", kernel->name.c_str());
-            if (r2 && r2 < (uint64_t)n * 4)
+            if (r2 && r2 < (uint64_t)n * es)
                 return fail(SGQ_ERR_VALIDATION, "%s: y binding too small", kernel->name.c_str());
+            if (kernel->f16)
+                return launch_gemv_q4_0(st, p0, static_cast<const uint16_t *>(p1),
+                                        static_cast<uint16_t *>(p2), n, k, ctx->workspace);
             return launch_gemv_q4_0(st, p0, static_cast<const float *>(p1), static_cast<float *>(p2),
                                     n, k, ctx->workspace);
         }
         case Kind::GemvQ6kLogits: {
-            // bindings: 0 padded Q6_K rows, 1 x (fp32 here; f16 in the
-            // reference), 2 logits; groups [N, 1, 1] (one per vocabulary row)
+            // bindings: 0 padded Q6_K rows, 1 x (f16; fp32 for the _f32
+            // form), 2 logits fp32; groups [N, 1, 1] (one per vocabulary row)
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
                 return rc;
             const uint32_t n = groups[0];
             if (r0 && r0 < (uint64_t)n * kernel->param)
                 return fail(SGQ_ERR_VALIDATION, "%s: weights binding too small", kernel->name.c_str());
-            if (r1 && r1 < (uint64_t)kernel->k * 4)
+            if (r1 && r1 < (uint64_t)kernel->k * (kernel->f16 ? 2 : 4))
                 return fail(SGQ_ERR_VALIDATION, "%s: x binding too small", kernel->name.c_str());
             if (r2 && r2 < (uint64_t)n * 4)
                 return fail(SGQ_ERR_VALIDATION, "%s: logits binding too small", kernel->name.c_str());
+            if (kernel->f16)
+                return launch_gemv_q6_k(st, p0, kernel->param, static_cast<const uint16_t *>(p1),
+                                        static_cast<float *>(p2), n, kernel->k, 30.0f);
             return launch_gemv_q6_k(st, p0, kernel->param, static_cast<const float *>(p1),
                                     static_cast<float *>(p2), n, kernel->k, 30.0f);
         }
@@ -593,9 +644,13 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             // bindings: 0 x, 1 w, 2 y; one workgroup per row (groups[0] rows)
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
                 return rc;
-            const uint64_t need = (uint64_t)groups[0] * kernel->k * 4;
+            const uint64_t need = (uint64_t)groups[0] * kernel->k * (kernel->f16 ? 2 : 4);
             if ((r0 && r0 < need) || (r2 && r2 < need) || (r1 && r1 < (uint64_t)kernel->k * 4))
                 return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            if (kernel->f16)
+                return launch_rmsnorm(st, static_cast<const uint16_t *>(p0),
+                                      static_cast<const float *>(p1), static_cast<uint16_t *>(p2),
+                                      groups[0], kernel->k, (int)kernel->param, 1e-6f);
             return launch_rmsnorm(st, static_cast<const float *>(p0), static_cast<const float *>(p1),
                                   static_cast<float *>(p2), groups[0], kernel->k, (int)kernel->param,
                                   1e-6f);
@@ -605,10 +660,13 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             // [token × rot/2] (cos, sin); pairs = arrayLength(xs)/head_dim·rot/2
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1))) return rc;
             if (!r0) return fail(SGQ_ERR_VALIDATION, "%s: xs range required", kernel->name.c_str());
-            const uint64_t rows = r0 / 4 / kernel->k;
+            const uint64_t rows = r0 / (kernel->f16 ? 2 : 4) / kernel->k;
             const uint64_t tokens = (rows + kernel->n - 1) / kernel->n;
             if (r1 && r1 < tokens * (kernel->param / 2) * 8)
                 return fail(SGQ_ERR_VALIDATION, "%s: cos_sin binding too small", kernel->name.c_str());
+            if (kernel->f16)
+                return launch_rope(st, static_cast<uint16_t *>(p0), static_cast<const float *>(p1),
+                                   rows, kernel->k, kernel->param, kernel->n);
             return launch_rope(st, static_cast<float *>(p0), static_cast<const float *>(p1), rows,
                                kernel->k, kernel->param, kernel->n);
         }
@@ -618,9 +676,19 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
                 return rc;
             if (!r2) return fail(SGQ_ERR_VALIDATION, "%s: y range required", kernel->name.c_str());
-            const uint64_t n = r2 / 4;
-            if ((r0 && r0 < n * 4) || (r1 && r1 < n * 4))
+            const uint64_t es = kernel->f16 ? 2 : 4;
+            const uint64_t n = r2 / es;
+            if ((r0 && r0 < n * es) || (r1 && r1 < n * es))
                 return fail(SGQ_ERR_VALIDATION, "%s: binding too small", kernel->name.c_str());
+            if (kernel->f16) {
+                const auto *a = static_cast<const uint16_t *>(p0);
+                const auto *b = static_cast<const uint16_t *>(p1);
+                auto *y = static_cast<uint16_t *>(p2);
+                if (kernel->kind == Kind::Geglu) return launch_geglu(st, a, b, y, n);
+                float sc;
+                std::memcpy(&sc, push, 4);
+                return launch_add_scaled(st, a, b, y, n, sc);
+            }
             if (kernel->kind == Kind::Geglu)
                 return launch_geglu(st, static_cast<const float *>(p0), static_cast<const float *>(p1),
                                     static_cast<float *>(p2), n);
@@ -634,7 +702,14 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
                 return rc;
             if (!r0) return fail(SGQ_ERR_VALIDATION, "kv_quant_q8: src range required");
-            const uint64_t n = r0 / 4 / 32 * 32;
+            const uint64_t es = kernel->f16 ? 2 : 4;
+            const uint64_t n = r0 / es / 32 * 32;
+            if ((r1 && r1 < n / 32 * 2) || (r2 && r2 < n))
+                return fail(SGQ_ERR_VALIDATION, "%s: scales/quants binding too small",
+                            kernel->name.c_str());
+            if (kernel->f16)
+                return launch_quant_q8_0(st, static_cast<const uint16_t *>(p0),
+                                         static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2), n);
             return launch_quant_q8_0(st, static_cast<const float *>(p0), static_cast<uint16_t *>(p1),
                                      static_cast<int8_t *>(p2), n);
         }
@@ -643,6 +718,12 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)))
                 return rc;
             if (!r1) return fail(SGQ_ERR_VALIDATION, "kv_dequant_q8: quants range required");
+            if (r2 && r2 < r1 / 32 * 32 * (kernel->f16 ? 2 : 4))
+                return fail(SGQ_ERR_VALIDATION, "%s: out binding too small", kernel->name.c_str());
+            if (kernel->f16)
+                return launch_dequant_q8_0(st, static_cast<const uint16_t *>(p0),
+                                           static_cast<const int8_t *>(p1),
+                                           static_cast<uint16_t *>(p2), r1 / 32 * 32);
             return launch_dequant_q8_0(st, static_cast<const uint16_t *>(p0),
                                        static_cast<const int8_t *>(p1), static_cast<float *>(p2),
                                        r1 / 32 * 32);
@@ -656,8 +737,16 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                 (rc = B.get(3, &p3, &r3)))
                 return rc;
             const uint32_t row = groups[1] > 1 ? groups[1] * 32 : 2048;
-            if (!r0) return fail(SGQ_ERR_VALIDATION, "kv_append: src range required");
-            const uint32_t ntok = (uint32_t)(r0 / 4 / row);
+            const uint64_t es = kernel->f16 ? 2 : 4;
+            if (!r0 || r0 % (row * es))
+                return fail(SGQ_ERR_VALIDATION, "%s: src range must be whole rows of %u",
+                            kernel->name.c_str(), row);
+            const uint32_t ntok = (uint32_t)(r0 / es / row);
+            if (kernel->f16)
+                return launch_kv_append_q8(st, static_cast<const uint16_t *>(p0),
+                                           static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2),
+                                           static_cast<const uint32_t *>(p3), ntok, row,
+                                           kernel->param);
             return launch_kv_append_q8(st, static_cast<const float *>(p0),
                                        static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2),
                                        static_cast<const uint32_t *>(p3), ntok, row, kernel->param);
@@ -676,8 +765,12 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
                 return fail(SGQ_ERR_VALIDATION, "%s: groups.y must be %u", kernel->name.c_str(), n / 16);
             if (r1 && r1 < (uint64_t)m * k)
                 return fail(SGQ_ERR_VALIDATION, "%s: x binding too small for M=%u", kernel->name.c_str(), m);
-            if (r3 && r3 < (uint64_t)m * n * 4)
+            if (r3 && r3 < (uint64_t)m * n * (kernel->f16 ? 2 : 4))
                 return fail(SGQ_ERR_VALIDATION, "%s: y binding too small", kernel->name.c_str());
+            if (kernel->f16)
+                return launch_gemm_q4_0_q8(st, p0, static_cast<const int8_t *>(p1),
+                                           static_cast<const uint16_t *>(p2),
+                                           static_cast<uint16_t *>(p3), m, n, k);
             uint32_t split = 1;
             float *partials = nullptr;
             if (kernel->kind == Kind::GemmI8Split) {
@@ -695,9 +788,22 @@ int sgq_dispatch(sgq_ctx *ctx, const sgq_kernel *kernel, const sgq_binding *bind
             if ((rc = B.get(0, &p0, &r0)) || (rc = B.get(1, &p1, &r1)) || (rc = B.get(2, &p2, &r2)) ||
                 (rc = B.get(3, &p3, &r3)))
                 return rc;
+            // row = groups.y·32 when groups.y > 1, else 2048; src must hold
+            // whole rows; quants cover the appended rows and scales their
+            // 32-key blocks (from pos = step[0], a multiple of 32)
             const uint32_t row = groups[1] > 1 ? groups[1] * 32 : 2048;
-            if (!r0) return fail(SGQ_ERR_VALIDATION, "kv_append_global_v_q8: src range required");
-            const uint32_t ntok = (uint32_t)(r0 / 4 / row);
+            const uint64_t es = kernel->f16 ? 2 : 4;
+            if (!r0 || r0 % (row * es))
+                return fail(SGQ_ERR_VALIDATION, "%s: src range must be whole rows of %u",
+                            kernel->name.c_str(), row);
+            const uint32_t ntok = (uint32_t)(r0 / es / row);
+            if ((r1 && r1 < (uint64_t)(ntok + 31) / 32 * row * 2) || (r2 && r2 < (uint64_t)ntok * row))
+                return fail(SGQ_ERR_VALIDATION, "%s: scales/quants binding too small for %u rows",
+                            kernel->name.c_str(), ntok);
+            if (kernel->f16)
+                return launch_kv_append_v_q8(st, static_cast<const uint16_t *>(p0),
+                                             static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2),
+                                             static_cast<const uint32_t *>(p3), 0, ntok, row);
             return launch_kv_append_v_q8(st, static_cast<const float *>(p0),
                                          static_cast<uint16_t *>(p1), static_cast<int8_t *>(p2),
                                          static_cast<const uint32_t *>(p3), 0, ntok, row);

@@ -63,10 +63,10 @@ __device__ __forceinline__ void load_tile(uint32_t (&wv)[R][NBL][5], const uint8
 // per wave per tile.  Each lane quantizes its own blocks of x; the tile loop
 // is software-pipelined (the next tile's weights load while this one
 // computes).
-template <int NBL, int R>
+template <int NBL, int R, typename TX, typename TY>
 __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restrict__ W,
-                                                        const float *__restrict__ x,
-                                                        float *__restrict__ y, int n, int nb,
+                                                        const TX *__restrict__ x,
+                                                        TY *__restrict__ y, int n, int nb,
                                                         int S, int slice_blocks) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
                 for (int r = 1; r < R; r++)
                     if (lane == r) v = acc[r];
                 const int row = row0 + lane;
-                if (row < n) y[row] = v;
+                if (row < n) act_st(y, row, v);
             }
         } else {
             if (lane == 0) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
                 float v = 0.f;
                 for (int q = 0; q < S; q++) v += red[p * S + q][lane];
                 const int row = row0 + lane;
-                if (row < n) y[row] = v;
+                if (row < n) act_st(y, row, v);
             }
             __syncthreads();
         }
@@ -205,13 +205,14 @@ __device__ __forceinline__ void issue_slice(const GemvTargets &tg, uint8_t *slot
                                          kStreamPolicy);
 }
 
-// x (fp32, nb blocks of 32) -> limb table, one thread per block.
-// x limbs: 8 lanes per 32-block, one float4 each (limbs_block8).
-__global__ __launch_bounds__(256) void gemv_prep_x_kernel(const float *__restrict__ x,
+// x (fp32 or f16, nb blocks of 32) -> limb table: 8 lanes per 32-block,
+// four values each (limbs_block8).
+template <typename T>
+__global__ __launch_bounds__(256) void gemv_prep_x_kernel(const T *__restrict__ x,
                                                           BlockLimbs *__restrict__ xl, int nb) {
-    const int i = blockIdx.x * 256 + threadIdx.x;  // float4 index
+    const int i = blockIdx.x * 256 + threadIdx.x;  // index of 4 values
     if (i >= nb * 8) return;                         // whole 8-lane groups exit together
-    const float4 v = reinterpret_cast<const float4 *>(x)[i];
+    const float4 v = act_ld4(x, i);
     limbs_block8(v, i & 7, &xl[i >> 3]);
 }
 
@@ -219,7 +220,10 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
     int local;
     const int j = target_of(tg, row, &local);
     if (tg.softcap > 0.f) v = tg.softcap * tanhf(v / tg.softcap);
-    tg.y[j][local] = v;
+    if (tg.half_out)
+        act_st(reinterpret_cast<uint16_t *>(tg.y[j]), local, v);
+    else
+        tg.y[j][local] = v;
 }
 
 // LDS of the streamed kernel: the wave rings, then 64 B of row partials,
@@ -797,13 +801,14 @@ int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int
     return SGQ_OK;
 }
 
-template <int NBL, int R>
-int launch(hipStream_t st, const void *w, const float *x, float *y, int n, int nb, int S,
+template <int NBL, int R, typename TX, typename TY>
+int launch(hipStream_t st, const void *w, const TX *x, TY *y, int n, int nb, int S,
            int slice_blocks) {
     static int max_blocks_per_cu = 0;
     if (max_blocks_per_cu == 0) {
         int v = 0;
-        SGQ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_q4_0_kernel<NBL, R>, kWG, 0));
+        SGQ_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_q4_0_kernel<NBL, R, TX, TY>,
+                                                             kWG, 0));
         max_blocks_per_cu = v > 0 ? v : 1;
     }
     const int P = (kWG / kWave) / S;
@@ -812,7 +817,7 @@ int launch(hipStream_t st, const void *w, const float *x, float *y, int n, int n
     const int max_grid = device_info().cus * max_blocks_per_cu;
     const int rounds = (tiles + max_grid - 1) / max_grid;
     const int grid = (tiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL((gemv_q4_0_kernel<NBL, R>), dim3(grid), dim3(kWG), 0, st,
+    hipLaunchKernelGGL((gemv_q4_0_kernel<NBL, R, TX, TY>), dim3(grid), dim3(kWG), 0, st,
                        static_cast<const uint8_t *>(w), x, y, n, nb, S, slice_blocks);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
@@ -914,18 +919,31 @@ int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     }
     SGQ_CHECK(!tg.split_out || (tg.count == 1 && tg.softcap == 0.f && epi == kEpiRows),
               "gemv (fused): split output needs one target and no softcap");
+    SGQ_CHECK(!tg.half_out || (!tg.split_out && epi == kEpiRows),
+              "gemv (fused): f16 output needs plain row stores");
     return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), n, nb, S, slice, pro, epi,
                            fz);
 }
 
-int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k) {
+namespace {
+template <typename T>
+int quant_limbs_t(hipStream_t st, const T *x, void *xl, uint32_t k) {
     SGQ_CHECK(k % 32 == 0 && k > 0, "quant_limbs: k=%u must be a multiple of 32", k);
-    SGQ_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)xl & 15) == 0, "quant_limbs: misaligned");
+    SGQ_CHECK(((uintptr_t)x & (4 * sizeof(T) - 1)) == 0 && ((uintptr_t)xl & 15) == 0,
+              "quant_limbs: misaligned");
     const int nb = (int)(k / 32);
-    hipLaunchKernelGGL(gemv_prep_x_kernel, dim3((nb * 8 + 255) / 256), dim3(256), 0, st, x,
+    hipLaunchKernelGGL(gemv_prep_x_kernel<T>, dim3((nb * 8 + 255) / 256), dim3(256), 0, st, x,
                        static_cast<BlockLimbs *>(xl), nb);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
+}
+}  // namespace
+
+int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k) {
+    return quant_limbs_t(st, x, xl, k);
+}
+int launch_quant_limbs(hipStream_t st, const uint16_t *x, void *xl, uint32_t k) {
+    return quant_limbs_t(st, x, xl, k);
 }
 
 int gemv_slices(uint32_t k) {
@@ -946,17 +964,21 @@ int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     SGQ_CHECK(ring_geometry(nb, &S, &slice), "gemv (limbs): k=%u outside the streamed geometry", k);
     SGQ_CHECK(!tg.split_out || (tg.count == 1 && tg.softcap == 0.f),
               "gemv (limbs): split output needs one target and no softcap");
+    SGQ_CHECK(!tg.half_out || !tg.split_out, "gemv (limbs): f16 output with split output");
     return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1], nb,
                            S, slice);
 }
 
-int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
-                     uint32_t k, void *workspace) {
+namespace {
+template <typename TX, typename TY>
+int gemv_q4_0_t(hipStream_t st, const void *w, const TX *x, TY *y, uint32_t n, uint32_t k,
+                void *workspace) {
     SGQ_CHECK(k % 64 == 0 && k > 0, "gemv_q4_0: k=%u must be a positive multiple of 64", k);
     SGQ_CHECK(k <= 65536, "gemv_q4_0: k=%u exceeds 65536", k);
     SGQ_CHECK(n > 0 && n < (1u << 31), "gemv_q4_0: bad n=%u", n);
     SGQ_CHECK(((uintptr_t)w & 3) == 0, "gemv_q4_0: weights must be 4-byte aligned");
-    SGQ_CHECK(((uintptr_t)x & 15) == 0, "gemv_q4_0: x must be 16-byte aligned");
+    SGQ_CHECK(((uintptr_t)x & (4 * sizeof(TX) - 1)) == 0, "gemv_q4_0: x must be %zu-byte aligned",
+              4 * sizeof(TX));
     const int nb = (int)(k / 32);
     // Streamed path: 16-byte aligned rows (K % 256 == 0), x limbs prepared
     // once into the workspace, row slices of <= 170 blocks.
@@ -966,7 +988,8 @@ int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, ui
         if (rc) return rc;
         GemvTargets tg{};
         tg.w[0] = w;
-        tg.y[0] = y;
+        tg.y[0] = reinterpret_cast<float *>(y);
+        tg.half_out = sizeof(TY) == 2;
         tg.end[0] = (int)n;
         tg.count = 1;
         return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(workspace), (int)n, nb, S,
@@ -987,6 +1010,16 @@ int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, ui
         case 6: return launch<6, 1>(st, w, x, y, (int)n, nb, S, slice);
         default: return launch<8, 1>(st, w, x, y, (int)n, nb, S, slice);
     }
+}
+}  // namespace
+
+int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
+                     uint32_t k, void *workspace) {
+    return gemv_q4_0_t(st, w, x, y, n, k, workspace);
+}
+int launch_gemv_q4_0(hipStream_t st, const void *w, const uint16_t *x, uint16_t *y, uint32_t n,
+                     uint32_t k, void *workspace) {
+    return gemv_q4_0_t(st, w, x, y, n, k, workspace);
 }
 
 }  // namespace sgq

@@ -99,9 +99,15 @@ __device__ __forceinline__ float q6_task(const uint8_t *row, const _Float16 *xh,
     return acc;
 }
 
+__device__ __forceinline__ _Float16 to_half(float v) { return (_Float16)v; }
+__device__ __forceinline__ _Float16 to_half(uint16_t bits) {
+    return __builtin_bit_cast(_Float16, bits);
+}
+
+template <typename TX>
 __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restrict__ W,
                                                           uint32_t stride,
-                                                          const float *__restrict__ x,
+                                                          const TX *__restrict__ x,
                                                           float *__restrict__ y, int n, int k,
                                                           float softcap) {
     extern __shared__ __align__(16) uint8_t q6_smem[];
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
     load(pb, r + G);
     load(pc, r + 2 * G);
     load(pd, r + 3 * G);
-    for (int i = threadIdx.x; i < k; i += kQ6WG) xh[i] = (_Float16)x[i];
+    for (int i = threadIdx.x; i < k; i += kQ6WG) xh[i] = to_half(x[i]);
     __syncthreads();
 
     for (; r < n; r += 4 * G) {
@@ -183,8 +189,10 @@ __global__ __launch_bounds__(kQ6WG) void gemv_q6_k_kernel(const uint8_t *__restr
 
 }  // namespace
 
-int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const float *x, float *y,
-                     uint32_t n, uint32_t k, float softcap) {
+namespace {
+template <typename TX>
+int gemv_q6_k_t(hipStream_t st, const void *w, size_t row_stride, const TX *x, float *y,
+                uint32_t n, uint32_t k, float softcap) {
     SGQ_CHECK(k > 0 && k % 256 == 0 && k / 256 <= (uint32_t)kQ6MaxBlocks,
               "gemv_q6_k: k=%u must be a multiple of 256, at most %d", k, 256 * kQ6MaxBlocks);
     SGQ_CHECK(row_stride % 16 == 0 && row_stride >= (size_t)(k / 256) * kQ6BlockBytes &&
@@ -200,11 +208,21 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const flo
     int grid = device_info().cus * 3;
     const int max_grid = (int)((n + rows_per_wg - 1) / rows_per_wg);
     if (grid > max_grid) grid = max_grid;
-    hipLaunchKernelGGL(gemv_q6_k_kernel, dim3(grid), dim3(kQ6WG), lds, st,
+    hipLaunchKernelGGL(gemv_q6_k_kernel<TX>, dim3(grid), dim3(kQ6WG), lds, st,
                        static_cast<const uint8_t *>(w), (uint32_t)row_stride, x, y, (int)n,
                        (int)k, softcap);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
+}
+}  // namespace
+
+int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const float *x, float *y,
+                     uint32_t n, uint32_t k, float softcap) {
+    return gemv_q6_k_t(st, w, row_stride, x, y, n, k, softcap);
+}
+int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uint16_t *x,
+                     float *y, uint32_t n, uint32_t k, float softcap) {
+    return gemv_q6_k_t(st, w, row_stride, x, y, n, k, softcap);
 }
 
 }  // namespace sgq

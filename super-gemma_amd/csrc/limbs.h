@@ -67,14 +67,12 @@ __device__ __forceinline__ void quantize_values(const float (&v)[32], XLimbs<NBL
         for (int w = 0; w < 4; w++) L.q[i][l][w] = (int)word[l][w];
 }
 
-template <int NBL>
-__device__ __forceinline__ void quantize_block(const float *__restrict__ xb, XLimbs<NBL> &L,
-                                               int i) {
+template <int NBL, typename T>
+__device__ __forceinline__ void quantize_block(const T *__restrict__ xb, XLimbs<NBL> &L, int i) {
     float v[32];
-    const float4 *x4 = reinterpret_cast<const float4 *>(xb);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        float4 t = x4[j];
+        float4 t = act_ld4(xb, j);
         v[4 * j] = t.x;
         v[4 * j + 1] = t.y;
         v[4 * j + 2] = t.z;

@@ -186,11 +186,13 @@ __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
     }
 }
 
-template <bool AL>
+// HOUT: the output is f16 (uint16_t bits, each sum rounded to nearest even:
+// the reference's y binding, gemm_q4_0_i8.wgsl:63); else fp32.
+template <bool AL, bool HOUT>
 __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint8_t *__restrict__ W,
                                                       const int8_t *__restrict__ xq,
                                                       const uint16_t *__restrict__ xs,
-                                                      float *__restrict__ out, int m, int n,
+                                                      void *__restrict__ out_, int m, int n,
                                                       int k, int mt, int nt, int split) {
     extern __shared__ __align__(16) uint8_t smem[];
     Stage *stages = reinterpret_cast<Stage *>(smem);
@@ -307,7 +309,8 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
     };
     for (int s = 0; s < n_stages; s++) step(s);
 
-    float *dst = out + (size_t)z * m * n;
+    float *dst = static_cast<float *>(out_) + (size_t)z * m * n;
+    uint16_t *dsth = static_cast<uint16_t *>(out_);
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -317,7 +320,12 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const int row = m0 + wm * 64 + i * 32 + 8 * (q / 4) + 4 * h + (q % 4);
-                if (AL || row < m) dst[(size_t)row * n + col] = acc[i][j][q];
+                if (AL || row < m) {
+                    if (HOUT)
+                        dsth[(size_t)row * n + col] = f32_to_f16_bits(acc[i][j][q]);
+                    else
+                        dst[(size_t)row * n + col] = acc[i][j][q];
+                }
             }
         }
 }
@@ -340,14 +348,16 @@ __global__ void splitk_reduce_kernel(const float4 *__restrict__ part, float4 *__
 
 }  // namespace
 
-int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
-                        float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
-                        float *partials) {
+namespace {
+template <bool HOUT>
+int gemm_t(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs, void *y,
+           uint32_t m, uint32_t n, uint32_t k, uint32_t split_k, float *partials) {
     SGQ_CHECK(k % 64 == 0 && k > 0, "gemm_q4_0_q8: k=%u must be a positive multiple of 64", k);
     SGQ_CHECK(m > 0 && n > 0, "gemm_q4_0_q8: empty shape");
     SGQ_CHECK(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8,
               "gemm_q4_0_q8: split_k=%u not in {1,2,4,8}", split_k);
     SGQ_CHECK(split_k == 1 || partials != nullptr, "gemm_q4_0_q8: split_k>1 needs partials");
+    SGQ_CHECK(!HOUT || split_k == 1, "gemm_q4_0_q8: f16 output is not built with split-K");
     SGQ_CHECK(k % 16 == 0 && ((uintptr_t)xq & 15) == 0, "gemm_q4_0_q8: xq must be 16-byte aligned");
     SGQ_CHECK(((uintptr_t)w & 3) == 0, "gemm_q4_0_q8: weights must be 4-byte aligned");
     SGQ_CHECK((uint64_t)m * n < (1ull << 31) * 4, "gemm_q4_0_q8: output too large");
@@ -355,24 +365,24 @@ int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const u
     static bool attr = false;
     const size_t lds = 2 * sizeof(Stage);
     if (!attr) {
-        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<false>,
+        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<false, HOUT>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<true>,
+        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<true, HOUT>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
     const int mt = (int)((m + BM - 1) / BM), nt = (int)((n + BN - 1) / BN);
-    float *dst = split_k == 1 ? y : partials;
+    void *dst = split_k == 1 ? y : static_cast<void *>(partials);
     // every split's block range is a multiple of KB when nb is (the split
     // bounds are rounded down to KB)
     const bool aligned = m % BM == 0 && n % BN == 0 && (k / 32) % KB == 0 &&
                          ((uintptr_t)xs & 7) == 0;
     if (aligned)
-        hipLaunchKernelGGL(mmq_kernel<true>, dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+        hipLaunchKernelGGL((mmq_kernel<true, HOUT>), dim3(mt * nt, split_k), dim3(kMWG), lds, st,
                            static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k,
                            mt, nt, (int)split_k);
     else
-        hipLaunchKernelGGL(mmq_kernel<false>, dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+        hipLaunchKernelGGL((mmq_kernel<false, HOUT>), dim3(mt * nt, split_k), dim3(kMWG), lds, st,
                            static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k,
                            mt, nt, (int)split_k);
     SGQ_HIP(hipGetLastError());
@@ -382,10 +392,22 @@ int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const u
         if (g > (uint64_t)device_info().cus * 8) g = (uint64_t)device_info().cus * 8;
         hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)g), dim3(256), 0, st,
                            reinterpret_cast<const float4 *>(partials),
-                           reinterpret_cast<float4 *>(y), n4, (int)split_k);
+                           static_cast<float4 *>(y), n4, (int)split_k);
         SGQ_HIP(hipGetLastError());
     }
     return SGQ_OK;
+}
+
+}  // namespace
+
+int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
+                        float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
+                        float *partials) {
+    return gemm_t<false>(st, w, xq, xs, y, m, n, k, split_k, partials);
+}
+int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
+                        uint16_t *y, uint32_t m, uint32_t n, uint32_t k) {
+    return gemm_t<true>(st, w, xq, xs, y, m, n, k, 1, nullptr);
 }
 
 }  // namespace sgq

@@ -50,6 +50,10 @@ constexpr size_t kAttnPartOff = kAttnCounterOff + 4096;
 constexpr size_t kWorkspaceBytes = 16u << 20;
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
                      uint32_t k, void *workspace);
+// f16 x and y (the reference's gemv_q4_0 binding types): sums in f32 as
+// for fp32 x, each output rounded to f16.
+int launch_gemv_q4_0(hipStream_t st, const void *w, const uint16_t *x, uint16_t *y, uint32_t n,
+                     uint32_t k, void *workspace);
 // Up to kGemvMaxTargets Q4_0 matrices with the same K whose rows form one
 // concatenated row space (rows [end[j-1], end[j]) belong to matrix j), read
 // against one x limb table.  softcap > 0 applies cap*tanh(v/cap) on output.
@@ -64,6 +68,9 @@ struct GemvTargets {
     // writes its partial row sums to y[0] + s*n instead of meeting at a
     // workgroup barrier; the consumer adds the slices in order s = 0..S-1.
     int split_out;
+    // half_out != 0: the targets y[j] hold f16 rows (uint16_t bits; rows
+    // are rounded to nearest even); not with split_out
+    int half_out;
 };
 // Number of K-slices the streamed GEMV uses for K (1, 2 or 4); 0 if K is
 // outside the streamed geometry.
@@ -71,9 +78,13 @@ int gemv_slices(uint32_t k);
 // Sets the streamed kernels' launch attributes (call before graph capture).
 int gemv_prepare();
 int launch_quant_limbs(hipStream_t st, const float *x, void *xl, uint32_t k);
+int launch_quant_limbs(hipStream_t st, const uint16_t *x, void *xl, uint32_t k);
 // Q6_K logits GEMV (gemv_q6_k.hip): rows at a 16-byte-multiple stride.
 int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const float *x, float *y,
                      uint32_t n, uint32_t k, float softcap);
+// f16 x (gemv_q6_k_logits.wgsl:19); the fp32 form rounds x to f16 itself.
+int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uint16_t *x,
+                     float *y, uint32_t n, uint32_t k, float softcap);
 // Fused forms of the streamed GEMV (single K-slice for the prologues).
 // Prologue (what the GEMV's x limbs are computed from, inside the launch):
 //   kProTable  the limb table xl (written by an earlier kernel);
@@ -131,6 +142,17 @@ int launch_kv_append_q8(hipStream_t st, const float *src, uint16_t *scales, int8
 // a multiple of 32), scales [block × row_len] f16.
 int launch_kv_append_v_q8(hipStream_t st, const float *src, uint16_t *scales, int8_t *quants,
                           const uint32_t *step, uint32_t pos, uint32_t n_tokens, uint32_t row_len);
+// The Q8_0 operators over f16 activations (uint16_t bits): an f16 source
+// widens exactly, so quants and scales are those of its fp32 value; the
+// dequantized output rounds to f16.
+int launch_quant_q8_0(hipStream_t st, const uint16_t *x, uint16_t *scales, int8_t *quants,
+                      uint64_t n_elems);
+int launch_dequant_q8_0(hipStream_t st, const uint16_t *scales, const int8_t *quants,
+                        uint16_t *out, uint64_t n_elems);
+int launch_kv_append_q8(hipStream_t st, const uint16_t *src, uint16_t *scales, int8_t *quants,
+                        const uint32_t *step, uint32_t n_tokens, uint32_t row_len, uint32_t ring);
+int launch_kv_append_v_q8(hipStream_t st, const uint16_t *src, uint16_t *scales, int8_t *quants,
+                          const uint32_t *step, uint32_t pos, uint32_t n_tokens, uint32_t row_len);
 // Prefill attention with int8 PV (attn_prefill_global_flash_sp_ipv.wgsl):
 // causal over a linear Q8_0 cache with key-blocked V scales vs_kb
 // [ceil(keys/32) × n_kv × 128]; q0 from step[3] when step is given.
@@ -140,6 +162,9 @@ int launch_attn_prefill_ipv(hipStream_t st, const float *q, const int8_t *kq, co
 int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
                         float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
                         float *partials);
+// f16 output (the reference's y binding), no split-K.
+int launch_gemm_q4_0_q8(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
+                        uint16_t *y, uint32_t m, uint32_t n, uint32_t k);
 int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, const uint16_t *ks,
                           const int8_t *vq, const uint16_t *vs, const uint32_t *step,
                           int step_word, uint32_t kv_len, int n_q, int n_kv, int head_dim,
@@ -243,6 +268,16 @@ int launch_rope(hipStream_t st, float *xs, const float *cos_sin, uint64_t rows, 
 int launch_geglu(hipStream_t st, const float *g, const float *u, float *y, uint64_t n);
 int launch_add_scaled(hipStream_t st, const float *a, const float *b, float *y, uint64_t n,
                       float s);
+// The same operators over f16 activations (uint16_t bits), the reference's
+// storage type: rmsnorm/geglu/add_scaled read f16, compute in f32, round
+// the result to f16; rope rotates f16 rows in place.
+int launch_rmsnorm(hipStream_t st, const uint16_t *x, const float *w, uint16_t *y, uint32_t rows,
+                   uint32_t row_len, int plus_one, float eps);
+int launch_rope(hipStream_t st, uint16_t *xs, const float *cos_sin, uint64_t rows,
+                uint32_t head_dim, uint32_t rot_dims, uint32_t n_heads);
+int launch_geglu(hipStream_t st, const uint16_t *g, const uint16_t *u, uint16_t *y, uint64_t n);
+int launch_add_scaled(hipStream_t st, const uint16_t *a, const uint16_t *b, uint16_t *y,
+                      uint64_t n, float s);
 int launch_fill_q4_0(hipStream_t st, void *w, uint64_t n_blocks, uint64_t seed, float sigma);
 int launch_fill_normal(hipStream_t st, float *x, uint64_t n, uint64_t seed, float mean,
                        float sigma);
@@ -261,6 +296,23 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
     // v_cvt_f16_f32 rounds to nearest even in the default FP mode.
     return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Activation element access for kernels built for both activation types:
+// fp32, or f16 held as its bits (the reference's activation storage).  A
+// load widens exactly; an f16 store rounds to nearest even.
+__device__ __forceinline__ float act_ld(const float *p, size_t i) { return p[i]; }
+__device__ __forceinline__ float act_ld(const uint16_t *p, size_t i) { return f16_bits_to_f32(p[i]); }
+__device__ __forceinline__ void act_st(float *p, size_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void act_st(uint16_t *p, size_t i, float v) { p[i] = f32_to_f16_bits(v); }
+// Four consecutive activations starting at element 4j.
+__device__ __forceinline__ float4 act_ld4(const float *p, size_t j) {
+    return reinterpret_cast<const float4 *>(p)[j];
+}
+__device__ __forceinline__ float4 act_ld4(const uint16_t *p, size_t j) {
+    const uint2 w = reinterpret_cast<const uint2 *>(p)[j];
+    return make_float4(f16_bits_to_f32(w.x & 0xffffu), f16_bits_to_f32(w.x >> 16),
+                       f16_bits_to_f32(w.y & 0xffffu), f16_bits_to_f32(w.y >> 16));
 }
 
 }  // namespace sgq

@@ -139,3 +139,29 @@ def test_every_variant_the_reference_model_loads_resolves():
     for n in MODEL_VARIANTS:
         rc = L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info))
         assert rc == 0, (n, L.sgq_last_error())
+
+
+def test_f32_suffix_forms_resolve():
+    """The reference's names take f16 activations; NAME_f32 is the same
+    kernel over fp32 and has the same binding / push layout.  The families
+    of this build's own geometry take fp32 only and refuse the suffix."""
+    import sgq
+
+    L = sgq.lib()
+    h = C.c_void_p()
+    for n in ("gemv_q4_0_k5376", "gemv_q4_0_generic", "gemv_q6_k_logits", "rmsnorm_5376_plus1",
+              "rope_sliding_q", "rope_global_k", "geglu", "add_scaled", "kv_quant_q8",
+              "kv_dequant_q8", "kv_append_global_q8", "kv_append_global_v_q8",
+              "gemm_q4_0_i8_swz_m4n1_k5376_n21504", "gemm_q4_0_i8_bb_pfd4"):
+        a, b = sgq._Info(), sgq._Info()
+        assert L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(a)) == 0, n
+        assert L.sgq_kernel_lookup(None, (n + "_f32").encode(), C.byref(h), C.byref(b)) == 0, n
+        assert (a.bindings, a.push_bytes, list(a.workgroup)) == \
+            (b.bindings, b.push_bytes, list(b.workgroup)), n
+    for n in ("rope_hd128_sliding_q", "kv_append_sliding_q8", "attn_reduce_d128",
+              "attn_decode_global_q8_hd128", "gemm_q4_0_i8_splitk4_k21504_n5376",
+              "attn_decode_sliding", "kv_append_global"):
+        info = sgq._Info()
+        assert L.sgq_kernel_lookup(None, n.encode(), C.byref(h), C.byref(info)) == 0, n
+        rc = L.sgq_kernel_lookup(None, (n + "_f32").encode(), C.byref(h), C.byref(info))
+        assert rc == 4, n

@@ -47,7 +47,7 @@ def test_rmsnorm_weightless_and_name_dispatch(ctx, oracle):
     ctx.rmsnorm(dev(x), None, y, rows, row_len)
     torch.cuda.synchronize()
     _close(host(y), oracle.rmsnorm(x, None, row_len), "weightless")
-    for name, p1 in (("rmsnorm_5376", False), ("rmsnorm_5376_plus1", True)):
+    for name, p1 in (("rmsnorm_5376_f32", False), ("rmsnorm_5376_plus1_f32", True)):
         k = ctx.load_kernel(name)
         y2 = empty(rows * row_len, torch.float32)
         ctx.dispatch_blocking(k, [sgq.BufferBinding.buffer(0, dev(x)), sgq.BufferBinding.buffer(1, dev(w)),
@@ -78,7 +78,7 @@ def test_rope_variants_match_oracle(ctx, oracle, name, head_dim, rot, n_heads):
     torch.cuda.synchronize()
     _close(host(tx), want, name)
     tx2 = dev(x)
-    k = ctx.load_kernel(name)
+    k = ctx.load_kernel(name if "hd128" in name else name + "_f32")
     ctx.dispatch_blocking(k, [sgq.BufferBinding.buffer(0, tx2), sgq.BufferBinding.buffer(1, dev(cs))],
                           None, [(n_tok * n_heads * rot // 2 + 255) // 256, 1, 1])
     _close(host(tx2), want, name + " dispatch")
@@ -101,7 +101,7 @@ def test_geglu_and_add_scaled(ctx, oracle):
     ctx.geglu(dev(g), dev(u), y)
     torch.cuda.synchronize()
     _close(host(y), oracle.geglu(g, u), "geglu")
-    k = ctx.load_kernel("geglu")
+    k = ctx.load_kernel("geglu_f32")
     y2 = empty(n, torch.float32)
     ctx.dispatch_blocking(k, [sgq.BufferBinding.buffer(0, dev(g)), sgq.BufferBinding.buffer(1, dev(u)),
                               sgq.BufferBinding.buffer(2, y2)], None, [(n + 255) // 256, 1, 1])
@@ -119,7 +119,7 @@ def test_geglu_and_add_scaled(ctx, oracle):
     torch.cuda.synchronize()
     assert np.array_equal(host(ya).view(np.uint32), oracle.add_scaled(a, b, 0.75).view(np.uint32))
     import struct
-    k = ctx.load_kernel("add_scaled")
+    k = ctx.load_kernel("add_scaled_f32")
     yb = empty(n, torch.float32)
     ctx.dispatch_blocking(k, [sgq.BufferBinding.buffer(0, dev(a)), sgq.BufferBinding.buffer(1, dev(b)),
                               sgq.BufferBinding.buffer(2, yb)], struct.pack("<f", 0.75),

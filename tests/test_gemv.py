@@ -110,9 +110,10 @@ def test_gemv_is_bit_deterministic(ctx, oracle):
 
 
 def test_gemv_name_dispatch_matches_typed(ctx, oracle):
-    """The reference surface: load_kernel(variant) + dispatch(bindings 0..2,
-    groups [N,1,1]) gives the typed entry point's bits; the generic variant
-    takes K as a 4-byte push constant."""
+    """The reference surface over fp32 activations (the _f32 forms of the
+    variant names): load_kernel(variant) + dispatch(bindings 0..2, groups
+    [N,1,1]) gives the typed entry point's bits; the generic variant takes K
+    as a 4-byte push constant."""
     import sgq
 
     k, n = 5376, 4096
@@ -120,12 +121,12 @@ def test_gemv_name_dispatch_matches_typed(ctx, oracle):
     tw, tx = dev(w), dev(x)
     ref = empty(n, torch.float32)
     ctx.gemv_q4_0(tw, tx, ref, n, k)
-    kern = ctx.load_kernel("gemv_q4_0_k5376")
+    kern = ctx.load_kernel("gemv_q4_0_k5376_f32")
     assert kern.bindings == 3 and kern.push_bytes == 0 and kern.workgroup[0] == 64
     y1 = empty(n, torch.float32)
     ctx.dispatch_blocking(kern, [sgq.BufferBinding.buffer(0, tw), sgq.BufferBinding.buffer(1, tx),
                                  sgq.BufferBinding.buffer(2, y1)], None, [n, 1, 1])
-    gen = ctx.load_kernel("gemv_q4_0_generic")
+    gen = ctx.load_kernel("gemv_q4_0_generic_f32")
     y2 = empty(n, torch.float32)
     ctx.dispatch_blocking(gen, [sgq.BufferBinding.buffer(0, tw), sgq.BufferBinding.buffer(1, tx),
                                 sgq.BufferBinding.buffer(2, y2)], struct.pack("<I", k), [n, 1, 1])

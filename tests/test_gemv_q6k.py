@@ -73,7 +73,7 @@ def test_q6k_name_dispatch_matches_typed(ctx, oracle):
     tw, tx = dev(w), dev(x)
     ref = empty(n, torch.float32)
     ctx.gemv_q6_k(tw, STRIDE, tx, ref, n, K, 30.0)
-    kern = ctx.load_kernel("gemv_q6_k_logits")
+    kern = ctx.load_kernel("gemv_q6_k_logits_f32")
     assert kern.bindings == 3 and kern.push_bytes == 0
     y = empty(n, torch.float32)
     ctx.dispatch_blocking(kern, [sgq.BufferBinding.buffer(0, tw), sgq.BufferBinding.buffer(1, tx),

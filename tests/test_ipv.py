@@ -61,7 +61,7 @@ def test_kv_append_v_q8_bit_exact(ctx, oracle):
     ts.zero_()
     step = torch.zeros(8, dtype=torch.int32, device="cuda")
     ctx.step_write(step, sgq.StepState(pos, 0, 0, 0))
-    k = ctx.load_kernel("kv_append_global_v_q8")
+    k = ctx.load_kernel("kv_append_global_v_q8_f32")
     B = sgq.BufferBinding.buffer
     ctx.dispatch_blocking(k, [B(0, dev(src)), B(1, ts), B(2, tq), B(3, step)], None,
                           [(n_tok + 31) // 32 * row // 256, 1, 1])

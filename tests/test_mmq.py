@@ -152,7 +152,7 @@ def test_mmq_name_dispatch_variants(ctx, oracle):
     xq, xs = _quant_on_gpu(ctx, x, m, k)
     ref = empty(m * n, torch.float32)
     ctx.gemm_q4_0_q8(w, xq, xs, ref, m, n, k)
-    kern = ctx.load_kernel("gemm_q4_0_i8_swz_m4n1_k5376_n2048")
+    kern = ctx.load_kernel("gemm_q4_0_i8_swz_m4n1_k5376_n2048_f32")
     y = empty(m * n, torch.float32)
     B = sgq.BufferBinding.buffer
     ctx.dispatch_blocking(kern, [B(0, w), B(1, xq), B(2, xs), B(3, y)], None, [m // 64, n // 16, 1])
@@ -166,7 +166,7 @@ def test_mmq_name_dispatch_variants(ctx, oracle):
     xq, xs = _quant_on_gpu(ctx, x, m, k)
     ref = empty(m * n, torch.float32)
     ctx.gemm_q4_0_q8(w, xq, xs, ref, m, n, k)
-    down = ctx.load_kernel("gemm_q4_0_i8_bb_pfd4")
+    down = ctx.load_kernel("gemm_q4_0_i8_bb_pfd4_f32")
     y = empty(m * n, torch.float32)
     ctx.dispatch_blocking(down, [B(0, w), B(1, xq), B(2, xs), B(3, y)], None, [m // 64, 336, 1])
     assert torch.equal(ref, y)

@@ -360,3 +360,30 @@ def test_q8_activation_noise_spread():
         spreads.append(float(np.abs(out - base).max() / np.abs(base).max()))
     assert max(spreads) > 0.0, spreads
     assert max(spreads) < 2e-2, spreads
+
+
+def test_f16_graph_rounds_every_buffer_and_keeps_page_formats():
+    """F16Graph (the reference GPU graph's storage, graph.rs:282-313,
+    :581-611): every layer output is f16-representable, sliding caches hold
+    the f16 K/V rows themselves, global caches Q8_0 K and f16 V; and it stays
+    within f16 noise of the fp32 forward on the same weights."""
+    from oracle.model import F16Graph
+
+    c = _cfg(n_layers=2, global_every=2)
+    w = _weights(c)
+    ref16, ref32 = F16Graph(c, w), OracleDecoder(c, w)
+    ref16.taps = {}
+    for t in (5, 77, 3):
+        got, want = ref16.decode(t), ref32.decode(t)
+        top = float(np.abs(want).max())
+        assert np.abs(got - want).max() <= 2e-2 * top
+        assert not np.array_equal(got, want)  # the roundings are really there
+        for l in range(2):
+            x = ref16.taps[("x_layer", l)]
+            assert np.array_equal(O.through_f16(x), x)
+        k, v = ref16.taps[("k_rope", 1)], ref16.taps[("v_norm", 1)]
+        s, q = O.quant_q8_0(k)
+        assert np.array_equal(ref16.k_cache[1][-1], O.dequant_q8_0(s, q))
+        assert np.array_equal(ref16.v_cache[1][-1], v)
+        assert np.array_equal(ref16.k_cache[0][-1], ref16.taps[("k_rope", 0)])
+        assert np.array_equal(O.through_f16(v), v)

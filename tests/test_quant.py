@@ -71,7 +71,7 @@ def test_kv_quant_q8_name_dispatch(ctx, oracle):
     n = 2048 + 64
     x = oracle.Rng(0xB5).f32_vec(n)
     s_want, q_want = oracle.quant_q8_0(x)
-    kern = ctx.load_kernel("kv_quant_q8")
+    kern = ctx.load_kernel("kv_quant_q8_f32")
     ts, tq = empty(n // 32, torch.int16), empty(n, torch.int8)
     ctx.dispatch_blocking(kern, [sgq.BufferBinding.buffer(0, dev(x)), sgq.BufferBinding.buffer(1, ts),
                                  sgq.BufferBinding.buffer(2, tq)], None, kern.groups_for(n // 32))
@@ -91,7 +91,7 @@ def test_kv_append_global_q8_places_rows_at_pos(ctx, oracle):
     quants = torch.full((slots * row,), 3, dtype=torch.int8, device="cuda")
     step = torch.zeros(4, dtype=torch.int32, device="cuda")
     ctx.step_write(step, sgq.StepState(pos=pos, kv_len_sliding=0, kv_len_global=pos + n_tok, q0=pos))
-    kern = ctx.load_kernel("kv_append_global_q8")
+    kern = ctx.load_kernel("kv_append_global_q8_f32")
     ctx.dispatch_blocking(kern, [sgq.BufferBinding.buffer(0, dev(x)), sgq.BufferBinding.buffer(1, scales),
                                  sgq.BufferBinding.buffer(2, quants), sgq.BufferBinding.buffer(3, step)],
                           None, [n_tok * row // 32 // 64 + 1, row // 32, 1])
