@@ -231,8 +231,14 @@ int sgq_gemv_q4_0_limbs(sgq_ctx *ctx, uint32_t n_targets, const void *const *w, 
  * work goes on `hip_stream` (NULL = the null stream), which must belong to the
  * current device.  The x limb table lives in a library-owned device array of
  * 192 KiB per device (kept until the process ends), so k <= 65536; larger k
- * returns SGQ_ERR_VALIDATION.  Every call on one device shares that array:
- * calls that overlap on one device (different streams, or threads) race. */
+ * returns SGQ_ERR_VALIDATION.  Every call on one device shares that array.
+ * Calls on one stream are ordered; a call on a different stream while the
+ * previous eager call (on another stream) has not finished returns
+ * SGQ_ERR_VALIDATION instead of racing (a library-owned event, created with
+ * the array's address on the device's first call, marks the end of each
+ * eager call).  Calls recorded under graph capture are not tracked: graph
+ * replays that overlap other calls on the device race, as do calls from two
+ * host threads that enqueue on two streams at the same moment. */
 int sgq_gemv_q4_0_noalloc(void *hip_stream, const void *w, const float *x, float *y, uint32_t n,
                           uint32_t k);
 

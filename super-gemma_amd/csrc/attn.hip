@@ -18,38 +18,6 @@ __global__ __launch_bounds__(W * kWave) void attn_decode_q8_kernel(
                               limbs_out, post, blockIdx.x, blockIdx.y, FUSED ? step[0] : 0u);
 }
 
-// The same with the merge done by the last split of each kv head to finish
-// (no second launch): every split stores its partial with agent-scope
-// stores (attn_chunk), waits for them, and bumps the kv head's counter; the
-// one that sees n_splits-1 merges, reading the partials with agent-scope
-// loads, and resets the counter for the next launch.  The merge order is
-// still split order 0..S-1, so the result does not depend on which split
-// finished last.  With one split the workgroup writes the limbs itself.
-template <int QPK, int W>
-__global__ __launch_bounds__(W * kWave) void attn_decode_merge_kernel(
-    const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
-    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
-    const uint32_t *__restrict__ step, int step_word, int n_kv, int n_splits, float scale,
-    float *__restrict__ part, AttnPost post, unsigned *__restrict__ counters,
-    BlockLimbs *__restrict__ limbs_out) {
-    __shared__ __align__(16) float o_s[QPK * kHD];
-    __shared__ int last_s;
-    attn_chunk<QPK, true, W>(nullptr, kq, ks, vq, vs, step[step_word], n_kv, n_splits, scale,
-                             part, nullptr, limbs_out, post, blockIdx.x, blockIdx.y, step[0]);
-    if (n_splits == 1) return;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned *c = counters + blockIdx.x;
-        const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        last_s = old + 1 == (unsigned)n_splits;
-        if (last_s) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (last_s) attn_merge<QPK, true>(part, n_splits, blockIdx.x, nullptr, limbs_out, o_s);
-}
-
 // Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
 // out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s.  One
 // 256-thread workgroup per query head (attn_merge_head); the kernel
@@ -170,11 +138,8 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                              const float *rope_cs, float eps, const uint32_t *step, int step_word,
                              uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
                              int n_q, int n_kv, int n_splits, float scale, float *out,
-                             void *workspace, size_t workspace_bytes, void *limbs_out,
-                             bool merge_in_launch) {
+                             void *workspace, size_t workspace_bytes, void *limbs_out) {
     SGQ_CHECK(step != nullptr, "attn (fused): needs the step buffer");
-    SGQ_CHECK(!merge_in_launch || (limbs_out != nullptr && out == nullptr && n_kv <= kAttnMaxKv),
-              "attn (fused): the in-launch merge writes limbs only");
     SGQ_CHECK(n_kv > 0 && n_q % n_kv == 0, "attn (fused): n_q %% n_kv != 0");
     SGQ_CHECK(n_splits >= 1 && n_splits <= kMergeMaxSplits, "attn (fused): n_splits %d", n_splits);
     SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 15) == 0 && ((uintptr_t)ks & 7) == 0 &&
@@ -187,21 +152,9 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                         kq, vq, ks, vs};
     if (int rc = attn_prepare()) return rc;
     dim3 grid(n_kv, n_splits);
-    unsigned *counters = reinterpret_cast<unsigned *>(static_cast<uint8_t *>(workspace) +
-                                                      kAttnCounterOff);
     const int qpk = n_q / n_kv;
     SGQ_CHECK(qpk == 1 || qpk == 2, "attn (fused): %d q heads per kv head unsupported", qpk);
     BlockLimbs *lo = static_cast<BlockLimbs *>(limbs_out);
-    if (merge_in_launch) {
-#define SGQ_ATTN(Q, W)                                                                            \
-    hipLaunchKernelGGL((attn_decode_merge_kernel<Q, W>), grid, dim3(W * kWave), 0, st, kq, ks, vq, \
-                       vs, step, step_word, n_kv, n_splits, scale, part, post, counters, lo)
-        if (qpk == 1) SGQ_ATTN(1, kAttnWaves);
-        else SGQ_ATTN(2, kAttnWaves);
-#undef SGQ_ATTN
-        SGQ_HIP(hipGetLastError());
-        return SGQ_OK;
-    }
     float *out1 = n_splits == 1 ? out : nullptr;
     BlockLimbs *lo1 = n_splits == 1 ? lo : nullptr;
 #define SGQ_ATTN(Q, W)                                                                            \

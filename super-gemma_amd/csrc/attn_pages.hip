@@ -321,9 +321,12 @@ __global__ __launch_bounds__(256) void attn_reduce_pages_kernel(const float *__r
     if (tid == 0) l_s[0] = lsum;
     __syncthreads();
     const float l = l_s[0];
+    // every split empty (kv_len 0): l = 0 and acc = 0; the output is 0, not
+    // the 0/0 that attn_reduce.wgsl's acc/l would give
 #pragma unroll
     for (int e = 0; e < ND; e++)
-        out[(size_t)h * HD + tid * ND + e] = __builtin_bit_cast(uint16_t, (_Float16)(acc[e] / l));
+        out[(size_t)h * HD + tid * ND + e] =
+            __builtin_bit_cast(uint16_t, (_Float16)(l > 0.f ? acc[e] / l : 0.f));
 }
 
 // f16 rows [n_tok × row] to slot step[0] + t (mod ring when ring > 0); eight

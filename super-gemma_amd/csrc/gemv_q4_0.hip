@@ -1040,21 +1040,32 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-void *g_scratch_ptr[kMaxDevices] = {};
+// Per device: the scratch array's address, an event recorded after each
+// eager call (its completion says the array is free again) and the stream
+// of that call (compared, never used).
+struct ScratchState {
+    void *ptr = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;
+};
+ScratchState g_scratch[kMaxDevices];
 
-// The current device's copy of `scratch` (looked up on its first use).
-int scratch_for_current_device(void **out) {
+// Set-up on a device's first call: the current device's copy of `scratch`
+// and its completion event.
+int scratch_for_current_device(ScratchState **out) {
     int dev = -1;
     SGQ_HIP(hipGetDevice(&dev));
     SGQ_CHECK(dev >= 0 && dev < kMaxDevices, "gemv_q4_0_noalloc: device %d out of range", dev);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (g_scratch_ptr[dev] == nullptr) {
+    ScratchState &sc = g_scratch[dev];
+    if (sc.ptr == nullptr) {
         void *p = nullptr;
         SGQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         SGQ_CHECK(p != nullptr, "gemv_q4_0_noalloc: no device address for the scratch array");
-        g_scratch_ptr[dev] = p;
+        SGQ_HIP(hipEventCreateWithFlags(&sc.done, hipEventDisableTiming));
+        sc.ptr = p;
     }
-    *out = g_scratch_ptr[dev];
+    *out = &sc;
     return SGQ_OK;
 }
 
@@ -1072,7 +1083,28 @@ extern "C" int sgq_gemv_q4_0_noalloc(void *hip_stream, const void *w, const floa
     SGQ_CHECK((size_t)(k / 32) * sizeof(BlockLimbs) <= kNoAllocScratchBytes,
               "gemv_q4_0_noalloc: k=%u needs %zu scratch bytes, %zu available", k,
               (size_t)(k / 32) * sizeof(BlockLimbs), kNoAllocScratchBytes);
-    void *ws = nullptr;
-    if (int rc = scratch_for_current_device(&ws)) return rc;
-    return launch_gemv_q4_0(static_cast<hipStream_t>(hip_stream), w, x, y, n, k, ws);
+    const hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchState *sc = nullptr;
+    if (int rc = scratch_for_current_device(&sc)) return rc;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SGQ_HIP(hipStreamIsCapturing(st, &cap));
+    const bool eager = cap == hipStreamCaptureStatusNone;
+    // Calls on one stream are ordered; a call on another stream while the
+    // previous eager call may still be running would share the array with it
+    if (eager && sc->used && st != sc->last) {
+        const hipError_t q = hipEventQuery(sc->done);
+        if (q == hipErrorNotReady)
+            return fail(SGQ_ERR_VALIDATION,
+                        "gemv_q4_0_noalloc: the previous call, on another stream, may still be "
+                        "running and shares this device's scratch array; synchronize it first");
+        if (q != hipSuccess) return check_hip(q, "hipEventQuery");
+    }
+    if (int rc = launch_gemv_q4_0(st, w, x, y, n, k, sc->ptr)) return rc;
+    if (eager) {
+        SGQ_HIP(hipEventRecord(sc->done, st));
+        sc->last = st;
+        sc->used = true;
+    }
+    return SGQ_OK;
 }

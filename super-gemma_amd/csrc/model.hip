@@ -610,14 +610,10 @@ struct LayerW {
     uint32_t hd, n_kv;  // this layer kind's head_dim and kv heads
 };
 
-// The split merge of the fused decode runs as its own launch (queued behind
-// the split kernel it costs little; measured 1.7% faster per step than the
-// last split of each kv head merging in the split kernel, which adds a store
-// drain and a counter to every workgroup).  1 selects the in-launch merge.
-#ifndef SGQ_MERGE_IN_LAUNCH
-#define SGQ_MERGE_IN_LAUNCH 0
-#endif
-constexpr bool kMergeInLaunch = SGQ_MERGE_IN_LAUNCH;
+// The split merge of the fused decode runs as its own launch: queued behind
+// the split kernel it costs little, and measured 1.7% faster per step than
+// the last split of each kv head merging inside the split kernel (which
+// adds a store drain and a counter to every workgroup).
 
 // Decode attention splits per kv head: 16 for a 1024-slot ring (64 slots
 // per split; with the merge as its own launch, 16 and 32 measured equal and
@@ -848,8 +844,7 @@ int record_step_generic(sgq_model *m, float *logits, bool head) {
 //                  this layer's input RMSNorm, from the down GEMV's partial
 //                  sums (layer 0: the embedding row); writes x (xa)
 //   attention      fused q/k/v post-projection and K/V append
-//   merge          the splits in split order -> the O GEMV's limbs (or, with
-//                  SGQ_MERGE_IN_LAUNCH, by the last split inside attention)
+//   merge          the splits in split order -> the O GEMV's limbs
 //   O GEMV         epilogue: u/A/B rows and partial sums for the post-
 //                  attention residual and the FFN norm
 //   gate/up GEMV   prologue: the post-attention residual (writes xb) and the
@@ -922,7 +917,7 @@ int record_step_fused(sgq_model *m, float *logits) {
                         m->rope_cs + (L.global ? kHeadDim : 0), c.eps, m->step, L.global ? 2 : 1,
                         L.global ? 0u : L.slots, L.kq, L.ks, L.vq, L.vs, nq, nkv,
                         decode_splits(L), c.attn_scale, nullptr, ctx_workspace(m->ctx),
-                        kWorkspaceBytes, m->fx.xl_o, kMergeInLaunch))) {
+                        kWorkspaceBytes, m->fx.xl_o))) {
             return rc;
         }
         GemvTargets ot{};
@@ -1016,8 +1011,10 @@ int sgq_model_create(sgq_ctx *ctx, const sgq_model_config *cfg, sgq_model **out)
     SGQ_CHECK(ok_qpk(kv_s) && ok_qpk(kv_g),
               "model: %u q heads over %u / %u kv heads (1 or 2 per kv head at the benchmark "
               "geometry, 1/2/4/8 otherwise)", c.n_q_heads, kv_s, kv_g);
-    SGQ_CHECK(c.hidden % 256 == 0 && c.ffn % 256 == 0 && (c.n_q_heads * hd_s) % 256 == 0,
-              "model: hidden, ffn and q_dim must be multiples of 256");
+    SGQ_CHECK(c.hidden % 256 == 0 && c.ffn % 256 == 0 && (c.n_q_heads * hd_s) % 256 == 0 &&
+                  (c.n_q_heads * hd_g) % 256 == 0,
+              "model: hidden, ffn and both layer kinds' q_dim must be multiples of 256");
+    SGQ_CHECK(c.reserved == 0, "model: the reserved config field must be 0");
     SGQ_CHECK(c.hidden <= 16384, "model: hidden above 16384 (row kernels)");
     SGQ_CHECK(c.ffn <= 65536 && c.n_q_heads * std::max(hd_s, hd_g) <= 65536,
               "model: GEMV K above 65536");

@@ -45,8 +45,7 @@ constexpr size_t kGemvWorkspace = 2048 * 96;
 //   [0, kGemvWorkspace)                GEMV x limb table
 //   [kAttnPartOff, kWorkspaceBytes)    attention split partials
 constexpr int kAttnMaxKv = 1024;
-constexpr size_t kAttnCounterOff = 256 * 1024;
-constexpr size_t kAttnPartOff = kAttnCounterOff + 4096;
+constexpr size_t kAttnPartOff = 256 * 1024 + 4096;
 constexpr size_t kWorkspaceBytes = 16u << 20;
 int launch_gemv_q4_0(hipStream_t st, const void *w, const float *x, float *y, uint32_t n,
                      uint32_t k, void *workspace);
@@ -238,10 +237,8 @@ int launch_attn_decode_generic(hipStream_t st, const float *q, const int8_t *kq,
                                void *xl, const GenericPost *post = nullptr);
 // Sets the attention kernels' launch attributes (call before graph capture).
 int attn_prepare();
-// Decode attention with the step's q/k/v post-projection fused in (and,
-// with merge_in_launch, the split merge: limbs only, counters in the
-// workspace, which must start zeroed): q, k
-// and v_src are the raw projections (v_src may alias k_raw), rope_cs the
+// Decode attention with the step's q/k/v post-projection fused in, then the
+// split merge as a second launch: q, k and v_src are the raw projections (v_src may alias k_raw), rope_cs the
 // (cos, sin) table of the current position; appends the new K/V rows at the
 // current slot (pos % ring, or pos when ring == 0).  head_dim 128.
 int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_raw,
@@ -249,8 +246,7 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
                              const float *rope_cs, float eps, const uint32_t *step, int step_word,
                              uint32_t ring, int8_t *kq, uint16_t *ks, int8_t *vq, uint16_t *vs,
                              int n_q, int n_kv, int n_splits, float scale, float *out,
-                             void *workspace, size_t workspace_bytes, void *limbs_out,
-                             bool merge_in_launch = false);
+                             void *workspace, size_t workspace_bytes, void *limbs_out);
 // Keys before q0 come from the cache (ring: slot = pos % ring), keys from q0
 // on from the chunk's pages ckq.. (row = pos - q0) when given, else the cache.
 // With step non-null, q0 is read on the device from step[3] (the host value

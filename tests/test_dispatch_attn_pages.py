@@ -538,3 +538,17 @@ def test_chunked_sliding_prefill_attend_then_append(ctx, oracle):
                                                          max(0, q0 + i + 1 - 1024), q0 + i)
                                    for h in heads]) for i in range(m)])
         _prefill_check(got[:, heads], want, f"chunk {c}")
+
+
+@pytest.mark.parametrize("kind", ["sliding", "global_q8k"])
+def test_empty_context_merges_to_zero(ctx, oracle, kind):
+    """kv_len 0: every split is empty (m = -3e38, l = 0, acc = 0) and the
+    merged row is 0 (attn_reduce.wgsl's acc/l would be 0/0 here; the
+    reference's graph never runs a step with an empty cache)."""
+    hd, nkv, word = GEOM[kind]
+    q16, _, kbind, _, tv, _ = _pages(oracle, 0xE0E + hd, kind, 64)
+    step = _step(ctx, 0, 0, 0)
+    part, out = _decode(ctx, kind, dev(q16), kbind, tv, step, 4, 1.0)
+    p = host(part).reshape(NQ, 4, hd + 2)
+    assert (p[:, :, hd] == np.float32(-3e38)).all() and (p[:, :, hd + 1] == 0).all()
+    assert (host(out, np.uint16) == 0).all()

@@ -58,3 +58,36 @@ def test_gemv_noalloc_rejects_oversize_and_null(ctx):
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert sgq.lib().sgq_gemv_q4_0_noalloc(stream, None, C.c_void_p(x.data_ptr()),
                                             C.c_void_p(y.data_ptr()), 1, 64) == 6
+
+
+def test_gemv_noalloc_refuses_a_second_stream_while_busy(ctx, oracle):
+    """A call on stream B while the previous call, on stream A, is still
+    queued behind a long kernel is refused (the two would share the scratch
+    array); once A has drained, B is accepted and the result is right."""
+    import sgq
+
+    k, n = 5376, 512
+    rng = oracle.Rng(0x0A12)
+    w, x = rng.random_q4_0(n * k // 32), rng.f32_vec(k)
+    tw, tx = dev(w), dev(x)
+    ya, yb = empty(n, torch.float32), empty(n, torch.float32)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    L = sgq.lib()
+
+    def call(s, y):
+        return L.sgq_gemv_q4_0_noalloc(C.c_void_p(s.cuda_stream), C.c_void_p(tw.data_ptr()),
+                                       C.c_void_p(tx.data_ptr()), C.c_void_p(y.data_ptr()), n, k)
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(200_000_000)  # ~0.1 s of spinning ahead of the call on A
+    assert call(sa, ya) == 0, L.sgq_last_error()
+    assert call(sb, yb) == 6
+    assert b"another stream" in L.sgq_last_error()
+    assert call(sa, ya) == 0  # the same stream is ordered: accepted
+    sa.synchronize()
+    assert call(sb, yb) == 0, L.sgq_last_error()
+    sb.synchronize()
+    assert torch.equal(ya, yb)
+    want = oracle.gemv_rows(w, x, k, np.arange(n))
+    assert rel_err(host(yb), want) <= 1e-4
