@@ -163,19 +163,21 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 //
 // Each wave owns a private ring of kGStages LDS slots and streams exactly
 // the row slices it reduces with global_load_lds_dwordx4 (a lane moves 16 B
-// straight into LDS; the data never occupies VGPRs, so ~5 slices per wave,
-// ~120 KB per CU, stay in flight without hurting occupancy).  A wave waits
-// only on its own vmcnt.  For K <= 5440 a row is one slice and waves never
-// synchronize; for longer K the S = 2 or 4 waves of a workgroup take the S
-// slices of the same row and combine partials through LDS in fixed order
-// (one barrier per row).
+// straight into LDS; the data never occupies VGPRs).  Both slots are filled
+// before the loop; each slot is refilled with the slice two rounds ahead as
+// soon as its words are in registers, so one slice streams in while a row
+// computes.  A wave waits only on its own vmcnt.  For K <= 5440 a row is one
+// slice and waves never synchronize; for longer K the S = 2 or 4 waves of a
+// workgroup take the S slices of the same row and combine partials through
+// LDS in fixed order (one barrier per row).
 // ---------------------------------------------------------------------------
 constexpr int kRWG = 256;                       // 4 waves
-// Three slots (two slices in flight per wave, 12 MB over the chip) beat
-// deeper rings: with more in flight every wave's first slices arrive in one
-// burst and the waves then compute in lockstep while the stream idles
-// (measured at K=5376, N=21504: 14.1 us with 3 slots, 15.8 us with 6).
-constexpr int kGStages = 3;
+// Two slots per wave (3 to 6 MB in flight over the chip, two workgroups per
+// CU): fewer bytes in flight stream faster here.  Measured at K=5376,
+// N=21504 against three slots: 12.8-13.1 vs 13.3-13.5 us (and 15.8 us with
+// six); three or four workgroups per CU, or one, are slower still.
+constexpr int kGStages = 2;
+constexpr int kPreSlices = kGStages;  // slots filled before the loop
 
 // Row r of the concatenated targets -> (matrix, local row).
 __device__ __forceinline__ int target_of(const GemvTargets &tg, int row, int *local) {
@@ -360,6 +362,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     }
     // rounds of rows this workgroup owns (the same for all its waves); only
     // real rounds are fetched, so no wave waits on loads it never uses
+    auto row_of = [&](int it) -> int { return r0 + it * G; };  // row of round `it`
     const int rows_rounds =
         EPI == kEpiGeglu ? 2 * kUnitsPerWave : (n - blockIdx.x * P + G - 1) / G;
     // the weight slice of round `it` into ring slot `slot`
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
                                                  (lvoid_t *)(slot + i * kWave * 16), 16, 0,
                                          kStreamPolicy);
         } else {
-            issue_slice(tg, slot, r0 + it * G, n, row_bytes, slice_off, doff);
+            issue_slice(tg, slot, row_of(it), n, row_bytes, slice_off, doff);
         }
     };
 
@@ -458,9 +461,9 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             : "memory");
         // the stream's first two slices, then the wait for the loads above
         // (the 6 slice loads issued after them may stay in flight)
-        issue(0);
-        issue(1);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 2));
+#pragma unroll
+        for (int j = 0; j < kPreSlices; j++) issue(j);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * kPreSlices));
         auto f4 = [](f32x4_t v) { return make_float4(v.x, v.y, v.z, v.w); };
         pv[0] = f4(t0), pv[1] = f4(t1), pv[2] = f4(t2), pv[3] = f4(t3), pv[4] = f4(t4),
         pv[5] = f4(t5), pv[6] = f4(t6), pv[7] = f4(t7);
@@ -511,12 +514,35 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         }
     }
 
+    // kProTable: this lane's limb table entries (L2-resident), loaded by asm
+    // before the stream so that one wait after the stream's first slices
+    // covers them and leaves the slices in flight
+    f32x4_t g00 = {}, g01 = {}, g02 = {}, g03 = {}, g10 = {}, g11 = {}, g12 = {}, g13 = {},
+            g20 = {}, g21 = {}, g22 = {}, g23 = {};
+    float gd0 = 0.f, gd1 = 0.f, gd2 = 0.f;
+    if (PRO == kProTable) {
+        static_assert(NBL <= 3, "table load layout");
+        const BlockLimbs *t0 = xl + b0 + min(lane, slice_blocks - 1);
+        const BlockLimbs *t1 = xl + b0 + min(lane + kWave, slice_blocks - 1);
+        const BlockLimbs *t2 = xl + b0 + min(lane + 2 * kWave, slice_blocks - 1);
+#define SGQ_LDBLK(A, Q0, Q1, Q2, Q3, D)                                                      \
+    asm volatile("global_load_dwordx4 %0, %5, off\n global_load_dwordx4 %1, %5, off offset:16\n" \
+                 "global_load_dwordx4 %2, %5, off offset:32\n"                                 \
+                 "global_load_dwordx4 %3, %5, off offset:48\n global_load_dword %4, %5, off offset:64" \
+                 : "=&v"(Q0), "=&v"(Q1), "=&v"(Q2), "=&v"(Q3), "=&v"(D)                       \
+                 : "v"(A)                                                                    \
+                 : "memory")
+        SGQ_LDBLK(t0, g00, g01, g02, g03, gd0);
+        if (NBL > 1) SGQ_LDBLK(t1, g10, g11, g12, g13, gd1);
+        if (NBL > 2) SGQ_LDBLK(t2, g20, g21, g22, g23, gd2);
+#undef SGQ_LDBLK
+    }
     // ---- the stream starts ------------------------------------------------
     // (unconditional: a missing round loads row 0, which keeps the number of
     // loads in flight known to the compiler's wait counting)
     if (PRO != kProNorm) {  // (kProNorm started it above)
 #pragma unroll
-        for (int j = 0; j < kGStages - 1; j++) issue(j);
+        for (int j = 0; j < kPreSlices; j++) issue(j);
     }
     asm volatile("" ::: "memory");
 
@@ -528,19 +554,29 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         boff[i] = lb < slice_blocks ? lb * 18 - (lane & 1) * 2 : (lane & 1) * 16;
     }
     if (PRO == kProTable) {
-        // limbs for this lane's blocks, straight from the (L2-resident) table
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int lb = lane + kWave * i;
-            BlockLimbs t = lb < slice_blocks ? xl[b0 + lb] : BlockLimbs{};
-#pragma unroll
-            for (int l = 0; l < kLimbs; l++)
-#pragma unroll
-                for (int w = 0; w < 4; w++) L.q[i][l][w] = t.q[l][w];
-            L.d[i] = t.d;
-        }
-        // the DMA prologue was issued first, so this one wait covers both
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // the wait names the loaded registers, so no copy of them can be
+        // placed ahead of it
+        asm volatile("s_waitcnt vmcnt(%15)"
+                     : "+v"(g00), "+v"(g01), "+v"(g02), "+v"(g03), "+v"(g10), "+v"(g11),
+                       "+v"(g12), "+v"(g13), "+v"(g20), "+v"(g21), "+v"(g22), "+v"(g23),
+                       "+v"(gd0), "+v"(gd1), "+v"(gd2)
+                     : "n"(kRLoads * kPreSlices)
+                     : "memory");
+        // (named vectors, not an array of them: see the LDS table read below)
+        auto f4g = [](f32x4_t v) { return make_float4(v.x, v.y, v.z, v.w); };
+        auto putg = [&](int i, float4 q0, float4 q1, float4 q2, float4 q3, float d) {
+#define SGQ_PUTG(l, Q)                                    \
+    L.q[i][l][0] = __builtin_bit_cast(int, Q.x);          \
+    L.q[i][l][1] = __builtin_bit_cast(int, Q.y);          \
+    L.q[i][l][2] = __builtin_bit_cast(int, Q.z);          \
+    L.q[i][l][3] = __builtin_bit_cast(int, Q.w);
+            SGQ_PUTG(0, q0) SGQ_PUTG(1, q1) SGQ_PUTG(2, q2) SGQ_PUTG(3, q3)
+#undef SGQ_PUTG
+            L.d[i] = lane + kWave * i < slice_blocks ? d : 0.f;
+        };
+        putg(0, f4g(g00), f4g(g01), f4g(g02), f4g(g03), gd0);
+        if (NBL > 1) putg(1, f4g(g10), f4g(g11), f4g(g12), f4g(g13), gd1);
+        if (NBL > 2) putg(2, f4g(g20), f4g(g21), f4g(g22), f4g(g23), gd2);
         if (EPI == kEpiResid) {
             settle(ex);
             settle(ewp);
@@ -673,19 +709,24 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const uint32_t sel = (lane & 1) ? 0x07060504u : 0x05040302u;
     const uint32_t dshift = (lane & 1) ? 16u : 0u;
     float gate = 0.f;                              // kEpiGeglu
+    float held = 0.f;                              // kEpiRows, deferred stores
     for (int it = 0; it < rows_rounds; it++) {
-        const int row = r0 + it * G;
-        if (it + kGStages - 1 < rows_rounds) issue(it + kGStages - 1);
         // wait for round `it`: the slices issued after it may stay in flight
-        static_assert(kGStages == 3, "the wait switch below covers 0..2 rounds ahead");
+        static_assert(kGStages >= 2 && kGStages <= 6, "the wait switch covers 0..5 rounds ahead");
         switch (min(kGStages - 1, rows_rounds - 1 - it)) {
+            case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 5)); break;
+            case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 4)); break;
+            case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 3)); break;
             case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 2)); break;
             case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 1)); break;
             default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
         }
+        float a = 0.f;
         uint32_t wv[NBL][5];
         lds_read_blocks<NBL>(ring + (it % kGStages) * kRSlot, boff, wv);
-        float a = 0.f;
+        // the slot's words are in registers: refill it now, so that all
+        // kGStages slots stream while this row computes
+        if (it + kGStages < rows_rounds) issue(it + kGStages);
 #pragma unroll
         for (int i = 0; i < NBL; i++) a += block_dot(wv[i], sel, dshift, L, i);
         a = wave_sum_dpp(a);
@@ -720,13 +761,19 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
                 a = v;
             }
         }
-        if (!have || row >= n) continue;
-        if (S == 1) {
-            if (lane == 0) store_row(tg, row, a);
-        } else if (tg.split_out) {
-            if (lane == 0) tg.y[0][(size_t)s * n + row] = a;
-        } else {
-            if (lane == 0) store_row(tg, row, a);
+        // rows are stored 64 rounds at a time (lane j: round it0 + j), not
+        // one store per row: a store inside the loop counts in vmcnt and
+        // would make the next slot's wait cover part of a later slice
+        if (have && lane == (it & (kWave - 1))) held = a;
+        if ((it & (kWave - 1)) == kWave - 1 || it == rows_rounds - 1) {
+            const int it0 = it & ~(kWave - 1);
+            const int rowl = row_of(it0 + lane);
+            if (have && lane <= (it & (kWave - 1)) && rowl < n) {
+                if (S > 1 && tg.split_out)
+                    tg.y[0][(size_t)s * n + rowl] = held;
+                else
+                    store_row(tg, rowl, held);
+            }
         }
     }
     if (EPI == kEpiResid) {
@@ -1108,3 +1155,4 @@ extern "C" int sgq_gemv_q4_0_noalloc(void *hip_stream, const void *w, const floa
     }
     return SGQ_OK;
 }
+
