@@ -171,7 +171,11 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // workgroup take the S slices of the same row and combine partials through
 // LDS in fixed order (one barrier per row).
 // ---------------------------------------------------------------------------
-constexpr int kRWG = 256;                       // 4 waves
+// Waves per workgroup.  Eight (one workgroup per CU, half the redundant
+// prologue work per CU) measured slower in the decode step: 218.2 against
+// 225.5 tok/s.
+constexpr int kRWaves = 4;
+constexpr int kRWG = kRWaves * kWave;
 // Two slots per wave (3 to 6 MB in flight over the chip, two workgroups per
 // CU): fewer bytes in flight stream faster here.  Measured at K=5376,
 // N=21504 against three slots: 12.8-13.1 vs 13.3-13.5 us (and 15.8 us with
@@ -228,16 +232,19 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
         tg.y[j][local] = v;
 }
 
-// LDS of the streamed kernel: the wave rings, then 64 B of row partials,
-// 256 B of cross-wave scratch, then (prologues only) the x limb table.
-constexpr int kRingBytes = (kRWG / kWave) * kGStages * kRSlot;
+// LDS of the streamed kernel: the wave rings, then two rounds of row
+// partials (one float per wave), cross-wave scratch, the row results of the
+// residual epilogue (64 rounds per wave), then (prologues only) the x limb
+// table.
+constexpr int kGegluUnits = 8 * kRWaves;  // units (gate/up row pairs) per workgroup
+constexpr int kRingBytes = kRWaves * kGStages * kRSlot;
 constexpr int kRedOff = kRingBytes;
-constexpr int kScrOff = kRedOff + 64;
-constexpr int kRowsOff = kScrOff + 256;    // kEpiResid: row results, 256 floats
-constexpr int kTabOff = kRowsOff + 1024;
+constexpr int kScrOff = kRedOff + 2 * 4 * kRWaves;
+constexpr int kScrBytes = (kGegluUnits * 4 > 16 * kRWaves ? kGegluUnits * 4 : 16 * kRWaves);
+constexpr int kRowsOff = kScrOff + kScrBytes;
+constexpr int kTabOff = kRowsOff + kRWaves * kWave * 4;
 constexpr int kRLds = kTabOff;
 constexpr int kMaxTabBlocks = 3 * kWave;  // one slice: <= 192 blocks
-constexpr int kGegluUnits = 32;           // units (gate/up row pairs) per workgroup
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void lds_write_f32x4(uint8_t *p, float4 v) {
@@ -340,7 +347,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     const int rw = wave / S;             // row within the workgroup's row group
     const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
     uint8_t *ring = gemv_smem + wave * (kGStages * kRSlot);
-    uint8_t *red = gemv_smem + kRedOff;  // [2][4] floats
+    uint8_t *red = gemv_smem + kRedOff;  // [2][waves] floats
     uint8_t *scr = gemv_smem + kScrOff;
     uint8_t *tab = gemv_smem + kTabOff;
     uint8_t *rows_s = gemv_smem + kRowsOff;
@@ -382,7 +389,8 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     };
 
     // ---- prologue loads (before the stream) --------------------------------
-    constexpr int kPB = (kMaxTabBlocks + 31) / 32;  // blocks per 8-lane group
+    constexpr int kGroups = kRWG / 8;                         // 8-lane groups
+    constexpr int kPB = (kMaxTabBlocks + kGroups - 1) / kGroups;  // blocks per group
     const int grp = threadIdx.x >> 3, ge = threadIdx.x & 7;
     float4 pv[kGemvMaxPartials / kWave];
     float4 av[kPB], bv[kPB], xo_in, xo_u;
@@ -413,7 +421,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         const uint32_t ox = (uint32_t)(xo_on ? xo_i : 0) * 16u;
         uint32_t ob[kPB];
 #pragma unroll
-        for (int k = 0; k < kPB; k++) ob[k] = (uint32_t)(min(grp + 32 * k, nb - 1) * 8 + ge) * 16u;
+        for (int k = 0; k < kPB; k++) ob[k] = (uint32_t)(min(grp + kGroups * k, nb - 1) * 8 + ge) * 16u;
         f32x4_t t0, t1, t2, t3, t4, t5, t6, t7, t8, t9;
         if (wave == 0) {
             asm volatile(
@@ -439,8 +447,21 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             : "=&v"(t8), "=&v"(t9)
             : "v"(ox), "s"(xi), "s"(xu)
             : "memory");
-        static_assert(kPB == 6 && kGemvMaxPartials == 8 * kWave, "asm prologue layout");
-        f32x4_t a0, a1, a2, a3, a4, a5, c0, c1, c2, c3, c4, c5;
+        static_assert((kPB == 6 || kPB == 3) && kGemvMaxPartials == 8 * kWave,
+                      "asm prologue layout");
+        f32x4_t a0, a1, a2, a3 = {}, a4 = {}, a5 = {}, c0, c1, c2, c3 = {}, c4 = {}, c5 = {};
+        if constexpr (kPB == 3) {
+            asm volatile(
+                "global_load_dwordx4 %0, %6, %9\n"
+                "global_load_dwordx4 %1, %7, %9\n"
+                "global_load_dwordx4 %2, %8, %9\n"
+                "global_load_dwordx4 %3, %6, %10\n"
+                "global_load_dwordx4 %4, %7, %10\n"
+                "global_load_dwordx4 %5, %8, %10\n"
+                : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(c0), "=&v"(c1), "=&v"(c2)
+                : "v"(ob[0]), "v"(ob[1]), "v"(ob[2]), "s"(A), "s"(B)
+                : "memory");
+        } else
         asm volatile(
             "global_load_dwordx4 %0, %12, %18\n"
             "global_load_dwordx4 %1, %13, %18\n"
@@ -456,8 +477,8 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             "global_load_dwordx4 %11, %17, %19\n"
             : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(a3), "=&v"(a4), "=&v"(a5), "=&v"(c0),
               "=&v"(c1), "=&v"(c2), "=&v"(c3), "=&v"(c4), "=&v"(c5)
-            : "v"(ob[0]), "v"(ob[1]), "v"(ob[2]), "v"(ob[3]), "v"(ob[4]), "v"(ob[5]), "s"(A),
-              "s"(B)
+            : "v"(ob[0]), "v"(ob[1]), "v"(ob[2]), "v"(ob[kPB > 3 ? 3 : 0]),
+              "v"(ob[kPB > 4 ? 4 : 0]), "v"(ob[kPB > 5 ? 5 : 0]), "s"(A), "s"(B)
             : "memory");
         // the stream's first two slices, then the wait for the loads above
         // (the 6 slice loads issued after them may stay in flight)
@@ -468,15 +489,17 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         pv[0] = f4(t0), pv[1] = f4(t1), pv[2] = f4(t2), pv[3] = f4(t3), pv[4] = f4(t4),
         pv[5] = f4(t5), pv[6] = f4(t6), pv[7] = f4(t7);
         xo_in = f4(t8), xo_u = f4(t9);
-        av[0] = f4(a0), av[1] = f4(a1), av[2] = f4(a2), av[3] = f4(a3), av[4] = f4(a4),
-        av[5] = f4(a5);
-        bv[0] = f4(c0), bv[1] = f4(c1), bv[2] = f4(c2), bv[3] = f4(c3), bv[4] = f4(c4),
-        bv[5] = f4(c5);
+        av[0] = f4(a0), av[1] = f4(a1), av[2] = f4(a2);
+        bv[0] = f4(c0), bv[1] = f4(c1), bv[2] = f4(c2);
+        if constexpr (kPB > 3) {
+            av[kPB > 3 ? 3 : 0] = f4(a3), av[kPB > 4 ? 4 : 0] = f4(a4), av[kPB > 5 ? 5 : 0] = f4(a5);
+            bv[kPB > 3 ? 3 : 0] = f4(c3), bv[kPB > 4 ? 4 : 0] = f4(c4), bv[kPB > 5 ? 5 : 0] = f4(c5);
+        }
     } else if (PRO == kProEmbed) {
         const uint8_t *er = fz.embd + (size_t)fz.step[4] * nb * 18;
 #pragma unroll
         for (int k = 0; k < kPB; k++) {
-            const int b = min(grp + 32 * k, nb - 1);
+            const int b = min(grp + kGroups * k, nb - 1);
             const uint8_t *blk = er + b * 18;
             const uint8_t *qs = blk + 2 + ((4 * ge) & 15);
             ed[k] = f16_bits_to_f32(blk[0] | (blk[1] << 8));
@@ -618,7 +641,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             // (same values into the same entry)
 #pragma unroll
             for (int k = 0; k < kPB; k++)
-                limb_words_to_lds(wd[k], dd[k], ge, tab + min(grp + 32 * k, nb - 1) * 80);
+                limb_words_to_lds(wd[k], dd[k], ge, tab + min(grp + kGroups * k, nb - 1) * 80);
             if (xo_on)
                 reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
                     make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
@@ -629,7 +652,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             const int sh = ge < 4 ? 0 : 4;
 #pragma unroll
             for (int k = 0; k < kPB; k++) {
-                const int b = grp + 32 * k;
+                const int b = grp + kGroups * k;
                 x0[k] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (b < nb) {
                     float e[4];
@@ -657,7 +680,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             }
 #pragma unroll
             for (int k = 0; k < kPB; k++)
-                if (grp + 32 * k < nb) limb_words_to_lds(wd[k], dd[k], ge, tab + (grp + 32 * k) * 80);
+                if (grp + kGroups * k < nb) limb_words_to_lds(wd[k], dd[k], ge, tab + (grp + kGroups * k) * 80);
         }
         lds_barrier();
         // this lane's blocks from the LDS table (a lane past the slice reads
@@ -751,7 +774,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             // one barrier per row: partials alternate between two slots, and
             // a slot is rewritten only after the next row's barrier, which
             // the reading wave reaches after its reads
-            uint8_t *rb = red + (it & 1) * 16;
+            uint8_t *rb = red + (it & 1) * 4 * kRWaves;
             if (lane == 0) lds_write_f32(rb + wave * 4, a);
             __builtin_amdgcn_s_barrier();
             have = s == 0;
@@ -807,9 +830,11 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         }
     } else if (EPI == kEpiGeglu) {
         lds_barrier();
-        if (threadIdx.x < 8) {
+        // 8 threads per 32-unit limb block
+        if (threadIdx.x < kGegluUnits / 4) {
             const float4 h = lds_read_f32x4(scr + threadIdx.x * 16);
-            limbs_block8(h, (int)threadIdx.x, &fz.hl[blockIdx.x]);
+            limbs_block8(h, (int)threadIdx.x & 7,
+                         &fz.hl[blockIdx.x * (kGegluUnits / 32) + (threadIdx.x >> 3)]);
         }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // nothing should be left; LDS is released at exit
@@ -832,7 +857,7 @@ int ring_attr() {
 int ring_grid(int n, int S, int epi) {
     if (epi == kEpiGeglu) return n / kGegluUnits;
     const int P = (kRWG / kWave) / S;
-    int grid = device_info().cus * 2;  // two workgroups (8 waves) per CU
+    int grid = device_info().cus * (8 / kRWaves);  // 8 waves per CU
     const int max_grid = (n + P - 1) / P;
     return grid > max_grid ? max_grid : grid;
 }
