@@ -171,11 +171,16 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // workgroup take the S slices of the same row and combine partials through
 // LDS in fixed order (one barrier per row).
 // ---------------------------------------------------------------------------
-// Waves per workgroup.  Eight (one workgroup per CU, half the redundant
-// prologue work per CU) measured slower in the decode step: 218.2 against
-// 225.5 tok/s.
-constexpr int kRWaves = 4;
-constexpr int kRWG = kRWaves * kWave;
+// Waves per workgroup, by prologue and epilogue (the enums are declared in
+// sgq_internal.h).  Eight waves (one workgroup per CU) for the norm and
+// embedding prologues with plain row stores (QKV, the LM head): half the
+// redundant prologue work per CU, 10.6 -> 9.1 us per QKV launch in the
+// decode step.  Four elsewhere: eight made the gate/up launch (GeGLU
+// epilogue, 32-unit limb blocks, so 336 workgroups on 256 CUs) 25.5 ->
+// 29.2 us, and table-fed launches gain nothing.
+constexpr int ring_waves(int pro, int epi) {
+    return (pro == kProNorm || pro == kProEmbed) && epi == kEpiRows ? 8 : 4;
+}
 // Two slots per wave (3 to 6 MB in flight over the chip, two workgroups per
 // CU): fewer bytes in flight stream faster here.  Measured at K=5376,
 // N=21504 against three slots: 12.8-13.1 vs 13.3-13.5 us (and 15.8 us with
@@ -236,14 +241,16 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
 // partials (one float per wave), cross-wave scratch, the row results of the
 // residual epilogue (64 rounds per wave), then (prologues only) the x limb
 // table.
-constexpr int kGegluUnits = 8 * kRWaves;  // units (gate/up row pairs) per workgroup
-constexpr int kRingBytes = kRWaves * kGStages * kRSlot;
-constexpr int kRedOff = kRingBytes;
-constexpr int kScrOff = kRedOff + 2 * 4 * kRWaves;
-constexpr int kScrBytes = (kGegluUnits * 4 > 16 * kRWaves ? kGegluUnits * 4 : 16 * kRWaves);
-constexpr int kRowsOff = kScrOff + kScrBytes;
-constexpr int kTabOff = kRowsOff + kRWaves * kWave * 4;
-constexpr int kRLds = kTabOff;
+constexpr int kGegluUnits = 32;  // units (gate/up row pairs) per workgroup (4 waves)
+template <int WV>
+struct RingLds {
+    static constexpr int kRing = WV * kGStages * kRSlot;
+    static constexpr int kRed = kRing;
+    static constexpr int kScr = kRed + 2 * 4 * WV;
+    static constexpr int kScrBytes = (kGegluUnits * 4 > 16 * WV ? kGegluUnits * 4 : 16 * WV);
+    static constexpr int kRows = kScr + kScrBytes;
+    static constexpr int kTab = kRows + WV * kWave * 4;
+};
 constexpr int kMaxTabBlocks = 3 * kWave;  // one slice: <= 192 blocks
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -303,7 +310,8 @@ __device__ __forceinline__ float gelu_tanh_g(float x) {
 
 // Sum of float4s over the workgroup in a fixed order (every workgroup that
 // sums the same inputs gets the same bits): lanes in DPP order, then the
-// four waves in order through `scr`.
+// WV waves in order through `scr`.
+template <int WV>
 __device__ __forceinline__ float4 wg_sum4(float4 v, uint8_t *scr) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     v.x = wave_sum_dpp(v.x);
@@ -314,7 +322,7 @@ __device__ __forceinline__ float4 wg_sum4(float4 v, uint8_t *scr) {
     lds_barrier();
     float4 r = lds_read_f32x4(scr);
 #pragma unroll
-    for (int w = 1; w < kRWG / kWave; w++) {
+    for (int w = 1; w < WV; w++) {
         const float4 t = lds_read_f32x4(scr + w * 16);
         r.x += t.x, r.y += t.y, r.z += t.z, r.w += t.w;
     }
@@ -336,21 +344,25 @@ __device__ __forceinline__ float4 wg_sum4(float4 v, uint8_t *scr) {
 // through asm accesses, so that the compiler, which cannot tell the table
 // from ring slots still being filled, does not drain the stream first.
 template <int NBL, int PRO, int EPI>
-__global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
+__global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_kernel(GemvTargets tg,
                                                               const BlockLimbs *__restrict__ xl,
                                                               int n, int nb, int S, int slice,
                                                               GemvFuse fz) {
     extern __shared__ __align__(16) uint8_t gemv_smem[];
+    constexpr int WV = ring_waves(PRO, EPI);
+    constexpr int kRWG = WV * kWave;
+    using Lds = RingLds<WV>;
+    static_assert(EPI != kEpiGeglu || WV * 8 == kGegluUnits, "8 GeGLU units per wave");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int s = wave % S;              // K-slice of this wave
     const int rw = wave / S;             // row within the workgroup's row group
     const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
     uint8_t *ring = gemv_smem + wave * (kGStages * kRSlot);
-    uint8_t *red = gemv_smem + kRedOff;  // [2][waves] floats
-    uint8_t *scr = gemv_smem + kScrOff;
-    uint8_t *tab = gemv_smem + kTabOff;
-    uint8_t *rows_s = gemv_smem + kRowsOff;
+    uint8_t *red = gemv_smem + Lds::kRed;  // [2][waves] floats
+    uint8_t *scr = gemv_smem + Lds::kScr;
+    uint8_t *tab = gemv_smem + Lds::kTab;
+    uint8_t *rows_s = gemv_smem + Lds::kRows;
     const size_t row_bytes = (size_t)nb * 18;
     const int b0 = s * slice;
     const int slice_blocks = min(slice, nb - b0);
@@ -668,7 +680,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
                         reinterpret_cast<float4 *>(fz.x_out)[i4] = x0[k];
                 }
             }
-            const float4 t = wg_sum4(make_float4(ss, 0.f, 0.f, 0.f), scr);
+            const float4 t = wg_sum4<WV>(make_float4(ss, 0.f, 0.f, 0.f), scr);
             const float r = 1.0f / sqrtf(t.x / (float)(nb * 32) + fz.eps);
             uint32_t wd[kPB][kLimbs];
             float dd[kPB];
@@ -774,7 +786,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
             // one barrier per row: partials alternate between two slots, and
             // a slot is rewritten only after the next row's barrier, which
             // the reading wave reaches after its reads
-            uint8_t *rb = red + (it & 1) * 4 * kRWaves;
+            uint8_t *rb = red + (it & 1) * 4 * WV;
             if (lane == 0) lds_write_f32(rb + wave * 4, a);
             __builtin_amdgcn_s_barrier();
             have = s == 0;
@@ -822,7 +834,7 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
         if (threadIdx.x == 0) {
             float4 r = lds_read_f32x4(scr);
 #pragma unroll
-            for (int w = 1; w < kRWG / kWave; w++) {
+            for (int w = 1; w < WV; w++) {
                 const float4 q = lds_read_f32x4(scr + w * 16);
                 r.x += q.x, r.y += q.y, r.z += q.z, r.w += q.w;
             }
@@ -840,7 +852,10 @@ __global__ __launch_bounds__(kRWG) void gemv_q4_0_ring_kernel(GemvTargets tg,
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // nothing should be left; LDS is released at exit
 }
 
-constexpr int lds_bytes(int pro, int nb) { return kRLds + (pro != kProTable ? nb * 80 : 0); }
+constexpr int lds_bytes(int pro, int epi, int nb) {
+    return (ring_waves(pro, epi) == 8 ? RingLds<8>::kTab : RingLds<4>::kTab) +
+           (pro != kProTable ? nb * 80 : 0);
+}
 
 template <int NBL, int PRO, int EPI>
 int ring_attr() {
@@ -848,16 +863,17 @@ int ring_attr() {
     if (!attr) {
         SGQ_HIP(hipFuncSetAttribute((const void *)gemv_q4_0_ring_kernel<NBL, PRO, EPI>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    lds_bytes(PRO, kMaxTabBlocks)));
+                                    lds_bytes(PRO, EPI, kMaxTabBlocks)));
         attr = true;
     }
     return SGQ_OK;
 }
 
-int ring_grid(int n, int S, int epi) {
+int ring_grid(int n, int S, int pro, int epi) {
     if (epi == kEpiGeglu) return n / kGegluUnits;
-    const int P = (kRWG / kWave) / S;
-    int grid = device_info().cus * (8 / kRWaves);  // 8 waves per CU
+    const int wv = ring_waves(pro, epi);
+    const int P = wv / S;
+    int grid = device_info().cus * (8 / wv);  // 8 waves per CU
     const int max_grid = (n + P - 1) / P;
     return grid > max_grid ? max_grid : grid;
 }
@@ -866,9 +882,10 @@ template <int NBL, int PRO, int EPI>
 int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int n, int nb, int S,
                 int slice, const GemvFuse &fz) {
     if (int rc = ring_attr<NBL, PRO, EPI>()) return rc;
-    const int grid = ring_grid(n, S, EPI);
-    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL, PRO, EPI>), dim3(grid), dim3(kRWG),
-                       lds_bytes(PRO, nb), st, tg, xl, n, nb, S, slice, fz);
+    const int grid = ring_grid(n, S, PRO, EPI);
+    hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL, PRO, EPI>), dim3(grid),
+                       dim3(ring_waves(PRO, EPI) * kWave), lds_bytes(PRO, EPI, nb), st, tg, xl, n,
+                       nb, S, slice, fz);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
 }
@@ -957,7 +974,7 @@ int gemv_prepare() {
 int gemv_fused_grid(uint32_t n, uint32_t k, int epi) {
     int S, slice;
     if (k % 256 != 0 || k == 0 || k > 65536 || !ring_geometry((int)(k / 32), &S, &slice)) return 0;
-    return ring_grid((int)n, S, epi);
+    return ring_grid((int)n, S, kProTable, epi);  // (the residual epilogue's launches)
 }
 
 int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k, int pro,
@@ -986,7 +1003,7 @@ int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uin
         SGQ_CHECK(tg.count == 1 && !tg.split_out && tg.softcap == 0.f && fz.x_res && fz.w_post &&
                       fz.w_next && fz.u_out && fz.A_out && fz.B_out && fz.part_out,
                   "gemv (fused): residual epilogue inputs");
-        const int G = ring_grid(n, S, epi) * ((kRWG / kWave) / S);
+        const int G = ring_grid(n, S, pro, epi) * (ring_waves(pro, epi) / S);
         SGQ_CHECK((n + G - 1) / G <= kWave, "gemv (fused): more than %d rows per wave", kWave);
     }
     SGQ_CHECK(!tg.split_out || (tg.count == 1 && tg.softcap == 0.f && epi == kEpiRows),
