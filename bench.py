@@ -683,7 +683,7 @@ def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
             rc = lib.sgq_gemv_q4_0_limbs(ctx.handle, 1, wp, yp, rows, C.c_void_p(xl.data_ptr()),
                                          k, 0.0)
             assert rc == 0, sgq.lib().sgq_last_error()
-    def full(m):  # the whole typed call: fp32 x -> limbs -> streamed kernel
+    def full(m):  # the whole typed call: fp32 x in, the limbs built in the kernel
         for j in range(m):
             rc = lib.sgq_gemv_q4_0(ctx.handle, C.c_void_p(w_ptrs[j % len(w_ptrs)]),
                                    C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr()), n, k)
@@ -710,7 +710,7 @@ def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
             "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic(),
             "kernel": f"gemv_q4_0_ring_kernel K={k} N={n}", "bytes_per_launch": nbytes,
             "us_per_launch": ms * 1e3, "launches": steps,
-            "full_call": {"what": "sgq_gemv_q4_0 (fp32 x -> limb kernel -> streamed kernel)",
+            "full_call": {"what": "sgq_gemv_q4_0 (fp32 x; limbs built in the streamed kernel's prologue)",
                           "us_per_call": ms_full * 1e3, "achieved": full_gbs,
                           "frac": full_gbs / HBM_PEAK_GBS, "bytes_per_call": full_bytes}}
 

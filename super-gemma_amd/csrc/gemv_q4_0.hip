@@ -175,11 +175,14 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // sgq_internal.h).  Eight waves (one workgroup per CU) for the norm and
 // embedding prologues with plain row stores (QKV, the LM head): half the
 // redundant prologue work per CU, 10.6 -> 9.1 us per QKV launch in the
-// decode step.  Four elsewhere: eight made the gate/up launch (GeGLU
+// decode step; and the x prologue of the typed call (full call at config 1
+// 14.4-14.6 us with a separate limb kernel, 13.0-13.4 with the prologue in
+// eight-wave workgroups, 13.5-14.6 in four-wave ones).  Four elsewhere:
+// eight made the gate/up launch (GeGLU
 // epilogue, 32-unit limb blocks, so 336 workgroups on 256 CUs) 25.5 ->
 // 29.2 us, and table-fed launches gain nothing.
 constexpr int ring_waves(int pro, int epi) {
-    return (pro == kProNorm || pro == kProEmbed) && epi == kEpiRows ? 8 : 4;
+    return (pro == kProNorm || pro == kProEmbed || pro == kProX) && epi == kEpiRows ? 8 : 4;
 }
 // Two slots per wave (3 to 6 MB in flight over the chip, two workgroups per
 // CU): fewer bytes in flight stream faster here.  Measured at K=5376,
@@ -519,6 +522,13 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                     ((uint32_t)qs[3] << 24);
             av[k] = reinterpret_cast<const float4 *>(fz.w)[b * 8 + ge];
         }
+    } else if (PRO == kProX) {
+#pragma unroll
+        for (int k = 0; k < kPB; k++) {
+            const int i4 = min(grp + kGroups * k, nb - 1) * 8 + ge;
+            av[k] = fz.x_half ? act_ld4(static_cast<const uint16_t *>(fz.x_raw), i4)
+                              : act_ld4(static_cast<const float *>(fz.x_raw), i4);
+        }
     }
     // kEpiResid: lane j holds the per-row inputs of round j
     float ex = 0.f, ewp = 0.f, ewn = 0.f;
@@ -541,6 +551,10 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 settle(eq[k]);
                 settle(av[k]);
             }
+        }
+        if (PRO == kProX) {
+#pragma unroll
+            for (int k = 0; k < kPB; k++) settle(av[k]);
         }
         if (EPI == kEpiResid) {
             settle(ex);
@@ -658,6 +672,14 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
                     make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
                                 s_out * (xo_in.z + ra * xo_u.z), s_out * (xo_in.w + ra * xo_u.w));
+        } else if (PRO == kProX) {
+            uint32_t wd[kPB][kLimbs];
+            float dd[kPB];
+#pragma unroll
+            for (int k = 0; k < kPB; k++) dd[k] = limbs_words8(av[k], ge, wd[k]);
+#pragma unroll
+            for (int k = 0; k < kPB; k++)
+                if (grp + kGroups * k < nb) limb_words_to_lds(wd[k], dd[k], ge, tab + (grp + kGroups * k) * 80);
         } else {  // kProEmbed
             float4 x0[kPB];
             float ss = 0.f;
@@ -946,6 +968,8 @@ static int launch_ring_any(hipStream_t st, const GemvTargets &tg, const BlockLim
         return launch_ring_nbl<kProNorm, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProEmbed && epi == kEpiRows)
         return launch_ring_nbl<kProEmbed, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProX && epi == kEpiRows)
+        return launch_ring_nbl<kProX, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProNorm && epi == kEpiGeglu)
         return launch_ring_nbl<kProNorm, kEpiGeglu>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProTable && epi == kEpiResid)
@@ -966,6 +990,7 @@ int gemv_prepare() {
     int rc = attr_nbl<kProTable, kEpiRows>();
     if (!rc) rc = attr_nbl<kProNorm, kEpiRows>();
     if (!rc) rc = attr_nbl<kProEmbed, kEpiRows>();
+    if (!rc) rc = attr_nbl<kProX, kEpiRows>();
     if (!rc) rc = attr_nbl<kProNorm, kEpiGeglu>();
     if (!rc) rc = attr_nbl<kProTable, kEpiResid>();
     return rc;
@@ -992,6 +1017,7 @@ int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uin
                                   fz.B && (!fz.x_out || (fz.x_in && fz.u))),
               "gemv (fused): norm prologue inputs");
     SGQ_CHECK(pro != kProEmbed || (fz.embd && fz.step && fz.w), "gemv (fused): embed inputs");
+    SGQ_CHECK(pro != kProX || fz.x_raw, "gemv (fused): x prologue input");
     int n = tg.end[tg.count - 1];
     if (epi == kEpiGeglu) {
         SGQ_CHECK(tg.count == 2 && tg.end[0] > 0 && tg.end[1] == 2 * tg.end[0] &&
@@ -1069,18 +1095,25 @@ int gemv_q4_0_t(hipStream_t st, const void *w, const TX *x, TY *y, uint32_t n, u
     SGQ_CHECK(((uintptr_t)x & (4 * sizeof(TX) - 1)) == 0, "gemv_q4_0: x must be %zu-byte aligned",
               4 * sizeof(TX));
     const int nb = (int)(k / 32);
-    // Streamed path: 16-byte aligned rows (K % 256 == 0), x limbs prepared
-    // once into the workspace, row slices of <= 170 blocks.
+    // Streamed path: 16-byte aligned rows (K % 256 == 0), row slices of
+    // <= 170 blocks; x limbs built in the kernel's prologue (one slice per
+    // row) or prepared once into the workspace (2 or 4 slices).
     int S, slice;
     if (((uintptr_t)w & 15) == 0 && workspace != nullptr && ring_geometry(nb, &S, &slice)) {
-        int rc = launch_quant_limbs(st, x, workspace, k);
-        if (rc) return rc;
         GemvTargets tg{};
         tg.w[0] = w;
         tg.y[0] = reinterpret_cast<float *>(y);
         tg.half_out = sizeof(TY) == 2;
         tg.end[0] = (int)n;
         tg.count = 1;
+        if (S == 1) {  // one K-slice: every workgroup builds the limb table itself
+            GemvFuse fz{};
+            fz.x_raw = x;
+            fz.x_half = sizeof(TX) == 2;
+            return launch_ring_any(st, tg, nullptr, (int)n, nb, S, slice, kProX, kEpiRows, fz);
+        }
+        int rc = launch_quant_limbs(st, x, workspace, k);
+        if (rc) return rc;
         return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(workspace), (int)n, nb, S,
                                slice);
     }

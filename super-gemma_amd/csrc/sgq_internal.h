@@ -96,7 +96,9 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uin
 //              rmsnorm(x_out)∘w_next, with A = x_in∘w_next, u = o∘w_post,
 //              B = u∘w_next;
 //   kProEmbed  x0 = dequant(embd[step[4]])·embed_scale, f = rmsnorm(x0)∘w,
-//              x_out = x0 (sliced).
+//              x_out = x0 (sliced);
+//   kProX      f = x_raw (fp32, or f16 when x_half), split into limbs by
+//              every workgroup.
 // Epilogue (what is done with the output rows o):
 //   kEpiRows   stored to the targets (softcap, split_out as GemvTargets);
 //   kEpiResid  single target: per row u = o·w_post, A = x_res·w_next,
@@ -105,7 +107,7 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uin
 //   kEpiGeglu  targets gate (w[0]) and up (w[1]), n = units: workgroup b
 //              computes units [32b, 32b+32) and writes block b of the limbs
 //              of gelu_tanh(gate)·up into hl.
-enum { kProTable = 0, kProNorm = 1, kProEmbed = 2 };
+enum { kProTable = 0, kProNorm = 1, kProEmbed = 2, kProX = 3 };
 enum { kEpiRows = 0, kEpiResid = 1, kEpiGeglu = 2 };
 constexpr int kGemvMaxPartials = 512;
 struct GemvFuse {
@@ -122,6 +124,8 @@ struct GemvFuse {
     float *u_out, *A_out, *B_out;
     float4 *part_out;
     struct BlockLimbs *hl;
+    const void *x_raw;  // kProX
+    int x_half;
 };
 // Workgroups a fused launch uses (= the np its kEpiResid partials need).
 int gemv_fused_grid(uint32_t n, uint32_t k, int epi);
