@@ -6,11 +6,31 @@
 namespace sgq {
 namespace {
 
-// Grid (split, kv head): consecutive workgroups take consecutive splits of
-// one kv head.  Over the slot-major cache ([slot][kv head][128]) that
-// streams faster than the 16 heads of one split side by side: 140.5 vs
-// 144.7 us at 128K, 40.0 vs 42.1 at 32K (a read-only probe of the same
-// pattern: 5.7 vs 4.7 TB/s).
+// Workgroup order (a 1-D grid of n_splits·n_kv): workgroup i runs on XCD
+// i % 8, and each XCD takes 4 kv heads of one split side by side, then the
+// next split (split ≡ XCD mod 8), then the next 4 heads.  The f16 scale
+// pages hold the 16 heads of a slot in one 128-byte line, so heads of the
+// same slots that run at the same time on the same XCD share its fetch
+// (128K: 946 -> 820 MB of HBM reads per launch against 570 MB
+// algorithmic), while consecutive splits of a head keep the K/V rows
+// streaming (side by side, 16 heads per split read the cache 4.7 against
+// 5.7 TB/s in a read-only probe).  Measured: 128K 140.5 -> 135.0 us, 32K
+// 40.2 -> 40.5 us, against consecutive splits of one head; all 16 heads
+// side by side: 134.6 and 41.3 us.
+__device__ __forceinline__ void attn_work_item(int n_kv, int n_splits, int *kvh, int *split) {
+    constexpr int HG = 4;
+    const int id = blockIdx.x;
+    if (n_splits % 8 == 0 && n_kv % HG == 0) {
+        const int x = id % 8, a = id / 8, S8 = n_splits / 8;
+        const int t = a / HG;
+        *split = (t % S8) * 8 + x;
+        *kvh = (t / S8) * HG + a % HG;
+    } else {
+        *split = id % n_splits;
+        *kvh = id / n_splits;
+    }
+}
+
 template <int QPK, bool FUSED, int W>
 __global__ __launch_bounds__(W * kWave) void attn_decode_q8_kernel(
     const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
@@ -19,8 +39,10 @@ __global__ __launch_bounds__(W * kWave) void attn_decode_q8_kernel(
     int n_splits, float scale, float *__restrict__ part, float *__restrict__ out,
     BlockLimbs *__restrict__ limbs_out, AttnPost post) {
     const uint32_t kv_len = step ? step[step_word] : kv_len_direct;
+    int kvh, split;
+    attn_work_item(n_kv, n_splits, &kvh, &split);
     attn_chunk<QPK, FUSED, W>(q, kq, ks, vq, vs, kv_len, n_kv, n_splits, scale, part, out,
-                              limbs_out, post, blockIdx.y, blockIdx.x, FUSED ? step[0] : 0u);
+                              limbs_out, post, kvh, split, FUSED ? step[0] : 0u);
 }
 
 // Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
@@ -79,7 +101,7 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
               kAttnPartOff + part_bytes);
     float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + kAttnPartOff);
     const int qpk = n_q / n_kv;
-    dim3 grid(n_splits, n_kv);
+    const dim3 grid(n_splits * n_kv);
     SGQ_CHECK(qpk == 1 || qpk == 2, "attn_decode_q8: %d q heads per kv head unsupported", qpk);
     BlockLimbs *lo = static_cast<BlockLimbs *>(limbs_out);
     float *out1 = n_splits == 1 ? out : nullptr;
@@ -111,7 +133,7 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
     SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0 && ((uintptr_t)ks & 7) == 0 &&
                   ((uintptr_t)vs & 7) == 0 && ((uintptr_t)part & 3) == 0,
               "attn_decode (parts): misaligned operand");
-    dim3 grid(n_splits, n_kv);
+    const dim3 grid(n_splits * n_kv);
     if (n_q == n_kv)
         hipLaunchKernelGGL((attn_decode_q8_kernel<1, false, kAttnWaves>), grid,
                            dim3(kAttnWaves * kWave), 0, st, q, kq, ks, vq, vs, step, step_word, 0u,
@@ -156,7 +178,7 @@ int launch_attn_decode_fused(hipStream_t st, const float *q_raw, const float *k_
     const AttnPost post{q_raw, k_raw, v_src, wq_norm, wk_norm, rope_cs, eps, (int)ring,
                         kq, vq, ks, vs};
     if (int rc = attn_prepare()) return rc;
-    dim3 grid(n_splits, n_kv);
+    const dim3 grid(n_splits * n_kv);
     const int qpk = n_q / n_kv;
     SGQ_CHECK(qpk == 1 || qpk == 2, "attn (fused): %d q heads per kv head unsupported", qpk);
     BlockLimbs *lo = static_cast<BlockLimbs *>(limbs_out);
