@@ -175,14 +175,16 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // sgq_internal.h).  Eight waves (one workgroup per CU) for the norm and
 // embedding prologues with plain row stores (QKV, the LM head): half the
 // redundant prologue work per CU, 10.6 -> 9.1 us per QKV launch in the
-// decode step; and the x prologue of the typed call (full call at config 1
+// decode step; the table-fed call with the table copied into LDS once per
+// workgroup instead of once per wave (config 1, 8 interleaved runs: median
+// 12.40 against 13.3 us); and the x prologue of the typed call (full call at config 1
 // 14.4-14.6 us with a separate limb kernel, 13.0-13.4 with the prologue in
 // eight-wave workgroups, 13.5-14.6 in four-wave ones).  Four elsewhere:
 // eight made the gate/up launch (GeGLU
 // epilogue, 32-unit limb blocks, so 336 workgroups on 256 CUs) 25.5 ->
 // 29.2 us, and table-fed launches gain nothing.
 constexpr int ring_waves(int pro, int epi) {
-    return (pro == kProNorm || pro == kProEmbed || pro == kProX) && epi == kEpiRows ? 8 : 4;
+    return (pro == kProNorm || pro == kProEmbed || pro == kProX || pro == kProTableLds) && epi == kEpiRows ? 8 : 4;
 }
 // Two slots per wave (3 to 6 MB in flight over the chip, two workgroups per
 // CU): fewer bytes in flight stream faster here.  Measured at K=5376,
@@ -522,6 +524,15 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                     ((uint32_t)qs[3] << 24);
             av[k] = reinterpret_cast<const float4 *>(fz.w)[b * 8 + ge];
         }
+    } else if (PRO == kProTableLds) {
+        // the limb table (nb·80 B, L2-resident, shared by every workgroup)
+        // into LDS by DMA, 16 B per lane; lanes past its end repeat the last
+        // chunk into the slack after it
+        const int chunks = nb * 5;
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(xl);
+        for (int c = wave * kWave; c < chunks; c += kRWG)
+            __builtin_amdgcn_global_load_lds((gvoid_t *)(src + min(c + lane, chunks - 1) * 16),
+                                             (lvoid_t *)(tab + c * 16), 16, 0, 0);
     } else if (PRO == kProX) {
 #pragma unroll
         for (int k = 0; k < kPB; k++) {
@@ -672,6 +683,9 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
                     make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
                                 s_out * (xo_in.z + ra * xo_u.z), s_out * (xo_in.w + ra * xo_u.w));
+        } else if (PRO == kProTableLds) {
+            // the table's DMA was issued before the stream's first slices
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * kPreSlices));
         } else if (PRO == kProX) {
             uint32_t wd[kPB][kLimbs];
             float dd[kPB];
@@ -876,7 +890,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
 
 constexpr int lds_bytes(int pro, int epi, int nb) {
     return (ring_waves(pro, epi) == 8 ? RingLds<8>::kTab : RingLds<4>::kTab) +
-           (pro != kProTable ? nb * 80 : 0);
+           (pro != kProTable ? nb * 80 : 0) + (pro == kProTableLds ? kWave * 16 : 0);
 }
 
 template <int NBL, int PRO, int EPI>
@@ -970,6 +984,10 @@ static int launch_ring_any(hipStream_t st, const GemvTargets &tg, const BlockLim
         return launch_ring_nbl<kProEmbed, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProX && epi == kEpiRows)
         return launch_ring_nbl<kProX, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProTableLds && epi == kEpiRows)
+        return launch_ring_nbl<kProTableLds, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProTableLds && epi == kEpiResid)
+        return launch_ring_nbl<kProTableLds, kEpiResid>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProNorm && epi == kEpiGeglu)
         return launch_ring_nbl<kProNorm, kEpiGeglu>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProTable && epi == kEpiResid)
@@ -991,15 +1009,17 @@ int gemv_prepare() {
     if (!rc) rc = attr_nbl<kProNorm, kEpiRows>();
     if (!rc) rc = attr_nbl<kProEmbed, kEpiRows>();
     if (!rc) rc = attr_nbl<kProX, kEpiRows>();
+    if (!rc) rc = attr_nbl<kProTableLds, kEpiRows>();
+    if (!rc) rc = attr_nbl<kProTableLds, kEpiResid>();
     if (!rc) rc = attr_nbl<kProNorm, kEpiGeglu>();
     if (!rc) rc = attr_nbl<kProTable, kEpiResid>();
     return rc;
 }
 
-int gemv_fused_grid(uint32_t n, uint32_t k, int epi) {
+int gemv_fused_grid(uint32_t n, uint32_t k, int epi, int pro) {
     int S, slice;
     if (k % 256 != 0 || k == 0 || k > 65536 || !ring_geometry((int)(k / 32), &S, &slice)) return 0;
-    return ring_grid((int)n, S, kProTable, epi);  // (the residual epilogue's launches)
+    return ring_grid((int)n, S, pro, epi);  // (the residual epilogue's launches)
 }
 
 int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k, int pro,
@@ -1012,7 +1032,7 @@ int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     const int nb = (int)(k / 32);
     SGQ_CHECK(ring_geometry(nb, &S, &slice), "gemv (fused): k=%u outside the streamed geometry", k);
     SGQ_CHECK(pro == kProTable || S == 1, "gemv (fused): prologues need k <= %d", kRSlot / 18 * 32);
-    SGQ_CHECK(pro != kProTable || xl != nullptr, "gemv (fused): no limb table");
+    SGQ_CHECK((pro != kProTable && pro != kProTableLds) || xl != nullptr, "gemv (fused): no limb table");
     SGQ_CHECK(pro != kProNorm || (fz.part && fz.np > 0 && fz.np <= kGemvMaxPartials && fz.A &&
                                   fz.B && (!fz.x_out || (fz.x_in && fz.u))),
               "gemv (fused): norm prologue inputs");
@@ -1080,6 +1100,9 @@ int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     SGQ_CHECK(!tg.split_out || (tg.count == 1 && tg.softcap == 0.f),
               "gemv (limbs): split output needs one target and no softcap");
     SGQ_CHECK(!tg.half_out || !tg.split_out, "gemv (limbs): f16 output with split output");
+    if (S == 1)  // one K-slice: the table goes to LDS once per workgroup
+        return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1],
+                               nb, S, slice, kProTableLds, kEpiRows);
     return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1], nb,
                            S, slice);
 }

@@ -866,7 +866,9 @@ int record_step_fused(sgq_model *m, float *logits) {
     for (size_t li = 0; li < nl; li++) {
         const LayerW &L = m->layers[li];
         const int hd = (int)L.hd, nkv = (int)L.n_kv, QD = nq * hd, KD = nkv * hd;
-        const int np_o = gemv_fused_grid((uint32_t)H, (uint32_t)QD, kEpiResid);
+        // O's limb table into LDS once per workgroup when it is one K-slice
+        const int pro_o = gemv_slices((uint32_t)QD) == 1 ? kProTableLds : kProTable;
+        const int np_o = gemv_fused_grid((uint32_t)H, (uint32_t)QD, kEpiResid, pro_o);
         SGQ_CHECK(np_o > 0 && np_o <= kGemvMaxPartials, "model (fused): partial sums %d", np_o);
         GemvTargets qkv{};
         qkv.w[0] = L.wq, qkv.w[1] = L.wk, qkv.w[2] = L.wv;
@@ -925,7 +927,7 @@ int record_step_fused(sgq_model *m, float *logits) {
         GemvFuse eo{};
         eo.x_res = xa, eo.w_post = L.post_attn_norm, eo.w_next = L.ffn_norm;
         eo.u_out = m->fx.u, eo.A_out = m->fx.a, eo.B_out = m->fx.b, eo.part_out = m->fx.part;
-        if ((rc = launch_gemv_fused(st, ot, m->fx.xl_o, (uint32_t)QD, kProTable, kEpiResid, eo)))
+        if ((rc = launch_gemv_fused(st, ot, m->fx.xl_o, (uint32_t)QD, pro_o, kEpiResid, eo)))
             return rc;
         GemvTargets gu{};
         gu.w[0] = L.wg, gu.w[1] = L.wu, gu.y[0] = m->g, gu.y[1] = m->u;

@@ -86,7 +86,10 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uin
                      float *y, uint32_t n, uint32_t k, float softcap);
 // Fused forms of the streamed GEMV (single K-slice for the prologues).
 // Prologue (what the GEMV's x limbs are computed from, inside the launch):
-//   kProTable  the limb table xl (written by an earlier kernel);
+//   kProTable  the limb table xl (written by an earlier kernel), each wave
+//              loading its lanes' entries into registers;
+//   kProTableLds  the same table copied into LDS once per workgroup by
+//              DMA (single K-slice only);
 //   kProNorm   f = rb·s·(A + ra·B) with ra = 1/sqrt(P1/K + eps),
 //              rb = 1/sqrt(s²(P4 + 2·ra·P2 + ra²·P3)/K + eps) from the np
 //              partial sums (P1..P4) an kEpiResid launch left in part, and
@@ -107,7 +110,7 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uin
 //   kEpiGeglu  targets gate (w[0]) and up (w[1]), n = units: workgroup b
 //              computes units [32b, 32b+32) and writes block b of the limbs
 //              of gelu_tanh(gate)·up into hl.
-enum { kProTable = 0, kProNorm = 1, kProEmbed = 2, kProX = 3 };
+enum { kProTable = 0, kProNorm = 1, kProEmbed = 2, kProX = 3, kProTableLds = 4 };
 enum { kEpiRows = 0, kEpiResid = 1, kEpiGeglu = 2 };
 constexpr int kGemvMaxPartials = 512;
 struct GemvFuse {
@@ -128,7 +131,7 @@ struct GemvFuse {
     int x_half;
 };
 // Workgroups a fused launch uses (= the np its kEpiResid partials need).
-int gemv_fused_grid(uint32_t n, uint32_t k, int epi);
+int gemv_fused_grid(uint32_t n, uint32_t k, int epi, int pro = kProTable);
 int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uint32_t k, int pro,
                       int epi, const GemvFuse &fz);
 
