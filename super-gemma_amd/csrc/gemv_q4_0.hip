@@ -179,7 +179,8 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // workgroup instead of once per wave (config 1, 8 interleaved runs: median
 // 12.40 against 13.3 us); and the x prologue of the typed call (full call at config 1
 // 14.4-14.6 us with a separate limb kernel, 13.0-13.4 with the prologue in
-// eight-wave workgroups, 13.5-14.6 in four-wave ones).  Four elsewhere:
+// eight-wave workgroups, 13.5-14.6 in four-wave ones; its x loads issued
+// ahead of the weight stream and waited for behind it: 12.95 -> 12.57 us).  Four elsewhere:
 // eight made the gate/up launch (GeGLU
 // epilogue, 32-unit limb blocks, so 336 workgroups on 256 CUs) 25.5 ->
 // 29.2 us, and table-fed launches gain nothing.
@@ -259,6 +260,7 @@ struct RingLds {
 constexpr int kMaxTabBlocks = 3 * kWave;  // one slice: <= 192 blocks
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void lds_write_f32x4(uint8_t *p, float4 v) {
     const uint32_t a = (uint32_t)(uintptr_t)p;
     const f32x4_t t = {v.x, v.y, v.z, v.w};
@@ -411,6 +413,8 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     const int grp = threadIdx.x >> 3, ge = threadIdx.x & 7;
     float4 pv[kGemvMaxPartials / kWave];
     float4 av[kPB], bv[kPB], xo_in, xo_u;
+    [[maybe_unused]] f32x4_t xq0 = {}, xq1 = {}, xq2 = {};  // kProX, fp32 x (asm loads)
+    [[maybe_unused]] i32x2_t xh0 = {}, xh1 = {}, xh2 = {};  // kProX, f16 x (asm loads)
     uint32_t eq[kPB];  // kProEmbed: 4 nibble bytes of the lane's values
     float ed[kPB];
     const int H4 = nb * 8;  // float4s of x
@@ -534,12 +538,24 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
             __builtin_amdgcn_global_load_lds((gvoid_t *)(src + min(c + lane, chunks - 1) * 16),
                                              (lvoid_t *)(tab + c * 16), 16, 0, 0);
     } else if (PRO == kProX) {
+        static_assert(PRO != kProX || kPB == 3, "x load layout");
+        uint32_t xo[kPB];
 #pragma unroll
-        for (int k = 0; k < kPB; k++) {
-            const int i4 = min(grp + kGroups * k, nb - 1) * 8 + ge;
-            av[k] = fz.x_half ? act_ld4(static_cast<const uint16_t *>(fz.x_raw), i4)
-                              : act_ld4(static_cast<const float *>(fz.x_raw), i4);
-        }
+        for (int k = 0; k < kPB; k++) xo[k] = (uint32_t)(min(grp + kGroups * k, nb - 1) * 8 + ge);
+        if (fz.x_half)
+            asm volatile(
+                "global_load_dwordx2 %0, %3, %6\n global_load_dwordx2 %1, %4, %6\n"
+                "global_load_dwordx2 %2, %5, %6"
+                : "=&v"(xh0), "=&v"(xh1), "=&v"(xh2)
+                : "v"(xo[0] * 8u), "v"(xo[1] * 8u), "v"(xo[2] * 8u), "s"(fz.x_raw)
+                : "memory");
+        else
+            asm volatile(
+                "global_load_dwordx4 %0, %3, %6\n global_load_dwordx4 %1, %4, %6\n"
+                "global_load_dwordx4 %2, %5, %6"
+                : "=&v"(xq0), "=&v"(xq1), "=&v"(xq2)
+                : "v"(xo[0] * 16u), "v"(xo[1] * 16u), "v"(xo[2] * 16u), "s"(fz.x_raw)
+                : "memory");
     }
     // kEpiResid: lane j holds the per-row inputs of round j
     float ex = 0.f, ewp = 0.f, ewn = 0.f;
@@ -562,10 +578,6 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 settle(eq[k]);
                 settle(av[k]);
             }
-        }
-        if (PRO == kProX) {
-#pragma unroll
-            for (int k = 0; k < kPB; k++) settle(av[k]);
         }
         if (EPI == kEpiResid) {
             settle(ex);
@@ -687,6 +699,23 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
             // the table's DMA was issued before the stream's first slices
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * kPreSlices));
         } else if (PRO == kProX) {
+            // the x loads were issued before the stream's first slices; the
+            // wait names their registers (as the table's above)
+            asm volatile("s_waitcnt vmcnt(%6)"
+                         : "+v"(xq0), "+v"(xq1), "+v"(xq2), "+v"(xh0), "+v"(xh1), "+v"(xh2)
+                         : "n"(kRLoads * kPreSlices)
+                         : "memory");
+            if (fz.x_half) {
+                auto h4 = [](i32x2_t v) {
+                    const uint32_t a = (uint32_t)v.x, b = (uint32_t)v.y;
+                    return make_float4(f16_bits_to_f32(a & 0xffffu), f16_bits_to_f32(a >> 16),
+                                       f16_bits_to_f32(b & 0xffffu), f16_bits_to_f32(b >> 16));
+                };
+                av[0] = h4(xh0), av[1] = h4(xh1), av[2] = h4(xh2);
+            } else {
+                auto f4 = [](f32x4_t v) { return make_float4(v.x, v.y, v.z, v.w); };
+                av[0] = f4(xq0), av[1] = f4(xq1), av[2] = f4(xq2);
+            }
             uint32_t wd[kPB][kLimbs];
             float dd[kPB];
 #pragma unroll
