@@ -559,12 +559,18 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     }
     // kEpiResid: lane j holds the per-row inputs of round j
     float ex = 0.f, ewp = 0.f, ewn = 0.f;
+    // (asm loads, waited for with the table behind the stream's first
+    // slices: a compiler-visible load waited for there would make the
+    // compiler drain the stream with it)
     if (EPI == kEpiResid) {
         int row = r0 + lane * G;
         row = lane < rows_rounds && row < n ? row : 0;
-        ex = fz.x_res[row];
-        ewp = fz.w_post[row];
-        ewn = fz.w_next[row];
+        asm volatile(
+            "global_load_dword %0, %3, %4\n global_load_dword %1, %3, %5\n"
+            "global_load_dword %2, %3, %6"
+            : "=&v"(ex), "=&v"(ewp), "=&v"(ewn)
+            : "v"((uint32_t)row * 4u), "s"(fz.x_res), "s"(fz.w_post), "s"(fz.w_next)
+            : "memory");
     }
 
     // The prologue's inputs are waited for before the stream starts (about
@@ -579,11 +585,8 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 settle(av[k]);
             }
         }
-        if (EPI == kEpiResid) {
-            settle(ex);
-            settle(ewp);
-            settle(ewn);
-        }
+        static_assert(EPI != kEpiResid || PRO == kProTable || PRO == kProTableLds,
+                      "the residual epilogue's row loads are waited for with the table");
     }
 
     // kProTable: this lane's limb table entries (L2-resident), loaded by asm
@@ -628,10 +631,10 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     if (PRO == kProTable) {
         // the wait names the loaded registers, so no copy of them can be
         // placed ahead of it
-        asm volatile("s_waitcnt vmcnt(%15)"
+        asm volatile("s_waitcnt vmcnt(%18)"
                      : "+v"(g00), "+v"(g01), "+v"(g02), "+v"(g03), "+v"(g10), "+v"(g11),
                        "+v"(g12), "+v"(g13), "+v"(g20), "+v"(g21), "+v"(g22), "+v"(g23),
-                       "+v"(gd0), "+v"(gd1), "+v"(gd2)
+                       "+v"(gd0), "+v"(gd1), "+v"(gd2), "+v"(ex), "+v"(ewp), "+v"(ewn)
                      : "n"(kRLoads * kPreSlices)
                      : "memory");
         // (named vectors, not an array of them: see the LDS table read below)
@@ -649,11 +652,6 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
         putg(0, f4g(g00), f4g(g01), f4g(g02), f4g(g03), gd0);
         if (NBL > 1) putg(1, f4g(g10), f4g(g11), f4g(g12), f4g(g13), gd1);
         if (NBL > 2) putg(2, f4g(g20), f4g(g21), f4g(g22), f4g(g23), gd2);
-        if (EPI == kEpiResid) {
-            settle(ex);
-            settle(ewp);
-            settle(ewn);
-        }
     } else {
         float rb_s = 1.f;  // scale of the values that go into the table
         float ra = 0.f, s_out = 1.f;
@@ -696,8 +694,12 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                     make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
                                 s_out * (xo_in.z + ra * xo_u.z), s_out * (xo_in.w + ra * xo_u.w));
         } else if (PRO == kProTableLds) {
-            // the table's DMA was issued before the stream's first slices
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * kPreSlices));
+            // the table's DMA (and the residual epilogue's row loads) were
+            // issued before the stream's first slices
+            asm volatile("s_waitcnt vmcnt(%3)"
+                         : "+v"(ex), "+v"(ewp), "+v"(ewn)
+                         : "n"(kRLoads * kPreSlices)
+                         : "memory");
         } else if (PRO == kProX) {
             // the x loads were issued before the stream's first slices; the
             // wait names their registers (as the table's above)
