@@ -189,7 +189,7 @@ class AttnDecode:
     over a context of `ctx_len` (4K/32K/128K), split over the sequence."""
     kernel = "attn_decode_q8_kernel"
 
-    def __init__(self, ctx, torch, ctx_len=32768):
+    def __init__(self, ctx, torch, ctx_len=32768, splits=None):
         self.ctx, self.torch, self.ctx_len = ctx, torch, ctx_len
         n_q, n_kv, hd = 32, 16, 128
         self.n_q, self.n_kv = n_q, n_kv
@@ -211,9 +211,9 @@ class AttnDecode:
         self.q = torch.empty(n_q * hd, dtype=torch.float32, device="cuda")
         ctx.fill_normal(self.q, seed=52)
         self.out = torch.empty_like(self.q)
-        # 512 slots per split, 16..128 splits (sweep: 4K flat from 16 to 32,
-        # 32K best at 64, 128K flat from 64 to 256)
-        self.splits = min(128, max(16, ctx_len // 512))
+        # 256 slots per split, 64..256 splits: the one-wave-per-(kv head,
+        # split) kernel (sweep: 4K best at 64, 32K at 128, 128K at 128-256)
+        self.splits = splits or min(256, max(64, ctx_len // 256))
         self.bytes = ctx_len * n_kv * (2 * hd + 2 * (hd // 32) * 2) + 2 * n_q * hd * 4
 
     def step(self, i):
@@ -850,6 +850,9 @@ def main():
     ap.add_argument("--gemv-rows", type=int, default=21504,
                     help="gemv workload: rows N (config 1 is 21504; other values sweep the "
                          "per-launch fixed cost against the streaming rate)")
+    ap.add_argument("--attn-splits", type=int, default=None,
+                    help="attn_decode_* workloads: split count (default: 256 slots per split, "
+                         "64..256 splits)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true",
                     help="skip the measured MFMA / HBM peak probes")
@@ -897,7 +900,8 @@ def main():
         wl = AttnPages(ctx, torch, "global_q8k",
                        {"4k": 4096, "8k": 8192, "32k": 32768}[args.workload[15:]])
     elif args.workload.startswith("attn_decode_"):
-        wl = AttnDecode(ctx, torch, {"4k": 4096, "32k": 32768, "128k": 131072}[args.workload[12:]])
+        wl = AttnDecode(ctx, torch, {"4k": 4096, "32k": 32768, "128k": 131072}[args.workload[12:]],
+                        splits=args.attn_splits)
     else:
         wl = Mmq(ctx, torch, m=2048, k=21504, n=5376, split=args.split_k, label="BASELINE config 3")
     torch.cuda.synchronize()

@@ -45,6 +45,36 @@ __global__ __launch_bounds__(W * kWave) void attn_decode_q8_kernel(
                               limbs_out, post, kvh, split, FUSED ? step[0] : 0u);
 }
 
+// One wave per (kv head, split) work item (attn_split_per_wave): workgroup
+// = the 4 adjacent kv heads 4g..4g+3 of one split, consecutive workgroups
+// take consecutive splits of one group.  Partials only (n_splits >= 1).
+// Used when that gives at least 4 waves per CU (n_splits·n_kv >= 1024,
+// decided from host-side counts only, so that the typed call and the
+// dispatch by name pick the same kernel): config 4 at 4K / 32K / 128K with
+// 64 / 128 / 256 splits 11.2 / 34.4 / 117.4 us against 11.5 / 40.2 / 130.2
+// for the four-waves-per-item kernel at its best split counts; with few
+// splits (the decode step's 16) it leaves most of the GPU idle.  (The 4
+// head groups of a split side by side on one XCD: 11.4 / 37.6 / 121.9 us.)
+template <int QPK>
+__global__ __launch_bounds__(4 * kWave) void attn_decode_q8_hw_kernel(
+    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
+    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs,
+    const uint32_t *__restrict__ step, int step_word, uint32_t kv_len_direct, int n_kv,
+    int n_splits, float scale, float *__restrict__ part) {
+    __shared__ __align__(16) int8_t ql_s[4][2][4][kHD];
+    __shared__ float qn_s[4][2];
+    __shared__ __align__(16) float pw_s[4][32 * 4 * 2];
+    const int wave = threadIdx.x / kWave;
+    const uint32_t kv_len = step ? step[step_word] : kv_len_direct;
+    const int split = blockIdx.x % n_splits, kvh = (blockIdx.x / n_splits) * 4 + wave;
+    attn_split_per_wave<QPK>(q, kq, ks, vq, vs, kv_len, n_kv, n_splits, scale, part, kvh, split,
+                             ql_s[wave], qn_s[wave], pw_s[wave]);
+}
+constexpr int kAttnPerWaveMinWaves = 1024;
+inline bool attn_per_wave(int n_kv, int n_splits) {
+    return n_kv % 4 == 0 && n_splits * n_kv >= kAttnPerWaveMinWaves;
+}
+
 // Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
 // out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s.  One
 // 256-thread workgroup per query head (attn_merge_head); the kernel
@@ -104,6 +134,19 @@ int launch_attn_decode_q8(hipStream_t st, const float *q, const int8_t *kq, cons
     const dim3 grid(n_splits * n_kv);
     SGQ_CHECK(qpk == 1 || qpk == 2, "attn_decode_q8: %d q heads per kv head unsupported", qpk);
     BlockLimbs *lo = static_cast<BlockLimbs *>(limbs_out);
+    if (attn_per_wave(n_kv, n_splits)) {
+        const dim3 g4(n_splits * (n_kv / 4));
+        if (qpk == 1)
+            hipLaunchKernelGGL(attn_decode_q8_hw_kernel<1>, g4, dim3(4 * kWave), 0, st, q, kq, ks, vq,
+                               vs, step, step_word, kv_len, n_kv, n_splits, scale, part);
+        else
+            hipLaunchKernelGGL(attn_decode_q8_hw_kernel<2>, g4, dim3(4 * kWave), 0, st, q, kq, ks, vq,
+                               vs, step, step_word, kv_len, n_kv, n_splits, scale, part);
+        SGQ_HIP(hipGetLastError());
+        launch_merge(st, qpk, n_q, n_kv, n_splits, part, out, lo);
+        SGQ_HIP(hipGetLastError());
+        return SGQ_OK;
+    }
     float *out1 = n_splits == 1 ? out : nullptr;
     BlockLimbs *lo1 = n_splits == 1 ? lo : nullptr;
 #define SGQ_ATTN(Q, W)                                                                            \
@@ -133,6 +176,17 @@ int launch_attn_decode_parts(hipStream_t st, const float *q, const int8_t *kq,
     SGQ_CHECK(((uintptr_t)kq & 15) == 0 && ((uintptr_t)vq & 3) == 0 && ((uintptr_t)ks & 7) == 0 &&
                   ((uintptr_t)vs & 7) == 0 && ((uintptr_t)part & 3) == 0,
               "attn_decode (parts): misaligned operand");
+    if (attn_per_wave(n_kv, n_splits)) {
+        const dim3 g4(n_splits * (n_kv / 4));
+        if (n_q == n_kv)
+            hipLaunchKernelGGL(attn_decode_q8_hw_kernel<1>, g4, dim3(4 * kWave), 0, st, q, kq, ks, vq,
+                               vs, step, step_word, 0u, n_kv, n_splits, scale, part);
+        else
+            hipLaunchKernelGGL(attn_decode_q8_hw_kernel<2>, g4, dim3(4 * kWave), 0, st, q, kq, ks, vq,
+                               vs, step, step_word, 0u, n_kv, n_splits, scale, part);
+        SGQ_HIP(hipGetLastError());
+        return SGQ_OK;
+    }
     const dim3 grid(n_splits * n_kv);
     if (n_q == n_kv)
         hipLaunchKernelGGL((attn_decode_q8_kernel<1, false, kAttnWaves>), grid,

@@ -94,6 +94,87 @@ __device__ __forceinline__ void attn_group_load(AttnGroup &g, const int8_t *__re
     }
 }
 
+// One 32-slot group of one wave (slots tb .. tb+31, valid below t_end):
+// QK on the int8 matrix cores against the q limbs in qa (this lane feeds
+// block myb), scores scaled by dh, online softmax per head (the running
+// max m_run and this lane's sum l_lane), p·vs into the wave's LDS strip
+// pw, and PV on the VALU into acc (dims 4c..4c+3 of both heads, slots of
+// this lane's parity).
+template <int QPK>
+__device__ __forceinline__ void attn_group_compute(const AttnGroup &g, uint32_t tb,
+                                                   uint32_t t_end, int lane, v4i_a qa, int myb,
+                                                   float dh, float (&m_run)[2], float &l_lane,
+                                                   float (&acc)[2][4], float *pw) {
+    const int hq = lane >> 5, c = lane & 31, par = lane >> 5;
+    // ---- QK: four block MFMAs into one tile
+    v16i_a dacc = {};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const v4i_a a = myb == b ? qa : v4i_a{0, 0, 0, 0};
+        dacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, g.k[b], dacc, 0, 0, 0);
+    }
+    float s = 0.f;
+    {
+        const float ksf[4] = {f16_bits_to_f32(g.ks.x & 0xffff), f16_bits_to_f32(g.ks.x >> 16),
+                              f16_bits_to_f32(g.ks.y & 0xffff), f16_bits_to_f32(g.ks.y >> 16)};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float blk = (float)dacc[4 * b] +
+                              (float)dacc[4 * b + 1] * (1.0f / kLimbBase) +
+                              (float)dacc[4 * b + 2] * (1.0f / (kLimbBase * kLimbBase));
+            s = __builtin_fmaf(ksf[b], blk, s);
+        }
+    }
+    const bool valid = tb + (uint32_t)c < t_end && hq < QPK;
+    s = valid ? s * dh : kNegBig;
+    // ---- online softmax per head (32-lane halves)
+    // max over each 16-lane row on the VALU (DPP), then over the two
+    // rows of each head from lanes 0/16 and 32/48
+    const float mx = row_max_dpp(s);
+    const float M0 = fmaxf(readlane_f(mx, 0), readlane_f(mx, 16));
+    const float M1 = fmaxf(readlane_f(mx, 32), readlane_f(mx, 48));
+    const float mn0 = fmaxf(m_run[0], M0), mn1 = fmaxf(m_run[1], M1);
+    const float corr0 = __expf(m_run[0] - mn0), corr1 = __expf(m_run[1] - mn1);
+    m_run[0] = mn0;
+    m_run[1] = mn1;
+    const float p = valid ? __expf(s - (hq ? mn1 : mn0)) : 0.f;
+    l_lane = __builtin_fmaf(l_lane, hq ? corr1 : corr0, p);
+    // p·vs[t, b] for the PV lanes: strip [t][b][h]
+    {
+        const float vsf[4] = {f16_bits_to_f32(g.vs.x & 0xffff), f16_bits_to_f32(g.vs.x >> 16),
+                              f16_bits_to_f32(g.vs.y & 0xffff), f16_bits_to_f32(g.vs.y >> 16)};
+#pragma unroll
+        // (select, not multiply: a masked slot's scale may be any bits)
+        for (int b = 0; b < 4; b++) pw[(c * 4 + b) * 2 + hq] = valid ? p * vsf[b] : 0.f;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        acc[0][e] *= corr0;
+        acc[1][e] *= corr1;
+    }
+    // ---- PV: dims 4c..4c+3, slots 2i + par
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float2 pp =
+            *reinterpret_cast<const float2 *>(&pw[((2 * i + par) * 4 + (c >> 3)) * 2]);
+        const int w = g.v[i];
+        const float v0 = (float)(int8_t)(w & 0xff), v1 = (float)(int8_t)((w >> 8) & 0xff);
+        const float v2 = (float)(int8_t)((w >> 16) & 0xff), v3 = (float)(int8_t)(w >> 24);
+        acc[0][0] = __builtin_fmaf(pp.x, v0, acc[0][0]);
+        acc[0][1] = __builtin_fmaf(pp.x, v1, acc[0][1]);
+        acc[0][2] = __builtin_fmaf(pp.x, v2, acc[0][2]);
+        acc[0][3] = __builtin_fmaf(pp.x, v3, acc[0][3]);
+        if (QPK == 2) {
+            acc[1][0] = __builtin_fmaf(pp.y, v0, acc[1][0]);
+            acc[1][1] = __builtin_fmaf(pp.y, v1, acc[1][1]);
+            acc[1][2] = __builtin_fmaf(pp.y, v2, acc[1][2]);
+            acc[1][3] = __builtin_fmaf(pp.y, v3, acc[1][3]);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 // The split work item of kv head kvh over the split's slots.  With
 // n_splits > 1, or with neither out nor limbs_out given, it writes the
 // partial (acc, m, l) of its QPK query heads to part (agent-scope stores, so
@@ -253,73 +334,7 @@ __device__ __forceinline__ void attn_chunk(const float *__restrict__ q,
             for (int i = 0; i < 16; i++)
                 if (tb + 2 * i + par == fresh_slot) g.v[i] = fv_s[c];
         }
-        // ---- QK: four block MFMAs into one tile
-        v16i_a dacc = {};
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const v4i_a a = myb == b ? qa : v4i_a{0, 0, 0, 0};
-            dacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, g.k[b], dacc, 0, 0, 0);
-        }
-        float s = 0.f;
-        {
-            const float ksf[4] = {f16_bits_to_f32(g.ks.x & 0xffff), f16_bits_to_f32(g.ks.x >> 16),
-                                  f16_bits_to_f32(g.ks.y & 0xffff), f16_bits_to_f32(g.ks.y >> 16)};
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const float blk = (float)dacc[4 * b] +
-                                  (float)dacc[4 * b + 1] * (1.0f / kLimbBase) +
-                                  (float)dacc[4 * b + 2] * (1.0f / (kLimbBase * kLimbBase));
-                s = __builtin_fmaf(ksf[b], blk, s);
-            }
-        }
-        const bool valid = tb + (uint32_t)c < t_end && hq < QPK;
-        s = valid ? s * dh : kNegBig;
-        // ---- online softmax per head (32-lane halves)
-        // max over each 16-lane row on the VALU (DPP), then over the two
-        // rows of each head from lanes 0/16 and 32/48
-        const float mx = row_max_dpp(s);
-        const float M0 = fmaxf(readlane_f(mx, 0), readlane_f(mx, 16));
-        const float M1 = fmaxf(readlane_f(mx, 32), readlane_f(mx, 48));
-        const float mn0 = fmaxf(m_run[0], M0), mn1 = fmaxf(m_run[1], M1);
-        const float corr0 = __expf(m_run[0] - mn0), corr1 = __expf(m_run[1] - mn1);
-        m_run[0] = mn0;
-        m_run[1] = mn1;
-        const float p = valid ? __expf(s - (hq ? mn1 : mn0)) : 0.f;
-        l_lane = __builtin_fmaf(l_lane, hq ? corr1 : corr0, p);
-        // p·vs[t, b] for the PV lanes: strip [t][b][h]
-        {
-            const float vsf[4] = {f16_bits_to_f32(g.vs.x & 0xffff), f16_bits_to_f32(g.vs.x >> 16),
-                                  f16_bits_to_f32(g.vs.y & 0xffff), f16_bits_to_f32(g.vs.y >> 16)};
-#pragma unroll
-            // (select, not multiply: a masked slot's scale may be any bits)
-            for (int b = 0; b < 4; b++) pw[(c * 4 + b) * 2 + hq] = valid ? p * vsf[b] : 0.f;
-        }
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            acc[0][e] *= corr0;
-            acc[1][e] *= corr1;
-        }
-        // ---- PV: dims 4c..4c+3, slots 2i + par
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float2 pp =
-                *reinterpret_cast<const float2 *>(&pw[((2 * i + par) * 4 + (c >> 3)) * 2]);
-            const int w = g.v[i];
-            const float v0 = (float)(int8_t)(w & 0xff), v1 = (float)(int8_t)((w >> 8) & 0xff);
-            const float v2 = (float)(int8_t)((w >> 16) & 0xff), v3 = (float)(int8_t)(w >> 24);
-            acc[0][0] = __builtin_fmaf(pp.x, v0, acc[0][0]);
-            acc[0][1] = __builtin_fmaf(pp.x, v1, acc[0][1]);
-            acc[0][2] = __builtin_fmaf(pp.x, v2, acc[0][2]);
-            acc[0][3] = __builtin_fmaf(pp.x, v3, acc[0][3]);
-            if (QPK == 2) {
-                acc[1][0] = __builtin_fmaf(pp.y, v0, acc[1][0]);
-                acc[1][1] = __builtin_fmaf(pp.y, v1, acc[1][1]);
-                acc[1][2] = __builtin_fmaf(pp.y, v2, acc[1][2]);
-                acc[1][3] = __builtin_fmaf(pp.y, v3, acc[1][3]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
+        attn_group_compute<QPK>(g, tb, t_end, lane, qa, myb, dh, m_run, l_lane, acc, pw);
     };
     for (uint32_t j = 0; j < n_mine; j += 2) {
         step(j, ga, gb);
@@ -380,6 +395,97 @@ __device__ __forceinline__ void attn_chunk(const float *__restrict__ q,
     if (tid < QPK * kHD / 4) {
         const float4 v = *reinterpret_cast<const float4 *>(&o_s[4 * tid]);
         limbs_block8<false>(v, tid & 7, &limbs_out[(kvh * QPK * kHD) / 32 + (tid >> 3)]);
+    }
+}
+
+// The same split work item with one wave per kv head: wave w of the
+// workgroup takes kv head kvh0 + w over all the split's 32-slot groups (two
+// in flight), so the four waves of a workgroup read the four heads' 128-byte
+// rows of the same slots (512 contiguous bytes of each slot's K and V row)
+// and share each slot's f16 scale line (one 128-byte line holds all heads'
+// scales of a slot) in the CU's caches.  The wave writes its QPK partials
+// (acc, m, l) itself; no cross-wave combine.  q from global memory (fp32,
+// [n_q × 128]); QPK·128 values per wave, four per lane.
+template <int QPK>
+__device__ __forceinline__ void attn_split_per_wave(
+    const float *__restrict__ q, const int8_t *__restrict__ kq, const uint16_t *__restrict__ ks,
+    const int8_t *__restrict__ vq, const uint16_t *__restrict__ vs, uint32_t kv_len, int n_kv,
+    int n_splits, float scale, float *__restrict__ part, int kvh, int split,
+    int8_t (&ql)[2][4][kHD], float (&qn)[2], float *pw) {
+    static_assert(QPK == 1 || QPK == 2, "1 or 2 query heads per kv head");
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t per = (kv_len + n_splits - 1) / n_splits;
+    const uint32_t chunk = (per + 31) & ~31u;
+    const uint32_t t_begin = min((uint32_t)split * chunk, kv_len);
+    const uint32_t t_end = min(t_begin + chunk, kv_len);
+    const uint32_t n_groups = (t_end - t_begin + 31) / 32;
+
+    // the first group's loads go out before the q limbs are formed
+    AttnGroup ga, gb;
+    if (n_groups > 0) attn_group_load(ga, kq, ks, vq, vs, t_begin, t_end, n_kv, kvh, lane);
+
+    // q limbs against ‖q_h‖: lane (h, i) = (lane/32, lane%32) holds dims
+    // 4i..4i+3 of head h (heads >= QPK are zero)
+    {
+        const int h = lane >> 5, d0 = 4 * (lane & 31);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (h < QPK) v = *reinterpret_cast<const float4 *>(q + (size_t)(kvh * QPK + h) * kHD + d0);
+        float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+        const float qnorm = sqrtf(ss);
+        const float f[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float y = qnorm > 0.f ? f[e] * (127.0f / qnorm) : 0.f;
+            const float l0 = __builtin_rintf(y);
+            const float r1 = (y - l0) * kLimbBase;
+            const float l1 = __builtin_rintf(r1);
+            const float l2 = __builtin_rintf((r1 - l1) * kLimbBase);
+            ql[h][0][d0 + e] = (int8_t)(int)l0;
+            ql[h][1][d0 + e] = (int8_t)(int)l1;
+            ql[h][2][d0 + e] = (int8_t)(int)l2;
+            ql[h][3][d0 + e] = 0;
+        }
+        if ((lane & 31) == 0) qn[h] = qnorm;
+    }
+    __builtin_amdgcn_wave_barrier();  // (LDS operations of one wave complete in order)
+    const int myb = (lane & 31) >> 3;
+    const v4i_a qa = *reinterpret_cast<const v4i_a *>(
+        &ql[(lane >> 2) & 1][lane & 3][32 * myb + 16 * (lane >> 5)]);
+    const int hq = lane >> 5;
+    const float dh = qn[hq] * (1.0f / 127.0f) * scale;
+
+    float m_run[2] = {kNegBig, kNegBig};
+    float l_lane = 0.f;
+    float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (uint32_t j = 0; j < n_groups; j += 2) {
+        const uint32_t tb = t_begin + 32 * j;
+        if (j + 1 < n_groups) attn_group_load(gb, kq, ks, vq, vs, tb + 32, t_end, n_kv, kvh, lane);
+        attn_group_compute<QPK>(ga, tb, t_end, lane, qa, myb, dh, m_run, l_lane, acc, pw);
+        if (j + 1 >= n_groups) break;
+        if (j + 2 < n_groups) attn_group_load(ga, kq, ks, vq, vs, tb + 64, t_end, n_kv, kvh, lane);
+        attn_group_compute<QPK>(gb, tb + 32, t_end, lane, qa, myb, dh, m_run, l_lane, acc, pw);
+    }
+    // the wave's partials: sum of p per head, both slot parities of acc
+    for (int o = 16; o > 0; o >>= 1) l_lane += __shfl_xor(l_lane, o, kWave);
+#pragma unroll
+    for (int hh = 0; hh < QPK; hh++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[hh][e] += __shfl_xor(acc[hh][e], 32, kWave);
+    constexpr int stride = kHD + 2;
+    const int c = lane & 31;
+    if (lane < 32) {
+#pragma unroll
+        for (int hh = 0; hh < QPK; hh++) {
+            float *pr = part + ((size_t)(kvh * QPK + hh) * n_splits + split) * stride;
+            *reinterpret_cast<float2 *>(pr + 4 * c) = make_float2(acc[hh][0], acc[hh][1]);
+            *reinterpret_cast<float2 *>(pr + 4 * c + 2) = make_float2(acc[hh][2], acc[hh][3]);
+        }
+    }
+    if ((lane & 31) == 0 && hq < QPK) {
+        float *pr = part + ((size_t)(kvh * QPK + hq) * n_splits + split) * stride;
+        pr[kHD] = m_run[hq];
+        pr[kHD + 1] = l_lane;
     }
 }
 
