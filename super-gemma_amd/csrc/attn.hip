@@ -77,15 +77,19 @@ inline bool attn_per_wave(int n_kv, int n_splits) {
 
 // Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
 // out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s.  One
-// 256-thread workgroup per query head (attn_merge_head); the kernel
-// boundary after the split kernel makes the partials visible.  Optionally
-// writes the x limbs of the output rows for the next GEMV.
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
-                                                         int n_splits, float *__restrict__ out,
-                                                         BlockLimbs *__restrict__ limbs_out) {
-    __shared__ float merge_s[kMergeSmem];
-    attn_merge_head<false>(part, n_splits, blockIdx.x, out, limbs_out, merge_s);
+// workgroup per query head (attn_merge_head): 4 waves up to 64 splits, 16
+// above, so that each wave's share of the rows is one batch of loads (at
+// 256 splits the step took 117.8 -> 116.1 us); the kernel boundary after the split kernel
+// makes the partials visible.  Optionally writes the x limbs of the output
+// rows for the next GEMV.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void attn_merge_kernel(const float *__restrict__ part,
+                                                             int n_splits, float *__restrict__ out,
+                                                             BlockLimbs *__restrict__ limbs_out) {
+    __shared__ float merge_s[merge_smem(NW)];
+    attn_merge_head<NW>(part, n_splits, blockIdx.x, out, limbs_out, merge_s);
 }
+constexpr int kMergeWideSplits = 64;  // above: 16-wave merge workgroups
 
 // The same merge for up to 16 splits: one workgroup per kv head, thread
 // (head, dim) loads all splits' (m, l, acc[dim]) in one batch and folds
@@ -100,8 +104,12 @@ __global__ __launch_bounds__(QPK * kHD) void attn_merge_fold_kernel(
 
 void launch_merge(hipStream_t st, int qpk, int n_q, int n_kv, int n_splits, const float *part,
                   float *out, BlockLimbs *lo) {
-    if (n_splits > 16)
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(n_q), dim3(256), 0, st, part, n_splits, out, lo);
+    if (n_splits > kMergeWideSplits)
+        hipLaunchKernelGGL(attn_merge_kernel<16>, dim3(n_q), dim3(16 * 64), 0, st, part, n_splits,
+                           out, lo);
+    else if (n_splits > 16)
+        hipLaunchKernelGGL(attn_merge_kernel<4>, dim3(n_q), dim3(4 * 64), 0, st, part, n_splits,
+                           out, lo);
     else if (qpk == 1)
         hipLaunchKernelGGL(attn_merge_fold_kernel<1>, dim3(n_kv), dim3(kHD), 0, st, part, n_splits,
                            out, lo);

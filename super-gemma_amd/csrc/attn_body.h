@@ -11,9 +11,9 @@
 // in split order 0..S-1, the fixed order of attn_reduce.wgsl:40-52:
 //  * attn_merge: one kv head's QPK query heads by the first QPK·128
 //    threads of a workgroup, 16 splits per load batch with a running max;
-//  * attn_merge_head: one query head by a 256-thread workgroup, the loads
-//    spread over the splits (lanes over splits for (m, l), waves over
-//    quarters of the splits for acc).
+//  * attn_merge_head: one query head by a workgroup of 4 or 16 waves, the
+//    loads spread over the splits (lanes over splits for (m, l), waves over
+//    shares of the splits for acc).
 // Both can also write the O projection's x limbs (limbs.h) instead of, or
 // besides, the fp32 rows.  Also here: the inputs of the fused q/k/v
 // post-projection (AttnPost) and agent-scope load/store helpers for
@@ -110,48 +110,44 @@ __device__ __forceinline__ void attn_merge(const float *__restrict__ part, int n
 }
 
 // Merge of query head hq's n_splits partials (row stride kHD + 2: acc, m, l)
-// by a 256-thread workgroup, spreading the loads over the splits instead of
+// by a workgroup of NW waves, spreading the loads over the splits instead of
 // folding them one after another:
 //   1. lanes over splits load (m_s, l_s) into LDS; M = max_s m_s;
 //   2. w_s = e^(m_s − M) in LDS, L = Σ_s w_s·l_s;
-//   3. wave w sums w_s·acc_s over the w-th quarter of the splits, lane
-//      (dims 2·lane, 2·lane + 1) by 16-split batches of row loads;
-//   4. the four wave sums are added in wave order; out = sum / L.
-// Every reduction has a fixed order, so results are bit-reproducible.
-// `sm` holds kMergeSmem floats.  `out` and `limbs_out` may each be null;
-// AGENT selects agent-scope loads of the partials and stores of the limbs
-// (written / read by other workgroups of the same launch).  All 256 threads
-// call; the caller separates two calls with a barrier.
+//   3. wave w sums w_s·acc_s over the w-th NW-th of the splits, lane
+//      (dims 2·lane, 2·lane + 1) by 16-split batches of row loads (the
+//      first batch is loaded together with (m, l): up to 16·NW splits take
+//      one round trip);
+//   4. the NW wave sums are added in wave order; out = sum / L.
+// Every reduction has a fixed order, so results are bit-reproducible for a
+// given NW.  `sm` holds merge_smem(NW) floats.  `out` and `limbs_out` may
+// each be null.  All NW·64 threads call.
 constexpr int kMergeMaxSplits = 1024;
-constexpr int kMergeSmem = 2 * kMergeMaxSplits + 4 * kHD + 8;
-template <bool AGENT>
+constexpr int merge_smem(int nw) { return 2 * kMergeMaxSplits + nw * kHD + 2 * nw; }
+template <int NW>
 __device__ __forceinline__ void attn_merge_head(const float *__restrict__ part, int n_splits,
                                                 int hq, float *__restrict__ out,
                                                 BlockLimbs *__restrict__ limbs_out, float *sm) {
-    constexpr int stride = kHD + 2, NT = 256;
+    constexpr int stride = kHD + 2, NT = NW * 64;
     float *w_s = sm, *l_s = sm + kMergeMaxSplits, *acc_s = sm + 2 * kMergeMaxSplits;
-    float *red = acc_s + 4 * kHD;
+    float *red = acc_s + NW * kHD;  // [0, NW): wave maxima, [NW, 2NW): wave sums of w·l
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *ph = part + (size_t)hq * n_splits * stride;
-    // this wave's quarter of the splits; its first 16 rows are loaded now,
-    // alongside (m, l), so that up to 64 splits take one round trip
-    const int per = (n_splits + 3) / 4;
+    const int per = (n_splits + NW - 1) / NW;
     const int s_lo = min(wave * per, n_splits), s_hi = min(s_lo + per, n_splits);
     float2 av[16];
     auto load_rows = [&](int s0, int nb) {
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const float *r = ph + (size_t)(s0 + min(u, max(nb - 1, 0))) * stride + 2 * lane;
-            av[u] = AGENT ? make_float2(ld_agent(r), ld_agent(r + 1))
-                          : *reinterpret_cast<const float2 *>(r);
+            av[u] = *reinterpret_cast<const float2 *>(r);
         }
     };
     load_rows(min(s_lo, n_splits - 1), min(16, s_hi - s_lo));
     float mx = kNegBig;
     for (int s = tid; s < n_splits; s += NT) {
-        const float m_ = AGENT ? ld_agent(ph + (size_t)s * stride + kHD) : ph[(size_t)s * stride + kHD];
-        const float l_ = AGENT ? ld_agent(ph + (size_t)s * stride + kHD + 1)
-                               : ph[(size_t)s * stride + kHD + 1];
+        const float m_ = ph[(size_t)s * stride + kHD];
+        const float l_ = ph[(size_t)s * stride + kHD + 1];
         w_s[s] = m_;
         l_s[s] = l_;
         mx = fmaxf(mx, m_);
@@ -159,7 +155,9 @@ __device__ __forceinline__ void attn_merge_head(const float *__restrict__ part, 
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
     if (lane == 0) red[wave] = mx;
     __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) M = fmaxf(M, red[w]);
     float lsum = 0.f;
     for (int s = tid; s < n_splits; s += NT) {
         const float w = __expf(w_s[s] - M);
@@ -167,9 +165,9 @@ __device__ __forceinline__ void attn_merge_head(const float *__restrict__ part, 
         lsum = __builtin_fmaf(w, l_s[s], lsum);
     }
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, kWave);
-    __syncthreads();  // w_s complete; red[0..3] read
-    if (lane == 0) red[4 + wave] = lsum;
-    // 3. this wave's quarter of the splits
+    __syncthreads();  // w_s complete; red[0, NW) read
+    if (lane == 0) red[NW + wave] = lsum;
+    // 3. this wave's share of the splits
     float2 acc = make_float2(0.f, 0.f);
     for (int s0 = s_lo; s0 < s_hi; s0 += 16) {
         const int nb = min(16, s_hi - s0);
@@ -185,8 +183,12 @@ __device__ __forceinline__ void attn_merge_head(const float *__restrict__ part, 
     __syncthreads();
     float res = 0.f;
     if (tid < kHD) {
-        const float L = ((red[4] + red[5]) + red[6]) + red[7];
-        const float a = ((acc_s[tid] + acc_s[kHD + tid]) + acc_s[2 * kHD + tid]) + acc_s[3 * kHD + tid];
+        float L = red[NW], a = acc_s[tid];
+#pragma unroll
+        for (int w = 1; w < NW; w++) {
+            L += red[NW + w];
+            a += acc_s[w * kHD + tid];
+        }
         res = L > 0.f ? a / L : 0.f;  // all splits empty: 0
         if (out) out[(size_t)hq * kHD + tid] = res;
     }
@@ -196,7 +198,7 @@ __device__ __forceinline__ void attn_merge_head(const float *__restrict__ part, 
     __syncthreads();
     if (tid < kHD / 4) {
         const float4 v = *reinterpret_cast<const float4 *>(&acc_s[4 * tid]);
-        limbs_block8<AGENT>(v, tid & 7, &limbs_out[(hq * kHD) / 32 + (tid >> 3)]);
+        limbs_block8<false>(v, tid & 7, &limbs_out[(hq * kHD) / 32 + (tid >> 3)]);
     }
 }
 
