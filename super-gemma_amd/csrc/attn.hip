@@ -78,10 +78,10 @@ inline bool attn_per_wave(int n_kv, int n_splits) {
 // Merge of the split partials (attn_reduce.wgsl:24-57): for query head h,
 // out = Σ_s a_s·e^(m_s−M) / Σ_s l_s·e^(m_s−M), M = max_s m_s.  One
 // workgroup per query head (attn_merge_head): 4 waves up to 64 splits, 16
-// above, so that each wave's share of the rows is one batch of loads (at
-// 256 splits the step took 117.8 -> 116.1 us); the kernel boundary after the split kernel
-// makes the partials visible.  Optionally writes the x limbs of the output
-// rows for the next GEMV.
+// above, so that each wave's share of the rows is one batch of loads (the
+// config-4 step at 128K with 256 splits: 117.8 -> 116.1 us).  The kernel
+// boundary after the split kernel makes the partials visible.  Optionally
+// writes the x limbs of the output rows for the next GEMV.
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void attn_merge_kernel(const float *__restrict__ part,
                                                              int n_splits, float *__restrict__ out,
