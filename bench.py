@@ -57,11 +57,11 @@ class Gemv:
     name = "gemv_q4_0 K=5376 N=21504 (BASELINE config 1), 8 rotating weight copies"
     kernel = "gemv_q4_0_ring_kernel"
 
-    def __init__(self, ctx, torch, n=21504):
+    def __init__(self, ctx, torch, n=21504, k=5376):
         self.ctx, self.torch = ctx, torch
-        self.k, self.n = 5376, n
-        if n != 21504:
-            self.name = f"gemv_q4_0 K=5376 N={n} (row-count sweep around config 1), 8 rotating copies"
+        self.k, self.n = k, n
+        if n != 21504 or k != 5376:
+            self.name = f"gemv_q4_0 K={k} N={n} (shape sweep around config 1), 8 rotating copies"
         self.copies = 8
         nbytes = q4_bytes(self.n, self.k)
         self.w = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(self.copies)]
@@ -83,7 +83,8 @@ class Gemv:
             "dtype": "q4_0 weights, fp32 x/y; x enters the i4 dot8 as 15-bit fixed point per "
                      "32-block (4 limbs)",
             "roofline": ring_roofline(self.ctx, self.torch, [w.data_ptr() for w in self.w],
-                                      self.k, self.n),
+                                      self.k, self.n,
+                                      traffic=(self.k, self.n) == (5376, 21504)),
             "config": {"workload": self.name, "m": 1, "k": self.k, "n": self.n,
                        "bytes_per_launch": self.bytes},
         }
@@ -657,7 +658,7 @@ def measured_traffic():
         return None
 
 
-def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
+def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124, traffic=True):
     """The dominant kernel, gemv_q4_0_ring_kernel, alone at K x N: x limbs
     made once, then `steps` single-matrix launches rotating over w_ptrs (so
     each launch streams its weights from HBM), recorded once as a hipGraph
@@ -707,7 +708,7 @@ def ring_roofline(ctx, torch, w_ptrs, k, n, steps=124):
     full_bytes = q4_bytes(n, k) + k * 4 + n * 4  # BASELINE's config-1 bytes (fp32 x in)
     full_gbs = full_bytes / (ms_full * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic(),
+            "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic() if traffic else None,
             "kernel": f"gemv_q4_0_ring_kernel K={k} N={n}", "bytes_per_launch": nbytes,
             "us_per_launch": ms * 1e3, "launches": steps,
             "full_call": {"what": "sgq_gemv_q4_0 (fp32 x; limbs built in the streamed kernel's prologue)",
@@ -850,6 +851,9 @@ def main():
     ap.add_argument("--gemv-rows", type=int, default=21504,
                     help="gemv workload: rows N (config 1 is 21504; other values sweep the "
                          "per-launch fixed cost against the streaming rate)")
+    ap.add_argument("--gemv-k", type=int, default=5376,
+                    help="gemv workload: K (config 1 is 5376; 21504 is the FFN down projection, "
+                         "streamed as four K-slices)")
     ap.add_argument("--attn-splits", type=int, default=None,
                     help="attn_decode_* workloads: split count (default: 256 slots per split, "
                          "64..256 splits)")
@@ -879,7 +883,7 @@ def main():
     elif args.workload == "prefill_real":
         wl = Prefill(ctx, torch, real=True)
     elif args.workload == "gemv":
-        wl = Gemv(ctx, torch, n=args.gemv_rows)
+        wl = Gemv(ctx, torch, n=args.gemv_rows, k=args.gemv_k)
     elif args.workload == "mmq":
         wl = Mmq(ctx, torch)
     elif args.workload == "head_q6k":
