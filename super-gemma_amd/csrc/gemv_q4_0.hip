@@ -812,6 +812,9 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     const uint32_t dshift = (lane & 1) ? 16u : 0u;
     float gate = 0.f;                              // kEpiGeglu
     float held = 0.f;                              // kEpiRows, deferred stores
+    // K-slices of plain rows combined after the loop (the row-partials area
+    // holds 64 rounds per wave); more rounds keep one barrier per row
+    const bool defer = EPI == kEpiRows && S > 1 && !tg.split_out && rows_rounds <= kWave;
     for (int it = 0; it < rows_rounds; it++) {
         // wait for round `it`: the slices issued after it may stay in flight
         static_assert(kGStages >= 2 && kGStages <= 6, "the wait switch covers 0..5 rounds ahead");
@@ -848,6 +851,13 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 lds_write_u32(rows_s + ((rw * kWave + it) * S + s) * 4, __builtin_bit_cast(uint32_t, a));
             continue;
         }
+        if (defer) {
+            // the K-slice partials of round `it` kept for after the loop
+            // (as the residual epilogue does): no barrier per row
+            if (lane == 0)
+                lds_write_u32(rows_s + ((rw * kWave + it) * S + s) * 4, __builtin_bit_cast(uint32_t, a));
+            continue;
+        }
         bool have = true;
         if (S > 1 && !(EPI == kEpiRows && tg.split_out)) {
             // one barrier per row: partials alternate between two slots, and
@@ -876,6 +886,17 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 else
                     store_row(tg, rowl, held);
             }
+        }
+    }
+    if (defer) {
+        // lane j of the first wave of each row group finishes round j's row:
+        // the K-slices summed in order
+        lds_barrier();
+        const int row = r0 + lane * G;
+        if (s == 0 && lane < rows_rounds && row < n) {
+            float o = 0.f;
+            for (int q = 0; q < S; q++) o += lds_read_f32(rows_s + ((rw * kWave + lane) * S + q) * 4);
+            store_row(tg, row, o);
         }
     }
     if (EPI == kEpiResid) {
