@@ -59,6 +59,24 @@ def test_gemv_matches_oracle(ctx, oracle, k, n):
     _check(oracle, w, x, host(ty), n, k)
 
 
+@pytest.mark.parametrize("k,n", [(21504, 32768), (21504, 40000), (10752, 70000)])
+def test_gemv_kslices_row_rounds(ctx, oracle, k, n):
+    """K above one slice (2 or 4 K-slices per row): up to 64 row rounds per
+    wave the slice partials are combined after the loop, beyond that with one
+    barrier per row (32768 rows at K=21504 are exactly 64 rounds of the
+    512-workgroup grid; 40000 and 70000 need more).  Weights filled on the
+    device, rows sampled across every round."""
+    print(f"gemv k-slices k={k} n={n}", flush=True)
+    tw = empty(n * k // 32 * 18, torch.uint8)
+    ctx.fill_q4_0_random(tw, n * k // 32, seed=0x51CE + n, sigma=0.02)
+    rng = oracle.Rng(0x51CF + k)
+    x = oracle.through_f16(rng.f32_vec(k))
+    ty = empty(n, torch.float32)
+    ctx.gemv_q4_0(tw, dev(x), ty, n, k)
+    torch.cuda.synchronize()
+    _check(oracle, host(tw), x, host(ty), n, k)
+
+
 @pytest.mark.parametrize("k,n", [(64, 1), (128, 37), (192, 5), (320, 333), (1536, 63),
                                  (6144, 130), (6208, 9), (12352, 17), (24640, 3), (65536, 11)])
 def test_gemv_ragged_shapes(ctx, oracle, k, n):
