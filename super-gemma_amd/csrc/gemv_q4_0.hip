@@ -161,15 +161,16 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // x by gemv_prep_x_kernel, or by a producer kernel that fuses it), so the
 // GEMV itself does no quantization and no LDS table.
 //
-// Each wave owns a private ring of kGStages LDS slots and streams exactly
+// Each wave owns a private ring of LDS slots (ring_stages) and streams exactly
 // the row slices it reduces with global_load_lds_dwordx4 (a lane moves 16 B
-// straight into LDS; the data never occupies VGPRs).  Both slots are filled
-// before the loop; each slot is refilled with the slice two rounds ahead as
-// soon as its words are in registers, so one slice streams in while a row
+// straight into LDS; the data never occupies VGPRs).  The slots are filled
+// before the loop; each is refilled with the slice ring_stages rounds ahead
+// as soon as its words are in registers, so slices stream in while a row
 // computes.  A wave waits only on its own vmcnt.  For K <= 5440 a row is one
 // slice and waves never synchronize; for longer K the S = 2 or 4 waves of a
 // workgroup take the S slices of the same row and combine partials through
-// LDS in fixed order (one barrier per row).
+// LDS in fixed order (after the loop, or with one barrier per row past 64
+// rounds per wave).
 // ---------------------------------------------------------------------------
 // Waves per workgroup, by prologue and epilogue (the enums are declared in
 // sgq_internal.h).  Eight waves (one workgroup per CU) for the norm and
@@ -187,12 +188,24 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 constexpr int ring_waves(int pro, int epi) {
     return (pro == kProNorm || pro == kProEmbed || pro == kProX || pro == kProTableLds) && epi == kEpiRows ? 8 : 4;
 }
-// Two slots per wave (3 to 6 MB in flight over the chip, two workgroups per
-// CU): fewer bytes in flight stream faster here.  Measured at K=5376,
-// N=21504 against three slots: 12.8-13.1 vs 13.3-13.5 us (and 15.8 us with
-// six); three or four workgroups per CU, or one, are slower still.
-constexpr int kGStages = 2;
-constexpr int kPreSlices = kGStages;  // slots filled before the loop
+// Ring slots per wave and waves per CU (the grid).  The one-slice plain
+// launches (the limb table copied into LDS, or built from x in the
+// prologue; row outputs: the typed and by-name GEMV at K <= 5440) run one
+// slot per wave at 16 waves per CU: at K=5376, N=21504 the kernel took
+// 12.1-12.35 against 12.6-13.35 us with two slots at 8 waves per CU
+// (interleaved runs on three boxes), the same bytes in flight spread over
+// twice the waves, which hides more of each row's compute.  Everything else
+// keeps two slots at 8 waves per CU: the norm-prologue launches would
+// repeat their prologue in twice the workgroups (decode step 233.1 -> 230.1
+// tok/s), and one slot made the residual and GeGLU launches and the
+// K-sliced rows (K=21504: 15.8-16.4 against 13.7-15.4 us) slower.  Fewer
+// bytes in flight stream faster here: three slots at 8 waves per CU took
+// 13.3-13.5 us at config 1, six 15.8 us.
+constexpr bool ring_plain(int pro, int epi) {
+    return (pro == kProTableLds || pro == kProX) && epi == kEpiRows;
+}
+constexpr int ring_stages(int pro, int epi) { return ring_plain(pro, epi) ? 1 : 2; }
+constexpr int ring_waves_per_cu(int pro, int epi) { return ring_plain(pro, epi) ? 16 : 8; }
 
 // Row r of the concatenated targets -> (matrix, local row).
 __device__ __forceinline__ int target_of(const GemvTargets &tg, int row, int *local) {
@@ -248,15 +261,19 @@ __device__ __forceinline__ void store_row(const GemvTargets &tg, int row, float 
 // residual epilogue (64 rounds per wave), then (prologues only) the x limb
 // table.
 constexpr int kGegluUnits = 32;  // units (gate/up row pairs) per workgroup (4 waves)
-template <int WV>
+template <int WV, int ST>
 struct RingLds {
-    static constexpr int kRing = WV * kGStages * kRSlot;
+    static constexpr int kRing = WV * ST * kRSlot;
     static constexpr int kRed = kRing;
     static constexpr int kScr = kRed + 2 * 4 * WV;
     static constexpr int kScrBytes = (kGegluUnits * 4 > 16 * WV ? kGegluUnits * 4 : 16 * WV);
     static constexpr int kRows = kScr + kScrBytes;
     static constexpr int kTab = kRows + WV * kWave * 4;
 };
+constexpr int ring_lds_tab(int wv, int st) {
+    return wv * st * kRSlot + 2 * 4 * wv + (kGegluUnits * 4 > 16 * wv ? kGegluUnits * 4 : 16 * wv) +
+           wv * kWave * 4;
+}
 constexpr int kMaxTabBlocks = 3 * kWave;  // one slice: <= 192 blocks
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -358,14 +375,17 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     extern __shared__ __align__(16) uint8_t gemv_smem[];
     constexpr int WV = ring_waves(PRO, EPI);
     constexpr int kRWG = WV * kWave;
-    using Lds = RingLds<WV>;
+    constexpr int GS = ring_stages(PRO, EPI);  // ring slots per wave
+    constexpr int kPreSlices = GS;             // slots filled before the loop
+    using Lds = RingLds<WV, GS>;
+    static_assert(Lds::kTab == ring_lds_tab(WV, GS), "LDS layout");
     static_assert(EPI != kEpiGeglu || WV * 8 == kGegluUnits, "8 GeGLU units per wave");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int s = wave % S;              // K-slice of this wave
     const int rw = wave / S;             // row within the workgroup's row group
     const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
-    uint8_t *ring = gemv_smem + wave * (kGStages * kRSlot);
+    uint8_t *ring = gemv_smem + wave * (GS * kRSlot);
     uint8_t *red = gemv_smem + Lds::kRed;  // [2][waves] floats
     uint8_t *scr = gemv_smem + Lds::kScr;
     uint8_t *tab = gemv_smem + Lds::kTab;
@@ -393,7 +413,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
         EPI == kEpiGeglu ? 2 * kUnitsPerWave : (n - blockIdx.x * P + G - 1) / G;
     // the weight slice of round `it` into ring slot `slot`
     auto issue = [&](int it) {
-        uint8_t *slot = ring + (it % kGStages) * kRSlot;
+        uint8_t *slot = ring + (it % GS) * kRSlot;
         if (EPI == kEpiGeglu) {
             const uint8_t *w = static_cast<const uint8_t *>((it & 1) ? tg.w[1] : tg.w[0]);
             const uint8_t *src = w + (size_t)(u0 + (it >> 1)) * row_bytes + slice_off;
@@ -817,8 +837,8 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     const bool defer = EPI == kEpiRows && S > 1 && !tg.split_out && rows_rounds <= kWave;
     for (int it = 0; it < rows_rounds; it++) {
         // wait for round `it`: the slices issued after it may stay in flight
-        static_assert(kGStages >= 2 && kGStages <= 6, "the wait switch covers 0..5 rounds ahead");
-        switch (min(kGStages - 1, rows_rounds - 1 - it)) {
+        static_assert(GS >= 1 && GS <= 6, "the wait switch covers 0..5 rounds ahead");
+        switch (min(GS - 1, rows_rounds - 1 - it)) {
             case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 5)); break;
             case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 4)); break;
             case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRLoads * 3)); break;
@@ -828,10 +848,10 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
         }
         float a = 0.f;
         uint32_t wv[NBL][5];
-        lds_read_blocks<NBL>(ring + (it % kGStages) * kRSlot, boff, wv);
+        lds_read_blocks<NBL>(ring + (it % GS) * kRSlot, boff, wv);
         // the slot's words are in registers: refill it now, so that all
-        // kGStages slots stream while this row computes
-        if (it + kGStages < rows_rounds) issue(it + kGStages);
+        // GS slots stream while this row computes
+        if (it + GS < rows_rounds) issue(it + GS);
 #pragma unroll
         for (int i = 0; i < NBL; i++) a += block_dot(wv[i], sel, dshift, L, i);
         a = wave_sum_dpp(a);
@@ -941,7 +961,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
 }
 
 constexpr int lds_bytes(int pro, int epi, int nb) {
-    return (ring_waves(pro, epi) == 8 ? RingLds<8>::kTab : RingLds<4>::kTab) +
+    return ring_lds_tab(ring_waves(pro, epi), ring_stages(pro, epi)) +
            (pro != kProTable ? nb * 80 : 0) + (pro == kProTableLds ? kWave * 16 : 0);
 }
 
@@ -961,7 +981,7 @@ int ring_grid(int n, int S, int pro, int epi) {
     if (epi == kEpiGeglu) return n / kGegluUnits;
     const int wv = ring_waves(pro, epi);
     const int P = wv / S;
-    int grid = device_info().cus * (8 / wv);  // 8 waves per CU
+    int grid = device_info().cus * (ring_waves_per_cu(pro, epi) / wv);
     const int max_grid = (n + P - 1) / P;
     return grid > max_grid ? max_grid : grid;
 }
