@@ -851,6 +851,8 @@ def main():
     ap.add_argument("--gemv-rows", type=int, default=21504,
                     help="gemv workload: rows N (config 1 is 21504; other values sweep the "
                          "per-launch fixed cost against the streaming rate)")
+    ap.add_argument("--mmq-m", type=int, default=512,
+                    help="mmq workload: M (config 2 is 512; other values sweep the tile rounds)")
     ap.add_argument("--gemv-k", type=int, default=5376,
                     help="gemv workload: K (config 1 is 5376; 21504 is the FFN down projection, "
                          "streamed as four K-slices)")
@@ -885,7 +887,8 @@ def main():
     elif args.workload == "gemv":
         wl = Gemv(ctx, torch, n=args.gemv_rows, k=args.gemv_k)
     elif args.workload == "mmq":
-        wl = Mmq(ctx, torch)
+        wl = (Mmq(ctx, torch) if args.mmq_m == 512 else
+              Mmq(ctx, torch, m=args.mmq_m, label="M sweep around BASELINE config 2"))
     elif args.workload == "head_q6k":
         wl = HeadQ6K(ctx, torch)
     elif args.workload == "attn_prefill":
