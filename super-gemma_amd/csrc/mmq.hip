@@ -259,16 +259,21 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
             o.sb[i] = S.dw[blk][wn * 64 + i * 32 + r];
         }
     };
+    // Scale operands: lane (r, h = 0) holds K term 0 = d of its row (A) /
+    // column (B); every other K term is zero.  Kept across blocks, so only
+    // the first word of each is rewritten per block (the zero words stay in
+    // their registers).
+    v4i asv[2] = {}, bsv[2] = {};
     // One block on the wave's 2×2 tiles.  Tile t's MFMAs are issued before
     // tile t-1's rescale, so the matrix cores work while the VALU converts.
     auto block = [&](const Ops &o) {
-        // scale operands: lane (r, h = 0) holds K term 0 = d of its row
-        // (A) / column (B); every other K term is zero
         h8 as[2], bs[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            as[i] = __builtin_bit_cast(h8, v4i{h == 0 ? (int)o.sa[i] : 0, 0, 0, 0});
-            bs[i] = __builtin_bit_cast(h8, v4i{h == 0 ? (int)o.sb[i] : 0, 0, 0, 0});
+            asv[i][0] = h == 0 ? (int)o.sa[i] : 0;
+            bsv[i][0] = h == 0 ? (int)o.sb[i] : 0;
+            as[i] = __builtin_bit_cast(h8, asv[i]);
+            bs[i] = __builtin_bit_cast(h8, bsv[i]);
         }
         v16i d[2];
         f32x16 sc[2];
