@@ -51,8 +51,8 @@ constexpr int kMWG = 256;
 struct Stage {
     int8_t a[BM * ROWB];      // activations, [row][k]
     int8_t b[BN * ROWB];      // weights (q-8), [col][k]
-    uint16_t da[KB][BM];      // activation scales (f16 bits), [block][row]
-    uint16_t dw[KB][BN];      // weight scales (f16 bits), [block][col]
+    uint16_t da[BM][KB];      // activation scales (f16 bits), [row][block]
+    uint16_t dw[BN][KB];      // weight scales (f16 bits), [col][block]
 };
 
 __device__ __forceinline__ uint32_t unpack_lo(uint32_t q) {
@@ -177,12 +177,13 @@ __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
         hi = make_uint4(unpack_hi(qb[0]), unpack_hi(qb[1]), unpack_hi(qb[2]), unpack_hi(qb[3]));
         *reinterpret_cast<uint4 *>(dst + 32) = lo;
         *reinterpret_cast<uint4 *>(dst + 48) = hi;
-        S.dw[2 * pair][col] = (uint16_t)(pf.w[0] & 0xffffu);
-        S.dw[2 * pair + 1][col] = (uint16_t)(pf.w[4] >> 16);
+        // the two blocks' scales: low half of word 0, high half of word 4
+        *reinterpret_cast<uint32_t *>(&S.dw[col][2 * pair]) =
+            (pf.w[0] & 0xffffu) | (pf.w[4] & 0xffff0000u);
     }
     if (t < BM) {
 #pragma unroll
-        for (int i = 0; i < KB; i++) S.da[i][t] = pf.da[i];
+        for (int i = 0; i < KB; i++) S.da[t][i] = pf.da[i];
     }
 }
 
@@ -243,10 +244,22 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
     __syncthreads();
 
     // LDS operands of one block: int8 fragments of the wave's two row and
-    // two column tiles, and the f16 scale bits of its rows and columns
+    // two column tiles
     struct Ops {
         v4i af[2], bf[2];
-        uint32_t sa[2], sb[2];
+    };
+    // the f16 scale bits of the wave's two row and two column tiles for the
+    // stage's four blocks (two per word), read once per stage; zero in the
+    // lanes (h = 1) whose K terms of the scale MFMA are zero
+    uint2 sa4[2], sb4[2];
+    auto ld_scales = [&](const Stage &S) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint2 a = *reinterpret_cast<const uint2 *>(&S.da[wm * 64 + i * 32 + r][0]);
+            const uint2 b = *reinterpret_cast<const uint2 *>(&S.dw[wn * 64 + i * 32 + r][0]);
+            sa4[i] = h == 0 ? a : make_uint2(0u, 0u);
+            sb4[i] = h == 0 ? b : make_uint2(0u, 0u);
+        }
     };
     auto ld_ops = [&](const Stage &S, int blk, Ops &o) {
 #pragma unroll
@@ -255,8 +268,6 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
                 &S.a[(wm * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
             o.bf[i] = *reinterpret_cast<const v4i *>(
                 &S.b[(wn * 64 + i * 32 + r) * ROWB + blk * 32 + h * 16]);
-            o.sa[i] = S.da[blk][wm * 64 + i * 32 + r];
-            o.sb[i] = S.dw[blk][wn * 64 + i * 32 + r];
         }
     };
     // Scale operands: lane (r, h = 0) holds K term 0 = d of its row (A) /
@@ -266,12 +277,14 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
     v4i asv[2] = {}, bsv[2] = {};
     // One block on the wave's 2×2 tiles.  Tile t's MFMAs are issued before
     // tile t-1's rescale, so the matrix cores work while the VALU converts.
-    auto block = [&](const Ops &o) {
+    // wa / wb: the scale words of the block pair (blocks 2p, 2p + 1), hi =
+    // the pair's second block
+    auto block = [&](const Ops &o, const uint32_t (&wa)[2], const uint32_t (&wb)[2], bool hi) {
         h8 as[2], bs[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            asv[i][0] = h == 0 ? (int)o.sa[i] : 0;
-            bsv[i][0] = h == 0 ? (int)o.sb[i] : 0;
+            asv[i][0] = (int)(hi ? wa[i] >> 16 : wa[i] & 0xffffu);
+            bsv[i][0] = (int)(hi ? wb[i] >> 16 : wb[i] & 0xffffu);
             as[i] = __builtin_bit_cast(h8, asv[i]);
             bs[i] = __builtin_bit_cast(h8, bsv[i]);
         }
@@ -299,15 +312,23 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
         const Stage &S = stages[s & 1];
         // the next block's LDS operands load while this block computes
         // (two blocks per iteration, so both operand sets keep fixed registers)
-        Ops cur;
-        ld_ops(S, 0, cur);
+        Ops o0, o1;
+        ld_ops(S, 0, o0);
+        ld_scales(S);
 #pragma unroll 1
-        for (int blk = 0; blk < KB; blk++) {
-            Ops nxt;
-            ld_ops(S, min(blk + 1, KB - 1), nxt);
+        for (int bp = 0; bp < KB; bp += 2) {
+            ld_ops(S, bp + 1, o1);
             asm volatile("" ::: "memory");  // keeps the reads above the block's MFMAs
-            block(cur);
-            cur = nxt;
+            uint32_t wa[2], wb[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                wa[i] = bp == 0 ? sa4[i].x : sa4[i].y;
+                wb[i] = bp == 0 ? sb4[i].x : sb4[i].y;
+            }
+            block(o0, wa, wb, false);
+            ld_ops(S, min(bp + 2, KB - 1), o0);
+            asm volatile("" ::: "memory");
+            block(o1, wa, wb, true);
         }
         if (s + 1 < n_stages) store_stage(pf, stages[(s + 1) & 1]);
         __syncthreads();
