@@ -186,7 +186,8 @@ __global__ __launch_bounds__(kWG) void gemv_q4_0_kernel(const uint8_t *__restric
 // epilogue, 32-unit limb blocks, so 336 workgroups on 256 CUs) 25.5 ->
 // 29.2 us, and table-fed launches gain nothing.
 constexpr int ring_waves(int pro, int epi) {
-    return (pro == kProNorm || pro == kProEmbed || pro == kProX || pro == kProTableLds) && epi == kEpiRows ? 8 : 4;
+    return (pro == kProNorm || pro == kProEmbed || pro == kProX || pro == kProTableLds ||
+            pro == kProSliceLds) && epi == kEpiRows ? 8 : 4;
 }
 // Ring slots per wave and waves per CU (the grid).  The one-slice plain
 // launches (the limb table copied into LDS, or built from x in the
@@ -202,7 +203,7 @@ constexpr int ring_waves(int pro, int epi) {
 // bytes in flight stream faster here: three slots at 8 waves per CU took
 // 13.3-13.5 us at config 1, six 15.8 us.
 constexpr bool ring_plain(int pro, int epi) {
-    return (pro == kProTableLds || pro == kProX) && epi == kEpiRows;
+    return (pro == kProTableLds || pro == kProSliceLds || pro == kProX) && epi == kEpiRows;
 }
 constexpr int ring_stages(int pro, int epi) { return ring_plain(pro, epi) ? 1 : 2; }
 constexpr int ring_waves_per_cu(int pro, int epi) { return ring_plain(pro, epi) ? 16 : 8; }
@@ -382,9 +383,16 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     static_assert(EPI != kEpiGeglu || WV * 8 == kGegluUnits, "8 GeGLU units per wave");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int s = wave % S;              // K-slice of this wave
-    const int rw = wave / S;             // row within the workgroup's row group
-    const int P = (kRWG / kWave) / S;    // rows per workgroup iteration
+    // kProSliceLds: the workgroup's waves share one K-slice (its table in
+    // LDS) and take P = WV different rows; otherwise the S waves of a row
+    // group take the row's S slices
+    constexpr bool kSliceWG = PRO == kProSliceLds;
+    constexpr bool kTabLds = PRO == kProTableLds || kSliceWG;
+    static_assert(!kSliceWG || EPI == kEpiRows, "per-workgroup slices write split rows");
+    const int s = kSliceWG ? (int)(blockIdx.x % S) : wave % S;  // K-slice of this wave
+    const int rw = kSliceWG ? wave : wave / S;  // row within the workgroup's row group
+    const int P = kSliceWG ? WV : (kRWG / kWave) / S;  // rows per workgroup iteration
+    const int wgi = kSliceWG ? (int)(blockIdx.x / S) : (int)blockIdx.x;  // row group
     uint8_t *ring = gemv_smem + wave * (GS * kRSlot);
     uint8_t *red = gemv_smem + Lds::kRed;  // [2][waves] floats
     uint8_t *scr = gemv_smem + Lds::kScr;
@@ -395,8 +403,8 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     const int slice_blocks = min(slice, nb - b0);
     const int slice_off = b0 * 18;
     const int slice_bytes = slice_blocks * 18;
-    const int G = gridDim.x * P;         // rows advanced per iteration by the grid
-    const int r0 = blockIdx.x * P + rw;
+    const int G = (kSliceWG ? (int)gridDim.x / S : (int)gridDim.x) * P;  // rows per round
+    const int r0 = wgi * P + rw;
     constexpr int kUnitsPerWave = kGegluUnits / (kRWG / kWave);
     const int u0 = blockIdx.x * kGegluUnits + wave * kUnitsPerWave;  // kEpiGeglu
 
@@ -410,7 +418,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     // real rounds are fetched, so no wave waits on loads it never uses
     auto row_of = [&](int it) -> int { return r0 + it * G; };  // row of round `it`
     const int rows_rounds =
-        EPI == kEpiGeglu ? 2 * kUnitsPerWave : (n - blockIdx.x * P + G - 1) / G;
+        EPI == kEpiGeglu ? 2 * kUnitsPerWave : (n - wgi * P + G - 1) / G;
     // the weight slice of round `it` into ring slot `slot`
     auto issue = [&](int it) {
         uint8_t *slot = ring + (it % GS) * kRSlot;
@@ -548,12 +556,13 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                     ((uint32_t)qs[3] << 24);
             av[k] = reinterpret_cast<const float4 *>(fz.w)[b * 8 + ge];
         }
-    } else if (PRO == kProTableLds) {
-        // the limb table (nb·80 B, L2-resident, shared by every workgroup)
-        // into LDS by DMA, 16 B per lane; lanes past its end repeat the last
-        // chunk into the slack after it
-        const int chunks = nb * 5;
-        const uint8_t *src = reinterpret_cast<const uint8_t *>(xl);
+    } else if (kTabLds) {
+        // the limb table (nb·80 B, or the workgroup's slice of it;
+        // L2-resident, shared by every workgroup) into LDS by DMA, 16 B per
+        // lane; lanes past its end repeat the last chunk into the slack
+        // after it
+        const int chunks = (kSliceWG ? slice_blocks : nb) * 5;
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(xl + (kSliceWG ? b0 : 0));
         for (int c = wave * kWave; c < chunks; c += kRWG)
             __builtin_amdgcn_global_load_lds((gvoid_t *)(src + min(c + lane, chunks - 1) * 16),
                                              (lvoid_t *)(tab + c * 16), 16, 0, 0);
@@ -605,7 +614,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 settle(av[k]);
             }
         }
-        static_assert(EPI != kEpiResid || PRO == kProTable || PRO == kProTableLds,
+        static_assert(EPI != kEpiResid || PRO == kProTable || kTabLds,
                       "the residual epilogue's row loads are waited for with the table");
     }
 
@@ -713,7 +722,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
                 reinterpret_cast<float4 *>(fz.x_out)[xo_i] =
                     make_float4(s_out * (xo_in.x + ra * xo_u.x), s_out * (xo_in.y + ra * xo_u.y),
                                 s_out * (xo_in.z + ra * xo_u.z), s_out * (xo_in.w + ra * xo_u.w));
-        } else if (PRO == kProTableLds) {
+        } else if (kTabLds) {
             // the table's DMA (and the residual epilogue's row loads) were
             // issued before the stream's first slices
             asm volatile("s_waitcnt vmcnt(%3)"
@@ -790,9 +799,10 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
         f32x4_t r00 = {}, r01 = {}, r02 = {}, r03 = {}, r10 = {}, r11 = {}, r12 = {}, r13 = {},
                 r20 = {}, r21 = {}, r22 = {}, r23 = {};
         float e0 = 0.f, e1 = 0.f, e2 = 0.f;
-        const uint32_t ta0 = (uint32_t)(uintptr_t)(tab + min(b0 + lane, nb - 1) * 80);
-        const uint32_t ta1 = (uint32_t)(uintptr_t)(tab + min(b0 + lane + kWave, nb - 1) * 80);
-        const uint32_t ta2 = (uint32_t)(uintptr_t)(tab + min(b0 + lane + 2 * kWave, nb - 1) * 80);
+        const int tb0 = kSliceWG ? 0 : b0, tlast = kSliceWG ? slice_blocks - 1 : nb - 1;
+        const uint32_t ta0 = (uint32_t)(uintptr_t)(tab + min(tb0 + lane, tlast) * 80);
+        const uint32_t ta1 = (uint32_t)(uintptr_t)(tab + min(tb0 + lane + kWave, tlast) * 80);
+        const uint32_t ta2 = (uint32_t)(uintptr_t)(tab + min(tb0 + lane + 2 * kWave, tlast) * 80);
 #define SGQ_RDBLK(A, Q0, Q1, Q2, Q3, D)                                                      \
     asm volatile("ds_read_b128 %0, %5\n ds_read_b128 %1, %5 offset:16\n"                      \
                  "ds_read_b128 %2, %5 offset:32\n ds_read_b128 %3, %5 offset:48\n"            \
@@ -834,7 +844,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
     float held = 0.f;                              // kEpiRows, deferred stores
     // K-slices of plain rows combined after the loop (the row-partials area
     // holds 64 rounds per wave); more rounds keep one barrier per row
-    const bool defer = EPI == kEpiRows && S > 1 && !tg.split_out && rows_rounds <= kWave;
+    const bool defer = EPI == kEpiRows && !kSliceWG && S > 1 && !tg.split_out && rows_rounds <= kWave;
     for (int it = 0; it < rows_rounds; it++) {
         // wait for round `it`: the slices issued after it may stay in flight
         static_assert(GS >= 1 && GS <= 6, "the wait switch covers 0..5 rounds ahead");
@@ -879,7 +889,7 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
             continue;
         }
         bool have = true;
-        if (S > 1 && !(EPI == kEpiRows && tg.split_out)) {
+        if (!kSliceWG && S > 1 && !(EPI == kEpiRows && tg.split_out)) {
             // one barrier per row: partials alternate between two slots, and
             // a slot is rewritten only after the next row's barrier, which
             // the reading wave reaches after its reads
@@ -962,7 +972,8 @@ __global__ __launch_bounds__(ring_waves(PRO, EPI) * kWave) void gemv_q4_0_ring_k
 
 constexpr int lds_bytes(int pro, int epi, int nb) {
     return ring_lds_tab(ring_waves(pro, epi), ring_stages(pro, epi)) +
-           (pro != kProTable ? nb * 80 : 0) + (pro == kProTableLds ? kWave * 16 : 0);
+           (pro != kProTable ? nb * 80 : 0) +
+           (pro == kProTableLds || pro == kProSliceLds ? kWave * 16 : 0);
 }
 
 template <int NBL, int PRO, int EPI>
@@ -971,7 +982,8 @@ int ring_attr() {
     if (!attr) {
         SGQ_HIP(hipFuncSetAttribute((const void *)gemv_q4_0_ring_kernel<NBL, PRO, EPI>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    lds_bytes(PRO, EPI, kMaxTabBlocks)));
+                                    PRO == kProTableLds ? 80 * 1024
+                                                        : lds_bytes(PRO, EPI, kMaxTabBlocks)));
         attr = true;
     }
     return SGQ_OK;
@@ -980,8 +992,13 @@ int ring_attr() {
 int ring_grid(int n, int S, int pro, int epi) {
     if (epi == kEpiGeglu) return n / kGegluUnits;
     const int wv = ring_waves(pro, epi);
-    const int P = wv / S;
     int grid = device_info().cus * (ring_waves_per_cu(pro, epi) / wv);
+    if (pro == kProSliceLds) {  // S workgroups per row group, one per K-slice
+        const int max_grid = (n + wv - 1) / wv * S;
+        grid = grid > max_grid ? max_grid : grid;
+        return grid / S * S;
+    }
+    const int P = wv / S;
     const int max_grid = (n + P - 1) / P;
     return grid > max_grid ? max_grid : grid;
 }
@@ -992,7 +1009,8 @@ int launch_ring(hipStream_t st, const GemvTargets &tg, const BlockLimbs *xl, int
     if (int rc = ring_attr<NBL, PRO, EPI>()) return rc;
     const int grid = ring_grid(n, S, PRO, EPI);
     hipLaunchKernelGGL((gemv_q4_0_ring_kernel<NBL, PRO, EPI>), dim3(grid),
-                       dim3(ring_waves(PRO, EPI) * kWave), lds_bytes(PRO, EPI, nb), st, tg, xl, n,
+                       dim3(ring_waves(PRO, EPI) * kWave),
+                       lds_bytes(PRO, EPI, PRO == kProSliceLds ? slice : nb), st, tg, xl, n,
                        nb, S, slice, fz);
     SGQ_HIP(hipGetLastError());
     return SGQ_OK;
@@ -1060,6 +1078,8 @@ static int launch_ring_any(hipStream_t st, const GemvTargets &tg, const BlockLim
         return launch_ring_nbl<kProTableLds, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProTableLds && epi == kEpiResid)
         return launch_ring_nbl<kProTableLds, kEpiResid>(st, tg, xl, n, nb, S, slice, fz);
+    if (pro == kProSliceLds && epi == kEpiRows)
+        return launch_ring_nbl<kProSliceLds, kEpiRows>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProNorm && epi == kEpiGeglu)
         return launch_ring_nbl<kProNorm, kEpiGeglu>(st, tg, xl, n, nb, S, slice, fz);
     if (pro == kProTable && epi == kEpiResid)
@@ -1083,6 +1103,7 @@ int gemv_prepare() {
     if (!rc) rc = attr_nbl<kProX, kEpiRows>();
     if (!rc) rc = attr_nbl<kProTableLds, kEpiRows>();
     if (!rc) rc = attr_nbl<kProTableLds, kEpiResid>();
+    if (!rc) rc = attr_nbl<kProSliceLds, kEpiRows>();
     if (!rc) rc = attr_nbl<kProNorm, kEpiGeglu>();
     if (!rc) rc = attr_nbl<kProTable, kEpiResid>();
     return rc;
@@ -1103,7 +1124,10 @@ int launch_gemv_fused(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     int S, slice;
     const int nb = (int)(k / 32);
     SGQ_CHECK(ring_geometry(nb, &S, &slice), "gemv (fused): k=%u outside the streamed geometry", k);
-    SGQ_CHECK(pro == kProTable || S == 1, "gemv (fused): prologues need k <= %d", kRSlot / 18 * 32);
+    SGQ_CHECK(pro == kProTable || pro == kProTableLds || S == 1,
+              "gemv (fused): prologues need k <= %d", kRSlot / 18 * 32);
+    SGQ_CHECK(pro != kProTableLds || lds_bytes(pro, epi, nb) <= 80 * 1024,
+              "gemv (fused): k=%u: the limb table does not fit two workgroups' LDS", k);
     SGQ_CHECK((pro != kProTable && pro != kProTableLds) || xl != nullptr, "gemv (fused): no limb table");
     SGQ_CHECK(pro != kProNorm || (fz.part && fz.np > 0 && fz.np <= kGemvMaxPartials && fz.A &&
                                   fz.B && (!fz.x_out || (fz.x_in && fz.u))),
@@ -1175,6 +1199,12 @@ int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     if (S == 1)  // one K-slice: the table goes to LDS once per workgroup
         return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1],
                                nb, S, slice, kProTableLds, kEpiRows);
+    // split rows: one K-slice per workgroup and its part of the table in LDS
+    // (K=21504, N=5376: 12.4-13.2 against 14.0-14.8 us with the S waves of
+    // a row group taking the row's S slices, bit-identical partials)
+    if (tg.split_out)
+        return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1],
+                               nb, S, slice, kProSliceLds, kEpiRows);
     return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1], nb,
                            S, slice);
 }

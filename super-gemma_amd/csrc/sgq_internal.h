@@ -89,7 +89,11 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uin
 //   kProTable  the limb table xl (written by an earlier kernel), each wave
 //              loading its lanes' entries into registers;
 //   kProTableLds  the same table copied into LDS once per workgroup by
-//              DMA (single K-slice only);
+//              DMA (one K-slice, or up to four with the residual epilogue
+//              while the table fits two workgroups' LDS);
+//   kProSliceLds  K-sliced rows with split output: workgroup b takes K-slice
+//              b % S of its rows and copies only that slice of the table
+//              into LDS; each K-slice partial goes to y[slice·n + row];
 //   kProNorm   f = rb·s·(A + ra·B) with ra = 1/sqrt(P1/K + eps),
 //              rb = 1/sqrt(s²(P4 + 2·ra·P2 + ra²·P3)/K + eps) from the np
 //              partial sums (P1..P4) an kEpiResid launch left in part, and
@@ -110,7 +114,7 @@ int launch_gemv_q6_k(hipStream_t st, const void *w, size_t row_stride, const uin
 //   kEpiGeglu  targets gate (w[0]) and up (w[1]), n = units: workgroup b
 //              computes units [32b, 32b+32) and writes block b of the limbs
 //              of gelu_tanh(gate)·up into hl.
-enum { kProTable = 0, kProNorm = 1, kProEmbed = 2, kProX = 3, kProTableLds = 4 };
+enum { kProTable = 0, kProNorm = 1, kProEmbed = 2, kProX = 3, kProTableLds = 4, kProSliceLds = 5 };
 enum { kEpiRows = 0, kEpiResid = 1, kEpiGeglu = 2 };
 constexpr int kGemvMaxPartials = 512;
 struct GemvFuse {
