@@ -1205,6 +1205,12 @@ int launch_gemv_limbs(hipStream_t st, const GemvTargets &tg, const void *xl, uin
     if (tg.split_out)
         return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1],
                                nb, S, slice, kProSliceLds, kEpiRows);
+    // K-sliced rows combined in the launch: the whole table in LDS when two
+    // workgroups' copies fit the CU (K <= 21504 or so; K=21504, N=5376:
+    // 13.4-14.5 -> 12.8-13.0 us)
+    if (lds_bytes(kProTableLds, kEpiRows, nb) <= 80 * 1024)
+        return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1],
+                               nb, S, slice, kProTableLds, kEpiRows);
     return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(xl), tg.end[tg.count - 1], nb,
                            S, slice);
 }
@@ -1239,8 +1245,7 @@ int gemv_q4_0_t(hipStream_t st, const void *w, const TX *x, TY *y, uint32_t n, u
         }
         int rc = launch_quant_limbs(st, x, workspace, k);
         if (rc) return rc;
-        return launch_ring_any(st, tg, static_cast<const BlockLimbs *>(workspace), (int)n, nb, S,
-                               slice);
+        return launch_gemv_limbs(st, tg, workspace, k);
     }
     // Register path (any K % 64 == 0): each wave quantizes its own blocks.
     S = 1;
