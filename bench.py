@@ -870,7 +870,7 @@ def main():
                     help="gemv workload: rows N (config 1 is 21504; other values sweep the "
                          "per-launch fixed cost against the streaming rate)")
     ap.add_argument("--mmq-m", type=int, default=512,
-                    help="mmq workload: M (config 2 is 512; other values sweep the tile rounds)")
+                    help="mmq / splitk workloads: M (512 keeps configs 2 and 3; other values sweep the tile rounds)")
     ap.add_argument("--gemv-k", type=int, default=5376,
                     help="gemv workload: K (config 1 is 5376; 21504 is the FFN down projection, "
                          "streamed as four K-slices)")
@@ -928,7 +928,10 @@ def main():
         wl = AttnDecode(ctx, torch, {"4k": 4096, "32k": 32768, "128k": 131072}[args.workload[12:]],
                         splits=args.attn_splits)
     else:
-        wl = Mmq(ctx, torch, m=2048, k=21504, n=5376, split=args.split_k, label="BASELINE config 3")
+        wl = (Mmq(ctx, torch, m=2048, k=21504, n=5376, split=args.split_k, label="BASELINE config 3")
+              if args.mmq_m == 512 else
+              Mmq(ctx, torch, m=args.mmq_m, k=21504, n=5376, split=args.split_k,
+                  label="M sweep around BASELINE config 3"))
     torch.cuda.synchronize()
     for i in range(args.warmup):
         wl.step(i)
