@@ -177,3 +177,28 @@ def test_fused_after_prefill(ctx, oracle):
         torch.cuda.synchronize()
         _check_logits(host(logits), ref.decode(t), f"after prefill {i}")
     model.close()
+
+
+@pytest.mark.parametrize("ffn", [8192, 21504])
+@pytest.mark.parametrize("mode", [0, 2])
+def test_k_sliced_down_projection_matches_oracle(ctx, oracle, ffn, mode):
+    """FFN widths whose down projection runs in 2 (8192) or 4 (21504)
+    K-slices: the kernel-per-operator mode writes the slice partials with
+    one K-slice per workgroup (its part of the limb table in LDS), the fused
+    mode keeps the whole table in LDS and sums the slices in the residual
+    epilogue; both against the oracle decoder."""
+    import sgq
+    from oracle.model import OracleDecoder
+
+    print(f"k-sliced down ffn={ffn} mode={mode}", flush=True)
+    cfg = _small_cfg(sgq, n_layers=2, ffn=ffn, seed=0x51CE + ffn)
+    model = sgq.Model(ctx, cfg)
+    model.decode_mode = mode
+    d = cfg.as_dict()
+    ref = OracleDecoder(d, _weights(model, d))
+    logits = empty(cfg.vocab, torch.float32)
+    for i, t in enumerate([7, 1000, 3, 2047, 64]):
+        model.decode(t, logits)
+        torch.cuda.synchronize()
+        _check_logits(host(logits), ref.decode(t), i)
+    model.close()
