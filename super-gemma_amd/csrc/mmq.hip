@@ -28,7 +28,8 @@
 //  * Tile order is XCD-aware: consecutive workgroup ids land on different
 //    XCDs (each with its own L2), so ids are remapped so that every XCD
 //    walks a contiguous range of N-tiles with all their M-tiles, and a
-//    weight strip is fetched from HBM once per XCD.
+//    weight strip is fetched from HBM once per XCD; with many M-tiles the
+//    XCD takes them 8 at a time across its N-tiles.
 //  * Split-K (slices of the block range, factor 1/2/4/8) writes fp32
 //    partial tiles; a second kernel sums them in fixed order s = 0..S-1.
 #include "sgq_internal.h"
@@ -202,8 +203,23 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
     const int tiles = mt * nt;
     int id = blockIdx.x;
     const int xcds = 8;
-    if (tiles % xcds == 0) id = (id % xcds) * (tiles / xcds) + id / xcds;
-    const int tn = id / mt, tm = id % mt;
+    constexpr int kGroupM = 8;
+    int tn, tm;
+    if (nt % xcds == 0 && mt % kGroupM == 0) {
+        // XCD x owns N-tiles [x·nt/8, (x+1)·nt/8) with every M-tile, walked in
+        // groups of 8 M-tiles across all its N-tiles: the XCD's resident
+        // tiles (64) then share 8 activation panels and 8 weight strips in
+        // its L2 instead of all M-tiles' panels and 2 strips (M = 4096: 646
+        // -> 656 TOP/s, the 4096-token prefill +1.3-2%; 16 M-tiles per group
+        // measured as the plain order)
+        const int x = id % xcds, j = id / xcds, ntx = nt / xcds, gs = kGroupM * ntx;
+        const int g = j / gs, r = j % gs;
+        tm = g * kGroupM + r % kGroupM;
+        tn = x * ntx + r / kGroupM;
+    } else {
+        if (tiles % xcds == 0) id = (id % xcds) * (tiles / xcds) + id / xcds;
+        tn = id / mt, tm = id % mt;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int nb = k / 32;
