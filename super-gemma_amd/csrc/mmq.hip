@@ -98,7 +98,7 @@ __device__ __forceinline__ void load_stage(Prefetch &pf, const int8_t *__restric
             const bool two = b + 1 < b_end;
 #pragma unroll
             for (int j = 0; j < 9; j++)
-                pf.w[j] = (j < 5 || two) ? __builtin_nontemporal_load(src + j) : 0u;
+                pf.w[j] = (j < 5 || two) ? src[j] : 0u;
         } else {
 #pragma unroll
             for (int j = 0; j < 9; j++) pf.w[j] = 0u;
@@ -140,8 +140,11 @@ __device__ __forceinline__ void load_stage_al(Prefetch &pf, const AlignedSrc &sr
 #pragma unroll
     for (int i = 0; i < 4; i++) pf.a[i] = a[i];
     const uint32_t *w = src.w + (b0 * 18) / 4;  // b0 % 4 == 0: 72 B per stage
+    // plain loads: a weight strip serves every M-tile of its column group
+    // (from L2); with the nontemporal hint config 2 ran at 526-530 against
+    // 573-579 TOP/s and M = 4096 at 676 against 758-763
 #pragma unroll
-    for (int j = 0; j < 9; j++) pf.w[j] = __builtin_nontemporal_load(w + j);
+    for (int j = 0; j < 9; j++) pf.w[j] = w[j];
     if (threadIdx.x < BM) {
         const uint2 d = src.da[b0 / 4];
         pf.da[0] = (uint16_t)(d.x & 0xffffu);
