@@ -19,9 +19,11 @@
 //    32 distinct banks.  Double-buffered: stage s+1's global loads are in
 //    flight while stage s computes; one barrier per stage.
 //  * Rescale: the scale products d_a·d_w of a 32×32 tile come from the
-//    matrix cores too — one v_mfma_f32_32x32x16_f16 whose only non-zero K
+//    matrix cores too — one v_mfma_f32_32x32x8_f16 whose only non-zero K
 //    term is (d_a[row], d_w[col]) gives the exact outer product (f16·f16 is
-//    exact in f32) in the accumulator layout of the int8 MFMA.  The VALU is
+//    exact in f32) in the accumulator layout of the int8 MFMA (the K=8 form
+//    costs the matrix cores less than the K=16 one: config 2 571 -> 620-627
+//    TOP/s, M = 4096 750 -> 786, with half the operand registers).  The VALU is
 //    left with one cvt and one FMA per output element and block, and that —
 //    not the MFMA — still bounds the kernel (a wave64 VALU op costs 4
 //    cycles against 32 for an MFMA covering 1024 elements).
@@ -39,7 +41,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, KB = 4;   // tile rows, cols, blocks per stage
@@ -301,19 +304,19 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
     // column (B); every other K term is zero.  Kept across blocks, so only
     // the first word of each is rewritten per block (the zero words stay in
     // their registers).
-    v4i asv[2] = {}, bsv[2] = {};
+    v2i asv[2] = {}, bsv[2] = {};
     // One block on the wave's 2×2 tiles.  Tile t's MFMAs are issued before
     // tile t-1's rescale, so the matrix cores work while the VALU converts.
     // wa / wb: the scale words of the block pair (blocks 2p, 2p + 1), hi =
     // the pair's second block
     auto block = [&](const Ops &o, const uint32_t (&wa)[2], const uint32_t (&wb)[2], bool hi) {
-        h8 as[2], bs[2];
+        h4 as[2], bs[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             asv[i][0] = (int)(hi ? wa[i] >> 16 : wa[i] & 0xffffu);
             bsv[i][0] = (int)(hi ? wb[i] >> 16 : wb[i] & 0xffffu);
-            as[i] = __builtin_bit_cast(h8, asv[i]);
-            bs[i] = __builtin_bit_cast(h8, bsv[i]);
+            as[i] = __builtin_bit_cast(h4, asv[i]);
+            bs[i] = __builtin_bit_cast(h4, bsv[i]);
         }
         v16i d[2];
         f32x16 sc[2];
@@ -324,7 +327,7 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
             if (t < 4) {
                 const int i = t >> 1, j = t & 1;
                 d[t & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.af[i], o.bf[j], zero, 0, 0, 0);
-                sc[t & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as[i], bs[j], fzero, 0, 0, 0);
+                sc[t & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(as[i], bs[j], fzero, 0, 0, 0);
             }
             if (t > 0) {
                 const int u = t - 1, i = u >> 1, j = u & 1;
