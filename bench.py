@@ -783,7 +783,7 @@ def measured_peaks(torch):
     out["hbm_read_gbs"] = nbytes / (ms * 1e-3) / 1e9
     del big
     out["note"] = ("int8 MFMA 32x32x32 only (16 waves/CU); the same with 16 cvt + 16 FMA "
-                   "per MFMA, and with the f16 scale MFMA too (8 waves/CU, the MMQ's "
+                   "per MFMA, and with the f16 scale MFMA (32x32x8) too (8 waves/CU, the MMQ's "
                    "occupancy); streaming read of 4 GiB (64 KB chunks, nontemporal 16-byte loads)")
     return out
 

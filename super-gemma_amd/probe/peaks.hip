@@ -8,7 +8,7 @@
 //              MMQ issues it) also 16 v_cvt_f32_i32 + 16 FMA of its result
 //              into fp32 accumulators: the ceiling of any kernel that
 //              rescales every block's exact i32 dot on the VALU;
-//      mode 2  mode 1 plus the v_mfma_f32_32x32x16_f16 that forms the
+//      mode 2  mode 1 plus the v_mfma_f32_32x32x8_f16 that forms the
 //              block's d_a x d_w scale outer product (the MMQ's structure);
 //      mode 3  the block dot on the f16 matrix cores (exact), the scale
 //              MFMA and one FMA per output element, software-pipelined.
@@ -24,6 +24,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // mode 3: the block dot on the f16 matrix cores (int8 and q-8 values are
@@ -79,8 +81,8 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int *__restr
     } else {
         const v16i zero = {};
         const f32x16 fzero = {};
-        const h8 sa = __builtin_bit_cast(h8, v4i{0x3c00 + (t & 7), 0, 0, 0});
-        const h8 sb = __builtin_bit_cast(h8, v4i{0x3800 + (t & 3), 0, 0, 0});
+        const h4 sa = __builtin_bit_cast(h4, v2i{0x3c00 + (t & 7), 0});
+        const h4 sb = __builtin_bit_cast(h4, v2i{0x3800 + (t & 3), 0});
         f32x16 acc0 = {}, acc1 = {};
         f32x16 sc0, sc1;
 #pragma unroll
@@ -92,9 +94,9 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int *__restr
             // two block tiles per iteration: each MFMA's result is rescaled
             // while the other one runs, as in the MMQ's software pipeline
             const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, zero, 0, 0, 0);
-            if (MODE == 2) sc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, sb, fzero, 0, 0, 0);
+            if (MODE == 2) sc0 = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sb, fzero, 0, 0, 0);
             const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, zero, 0, 0, 0);
-            if (MODE == 2) sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(sb, sa, fzero, 0, 0, 0);
+            if (MODE == 2) sc1 = __builtin_amdgcn_mfma_f32_32x32x8f16(sb, sa, fzero, 0, 0, 0);
 #pragma unroll
             for (int q = 0; q < 16; q++) acc0[q] = __builtin_fmaf((float)d0[q], sc0[q], acc0[q]);
 #pragma unroll
