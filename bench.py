@@ -110,8 +110,9 @@ class Mmq:
         ctx.quant_q8_0(x, self.xs, self.xq)
         del x
         self.y = torch.empty(m * n, dtype=torch.float32, device="cuda")
-        self.part = (torch.empty(split * m * n, dtype=torch.float32, device="cuda")
-                     if split > 1 else None)
+        # split > 1: the K-slice partials; split 1: the workspace that lets the
+        # last part-filled round of tiles split over K
+        self.part = torch.empty(split * m * n, dtype=torch.float32, device="cuda")
         self.ops = 2.0 * m * n * k
 
     def step(self, i):

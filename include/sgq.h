@@ -267,7 +267,11 @@ int sgq_dequant_q8_0(sgq_ctx *ctx, const uint16_t *scales, const int8_t *quants,
  * (d_a[m,b]*d_w[n,b]) in fp32: gemm_q4_0_i8_* (crates/sg-gpu/shaders/
  * gemm_q4_0_i8.wgsl:153-393, gemm_q4_0_i8_bb_pfd.wgsl).  split_k in
  * {1,2,4,8}: for split_k > 1, `partials` must hold split_k*m*n floats and the
- * slices are summed in fixed order s = 0..split_k-1.  k % 32 == 0. */
+ * slices are summed in fixed order s = 0..split_k-1.  With split_k == 1,
+ * `partials` is optional (NULL or at least m*n floats): when given, tiles
+ * past the last whole round of resident workgroups are split over K into
+ * 2-4 parts summed in part order (fp32 output, m and n multiples of 128).
+ * k % 32 == 0. */
 int sgq_gemm_q4_0_q8(sgq_ctx *ctx, const void *w, const int8_t *xq, const uint16_t *xs,
                      float *y, uint32_t m, uint32_t n, uint32_t k, uint32_t split_k,
                      float *partials);

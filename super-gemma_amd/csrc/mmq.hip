@@ -194,50 +194,80 @@ __device__ __forceinline__ void store_stage(const Prefetch &pf, Stage &S) {
     }
 }
 
-// HOUT: the output is f16 (uint16_t bits, each sum rounded to nearest even:
-// the reference's y binding, gemm_q4_0_i8.wgsl:63); else fp32.
-template <bool AL, bool HOUT>
-__global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint8_t *__restrict__ W,
-                                                      const int8_t *__restrict__ xq,
-                                                      const uint16_t *__restrict__ xs,
-                                                      void *__restrict__ out_, int m, int n,
-                                                      int k, int mt, int nt, int split) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Stage *stages = reinterpret_cast<Stage *>(smem);
-
-    // XCD-aware tile order (see header).
+// Tile of the jl-th workgroup slot of XCD x (workgroup b runs on XCD b % 8,
+// jl = b / 8; tiles % 8 == 0, else x = 0 and jl = b).  XCD-aware order:
+// every XCD walks a contiguous range of the tiles.
+constexpr int kXcds = 8, kGroupM = 8;
+__device__ __forceinline__ void mmq_tile(int x, int jl, int mt, int nt, int *tm, int *tn) {
     const int tiles = mt * nt;
-    int id = blockIdx.x;
-    const int xcds = 8;
-    constexpr int kGroupM = 8;
-    int tn, tm;
-    if (nt % xcds == 0 && mt % kGroupM == 0) {
+    if (nt % kXcds == 0 && mt % kGroupM == 0) {
         // XCD x owns N-tiles [x·nt/8, (x+1)·nt/8) with every M-tile, walked in
         // groups of 8 M-tiles across all its N-tiles: the XCD's resident
         // tiles (64) then share 8 activation panels and 8 weight strips in
         // its L2 instead of all M-tiles' panels and 2 strips (M = 4096: 646
         // -> 656 TOP/s, the 4096-token prefill +1.3-2%; 16 M-tiles per group
         // measured as the plain order)
-        const int x = id % xcds, j = id / xcds, ntx = nt / xcds, gs = kGroupM * ntx;
-        const int g = j / gs, r = j % gs;
-        tm = g * kGroupM + r % kGroupM;
-        tn = x * ntx + r / kGroupM;
-    } else if (tiles % xcds == 0 && mt % kGroupM == 0) {
+        const int ntx = nt / kXcds, gs = kGroupM * ntx;
+        const int g = jl / gs, r = jl % gs;
+        *tm = g * kGroupM + r % kGroupM;
+        *tn = x * ntx + r / kGroupM;
+    } else if (tiles % kXcds == 0 && mt % kGroupM == 0) {
         // N-tiles not a multiple of 8: the same grouped order over the whole
         // grid, each XCD a contiguous eighth of it (the down projection at
         // M = 4096, K = 21504: 614-627 -> 634-642 TOP/s)
-        const int j = (id % xcds) * (tiles / xcds) + id / xcds, gs = kGroupM * nt;
+        const int j = x * (tiles / kXcds) + jl, gs = kGroupM * nt;
         const int g = j / gs, r = j % gs;
-        tm = g * kGroupM + r % kGroupM;
-        tn = r / kGroupM;
+        *tm = g * kGroupM + r % kGroupM;
+        *tn = r / kGroupM;
     } else {
-        if (tiles % xcds == 0) id = (id % xcds) * (tiles / xcds) + id / xcds;
-        tn = id / mt, tm = id % mt;
+        const int id = tiles % kXcds == 0 ? x * (tiles / kXcds) + jl : jl;
+        *tn = id / mt, *tm = id % mt;
     }
+}
+
+// Tail split (split = 1 only): when the tiles are more than whole rounds of
+// the resident workgroups, each XCD computes its first tail_fx tiles whole
+// and splits each of its remaining tiles over K into tail_st parts, one
+// workgroup each, so the last round is full; the parts go to tailp as
+// 128×128 fp32 tiles (slot = x·(tiles/8 − tail_fx) + tail tile, part) and
+// mmq_tail_reduce_kernel sums them in part order.
+struct TailSplit {
+    int fx, st;    // whole tiles per XCD, parts per tail tile (0: off)
+    float *part;
+};
+
+// HOUT: the output is f16 (uint16_t bits, each sum rounded to nearest even:
+// the reference's y binding, gemm_q4_0_i8.wgsl:63); else fp32.  TAIL: the
+// tail split is built in (a separate kernel, so the others keep their code).
+template <bool AL, bool HOUT, bool TAIL = false>
+__global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint8_t *__restrict__ W,
+                                                      const int8_t *__restrict__ xq,
+                                                      const uint16_t *__restrict__ xs,
+                                                      void *__restrict__ out_, int m, int n,
+                                                      int k, int mt, int nt, int split,
+                                                      TailSplit ts) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    Stage *stages = reinterpret_cast<Stage *>(smem);
+
+    // XCD-aware tile order (see header).
+    const int tiles = mt * nt;
+    const bool by_xcd = tiles % kXcds == 0;
+    const int x = by_xcd ? (int)(blockIdx.x % kXcds) : 0;
+    int jl = by_xcd ? (int)(blockIdx.x / kXcds) : (int)blockIdx.x;
+    int z = blockIdx.y;
+    int tail_slot = -1;
+    if (TAIL && jl >= ts.fx) {
+        const int k2 = jl - ts.fx, lx = tiles / kXcds - ts.fx;
+        jl = ts.fx + k2 / ts.st;
+        z = k2 % ts.st;
+        split = ts.st;
+        tail_slot = x * lx + k2 / ts.st;
+    }
+    int tm, tn;
+    mmq_tile(x, jl, mt, nt, &tm, &tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int nb = k / 32;
-    const int z = blockIdx.y;
     const int b_beg = (int)((long)nb * z / split) & ~(KB - 1);
     const int b_end = z + 1 == split ? nb : ((int)((long)nb * (z + 1) / split) & ~(KB - 1));
     const int n_stages = (b_end - b_beg + KB - 1) / KB;
@@ -367,6 +397,18 @@ __global__ __launch_bounds__(kMWG, SGQ_MMQ_WG_PER_CU) void mmq_kernel(const uint
 
     float *dst = static_cast<float *>(out_) + (size_t)z * m * n;
     uint16_t *dsth = static_cast<uint16_t *>(out_);
+    if (TAIL && tail_slot >= 0) {  // a K-part of a tail tile: tile-local rows of 128
+        float *tp = ts.part + ((size_t)tail_slot * ts.st + z) * (BM * BN);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    tp[(wm * 64 + i * 32 + 8 * (q / 4) + 4 * h + (q % 4)) * BN + wn * 64 + j * 32 +
+                       r] = acc[i][j][q];
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -402,6 +444,29 @@ __global__ void splitk_reduce_kernel(const float4 *__restrict__ part, float4 *__
     }
 }
 
+// y of the tail tiles: the tail_st parts summed in part order (float4 per
+// thread, one 128×128 tile per 16 workgroups of 256 threads).
+__global__ __launch_bounds__(256) void mmq_tail_reduce_kernel(TailSplit ts, float *__restrict__ y,
+                                                              int n, int mt, int nt) {
+    const int tiles = mt * nt, lx = tiles / kXcds - ts.fx;
+    const int slot = blockIdx.x / 16;  // tail tile
+    const int e = (blockIdx.x % 16) * 256 + threadIdx.x;  // float4 within the tile
+    const int x = slot / lx, jl = ts.fx + slot % lx;
+    int tm, tn;
+    mmq_tile(x, jl, mt, nt, &tm, &tn);
+    const float4 *p = reinterpret_cast<const float4 *>(ts.part + (size_t)slot * ts.st * (BM * BN));
+    float4 a = p[e];
+    for (int zz = 1; zz < ts.st; zz++) {
+        const float4 b = p[(size_t)zz * (BM * BN / 4) + e];
+        a.x += b.x;
+        a.y += b.y;
+        a.z += b.z;
+        a.w += b.w;
+    }
+    const int row = e / (BN / 4), c4 = e % (BN / 4);
+    *reinterpret_cast<float4 *>(y + (size_t)(tm * BM + row) * n + tn * BN + 4 * c4) = a;
+}
+
 }  // namespace
 
 namespace {
@@ -425,6 +490,8 @@ int gemm_t(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs, 
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<true, HOUT>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        SGQ_HIP(hipFuncSetAttribute((const void *)mmq_kernel<true, false, true>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr = true;
     }
     const int mt = (int)((m + BM - 1) / BM), nt = (int)((n + BN - 1) / BN);
@@ -433,15 +500,38 @@ int gemm_t(hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs, 
     // bounds are rounded down to KB)
     const bool aligned = m % BM == 0 && n % BN == 0 && (k / 32) % KB == 0 &&
                          ((uintptr_t)xs & 7) == 0;
-    if (aligned)
-        hipLaunchKernelGGL((mmq_kernel<true, HOUT>), dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+    // Tail split: aligned fp32 output, split_k = 1 and a partials buffer
+    // (m·n floats always suffice: the parts are at most one round of tiles)
+    TailSplit ts{0, 0, partials};
+    const int tiles = mt * nt, slots_x = device_info().cus * SGQ_MMQ_WG_PER_CU / kXcds;
+    // (only below two whole rounds: at M = 4096, N = 21504, with a tail of
+    // half a round split in 2, the launch measured 1.3% slower)
+    if (aligned && !HOUT && split_k == 1 && partials != nullptr && tiles % kXcds == 0 &&
+        slots_x > 0 && tiles / kXcds > slots_x && tiles / kXcds < 2 * slots_x) {
+        const int tx = tiles / kXcds, fx = tx / slots_x * slots_x, lx = tx - fx;
+        const int parts = lx > 0 ? std::min(4, slots_x / lx) : 0;
+        if (parts >= 2 && (int)(k / 32) / parts >= 4 * KB) ts.fx = fx, ts.st = parts;
+    }
+    const int grid_x = ts.st ? kXcds * (ts.fx + (tiles / kXcds - ts.fx) * ts.st) : tiles;
+    if (ts.st)
+        hipLaunchKernelGGL((mmq_kernel<true, false, true>), dim3(grid_x, split_k), dim3(kMWG), lds,
+                           st, static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n,
+                           (int)k, mt, nt, (int)split_k, ts);
+    else if (aligned)
+        hipLaunchKernelGGL((mmq_kernel<true, HOUT>), dim3(grid_x, split_k), dim3(kMWG), lds, st,
                            static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k,
-                           mt, nt, (int)split_k);
+                           mt, nt, (int)split_k, ts);
     else
-        hipLaunchKernelGGL((mmq_kernel<false, HOUT>), dim3(mt * nt, split_k), dim3(kMWG), lds, st,
+        hipLaunchKernelGGL((mmq_kernel<false, HOUT>), dim3(grid_x, split_k), dim3(kMWG), lds, st,
                            static_cast<const uint8_t *>(w), xq, xs, dst, (int)m, (int)n, (int)k,
-                           mt, nt, (int)split_k);
+                           mt, nt, (int)split_k, ts);
     SGQ_HIP(hipGetLastError());
+    if (ts.st) {
+        const int tail_tiles = kXcds * (tiles / kXcds - ts.fx);
+        hipLaunchKernelGGL(mmq_tail_reduce_kernel, dim3(tail_tiles * 16), dim3(256), 0, st, ts,
+                           static_cast<float *>(y), (int)n, mt, nt);
+        SGQ_HIP(hipGetLastError());
+    }
     if (split_k > 1) {
         const uint64_t n4 = (uint64_t)m * n / 4;
         uint64_t g = (n4 + 255) / 256;

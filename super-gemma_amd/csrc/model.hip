@@ -1304,7 +1304,12 @@ int pf_alloc(sgq_model *m) {
 int mmq(sgq_model *m, hipStream_t st, const void *w, const int8_t *xq, const uint16_t *xs,
         float *y, uint32_t M, uint32_t n, uint32_t k) {
     const uint32_t split = mmq_split(M, n, k);
-    return launch_gemm_q4_0_q8(st, w, xq, xs, y, M, n, k, split, split > 1 ? m->pf.part : nullptr);
+    // split 1: the partials buffer lets the last part-filled round of tiles
+    // split over K (at most one round of 128x128 tiles: 2 per CU)
+    const bool tail_ok = (uint64_t)M * n <= kPfPartialFloats ||
+                         2ull * device_info().cus * 128 * 128 <= kPfPartialFloats;
+    return launch_gemm_q4_0_q8(st, w, xq, xs, y, M, n, k, split,
+                               split > 1 || tail_ok ? m->pf.part : nullptr);
 }
 
 // One chunk of M tokens at positions q0..q0+M-1 (tokens already on the device).

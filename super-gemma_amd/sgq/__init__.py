@@ -359,6 +359,8 @@ class GpuContext:
         _need(y, torch.float32, m * n, "y")
         if split_k > 1:
             _need(partials, torch.float32, split_k * m * n, "partials")
+        elif partials is not None:  # optional: lets the last part-filled round split over K
+            _need(partials, torch.float32, m * n, "partials")
         _check(lib().sgq_gemm_q4_0_q8(self._h, _ptr(w), _ptr(xq), _ptr(xs), _ptr(y), m, n, k,
                                       split_k, _ptr(partials)))
 

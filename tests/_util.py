@@ -21,6 +21,15 @@ def empty(n, dtype) -> torch.Tensor:
     return torch.empty(n, dtype=dtype, device="cuda")
 
 
+def zeros_synced(n, dtype) -> torch.Tensor:
+    """A zeroed device buffer whose fill has completed: torch.zeros runs on
+    torch's current stream, and a context on a side stream that writes the
+    buffer next (a step buffer) is not ordered after that fill."""
+    t = torch.zeros(n, dtype=dtype, device="cuda")
+    torch.cuda.current_stream().synchronize()
+    return t
+
+
 def assert_close(got, want, rtol, atol, what=""):
     """|got-want| <= atol + rtol*|want| elementwise (mod.rs:137-153 form)."""
     got = np.asarray(got, np.float64)

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import assert_close, dev, empty, host, rel_err
+from _util import assert_close, dev, empty, host, rel_err, zeros_synced
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +39,7 @@ def _cache(oracle, seed, slots):
 def _step(ctx, pos, kv_sl, kv_gl, q0):
     import sgq
 
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     ctx.step_write(step, sgq.StepState(pos, kv_sl, kv_gl, q0))
     return step
 
@@ -100,7 +100,7 @@ def test_decode_sliding_ring_by_name_and_graph_replay(ctx, oracle):
 
     attn = ctx.load_kernel("attn_decode_sliding_q8_hd128")
     red = ctx.load_kernel("attn_reduce_d128")
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     part = empty(NQ * 16 * (HD + 2), torch.float32)
     out = empty(NQ * HD, torch.float32)
     s = torch.cuda.Stream()
@@ -212,8 +212,8 @@ def test_kv_append_sliding_by_name_wraps_the_ring(ctx, oracle):
     rng = oracle.Rng(0xA99)
     src = rng.f32_vec(n_tok * NKV * HD)
     s_want, q_want = oracle.quant_q8_0(src)
-    scales = torch.zeros(RING * NKV * HD // 32, dtype=torch.int16, device="cuda")
-    quants = torch.zeros(RING * NKV * HD, dtype=torch.int8, device="cuda")
+    scales = zeros_synced(RING * NKV * HD // 32, torch.int16)
+    quants = zeros_synced(RING * NKV * HD, torch.int8)
     k = ctx.load_kernel("kv_append_sliding_q8")
     ctx.dispatch_blocking(k, _bind(sgq, dev(src), scales, quants, _step(ctx, 1022, 0, 0, 0)),
                           None, [n_tok, NKV * HD // 32, 1])

@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import assert_close, dev, empty, host
+from _util import assert_close, dev, empty, host, zeros_synced
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def _bind(sgq, *tensors):
 def _step(ctx, pos, kv_sl, kv_gl, q0=0):
     import sgq
 
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     ctx.step_write(step, sgq.StepState(pos, kv_sl, kv_gl, q0))
     return step
 
@@ -198,7 +198,7 @@ def test_real_decode_layer_graph_replay(ctx, oracle):
     app = ctx.load_kernel("kv_append_global")
     attn = ctx.load_kernel("attn_decode_global_q8k")
     red = ctx.load_kernel("attn_reduce_d512")
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     part = empty(NQ * splits * (hd + 2), torch.float32)
     out = empty(NQ * hd, torch.int16)
     v_eager = tv.clone()
@@ -460,7 +460,7 @@ def test_prefill_ring_graph_replay_with_step_q0(ctx, oracle):
     tkc = empty(m * row, torch.int16)
     tvc = empty(m * row, torch.int16)
     out = empty(m * NQ * hd, torch.int16)
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     binds = [tq, tkr, tvr, tkc, tvc, out, step]
     B = [sgq.BufferBinding.buffer(i, t) for i, t in enumerate(binds)]
     push = struct.pack("<f", 0.0625)
@@ -516,8 +516,8 @@ def test_chunked_sliding_prefill_attend_then_append(ctx, oracle):
     kf, vf = oracle.f16_bits_to_f32(kb), oracle.f16_bits_to_f32(vb)
     attn = ctx.load_kernel("attn_prefill_sliding_ring")
     app = ctx.load_kernel("kv_append_sliding")
-    ring_k = torch.zeros(RING * row, dtype=torch.int16, device="cuda")
-    ring_v = torch.zeros(RING * row, dtype=torch.int16, device="cuda")
+    ring_k = zeros_synced(RING * row, torch.int16)
+    ring_v = zeros_synced(RING * row, torch.int16)
     out = empty(m * NQ * hd, torch.int16)
     B = sgq.BufferBinding.buffer
     for c in range(chunks):

@@ -25,7 +25,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import dev, empty, host, sample_rows
+from _util import dev, empty, host, sample_rows, zeros_synced
 
 pytestmark = pytest.mark.gpu
 
@@ -210,7 +210,7 @@ def test_kv_quant_dequant_append_f16(ctx, oracle):
     row, pos, slots = 2048, 4, 9
     scales = torch.full((slots * row // 32,), 7, dtype=torch.int16, device="cuda")
     quants = torch.full((slots * row,), 3, dtype=torch.int8, device="cuda")
-    step = torch.zeros(4, dtype=torch.int32, device="cuda")
+    step = zeros_synced(4, torch.int32)
     ctx.step_write(step, sgq.StepState(pos, 0, pos + 3, 0))
     ka = ctx.load_kernel("kv_append_global_q8")
     ctx.dispatch_blocking(ka, [B(0, tx), B(1, scales), B(2, quants), B(3, step)], None,
@@ -240,7 +240,7 @@ def test_kv_append_global_v_q8_f16(ctx, oracle):
     ws = np.zeros(slots // 32 * row, np.uint16)
     oracle.kv_append_v_q8(src, n_tok, row, pos, wq, ws)
     tq, ts = dev(np.zeros_like(wq)), dev(np.zeros_like(ws))
-    step = torch.zeros(4, dtype=torch.int32, device="cuda")
+    step = zeros_synced(4, torch.int32)
     ctx.step_write(step, sgq.StepState(pos, 0, 0, 0))
     k = ctx.load_kernel("kv_append_global_v_q8")
     ctx.dispatch_blocking(k, [B(0, tsrc), B(1, ts), B(2, tq), B(3, step)], None,

@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import assert_close, dev, empty, host, rel_err
+from _util import assert_close, dev, empty, host, rel_err, zeros_synced
 
 pytestmark = pytest.mark.gpu
 
@@ -50,8 +50,8 @@ def test_kv_append_v_q8_bit_exact(ctx, oracle):
     wq = np.zeros(slots * row, np.int8)
     ws = np.zeros((slots // 32) * row, np.uint16)
     oracle.kv_append_v_q8(src, n_tok, row, pos, wq, ws)
-    tq = torch.zeros(slots * row, dtype=torch.int8, device="cuda")
-    ts = torch.zeros((slots // 32) * row, dtype=torch.int16, device="cuda")
+    tq = zeros_synced(slots * row, torch.int8)
+    ts = zeros_synced((slots // 32) * row, torch.int16)
     ctx.kv_append_v_q8(dev(src), n_tok, row, pos, tq, ts)
     torch.cuda.synchronize()
     assert np.array_equal(host(ts, np.uint16), ws)
@@ -59,7 +59,7 @@ def test_kv_append_v_q8_bit_exact(ctx, oracle):
     # by name, pos from the step buffer
     tq.zero_()
     ts.zero_()
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     ctx.step_write(step, sgq.StepState(pos, 0, 0, 0))
     k = ctx.load_kernel("kv_append_global_v_q8_f32")
     B = sgq.BufferBinding.buffer
@@ -139,7 +139,7 @@ def test_attn_prefill_ipv_config4_sampled_and_by_name(ctx, oracle):
     _check(got[rows], _want(oracle, q, kd, vd, rows, 0, n_q, n_kv, scale), "ipv config 4")
     k = ctx.load_kernel("attn_prefill_global_flash_ipv_hd128")
     out = empty(n_tok * n_q * HD, torch.float32)
-    step = torch.zeros(8, dtype=torch.int32, device="cuda")
+    step = zeros_synced(8, torch.int32)
     ctx.step_write(step, sgq.StepState(0, 0, 0, 0))
     B = sgq.BufferBinding.buffer
     ctx.dispatch_blocking(k, [B(0, dev(q)), B(1, dev(kq)), B(2, dev(ks)), B(3, dev(vq)),

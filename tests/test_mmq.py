@@ -215,3 +215,30 @@ def test_mmq_config3_m2048(ctx, oracle, split):
     ns = np.concatenate([gen.integers(0, n, 396), [0, n - 1, 0, n - 1]])
     _check_pairs(oracle, host(tw), host(xq_t), host(xs_t, np.uint16), host(ys).reshape(m, n), k,
                  ms, ns, f"config 3 split {split}")
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 5376, 21504), (2048, 21504, 5376), (768, 5376, 21504)])
+def test_mmq_tail_split_matches_plain(ctx, m, k, n):
+    """split_k = 1 with a partials buffer: the tiles past the last whole round
+    of resident workgroups are split over K and summed in part order (config
+    2 and config 3 at split 1 have such a part-filled round; M=768 has none
+    to split).  Every output written (the buffer starts as NaN), equal to the
+    unsplit call up to the K reassociation of the tail tiles."""
+    print(f"mmq tail split m={m} k={k} n={n}", flush=True)
+    tw = empty(n * k // 32 * 18, torch.uint8)
+    ctx.fill_q4_0_random(tw, n * k // 32, seed=31, sigma=0.02)
+    tx = empty(m * k, torch.float32)
+    ctx.fill_normal(tx, seed=32)
+    xq_t, xs_t = _quant_on_gpu(ctx, tx, m, k)
+    y0 = empty(m * n, torch.float32)
+    ctx.gemm_q4_0_q8(tw, xq_t, xs_t, y0, m, n, k)
+    y1 = torch.full((m * n,), float("nan"), dtype=torch.float32, device="cuda")
+    part = empty(m * n, torch.float32)
+    ctx.gemm_q4_0_q8(tw, xq_t, xs_t, y1, m, n, k, 1, part)
+    torch.cuda.synchronize()
+    a, b = host(y0), host(y1)
+    assert np.isfinite(b).all(), "tail split left outputs unwritten"
+    top = float(np.abs(a).max())
+    assert np.abs(a - b).max() <= 2e-6 * top, f"max diff {np.abs(a - b).max()} vs {top}"
+    # whole tiles are bit-identical; only the tail tiles (< 1 round) may differ
+    assert np.count_nonzero(a != b) <= 512 * 128 * 128

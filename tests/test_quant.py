@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import dev, empty, host
+from _util import dev, empty, host, zeros_synced
 
 pytestmark = pytest.mark.gpu
 
@@ -89,7 +89,7 @@ def test_kv_append_global_q8_places_rows_at_pos(ctx, oracle):
     s_want, q_want = oracle.quant_q8_0(x)
     scales = torch.full((slots * row // 32,), 7, dtype=torch.int16, device="cuda")
     quants = torch.full((slots * row,), 3, dtype=torch.int8, device="cuda")
-    step = torch.zeros(4, dtype=torch.int32, device="cuda")
+    step = zeros_synced(4, torch.int32)
     ctx.step_write(step, sgq.StepState(pos=pos, kv_len_sliding=0, kv_len_global=pos + n_tok, q0=pos))
     kern = ctx.load_kernel("kv_append_global_q8_f32")
     ctx.dispatch_blocking(kern, [sgq.BufferBinding.buffer(0, dev(x)), sgq.BufferBinding.buffer(1, scales),

@@ -32,7 +32,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import dev, empty, host, rel_err
+from _util import dev, empty, host, rel_err, zeros_synced
 from test_model import _weights
 
 pytestmark = pytest.mark.gpu
@@ -54,7 +54,7 @@ class _Graph:
 
     def __init__(self, ctx, sgq, wts, cfg):
         self.ctx, self.sgq = ctx, sgq
-        h16 = lambda n: torch.zeros(n, dtype=torch.int16, device="cuda")  # noqa: E731
+        h16 = lambda n: zeros_synced(n, torch.int16)  # noqa: E731
         self.qd = {"s": NQ * 256, "g": NQ * 512}
         self.kvd = {"s": 16 * 256, "g": 4 * 512}
         self.x, self.xn, self.o, self.on, self.x2, self.fin, self.f, self.fn2 = \
@@ -69,7 +69,7 @@ class _Graph:
         self.v = {k: h16(v) for k, v in self.kvd.items()}
         self.part = {"s": empty(NQ * SPLITS_SL * 258, torch.float32),
                      "g": empty(NQ * SPLITS_GL * 514, torch.float32)}
-        self.step = torch.zeros(4, dtype=torch.int32, device="cuda")
+        self.step = zeros_synced(4, torch.int32)
         self.cs = {"s": empty(128 * 2, torch.float32), "g": empty(64 * 2, torch.float32)}
         self.ones = torch.ones(512, dtype=torch.float32, device="cuda")
         self.w = {key: dev(a) for key, a in wts.items()}
